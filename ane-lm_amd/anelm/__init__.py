@@ -1,0 +1,233 @@
+"""ctypes binding of libanelm_hip.so for Python callers (tests, bench).
+
+PyTorch is used only for device memory and streams: every function takes
+torch tensors that already live on the GPU, passes their raw device
+pointers and the current HIP stream to the C ABI (include/anelm_hip.h),
+and raises AnelmError with the library's message on a non-zero status.
+There is no fallback: if the library is missing or fails, the call raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+_PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(_PKG, "lib", "libanelm_hip.so")
+
+F32, F16, BF16 = 0, 1, 2
+OK, ERR_INVALID, ERR_RANGE, ERR_HIP, ERR_WORKSPACE = 0, -1, -2, -3, -4
+
+
+class AnelmError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"anelm error {code}: {msg}")
+        self.code = code
+
+
+class SamplingParams(ctypes.Structure):
+    """anelm_sampling_params; defaults of core/sampling.h:7-12."""
+
+    _fields_ = [
+        ("temperature", ctypes.c_float),
+        ("repetition_penalty", ctypes.c_float),
+        ("repetition_context_size", ctypes.c_int),
+        ("frequency_penalty", ctypes.c_float),
+    ]
+
+    def __init__(self, temperature=0.6, repetition_penalty=1.2, repetition_context_size=256,
+                 frequency_penalty=0.1):
+        super().__init__(temperature, repetition_penalty, repetition_context_size, frequency_penalty)
+
+
+_lib = None
+_P = ctypes.c_void_p
+_L = ctypes.c_long
+_I = ctypes.c_int
+_F = ctypes.c_float
+_S = ctypes.c_size_t
+
+_SIGS = {
+    "anelm_last_error": (ctypes.c_char_p, []),
+    "anelm_version": (_I, []),
+    "anelm_rmsnorm": (_I, [_P, _P, _P, _I, _L, _I, _L, _L, _F, _P]),
+    "anelm_add_rmsnorm": (_I, [_P, _P, _P, _P, _I, _L, _I, _L, _L, _L, _F, _P]),
+    "anelm_qknorm_rope": (_I, [_P, _P, _L, _L, _P, _P, _I, _P, _P, _P, _I, _F, _L, _I, _I, _I, _F, _P]),
+    "anelm_rope_cached": (_I, [_P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _P, _P, _P]),
+    "anelm_rope_table": (_I, [_P, _P, _I, _I, _F, _P]),
+    "anelm_residual_add": (_I, [_P, _P, _S, _P]),
+    "anelm_silu_mul": (_I, [_P, _P, _P, _L, _L, _L, _L, _L, _P]),
+    "anelm_silu": (_I, [_P, _S, _P]),
+    "anelm_mul_sigmoid": (_I, [_P, _P, _S, _P]),
+    "anelm_embed_gather": (_I, [_P, _P, _I, _P, _L, _L, _L, _P, _P]),
+    "anelm_bf16_to_f16": (_I, [_P, _P, _S, _P]),
+    "anelm_bf16_to_f32": (_I, [_P, _P, _S, _P]),
+    "anelm_f16_to_f32": (_I, [_P, _P, _S, _P]),
+    "anelm_softmax_workspace_size": (_S, [_L, _L]),
+    "anelm_softmax": (_I, [_P, _L, _L, _L, _P, _S, _P]),
+    "anelm_sample_workspace_size": (_S, [_L, _L]),
+    "anelm_sample": (_I, [_P, _P, _L, _P, _L, _L, _L, _P, _L, _P, ctypes.POINTER(SamplingParams), _P, _P, _S, _P]),
+}
+
+EXPORTED = tuple(_SIGS)
+
+
+def lib():
+    """Load libanelm_hip.so (after torch, so both share torch's HIP runtime)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    import torch  # noqa: F401  -- torch's libamdhip64.so.7 must be the one in the process
+
+    if not os.path.exists(LIB_PATH):
+        raise AnelmError(ERR_HIP, f"{LIB_PATH} is not built (python ane-lm_amd/build.py)")
+    l = ctypes.CDLL(LIB_PATH)
+    for name, (res, args) in _SIGS.items():
+        fn = getattr(l, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = l
+    return l
+
+
+def last_error() -> str:
+    return lib().anelm_last_error().decode()
+
+
+def _check(rc: int) -> None:
+    if rc != 0:
+        raise AnelmError(rc, last_error())
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(stream):
+    import torch
+
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return ctypes.c_void_p(stream.cuda_stream)
+
+
+def _dtype_code(t) -> int:
+    import torch
+
+    return {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}[t.dtype]
+
+
+def _need(cond: bool, msg: str) -> None:
+    if not cond:
+        raise AnelmError(ERR_INVALID, msg)
+
+
+def _rows(x):
+    """(rows, dim, ld) of a 2-D tensor with unit inner stride."""
+    _need(x.dim() == 2 and x.stride(1) == 1, "expected a 2-D tensor with unit inner stride")
+    return x.shape[0], x.shape[1], x.stride(0)
+
+
+# ---------------------------------------------------------------- ops
+
+def rmsnorm(out, x, w, eps=1e-6, stream=None):
+    rows, dim, ldx = _rows(x)
+    _, _, ldo = _rows(out)
+    _check(lib().anelm_rmsnorm(_ptr(out), _ptr(x), _ptr(w), _dtype_code(w), rows, dim, ldx, ldo, eps,
+                               _stream(stream)))
+
+
+def add_rmsnorm(x, y, out, w, eps=1e-6, stream=None):
+    rows, dim, ldx = _rows(x)
+    _, _, ldy = _rows(y)
+    _, _, ldo = _rows(out)
+    _check(lib().anelm_add_rmsnorm(_ptr(x), _ptr(y), _ptr(out), _ptr(w), _dtype_code(w), rows, dim, ldx, ldy,
+                                   ldo, eps, _stream(stream)))
+
+
+def qknorm_rope(q, k, wq, wk, pos, cos_tab, sin_tab, theta=1e6, eps=1e-6, nq=None, nk=None, head_dim=128,
+                stream=None):
+    """q: [T, >= nq*head_dim] rows, k: [T, >= nk*head_dim] rows (views allowed)."""
+    T = pos.shape[0]
+    q_ld = q.stride(0) if q is not None else 0
+    k_ld = k.stride(0) if k is not None else 0
+    nq = (q.shape[1] // head_dim if q is not None else 0) if nq is None else nq
+    nk = (k.shape[1] // head_dim if k is not None else 0) if nk is None else nk
+    wdt = _dtype_code(wq if wq is not None else (wk if wk is not None else q))
+    tab_len = cos_tab.shape[0] if cos_tab is not None else 0
+    _check(lib().anelm_qknorm_rope(_ptr(q), _ptr(k), q_ld, k_ld, _ptr(wq), _ptr(wk), wdt, _ptr(pos), _ptr(cos_tab),
+                                   _ptr(sin_tab), tab_len, theta, T, nq, nk, head_dim, eps, _stream(stream)))
+
+
+def rope_cached(q, k, n_q_heads, n_kv_heads, head_dim, q_head_stride, k_head_stride, rot_dim, pos, theta,
+                cos_row=None, sin_row=None, stream=None):
+    _check(lib().anelm_rope_cached(_ptr(q), _ptr(k), n_q_heads, n_kv_heads, head_dim, q_head_stride,
+                                   k_head_stride, rot_dim, pos, theta, _ptr(cos_row), _ptr(sin_row),
+                                   _stream(stream)))
+
+
+def rope_table(cos_tab, sin_tab, theta=1e6, stream=None):
+    n_pos, half = cos_tab.shape
+    _check(lib().anelm_rope_table(_ptr(cos_tab), _ptr(sin_tab), n_pos, 2 * half, theta, _stream(stream)))
+
+
+def residual_add(x, y, stream=None):
+    _need(x.numel() == y.numel() and x.is_contiguous() and y.is_contiguous(), "residual_add: shapes")
+    _check(lib().anelm_residual_add(_ptr(x), _ptr(y), x.numel(), _stream(stream)))
+
+
+def silu_mul(h, g, u, stream=None):
+    rows, inter, ldg = _rows(g)
+    _, _, ldu = _rows(u)
+    _, _, ldh = _rows(h)
+    _check(lib().anelm_silu_mul(_ptr(h), _ptr(g), _ptr(u), rows, inter, ldh, ldg, ldu, _stream(stream)))
+
+
+def silu(x, stream=None):
+    _check(lib().anelm_silu(_ptr(x), x.numel(), _stream(stream)))
+
+
+def mul_sigmoid(y, z, stream=None):
+    _check(lib().anelm_mul_sigmoid(_ptr(y), _ptr(z), y.numel(), _stream(stream)))
+
+
+def embed_gather(out, table, ids, bad_count=None, stream=None):
+    vocab, hidden = table.shape
+    _check(lib().anelm_embed_gather(_ptr(out), _ptr(table), _dtype_code(table), _ptr(ids), ids.shape[0], hidden, vocab,
+                                    _ptr(bad_count), _stream(stream)))
+
+
+def bf16_to_f16(dst, src, stream=None):
+    """dst/src: uint16/int16 (or bf16/f16) tensors of the same element count."""
+    _check(lib().anelm_bf16_to_f16(_ptr(dst), _ptr(src), src.numel(), _stream(stream)))
+
+
+def bf16_to_f32(dst, src, stream=None):
+    _check(lib().anelm_bf16_to_f32(_ptr(dst), _ptr(src), src.numel(), _stream(stream)))
+
+
+def f16_to_f32(dst, src, stream=None):
+    _check(lib().anelm_f16_to_f32(_ptr(dst), _ptr(src), src.numel(), _stream(stream)))
+
+
+def softmax_workspace_size(rows, n) -> int:
+    return lib().anelm_softmax_workspace_size(rows, n)
+
+
+def softmax(x, workspace, stream=None):
+    rows, n, ld = _rows(x)
+    _check(lib().anelm_softmax(_ptr(x), rows, n, ld, _ptr(workspace), workspace.numel() * workspace.element_size(),
+                               _stream(stream)))
+
+
+def sample_workspace_size(rows, vocab) -> int:
+    return lib().anelm_sample_workspace_size(rows, vocab)
+
+
+def sample(ids, probs, logits, hist, hist_len, params: SamplingParams, r, workspace, stream=None):
+    rows, vocab, ldl = _rows(logits)
+    ldp = probs.stride(0) if probs is not None else 0
+    hist_ld = hist.stride(0) if hist is not None and hist.numel() else 0
+    _check(lib().anelm_sample(_ptr(ids), _ptr(probs), ldp, _ptr(logits), ldl, rows, vocab,
+                              _ptr(hist) if hist_ld else None, hist_ld, _ptr(hist_len), ctypes.byref(params),
+                              _ptr(r), _ptr(workspace), workspace.numel() * workspace.element_size(),
+                              _stream(stream)))

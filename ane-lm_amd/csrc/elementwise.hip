@@ -1,0 +1,324 @@
+// Streaming elementwise ops for gfx950: residual add, SwiGLU, SiLU,
+// mul-sigmoid, the bf16/fp16 weight converts and the embedding gather.
+//
+// Every op here is a pure stream (< 1 flop/byte).  The vector kernels move
+// 16 bytes per lane per access and keep U independent 16-byte loads per
+// stream in flight per lane before the first store, with a one-shot grid
+// (one tile of 256*U vectors per workgroup, no grid-stride loop), so a
+// launch has ~n/(256*U) workgroups -- far more than the 256 CUs.  Outputs
+// that are written once and not re-read by the kernel use non-temporal
+// stores.
+#include "anelm_common.hpp"
+
+namespace anelm {
+
+constexpr int kU = 4;  // 16-byte vectors per lane per stream
+
+// ------------------------------------------------------------ residual add
+// qwen3.cpp:516/:527: x = x + y, one IEEE add per element (bit-exact).
+__global__ __launch_bounds__(256) void residual_add_vec_kernel(float4* x, const float4* y, size_t n4) {
+    const size_t base = (size_t)blockIdx.x * (256 * kU) + threadIdx.x;
+    float4 a[kU], b[kU];
+#pragma unroll
+    for (int i = 0; i < kU; i++) {
+        const size_t idx = base + (size_t)i * 256;
+        if (idx < n4) {
+            a[i] = x[idx];
+            b[i] = ld_nt(y + idx);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < kU; i++) {
+        const size_t idx = base + (size_t)i * 256;
+        if (idx < n4) {
+            float4 r;
+            r.x = a[i].x + b[i].x;
+            r.y = a[i].y + b[i].y;
+            r.z = a[i].z + b[i].z;
+            r.w = a[i].w + b[i].w;
+            st_nt(x + idx, r);
+        }
+    }
+}
+
+__global__ __launch_bounds__(256) void residual_add_scalar_kernel(float* x, const float* y, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256)
+        x[i] = x[i] + y[i];
+}
+
+// ------------------------------------------------------------ SiLU family
+// core/cpu_ops.cpp:7-14 form: silu(g) = g / (1 + expf(-g)) with a correctly
+// rounded divide; SwiGLU multiplies by up (core/ane_runtime.cpp:393-395).
+__device__ __forceinline__ float silu_ref(float g) {
+    const float t = expf(-g) + 1.0f;
+    return g / t;
+}
+
+__device__ __forceinline__ float4 silu_mul4(float4 g, float4 u) {
+    float4 r;
+    r.x = silu_ref(g.x) * u.x;
+    r.y = silu_ref(g.y) * u.y;
+    r.z = silu_ref(g.z) * u.z;
+    r.w = silu_ref(g.w) * u.w;
+    return r;
+}
+
+__global__ __launch_bounds__(256) void silu_mul_vec_kernel(float4* h, const float4* g, const float4* u, size_t n4) {
+    const size_t base = (size_t)blockIdx.x * (256 * kU) + threadIdx.x;
+    float4 a[kU], b[kU];
+#pragma unroll
+    for (int i = 0; i < kU; i++) {
+        const size_t idx = base + (size_t)i * 256;
+        if (idx < n4) {
+            a[i] = ld_nt(g + idx);
+            b[i] = ld_nt(u + idx);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < kU; i++) {
+        const size_t idx = base + (size_t)i * 256;
+        if (idx < n4) st_nt(h + idx, silu_mul4(a[i], b[i]));
+    }
+}
+
+// strided rows (gate/up as slices of a wider buffer), any alignment
+__global__ __launch_bounds__(256) void silu_mul_rows_kernel(float* h, const float* g, const float* u,
+                                                            long rows, long inter, long ld_h, long ld_g,
+                                                            long ld_u) {
+    const long n = rows * inter;
+    for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long)gridDim.x * 256) {
+        const long r = i / inter, c = i % inter;
+        h[r * ld_h + c] = silu_ref(g[r * ld_g + c]) * u[r * ld_u + c];
+    }
+}
+
+// silu_vec_inplace (cpu_ops.cpp:7-14) and mul_sigmoid_inplace (:16-23):
+// y = y / (1 + expf(-z)); silu is the case z = y.
+__global__ __launch_bounds__(256) void mul_sigmoid_kernel(float* y, const float* z, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
+        const float t = expf(-z[i]) + 1.0f;
+        y[i] = y[i] / t;
+    }
+}
+
+// ------------------------------------------------------------ converts
+// bf16 -> fp16 truncating (include/ane_lm/common.h:58-83), 8 elements per
+// 16-byte vector, integer ops only.
+__device__ __forceinline__ uint32_t cvt_pair(uint32_t w) {
+    return bf16_to_f16_trunc(w & 0xFFFFu) | (bf16_to_f16_trunc(w >> 16) << 16);
+}
+
+__global__ __launch_bounds__(256) void bf16_to_f16_vec_kernel(uint4* dst, const uint4* src, size_t n8) {
+    const size_t base = (size_t)blockIdx.x * (256 * kU) + threadIdx.x;
+    uint4 a[kU];
+#pragma unroll
+    for (int i = 0; i < kU; i++) {
+        const size_t idx = base + (size_t)i * 256;
+        if (idx < n8) a[i] = ld_nt(src + idx);
+    }
+#pragma unroll
+    for (int i = 0; i < kU; i++) {
+        const size_t idx = base + (size_t)i * 256;
+        if (idx < n8) {
+            uint4 r;
+            r.x = cvt_pair(a[i].x);
+            r.y = cvt_pair(a[i].y);
+            r.z = cvt_pair(a[i].z);
+            r.w = cvt_pair(a[i].w);
+            st_nt(dst + idx, r);
+        }
+    }
+}
+
+__global__ __launch_bounds__(256) void bf16_to_f16_scalar_kernel(uint16_t* dst, const uint16_t* src, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256)
+        dst[i] = (uint16_t)bf16_to_f16_trunc(src[i]);
+}
+
+template <bool F16>
+__global__ __launch_bounds__(256) void widen_kernel(float* dst, const uint16_t* src, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256)
+        dst[i] = F16 ? f16_to_f32_exact(src[i]) : bf16_to_f32(src[i]);
+}
+
+// ------------------------------------------------------------ gather
+// qwen3.cpp:498: x = E[id].  gridDim.y = ids; each block moves a slice of
+// the row.  A bad id leaves its row unwritten and bumps *bad once.
+template <int DT>
+__global__ __launch_bounds__(256) void gather_vec_kernel(float* out, const void* table, const int32_t* ids,
+                                                         long hidden, long vocab, int32_t* bad) {
+    const long b = blockIdx.y;
+    const int id = ids[b];
+    if (id < 0 || id >= vocab) {
+        if (bad && blockIdx.x == 0 && threadIdx.x == 0) atomicAdd(bad, 1);
+        return;
+    }
+    float* o = out + b * hidden;
+    if (DT == ANELM_F32) {
+        const float4* src = reinterpret_cast<const float4*>(static_cast<const float*>(table) + (long)id * hidden);
+        const long n4 = hidden / 4;
+        for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n4; i += (long)gridDim.x * 256)
+            reinterpret_cast<float4*>(o)[i] = src[i];
+    } else {
+        // 8 halves (16 bytes) in, 2 float4 out per lane
+        const uint4* src = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(table) + (long)id * hidden);
+        const long n8 = hidden / 8;
+        for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n8; i += (long)gridDim.x * 256) {
+            const uint4 v = src[i];
+            float4 lo, hi;
+            if (DT == ANELM_F16) {
+                lo = make_float4(f16_to_f32_exact(v.x & 0xFFFFu), f16_to_f32_exact(v.x >> 16),
+                                 f16_to_f32_exact(v.y & 0xFFFFu), f16_to_f32_exact(v.y >> 16));
+                hi = make_float4(f16_to_f32_exact(v.z & 0xFFFFu), f16_to_f32_exact(v.z >> 16),
+                                 f16_to_f32_exact(v.w & 0xFFFFu), f16_to_f32_exact(v.w >> 16));
+            } else {
+                lo = make_float4(bf16_to_f32(v.x & 0xFFFFu), bf16_to_f32(v.x >> 16),
+                                 bf16_to_f32(v.y & 0xFFFFu), bf16_to_f32(v.y >> 16));
+                hi = make_float4(bf16_to_f32(v.z & 0xFFFFu), bf16_to_f32(v.z >> 16),
+                                 bf16_to_f32(v.w & 0xFFFFu), bf16_to_f32(v.w >> 16));
+            }
+            reinterpret_cast<float4*>(o)[2 * i] = lo;
+            reinterpret_cast<float4*>(o)[2 * i + 1] = hi;
+        }
+    }
+}
+
+template <int DT>
+__global__ __launch_bounds__(256) void gather_scalar_kernel(float* out, const void* table, const int32_t* ids,
+                                                            long hidden, long vocab, int32_t* bad) {
+    const long b = blockIdx.y;
+    const int id = ids[b];
+    if (id < 0 || id >= vocab) {
+        if (bad && blockIdx.x == 0 && threadIdx.x == 0) atomicAdd(bad, 1);
+        return;
+    }
+    for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < hidden; i += (long)gridDim.x * 256)
+        out[b * hidden + i] = load_w<DT>(table, (long)id * hidden + i);
+}
+
+static unsigned grid_for(size_t work_items, size_t per_block) {
+    size_t g = (work_items + per_block - 1) / per_block;
+    return (unsigned)(g == 0 ? 1 : g);
+}
+
+static unsigned grid_stride_blocks(size_t n) {
+    size_t g = (n + 255) / 256;
+    if (g > 16384) g = 16384;
+    return (unsigned)(g == 0 ? 1 : g);
+}
+
+}  // namespace anelm
+
+using namespace anelm;
+
+extern "C" int anelm_residual_add(float* x, const float* y, size_t n, void* stream) {
+    if (!x || !y) return fail(ANELM_ERR_INVALID, "anelm_residual_add: null pointer");
+    if (n == 0) return fail(ANELM_ERR_INVALID, "anelm_residual_add: n == 0");
+    clear_error();
+    hipStream_t st = as_stream(stream);
+    if (n % 4 == 0 && aligned16(x) && aligned16(y)) {
+        const size_t n4 = n / 4;
+        residual_add_vec_kernel<<<grid_for(n4, 256 * kU), 256, 0, st>>>(reinterpret_cast<float4*>(x),
+                                                                         reinterpret_cast<const float4*>(y), n4);
+    } else {
+        residual_add_scalar_kernel<<<grid_stride_blocks(n), 256, 0, st>>>(x, y, n);
+    }
+    return launch_status("residual_add");
+}
+
+extern "C" int anelm_silu_mul(float* h, const float* g, const float* u, long rows, long inter, long ld_h,
+                              long ld_g, long ld_u, void* stream) {
+    if (!h || !g || !u) return fail(ANELM_ERR_INVALID, "anelm_silu_mul: null pointer");
+    if (rows <= 0 || inter <= 0) return fail(ANELM_ERR_INVALID, "anelm_silu_mul: rows=%ld inter=%ld", rows, inter);
+    if (ld_h < inter || ld_g < inter || ld_u < inter) return fail(ANELM_ERR_INVALID, "anelm_silu_mul: ld < inter");
+    clear_error();
+    hipStream_t st = as_stream(stream);
+    const size_t n = (size_t)rows * (size_t)inter;
+    const bool contiguous = (ld_h == inter && ld_g == inter && ld_u == inter) || rows == 1;
+    if (contiguous && n % 4 == 0 && aligned16(h) && aligned16(g) && aligned16(u)) {
+        const size_t n4 = n / 4;
+        silu_mul_vec_kernel<<<grid_for(n4, 256 * kU), 256, 0, st>>>(
+            reinterpret_cast<float4*>(h), reinterpret_cast<const float4*>(g), reinterpret_cast<const float4*>(u), n4);
+    } else {
+        silu_mul_rows_kernel<<<grid_stride_blocks(n), 256, 0, st>>>(h, g, u, rows, inter, ld_h, ld_g, ld_u);
+    }
+    return launch_status("silu_mul");
+}
+
+extern "C" int anelm_silu(float* x, size_t n, void* stream) {
+    if (!x) return fail(ANELM_ERR_INVALID, "anelm_silu: null pointer");
+    if (n == 0) return fail(ANELM_ERR_INVALID, "anelm_silu: n == 0");
+    clear_error();
+    mul_sigmoid_kernel<<<grid_stride_blocks(n), 256, 0, as_stream(stream)>>>(x, x, n);
+    return launch_status("silu");
+}
+
+extern "C" int anelm_mul_sigmoid(float* y, const float* z, size_t n, void* stream) {
+    if (!y || !z) return fail(ANELM_ERR_INVALID, "anelm_mul_sigmoid: null pointer");
+    if (n == 0) return fail(ANELM_ERR_INVALID, "anelm_mul_sigmoid: n == 0");
+    clear_error();
+    mul_sigmoid_kernel<<<grid_stride_blocks(n), 256, 0, as_stream(stream)>>>(y, z, n);
+    return launch_status("mul_sigmoid");
+}
+
+extern "C" int anelm_bf16_to_f16(uint16_t* dst, const uint16_t* src, size_t n, void* stream) {
+    if (!dst || !src) return fail(ANELM_ERR_INVALID, "anelm_bf16_to_f16: null pointer");
+    if (n == 0) return fail(ANELM_ERR_INVALID, "anelm_bf16_to_f16: n == 0");
+    clear_error();
+    hipStream_t st = as_stream(stream);
+    if (n % 8 == 0 && aligned16(dst) && aligned16(src)) {
+        const size_t n8 = n / 8;
+        bf16_to_f16_vec_kernel<<<grid_for(n8, 256 * kU), 256, 0, st>>>(reinterpret_cast<uint4*>(dst),
+                                                                        reinterpret_cast<const uint4*>(src), n8);
+    } else {
+        bf16_to_f16_scalar_kernel<<<grid_stride_blocks(n), 256, 0, st>>>(dst, src, n);
+    }
+    return launch_status("bf16_to_f16");
+}
+
+extern "C" int anelm_bf16_to_f32(float* dst, const uint16_t* src, size_t n, void* stream) {
+    if (!dst || !src) return fail(ANELM_ERR_INVALID, "anelm_bf16_to_f32: null pointer");
+    if (n == 0) return fail(ANELM_ERR_INVALID, "anelm_bf16_to_f32: n == 0");
+    clear_error();
+    widen_kernel<false><<<grid_stride_blocks(n), 256, 0, as_stream(stream)>>>(dst, src, n);
+    return launch_status("bf16_to_f32");
+}
+
+extern "C" int anelm_f16_to_f32(float* dst, const uint16_t* src, size_t n, void* stream) {
+    if (!dst || !src) return fail(ANELM_ERR_INVALID, "anelm_f16_to_f32: null pointer");
+    if (n == 0) return fail(ANELM_ERR_INVALID, "anelm_f16_to_f32: n == 0");
+    clear_error();
+    widen_kernel<true><<<grid_stride_blocks(n), 256, 0, as_stream(stream)>>>(dst, src, n);
+    return launch_status("f16_to_f32");
+}
+
+template <int DT>
+static void launch_gather(float* out, const void* table, const int32_t* ids, long n_ids, long hidden,
+                          long vocab, int32_t* bad, hipStream_t st) {
+    const int esz = DT == ANELM_F32 ? 4 : 2;
+    const long per_vec = DT == ANELM_F32 ? 4 : 8;
+    const bool vec = hidden % per_vec == 0 && aligned16(out) && aligned16(table) &&
+                     ((hidden * esz) % 16 == 0);
+    const long units = vec ? hidden / per_vec : hidden;
+    long bx = (units + 255) / 256;
+    if (bx > 64) bx = 64;
+    const dim3 grd((unsigned)bx, (unsigned)n_ids);
+    if (vec) gather_vec_kernel<DT><<<grd, 256, 0, st>>>(out, table, ids, hidden, vocab, bad);
+    else gather_scalar_kernel<DT><<<grd, 256, 0, st>>>(out, table, ids, hidden, vocab, bad);
+}
+
+extern "C" int anelm_embed_gather(float* out, const void* table, int table_dtype, const int32_t* ids, long n_ids,
+                                  long hidden, long vocab, int32_t* bad_count, void* stream) {
+    if (!out || !table || !ids) return fail(ANELM_ERR_INVALID, "anelm_embed_gather: null pointer");
+    if (n_ids <= 0 || hidden <= 0 || vocab <= 0) return fail(ANELM_ERR_INVALID, "anelm_embed_gather: empty");
+    if (n_ids > 65535) return fail(ANELM_ERR_INVALID, "anelm_embed_gather: n_ids %ld > 65535", n_ids);
+    clear_error();
+    hipStream_t st = as_stream(stream);
+    switch (table_dtype) {
+        case ANELM_F32: launch_gather<ANELM_F32>(out, table, ids, n_ids, hidden, vocab, bad_count, st); break;
+        case ANELM_F16: launch_gather<ANELM_F16>(out, table, ids, n_ids, hidden, vocab, bad_count, st); break;
+        case ANELM_BF16: launch_gather<ANELM_BF16>(out, table, ids, n_ids, hidden, vocab, bad_count, st); break;
+        default: return fail(ANELM_ERR_INVALID, "anelm_embed_gather: unknown dtype %d", table_dtype);
+    }
+    return launch_status("embed_gather");
+}

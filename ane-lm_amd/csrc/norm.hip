@@ -1,0 +1,441 @@
+// RMSNorm, fused residual-add + RMSNorm, per-head q/k RMSNorm + RoPE, the
+// apply_rope_cached variant and the RoPE table, for gfx950.
+//
+// All of these are HBM-bound (< 1 flop/byte).  Row kernels give one wave64
+// a whole row held in registers as float4s, so a row crosses HBM once
+// (read) plus once per output (write); reductions are wave shuffles and
+// need no LDS or barrier.
+#include <cmath>
+
+#include "anelm_common.hpp"
+
+namespace anelm {
+
+// ---------------------------------------------------------------- RMSNorm
+// core/cpu_ops.cpp:25-31: ss = sum x^2; s = 1/sqrtf(ss/dim + eps) (true
+// divide and square root, correctly rounded); out = (x*s)*w with the two
+// products rounded separately.  With ADD, first x += y (qwen3.cpp:516) and
+// the updated x is written back.
+//
+// One wave per row, NV float4 per lane (dim <= 256*NV, dim % 4 == 0, rows
+// 16-byte aligned).  The whole row is read into registers before anything
+// is written, so out may alias x and y may alias out.
+template <int NV, int DT, bool ADD>
+__global__ __launch_bounds__(256) void rmsnorm_wave_kernel(float* out, float* x, const float* y,
+                                                           const void* w, long rows, int dim,
+                                                           long ld_x, long ld_y, long ld_out,
+                                                           float eps) {
+    const int lane = threadIdx.x & 63;
+    const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    float* xr = x + row * ld_x;
+    float4 v[NV];
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        const int c = (i * 64 + lane) * 4;
+        v[i] = c < dim ? *reinterpret_cast<const float4*>(xr + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    if (ADD) {
+        const float* yr = y + row * ld_y;
+        float4 b[NV];
+#pragma unroll
+        for (int i = 0; i < NV; i++) {
+            const int c = (i * 64 + lane) * 4;
+            b[i] = c < dim ? *reinterpret_cast<const float4*>(yr + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int i = 0; i < NV; i++) {
+            const int c = (i * 64 + lane) * 4;
+            v[i].x = v[i].x + b[i].x;
+            v[i].y = v[i].y + b[i].y;
+            v[i].z = v[i].z + b[i].z;
+            v[i].w = v[i].w + b[i].w;
+            if (c < dim) *reinterpret_cast<float4*>(xr + c) = v[i];
+        }
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        ss = fmaf(v[i].x, v[i].x, ss);
+        ss = fmaf(v[i].y, v[i].y, ss);
+        ss = fmaf(v[i].z, v[i].z, ss);
+        ss = fmaf(v[i].w, v[i].w, ss);
+    }
+    ss = wave_sum(ss);
+    const float s = 1.0f / sqrtf(ss / (float)dim + eps);
+    float* orow = out + row * ld_out;
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        const int c = (i * 64 + lane) * 4;
+        if (c < dim) {
+            const float4 wv = load_w4<DT>(w, c);
+            float4 o;
+            o.x = (v[i].x * s) * wv.x;
+            o.y = (v[i].y * s) * wv.y;
+            o.z = (v[i].z * s) * wv.z;
+            o.w = (v[i].w * s) * wv.w;
+            st_nt(reinterpret_cast<float4*>(orow + c), o);
+        }
+    }
+}
+
+// Any dim / alignment: one 256-thread block per row, two passes over the row
+// (the second re-reads x, which the same thread wrote in the ADD case).
+template <int DT, bool ADD>
+__global__ __launch_bounds__(256) void rmsnorm_block_kernel(float* out, float* x, const float* y,
+                                                            const void* w, long rows, int dim,
+                                                            long ld_x, long ld_y, long ld_out,
+                                                            float eps) {
+    __shared__ float part[4];
+    const long row = blockIdx.x;
+    float* xr = x + row * ld_x;
+    const float* yr = ADD ? y + row * ld_y : nullptr;
+    float ss = 0.f;
+    for (int c = threadIdx.x; c < dim; c += 256) {
+        float a = xr[c];
+        if (ADD) {
+            a = a + yr[c];
+            xr[c] = a;
+        }
+        ss = fmaf(a, a, ss);
+    }
+    ss = wave_sum(ss);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    ss = (part[0] + part[1]) + (part[2] + part[3]);
+    const float s = 1.0f / sqrtf(ss / (float)dim + eps);
+    float* orow = out + row * ld_out;
+    for (int c = threadIdx.x; c < dim; c += 256) orow[c] = (xr[c] * s) * load_w<DT>(w, c);
+}
+
+template <int DT, bool ADD>
+static int launch_rmsnorm_dt(float* out, float* x, const float* y, const void* w, long rows,
+                             int dim, long ld_x, long ld_y, long ld_out, float eps,
+                             hipStream_t st) {
+    const bool vec = (dim % 4 == 0) && (ld_x % 4 == 0) && (ld_out % 4 == 0) && aligned16(x) &&
+                     aligned16(out) && (DT == ANELM_F32 ? aligned16(w) : aligned8(w)) &&
+                     (!ADD || ((ld_y % 4 == 0) && aligned16(y)));
+    const int nv = (dim + 255) / 256;
+    const dim3 blk(256);
+    const dim3 grd((unsigned)((rows + 3) / 4));
+#define ANELM_RMS_CASE(N)                                                                       \
+    if (nv <= N) {                                                                              \
+        rmsnorm_wave_kernel<N, DT, ADD><<<grd, blk, 0, st>>>(out, x, y, w, rows, dim, ld_x, ld_y, \
+                                                             ld_out, eps);                      \
+        return launch_status("rmsnorm");                                                        \
+    }
+    if (vec) {
+        ANELM_RMS_CASE(1)
+        ANELM_RMS_CASE(2)
+        ANELM_RMS_CASE(4)
+        ANELM_RMS_CASE(6)
+        ANELM_RMS_CASE(8)
+        ANELM_RMS_CASE(10)
+        ANELM_RMS_CASE(12)
+        ANELM_RMS_CASE(16)
+        ANELM_RMS_CASE(20)
+        ANELM_RMS_CASE(24)
+        ANELM_RMS_CASE(32)
+    }
+#undef ANELM_RMS_CASE
+    rmsnorm_block_kernel<DT, ADD><<<dim3((unsigned)rows), blk, 0, st>>>(out, x, y, w, rows, dim, ld_x,
+                                                                        ld_y, ld_out, eps);
+    return launch_status("rmsnorm");
+}
+
+template <bool ADD>
+static int launch_rmsnorm(float* out, float* x, const float* y, const void* w, int dt, long rows,
+                          int dim, long ld_x, long ld_y, long ld_out, float eps, hipStream_t st) {
+    switch (dt) {
+        case ANELM_F32: return launch_rmsnorm_dt<ANELM_F32, ADD>(out, x, y, w, rows, dim, ld_x, ld_y, ld_out, eps, st);
+        case ANELM_F16: return launch_rmsnorm_dt<ANELM_F16, ADD>(out, x, y, w, rows, dim, ld_x, ld_y, ld_out, eps, st);
+        case ANELM_BF16: return launch_rmsnorm_dt<ANELM_BF16, ADD>(out, x, y, w, rows, dim, ld_x, ld_y, ld_out, eps, st);
+        default: return fail(ANELM_ERR_INVALID, "rmsnorm: unknown weight dtype %d", dt);
+    }
+}
+
+// ------------------------------------------------------- q/k norm + RoPE
+// models/llm/qwen3.cpp:444-472.  Per (token, head): rmsnorm over head_dim
+// with the shared gamma (ane_lm::rmsnorm(qh, qh, q_norm, hd, eps)), then the
+// Qwen3 half-split rotation (qwen3.cpp:17-26):
+//   v[j]'      = v[j]*c[j] - v[j+half]*s[j]
+//   v[j+half]' = v[j+half]*c[j] + v[j]*s[j]
+// with c/s from table row pos (0 <= pos < tab_len, qwen3.cpp:463-469) or the
+// fallback angle pos*inv_freq[j] (qwen3.cpp:39-49).
+//
+// head_dim 128 kernel: one wave per token.  A 16-lane group owns one head:
+// lane l holds elements 4l..4l+3 and 64+4l..64+4l+3, so each rotation pair
+// sits in one lane and the sum of squares is a 16-lane shuffle reduction.
+// The token's cos/sin row and both gammas are loaded once and reused for
+// all nq+nk heads.
+template <int DT>
+__global__ __launch_bounds__(256) void qknorm_rope128_kernel(
+    float* q, float* k, long q_ld, long k_ld, const void* wq, const void* wk, const int32_t* pos,
+    const float* cos_tab, const float* sin_tab, int tab_len, const InvFreq inv, long T, int nq,
+    int nk, float eps) {
+    const int lane = threadIdx.x & 63;
+    const long t = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= T) return;
+    const int slot = lane >> 4;
+    const int j0 = 4 * (lane & 15);
+    const int p = pos[t];
+    float4 c, s;
+    if (p >= 0 && p < tab_len) {
+        c = *reinterpret_cast<const float4*>(cos_tab + (long)p * 64 + j0);
+        s = *reinterpret_cast<const float4*>(sin_tab + (long)p * 64 + j0);
+    } else {
+        const float pf = (float)p;
+        const float a0 = pf * inv.v[j0], a1 = pf * inv.v[j0 + 1];
+        const float a2 = pf * inv.v[j0 + 2], a3 = pf * inv.v[j0 + 3];
+        c = make_float4(cosf(a0), cosf(a1), cosf(a2), cosf(a3));
+        s = make_float4(sinf(a0), sinf(a1), sinf(a2), sinf(a3));
+    }
+    const bool nq_on = wq != nullptr, nk_on = wk != nullptr;
+    const float4 one4 = make_float4(1.f, 1.f, 1.f, 1.f);
+    const float4 wql = nq_on ? load_w4<DT>(wq, j0) : one4;
+    const float4 wqh = nq_on ? load_w4<DT>(wq, j0 + 64) : one4;
+    const float4 wkl = nk_on ? load_w4<DT>(wk, j0) : one4;
+    const float4 wkh = nk_on ? load_w4<DT>(wk, j0 + 64) : one4;
+    const int nh = nq + nk;
+    float* qt = q + t * q_ld;
+    float* kt = k + t * k_ld;
+    for (int hb = 0; hb < nh; hb += 4) {
+        const int h = hb + slot;
+        const bool act = h < nh;
+        const bool isq = h < nq;
+        float* v = isq ? qt + (long)h * 128 : kt + (long)(h - nq) * 128;
+        float4 lo = make_float4(0.f, 0.f, 0.f, 0.f), hi = lo;
+        if (act) {
+            lo = *reinterpret_cast<const float4*>(v + j0);
+            hi = *reinterpret_cast<const float4*>(v + 64 + j0);
+        }
+        float ss = 0.f;
+        ss = fmaf(lo.x, lo.x, ss);
+        ss = fmaf(lo.y, lo.y, ss);
+        ss = fmaf(lo.z, lo.z, ss);
+        ss = fmaf(lo.w, lo.w, ss);
+        ss = fmaf(hi.x, hi.x, ss);
+        ss = fmaf(hi.y, hi.y, ss);
+        ss = fmaf(hi.z, hi.z, ss);
+        ss = fmaf(hi.w, hi.w, ss);
+        ss = group16_sum(ss);
+        if (isq ? nq_on : nk_on) {
+            const float sc = 1.0f / sqrtf(ss / 128.0f + eps);
+            const float4 wl = isq ? wql : wkl;
+            const float4 wh = isq ? wqh : wkh;
+            lo.x = (lo.x * sc) * wl.x;
+            lo.y = (lo.y * sc) * wl.y;
+            lo.z = (lo.z * sc) * wl.z;
+            lo.w = (lo.w * sc) * wl.w;
+            hi.x = (hi.x * sc) * wh.x;
+            hi.y = (hi.y * sc) * wh.y;
+            hi.z = (hi.z * sc) * wh.z;
+            hi.w = (hi.w * sc) * wh.w;
+        }
+        float4 ol, oh;
+        ol.x = lo.x * c.x - hi.x * s.x;
+        ol.y = lo.y * c.y - hi.y * s.y;
+        ol.z = lo.z * c.z - hi.z * s.z;
+        ol.w = lo.w * c.w - hi.w * s.w;
+        oh.x = hi.x * c.x + lo.x * s.x;
+        oh.y = hi.y * c.y + lo.y * s.y;
+        oh.z = hi.z * c.z + lo.z * s.z;
+        oh.w = hi.w * c.w + lo.w * s.w;
+        if (act) {
+            *reinterpret_cast<float4*>(v + j0) = ol;
+            *reinterpret_cast<float4*>(v + 64 + j0) = oh;
+        }
+    }
+}
+
+// Any even head_dim <= 1024: one wave per (token, head), two passes.
+template <int DT>
+__global__ __launch_bounds__(256) void qknorm_rope_generic_kernel(
+    float* q, float* k, long q_ld, long k_ld, const void* wq, const void* wk, const int32_t* pos,
+    const float* cos_tab, const float* sin_tab, int tab_len, const InvFreq inv, long T, int nq,
+    int nk, int head_dim, float eps) {
+    const int lane = threadIdx.x & 63;
+    const int nh = nq + nk;
+    const long gid = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (gid >= T * nh) return;
+    const long t = gid / nh;
+    const int h = (int)(gid % nh);
+    const bool isq = h < nq;
+    float* v = isq ? q + t * q_ld + (long)h * head_dim : k + t * k_ld + (long)(h - nq) * head_dim;
+    const void* w = isq ? wq : wk;
+    const int half = head_dim / 2;
+    float sc = 1.0f;
+    if (w) {
+        float ss = 0.f;
+        for (int j = lane; j < head_dim; j += 64) ss = fmaf(v[j], v[j], ss);
+        ss = wave_sum(ss);
+        sc = 1.0f / sqrtf(ss / (float)head_dim + eps);
+    }
+    const int p = pos[t];
+    const bool tab = p >= 0 && p < tab_len;
+    for (int j = lane; j < half; j += 64) {
+        float a = v[j], b = v[j + half];
+        if (w) {
+            a = (a * sc) * load_w<DT>(w, j);
+            b = (b * sc) * load_w<DT>(w, j + half);
+        }
+        float cc, ssn;
+        if (tab) {
+            cc = cos_tab[(long)p * half + j];
+            ssn = sin_tab[(long)p * half + j];
+        } else {
+            const float ang = (float)p * inv.v[j];
+            cc = cosf(ang);
+            ssn = sinf(ang);
+        }
+        v[j] = a * cc - b * ssn;
+        v[j + half] = b * cc + a * ssn;
+    }
+}
+
+// core/cpu_ops.cpp:56-80 for one token.  Table path: half-split over
+// rot_dim; fallback: adjacent pairs (2i, 2i+1), as the reference does.
+__global__ __launch_bounds__(256) void rope_cached_kernel(float* q, float* k, int nq, int nk,
+                                                          int q_stride, int k_stride, int rot_dim,
+                                                          int pos, const float* cos_row,
+                                                          const float* sin_row, const InvFreq inv) {
+    const int lane = threadIdx.x & 63;
+    const int h = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (h >= nq + nk) return;
+    float* v = h < nq ? q + (long)h * q_stride : k + (long)(h - nq) * k_stride;
+    const int half = rot_dim / 2;
+    for (int j = lane; j < half; j += 64) {
+        if (cos_row) {
+            const float c = cos_row[j], s = sin_row[j];
+            const float a = v[j], b = v[j + half];
+            v[j] = a * c - b * s;
+            v[j + half] = b * c + a * s;
+        } else {
+            const float ang = (float)pos * inv.v[j];
+            const float c = cosf(ang), s = sinf(ang);
+            const float a = v[2 * j], b = v[2 * j + 1];
+            v[2 * j] = a * c - b * s;
+            v[2 * j + 1] = a * s + b * c;
+        }
+    }
+}
+
+// models/llm/qwen3.cpp:210-218: cos/sin of the fp32 angle (float)pos*inv[j].
+__global__ __launch_bounds__(256) void rope_table_kernel(float* cos_tab, float* sin_tab, int n_pos,
+                                                         int half, const InvFreq inv) {
+    const long n = (long)n_pos * half;
+    for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long)gridDim.x * 256) {
+        const int p = (int)(i / half);
+        const int j = (int)(i % half);
+        const float ang = (float)p * inv.v[j];
+        cos_tab[i] = cosf(ang);
+        sin_tab[i] = sinf(ang);
+    }
+}
+
+}  // namespace anelm
+
+using namespace anelm;
+
+extern "C" int anelm_rmsnorm(float* out, const float* x, const void* w, int w_dtype, long rows,
+                             int dim, long ld_x, long ld_out, float eps, void* stream) {
+    if (!out || !x || !w) return fail(ANELM_ERR_INVALID, "anelm_rmsnorm: null pointer");
+    if (rows <= 0 || dim <= 0) return fail(ANELM_ERR_INVALID, "anelm_rmsnorm: rows=%ld dim=%d", rows, dim);
+    if (ld_x < dim || ld_out < dim) return fail(ANELM_ERR_INVALID, "anelm_rmsnorm: ld < dim");
+    if (rows > 0x7FFFFFFFL) return fail(ANELM_ERR_INVALID, "anelm_rmsnorm: too many rows");
+    clear_error();
+    return launch_rmsnorm<false>(out, const_cast<float*>(x), nullptr, w, w_dtype, rows, dim, ld_x, 0,
+                                 ld_out, eps, as_stream(stream));
+}
+
+extern "C" int anelm_add_rmsnorm(float* x, const float* y, float* out, const void* w, int w_dtype,
+                                 long rows, int dim, long ld_x, long ld_y, long ld_out, float eps,
+                                 void* stream) {
+    if (!out || !x || !y || !w) return fail(ANELM_ERR_INVALID, "anelm_add_rmsnorm: null pointer");
+    if (rows <= 0 || dim <= 0) return fail(ANELM_ERR_INVALID, "anelm_add_rmsnorm: rows=%ld dim=%d", rows, dim);
+    if (ld_x < dim || ld_y < dim || ld_out < dim) return fail(ANELM_ERR_INVALID, "anelm_add_rmsnorm: ld < dim");
+    if (out == x) return fail(ANELM_ERR_INVALID, "anelm_add_rmsnorm: out must not alias x");
+    if (rows > 0x7FFFFFFFL) return fail(ANELM_ERR_INVALID, "anelm_add_rmsnorm: too many rows");
+    clear_error();
+    return launch_rmsnorm<true>(out, x, y, w, w_dtype, rows, dim, ld_x, ld_y, ld_out, eps,
+                                as_stream(stream));
+}
+
+template <int DT>
+static int launch_qknorm(float* q, float* k, long q_ld, long k_ld, const void* wq, const void* wk,
+                         const int32_t* pos, const float* cos_tab, const float* sin_tab, int tab_len,
+                         const InvFreq& inv, long T, int nq, int nk, int head_dim, float eps,
+                         hipStream_t st) {
+    const bool fast = head_dim == 128 && aligned16(q) && aligned16(k) && q_ld % 4 == 0 &&
+                      k_ld % 4 == 0 && (tab_len == 0 || (aligned16(cos_tab) && aligned16(sin_tab))) &&
+                      (!wq || (DT == ANELM_F32 ? aligned16(wq) : aligned8(wq))) &&
+                      (!wk || (DT == ANELM_F32 ? aligned16(wk) : aligned8(wk)));
+    if (fast) {
+        qknorm_rope128_kernel<DT><<<dim3((unsigned)((T + 3) / 4)), dim3(256), 0, st>>>(
+            q, k, q_ld, k_ld, wq, wk, pos, cos_tab, sin_tab, tab_len, inv, T, nq, nk, eps);
+    } else {
+        const long waves = T * (nq + nk);
+        qknorm_rope_generic_kernel<DT><<<dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, st>>>(
+            q, k, q_ld, k_ld, wq, wk, pos, cos_tab, sin_tab, tab_len, inv, T, nq, nk, head_dim, eps);
+    }
+    return launch_status("qknorm_rope");
+}
+
+extern "C" int anelm_qknorm_rope(float* q, float* k, long q_ld, long k_ld, const void* wq,
+                                 const void* wk, int w_dtype, const int32_t* pos,
+                                 const float* cos_tab, const float* sin_tab, int tab_len, float theta,
+                                 long T, int nq, int nk, int head_dim, float eps, void* stream) {
+    if (!pos) return fail(ANELM_ERR_INVALID, "anelm_qknorm_rope: null pos");
+    if (T <= 0 || nq < 0 || nk < 0 || nq + nk == 0) return fail(ANELM_ERR_INVALID, "anelm_qknorm_rope: empty");
+    if ((nq > 0 && !q) || (nk > 0 && !k)) return fail(ANELM_ERR_INVALID, "anelm_qknorm_rope: null q/k");
+    if (head_dim <= 0 || head_dim % 2 || head_dim > 1024) return fail(ANELM_ERR_INVALID, "anelm_qknorm_rope: head_dim %d", head_dim);
+    if ((nq > 0 && q_ld < (long)nq * head_dim) || (nk > 0 && k_ld < (long)nk * head_dim))
+        return fail(ANELM_ERR_INVALID, "anelm_qknorm_rope: token stride too small");
+    if (tab_len < 0 || (tab_len > 0 && (!cos_tab || !sin_tab))) return fail(ANELM_ERR_INVALID, "anelm_qknorm_rope: table");
+    if (T * (nq + nk) / 4 + 1 > 0x7FFFFFFFL) return fail(ANELM_ERR_INVALID, "anelm_qknorm_rope: too large");
+    if (w_dtype < ANELM_F32 || w_dtype > ANELM_BF16) return fail(ANELM_ERR_INVALID, "anelm_qknorm_rope: dtype");
+    InvFreq inv;
+    rope_inv_freq(&inv, head_dim, theta);
+    clear_error();
+    hipStream_t st = as_stream(stream);
+    if (nq == 0) q = k;  // never dereferenced, keeps pointer arithmetic defined
+    if (nk == 0) k = q;
+    switch (w_dtype) {
+        case ANELM_F32: return launch_qknorm<ANELM_F32>(q, k, q_ld, k_ld, wq, wk, pos, cos_tab, sin_tab, tab_len, inv, T, nq, nk, head_dim, eps, st);
+        case ANELM_F16: return launch_qknorm<ANELM_F16>(q, k, q_ld, k_ld, wq, wk, pos, cos_tab, sin_tab, tab_len, inv, T, nq, nk, head_dim, eps, st);
+        default: return launch_qknorm<ANELM_BF16>(q, k, q_ld, k_ld, wq, wk, pos, cos_tab, sin_tab, tab_len, inv, T, nq, nk, head_dim, eps, st);
+    }
+}
+
+extern "C" int anelm_rope_cached(float* q, float* k, int n_q_heads, int n_kv_heads, int head_dim,
+                                 int q_head_stride, int k_head_stride, int rot_dim, int pos,
+                                 float theta, const float* cos_row, const float* sin_row,
+                                 void* stream) {
+    if (n_q_heads < 0 || n_kv_heads < 0 || n_q_heads + n_kv_heads == 0) return fail(ANELM_ERR_INVALID, "anelm_rope_cached: no heads");
+    if ((n_q_heads > 0 && !q) || (n_kv_heads > 0 && !k)) return fail(ANELM_ERR_INVALID, "anelm_rope_cached: null q/k");
+    if (rot_dim <= 0 || rot_dim % 2 || rot_dim > 1024 || rot_dim > head_dim) return fail(ANELM_ERR_INVALID, "anelm_rope_cached: rot_dim %d", rot_dim);
+    if ((cos_row == nullptr) != (sin_row == nullptr)) return fail(ANELM_ERR_INVALID, "anelm_rope_cached: one of cos/sin row missing");
+    InvFreq inv;
+    rope_inv_freq(&inv, rot_dim, theta);
+    clear_error();
+    if (n_q_heads == 0) q = k;
+    if (n_kv_heads == 0) k = q;
+    const int nh = n_q_heads + n_kv_heads;
+    rope_cached_kernel<<<dim3((unsigned)((nh + 3) / 4)), dim3(256), 0, as_stream(stream)>>>(
+        q, k, n_q_heads, n_kv_heads, q_head_stride, k_head_stride, rot_dim, pos, cos_row, sin_row, inv);
+    return launch_status("rope_cached");
+}
+
+extern "C" int anelm_rope_table(float* cos_tab, float* sin_tab, int n_pos, int rot_dim, float theta,
+                                void* stream) {
+    if (!cos_tab || !sin_tab) return fail(ANELM_ERR_INVALID, "anelm_rope_table: null pointer");
+    if (n_pos <= 0 || rot_dim <= 0 || rot_dim % 2 || rot_dim > 1024) return fail(ANELM_ERR_INVALID, "anelm_rope_table: n_pos=%d rot_dim=%d", n_pos, rot_dim);
+    InvFreq inv;
+    rope_inv_freq(&inv, rot_dim, theta);
+    clear_error();
+    const long n = (long)n_pos * (rot_dim / 2);
+    long blocks = (n + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    rope_table_kernel<<<dim3((unsigned)blocks), dim3(256), 0, as_stream(stream)>>>(cos_tab, sin_tab, n_pos, rot_dim / 2, inv);
+    return launch_status("rope_table");
+}

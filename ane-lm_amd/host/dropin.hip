@@ -1,0 +1,270 @@
+// The reference-signature drop-in layer (ane_lm::rmsnorm, ane_lm::softmax,
+// ane_lm::sample_token, ...) over the C ABI.  Host pointers in, host pointers
+// out: each call stages its operands into a per-thread device buffer, runs
+// the HIP kernels on a per-thread stream and copies the results back before
+// returning, so callers that run these functions concurrently from several
+// threads (as models/llm/qwen3.cpp:451-461 does) never share state.
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <vector>
+
+#include "anelm_hip.h"
+#include "ane_lm/convert.h"
+#include "ane_lm/cpu_ops.h"
+#include "ane_lm/sampling.h"
+
+namespace ane_lm {
+namespace {
+
+[[noreturn]] void die(const char* what, const char* msg) {
+    fprintf(stderr, "ane_lm (HIP): %s failed: %s\n", what, msg);
+    abort();
+}
+
+void check_rc(int rc, const char* what) {
+    if (rc != ANELM_OK) die(what, anelm_last_error());
+}
+
+void check_hip(hipError_t e, const char* what) {
+    if (e != hipSuccess) die(what, hipGetErrorString(e));
+}
+
+// Per-thread stream and growable device buffer.  They live until the
+// process ends (freed by the driver at exit), because the HIP runtime may
+// already be shut down when thread-local destructors run.
+struct Staging {
+    hipStream_t stream = nullptr;
+    char* buf = nullptr;
+    size_t cap = 0;
+
+    hipStream_t s() {
+        if (!stream) check_hip(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking), "hipStreamCreate");
+        return stream;
+    }
+    // Device memory for the given byte sizes, each 256-byte aligned.
+    template <size_t N>
+    void get(const size_t (&sizes)[N], char* (&out)[N]) {
+        size_t off[N], total = 0;
+        for (size_t i = 0; i < N; i++) {
+            off[i] = total;
+            total += (sizes[i] + 255) & ~(size_t)255;
+        }
+        if (total > cap) {
+            if (buf) check_hip(hipFree(buf), "hipFree");
+            size_t ncap = total < ((size_t)1 << 20) ? ((size_t)1 << 20) : total;
+            check_hip(hipMalloc(reinterpret_cast<void**>(&buf), ncap), "hipMalloc");
+            cap = ncap;
+        }
+        for (size_t i = 0; i < N; i++) out[i] = buf + off[i];
+    }
+    void h2d(void* d, const void* h, size_t n) { check_hip(hipMemcpyAsync(d, h, n, hipMemcpyHostToDevice, s()), "hipMemcpy H2D"); }
+    void d2h(void* h, const void* d, size_t n) { check_hip(hipMemcpyAsync(h, d, n, hipMemcpyDeviceToHost, s()), "hipMemcpy D2H"); }
+    void sync() { check_hip(hipStreamSynchronize(s()), "hipStreamSynchronize"); }
+};
+
+thread_local Staging t_stage;
+
+}  // namespace
+
+// core/cpu_ops.cpp:7-14
+void silu_vec_inplace(float* x, int n, float* /*tmp*/) {
+    if (n <= 0) return;
+    Staging& S = t_stage;
+    const size_t sz[1] = {(size_t)n * 4};
+    char* d[1];
+    S.get(sz, d);
+    S.h2d(d[0], x, sz[0]);
+    check_rc(anelm_silu(reinterpret_cast<float*>(d[0]), (size_t)n, S.s()), "silu_vec_inplace");
+    S.d2h(x, d[0], sz[0]);
+    S.sync();
+}
+
+// core/cpu_ops.cpp:16-23
+void mul_sigmoid_inplace(float* y, const float* z, int n, float* /*tmp*/) {
+    if (n <= 0) return;
+    Staging& S = t_stage;
+    const size_t sz[2] = {(size_t)n * 4, (size_t)n * 4};
+    char* d[2];
+    S.get(sz, d);
+    S.h2d(d[0], y, sz[0]);
+    S.h2d(d[1], z, sz[1]);
+    check_rc(anelm_mul_sigmoid(reinterpret_cast<float*>(d[0]), reinterpret_cast<const float*>(d[1]), (size_t)n, S.s()),
+             "mul_sigmoid_inplace");
+    S.d2h(y, d[0], sz[0]);
+    S.sync();
+}
+
+// core/cpu_ops.cpp:25-31
+void rmsnorm(float* out, const float* x, const float* weight, int dim, float eps) {
+    if (dim <= 0) return;
+    Staging& S = t_stage;
+    const size_t sz[2] = {(size_t)dim * 4, (size_t)dim * 4};
+    char* d[2];
+    S.get(sz, d);
+    S.h2d(d[0], x, sz[0]);
+    S.h2d(d[1], weight, sz[1]);
+    float* dx = reinterpret_cast<float*>(d[0]);
+    check_rc(anelm_rmsnorm(dx, dx, d[1], ANELM_F32, 1, dim, dim, dim, eps, S.s()), "rmsnorm");
+    S.d2h(out, d[0], sz[0]);
+    S.sync();
+}
+
+// core/cpu_ops.cpp:56-80
+void apply_rope_cached(float* q, float* k, int n_q_heads, int n_kv_heads, int head_dim, int q_head_stride,
+                       int k_head_stride, int rot_dim, int pos, float theta, const float* cos_row,
+                       const float* sin_row) {
+    const int nh = n_q_heads + n_kv_heads;
+    if (nh <= 0 || rot_dim <= 0) return;
+    Staging& S = t_stage;
+    // span of each operand that the rotation touches
+    const size_t qn = n_q_heads > 0 ? (size_t)(n_q_heads - 1) * q_head_stride + rot_dim : 0;
+    const size_t kn = n_kv_heads > 0 ? (size_t)(n_kv_heads - 1) * k_head_stride + rot_dim : 0;
+    const bool tab = cos_row && sin_row;
+    const size_t half = (size_t)rot_dim / 2;
+    const size_t sz[4] = {qn * 4, kn * 4, tab ? half * 4 : 0, tab ? half * 4 : 0};
+    char* d[4];
+    S.get(sz, d);
+    if (qn) S.h2d(d[0], q, sz[0]);
+    if (kn) S.h2d(d[1], k, sz[1]);
+    if (tab) {
+        S.h2d(d[2], cos_row, sz[2]);
+        S.h2d(d[3], sin_row, sz[3]);
+    }
+    check_rc(anelm_rope_cached(qn ? reinterpret_cast<float*>(d[0]) : nullptr, kn ? reinterpret_cast<float*>(d[1]) : nullptr,
+                               n_q_heads, n_kv_heads, head_dim, q_head_stride, k_head_stride, rot_dim, pos, theta,
+                               tab ? reinterpret_cast<const float*>(d[2]) : nullptr,
+                               tab ? reinterpret_cast<const float*>(d[3]) : nullptr, S.s()),
+             "apply_rope_cached");
+    if (qn) S.d2h(q, d[0], sz[0]);
+    if (kn) S.d2h(k, d[1], sz[1]);
+    S.sync();
+}
+
+// core/cpu_ops.cpp:83-99
+void softmax(float* x, int n) {
+    if (n <= 0) return;
+    Staging& S = t_stage;
+    const size_t ws = anelm_softmax_workspace_size(1, n);
+    const size_t sz[2] = {(size_t)n * 4, ws};
+    char* d[2];
+    S.get(sz, d);
+    S.h2d(d[0], x, sz[0]);
+    check_rc(anelm_softmax(reinterpret_cast<float*>(d[0]), 1, n, n, d[1], ws, S.s()), "softmax");
+    S.d2h(x, d[0], sz[0]);
+    S.sync();
+}
+
+// core/sampling.cpp:10-66
+int sample_token(const float* logits, int vocab_size, const SamplingParams& params,
+                 const std::vector<int>& recent_tokens) {
+    if (vocab_size <= 0) die("sample_token", "vocab_size <= 0");
+    Staging& S = t_stage;
+    const long nh = (long)recent_tokens.size();
+    const size_t ws = anelm_sample_workspace_size(1, vocab_size);
+    const size_t sz[5] = {(size_t)vocab_size * 4, (size_t)(nh > 0 ? nh : 1) * 4, 16, 16, ws};
+    char* d[5];
+    S.get(sz, d);
+    S.h2d(d[0], logits, sz[0]);
+    if (nh > 0) S.h2d(d[1], recent_tokens.data(), (size_t)nh * 4);
+    const bool draw = params.temperature > 0.0f;
+    // the reference's draw (sampling.cpp:58), only on the sampling path
+    const float r = draw ? (float)drand48() : 0.0f;
+    S.h2d(d[2], &r, 4);
+    anelm_sampling_params p;
+    p.temperature = params.temperature;
+    p.repetition_penalty = params.repetition_penalty;
+    p.repetition_context_size = params.repetition_context_size;
+    p.frequency_penalty = params.frequency_penalty;
+    check_rc(anelm_sample(reinterpret_cast<int32_t*>(d[3]), nullptr, 0, reinterpret_cast<const float*>(d[0]),
+                          vocab_size, 1, vocab_size, nh > 0 ? reinterpret_cast<const int32_t*>(d[1]) : nullptr, nh,
+                          nullptr, &p, reinterpret_cast<const float*>(d[2]), d[4], ws, S.s()),
+             "sample_token");
+    int32_t id = 0;
+    S.d2h(&id, d[3], 4);
+    S.sync();
+    return id;
+}
+
+namespace hip {
+
+void residual_add(float* x, const float* y, int n) {
+    if (n <= 0) return;
+    Staging& S = t_stage;
+    const size_t sz[2] = {(size_t)n * 4, (size_t)n * 4};
+    char* d[2];
+    S.get(sz, d);
+    S.h2d(d[0], x, sz[0]);
+    S.h2d(d[1], y, sz[1]);
+    check_rc(anelm_residual_add(reinterpret_cast<float*>(d[0]), reinterpret_cast<const float*>(d[1]), (size_t)n, S.s()),
+             "residual_add");
+    S.d2h(x, d[0], sz[0]);
+    S.sync();
+}
+
+void qknorm_rope_qwen3(float* q, float* k, int nq, int nk, int head_dim, const float* q_norm, const float* k_norm,
+                       float eps, int pos, float theta, const float* cos_row, const float* sin_row) {
+    if (nq + nk <= 0 || head_dim <= 0) return;
+    Staging& S = t_stage;
+    const size_t qn = (size_t)nq * head_dim, kn = (size_t)nk * head_dim, half = (size_t)head_dim / 2;
+    const bool tab = cos_row && sin_row;
+    const size_t sz[7] = {qn * 4, kn * 4, (size_t)head_dim * 4, (size_t)head_dim * 4, half * 4, half * 4, 4};
+    char* d[7];
+    S.get(sz, d);
+    if (qn) S.h2d(d[0], q, sz[0]);
+    if (kn) S.h2d(d[1], k, sz[1]);
+    if (q_norm) S.h2d(d[2], q_norm, sz[2]);
+    if (k_norm) S.h2d(d[3], k_norm, sz[3]);
+    if (tab) {
+        S.h2d(d[4], cos_row, sz[4]);
+        S.h2d(d[5], sin_row, sz[5]);
+    }
+    // with a table the row is passed as a one-row table at position 0
+    const int32_t p = tab ? 0 : pos;
+    S.h2d(d[6], &p, 4);
+    check_rc(anelm_qknorm_rope(qn ? reinterpret_cast<float*>(d[0]) : nullptr, kn ? reinterpret_cast<float*>(d[1]) : nullptr,
+                               (long)qn, (long)kn, q_norm ? d[2] : nullptr, k_norm ? d[3] : nullptr, ANELM_F32,
+                               reinterpret_cast<const int32_t*>(d[6]), tab ? reinterpret_cast<const float*>(d[4]) : nullptr,
+                               tab ? reinterpret_cast<const float*>(d[5]) : nullptr, tab ? 1 : 0, theta, 1, nq, nk, head_dim,
+                               eps, S.s()),
+             "qknorm_rope_qwen3");
+    if (qn) S.d2h(q, d[0], sz[0]);
+    if (kn) S.d2h(k, d[1], sz[1]);
+    S.sync();
+}
+
+void silu_mul(float* h, const float* g, const float* u, int n) {
+    if (n <= 0) return;
+    Staging& S = t_stage;
+    const size_t sz[2] = {(size_t)n * 4, (size_t)n * 4};
+    char* d[2];
+    S.get(sz, d);
+    S.h2d(d[0], g, sz[0]);
+    S.h2d(d[1], u, sz[1]);
+    float* dg = reinterpret_cast<float*>(d[0]);
+    check_rc(anelm_silu_mul(dg, dg, reinterpret_cast<const float*>(d[1]), 1, n, n, n, n, S.s()), "silu_mul");
+    S.d2h(h, d[0], sz[0]);
+    S.sync();
+}
+
+void bf16_to_f16_vec_n(uint16_t* out, const uint16_t* in, size_t n) {
+    if (n == 0) return;
+    Staging& S = t_stage;
+    const size_t sz[1] = {n * 2};
+    char* d[1];
+    S.get(sz, d);
+    S.h2d(d[0], in, sz[0]);
+    uint16_t* dp = reinterpret_cast<uint16_t*>(d[0]);
+    check_rc(anelm_bf16_to_f16(dp, dp, n, S.s()), "bf16_to_f16_vec");
+    S.d2h(out, d[0], sz[0]);
+    S.sync();
+}
+
+void bf16_to_f16_vec(uint16_t* out, const uint16_t* in, int n) {
+    if (n > 0) bf16_to_f16_vec_n(out, in, (size_t)n);
+}
+
+}  // namespace hip
+}  // namespace ane_lm

@@ -1,0 +1,187 @@
+/*
+ * anelm_hip.h -- C ABI of the MI355X (gfx950) fused layer-op library
+ * (libanelm_hip.so).
+ *
+ * Replaces the host-side hot path of Lolendorka/ANE-LM: core/cpu_ops
+ * (RMSNorm, per-head q/k RMSNorm, RoPE, SiLU/SwiGLU, softmax), the inline
+ * ops of models/llm/qwen3.cpp (embedding gather, residual add, the RoPE
+ * table), core/sampling (penalties, temperature, softmax, categorical draw)
+ * and the bf16->fp16 weight convert of include/ane_lm/common.h.
+ *
+ * Conventions
+ *  - every pointer argument is a DEVICE pointer unless stated otherwise;
+ *  - `stream` is a hipStream_t (NULL = the default stream); every call is
+ *    asynchronous on it and performs no allocation and no synchronisation;
+ *  - element counts and strides are in elements, never bytes;
+ *  - return 0 (ANELM_OK) or a negative ANELM_ERR_*; on error nothing was
+ *    launched and nothing was written, and anelm_last_error() (per thread)
+ *    describes the failure;
+ *  - calls are reentrant: no global mutable state besides the per-thread
+ *    error string;
+ *  - fp32 arithmetic follows the reference's formulas with correctly rounded
+ *    division and square root; no fast-math anywhere.
+ *
+ * The C++ drop-in layer with the reference's own signatures
+ * (ane_lm::rmsnorm, ane_lm::sample_token, ...) is declared in
+ * ane-lm_amd/host/ane_lm/{cpu_ops,sampling,convert}.h and is built into the
+ * same library.
+ */
+#ifndef ANELM_HIP_H
+#define ANELM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ANELM_OK             0
+#define ANELM_ERR_INVALID  (-1)  /* null pointer, bad size, stride or alignment */
+#define ANELM_ERR_RANGE    (-2)  /* a host-visible index out of range */
+#define ANELM_ERR_HIP      (-3)  /* the HIP runtime reported an error */
+#define ANELM_ERR_WORKSPACE (-4) /* workspace missing or too small */
+
+/* storage types of weights / tables */
+#define ANELM_F32  0
+#define ANELM_F16  1
+#define ANELM_BF16 2
+
+/* Description of the last error on the calling thread ("" if none). */
+const char* anelm_last_error(void);
+/* Library version, major*10000 + minor*100 + patch. */
+int anelm_version(void);
+
+/* ---------------------------------------------------------------- norms */
+
+/* RMSNorm over `rows` rows of `dim` floats:
+ *   out[r,:] = (x[r,:] * s) * w,  s = 1/sqrtf(sum(x^2)/dim + eps)
+ * Replaces ane_lm::rmsnorm, core/cpu_ops.h:21 / core/cpu_ops.cpp:25-31
+ * (callers models/llm/qwen3.cpp:503, :518, :530), batched over rows.
+ * w has `dim` entries of type w_dtype (ANELM_F32/F16/BF16).  out may equal x. */
+int anelm_rmsnorm(float* out, const float* x, const void* w, int w_dtype, long rows, int dim,
+                  long ld_x, long ld_out, float eps, void* stream);
+
+/* Fused residual add + RMSNorm:  x[r,:] += y[r,:];  out[r,:] = rmsnorm(x[r,:]).
+ * Replaces the pair vDSP_vadd(x_, attn_out, x_) + rmsnorm(x_norm_, x_, ...)
+ * of models/llm/qwen3.cpp:516-518.  y may equal out (the reference's
+ * attn_out aliases x_norm_). */
+int anelm_add_rmsnorm(float* x, const float* y, float* out, const void* w, int w_dtype, long rows,
+                      int dim, long ld_x, long ld_y, long ld_out, float eps, void* stream);
+
+/* Per-head q/k RMSNorm followed by Qwen3 half-split RoPE, in place, for T
+ * tokens.  q[t*q_ld + h*head_dim + d] (h < nq), k likewise with k_ld, nk.
+ * wq / wk: head_dim gammas shared by all q (k) heads; NULL skips that norm.
+ * pos[t] selects row pos[t] of cos_tab/sin_tab ([tab_len, head_dim/2]) when
+ * 0 <= pos[t] < tab_len; otherwise the angle pos*inv_freq[j] is evaluated
+ * on the fly with inv_freq[j] = 1/powf(theta, 2j/head_dim) computed on the
+ * host exactly as the reference does.
+ * Replaces models/llm/qwen3.cpp:444-472 (qk-norm via ane_lm::rmsnorm, then
+ * the static apply_rope_qwen3 :28-52, row choice :463-469). */
+int anelm_qknorm_rope(float* q, float* k, long q_ld, long k_ld, const void* wq, const void* wk,
+                      int w_dtype, const int32_t* pos, const float* cos_tab, const float* sin_tab,
+                      int tab_len, float theta, long T, int nq, int nk, int head_dim, float eps,
+                      void* stream);
+
+/* ane_lm::apply_rope_cached semantics (core/cpu_ops.h:26-29,
+ * core/cpu_ops.cpp:56-80) for ONE token: heads at q + h*q_head_stride and
+ * k + h*k_head_stride, the first rot_dim elements rotated.  With a table row
+ * (cos_row/sin_row non-NULL, rot_dim/2 entries) the pairs are (j, j+rot_dim/2);
+ * without one the reference's fallback rotates ADJACENT pairs (2i, 2i+1)
+ * with freq 1/powf(theta, 2i/rot_dim) and angle pos*freq. */
+int anelm_rope_cached(float* q, float* k, int n_q_heads, int n_kv_heads, int head_dim,
+                      int q_head_stride, int k_head_stride, int rot_dim, int pos, float theta,
+                      const float* cos_row, const float* sin_row, void* stream);
+
+/* RoPE table: cos_tab/sin_tab[p*(rot_dim/2) + j] = cos/sin(p * inv_freq[j]),
+ * inv_freq as above, for p in [0, n_pos).  Replaces the load-time loop of
+ * models/llm/qwen3.cpp:200-219.  rot_dim even, <= 1024. */
+int anelm_rope_table(float* cos_tab, float* sin_tab, int n_pos, int rot_dim, float theta,
+                     void* stream);
+
+/* ---------------------------------------------------------- elementwise */
+
+/* Residual add x[i] += y[i] (one IEEE add; bit-exact).
+ * Replaces vDSP_vadd at models/llm/qwen3.cpp:516 and :527. */
+int anelm_residual_add(float* x, const float* y, size_t n, void* stream);
+
+/* SwiGLU in fp32: h[r,i] = (g / (1 + expf(-g))) * u  for rows x inter.
+ * Op order of the reference's fused_ffn (core/ane_runtime.cpp:393-395) with
+ * silu in the core/cpu_ops.cpp:7-14 form.  h may equal g or u. */
+int anelm_silu_mul(float* h, const float* g, const float* u, long rows, long inter, long ld_h,
+                   long ld_g, long ld_u, void* stream);
+
+/* x[i] = x[i] / (1 + expf(-x[i]))    -- ane_lm::silu_vec_inplace, cpu_ops.h:16 */
+int anelm_silu(float* x, size_t n, void* stream);
+/* y[i] = y[i] / (1 + expf(-z[i]))    -- ane_lm::mul_sigmoid_inplace, cpu_ops.h:17 */
+int anelm_mul_sigmoid(float* y, const float* z, size_t n, void* stream);
+
+/* Embedding gather: out[b,:] = table[ids[b],:] widened exactly to fp32
+ * (table_dtype ANELM_F32 copy, ANELM_F16 as f16_to_f32 common.h:35-56 incl.
+ * NaN payloads, ANELM_BF16 as bf16_to_f32 common.h:21-26).
+ * Replaces the memcpy of models/llm/qwen3.cpp:498, batched.  ids live in
+ * device memory, so range errors are reported on the device: a row whose id
+ * is outside [0, vocab) is not written and, if bad_count is non-NULL,
+ * *bad_count is incremented once for it. */
+int anelm_embed_gather(float* out, const void* table, int table_dtype, const int32_t* ids,
+                       long n_ids, long hidden, long vocab, int32_t* bad_count, void* stream);
+
+/* ---------------------------------------------------------- conversions */
+
+/* bf16 -> fp16, bit-exact with the reference's TRUNCATING convert
+ * (bf16_to_f16_vec, include/ane_lm/common.h:73-83: round toward zero,
+ * below 2^-25 -> +-0, overflow and NaN -> +-Inf).  Integer arithmetic only.
+ * Replaces the per-weight loop at core/safetensors.cpp:335 (write_ane_blob)
+ * and core/ane_runtime.cpp:207 (build_weight_blob).  dst may equal src. */
+int anelm_bf16_to_f16(uint16_t* dst, const uint16_t* src, size_t n, void* stream);
+/* bf16 -> fp32 (bf16_to_f32_vec, common.h:77-79; used by load_bf16_to_f32,
+ * core/safetensors.cpp:266-281). */
+int anelm_bf16_to_f32(float* dst, const uint16_t* src, size_t n, void* stream);
+/* fp16 -> fp32 exact widening (f16_to_f32, common.h:35-56). */
+int anelm_f16_to_f32(float* dst, const uint16_t* src, size_t n, void* stream);
+
+/* ---------------------------------------------------- softmax / sampling */
+
+/* Row softmax in place over `rows` rows of n floats at stride ld
+ * (ane_lm::softmax, core/cpu_ops.h:33 / core/cpu_ops.cpp:83-99):
+ * max, x - max, exp, sum, x * (1/sum).  The exp is a fixed <= 1 ulp
+ * sequence of IEEE operations and the sum an exact integer fixed-point sum
+ * rounded once, so results do not depend on launch geometry.
+ * Needs anelm_softmax_workspace_size(rows, n) bytes of device workspace. */
+size_t anelm_softmax_workspace_size(long rows, long n);
+int anelm_softmax(float* x, long rows, long n, long ld, void* workspace, size_t workspace_bytes,
+                  void* stream);
+
+/* Sampling parameters; field meaning and defaults of ane_lm::SamplingParams
+ * (core/sampling.h:7-12): 0.6, 1.2, 256, 0.1. */
+typedef struct anelm_sampling_params {
+    float temperature;
+    float repetition_penalty;
+    int   repetition_context_size;
+    float frequency_penalty;
+} anelm_sampling_params;
+
+/* Batched ane_lm::sample_token (core/sampling.h:14-16, core/sampling.cpp:10-66)
+ * over `rows` independent rows of `vocab` logits at stride ld_logits
+ * (logits are not modified):
+ *  - history row b: hist[b*hist_ld + j], j < (hist_len ? hist_len[b] : hist_ld);
+ *    the last repetition_context_size entries are used, ids outside
+ *    [0, vocab) ignored; each distinct id gets the repetition penalty once
+ *    (l>0 ? l/rep : l*rep, only if rep > 1) then l -= freq*count (if freq > 0);
+ *  - temperature <= 0: ids[b] = first argmax, r and probs untouched;
+ *  - else x *= 1/T, softmax (as anelm_softmax) written to probs (stride
+ *    ld_probs; may be NULL), then ids[b] = first i whose SEQUENTIAL fp32
+ *    running sum p[0]+...+p[i] is >= r[b], or vocab-1 if none -- computed
+ *    exactly, identical to the reference's walk (sampling.cpp:59-65).
+ * r[b] is the uniform draw (the reference's (float)drand48()).
+ * Needs anelm_sample_workspace_size(rows, vocab) bytes of device workspace. */
+size_t anelm_sample_workspace_size(long rows, long vocab);
+int anelm_sample(int32_t* ids, float* probs, long ld_probs, const float* logits, long ld_logits,
+                 long rows, long vocab, const int32_t* hist, long hist_ld,
+                 const int32_t* hist_len, const anelm_sampling_params* params, const float* r,
+                 void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,248 @@
+"""numpy binding of the CPU oracle (liboracle.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
+the cpu_baseline leg of bench.py as the checker.  The product never uses it.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+
+_P, _L, _I, _F, _S = ctypes.c_void_p, ctypes.c_long, ctypes.c_int, ctypes.c_float, ctypes.c_size_t
+_U16 = ctypes.c_uint16
+
+_SIGS = {
+    "orc_bf16_to_f32": (_F, [_U16]),
+    "orc_f32_to_bf16": (_U16, [_F]),
+    "orc_f16_to_f32": (_F, [_U16]),
+    "orc_f32_to_f16": (_U16, [_F]),
+    "orc_bf16_to_f16": (_U16, [_U16]),
+    "orc_bf16_to_f16_vec": (None, [_P, _P, _S, _I]),
+    "orc_bf16_to_f32_vec": (None, [_P, _P, _S]),
+    "orc_f16_to_f32_vec": (None, [_P, _P, _S]),
+    "orc_rmsnorm": (None, [_P, _P, _P, _I, _F]),
+    "orc_rmsnorm_rows": (None, [_P, _P, _P, _L, _I, _L, _L, _F, _I]),
+    "orc_silu_vec": (None, [_P, _S]),
+    "orc_mul_sigmoid": (None, [_P, _P, _S]),
+    "orc_silu_mul": (None, [_P, _P, _P, _S, _I]),
+    "orc_rope_inv_freq": (None, [_P, _I, _F]),
+    "orc_rope_table": (None, [_P, _P, _I, _I, _F]),
+    "orc_rope_qwen3": (None, [_P, _P, _I, _I, _I, _I, _F, _P, _P]),
+    "orc_rope_cached": (None, [_P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _P, _P]),
+    "orc_qknorm_rope": (None, [_P, _P, _L, _L, _P, _P, _P, _P, _P, _I, _F, _L, _I, _I, _I, _F, _I]),
+    "orc_residual_add": (None, [_P, _P, _S, _I]),
+    "orc_embed_gather": (_I, [_P, _P, _I, _P, _L, _L, _L]),
+    "orc_sampler_expf": (_F, [_F]),
+    "orc_softmax": (None, [_P, _I]),
+    "orc_softmax_shift": (_I, [_L]),
+    "orc_sample_token": (_I, [_P, _I, _F, _F, _I, _F, _P, _I, _F, _P]),
+    "orc_cdf_walk": (_I, [_P, _I, _F]),
+    "orc_layer_chain": (None, [_L, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                               _P, _P, _I, _F, _F, _I]),
+    "orc_max_threads": (_I, []),
+}
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} not built (make -C oracle)")
+        l = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(l, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = l
+    return _lib
+
+
+def _p(a):
+    return None if a is None else ctypes.c_void_p(a.ctypes.data)
+
+
+def _c(a, dtype):
+    a = np.ascontiguousarray(a, dtype=dtype)
+    return a
+
+
+# ---------------------------------------------------------------- converts
+
+def bf16_to_f16(bits: np.ndarray, nthreads: int = 0) -> np.ndarray:
+    src = _c(bits, np.uint16)
+    out = np.empty_like(src)
+    lib().orc_bf16_to_f16_vec(_p(out), _p(src), src.size, nthreads)
+    return out
+
+
+def f16_to_f32(bits: np.ndarray) -> np.ndarray:
+    src = _c(bits, np.uint16)
+    out = np.empty(src.shape, np.float32)
+    lib().orc_f16_to_f32_vec(_p(out), _p(src), src.size)
+    return out
+
+
+def bf16_to_f32(bits: np.ndarray) -> np.ndarray:
+    src = _c(bits, np.uint16)
+    out = np.empty(src.shape, np.float32)
+    lib().orc_bf16_to_f32_vec(_p(out), _p(src), src.size)
+    return out
+
+
+def f32_to_f16_scalar(x: float) -> int:
+    return lib().orc_f32_to_f16(x)
+
+
+def f32_to_bf16(x: np.ndarray) -> np.ndarray:
+    """Truncating fp32 -> bf16 bits (include/ane_lm/common.h:28-32)."""
+    return (_c(x, np.float32).view(np.uint32) >> 16).astype(np.uint16)
+
+
+# ---------------------------------------------------------------- norms
+
+def rmsnorm_rows(x: np.ndarray, w: np.ndarray, eps: float = 1e-6, nthreads: int = 0) -> np.ndarray:
+    x = _c(x, np.float32)
+    w = _c(w, np.float32)
+    rows, dim = x.shape
+    out = np.empty_like(x)
+    lib().orc_rmsnorm_rows(_p(out), _p(x), _p(w), rows, dim, dim, dim, eps, nthreads)
+    return out
+
+
+def rmsnorm(x: np.ndarray, w: np.ndarray, eps: float = 1e-6) -> np.ndarray:
+    x = _c(x, np.float32)
+    out = np.empty_like(x)
+    lib().orc_rmsnorm(_p(out), _p(x), _p(_c(w, np.float32)), x.size, eps)
+    return out
+
+
+def silu(x: np.ndarray) -> np.ndarray:
+    y = _c(x, np.float32).copy()
+    lib().orc_silu_vec(_p(y), y.size)
+    return y
+
+
+def mul_sigmoid(y: np.ndarray, z: np.ndarray) -> np.ndarray:
+    y = _c(y, np.float32).copy()
+    z = _c(z, np.float32)
+    lib().orc_mul_sigmoid(_p(y), _p(z), y.size)
+    return y
+
+
+def silu_mul(g: np.ndarray, u: np.ndarray, nthreads: int = 0) -> np.ndarray:
+    g = _c(g, np.float32)
+    u = _c(u, np.float32)
+    h = np.empty_like(g)
+    lib().orc_silu_mul(_p(h), _p(g), _p(u), g.size, nthreads)
+    return h
+
+
+def residual_add(x: np.ndarray, y: np.ndarray, nthreads: int = 0) -> np.ndarray:
+    x = _c(x, np.float32).copy()
+    lib().orc_residual_add(_p(x), _p(_c(y, np.float32)), x.size, nthreads)
+    return x
+
+
+# ---------------------------------------------------------------- RoPE
+
+def rope_inv_freq(rot_dim: int, theta: float) -> np.ndarray:
+    out = np.empty(rot_dim // 2, np.float32)
+    lib().orc_rope_inv_freq(_p(out), rot_dim, theta)
+    return out
+
+
+def rope_table(n_pos: int, rot_dim: int, theta: float):
+    c = np.empty((n_pos, rot_dim // 2), np.float32)
+    s = np.empty_like(c)
+    lib().orc_rope_table(_p(c), _p(s), n_pos, rot_dim, theta)
+    return c, s
+
+
+def qknorm_rope(q, k, wq, wk, pos, cos_tab, sin_tab, theta, nq, nk, head_dim, eps=1e-6, nthreads=0):
+    """q: [T, q_ld], k: [T, k_ld] (copied); returns (q', k')."""
+    q = _c(q, np.float32).copy()
+    k = _c(k, np.float32).copy()
+    pos = _c(pos, np.int32)
+    T = pos.shape[0]
+    tab_len = 0 if cos_tab is None else cos_tab.shape[0]
+    lib().orc_qknorm_rope(_p(q), _p(k), q.shape[1], k.shape[1], _p(None if wq is None else _c(wq, np.float32)),
+                          _p(None if wk is None else _c(wk, np.float32)), _p(pos),
+                          _p(None if cos_tab is None else _c(cos_tab, np.float32)),
+                          _p(None if sin_tab is None else _c(sin_tab, np.float32)), tab_len, theta, T, nq, nk,
+                          head_dim, eps, nthreads)
+    return q, k
+
+
+def rope_cached(q, k, n_q_heads, n_kv_heads, head_dim, q_head_stride, k_head_stride, rot_dim, pos, theta,
+                cos_row=None, sin_row=None):
+    q = _c(q, np.float32).copy()
+    k = _c(k, np.float32).copy()
+    lib().orc_rope_cached(_p(q), _p(k), n_q_heads, n_kv_heads, head_dim, q_head_stride, k_head_stride, rot_dim,
+                          pos, theta, _p(None if cos_row is None else _c(cos_row, np.float32)),
+                          _p(None if sin_row is None else _c(sin_row, np.float32)))
+    return q, k
+
+
+# ---------------------------------------------------------------- gather
+
+def embed_gather(table: np.ndarray, ids: np.ndarray, dtype_code: int):
+    """dtype_code 0 fp32 table, 1 fp16 bits, 2 bf16 bits."""
+    table = np.ascontiguousarray(table)
+    ids = _c(ids, np.int32)
+    vocab, hidden = table.shape
+    out = np.empty((ids.shape[0], hidden), np.float32)
+    rc = lib().orc_embed_gather(_p(out), _p(table), dtype_code, _p(ids), ids.shape[0], hidden, vocab)
+    if rc != 0:
+        raise IndexError("embedding id out of range")
+    return out
+
+
+# ---------------------------------------------------------------- sampling
+
+def sampler_expf(x: float) -> float:
+    return lib().orc_sampler_expf(x)
+
+
+def softmax(x: np.ndarray) -> np.ndarray:
+    y = _c(x, np.float32).copy()
+    lib().orc_softmax(_p(y), y.size)
+    return y
+
+
+def softmax_shift(n: int) -> int:
+    return lib().orc_softmax_shift(n)
+
+
+def sample_token(logits: np.ndarray, temperature=0.6, repetition_penalty=1.2, repetition_context_size=256,
+                 frequency_penalty=0.1, recent=None, r=0.0, want_probs=False):
+    logits = _c(logits, np.float32)
+    V = logits.size
+    rec = _c(recent if recent is not None else np.zeros(0, np.int32), np.int32)
+    probs = np.empty(V, np.float32) if want_probs else None
+    tok = lib().orc_sample_token(_p(logits), V, temperature, repetition_penalty, repetition_context_size,
+                                 frequency_penalty, _p(rec) if rec.size else None, rec.size, r, _p(probs))
+    return (tok, probs) if want_probs else tok
+
+
+def cdf_walk(p: np.ndarray, r: float) -> int:
+    p = _c(p, np.float32)
+    return lib().orc_cdf_walk(_p(p), p.size, r)
+
+
+def layer_chain(T, H, nq, nk, D, I, x, xn, attn_out, mlp_out, q, k, g, u, h, w_in, w_post, wq, wk, pos, cos_tab,
+                sin_tab, theta, eps, nthreads=0):
+    """In place on x, xn, q, k, h (contiguous float32 numpy arrays)."""
+    lib().orc_layer_chain(T, H, nq, nk, D, I, _p(x), _p(xn), _p(attn_out), _p(mlp_out), _p(q), _p(k), _p(g), _p(u),
+                          _p(h), _p(w_in), _p(w_post), _p(wq), _p(wk), _p(pos), _p(cos_tab), _p(sin_tab),
+                          cos_tab.shape[0], theta, eps, nthreads)
+
+
+def max_threads() -> int:
+    return lib().orc_max_threads()

@@ -1,0 +1,193 @@
+// Calls the ane_lm:: drop-in functions exactly as the reference's model and
+// generation code do (host pointers, reference signatures) and compares each
+// with the CPU oracle on the same seeded inputs.  Prints one PASS/FAIL line
+// per check; exit status 0 only if all pass.  Needs a GPU.
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <random>
+#include <thread>
+#include <vector>
+
+#include "anelm_oracle.h"
+#include "ane_lm/convert.h"
+#include "ane_lm/cpu_ops.h"
+#include "ane_lm/sampling.h"
+
+static int g_fail = 0;
+
+static void report(bool ok, const char* name, double err) {
+    printf("%s %s (err %.3g)\n", ok ? "PASS" : "FAIL", name, err);
+    if (!ok) g_fail++;
+}
+
+static double max_rel(const float* a, const float* b, size_t n) {
+    double m = 0;
+    for (size_t i = 0; i < n; i++) {
+        double d = std::fabs((double)a[i] - b[i]) / std::fmax(std::fabs((double)b[i]), 1e-30);
+        if (d > m || std::isnan(d)) m = std::isnan(d) ? INFINITY : d;
+    }
+    return m;
+}
+
+static bool same_bits(const void* a, const void* b, size_t bytes) { return std::memcmp(a, b, bytes) == 0; }
+
+int main() {
+    std::mt19937 gen(1234);
+    std::normal_distribution<float> nd(0.f, 1.f);
+    auto randv = [&](size_t n, float scale = 1.f) {
+        std::vector<float> v(n);
+        for (auto& x : v) x = nd(gen) * scale;
+        return v;
+    };
+
+    // rmsnorm (qwen3.cpp:503), out != x and out == x (qwen3.cpp:530)
+    {
+        const int dim = 1024;
+        auto x = randv(dim), w = randv(dim, 0.02f);
+        for (auto& e : w) e += 1.f;
+        std::vector<float> out(dim), ref(dim);
+        ane_lm::rmsnorm(out.data(), x.data(), w.data(), dim, 1e-6f);
+        orc_rmsnorm(ref.data(), x.data(), w.data(), dim, 1e-6f);
+        report(max_rel(out.data(), ref.data(), dim) <= 1e-5, "rmsnorm", max_rel(out.data(), ref.data(), dim));
+        ane_lm::rmsnorm(x.data(), x.data(), w.data(), dim, 1e-6f);
+        report(max_rel(x.data(), ref.data(), dim) <= 1e-5, "rmsnorm in place", max_rel(x.data(), ref.data(), dim));
+    }
+
+    // per-head q/k norm from concurrent threads on disjoint heads (qwen3.cpp:451-461)
+    {
+        const int nh = 40, hd = 128;
+        auto qk = randv((size_t)nh * hd), w = randv(hd, 0.02f);
+        for (auto& e : w) e += 1.f;
+        std::vector<float> ref(qk);
+        for (int h = 0; h < nh; h++) orc_rmsnorm(&ref[(size_t)h * hd], &ref[(size_t)h * hd], w.data(), hd, 1e-6f);
+        std::vector<std::thread> th;
+        for (int t = 0; t < 8; t++)
+            th.emplace_back([&, t] {
+                for (int h = t; h < nh; h += 8) ane_lm::rmsnorm(&qk[(size_t)h * hd], &qk[(size_t)h * hd], w.data(), hd, 1e-6f);
+            });
+        for (auto& t : th) t.join();
+        report(max_rel(qk.data(), ref.data(), qk.size()) <= 1e-5, "rmsnorm from 8 threads", max_rel(qk.data(), ref.data(), qk.size()));
+    }
+
+    // apply_rope_cached (qwen3_5.cpp:595-597 shape): table row and fallback
+    {
+        const int hd = 256, rot = 64, nq = 8, nk = 2, pos = 777;
+        std::vector<float> cosr(rot / 2), sinr(rot / 2);
+        std::vector<float> ct((size_t)1024 * rot / 2), st((size_t)1024 * rot / 2);
+        orc_rope_table(ct.data(), st.data(), 1024, rot, 1e7f);
+        std::memcpy(cosr.data(), &ct[(size_t)pos * rot / 2], rot / 2 * 4);
+        std::memcpy(sinr.data(), &st[(size_t)pos * rot / 2], rot / 2 * 4);
+        for (int with_row = 1; with_row >= 0; with_row--) {
+            auto q = randv((size_t)nq * 2 * hd), k = randv((size_t)nk * hd);
+            std::vector<float> rq(q), rk(k);
+            ane_lm::apply_rope_cached(q.data(), k.data(), nq, nk, hd, 2 * hd, hd, rot, pos, 1e7f,
+                                      with_row ? cosr.data() : nullptr, with_row ? sinr.data() : nullptr);
+            orc_rope_cached(rq.data(), rk.data(), nq, nk, hd, 2 * hd, hd, rot, pos, 1e7f,
+                            with_row ? cosr.data() : nullptr, with_row ? sinr.data() : nullptr);
+            double e = 0;
+            for (size_t i = 0; i < q.size(); i++) e = std::fmax(e, std::fabs(q[i] - rq[i]));
+            for (size_t i = 0; i < k.size(); i++) e = std::fmax(e, std::fabs(k[i] - rk[i]));
+            report(e <= 4e-5, with_row ? "apply_rope_cached table row" : "apply_rope_cached fallback", e);
+        }
+    }
+
+    // softmax (sampling.cpp:56): bit-identical to the oracle
+    {
+        auto x = randv(151936, 5.f), ref = x;
+        ane_lm::softmax(x.data(), (int)x.size());
+        orc_softmax(ref.data(), (int)ref.size());
+        report(same_bits(x.data(), ref.data(), x.size() * 4), "softmax bit-exact", max_rel(x.data(), ref.data(), x.size()));
+    }
+
+    // silu_vec_inplace / mul_sigmoid_inplace (qwen3_5.cpp:514, :621)
+    {
+        auto x = randv(6144, 3.f), ref = x, z = randv(6144, 3.f), y = randv(6144), yref = y;
+        std::vector<float> tmp(6144);
+        ane_lm::silu_vec_inplace(x.data(), (int)x.size(), tmp.data());
+        orc_silu_vec(ref.data(), ref.size());
+        report(max_rel(x.data(), ref.data(), x.size()) <= 1e-5, "silu_vec_inplace", max_rel(x.data(), ref.data(), x.size()));
+        ane_lm::mul_sigmoid_inplace(y.data(), z.data(), (int)y.size(), tmp.data());
+        orc_mul_sigmoid(yref.data(), z.data(), yref.size());
+        report(max_rel(y.data(), yref.data(), y.size()) <= 1e-5, "mul_sigmoid_inplace", max_rel(y.data(), yref.data(), y.size()));
+    }
+
+    // sample_token over a generation-like loop (generate.cpp:80, :129): same
+    // srand48 seed, same ids; the greedy call in the middle draws nothing.
+    {
+        const int V = 151936;
+        std::vector<int> recent;
+        std::vector<int> got, want;
+        std::vector<std::vector<float>> steps;
+        for (int s = 0; s < 12; s++) steps.push_back(randv(V, 3.f));
+        ane_lm::SamplingParams p;
+        srand48(42);
+        for (int s = 0; s < 12; s++) {
+            ane_lm::SamplingParams ps = p;
+            if (s == 5) ps.temperature = 0.f;
+            int id = ane_lm::sample_token(steps[s].data(), V, ps, recent);
+            got.push_back(id);
+            recent.push_back(id);
+        }
+        srand48(42);
+        recent.clear();
+        for (int s = 0; s < 12; s++) {
+            float temp = s == 5 ? 0.f : p.temperature;
+            float r = temp > 0 ? (float)drand48() : 0.f;
+            int id = orc_sample_token(steps[s].data(), V, temp, p.repetition_penalty, p.repetition_context_size,
+                                      p.frequency_penalty, recent.data(), (int)recent.size(), r, nullptr);
+            want.push_back(id);
+            recent.push_back(id);
+        }
+        report(got == want, "sample_token stream", got == want ? 0 : 1);
+    }
+
+    // bf16 -> fp16 convert hook (safetensors.cpp:335): all 65,536 patterns
+    {
+        std::vector<uint16_t> src(65536), dst(65536), ref(65536);
+        for (int i = 0; i < 65536; i++) src[i] = (uint16_t)i;
+        ane_lm::hip::bf16_to_f16_vec(dst.data(), src.data(), 65536);
+        orc_bf16_to_f16_vec(ref.data(), src.data(), 65536, 1);
+        report(dst == ref, "bf16_to_f16_vec all patterns", dst == ref ? 0 : 1);
+    }
+
+    // additive entry points: residual add, qk-norm + RoPE, SwiGLU
+    {
+        auto x = randv(4096), y = randv(4096);
+        std::vector<float> ref(4096);
+        for (int i = 0; i < 4096; i++) ref[i] = x[i] + y[i];
+        ane_lm::hip::residual_add(x.data(), y.data(), 4096);
+        report(same_bits(x.data(), ref.data(), 4096 * 4), "residual_add bit-exact", 0);
+
+        const int nq = 16, nk = 8, hd = 128;
+        std::vector<float> ct((size_t)4096 * 64), st((size_t)4096 * 64);
+        orc_rope_table(ct.data(), st.data(), 4096, hd, 1e6f);
+        auto wq = randv(hd, 0.02f), wk = randv(hd, 0.02f);
+        for (auto& e : wq) e += 1.f;
+        for (auto& e : wk) e += 1.f;
+        for (int pos : {3000, 20000}) {
+            auto q = randv((size_t)nq * hd), k = randv((size_t)nk * hd);
+            std::vector<float> rq(q), rk(k);
+            const float* cr = pos < 4096 ? &ct[(size_t)pos * 64] : nullptr;
+            const float* sr = pos < 4096 ? &st[(size_t)pos * 64] : nullptr;
+            ane_lm::hip::qknorm_rope_qwen3(q.data(), k.data(), nq, nk, hd, wq.data(), wk.data(), 1e-6f, pos, 1e6f, cr, sr);
+            for (int h = 0; h < nq; h++) orc_rmsnorm(&rq[(size_t)h * hd], &rq[(size_t)h * hd], wq.data(), hd, 1e-6f);
+            for (int h = 0; h < nk; h++) orc_rmsnorm(&rk[(size_t)h * hd], &rk[(size_t)h * hd], wk.data(), hd, 1e-6f);
+            orc_rope_qwen3(rq.data(), rk.data(), nq, nk, hd, pos, 1e6f, cr, sr);
+            double e = 0;
+            for (size_t i = 0; i < q.size(); i++) e = std::fmax(e, std::fabs(q[i] - rq[i]));
+            for (size_t i = 0; i < k.size(); i++) e = std::fmax(e, std::fabs(k[i] - rk[i]));
+            report(e <= 1e-4, pos < 4096 ? "qknorm_rope_qwen3 table" : "qknorm_rope_qwen3 fallback", e);
+        }
+
+        auto g = randv(3072), u = randv(3072);
+        std::vector<float> h(3072), hr(3072);
+        ane_lm::hip::silu_mul(h.data(), g.data(), u.data(), 3072);
+        orc_silu_mul(hr.data(), g.data(), u.data(), 3072, 1);
+        report(max_rel(h.data(), hr.data(), 3072) <= 1e-5, "silu_mul", max_rel(h.data(), hr.data(), 3072));
+    }
+
+    printf("%s: %d failure(s)\n", g_fail ? "FAILED" : "OK", g_fail);
+    return g_fail ? 1 : 0;
+}

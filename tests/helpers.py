@@ -1,0 +1,65 @@
+"""Comparison helpers with the tolerances the parity tests state."""
+import numpy as np
+
+# fp32 outputs of norm, RoPE and softmax: max relative error <= 1e-5
+REL_TOL = 1e-5
+
+
+def max_rel_err(got, ref, denom=None):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    d = np.abs(ref) if denom is None else np.asarray(denom, np.float64)
+    d = np.maximum(d, np.finfo(np.float32).tiny)
+    return float(np.max(np.abs(got - ref) / d)) if got.size else 0.0
+
+
+def bits(a):
+    a = np.ascontiguousarray(a)
+    return a.view(np.uint32 if a.dtype.itemsize == 4 else np.uint16)
+
+
+def assert_bitexact(got, ref, what=""):
+    g, r = bits(got), bits(ref)
+    bad = np.flatnonzero(g.ravel() != r.ravel())
+    assert bad.size == 0, f"{what}: {bad.size} mismatches, first at {bad[:5]}: {g.ravel()[bad[:5]]} vs {r.ravel()[bad[:5]]}"
+
+
+# ---------------------------------------------------------------- GPU plumbing
+
+def dev(a):
+    """numpy -> torch tensor on cuda:0 (uint16 arrays travel as int16)."""
+    import torch
+
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.uint16:
+        a = a.view(np.int16)
+    return torch.from_numpy(a).cuda()
+
+
+def host(t):
+    import torch
+
+    torch.cuda.synchronize()
+    a = t.detach().cpu()
+    if a.dtype in (torch.float16, torch.bfloat16):
+        a = a.view(torch.int16)
+    a = a.numpy()
+    return a.view(np.uint16) if a.dtype == np.int16 else a
+
+
+def f16_normal(rng, shape, std):
+    """fp16 bits of the RNE fp16 of an fp32 N(0, std) draw."""
+    return (rng.standard_normal(shape, dtype=np.float32) * np.float32(std)).astype(np.float16).view(np.uint16)
+
+
+def gamma_f16(rng, n):
+    """norm gammas ~ 1 + N(0, 0.02) stored as fp16 bits"""
+    return (1.0 + rng.normal(0, 0.02, n)).astype(np.float32).astype(np.float16).view(np.uint16)
+
+
+def rope_den(n, c, s, half):
+    """|a c| + |b s| for the two halves of each head: the RoPE error scale.
+    n: [..., 2*half] normalised (unrotated) heads; c, s: [..., half]."""
+    a, b = n[..., :half].astype(np.float64), n[..., half:].astype(np.float64)
+    c, s = np.abs(c.astype(np.float64)), np.abs(s.astype(np.float64))
+    return np.concatenate([np.abs(a) * c + np.abs(b) * s, np.abs(b) * c + np.abs(a) * s], axis=-1)

@@ -1,0 +1,116 @@
+"""The C-ABI library loads and exports every symbol include/anelm_hip.h
+declares, plus the ane_lm:: drop-in functions; argument validation fails
+with a status and a message before anything touches the GPU.  No compute
+calls: this runs without a GPU."""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "anelm_hip.h")
+
+
+def declared():
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(anelm_[a-z0-9_]+)\s*\(", src)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    import anelm
+
+    return anelm.lib()
+
+
+def test_header_declares_the_path():
+    names = declared()
+    for n in ["anelm_rmsnorm", "anelm_add_rmsnorm", "anelm_qknorm_rope", "anelm_rope_cached", "anelm_rope_table",
+              "anelm_residual_add", "anelm_silu_mul", "anelm_silu", "anelm_mul_sigmoid", "anelm_embed_gather",
+              "anelm_bf16_to_f16", "anelm_softmax", "anelm_sample", "anelm_sample_workspace_size",
+              "anelm_last_error"]:
+        assert n in names
+
+
+def test_every_declared_symbol_is_exported(lib):
+    missing = [n for n in declared() if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_python_binding_covers_header():
+    import anelm
+
+    assert sorted(anelm.EXPORTED) == declared()
+
+
+def test_dropin_cpp_symbols_exported():
+    import anelm
+
+    out = subprocess.run(["nm", "-D", "--defined-only", "-C", anelm.LIB_PATH], capture_output=True, text=True,
+                         check=True).stdout
+    for sig in ["ane_lm::rmsnorm(float*, float const*, float const*, int, float)",
+                "ane_lm::softmax(float*, int)",
+                "ane_lm::silu_vec_inplace(float*, int, float*)",
+                "ane_lm::mul_sigmoid_inplace(float*, float const*, int, float*)",
+                "ane_lm::apply_rope_cached(float*, float*, int, int, int, int, int, int, int, float, float const*, float const*)",
+                "ane_lm::sample_token(float const*, int, ane_lm::SamplingParams const&, std::vector<int, std::allocator<int> > const&)",
+                "ane_lm::hip::bf16_to_f16_vec(unsigned short*, unsigned short const*, int)",
+                "ane_lm::hip::residual_add(float*, float const*, int)"]:
+        assert sig in out, sig
+
+
+def test_version(lib):
+    assert lib.anelm_version() >= 100
+
+
+def test_invalid_arguments_return_status_and_message(lib):
+    P = ctypes.c_void_p
+    assert lib.anelm_rmsnorm(None, None, None, 0, 1, 16, 16, 16, 1e-6, None) == -1
+    assert b"null" in lib.anelm_last_error()
+    fake = P(0x1000)  # never dereferenced: validation fails first
+    assert lib.anelm_rmsnorm(fake, fake, fake, 0, 0, 16, 16, 16, 1e-6, None) == -1
+    assert lib.anelm_rmsnorm(fake, fake, fake, 0, 4, 16, 8, 16, 1e-6, None) == -1       # ld < dim
+    assert lib.anelm_rmsnorm(fake, fake, fake, 7, 4, 16, 16, 16, 1e-6, None) == -1      # dtype
+    assert lib.anelm_add_rmsnorm(fake, fake, fake, fake, 0, 4, 16, 16, 16, 16, 1e-6, None) == -1  # out == x
+    assert lib.anelm_qknorm_rope(fake, fake, 128, 128, None, None, 0, None, None, None, 0, 1e6, 1, 1, 1, 128,
+                                 1e-6, None) == -1                                       # null pos
+    assert lib.anelm_qknorm_rope(fake, fake, 128, 128, None, None, 0, fake, None, None, 0, 1e6, 1, 1, 1, 127,
+                                 1e-6, None) == -1                                       # odd head_dim
+    assert lib.anelm_residual_add(fake, fake, 0, None) == -1
+    assert lib.anelm_bf16_to_f16(None, fake, 8, None) == -1
+    assert lib.anelm_embed_gather(fake, fake, 1, fake, 70000, 16, 16, None, None) == -1  # grid.y limit
+    import anelm
+
+    p = anelm.SamplingParams()
+    assert lib.anelm_sample(fake, None, 0, fake, 100, 1, 100, None, 0, None, ctypes.byref(p), None, fake, 1 << 20,
+                            None) == -1                                                  # r required
+    assert lib.anelm_sample(fake, None, 0, fake, 100, 1, 100, None, 0, None, ctypes.byref(p), fake, fake, 16,
+                            None) == -4                                                  # workspace too small
+    assert b"workspace" in lib.anelm_last_error()
+
+
+def test_workspace_sizes(lib):
+    # 64 rows x 38 chunks of 4096 logits: u64 sums + f32 maxima + i32 argmax + i32 flags
+    n = 64 * 38
+    assert lib.anelm_sample_workspace_size(64, 151936) == n * 8 + n * 4 * 3
+    assert lib.anelm_sample_workspace_size(0, 10) == 0
+    assert lib.anelm_softmax_workspace_size(1, 4096) > 0
+
+
+def test_error_string_is_per_thread(lib):
+    import threading
+
+    lib.anelm_residual_add(None, None, 1, None)
+    seen = {}
+
+    def other():
+        seen["msg"] = lib.anelm_last_error()
+
+    t = threading.Thread(target=other)
+    t.start()
+    t.join()
+    assert seen["msg"] == b""
+    assert b"null" in lib.anelm_last_error()

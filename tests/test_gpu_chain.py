@@ -1,0 +1,118 @@
+"""One or more layers of the op chain (models/llm/qwen3.cpp:502-528) run
+through the C ABI in the order the reference runs them, against the
+oracle's per-token layer chain, at the configurations' shapes."""
+import numpy as np
+import pytest
+
+from helpers import REL_TOL, assert_bitexact, dev, gamma_f16, host, max_rel_err, rope_den
+
+pytestmark = pytest.mark.gpu
+THETA, EPS, D = 1e6, 1e-6, 128
+
+
+def make_layer(rng, T, H, nq, nk, I, pmax, sequential):
+    L = {
+        "attn": rng.standard_normal((T, H), dtype=np.float32),
+        "mlp": rng.standard_normal((T, H), dtype=np.float32),
+        "q": rng.standard_normal((T, nq * D), dtype=np.float32),
+        "k": rng.standard_normal((T, nk * D), dtype=np.float32),
+        "g": rng.standard_normal((T, I), dtype=np.float32),
+        "u": rng.standard_normal((T, I), dtype=np.float32),
+        "w_in": gamma_f16(rng, H), "w_post": gamma_f16(rng, H), "wq": gamma_f16(rng, D), "wk": gamma_f16(rng, D),
+    }
+    L["pos"] = (np.arange(T) if sequential else rng.integers(0, pmax, T)).astype(np.int32)
+    return L
+
+
+def w32(bits):
+    return bits.view(np.float16).astype(np.float32)
+
+
+def gpu_layer(hip, x, L, c_tab, s_tab, nq, nk):
+    """(1) norm, (2) qk-norm+RoPE, (3) add+norm, (4) SwiGLU, (5) add."""
+    import torch
+
+    T, H = x.shape
+    xn = torch.empty_like(x)
+    q, k, g, u = dev(L["q"]), dev(L["k"]), dev(L["g"]), dev(L["u"])
+    h = torch.empty_like(g)
+    f16 = lambda b: dev(b).view(torch.float16)
+    hip.rmsnorm(xn, x, f16(L["w_in"]), EPS)
+    hip.qknorm_rope(q, k, f16(L["wq"]), f16(L["wk"]), dev(L["pos"]), c_tab, s_tab, THETA, EPS, nq=nq, nk=nk)
+    hip.add_rmsnorm(x, dev(L["attn"]), xn, f16(L["w_post"]), EPS)
+    hip.silu_mul(h, g, u)
+    hip.residual_add(x, dev(L["mlp"]))
+    return xn, q, k, h
+
+
+@pytest.mark.parametrize("cfg", [
+    dict(name="0.6B decode", T=1, H=1024, nq=16, nk=8, I=3072, pmax=4096, seq=False, layers=28),
+    dict(name="0.6B prefill rows", T=64, H=1024, nq=16, nk=8, I=3072, pmax=2048, seq=True, layers=2),
+    dict(name="4B batched decode", T=64, H=2560, nq=32, nk=8, I=9728, pmax=32768, seq=False, layers=2),
+    dict(name="8B prefill rows", T=16, H=4096, nq=32, nk=8, I=12288, pmax=8192, seq=True, layers=2),
+], ids=lambda c: c["name"])
+def test_layer_chain(hip, orc, rng, cfg):
+    T, H, nq, nk, I = cfg["T"], cfg["H"], cfg["nq"], cfg["nk"], cfg["I"]
+    c_np, s_np = orc.rope_table(16384, D, THETA)
+    c_tab, s_tab = dev(c_np), dev(s_np)
+    x0 = rng.standard_normal((T, H), dtype=np.float32)
+    x_gpu = dev(x0)
+    x_ref = x0.copy()
+    for _ in range(cfg["layers"]):
+        L = make_layer(rng, T, H, nq, nk, I, cfg["pmax"], cfg["seq"])
+        xn, q, k, h = gpu_layer(hip, x_gpu, L, c_tab, s_tab, nq, nk)
+        q0, k0 = L["q"].copy(), L["k"].copy()
+        xn_ref = np.empty_like(x_ref)
+        h_ref = np.empty_like(L["g"])
+        orc.layer_chain(T, H, nq, nk, D, I, x_ref, xn_ref, L["attn"], L["mlp"], L["q"], L["k"], L["g"], L["u"], h_ref,
+                        w32(L["w_in"]), w32(L["w_post"]), w32(L["wq"]), w32(L["wk"]), L["pos"], c_np, s_np, THETA, EPS)
+        # the residual stream is two exact IEEE adds per layer: bit-exact
+        assert_bitexact(host(x_gpu), x_ref, "residual stream")
+        assert max_rel_err(host(xn), xn_ref) <= REL_TOL
+        assert max_rel_err(host(h), h_ref) <= REL_TOL
+        nq0, nk0 = orc.qknorm_rope(q0, k0, w32(L["wq"]), w32(L["wk"]), np.zeros(T, np.int32), None, None, THETA,
+                                   nq, nk, D)
+        inv = orc.rope_inv_freq(D, THETA)
+        ang = (L["pos"].astype(np.float32)[:, None] * inv[None, :]).astype(np.float64)
+        c, s = np.cos(ang)[:, None, :], np.sin(ang)[:, None, :]
+        assert max_rel_err(host(q).reshape(T, nq, D), L["q"].reshape(T, nq, D),
+                           rope_den(nq0.reshape(T, nq, D), c, s, 64)) <= REL_TOL
+        assert max_rel_err(host(k).reshape(T, nk, D), L["k"].reshape(T, nk, D),
+                           rope_den(nk0.reshape(T, nk, D), c, s, 64)) <= REL_TOL
+
+
+@pytest.mark.slow
+def test_full_8b_prefill_layer_sampled_rows(hip, orc, rng):
+    """One full T=8192 layer of the 8B prefill chain on the GPU; 48 random
+    token rows are re-run through the oracle from the same inputs."""
+    import torch
+
+    T, H, nq, nk, I = 8192, 4096, 32, 8, 12288
+    gen = torch.Generator(device="cuda").manual_seed(3)
+    rn = lambda *s: torch.randn(*s, generator=gen, device="cuda")
+    x, attn, mlp = rn(T, H), rn(T, H), rn(T, H)
+    q, k, g, u = rn(T, nq * D), rn(T, nk * D), rn(T, I), rn(T, I)
+    wb = {n: gamma_f16(rng, H if n in ("w_in", "w_post") else D) for n in ("w_in", "w_post", "wq", "wk")}
+    pos = np.arange(T, dtype=np.int32)
+    rows = np.sort(rng.choice(T, 48, replace=False))
+    ri = torch.from_numpy(rows).cuda()
+    before = {n: host(t[ri]) for n, t in dict(x=x, attn=attn, mlp=mlp, q=q, k=k, g=g, u=u).items()}
+    c_np, s_np = orc.rope_table(16384, D, THETA)
+    xn = torch.empty_like(x)
+    h = torch.empty_like(g)
+    f16 = lambda b: dev(b).view(torch.float16)
+    hip.rmsnorm(xn, x, f16(wb["w_in"]), EPS)
+    hip.qknorm_rope(q, k, f16(wb["wq"]), f16(wb["wk"]), dev(pos), dev(c_np), dev(s_np), THETA, EPS, nq=nq, nk=nk)
+    hip.add_rmsnorm(x, attn, xn, f16(wb["w_post"]), EPS)
+    hip.silu_mul(h, g, u)
+    hip.residual_add(x, mlp)
+    xr, qr, kr = before["x"].copy(), before["q"].copy(), before["k"].copy()
+    xnr, hr = np.empty_like(xr), np.empty_like(before["g"])
+    orc.layer_chain(48, H, nq, nk, D, I, xr, xnr, before["attn"], before["mlp"], qr, kr, before["g"], before["u"], hr,
+                    w32(wb["w_in"]), w32(wb["w_post"]), w32(wb["wq"]), w32(wb["wk"]), pos[rows], c_np, s_np, THETA, EPS)
+    assert_bitexact(host(x[ri]), xr, "residual stream")
+    assert max_rel_err(host(xn[ri]), xnr) <= REL_TOL
+    assert max_rel_err(host(h[ri]), hr) <= REL_TOL
+    # RoPE outputs: absolute error against the per-head output scale
+    for got, ref in ((host(q[ri]), qr), (host(k[ri]), kr)):
+        assert np.max(np.abs(got - ref)) <= REL_TOL * 4 * np.max(np.abs(ref))

@@ -1,0 +1,196 @@
+"""RMSNorm (core/cpu_ops.cpp:25-31), fused add+RMSNorm (qwen3.cpp:516-518),
+q/k-norm + RoPE (qwen3.cpp:444-472), apply_rope_cached (cpu_ops.cpp:56-80)
+and the RoPE table (qwen3.cpp:200-219) on the GPU against the oracle.
+Tolerance: max relative error <= 1e-5 (RoPE: relative to |a c| + |b s|)."""
+import numpy as np
+import pytest
+
+from helpers import REL_TOL, assert_bitexact, dev, gamma_f16, host, max_rel_err, rope_den
+
+pytestmark = pytest.mark.gpu
+THETA = 1e6
+EPS = 1e-6
+
+
+def _gamma(rng, n, dt):
+    import torch
+
+    g16 = gamma_f16(rng, n)
+    w32 = g16.view(np.float16).astype(np.float32)          # exact widening: the oracle's gamma
+    if dt == "f16":
+        return dev(g16).view(torch.float16), w32
+    if dt == "bf16":
+        wb = (w32.view(np.uint32) >> 16).astype(np.uint16)
+        return dev(wb).view(torch.bfloat16), (wb.astype(np.uint32) << 16).view(np.float32)
+    return dev(w32), w32
+
+
+@pytest.mark.parametrize("rows,dim", [(1, 1024), (2048, 1024), (64, 2560), (512, 4096), (3, 1000), (5, 7),
+                                      (2, 5120), (2, 8192), (4, 12288)])
+@pytest.mark.parametrize("dt", ["f16", "f32", "bf16"])
+def test_rmsnorm(hip, orc, rng, rows, dim, dt):
+    import torch
+
+    x = rng.standard_normal((rows, dim), dtype=np.float32)
+    wt, w32 = _gamma(rng, dim, dt)
+    out = torch.empty(rows, dim, device="cuda")
+    hip.rmsnorm(out, dev(x), wt, EPS)
+    assert max_rel_err(host(out), orc.rmsnorm_rows(x, w32, EPS)) <= REL_TOL
+
+
+def test_rmsnorm_in_place_and_strided(hip, orc, rng):
+    import torch
+
+    x = rng.standard_normal((33, 1536), dtype=np.float32)
+    wt, w32 = _gamma(rng, 1024, "f16")
+    t = dev(x)
+    view = t[:, 256:1280]                       # rows of 1024 at stride 1536
+    hip.rmsnorm(view, view, wt, EPS)            # out aliases x (qwen3.cpp:530)
+    got = host(t)
+    assert max_rel_err(got[:, 256:1280], orc.rmsnorm_rows(x[:, 256:1280], w32, EPS)) <= REL_TOL
+    assert np.array_equal(got[:, :256], x[:, :256]) and np.array_equal(got[:, 1280:], x[:, 1280:])
+
+
+@pytest.mark.parametrize("rows,dim", [(1, 1024), (2048, 1024), (64, 2560), (256, 4096), (3, 1001)])
+def test_add_rmsnorm(hip, orc, rng, rows, dim):
+    import torch
+
+    x = rng.standard_normal((rows, dim), dtype=np.float32)
+    y = rng.standard_normal((rows, dim), dtype=np.float32)
+    wt, w32 = _gamma(rng, dim, "f16")
+    xt, out = dev(x), torch.empty(rows, dim, device="cuda")
+    hip.add_rmsnorm(xt, dev(y), out, wt, EPS)
+    assert_bitexact(host(xt), x + y, "residual stream")
+    assert max_rel_err(host(out), orc.rmsnorm_rows(x + y, w32, EPS)) <= REL_TOL
+
+
+def test_add_rmsnorm_y_aliases_out(hip, orc, rng):
+    """attn_out lives in x_norm_ (qwen3.cpp:508-518): y == out."""
+    x = rng.standard_normal((16, 1024), dtype=np.float32)
+    y = rng.standard_normal((16, 1024), dtype=np.float32)
+    wt, w32 = _gamma(rng, 1024, "f32")
+    xt, yt = dev(x), dev(y)
+    hip.add_rmsnorm(xt, yt, yt, wt, EPS)
+    assert_bitexact(host(xt), x + y, "residual stream")
+    assert max_rel_err(host(yt), orc.rmsnorm_rows(x + y, w32, EPS)) <= REL_TOL
+
+
+def _check_qk(orc, q, k, q2, k2, wq32, wk32, pos, c_tab, s_tab, nq, nk, D):
+    """Compare GPU q2/k2 with the oracle; errors scaled by |a c| + |b s|."""
+    T = len(pos)
+    rq, rk = orc.qknorm_rope(q, k, wq32, wk32, pos, c_tab, s_tab, THETA, nq, nk, D)
+    nq0, nk0 = orc.qknorm_rope(q, k, wq32, wk32, np.zeros(T, np.int32), c_tab, s_tab, THETA, nq, nk, D)
+    half = D // 2
+    inv = orc.rope_inv_freq(D, THETA)
+    ang = (pos.astype(np.float32)[:, None] * inv[None, :]).astype(np.float64)
+    c, s = np.cos(ang)[:, None, :], np.sin(ang)[:, None, :]
+    for got, ref, n0, nh, ld in ((q2, rq, nq0, nq, q.shape[1]), (k2, rk, nk0, nk, k.shape[1])):
+        if nh == 0:
+            continue
+        g = got[:, :nh * D].reshape(T, nh, D)
+        r = ref[:, :nh * D].reshape(T, nh, D)
+        den = rope_den(n0[:, :nh * D].reshape(T, nh, D), c, s, half)
+        assert max_rel_err(g, r, den) <= REL_TOL
+        assert np.array_equal(got[:, nh * D:], ref[:, nh * D:])   # bytes past the heads untouched
+
+
+@pytest.mark.parametrize("T,nq,nk,pmax,tab", [(1, 16, 8, 4096, 16384),       # 0.6B decode
+                                              (256, 16, 8, 2048, 16384),     # 0.6B prefill rows
+                                              (64, 32, 8, 32768, 16384),     # 4B batched decode: half fallback
+                                              (128, 32, 8, 8192, 16384),     # 8B prefill rows
+                                              (7, 5, 3, 100, 0)])            # no table at all
+def test_qknorm_rope(hip, orc, rng, T, nq, nk, pmax, tab):
+    import torch
+
+    D = 128
+    q = rng.standard_normal((T, nq * D), dtype=np.float32)
+    k = rng.standard_normal((T, nk * D), dtype=np.float32)
+    pos = rng.integers(0, pmax, T).astype(np.int32)
+    pos[0] = 0
+    if T > 2:
+        pos[1] = pmax - 1
+    wq, wq32 = _gamma(rng, D, "f16")
+    wk, wk32 = _gamma(rng, D, "f16")
+    c_tab, s_tab = orc.rope_table(tab, D, THETA) if tab else (None, None)
+    qt, kt = dev(q), dev(k)
+    hip.qknorm_rope(qt, kt, wq, wk, dev(pos), dev(c_tab) if tab else None, dev(s_tab) if tab else None, THETA,
+                    EPS, nq=nq, nk=nk)
+    _check_qk(orc, q, k, host(qt), host(kt), wq32, wk32, pos, c_tab, s_tab, nq, nk, D)
+
+
+def test_qknorm_rope_fused_qkv_layout(hip, orc, rng):
+    """q and k as slices of the fused [q|k|v] row (qwen3.cpp:440-442)."""
+    T, nq, nk, D = 40, 16, 8, 128
+    row = (nq + 2 * nk) * D
+    qkv = rng.standard_normal((T, row), dtype=np.float32)
+    pos = np.arange(T, dtype=np.int32) * 37
+    wq, wq32 = _gamma(rng, D, "f32")
+    wk, wk32 = _gamma(rng, D, "f32")
+    c_tab, s_tab = orc.rope_table(2048, D, THETA)
+    t = dev(qkv)
+    hip.qknorm_rope(t[:, :nq * D], t[:, nq * D:(nq + nk) * D], wq, wk, dev(pos), dev(c_tab), dev(s_tab), THETA, EPS,
+                    nq=nq, nk=nk)
+    got = host(t)
+    q, k = np.ascontiguousarray(qkv[:, :nq * D]), np.ascontiguousarray(qkv[:, nq * D:(nq + nk) * D])
+    _check_qk(orc, q, k, np.ascontiguousarray(got[:, :nq * D]), np.ascontiguousarray(got[:, nq * D:(nq + nk) * D]),
+              wq32, wk32, pos, c_tab, s_tab, nq, nk, D)
+    assert np.array_equal(got[:, (nq + nk) * D:], qkv[:, (nq + nk) * D:])   # v untouched
+
+
+def test_qknorm_rope_without_norm(hip, orc, rng):
+    T, nq, nk, D = 9, 4, 2, 128
+    q = rng.standard_normal((T, nq * D), dtype=np.float32)
+    k = rng.standard_normal((T, nk * D), dtype=np.float32)
+    pos = rng.integers(0, 20000, T).astype(np.int32)
+    c_tab, s_tab = orc.rope_table(16384, D, THETA)
+    qt, kt = dev(q), dev(k)
+    hip.qknorm_rope(qt, kt, None, None, dev(pos), dev(c_tab), dev(s_tab), THETA, EPS, nq=nq, nk=nk)
+    _check_qk(orc, q, k, host(qt), host(kt), None, None, pos, c_tab, s_tab, nq, nk, D)
+
+
+@pytest.mark.parametrize("D", [64, 256, 96])
+def test_qknorm_rope_other_head_dims(hip, orc, rng, D):
+    T, nq, nk = 11, 3, 2
+    q = rng.standard_normal((T, nq * D), dtype=np.float32)
+    k = rng.standard_normal((T, nk * D), dtype=np.float32)
+    pos = rng.integers(0, 3000, T).astype(np.int32)
+    wq, wq32 = _gamma(rng, D, "f16")
+    wk, wk32 = _gamma(rng, D, "f16")
+    c_tab, s_tab = orc.rope_table(1024, D, THETA)
+    qt, kt = dev(q), dev(k)
+    hip.qknorm_rope(qt, kt, wq, wk, dev(pos), dev(c_tab), dev(s_tab), THETA, EPS, nq=nq, nk=nk, head_dim=D)
+    _check_qk(orc, q, k, host(qt), host(kt), wq32, wk32, pos, c_tab, s_tab, nq, nk, D)
+
+
+@pytest.mark.parametrize("with_row", [True, False])
+def test_rope_cached(hip, orc, rng, with_row):
+    """Qwen3.5 call shape (qwen3_5.cpp:595-597): q stride 2*head_dim, partial rotary."""
+    D, rot, nq, nk, pos = 256, 64, 8, 2, 1234
+    q = rng.standard_normal(nq * 2 * D, dtype=np.float32)
+    k = rng.standard_normal(nk * D, dtype=np.float32)
+    c_tab, s_tab = orc.rope_table(2048, rot, THETA)
+    cr, sr = (c_tab[pos], s_tab[pos]) if with_row else (None, None)
+    qt, kt = dev(q), dev(k)
+    hip.rope_cached(qt, kt, nq, nk, D, 2 * D, D, rot, pos, THETA, dev(cr) if with_row else None,
+                    dev(sr) if with_row else None)
+    rq, rk = orc.rope_cached(q, k, nq, nk, D, 2 * D, D, rot, pos, THETA, cr, sr)
+    gq, gk = host(qt), host(kt)
+    scale = np.abs(q).max()
+    assert np.max(np.abs(gq - rq)) <= 4e-6 * scale
+    assert np.max(np.abs(gk - rk)) <= 4e-6 * scale
+    mask = np.ones(nq * 2 * D, bool)
+    for h in range(nq):
+        mask[h * 2 * D:h * 2 * D + rot] = False
+    assert np.array_equal(gq[mask], q[mask])
+
+
+@pytest.mark.parametrize("n_pos", [16384, 32768])
+def test_rope_table(hip, orc, n_pos):
+    import torch
+
+    c, s = torch.empty(n_pos, 64, device="cuda"), torch.empty(n_pos, 64, device="cuda")
+    hip.rope_table(c, s, THETA)
+    rc, rs = orc.rope_table(n_pos, 128, THETA)
+    gc, gs = host(c), host(s)
+    assert np.all(gc[0] == 1.0) and np.all(gs[0] == 0.0)
+    assert np.max(np.abs(gc - rc)) <= 2.0 ** -22 and np.max(np.abs(gs - rs)) <= 2.0 ** -22
