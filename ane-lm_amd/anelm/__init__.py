@@ -121,10 +121,16 @@ def _need(cond: bool, msg: str) -> None:
         raise AnelmError(ERR_INVALID, msg)
 
 
+def _ld(x):
+    """Row stride of a 2-D tensor; a single row's stride is arbitrary
+    (numpy/torch may report 0 for it), so the row length stands in."""
+    return x.stride(0) if x.shape[0] > 1 else x.shape[1]
+
+
 def _rows(x):
     """(rows, dim, ld) of a 2-D tensor with unit inner stride."""
-    _need(x.dim() == 2 and x.stride(1) == 1, "expected a 2-D tensor with unit inner stride")
-    return x.shape[0], x.shape[1], x.stride(0)
+    _need(x.dim() == 2 and (x.stride(1) == 1 or x.shape[1] == 1), "expected a 2-D tensor with unit inner stride")
+    return x.shape[0], x.shape[1], _ld(x)
 
 
 # ---------------------------------------------------------------- ops
@@ -148,8 +154,8 @@ def qknorm_rope(q, k, wq, wk, pos, cos_tab, sin_tab, theta=1e6, eps=1e-6, nq=Non
                 stream=None):
     """q: [T, >= nq*head_dim] rows, k: [T, >= nk*head_dim] rows (views allowed)."""
     T = pos.shape[0]
-    q_ld = q.stride(0) if q is not None else 0
-    k_ld = k.stride(0) if k is not None else 0
+    q_ld = _ld(q) if q is not None else 0
+    k_ld = _ld(k) if k is not None else 0
     nq = (q.shape[1] // head_dim if q is not None else 0) if nq is None else nq
     nk = (k.shape[1] // head_dim if k is not None else 0) if nk is None else nk
     wdt = _dtype_code(wq if wq is not None else (wk if wk is not None else q))
@@ -225,8 +231,8 @@ def sample_workspace_size(rows, vocab) -> int:
 
 def sample(ids, probs, logits, hist, hist_len, params: SamplingParams, r, workspace, stream=None):
     rows, vocab, ldl = _rows(logits)
-    ldp = probs.stride(0) if probs is not None else 0
-    hist_ld = hist.stride(0) if hist is not None and hist.numel() else 0
+    ldp = _ld(probs) if probs is not None else 0
+    hist_ld = _ld(hist) if hist is not None and hist.numel() else 0
     _check(lib().anelm_sample(_ptr(ids), _ptr(probs), ldp, _ptr(logits), ldl, rows, vocab,
                               _ptr(hist) if hist_ld else None, hist_ld, _ptr(hist_len), ctypes.byref(params),
                               _ptr(r), _ptr(workspace), workspace.numel() * workspace.element_size(),

@@ -5,17 +5,21 @@
 // 16 bytes per lane per access and keep U independent 16-byte loads per
 // stream in flight per lane before the first store, with a one-shot grid
 // (one tile of 256*U vectors per workgroup, no grid-stride loop), so a
-// launch has ~n/(256*U) workgroups -- far more than the 256 CUs.  Outputs
-// that are written once and not re-read by the kernel use non-temporal
-// stores.
+// launch has ~n/(256*U) workgroups -- far more than the 256 CUs.  U was
+// chosen per kernel by measurement at the 8B prefill sizes (lighter
+// workgroups won for SwiGLU and the convert).  Streamed inputs and
+// write-once outputs use non-temporal loads and stores.
 #include "anelm_common.hpp"
 
 namespace anelm {
 
-constexpr int kU = 4;  // 16-byte vectors per lane per stream
+constexpr int kU_add = 4;   // residual add
+constexpr int kU_silu = 1;  // SwiGLU
+constexpr int kU_cvt = 2;   // bf16 -> fp16
 
 // ------------------------------------------------------------ residual add
 // qwen3.cpp:516/:527: x = x + y, one IEEE add per element (bit-exact).
+template <int kU>
 __global__ __launch_bounds__(256) void residual_add_vec_kernel(float4* x, const float4* y, size_t n4) {
     const size_t base = (size_t)blockIdx.x * (256 * kU) + threadIdx.x;
     float4 a[kU], b[kU];
@@ -63,6 +67,7 @@ __device__ __forceinline__ float4 silu_mul4(float4 g, float4 u) {
     return r;
 }
 
+template <int kU>
 __global__ __launch_bounds__(256) void silu_mul_vec_kernel(float4* h, const float4* g, const float4* u, size_t n4) {
     const size_t base = (size_t)blockIdx.x * (256 * kU) + threadIdx.x;
     float4 a[kU], b[kU];
@@ -108,6 +113,7 @@ __device__ __forceinline__ uint32_t cvt_pair(uint32_t w) {
     return bf16_to_f16_trunc(w & 0xFFFFu) | (bf16_to_f16_trunc(w >> 16) << 16);
 }
 
+template <int kU>
 __global__ __launch_bounds__(256) void bf16_to_f16_vec_kernel(uint4* dst, const uint4* src, size_t n8) {
     const size_t base = (size_t)blockIdx.x * (256 * kU) + threadIdx.x;
     uint4 a[kU];
@@ -218,7 +224,7 @@ extern "C" int anelm_residual_add(float* x, const float* y, size_t n, void* stre
     hipStream_t st = as_stream(stream);
     if (n % 4 == 0 && aligned16(x) && aligned16(y)) {
         const size_t n4 = n / 4;
-        residual_add_vec_kernel<<<grid_for(n4, 256 * kU), 256, 0, st>>>(reinterpret_cast<float4*>(x),
+        residual_add_vec_kernel<kU_add><<<grid_for(n4, 256 * kU_add), 256, 0, st>>>(reinterpret_cast<float4*>(x),
                                                                          reinterpret_cast<const float4*>(y), n4);
     } else {
         residual_add_scalar_kernel<<<grid_stride_blocks(n), 256, 0, st>>>(x, y, n);
@@ -237,7 +243,7 @@ extern "C" int anelm_silu_mul(float* h, const float* g, const float* u, long row
     const bool contiguous = (ld_h == inter && ld_g == inter && ld_u == inter) || rows == 1;
     if (contiguous && n % 4 == 0 && aligned16(h) && aligned16(g) && aligned16(u)) {
         const size_t n4 = n / 4;
-        silu_mul_vec_kernel<<<grid_for(n4, 256 * kU), 256, 0, st>>>(
+        silu_mul_vec_kernel<kU_silu><<<grid_for(n4, 256 * kU_silu), 256, 0, st>>>(
             reinterpret_cast<float4*>(h), reinterpret_cast<const float4*>(g), reinterpret_cast<const float4*>(u), n4);
     } else {
         silu_mul_rows_kernel<<<grid_stride_blocks(n), 256, 0, st>>>(h, g, u, rows, inter, ld_h, ld_g, ld_u);
@@ -268,7 +274,7 @@ extern "C" int anelm_bf16_to_f16(uint16_t* dst, const uint16_t* src, size_t n, v
     hipStream_t st = as_stream(stream);
     if (n % 8 == 0 && aligned16(dst) && aligned16(src)) {
         const size_t n8 = n / 8;
-        bf16_to_f16_vec_kernel<<<grid_for(n8, 256 * kU), 256, 0, st>>>(reinterpret_cast<uint4*>(dst),
+        bf16_to_f16_vec_kernel<kU_cvt><<<grid_for(n8, 256 * kU_cvt), 256, 0, st>>>(reinterpret_cast<uint4*>(dst),
                                                                         reinterpret_cast<const uint4*>(src), n8);
     } else {
         bf16_to_f16_scalar_kernel<<<grid_stride_blocks(n), 256, 0, st>>>(dst, src, n);

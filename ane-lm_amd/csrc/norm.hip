@@ -1,10 +1,9 @@
 // RMSNorm, fused residual-add + RMSNorm, per-head q/k RMSNorm + RoPE, the
 // apply_rope_cached variant and the RoPE table, for gfx950.
 //
-// All of these are HBM-bound (< 1 flop/byte).  Row kernels give one wave64
-// a whole row held in registers as float4s, so a row crosses HBM once
-// (read) plus once per output (write); reductions are wave shuffles and
-// need no LDS or barrier.
+// All of these are HBM-bound (< 1 flop/byte): every activation is read
+// from HBM once and written once, with 16-byte accesses, and reductions are
+// wave shuffles plus at most one LDS exchange of per-wave partials.
 #include <cmath>
 
 #include "anelm_common.hpp"
@@ -17,35 +16,40 @@ namespace anelm {
 // products rounded separately.  With ADD, first x += y (qwen3.cpp:516) and
 // the updated x is written back.
 //
-// One wave per row, NV float4 per lane (dim <= 256*NV, dim % 4 == 0, rows
-// 16-byte aligned).  The whole row is read into registers before anything
-// is written, so out may alias x and y may alias out.
+// One workgroup per row, ceil(dim/(4*NV))/64 waves, NV float4 per lane:
+// the row is read once into registers (non-temporal: it is not re-read),
+// reduced with wave shuffles plus one LDS exchange of the per-wave
+// partials, and written once.  Light workgroups (two float4 per lane at
+// H=4096) keep many rows in flight per CU, which measured faster than one
+// wave per row holding the whole row.  The row is entirely in registers
+// before anything is written, so out may alias x and y may alias out.
 template <int NV, int DT, bool ADD>
-__global__ __launch_bounds__(256) void rmsnorm_wave_kernel(float* out, float* x, const float* y,
+__global__ __launch_bounds__(1024) void rmsnorm_row_kernel(float* out, float* x, const float* y,
                                                            const void* w, long rows, int dim,
                                                            long ld_x, long ld_y, long ld_out,
                                                            float eps) {
-    const int lane = threadIdx.x & 63;
-    const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (row >= rows) return;
+    __shared__ float part[16];
+    const int tid = threadIdx.x, nthr = blockDim.x;
+    const long row = blockIdx.x;
     float* xr = x + row * ld_x;
     float4 v[NV];
 #pragma unroll
     for (int i = 0; i < NV; i++) {
-        const int c = (i * 64 + lane) * 4;
-        v[i] = c < dim ? *reinterpret_cast<const float4*>(xr + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+        const int c = (i * nthr + tid) * 4;
+        v[i] = c < dim ? (ADD ? *reinterpret_cast<const float4*>(xr + c) : ld_nt(reinterpret_cast<const float4*>(xr + c)))
+                       : make_float4(0.f, 0.f, 0.f, 0.f);
     }
     if (ADD) {
         const float* yr = y + row * ld_y;
         float4 b[NV];
 #pragma unroll
         for (int i = 0; i < NV; i++) {
-            const int c = (i * 64 + lane) * 4;
-            b[i] = c < dim ? *reinterpret_cast<const float4*>(yr + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+            const int c = (i * nthr + tid) * 4;
+            b[i] = c < dim ? ld_nt(reinterpret_cast<const float4*>(yr + c)) : make_float4(0.f, 0.f, 0.f, 0.f);
         }
 #pragma unroll
         for (int i = 0; i < NV; i++) {
-            const int c = (i * 64 + lane) * 4;
+            const int c = (i * nthr + tid) * 4;
             v[i].x = v[i].x + b[i].x;
             v[i].y = v[i].y + b[i].y;
             v[i].z = v[i].z + b[i].z;
@@ -62,11 +66,18 @@ __global__ __launch_bounds__(256) void rmsnorm_wave_kernel(float* out, float* x,
         ss = fmaf(v[i].w, v[i].w, ss);
     }
     ss = wave_sum(ss);
+    const int nw = nthr >> 6;
+    if (nw > 1) {
+        if ((tid & 63) == 0) part[tid >> 6] = ss;
+        __syncthreads();
+        ss = part[0];
+        for (int k = 1; k < nw; k++) ss += part[k];
+    }
     const float s = 1.0f / sqrtf(ss / (float)dim + eps);
     float* orow = out + row * ld_out;
 #pragma unroll
     for (int i = 0; i < NV; i++) {
-        const int c = (i * 64 + lane) * 4;
+        const int c = (i * nthr + tid) * 4;
         if (c < dim) {
             const float4 wv = load_w4<DT>(w, c);
             float4 o;
@@ -113,33 +124,25 @@ static int launch_rmsnorm_dt(float* out, float* x, const float* y, const void* w
                              int dim, long ld_x, long ld_y, long ld_out, float eps,
                              hipStream_t st) {
     const bool vec = (dim % 4 == 0) && (ld_x % 4 == 0) && (ld_out % 4 == 0) && aligned16(x) &&
-                     aligned16(out) && (DT == ANELM_F32 ? aligned16(w) : aligned8(w)) &&
+                     aligned16(out) &&
+                     (DT == ANELM_F32 ? aligned16(w) : aligned8(w)) &&
                      (!ADD || ((ld_y % 4 == 0) && aligned16(y)));
-    const int nv = (dim + 255) / 256;
-    const dim3 blk(256);
-    const dim3 grd((unsigned)((rows + 3) / 4));
-#define ANELM_RMS_CASE(N)                                                                       \
-    if (nv <= N) {                                                                              \
-        rmsnorm_wave_kernel<N, DT, ADD><<<grd, blk, 0, st>>>(out, x, y, w, rows, dim, ld_x, ld_y, \
-                                                             ld_out, eps);                      \
-        return launch_status("rmsnorm");                                                        \
+    const int nvec = dim / 4;  // float4 per row
+    if (vec && nvec <= 1024 * 4) {
+        // two float4 per lane where the row allows it, at most 16 waves
+        int nv = nvec <= 1024 * 2 ? (nvec <= 64 ? 1 : 2) : 4;
+        int threads = ((nvec + nv - 1) / nv + 63) / 64 * 64;
+        const dim3 grd((unsigned)rows);
+        if (nv == 1)
+            rmsnorm_row_kernel<1, DT, ADD><<<grd, threads, 0, st>>>(out, x, y, w, rows, dim, ld_x, ld_y, ld_out, eps);
+        else if (nv == 2)
+            rmsnorm_row_kernel<2, DT, ADD><<<grd, threads, 0, st>>>(out, x, y, w, rows, dim, ld_x, ld_y, ld_out, eps);
+        else
+            rmsnorm_row_kernel<4, DT, ADD><<<grd, threads, 0, st>>>(out, x, y, w, rows, dim, ld_x, ld_y, ld_out, eps);
+        return launch_status("rmsnorm");
     }
-    if (vec) {
-        ANELM_RMS_CASE(1)
-        ANELM_RMS_CASE(2)
-        ANELM_RMS_CASE(4)
-        ANELM_RMS_CASE(6)
-        ANELM_RMS_CASE(8)
-        ANELM_RMS_CASE(10)
-        ANELM_RMS_CASE(12)
-        ANELM_RMS_CASE(16)
-        ANELM_RMS_CASE(20)
-        ANELM_RMS_CASE(24)
-        ANELM_RMS_CASE(32)
-    }
-#undef ANELM_RMS_CASE
-    rmsnorm_block_kernel<DT, ADD><<<dim3((unsigned)rows), blk, 0, st>>>(out, x, y, w, rows, dim, ld_x,
-                                                                        ld_y, ld_out, eps);
+    rmsnorm_block_kernel<DT, ADD><<<dim3((unsigned)rows), dim3(256), 0, st>>>(out, x, y, w, rows, dim, ld_x,
+                                                                              ld_y, ld_out, eps);
     return launch_status("rmsnorm");
 }
 
@@ -163,21 +166,34 @@ static int launch_rmsnorm(float* out, float* x, const float* y, const void* w, i
 // with c/s from table row pos (0 <= pos < tab_len, qwen3.cpp:463-469) or the
 // fallback angle pos*inv_freq[j] (qwen3.cpp:39-49).
 //
-// head_dim 128 kernel: one wave per token.  A 16-lane group owns one head:
-// lane l holds elements 4l..4l+3 and 64+4l..64+4l+3, so each rotation pair
-// sits in one lane and the sum of squares is a 16-lane shuffle reduction.
-// The token's cos/sin row and both gammas are loaded once and reused for
-// all nq+nk heads.
+// head_dim 128 kernel: a flat grid over every head of every token (the T*nq
+// q heads, then the T*nk k heads).  A 16-lane group owns one head: lane l
+// holds elements 4l..4l+3 and 64+4l..64+4l+3, so each rotation pair sits in
+// one lane and the sum of squares is a 16-lane shuffle reduction.  A head is
+// read once and written once (non-temporal); its token's cos/sin row and
+// the gammas are shared by all heads and come from cache.
 template <int DT>
 __global__ __launch_bounds__(256) void qknorm_rope128_kernel(
     float* q, float* k, long q_ld, long k_ld, const void* wq, const void* wk, const int32_t* pos,
     const float* cos_tab, const float* sin_tab, int tab_len, const InvFreq inv, long T, int nq,
     int nk, float eps) {
-    const int lane = threadIdx.x & 63;
-    const long t = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (t >= T) return;
-    const int slot = lane >> 4;
-    const int j0 = 4 * (lane & 15);
+    const long gh = ((long)blockIdx.x * 256 + threadIdx.x) >> 4;
+    const int j0 = 4 * (threadIdx.x & 15);
+    const long nqh = T * nq;
+    if (gh >= nqh + T * nk) return;
+    const bool isq = gh < nqh;
+    long t;
+    float* v;
+    if (isq) {
+        t = gh / nq;
+        v = q + t * q_ld + (gh - t * nq) * 128;
+    } else {
+        const long g2 = gh - nqh;
+        t = g2 / nk;
+        v = k + t * k_ld + (g2 - t * nk) * 128;
+    }
+    float4 lo = ld_nt(reinterpret_cast<const float4*>(v + j0));
+    float4 hi = ld_nt(reinterpret_cast<const float4*>(v + 64 + j0));
     const int p = pos[t];
     float4 c, s;
     if (p >= 0 && p < tab_len) {
@@ -190,62 +206,41 @@ __global__ __launch_bounds__(256) void qknorm_rope128_kernel(
         c = make_float4(cosf(a0), cosf(a1), cosf(a2), cosf(a3));
         s = make_float4(sinf(a0), sinf(a1), sinf(a2), sinf(a3));
     }
-    const bool nq_on = wq != nullptr, nk_on = wk != nullptr;
-    const float4 one4 = make_float4(1.f, 1.f, 1.f, 1.f);
-    const float4 wql = nq_on ? load_w4<DT>(wq, j0) : one4;
-    const float4 wqh = nq_on ? load_w4<DT>(wq, j0 + 64) : one4;
-    const float4 wkl = nk_on ? load_w4<DT>(wk, j0) : one4;
-    const float4 wkh = nk_on ? load_w4<DT>(wk, j0 + 64) : one4;
-    const int nh = nq + nk;
-    float* qt = q + t * q_ld;
-    float* kt = k + t * k_ld;
-    for (int hb = 0; hb < nh; hb += 4) {
-        const int h = hb + slot;
-        const bool act = h < nh;
-        const bool isq = h < nq;
-        float* v = isq ? qt + (long)h * 128 : kt + (long)(h - nq) * 128;
-        float4 lo = make_float4(0.f, 0.f, 0.f, 0.f), hi = lo;
-        if (act) {
-            lo = *reinterpret_cast<const float4*>(v + j0);
-            hi = *reinterpret_cast<const float4*>(v + 64 + j0);
-        }
-        float ss = 0.f;
-        ss = fmaf(lo.x, lo.x, ss);
-        ss = fmaf(lo.y, lo.y, ss);
-        ss = fmaf(lo.z, lo.z, ss);
-        ss = fmaf(lo.w, lo.w, ss);
-        ss = fmaf(hi.x, hi.x, ss);
-        ss = fmaf(hi.y, hi.y, ss);
-        ss = fmaf(hi.z, hi.z, ss);
-        ss = fmaf(hi.w, hi.w, ss);
-        ss = group16_sum(ss);
-        if (isq ? nq_on : nk_on) {
-            const float sc = 1.0f / sqrtf(ss / 128.0f + eps);
-            const float4 wl = isq ? wql : wkl;
-            const float4 wh = isq ? wqh : wkh;
-            lo.x = (lo.x * sc) * wl.x;
-            lo.y = (lo.y * sc) * wl.y;
-            lo.z = (lo.z * sc) * wl.z;
-            lo.w = (lo.w * sc) * wl.w;
-            hi.x = (hi.x * sc) * wh.x;
-            hi.y = (hi.y * sc) * wh.y;
-            hi.z = (hi.z * sc) * wh.z;
-            hi.w = (hi.w * sc) * wh.w;
-        }
-        float4 ol, oh;
-        ol.x = lo.x * c.x - hi.x * s.x;
-        ol.y = lo.y * c.y - hi.y * s.y;
-        ol.z = lo.z * c.z - hi.z * s.z;
-        ol.w = lo.w * c.w - hi.w * s.w;
-        oh.x = hi.x * c.x + lo.x * s.x;
-        oh.y = hi.y * c.y + lo.y * s.y;
-        oh.z = hi.z * c.z + lo.z * s.z;
-        oh.w = hi.w * c.w + lo.w * s.w;
-        if (act) {
-            *reinterpret_cast<float4*>(v + j0) = ol;
-            *reinterpret_cast<float4*>(v + 64 + j0) = oh;
-        }
+    float ss = 0.f;
+    ss = fmaf(lo.x, lo.x, ss);
+    ss = fmaf(lo.y, lo.y, ss);
+    ss = fmaf(lo.z, lo.z, ss);
+    ss = fmaf(lo.w, lo.w, ss);
+    ss = fmaf(hi.x, hi.x, ss);
+    ss = fmaf(hi.y, hi.y, ss);
+    ss = fmaf(hi.z, hi.z, ss);
+    ss = fmaf(hi.w, hi.w, ss);
+    ss = group16_sum(ss);
+    const void* w = isq ? wq : wk;
+    if (w) {
+        const float sc = 1.0f / sqrtf(ss / 128.0f + eps);
+        const float4 wl = load_w4<DT>(w, j0);
+        const float4 wh = load_w4<DT>(w, j0 + 64);
+        lo.x = (lo.x * sc) * wl.x;
+        lo.y = (lo.y * sc) * wl.y;
+        lo.z = (lo.z * sc) * wl.z;
+        lo.w = (lo.w * sc) * wl.w;
+        hi.x = (hi.x * sc) * wh.x;
+        hi.y = (hi.y * sc) * wh.y;
+        hi.z = (hi.z * sc) * wh.z;
+        hi.w = (hi.w * sc) * wh.w;
     }
+    float4 ol, oh;
+    ol.x = lo.x * c.x - hi.x * s.x;
+    ol.y = lo.y * c.y - hi.y * s.y;
+    ol.z = lo.z * c.z - hi.z * s.z;
+    ol.w = lo.w * c.w - hi.w * s.w;
+    oh.x = hi.x * c.x + lo.x * s.x;
+    oh.y = hi.y * c.y + lo.y * s.y;
+    oh.z = hi.z * c.z + lo.z * s.z;
+    oh.w = hi.w * c.w + lo.w * s.w;
+    st_nt(reinterpret_cast<float4*>(v + j0), ol);
+    st_nt(reinterpret_cast<float4*>(v + 64 + j0), oh);
 }
 
 // Any even head_dim <= 1024: one wave per (token, head), two passes.
@@ -371,7 +366,8 @@ static int launch_qknorm(float* q, float* k, long q_ld, long k_ld, const void* w
                       (!wq || (DT == ANELM_F32 ? aligned16(wq) : aligned8(wq))) &&
                       (!wk || (DT == ANELM_F32 ? aligned16(wk) : aligned8(wk)));
     if (fast) {
-        qknorm_rope128_kernel<DT><<<dim3((unsigned)((T + 3) / 4)), dim3(256), 0, st>>>(
+        const long heads = T * (nq + nk);
+        qknorm_rope128_kernel<DT><<<dim3((unsigned)((heads * 16 + 255) / 256)), dim3(256), 0, st>>>(
             q, k, q_ld, k_ld, wq, wk, pos, cos_tab, sin_tab, tab_len, inv, T, nq, nk, eps);
     } else {
         const long waves = T * (nq + nk);
@@ -392,7 +388,7 @@ extern "C" int anelm_qknorm_rope(float* q, float* k, long q_ld, long k_ld, const
     if ((nq > 0 && q_ld < (long)nq * head_dim) || (nk > 0 && k_ld < (long)nk * head_dim))
         return fail(ANELM_ERR_INVALID, "anelm_qknorm_rope: token stride too small");
     if (tab_len < 0 || (tab_len > 0 && (!cos_tab || !sin_tab))) return fail(ANELM_ERR_INVALID, "anelm_qknorm_rope: table");
-    if (T * (nq + nk) / 4 + 1 > 0x7FFFFFFFL) return fail(ANELM_ERR_INVALID, "anelm_qknorm_rope: too large");
+    if (T * (nq + nk) / 4 + 1 > 0x7FFFFFFFL || T > (1L << 40)) return fail(ANELM_ERR_INVALID, "anelm_qknorm_rope: too large");
     if (w_dtype < ANELM_F32 || w_dtype > ANELM_BF16) return fail(ANELM_ERR_INVALID, "anelm_qknorm_rope: dtype");
     InvFreq inv;
     rope_inv_freq(&inv, head_dim, theta);

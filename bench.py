@@ -1,13 +1,18 @@
-"""Benchmark of the fused layer-op chain on one MI355X.
+"""Benchmark of the fused layer-op path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
 
-A step is one pass of the op chain over all layers of the workload:
+A step is one pass of the op chain over all layers of the headline workload
+(the Qwen3-8B-shaped prefill, T=8192, 36 layers):
   (1) RMSNorm  (2) q/k-norm + RoPE  (3) residual add + RMSNorm
   (4) SwiGLU   (5) residual add
-(models/llm/qwen3.cpp:502-528), on synthetic device-resident inputs with
-distinct per-layer inputs.  `value` is the chain's algorithmic HBM bytes per
-step divided by the measured step time (GB/s).  Prints one JSON line.
+in the order of models/llm/qwen3.cpp:502-528, on synthetic device-resident
+inputs (distinct inputs per layer).  The step is captured once into a HIP
+graph and replayed, so host launch overhead is not measured.  `value` is the
+chain's algorithmic HBM bytes per step divided by the measured step time.
+The same JSON line also reports the other configurations (0.6B decode and
+prefill, 4B batched decode, the sampling tail, the bf16->fp16 convert of the
+8.19 B-parameter set) and the CPU oracle timed on this host.
 """
 from __future__ import annotations
 
@@ -25,22 +30,17 @@ METRIC = "fused layer-op HBM GB/s (% of peak) + µs/layer-chain, Qwen3 shapes, 1
 D = 128
 THETA = 1e6
 EPS = 1e-6
+VOCAB = 151936
 
 WORKLOADS = {
-    # Qwen3-8B-shaped prefill, T=8192 (the target configuration)
-    "qwen3-8b-prefill": dict(T=8192, H=4096, nq=32, nk=8, I=12288, layers=36, positions="sequential", pmax=8192,
-                             convert=True),
-    # Qwen3-0.6B prefill, T=2048
-    "qwen3-0.6b-prefill": dict(T=2048, H=1024, nq=16, nk=8, I=3072, layers=28, positions="sequential", pmax=2048,
-                               convert=False),
-    # Qwen3-4B batched decode, 64 sequences
+    "qwen3-8b-prefill": dict(T=8192, H=4096, nq=32, nk=8, I=12288, layers=36, positions="sequential", pmax=8192),
+    "qwen3-0.6b-prefill": dict(T=2048, H=1024, nq=16, nk=8, I=3072, layers=28, positions="sequential", pmax=2048),
     "qwen3-4b-decode-b64": dict(T=64, H=2560, nq=32, nk=8, I=9728, layers=36, positions="uniform", pmax=32768,
-                                convert=False),
-    # Qwen3-0.6B single-token decode
+                                gather=True),
     "qwen3-0.6b-decode": dict(T=1, H=1024, nq=16, nk=8, I=3072, layers=28, positions="uniform", pmax=4096,
-                              convert=False),
+                              gather=True),
 }
-
+HEADLINE = "qwen3-8b-prefill"
 OPS = ["rmsnorm", "qknorm_rope", "add_rmsnorm", "silu_mul", "residual_add"]
 
 
@@ -49,23 +49,60 @@ def op_bytes(w):
     read once, every output written once (fp32 activations; gammas ignored)."""
     T, H, I, nh = w["T"], w["H"], w["I"], w["nq"] + w["nk"]
     return {
-        "rmsnorm": 2 * T * H * 4,                        # read x, write xn
-        "qknorm_rope": 2 * T * nh * D * 4 + T * (D // 2) * 2 * 4,  # q,k in place + cos/sin rows
-        "add_rmsnorm": 4 * T * H * 4,                    # read x, y; write x, xn
-        "silu_mul": 3 * T * I * 4,                       # read g, u; write h
-        "residual_add": 3 * T * H * 4,                   # read x, y; write x
+        "rmsnorm": 2 * T * H * 4,                                   # read x, write xn
+        "qknorm_rope": 2 * T * nh * D * 4 + T * (D // 2) * 2 * 4,   # q, k in place + cos/sin rows
+        "add_rmsnorm": 4 * T * H * 4,                               # read x, y; write x, xn
+        "silu_mul": 3 * T * I * 4,                                  # read g, u; write h
+        "residual_add": 3 * T * H * 4,                              # read x, y; write x
     }
 
 
+def gather_bytes(w):
+    return w["T"] * w["H"] * (2 + 4) if w.get("gather") else 0   # fp16 row in, fp32 row out
+
+
 def qwen3_8b_tensor_sizes():
-    H, I, V, L = 4096, 12288, 151936, 36
+    H, I, V, L = 4096, 12288, VOCAB, 36
     sizes = [V * H, V * H, H]
     for _ in range(L):
         sizes += [H * H, 1024 * H, 1024 * H, H * H, I * H, I * H, H * I, H, H, D, D]
     return sizes
 
 
+def capture(fn):
+    """Record fn's launches (on torch's current stream) into a HIP graph."""
+    import torch
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    torch.cuda.synchronize()
+    return g
+
+
+def time_region(fn, reps):
+    """Average ms per call of fn over reps calls, HIP events on the current stream."""
+    import torch
+
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    s.record()
+    for _ in range(reps):
+        fn()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / reps
+
+
 class Chain:
+    """Device buffers of one op-chain workload and its per-layer launches."""
+
     def __init__(self, w, seed=0):
         import torch
 
@@ -79,10 +116,8 @@ class Chain:
         self.x = rn(T, H)
         self.xn = torch.empty(T, H, device="cuda")
         self.h = torch.empty(T, I, device="cuda")
-        self.layers = []
-        for _ in range(L):
-            self.layers.append(dict(attn=rn(T, H), mlp=rn(T, H), q=rn(T, nq * D), k=rn(T, nk * D), g=rn(T, I),
-                                    u=rn(T, I), w_in=gamma(H), w_post=gamma(H), wq=gamma(D), wk=gamma(D)))
+        self.layers = [dict(attn=rn(T, H), mlp=rn(T, H), q=rn(T, nq * D), k=rn(T, nk * D), g=rn(T, I), u=rn(T, I),
+                            w_in=gamma(H), w_post=gamma(H), wq=gamma(D), wk=gamma(D)) for _ in range(L)]
         if w["positions"] == "sequential":
             self.pos = torch.arange(T, device="cuda", dtype=torch.int32)
         else:
@@ -90,6 +125,10 @@ class Chain:
         self.cos = torch.empty(16384, D // 2, device="cuda")
         self.sin = torch.empty(16384, D // 2, device="cuda")
         anelm.rope_table(self.cos, self.sin, THETA)
+        self.table = None
+        if w.get("gather"):  # embedding table [151936, H] fp16 ~N(0, 0.02) and the step's token ids
+            self.table = (0.02 * rn(VOCAB, H)).to(torch.float16)
+            self.ids = torch.randint(0, VOCAB, (T,), generator=g, device="cuda", dtype=torch.int32)
 
     def op(self, name, Ld):
         hip, w = self.hip, self.w
@@ -106,26 +145,67 @@ class Chain:
             hip.residual_add(self.x, Ld["mlp"])
 
     def step(self):
+        if self.table is not None:
+            self.hip.embed_gather(self.x, self.table, self.ids)
         for Ld in self.layers:
             for name in OPS:
                 self.op(name, Ld)
 
 
-def time_region(fn, reps):
+def measure_chain(w, steps, warmup, per_op):
     import torch
 
-    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    s.record()
-    for _ in range(reps):
-        fn()
-    e.record()
-    torch.cuda.synchronize()
-    return s.elapsed_time(e) / reps  # ms
+    chain = Chain(w)
+    g = capture(chain.step)
+    for _ in range(warmup):
+        g.replay()
+    ms = time_region(g.replay, steps)
+    ob = op_bytes(w)
+    layer_bytes = sum(ob.values())
+    chain_bytes = layer_bytes * w["layers"] + gather_bytes(w)
+    r = dict(ms_per_step=round(ms, 4), us_per_layer_chain=round(ms * 1e3 / w["layers"], 3),
+             GBps=round(chain_bytes / ms / 1e6, 1), frac=round(chain_bytes / ms / 1e6 / HBM_PEAK_GBPS, 4),
+             tokens_per_s=round(w["T"] / (ms / 1e3), 1), chain_bytes=chain_bytes)
+    if per_op:
+        ops = {}
+        for name in OPS:
+            go = capture(lambda: [chain.op(name, Ld) for Ld in chain.layers])
+            go.replay()
+            t = time_region(go.replay, 3 if w["T"] >= 1024 else 20) / len(chain.layers)
+            ops[name] = dict(us=round(t * 1e3, 2), GBps=round(ob[name] / t / 1e6, 1),
+                             frac=round(ob[name] / t / 1e6 / HBM_PEAK_GBPS, 4), bytes=ob[name])
+            del go
+        r["ops"] = ops
+    del g, chain
+    torch.cuda.empty_cache()
+    return r
 
 
-def bench_convert(hip, reps=3):
-    """bf16->fp16 of the 8,190,735,360-parameter Qwen3-8B set, one call per tensor."""
+def measure_sampler(hip, steps, rows=64, vocab=VOCAB):
+    """Logits [64, 151936] ~N(0,3), history [64, 256], rep 1.2, T 0.6, freq 0.1."""
+    import torch
+
+    g = torch.Generator(device="cuda").manual_seed(21)
+    logits = 3.0 * torch.randn(rows, vocab, generator=g, device="cuda")
+    hist = torch.randint(0, vocab, (rows, 256), generator=g, device="cuda", dtype=torch.int32)
+    r = torch.rand(rows, generator=g, device="cuda")
+    ids = torch.empty(rows, dtype=torch.int32, device="cuda")
+    probs = torch.empty(rows, vocab, device="cuda")
+    ws = torch.empty(hip.sample_workspace_size(rows, vocab), dtype=torch.uint8, device="cuda")
+    p = hip.SamplingParams()
+    call = lambda: hip.sample(ids, probs, logits, hist, None, p, r, ws)
+    gr = capture(call)
+    gr.replay()
+    ms = time_region(gr.replay, steps)
+    byt = 2 * rows * vocab * 4
+    return dict(us=round(ms * 1e3, 2), GBps=round(byt / ms / 1e6, 1), frac=round(byt / ms / 1e6 / HBM_PEAK_GBPS, 4),
+                rows_per_s=round(rows / (ms / 1e3), 1), bytes=byt,
+                note="algorithmic bytes = logits read once + probabilities written once")
+
+
+def measure_convert(hip, reps=3):
+    """bf16->fp16 of the 8,190,735,360-parameter Qwen3-8B set: one call over the
+    contiguous set, and one call per tensor (399 launches, graph-replayed)."""
     import torch
 
     sizes = qwen3_8b_tensor_sizes()
@@ -137,40 +217,47 @@ def bench_convert(hip, reps=3):
         m = min(step, n - i)
         src[i:i + m] = ((torch.randn(m, generator=g, device="cuda") * 0.02).view(torch.int32) >> 16).to(torch.int16)
     dst = torch.empty_like(src)
+    byt = 4 * n
+    one = lambda: hip.bf16_to_f16(dst, src)
+    one()
+    ms_one = time_region(one, reps)
     views = []
     off = 0
     for m in sizes:
         views.append((dst[off:off + m], src[off:off + m]))
         off += m
-
-    def run():
-        for d, s in views:
-            hip.bf16_to_f16(d, s)
-
-    run()
-    ms = time_region(run, reps)
-    del src, dst, views
+    gr = capture(lambda: [hip.bf16_to_f16(d, s) for d, s in views])
+    gr.replay()
+    ms_per = time_region(gr.replay, reps)
+    del src, dst, views, gr
     torch.cuda.empty_cache()
-    byt = 4 * n
-    return dict(params=n, ms=round(ms, 4), GBps=round(byt / ms / 1e6, 1), frac=round(byt / ms / 1e6 / HBM_PEAK_GBPS, 4),
-                bytes=byt, launches=len(sizes))
+    f = lambda ms: dict(ms=round(ms, 4), GBps=round(byt / ms / 1e6, 1), frac=round(byt / ms / 1e6 / HBM_PEAK_GBPS, 4))
+    return dict(params=n, bytes=byt, contiguous_set=f(ms_one), per_tensor=dict(f(ms_per), launches=len(sizes)))
 
 
-def cpu_baseline(w, target_s):
-    """The oracle's per-token layer chain on the host's cores over a bounded
-    sample of the workload: T_s tokens x 4 layers with distinct inputs,
-    repeated until ~target_s seconds have elapsed."""
-    import numpy as np
+# ------------------------------------------------------------------ CPU baseline
 
+def _oracle():
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle
 
-    T = min(w["T"], 512)
+    return oracle
+
+
+def cpu_chain(w, target_s, max_tokens=512, layers=4):
+    """The oracle's per-token layer chain (looping per token as the reference
+    does) on the host's cores, over a bounded sample: up to max_tokens tokens
+    x `layers` distinct layers of the workload's shapes, repeated for about
+    target_s seconds.  Reported in the GPU figure's unit (algorithmic GB/s)."""
+    import numpy as np
+
+    oracle = _oracle()
+    T = min(w["T"], max_tokens)
     H, I, nq, nk = w["H"], w["I"], w["nq"], w["nk"]
-    Ls = 4
     rng = np.random.default_rng(5)
     rn = lambda *s: rng.standard_normal(s, dtype=np.float32)
-    lay = [dict(attn=rn(T, H), mlp=rn(T, H), q=rn(T, nq * D), k=rn(T, nk * D), g=rn(T, I), u=rn(T, I)) for _ in range(Ls)]
+    lay = [dict(attn=rn(T, H), mlp=rn(T, H), q=rn(T, nq * D), k=rn(T, nk * D), g=rn(T, I), u=rn(T, I))
+           for _ in range(layers)]
     gam = lambda n: (1 + 0.02 * rng.standard_normal(n)).astype(np.float16).astype(np.float32)
     w_in, w_post, wq, wk = gam(H), gam(H), gam(D), gam(D)
     x, xn, h = rn(T, H), np.empty((T, H), np.float32), np.empty((T, I), np.float32)
@@ -188,11 +275,49 @@ def cpu_baseline(w, target_s):
         if el >= target_s:
             break
     per_layer_bytes = sum(op_bytes(dict(w, T=T)).values())
-    gbps = per_layer_bytes * Ls * passes / el / 1e9
+    gbps = per_layer_bytes * layers * passes / el / 1e9
+    us_layer = el / (layers * passes) * (w["T"] / T) * 1e6
     return dict(value=round(gbps, 2), unit="GB/s", cores=threads, kind="port",
-                sample=f"oracle layer chain (per-token loop as the reference), {T} tokens x {Ls} distinct layers "
-                       f"of the workload's shapes, {passes} passes in {el:.1f} s on {threads} OpenMP threads",
-                us_per_layer_chain_full_T=round(el / (Ls * passes) * (w["T"] / T) * 1e6, 1))
+                us_per_layer_chain=round(us_layer, 1),
+                sample=f"oracle layer chain, per-token loop as the reference, {T} tokens x {layers} distinct layers "
+                       f"of the workload's shapes, {passes} passes in {el:.1f} s on {threads} OpenMP threads")
+
+
+def cpu_sampler(target_s, rows=64, vocab=VOCAB):
+    import numpy as np
+
+    oracle = _oracle()
+    rng = np.random.default_rng(9)
+    logits = rng.normal(0, 3, (rows, vocab)).astype(np.float32)
+    hist = rng.integers(0, vocab, (rows, 256)).astype(np.int32)
+    t0 = time.perf_counter()
+    done = 0
+    while True:
+        oracle.sample_token(logits[done % rows], recent=hist[done % rows], r=0.5)
+        done += 1
+        el = time.perf_counter() - t0
+        if el >= target_s:
+            break
+    per_row = el / done
+    return dict(us=round(per_row * rows * 1e6, 1), GBps=round(2 * rows * vocab * 4 / (per_row * rows) / 1e9, 2),
+                cores=1, kind="port", sample=f"{done} rows of sample_token on 1 thread (the reference is single-threaded)")
+
+
+def cpu_convert(target_s):
+    import numpy as np
+
+    oracle = _oracle()
+    src = np.random.default_rng(3).integers(0, 65536, 1 << 26, dtype=np.uint32).astype(np.uint16)
+    t0 = time.perf_counter()
+    done = 0
+    while True:
+        oracle.bf16_to_f16(src)
+        done += src.size
+        el = time.perf_counter() - t0
+        if el >= target_s:
+            break
+    return dict(GBps=round(4 * done / el / 1e9, 2), cores=oracle.max_threads(), kind="port",
+                sample=f"{done} parameters in chunks of 2^26 on {oracle.max_threads()} threads")
 
 
 def main():
@@ -200,10 +325,12 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="qwen3-8b-prefill", choices=sorted(WORKLOADS))
-    ap.add_argument("--cpu-seconds", type=float, default=8.0)
+    ap.add_argument("--workload", default=HEADLINE, choices=sorted(WORKLOADS))
+    ap.add_argument("--cpu-seconds", type=float, default=8.0, help="CPU time budget of the headline baseline")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--no-convert", action="store_true")
+    ap.add_argument("--headline-only", action="store_true", help="skip the other configurations")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only time a 1 GiB device-to-device copy (reference for rocprof byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); the op chain shards "
@@ -214,42 +341,46 @@ def main():
 
     import anelm
 
+    if args.calibrate_copy:
+        src = torch.randn(1 << 28, device="cuda")
+        dst = torch.empty_like(src)
+        ms = time_region(lambda: dst.copy_(src), 5)
+        print(json.dumps(dict(calibration="device copy", bytes_read=1 << 30, bytes_written=1 << 30, ms=round(ms, 4),
+                              GBps=round(2 * (1 << 30) / ms / 1e6, 1))))
+        return
+
     anelm.lib()
     w = WORKLOADS[args.workload]
-    chain = Chain(w)
-    for _ in range(args.warmup):
-        chain.step()
-    ms = time_region(chain.step, args.steps)
-
-    # per-op launch durations over the same per-layer buffers
+    head = measure_chain(w, args.steps, args.warmup, per_op=True)
     ob = op_bytes(w)
-    ops = {}
-    reps = 3 if w["T"] >= 1024 else 50
-    for name in OPS:
-        t = time_region(lambda: [chain.op(name, Ld) for Ld in chain.layers], reps) / len(chain.layers)
-        ops[name] = dict(us=round(t * 1e3, 2), GBps=round(ob[name] / t / 1e6, 1),
-                         frac=round(ob[name] / t / 1e6 / HBM_PEAK_GBPS, 4), bytes=ob[name])
-    layer_bytes = sum(ob.values())
-    chain_bytes = layer_bytes * w["layers"]
-    gbps = chain_bytes / ms / 1e6
     dom = max(OPS, key=lambda n: ob[n])
-    roof = dict(bound="hbm", kernel=dom, achieved=ops[dom]["GBps"], peak=HBM_PEAK_GBPS, unit="GB/s",
-                frac=ops[dom]["frac"], traffic=None, algorithmic_bytes_per_launch=ob[dom])
-    del chain
-    torch.cuda.empty_cache()
-
-    extras = {}
-    if w["convert"] and not args.no_convert:
-        extras["convert_bf16_to_f16"] = bench_convert(anelm)
-    cpu = None if args.no_cpu else cpu_baseline(w, args.cpu_seconds)
+    roof = dict(bound="hbm", kernel=dom, achieved=head["ops"][dom]["GBps"], peak=HBM_PEAK_GBPS, unit="GB/s",
+                frac=head["ops"][dom]["frac"], traffic=None, algorithmic_bytes_per_launch=ob[dom])
+    configs = {}
+    if not args.headline_only:
+        for name, wl in WORKLOADS.items():
+            if name != args.workload:
+                configs[name] = measure_chain(wl, max(args.steps, 20), args.warmup, per_op=False)
+        configs["sampling-64x151936"] = measure_sampler(anelm, max(args.steps, 20))
+        configs["convert-qwen3-8b-bf16"] = measure_convert(anelm)
+    cpu = None
+    cpu_configs = {}
+    if not args.no_cpu:
+        cpu = cpu_chain(w, args.cpu_seconds)
+        if not args.headline_only:
+            for name, wl in WORKLOADS.items():
+                if name != args.workload:
+                    cpu_configs[name] = cpu_chain(wl, 1.5, max_tokens=256, layers=2)
+            cpu_configs["sampling-64x151936"] = cpu_sampler(1.5)
+            cpu_configs["convert-qwen3-8b-bf16"] = cpu_convert(1.5)
     out = {
         "metric": METRIC,
-        "value": round(gbps, 1),
+        "value": head["GBps"],
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms, 4),
+        "ms_per_step": head["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -257,15 +388,16 @@ def main():
         "data": "synthetic: seeded device randn activations N(0,1), fp16 gammas 1+N(0,0.02), distinct inputs per layer",
         "config": dict(workload=args.workload, tokens=w["T"], hidden=w["H"], q_heads=w["nq"], kv_heads=w["nk"],
                        head_dim=D, intermediate=w["I"], layers=w["layers"], rope_theta=THETA,
-                       positions=w["positions"]),
-        "frac_of_hbm_peak": round(gbps / HBM_PEAK_GBPS, 4),
-        "us_per_layer_chain": round(ms * 1e3 / w["layers"], 2),
-        "tokens_per_s": round(w["T"] / (ms / 1e3), 1),
-        "chain_bytes_per_step": chain_bytes,
+                       positions=w["positions"], launch="one HIP graph per step"),
+        "frac_of_hbm_peak": head["frac"],
+        "us_per_layer_chain": head["us_per_layer_chain"],
+        "tokens_per_s": head["tokens_per_s"],
+        "chain_bytes_per_step": head["chain_bytes"],
         "roofline": roof,
         "cpu_baseline": cpu,
-        "ops": ops,
-        **extras,
+        "ops": head["ops"],
+        "configs": configs,
+        "cpu_configs": cpu_configs,
     }
     print(json.dumps(out))
 
