@@ -164,8 +164,8 @@ int sample_token(const float* logits, int vocab_size, const SamplingParams& para
     Staging& S = t_stage;
     const long nh = (long)recent_tokens.size();
     const size_t ws = anelm_sample_workspace_size(1, vocab_size);
-    const size_t sz[5] = {(size_t)vocab_size * 4, (size_t)(nh > 0 ? nh : 1) * 4, 16, 16, ws};
-    char* d[5];
+    const size_t sz[6] = {(size_t)vocab_size * 4, (size_t)(nh > 0 ? nh : 1) * 4, 16, 16, ws, (size_t)vocab_size * 4};
+    char* d[6];
     S.get(sz, d);
     S.h2d(d[0], logits, sz[0]);
     if (nh > 0) S.h2d(d[1], recent_tokens.data(), (size_t)nh * 4);
@@ -178,7 +178,8 @@ int sample_token(const float* logits, int vocab_size, const SamplingParams& para
     p.repetition_penalty = params.repetition_penalty;
     p.repetition_context_size = params.repetition_context_size;
     p.frequency_penalty = params.frequency_penalty;
-    check_rc(anelm_sample(reinterpret_cast<int32_t*>(d[3]), nullptr, 0, reinterpret_cast<const float*>(d[0]),
+    check_rc(anelm_sample(reinterpret_cast<int32_t*>(d[3]), reinterpret_cast<float*>(d[5]), vocab_size,
+                          reinterpret_cast<const float*>(d[0]),
                           vocab_size, 1, vocab_size, nh > 0 ? reinterpret_cast<const int32_t*>(d[1]) : nullptr, nh,
                           nullptr, &p, reinterpret_cast<const float*>(d[2]), d[4], ws, S.s()),
              "sample_token");

@@ -170,9 +170,10 @@ typedef struct anelm_sampling_params {
  *    (l>0 ? l/rep : l*rep, only if rep > 1) then l -= freq*count (if freq > 0);
  *  - temperature <= 0: ids[b] = first argmax, r and probs untouched;
  *  - else x *= 1/T, softmax (as anelm_softmax) written to probs (stride
- *    ld_probs; may be NULL), then ids[b] = first i whose SEQUENTIAL fp32
- *    running sum p[0]+...+p[i] is >= r[b], or vocab-1 if none -- computed
- *    exactly, identical to the reference's walk (sampling.cpp:59-65).
+ *    ld_probs; required, it is also the draw's input), then ids[b] = first i
+ *    whose SEQUENTIAL fp32 running sum p[0]+...+p[i] is >= r[b], or vocab-1
+ *    if none -- computed exactly, identical to the reference's walk
+ *    (sampling.cpp:59-65).
  * r[b] is the uniform draw (the reference's (float)drand48()).
  * Needs anelm_sample_workspace_size(rows, vocab) bytes of device workspace. */
 size_t anelm_sample_workspace_size(long rows, long vocab);

@@ -87,15 +87,19 @@ def test_invalid_arguments_return_status_and_message(lib):
     p = anelm.SamplingParams()
     assert lib.anelm_sample(fake, None, 0, fake, 100, 1, 100, None, 0, None, ctypes.byref(p), None, fake, 1 << 20,
                             None) == -1                                                  # r required
-    assert lib.anelm_sample(fake, None, 0, fake, 100, 1, 100, None, 0, None, ctypes.byref(p), fake, fake, 16,
+    assert lib.anelm_sample(fake, None, 0, fake, 100, 1, 100, None, 0, None, ctypes.byref(p), fake, fake, 1 << 20,
+                            None) == -1                                                  # probs required
+    assert lib.anelm_sample(fake, fake, 100, fake, 100, 1, 100, None, 0, None, ctypes.byref(p), fake, fake, 16,
                             None) == -4                                                  # workspace too small
     assert b"workspace" in lib.anelm_last_error()
 
 
 def test_workspace_sizes(lib):
-    # 64 rows x 38 chunks of 4096 logits: u64 sums + f32 maxima + i32 argmax + i32 flags
-    n = 64 * 38
-    assert lib.anelm_sample_workspace_size(64, 151936) == n * 8 + n * 4 * 3
+    # 64 rows x 38 chunks of 4096 logits (u64 sums, f32 maxima, i32 argmax, i32 flags)
+    # + 64 rows x 594 sub-tiles of 256 (two u32 map words, i32 binade class), 16-byte aligned
+    al = lambda b: (b + 15) // 16 * 16
+    n, ns = 64 * 38, 64 * 594
+    assert lib.anelm_sample_workspace_size(64, 151936) == al(n * 8) + 3 * al(n * 4) + 3 * al(ns * 4)
     assert lib.anelm_sample_workspace_size(0, 10) == 0
     assert lib.anelm_softmax_workspace_size(1, 4096) > 0
 

@@ -31,7 +31,8 @@ def run_sample(hip, logits, hist=None, hist_len=None, r=None, want_probs=True, *
     rows, vocab = logits.shape
     p = hip.SamplingParams(**params)
     ids = torch.empty(rows, dtype=torch.int32, device="cuda")
-    probs = torch.empty(rows, vocab, device="cuda") if want_probs else None
+    # the probability buffer is required when sampling (it is the draw's input)
+    probs = torch.empty(rows, vocab, device="cuda") if (want_probs or p.temperature > 0) else None
     ws = torch.empty(hip.sample_workspace_size(rows, vocab), dtype=torch.uint8, device="cuda")
     hip.sample(ids, probs, dev(logits), dev(hist) if hist is not None else None,
                dev(hist_len) if hist_len is not None else None, p, dev(r) if r is not None else None, ws)
