@@ -42,6 +42,23 @@ WORKLOADS = {
 }
 HEADLINE = "qwen3-8b-prefill"
 OPS = ["rmsnorm", "qknorm_rope", "add_rmsnorm", "silu_mul", "residual_add"]
+# the kernel each op launches at the workload shapes: (name fragment, template fragment)
+OP_KERNELS = {"rmsnorm": ("rmsnorm_row_kernel", "false>"), "qknorm_rope": ("qknorm_rope128_kernel", ""),
+              "add_rmsnorm": ("rmsnorm_row_kernel", "true>"), "silu_mul": ("silu_mul_vec_kernel", ""),
+              "residual_add": ("residual_add_vec_kernel", "")}
+PROFILES = os.path.join(ROOT, "profiles")
+# The counter runs behind profiles/pmc_traffic_<workload>.txt (run from the repo root).
+PMC_COMMANDS = [
+    "rocprofv3 --pmc FETCH_SIZE --output-format csv -d gpurun_out/prof_fetch -o bench -- "
+    "python bench.py --headline-only --no-cpu --steps 1 --warmup 0",
+    "rocprofv3 --pmc WRITE_SIZE --output-format csv -d gpurun_out/prof_write -o bench -- "
+    "python bench.py --headline-only --no-cpu --steps 1 --warmup 0",
+    "rocprofv3 --pmc FETCH_SIZE --output-format csv -d gpurun_out/prof_copy_fetch -o copy -- "
+    "python bench.py --calibrate-copy",
+    "rocprofv3 --pmc WRITE_SIZE --output-format csv -d gpurun_out/prof_copy_write -o copy -- "
+    "python bench.py --calibrate-copy",
+]
+COPY_BYTES = 1 << 30  # read and written by --calibrate-copy
 
 
 def op_bytes(w):
@@ -320,6 +337,113 @@ def cpu_convert(target_s):
                 sample=f"{done} parameters in chunks of 2^26 on {oracle.max_threads()} threads")
 
 
+# ------------------------------------------------------------ rocprofv3 summaries
+
+def _csv_rows(d, suffix):
+    import csv
+    import glob
+
+    rows = []
+    for f in sorted(glob.glob(os.path.join(d, "**", "*" + suffix), recursive=True)):
+        with open(f, newline="") as fh:
+            rows += list(csv.DictReader(fh))
+    if not rows:
+        raise SystemExit(f"no *{suffix} under {d}")
+    return rows
+
+
+def _match(name, op):
+    frag, tmpl = OP_KERNELS[op]
+    return frag in name and tmpl in name
+
+
+def _counter_means(d):
+    """{(kernel name, counter): (dispatches, mean value)} of a --pmc run."""
+    acc = {}
+    for r in _csv_rows(d, "counter_collection.csv"):
+        k = (r["Kernel_Name"], r["Counter_Name"])
+        n, t = acc.get(k, (0, 0.0))
+        acc[k] = (n + 1, t + float(r["Counter_Value"]))
+    return {k: (n, t / n) for k, (n, t) in acc.items()}
+
+
+def pmc_summary(fetch_dir, write_dir, copy_fetch_dir, copy_write_dir, workload=HEADLINE):
+    """Text summary of the four counter runs of PMC_COMMANDS: HBM bytes per
+    dispatch of each op's kernel, with FETCH_SIZE / WRITE_SIZE (KiB) scaled
+    by what they read for a plain 1 GiB device copy."""
+    fe, wr = _counter_means(fetch_dir), _counter_means(write_dir)
+    cf, cw = _counter_means(copy_fetch_dir), _counter_means(copy_write_dir)
+    copy_f = max(v for (k, c), (n, v) in cf.items() if "copyBuffer" in k and c == "FETCH_SIZE")
+    copy_w = max(v for (k, c), (n, v) in cw.items() if "copyBuffer" in k and c == "WRITE_SIZE")
+    ff, wf = COPY_BYTES / 1024 / copy_f, COPY_BYTES / 1024 / copy_w
+    ob = op_bytes(WORKLOADS[workload])
+    lines = [f"# HBM traffic per dispatch, workload {workload} (rocprofv3 --pmc, one counter per run)", "#",
+             "# commands (from the repo root):"] + [f"#   {c}" for c in PMC_COMMANDS] + [
+             "#   python bench.py --pmc-summary gpurun_out/prof_fetch gpurun_out/prof_write "
+             "gpurun_out/prof_copy_fetch gpurun_out/prof_copy_write", "#",
+             f"# calibration, 1 GiB device copy: FETCH_SIZE {copy_f:.0f} KiB -> factor {ff:.4f}; "
+             f"WRITE_SIZE {copy_w:.0f} KiB -> factor {wf:.4f}", "",
+             "| op | kernel | dispatches | FETCH_SIZE KiB | WRITE_SIZE KiB | traffic bytes | algorithmic bytes | ratio |",
+             "|---|---|---|---|---|---|---|---|"]
+    traffic = {}
+    for op in OPS:
+        fk = [(k, v) for k, v in fe.items() if k[1] == "FETCH_SIZE" and _match(k[0], op)]
+        wk = [(k, v) for k, v in wr.items() if k[1] == "WRITE_SIZE" and _match(k[0], op)]
+        if not fk or not wk:
+            continue
+        (kname, _), (n, f) = fk[0]
+        _, (_, w_) = wk[0]
+        t = round((f * ff + w_ * wf) * 1024)
+        traffic[op] = t
+        short = kname.split("(")[0].replace("void ", "")
+        lines.append(f"| {op} | `{short}` | {n} | {f:.0f} | {w_:.0f} | {t} | {ob[op]} | {t / ob[op]:.4f} |")
+    lines += ["", "traffic_json: " + json.dumps(dict(workload=workload, fetch_factor=round(ff, 6),
+                                                      write_factor=round(wf, 6), bytes_per_dispatch=traffic))]
+    return "\n".join(lines)
+
+
+def trace_summary(d, command, top=10):
+    """Text summary of a --kernel-trace --stats run: the busiest kernels
+    overall, then every library kernel split by launch shape (the workloads
+    share kernel names, their grids tell them apart)."""
+    rows = _csv_rows(d, "kernel_stats.csv")
+    rows.sort(key=lambda r: -float(r["TotalDurationNs"]))
+    short = lambda n: n.split("(")[0].replace("void ", "")
+    lines = ["# rocprofv3 --kernel-trace --stats", "#", f"# command (from the repo root): {command}", "",
+             "## busiest kernels (kernel_stats.csv)", "",
+             "| kernel | calls | avg us | min us | max us | share % |", "|---|---|---|---|---|---|"]
+    for r in rows[:top]:
+        lines.append(f"| `{short(r['Name'])[:100]}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | "
+                     f"{float(r['MinNs']) / 1e3:.2f} | {float(r['MaxNs']) / 1e3:.2f} | {float(r['Percentage']):.2f} |")
+    groups = {}
+    for r in _csv_rows(d, "kernel_trace.csv"):
+        name = short(r["Kernel_Name"])
+        if not name.startswith("anelm::"):
+            continue
+        grid = "x".join(r[f"Grid_Size_{c}"] for c in "XYZ")
+        key = (name, grid, r["Workgroup_Size_X"])
+        groups.setdefault(key, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    lines += ["", "## library kernels by launch shape (kernel_trace.csv)", "",
+              "| kernel | grid (threads) | workgroup | calls | avg us | min us | max us |",
+              "|---|---|---|---|---|---|---|"]
+    for (name, grid, wg), t in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
+        lines.append(f"| `{name}` | {grid} | {wg} | {len(t)} | {sum(t) / len(t):.2f} | {min(t):.2f} | {max(t):.2f} |")
+    return "\n".join(lines)
+
+
+def load_traffic(workload, op):
+    """Calibrated HBM bytes per dispatch of op's kernel from the committed
+    counter summary, or None if there is none for this workload."""
+    f = os.path.join(PROFILES, f"pmc_traffic_{workload}.txt")
+    if not os.path.exists(f):
+        return None
+    with open(f) as fh:
+        for line in fh:
+            if line.startswith("traffic_json: "):
+                return json.loads(line[len("traffic_json: "):])["bytes_per_dispatch"].get(op)
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -331,7 +455,17 @@ def main():
     ap.add_argument("--headline-only", action="store_true", help="skip the other configurations")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only time a 1 GiB device-to-device copy (reference for rocprof byte counters)")
+    ap.add_argument("--pmc-summary", nargs=4, metavar=("FETCH", "WRITE", "COPY_FETCH", "COPY_WRITE"),
+                    help="print the traffic summary of four rocprofv3 --pmc output directories and exit")
+    ap.add_argument("--trace-summary", nargs=2, metavar=("DIR", "COMMAND"),
+                    help="print the summary of a rocprofv3 --kernel-trace --stats directory and exit")
     args = ap.parse_args()
+    if args.pmc_summary:
+        print(pmc_summary(*args.pmc_summary, workload=args.workload))
+        return
+    if args.trace_summary:
+        print(trace_summary(*args.trace_summary))
+        return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); the op chain shards "
               f"per token with no communication, so N GPUs would run N independent copies.", file=sys.stderr)
@@ -355,7 +489,10 @@ def main():
     ob = op_bytes(w)
     dom = max(OPS, key=lambda n: ob[n])
     roof = dict(bound="hbm", kernel=dom, achieved=head["ops"][dom]["GBps"], peak=HBM_PEAK_GBPS, unit="GB/s",
-                frac=head["ops"][dom]["frac"], traffic=None, algorithmic_bytes_per_launch=ob[dom])
+                frac=head["ops"][dom]["frac"], traffic=load_traffic(args.workload, dom),
+                algorithmic_bytes_per_launch=ob[dom],
+                traffic_source=f"profiles/pmc_traffic_{args.workload}.txt (FETCH_SIZE, WRITE_SIZE per dispatch, "
+                               f"copy-calibrated)")
     configs = {}
     if not args.headline_only:
         for name, wl in WORKLOADS.items():
