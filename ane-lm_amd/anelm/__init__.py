@@ -66,6 +66,10 @@ _SIGS = {
     "anelm_softmax": (_I, [_P, _L, _L, _L, _P, _S, _P]),
     "anelm_sample_workspace_size": (_S, [_L, _L]),
     "anelm_sample": (_I, [_P, _P, _L, _P, _L, _L, _L, _P, _L, _P, ctypes.POINTER(SamplingParams), _P, _P, _S, _P]),
+    "anelm_gqa_workspace_size": (_S, [_L, _I, _I, _I, _I]),
+    "anelm_gqa_attention": (_I, [_P, _P, _P, _P, _P, _P, _L, _I, _I, _I, _L, _I, _L, _I, _L, _P, _S, _P]),
+    "anelm_gqa_attention_ring": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _S, _P]),
+    "anelm_kv_ring_append": (_I, [_P, _P, _P, _P, _P, _P, _L, _L, _L, _I, _I, _I, _L, _P]),
 }
 
 EXPORTED = tuple(_SIGS)
@@ -237,3 +241,46 @@ def sample(ids, probs, logits, hist, hist_len, params: SamplingParams, r, worksp
                               _ptr(hist) if hist_ld else None, hist_ld, _ptr(hist_len), ctypes.byref(params),
                               _ptr(r), _ptr(workspace), workspace.numel() * workspace.element_size(),
                               _stream(stream)))
+
+
+def gqa_workspace_size(batch, n_heads, n_kv_heads, head_dim, capacity) -> int:
+    return lib().anelm_gqa_workspace_size(batch, n_heads, n_kv_heads, head_dim, capacity)
+
+
+def _nbytes(t):
+    return 0 if t is None else t.numel() * t.element_size()
+
+
+def gqa_attention(out, q, k_cache, v_cache, ring_start, ring_len, n_heads, n_kv_heads, head_dim, workspace,
+                  q_head_stride=None, stream=None):
+    """Batched decode attention.  q: [B, >= (n_heads-1)*q_head_stride + head_dim];
+    out: [B, >= n_heads*head_dim]; caches: [B, capacity, n_kv_heads*head_dim]
+    (any per-sequence stride); ring_start / ring_len: int32 [B]."""
+    B = q.shape[0]
+    cap = k_cache.shape[1]
+    _need(k_cache.stride() == v_cache.stride() and k_cache.stride(2) == 1 and k_cache.stride(1) == n_kv_heads * head_dim,
+          "gqa_attention: cache layout")
+    _check(lib().anelm_gqa_attention(_ptr(out), _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(ring_start),
+                                     _ptr(ring_len), B, n_heads, n_kv_heads, head_dim, _ld(q),
+                                     head_dim if q_head_stride is None else q_head_stride, _ld(out), cap,
+                                     k_cache.stride(0), _ptr(workspace), _nbytes(workspace), _stream(stream)))
+
+
+def gqa_attention_ring(out, q, k_cache, v_cache, n_heads, n_kv_heads, head_dim, cache_start, cache_len, workspace,
+                       q_head_stride=None, stream=None):
+    """The reference's single-sequence form (core/cpu_ops.cpp:173-240) with
+    host ring state; caches [capacity, n_kv_heads*head_dim]."""
+    cap = k_cache.shape[0]
+    _check(lib().anelm_gqa_attention_ring(_ptr(out), _ptr(q), _ptr(k_cache), _ptr(v_cache), n_heads, n_kv_heads,
+                                          head_dim, head_dim if q_head_stride is None else q_head_stride,
+                                          cache_start, cache_len, cap, _ptr(workspace), _nbytes(workspace),
+                                          _stream(stream)))
+
+
+def kv_ring_append(k_cache, v_cache, ring_start, ring_len, k, v, stream=None):
+    """Append row b of k, v ([B, n_kv_heads*head_dim]) to sequence b's ring
+    (caches [B, capacity, n_kv_heads*head_dim]) and advance its state."""
+    B, cap, row = k_cache.shape
+    _need(k.shape[1] == row and v.shape[1] == row and k_cache.stride() == v_cache.stride(), "kv_ring_append: shapes")
+    _check(lib().anelm_kv_ring_append(_ptr(k_cache), _ptr(v_cache), _ptr(ring_start), _ptr(ring_len), _ptr(k),
+                                      _ptr(v), _ld(k), _ld(v), B, 1, row, cap, k_cache.stride(0), _stream(stream)))

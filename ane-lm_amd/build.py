@@ -27,6 +27,7 @@ SOURCES = [
     os.path.join(CSRC, "norm.hip"),
     os.path.join(CSRC, "elementwise.hip"),
     os.path.join(CSRC, "sampling.hip"),
+    os.path.join(CSRC, "attention.hip"),
     os.path.join(HOST, "dropin.hip"),
 ]
 

@@ -1,0 +1,519 @@
+// GQA decode attention over per-sequence KV rings, and the ring append, for
+// gfx950.  Replaces ane_lm::gqa_attention (core/cpu_ops.cpp:173-240) and the
+// ring bookkeeping + row copies of models/llm/qwen3.cpp:475-488.
+//
+// Data layout: for sequence b the caches are k_cache/v_cache +
+// b*cache_seq_stride, each [capacity, n_kv_heads, head_dim] fp32 (the
+// reference's per-layer KVCache layout, qwen3.cpp:227-231).  The live rows
+// are positions start, start+1, ... (mod capacity), len of them.
+//
+// Decode attention is HBM-bound on the cache: each K and V row of a kv head
+// is read once and shared by all q heads of its group.  A workgroup owns one
+// (sequence, kv head, chunk of <= 512 ring positions):
+//   phase 1: 16 lanes per position (head_dim 128) hold 8 floats each of the
+//            K row; dots for all group heads, reduced in-row with DPP;
+//   phase 2: chunk softmax numerators (max, exp, sum) in LDS;
+//   phase 3: the same position mapping over V rows, weighted accumulation.
+// With one chunk per sequence the workgroup writes the normalised output;
+// otherwise it writes (max, sum, unnormalised output) partials that a second
+// kernel merges.
+#include "anelm_common.hpp"
+
+namespace anelm {
+namespace {
+
+constexpr int kAttnThreads = 256;     // 4 waves
+constexpr int kAttnWaves = kAttnThreads / kWave;
+constexpr int kMaxChunk = 512;        // ring positions per workgroup
+constexpr int kMinChunk = 32;
+constexpr int kMaxGD = 1024;          // group heads x head_dim per workgroup
+constexpr long kTargetBlocks = 2048;  // 8 workgroups per CU on 256 CUs
+constexpr int kMaxSplit = 4096;       // chunks per sequence (capacity <= 4096*32)
+
+struct AttnArgs {
+    float* out;
+    const float* q;
+    const float* kc;
+    const float* vc;
+    const int32_t* ring_start;  // [batch] or null (then start0)
+    const int32_t* ring_len;    // [batch] or null (then len0)
+    int start0, len0;
+    int nh, nkv, groups;
+    long q_ld;                  // between sequences (elements)
+    int q_hs;                   // between q heads
+    long out_ld;                // between sequences; heads are head_dim apart
+    int cap;
+    long seq_stride;            // between sequences' caches
+    int chunk, nsplit;
+    int g0, gcount;             // q heads g0 .. g0+gcount-1 of every group
+    float scale;
+    float* ws;                  // [batch*nh][nsplit][head_dim + 2] partials
+};
+
+// The ring state of sequence b, clamped so that every access stays inside
+// the caches: 0 <= len <= cap, 0 <= start < cap.
+__device__ __forceinline__ void ring_state(const AttnArgs& a, long b, int& start, int& len) {
+    int s = a.ring_start ? a.ring_start[b] : a.start0;
+    int l = a.ring_len ? a.ring_len[b] : a.len0;
+    l = l < 0 ? 0 : (l > a.cap ? a.cap : l);
+    s %= a.cap;
+    if (s < 0) s += a.cap;
+    start = s;
+    len = l;
+}
+
+// Ring slot of chunk position t (clamped to the chunk's last position n-1,
+// n >= 1): start < cap and t0 + t < len <= cap, so one wrap suffices.
+__device__ __forceinline__ int ring_slot(const AttnArgs& a, int start, int t0, int t, int n) {
+    int slot = start + t0 + (t < n ? t : n - 1);
+    if (slot >= a.cap) slot -= a.cap;
+    return slot;
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over aligned groups of LP lanes (8, 16 or 32); every lane of a group
+// receives the same value.
+template <int LP>
+__device__ __forceinline__ float lp_sum(float v) {
+    v += dpp<0xB1>(v);                       // quad_perm [1,0,3,2]
+    v += dpp<0x4E>(v);                       // quad_perm [2,3,0,1]
+    v += dpp<0x141>(v);                      // row_half_mirror: the other quad
+    if (LP >= 16) v += dpp<0x140>(v);        // row_mirror: the other 8 lanes
+    if (LP >= 32) v += __shfl_xor(v, 16);
+    return v;
+}
+
+// A lane's 8 elements of a head row: 4 at p[0..3] and 4 at p[D/2..D/2+3],
+// with p = row + 4*ds, so that each load instruction of a lane group covers
+// one contiguous half row.  NT: streamed once (non-temporal).
+template <int D, bool NT>
+__device__ __forceinline__ void load8(float (&x)[8], const float* p) {
+    const float4* a4 = reinterpret_cast<const float4*>(p);
+    const float4* b4 = reinterpret_cast<const float4*>(p + D / 2);
+    const float4 a = NT ? ld_nt(a4) : *a4;
+    const float4 b = NT ? ld_nt(b4) : *b4;
+    x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+    x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+}
+// head-row element held in slot i of lane slice ds
+template <int D>
+__device__ __forceinline__ int elem_of(int ds, int i) { return (i < 4 ? 0 : D / 2 - 4) + 4 * ds + i; }
+
+template <int D, int GM, bool FINAL>
+__global__ __launch_bounds__(kAttnThreads) void gqa_decode_kernel(AttnArgs a) {
+    constexpr int LP = D / 8;                  // lanes per position
+    constexpr int PPW = kWave / LP;            // positions per wave per round
+    constexpr int PPB = PPW * kAttnWaves;      // positions per workgroup per round
+    constexpr int U = 2;                       // rounds per batch of loads (two batches in flight)
+    constexpr int STEP = U * PPB;              // positions per batch
+    __shared__ float sc[GM][kMaxChunk];        // scores, then weights
+    __shared__ float red[kAttnWaves][GM][D];   // per-wave partial outputs
+    __shared__ float hm[GM], hl[GM];
+
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), wid = tid / kWave;
+    const int split = blockIdx.x, kvh = blockIdx.y;
+    const long b = blockIdx.z;
+    int start, len;
+    ring_state(a, b, start, len);
+    const int t0 = split * a.chunk;
+    const int n = min(t0 + a.chunk, len) - t0;     // positions of this chunk (may be <= 0)
+    const int ps = wid * PPW + lane / LP;          // position slot within a round
+    const int ds = lane % LP;                      // this lane's 8-float slice
+    const int row = a.nkv * D;                     // cap * row < 2^31 (checked on the host)
+    const long off = b * a.seq_stride + (long)kvh * D + 4 * ds;
+    const float* kbase = a.kc + off;
+    const float* vbase = a.vc + off;
+    const int gc = a.gcount;
+
+    // A batch is U rounds of PPB positions.  Batches are double-buffered in
+    // registers: the next batch's loads are in flight while this one is
+    // used.  Positions past the chunk re-read its last row (n >= 1 inside
+    // the loops) and are discarded.
+    auto load_batch = [&](float (&buf)[U][8], const float* base, int r0) {
+#pragma unroll
+        for (int u = 0; u < U; u++) load8<D, true>(buf[u], base + ring_slot(a, start, t0, r0 + u * PPB + ps, n) * row);
+    };
+
+    // phase 1: scores
+    {
+        float qv[GM][8];
+#pragma unroll
+        for (int g = 0; g < GM; g++) {
+            if (g < gc) {
+                load8<D, false>(qv[g], a.q + b * a.q_ld + (long)(kvh * a.groups + a.g0 + g) * a.q_hs + 4 * ds);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; i++) qv[g][i] = 0.0f;
+            }
+        }
+        auto scores = [&](const float (&kx)[U][8], int r0) {
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const int t = r0 + u * PPB + ps;
+                float mine = 0.0f;
+#pragma unroll
+                for (int g = 0; g < GM; g++) {
+                    float d = qv[g][0] * kx[u][0];
+#pragma unroll
+                    for (int i = 1; i < 8; i++) d = fmaf(qv[g][i], kx[u][i], d);
+                    d = lp_sum<LP>(d);
+                    if (g == ds) mine = d;
+                }
+                if (t < n && ds < gc) sc[ds][t] = mine * a.scale;
+            }
+        };
+        float ka[U][8], kb[U][8];
+        if (n > 0) load_batch(ka, kbase, 0);
+        for (int r0 = 0; r0 < n; r0 += 2 * STEP) {
+            if (r0 + STEP < n) load_batch(kb, kbase, r0 + STEP);
+            scores(ka, r0);
+            if (r0 + STEP >= n) break;
+            if (r0 + 2 * STEP < n) load_batch(ka, kbase, r0 + 2 * STEP);
+            scores(kb, r0 + STEP);
+        }
+    }
+    // the first V batch is in flight across the softmax
+    float va[U][8], vb[U][8];
+    if (n > 0) load_batch(va, vbase, 0);
+    __syncthreads();
+
+    // phase 2: softmax numerators per head over the chunk
+    for (int g = wid; g < gc; g += kAttnWaves) {
+        float m = -INFINITY;
+        for (int i = lane; i < n; i += kWave) m = fmaxf(m, sc[g][i]);
+        m = wave_max(m);
+        float l = 0.0f;
+        for (int i = lane; i < n; i += kWave) {
+            const float e = expf(sc[g][i] - m);
+            sc[g][i] = e;
+            l += e;
+        }
+        l = wave_sum(l);
+        if (FINAL) {  // the reference's p = e * (1/sum) (core/cpu_ops.cpp:97-98)
+            const float inv = 1.0f / l;
+            for (int i = lane; i < n; i += kWave) sc[g][i] = sc[g][i] * inv;
+        }
+        if (lane == 0) {
+            hm[g] = m;
+            hl[g] = l;
+        }
+    }
+    __syncthreads();
+
+    // phase 3: weighted sum of V rows
+    float acc[GM][8];
+#pragma unroll
+    for (int g = 0; g < GM; g++)
+#pragma unroll
+        for (int i = 0; i < 8; i++) acc[g][i] = 0.0f;
+    auto accumulate = [&](const float (&vx)[U][8], int r0) {
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int t = r0 + u * PPB + ps;
+            if (t < n) {
+#pragma unroll
+                for (int g = 0; g < GM; g++) {
+                    if (g < gc) {
+                        const float w = sc[g][t];
+#pragma unroll
+                        for (int i = 0; i < 8; i++) acc[g][i] = fmaf(w, vx[u][i], acc[g][i]);
+                    }
+                }
+            }
+        }
+    };
+    for (int r0 = 0; r0 < n; r0 += 2 * STEP) {
+        if (r0 + STEP < n) load_batch(vb, vbase, r0 + STEP);
+        accumulate(va, r0);
+        if (r0 + STEP >= n) break;
+        if (r0 + 2 * STEP < n) load_batch(va, vbase, r0 + 2 * STEP);
+        accumulate(vb, r0 + STEP);
+    }
+    // reduce over the position slots of the wave (lanes with the same slice)
+#pragma unroll
+    for (int g = 0; g < GM; g++)
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+#pragma unroll
+            for (int o = LP; o < kWave; o <<= 1) acc[g][i] += __shfl_xor(acc[g][i], o);
+    if (lane < LP) {
+#pragma unroll
+        for (int g = 0; g < GM; g++)
+#pragma unroll
+            for (int i = 0; i < 8; i++) red[wid][g][elem_of<D>(ds, i)] = acc[g][i];
+    }
+    __syncthreads();
+    for (int j = tid; j < gc * D; j += kAttnThreads) {
+        const int g = j / D, d = j % D;
+        float s = red[0][g][d];
+#pragma unroll
+        for (int w = 1; w < kAttnWaves; w++) s += red[w][g][d];
+        const int h = kvh * a.groups + a.g0 + g;
+        if (FINAL) {
+            a.out[b * a.out_ld + (long)h * D + d] = s;
+        } else {
+            float* p = a.ws + ((b * a.nh + h) * a.nsplit + split) * (long)(D + 2);
+            p[d] = s;
+            if (d == 0) {
+                p[D] = hm[g];
+                p[D + 1] = hl[g];
+            }
+        }
+    }
+}
+
+// Merges the per-chunk partials of one (sequence, q head): one wave; lane j
+// owns chunks j, j+64, ... for the (max, sum) merge, then every lane sums its
+// head_dim/64 outputs over all chunks with independent loads.
+template <int D>
+__global__ __launch_bounds__(kWave) void gqa_combine_kernel(AttnArgs a) {
+    const int lane = threadIdx.x;
+    const long bh = blockIdx.x;
+    const long b = bh / a.nh;
+    const int h = (int)(bh % a.nh);
+    const float* p = a.ws + bh * a.nsplit * (long)(D + 2);
+    // lane j holds chunk s0 + j's (max, sum); the first 64 stay in registers
+    const float m0 = lane < a.nsplit ? p[lane * (D + 2) + D] : -INFINITY;
+    const float l0 = lane < a.nsplit ? p[lane * (D + 2) + D + 1] : 0.0f;
+    float M = l0 > 0.0f ? m0 : -INFINITY;
+    for (int s = lane + kWave; s < a.nsplit; s += kWave) {
+        if (p[s * (D + 2) + D + 1] > 0.0f) M = fmaxf(M, p[s * (D + 2) + D]);
+    }
+    M = wave_max(M);
+    float L = 0.0f;
+    float o[D / kWave];
+#pragma unroll
+    for (int i = 0; i < D / kWave; i++) o[i] = 0.0f;
+    constexpr int kBatch = 32;   // partials loaded before they are used
+    for (int s0 = 0; s0 < a.nsplit; s0 += kWave) {
+        const int s = s0 + lane;
+        float ms = m0, ls = l0;
+        if (s0 > 0) {
+            ms = s < a.nsplit ? p[s * (D + 2) + D] : -INFINITY;
+            ls = s < a.nsplit ? p[s * (D + 2) + D + 1] : 0.0f;
+        }
+        // an empty chunk (sum 0) contributes nothing; NaN sums propagate
+        const float c = (!(ls > 0.0f) && ls == ls) ? 0.0f : expf(ms - M);
+        L = fmaf(ls, c, L);
+        const int cnt = min(kWave, a.nsplit - s0);
+        for (int j0 = 0; j0 < cnt; j0 += kBatch) {
+            float v[kBatch][D / kWave];
+#pragma unroll
+            for (int j = 0; j < kBatch; j++)
+#pragma unroll
+                for (int i = 0; i < D / kWave; i++)
+                    v[j][i] = j0 + j < cnt ? p[(s0 + j0 + j) * (D + 2) + lane + i * kWave] : 0.0f;
+#pragma unroll
+            for (int j = 0; j < kBatch; j++) {
+                const float cj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(c), j0 + j));
+#pragma unroll
+                for (int i = 0; i < D / kWave; i++) o[i] = fmaf(v[j][i], cj, o[i]);
+            }
+        }
+    }
+    L = wave_sum(L);
+    const float inv = L == 0.0f ? 0.0f : 1.0f / L;   // no live position: zeros (cpu_ops.cpp:177-180)
+#pragma unroll
+    for (int i = 0; i < D / kWave; i++) a.out[b * a.out_ld + (long)h * D + lane + i * kWave] = o[i] * inv;
+}
+
+// Ring append: one workgroup per sequence.
+__global__ __launch_bounds__(256) void kv_append_kernel(float* kc, float* vc, int32_t* rs, int32_t* rl,
+                                                        const float* k, const float* v, long k_ld, long v_ld,
+                                                        int row, int cap, long seq_stride, int vec) {
+    __shared__ int s_slot;
+    const long b = blockIdx.x;
+    if (threadIdx.x == 0) {
+        int s = rs[b], l = rl[b];
+        l = l < 0 ? 0 : (l > cap ? cap : l);
+        s %= cap;
+        if (s < 0) s += cap;
+        int slot;
+        if (l < cap) {                   // qwen3.cpp:476-479
+            slot = s + l;
+            if (slot >= cap) slot -= cap;
+            l++;
+        } else {                         // qwen3.cpp:480-484
+            slot = s;
+            s++;
+            if (s >= cap) s = 0;
+        }
+        s_slot = slot;
+        rs[b] = s;
+        rl[b] = l;
+    }
+    __syncthreads();
+    float* kd = kc + b * seq_stride + (long)s_slot * row;
+    float* vd = vc + b * seq_stride + (long)s_slot * row;
+    const float* ks = k + b * k_ld;
+    const float* vs = v + b * v_ld;
+    if (vec) {
+        for (int i = threadIdx.x; i < row / 4; i += blockDim.x) {
+            reinterpret_cast<float4*>(kd)[i] = reinterpret_cast<const float4*>(ks)[i];
+            reinterpret_cast<float4*>(vd)[i] = reinterpret_cast<const float4*>(vs)[i];
+        }
+    } else {
+        for (int i = threadIdx.x; i < row; i += blockDim.x) {
+            kd[i] = ks[i];
+            vd[i] = vs[i];
+        }
+    }
+}
+
+// Positions per workgroup for a ring of `bound` positions and `pairs`
+// (sequence, kv head) pairs: the largest chunk that still gives about
+// kTargetBlocks workgroups, at least kMinChunk.
+int pick_chunk(long pairs, int bound) {
+    for (int c = kMaxChunk; c > kMinChunk; c >>= 1) {
+        if (pairs * ((bound + c - 1) / c) >= kTargetBlocks) return c;
+    }
+    return kMinChunk;
+}
+
+int group_max(int D) { return kMaxGD / D < 8 ? kMaxGD / D : 8; }
+
+template <int D, int GM>
+void launch_gm(const AttnArgs& a, long batch, hipStream_t st) {
+    const dim3 grid(a.nsplit, a.nkv, batch);
+    if (a.nsplit == 1) {
+        hipLaunchKernelGGL((gqa_decode_kernel<D, GM, true>), grid, dim3(kAttnThreads), 0, st, a);
+    } else {
+        hipLaunchKernelGGL((gqa_decode_kernel<D, GM, false>), grid, dim3(kAttnThreads), 0, st, a);
+    }
+}
+
+template <int D>
+void launch_d(AttnArgs a, long batch, hipStream_t st) {
+    const int gmax = group_max(D);
+    for (int g0 = 0; g0 < a.groups; g0 += gmax) {
+        a.g0 = g0;
+        a.gcount = a.groups - g0 < gmax ? a.groups - g0 : gmax;
+        if (a.gcount <= 1) launch_gm<D, 1>(a, batch, st);
+        else if (a.gcount <= 2) launch_gm<D, 2>(a, batch, st);
+        else if (a.gcount <= 4) launch_gm<D, 4>(a, batch, st);
+        else launch_gm<D, (kMaxGD / D < 8 ? kMaxGD / D : 8)>(a, batch, st);
+    }
+    if (a.nsplit > 1) {
+        hipLaunchKernelGGL((gqa_combine_kernel<D>), dim3(batch * a.nh), dim3(kWave), 0, st, a);
+    }
+}
+
+size_t ws_bytes_for(long batch, int nh, int nkv, int D, int cap) {
+    const int chunk = pick_chunk(batch * nkv, cap);
+    const long nsplit = (cap + chunk - 1) / chunk;
+    if (nsplit <= 1) return 0;
+    return (size_t)batch * nh * nsplit * (D + 2) * sizeof(float);
+}
+
+int check_common(const void* out, const void* q, const void* kc, const void* vc, long batch, int nh, int nkv,
+                 int D, long q_ld, int q_hs, long out_ld, int cap, long seq_stride) {
+    if (!out || !q || !kc || !vc) return fail(ANELM_ERR_INVALID, "gqa_attention: null pointer");
+    if (batch < 0 || nh <= 0 || nkv <= 0 || cap <= 0) return fail(ANELM_ERR_INVALID, "gqa_attention: bad sizes");
+    if (batch > 65535 || nkv > 65535) return fail(ANELM_ERR_INVALID, "gqa_attention: batch and n_kv_heads <= 65535");
+    if (cap > kMaxSplit * kMinChunk) return fail(ANELM_ERR_INVALID, "gqa_attention: capacity above %d", kMaxSplit * kMinChunk);
+    if ((long)cap * nkv * D >= (1L << 31)) return fail(ANELM_ERR_INVALID, "gqa_attention: one sequence's cache above 2^31 floats");
+    if (nh % nkv != 0) return fail(ANELM_ERR_INVALID, "gqa_attention: n_heads %d not a multiple of n_kv_heads %d", nh, nkv);
+    if (D != 64 && D != 128 && D != 256) return fail(ANELM_ERR_INVALID, "gqa_attention: head_dim %d (64, 128 or 256)", D);
+    if (q_hs < D || (batch > 1 && (q_ld < (long)(nh - 1) * q_hs + D || out_ld < (long)nh * D)))
+        return fail(ANELM_ERR_INVALID, "gqa_attention: q/out strides overlap");
+    if (batch > 1 && seq_stride < (long)cap * nkv * D)
+        return fail(ANELM_ERR_INVALID, "gqa_attention: cache_seq_stride smaller than one sequence's cache");
+    if (!aligned16(q) || !aligned16(kc) || !aligned16(vc) || (q_ld & 3) || (q_hs & 3) || (seq_stride & 3))
+        return fail(ANELM_ERR_INVALID, "gqa_attention: q and caches need 16-byte alignment and strides of 4");
+    return ANELM_OK;
+}
+
+int run(AttnArgs a, long batch, int D, int bound, void* ws, size_t ws_bytes, hipStream_t st) {
+    a.groups = a.nh / a.nkv;
+    a.scale = 1.0f / sqrtf((float)D);   // core/cpu_ops.cpp:183
+    a.chunk = pick_chunk(batch * a.nkv, a.cap);
+    a.nsplit = (bound + a.chunk - 1) / a.chunk;
+    if (a.nsplit < 1) a.nsplit = 1;
+    if (a.nsplit > 1) {
+        const size_t need = (size_t)batch * a.nh * a.nsplit * (D + 2) * sizeof(float);
+        if (!ws || ws_bytes < need)
+            return fail(ANELM_ERR_WORKSPACE, "gqa_attention: workspace of %zu bytes needed, %zu given", need, ws_bytes);
+        if (!aligned16(ws)) return fail(ANELM_ERR_INVALID, "gqa_attention: workspace not 16-byte aligned");
+    }
+    a.ws = static_cast<float*>(ws);
+    if (batch == 0) return ANELM_OK;
+    if (D == 64) launch_d<64>(a, batch, st);
+    else if (D == 128) launch_d<128>(a, batch, st);
+    else launch_d<256>(a, batch, st);
+    return launch_status("gqa_attention");
+}
+
+}  // namespace
+}  // namespace anelm
+
+using namespace anelm;
+
+extern "C" size_t anelm_gqa_workspace_size(long batch, int n_heads, int n_kv_heads, int head_dim, int capacity) {
+    if (batch <= 0 || n_heads <= 0 || n_kv_heads <= 0 || head_dim <= 0 || capacity <= 0) return 0;
+    return ws_bytes_for(batch, n_heads, n_kv_heads, head_dim, capacity);
+}
+
+extern "C" int anelm_gqa_attention(float* out, const float* q, const float* k_cache, const float* v_cache,
+                                   const int32_t* ring_start, const int32_t* ring_len, long batch, int n_heads,
+                                   int n_kv_heads, int head_dim, long q_ld, int q_head_stride, long out_ld,
+                                   int capacity, long cache_seq_stride, void* workspace, size_t workspace_bytes,
+                                   void* stream) {
+    clear_error();
+    int rc = check_common(out, q, k_cache, v_cache, batch, n_heads, n_kv_heads, head_dim, q_ld, q_head_stride,
+                          out_ld, capacity, cache_seq_stride);
+    if (rc) return rc;
+    if (!ring_start || !ring_len) return fail(ANELM_ERR_INVALID, "gqa_attention: null ring state");
+    AttnArgs a{};
+    a.out = out; a.q = q; a.kc = k_cache; a.vc = v_cache;
+    a.ring_start = ring_start; a.ring_len = ring_len;
+    a.nh = n_heads; a.nkv = n_kv_heads;
+    a.q_ld = q_ld; a.q_hs = q_head_stride; a.out_ld = out_ld;
+    a.cap = capacity; a.seq_stride = cache_seq_stride;
+    return run(a, batch, head_dim, capacity, workspace, workspace_bytes, as_stream(stream));
+}
+
+extern "C" int anelm_gqa_attention_ring(float* out, const float* q, const float* k_cache, const float* v_cache,
+                                        int n_heads, int n_kv_heads, int head_dim, int q_head_stride,
+                                        int cache_start, int cache_len, int cache_capacity, void* workspace,
+                                        size_t workspace_bytes, void* stream) {
+    clear_error();
+    int rc = check_common(out, q, k_cache, v_cache, 1, n_heads, n_kv_heads, head_dim, 0, q_head_stride, 0,
+                          cache_capacity, 0);
+    if (rc) return rc;
+    if (cache_len > cache_capacity || (cache_len > 0 && (cache_start < 0 || cache_start >= cache_capacity)))
+        return fail(ANELM_ERR_RANGE, "gqa_attention: ring start %d / len %d outside capacity %d", cache_start,
+                    cache_len, cache_capacity);
+    AttnArgs a{};
+    a.out = out; a.q = q; a.kc = k_cache; a.vc = v_cache;
+    a.start0 = cache_len > 0 ? cache_start : 0;
+    a.len0 = cache_len > 0 ? cache_len : 0;
+    a.nh = n_heads; a.nkv = n_kv_heads;
+    a.q_hs = q_head_stride; a.out_ld = (long)n_heads * head_dim;
+    a.cap = cache_capacity; a.seq_stride = (long)cache_capacity * n_kv_heads * head_dim;
+    return run(a, 1, head_dim, a.len0 > 0 ? a.len0 : 1, workspace, workspace_bytes, as_stream(stream));
+}
+
+extern "C" int anelm_kv_ring_append(float* k_cache, float* v_cache, int32_t* ring_start, int32_t* ring_len,
+                                    const float* k, const float* v, long k_ld, long v_ld, long batch,
+                                    int n_kv_heads, int head_dim, int capacity, long cache_seq_stride,
+                                    void* stream) {
+    clear_error();
+    if (!k_cache || !v_cache || !ring_start || !ring_len || !k || !v)
+        return fail(ANELM_ERR_INVALID, "kv_ring_append: null pointer");
+    if (batch < 0 || n_kv_heads <= 0 || head_dim <= 0 || capacity <= 0)
+        return fail(ANELM_ERR_INVALID, "kv_ring_append: bad sizes");
+    const long row = (long)n_kv_heads * head_dim;
+    if (row > (1L << 30)) return fail(ANELM_ERR_INVALID, "kv_ring_append: row too long");
+    if (batch > 1 && (cache_seq_stride < (long)capacity * row || k_ld < row || v_ld < row))
+        return fail(ANELM_ERR_INVALID, "kv_ring_append: strides overlap");
+    if (batch == 0) return ANELM_OK;
+    const int vec = aligned16(k_cache) && aligned16(v_cache) && aligned16(k) && aligned16(v) && !(row & 3) &&
+                    !(k_ld & 3) && !(v_ld & 3) && !(cache_seq_stride & 3);
+    hipLaunchKernelGGL(kv_append_kernel, dim3(batch), dim3(256), 0, as_stream(stream), k_cache, v_cache, ring_start,
+                       ring_len, k, v, k_ld, v_ld, (int)row, capacity, cache_seq_stride, vec);
+    return launch_status("kv_ring_append");
+}

@@ -5,9 +5,9 @@
 // On any device error the call prints the library's message to stderr and
 // aborts: there is no CPU fallback.
 //
-// Only the functions on the fused layer-op path are provided here; matvec,
-// gqa_attention, l2_normalize, conv1d_update, ssm_step and rmsnorm_gated
-// keep their reference definitions.
+// Only the functions on the fused layer-op path and the decode attention are
+// provided here; matvec, l2_normalize, conv1d_update, ssm_step and
+// rmsnorm_gated keep their reference definitions.
 #pragma once
 
 #include <cmath>
@@ -36,6 +36,13 @@ void apply_rope_cached(float* q, float* k, int n_q_heads, int n_kv_heads,
 
 // core/cpu_ops.h:33
 void softmax(float* x, int n);
+
+// core/cpu_ops.h:53-56 -- caches [cache_capacity, n_kv_heads, head_dim]
+// (host memory, staged to the device on every call)
+void gqa_attention(float* out, const float* q,
+                   const float* k_cache, const float* v_cache,
+                   int n_heads, int n_kv_heads, int head_dim, int q_head_stride,
+                   int cache_start, int cache_len, int cache_capacity);
 
 // Additive entry points for the ops the reference performs inline in
 // models/llm/qwen3.cpp (not behind any header there).

@@ -157,6 +157,35 @@ void softmax(float* x, int n) {
     S.sync();
 }
 
+// core/cpu_ops.cpp:173-240
+void gqa_attention(float* out, const float* q, const float* k_cache, const float* v_cache, int n_heads,
+                   int n_kv_heads, int head_dim, int q_head_stride, int cache_start, int cache_len,
+                   int cache_capacity) {
+    if (n_heads <= 0 || head_dim <= 0) return;
+    if (cache_len <= 0) {  // :177-180
+        std::memset(out, 0, (size_t)n_heads * head_dim * sizeof(float));
+        return;
+    }
+    Staging& S = t_stage;
+    const size_t qn = (size_t)(n_heads - 1) * q_head_stride + head_dim;
+    const size_t cn = (size_t)cache_capacity * n_kv_heads * head_dim;
+    const size_t on = (size_t)n_heads * head_dim;
+    const size_t ws = anelm_gqa_workspace_size(1, n_heads, n_kv_heads, head_dim, cache_capacity);
+    const size_t sz[5] = {qn * 4, cn * 4, cn * 4, on * 4, ws};
+    char* d[5];
+    S.get(sz, d);
+    S.h2d(d[0], q, sz[0]);
+    S.h2d(d[1], k_cache, sz[1]);
+    S.h2d(d[2], v_cache, sz[2]);
+    check_rc(anelm_gqa_attention_ring(reinterpret_cast<float*>(d[3]), reinterpret_cast<const float*>(d[0]),
+                                      reinterpret_cast<const float*>(d[1]), reinterpret_cast<const float*>(d[2]),
+                                      n_heads, n_kv_heads, head_dim, q_head_stride, cache_start, cache_len,
+                                      cache_capacity, ws ? d[4] : nullptr, ws, S.s()),
+             "gqa_attention");
+    S.d2h(out, d[3], sz[3]);
+    S.sync();
+}
+
 // core/sampling.cpp:10-66
 int sample_token(const float* logits, int vocab_size, const SamplingParams& params,
                  const std::vector<int>& recent_tokens) {

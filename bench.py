@@ -47,17 +47,15 @@ OP_KERNELS = {"rmsnorm": ("rmsnorm_row_kernel", "false>"), "qknorm_rope": ("qkno
               "add_rmsnorm": ("rmsnorm_row_kernel", "true>"), "silu_mul": ("silu_mul_vec_kernel", ""),
               "residual_add": ("residual_add_vec_kernel", "")}
 PROFILES = os.path.join(ROOT, "profiles")
-# The counter runs behind profiles/pmc_traffic_<workload>.txt (run from the repo root).
-PMC_COMMANDS = [
-    "rocprofv3 --pmc FETCH_SIZE --output-format csv -d gpurun_out/prof_fetch -o bench -- "
-    "python bench.py --headline-only --no-cpu --steps 1 --warmup 0",
-    "rocprofv3 --pmc WRITE_SIZE --output-format csv -d gpurun_out/prof_write -o bench -- "
-    "python bench.py --headline-only --no-cpu --steps 1 --warmup 0",
-    "rocprofv3 --pmc FETCH_SIZE --output-format csv -d gpurun_out/prof_copy_fetch -o copy -- "
-    "python bench.py --calibrate-copy",
-    "rocprofv3 --pmc WRITE_SIZE --output-format csv -d gpurun_out/prof_copy_write -o copy -- "
-    "python bench.py --calibrate-copy",
-]
+# The counter runs behind profiles/pmc_traffic_<workload>.txt (run from the repo root):
+# one counter per run over `bench.py <args>`, and the same counter over a plain
+# 1 GiB device copy for the calibration.
+def pmc_commands(fetch_dir, write_dir, copy_fetch_dir, copy_write_dir, args):
+    run = lambda c, d, a: f"rocprofv3 --pmc {c} --output-format csv -d {d} -o r -- python bench.py {a}"
+    return [run("FETCH_SIZE", fetch_dir, args), run("WRITE_SIZE", write_dir, args),
+            run("FETCH_SIZE", copy_fetch_dir, "--calibrate-copy"), run("WRITE_SIZE", copy_write_dir, "--calibrate-copy")]
+
+
 COPY_BYTES = 1 << 30  # read and written by --calibrate-copy
 
 
@@ -252,6 +250,70 @@ def measure_convert(hip, reps=3):
     return dict(params=n, bytes=byt, contiguous_set=f(ms_one), per_tensor=dict(f(ms_per), launches=len(sizes)))
 
 
+ATTN_WORKLOADS = {
+    # Qwen3-8B attention shapes over the reference's 2048-row KV ring
+    # (models/llm/qwen3.h:56), every ring full and wrapped at a random start
+    "attention-qwen3-8b-decode-b64": dict(B=64, nq=32, nk=8, D=128, cap=2048),
+    "attention-qwen3-8b-decode-b1": dict(B=1, nq=32, nk=8, D=128, cap=2048),
+}
+
+
+def attn_bytes(w):
+    """K and V rows of every live position read once, q read and out written once."""
+    return w["B"] * (w["cap"] * w["nk"] * w["D"] * 4 * 2 + 2 * w["nq"] * w["D"] * 4)
+
+
+def measure_attention(hip, w, steps, layers=8):
+    """One decode step's attention over `layers` distinct layers' KV rings
+    (so the caches come from HBM), graph-replayed."""
+    import torch
+
+    B, nq, nk, D, cap = w["B"], w["nq"], w["nk"], w["D"], w["cap"]
+    g = torch.Generator(device="cuda").manual_seed(31)
+    rn = lambda *s: torch.randn(*s, generator=g, device="cuda")
+    lay = [dict(k=rn(B, cap, nk * D), v=rn(B, cap, nk * D), q=rn(B, nq * D)) for _ in range(layers)]
+    start = torch.randint(0, cap, (B,), generator=g, device="cuda", dtype=torch.int32)
+    length = torch.full((B,), cap, device="cuda", dtype=torch.int32)
+    out = torch.empty(B, nq * D, device="cuda")
+    ws = torch.empty(max(hip.gqa_workspace_size(B, nq, nk, D, cap), 1), dtype=torch.uint8, device="cuda")
+    call = lambda: [hip.gqa_attention(out, L["q"], L["k"], L["v"], start, length, nq, nk, D, ws) for L in lay]
+    gr = capture(call)
+    gr.replay()
+    ms = time_region(gr.replay, steps) / layers
+    byt = attn_bytes(w)
+    del lay, gr
+    torch.cuda.empty_cache()
+    return dict(us=round(ms * 1e3, 2), GBps=round(byt / ms / 1e6, 1), frac=round(byt / ms / 1e6 / HBM_PEAK_GBPS, 4),
+                bytes=byt, tokens_per_s=round(B / (ms / 1e3), 1),
+                note="per layer; algorithmic bytes = full K and V rings read once + q and out")
+
+
+def cpu_attention(w, target_s):
+    """The oracle's gqa_attention (heads in parallel, as the reference runs
+    them) for one sequence, repeated for about target_s seconds."""
+    import numpy as np
+
+    oracle = _oracle()
+    nq, nk, D, cap = w["nq"], w["nk"], w["D"], w["cap"]
+    rng = np.random.default_rng(4)
+    kc = rng.standard_normal((cap, nk * D), dtype=np.float32)
+    vc = rng.standard_normal((cap, nk * D), dtype=np.float32)
+    q = rng.standard_normal(nq * D, dtype=np.float32)
+    t0 = time.perf_counter()
+    done = 0
+    while True:
+        oracle.gqa_attention(q, kc, vc, nq, nk, D, 17, cap)
+        done += 1
+        el = time.perf_counter() - t0
+        if el >= target_s:
+            break
+    per_seq = el / done
+    byt = attn_bytes(dict(w, B=1))
+    return dict(us_per_sequence=round(per_seq * 1e6, 1), GBps=round(byt / per_seq / 1e9, 2),
+                cores=oracle.max_threads(), kind="port",
+                sample=f"{done} single-sequence calls (capacity {cap}, full ring) on {oracle.max_threads()} threads")
+
+
 # ------------------------------------------------------------------ CPU baseline
 
 def _oracle():
@@ -352,8 +414,15 @@ def _csv_rows(d, suffix):
     return rows
 
 
-def _match(name, op):
-    frag, tmpl = OP_KERNELS[op]
+ATTN_KERNELS = {"gqa_decode": ("gqa_decode_kernel", ""), "gqa_combine": ("gqa_combine_kernel", "")}
+
+
+def _kernels_of(workload):
+    return ATTN_KERNELS if workload in ATTN_WORKLOADS else OP_KERNELS
+
+
+def _match(name, op, kernels=None):
+    frag, tmpl = (kernels or OP_KERNELS)[op]
     return frag in name and tmpl in name
 
 
@@ -368,7 +437,7 @@ def _counter_means(d):
 
 
 def pmc_summary(fetch_dir, write_dir, copy_fetch_dir, copy_write_dir, workload=HEADLINE):
-    """Text summary of the four counter runs of PMC_COMMANDS: HBM bytes per
+    """Text summary of the four counter runs of pmc_commands(): HBM bytes per
     dispatch of each op's kernel, with FETCH_SIZE / WRITE_SIZE (KiB) scaled
     by what they read for a plain 1 GiB device copy."""
     fe, wr = _counter_means(fetch_dir), _counter_means(write_dir)
@@ -376,27 +445,36 @@ def pmc_summary(fetch_dir, write_dir, copy_fetch_dir, copy_write_dir, workload=H
     copy_f = max(v for (k, c), (n, v) in cf.items() if "copyBuffer" in k and c == "FETCH_SIZE")
     copy_w = max(v for (k, c), (n, v) in cw.items() if "copyBuffer" in k and c == "WRITE_SIZE")
     ff, wf = COPY_BYTES / 1024 / copy_f, COPY_BYTES / 1024 / copy_w
-    ob = op_bytes(WORKLOADS[workload])
+    kernels = _kernels_of(workload)
+    if workload in ATTN_WORKLOADS:
+        w = ATTN_WORKLOADS[workload]
+        ob = {"gqa_decode": attn_bytes(w), "gqa_combine": 0}
+        run_args = f"--only {workload} --steps 1"
+    else:
+        ob = op_bytes(WORKLOADS[workload])
+        run_args = f"--workload {workload} --headline-only --no-cpu --steps 1 --warmup 0"
+    commands = pmc_commands(fetch_dir, write_dir, copy_fetch_dir, copy_write_dir, run_args)
     lines = [f"# HBM traffic per dispatch, workload {workload} (rocprofv3 --pmc, one counter per run)", "#",
-             "# commands (from the repo root):"] + [f"#   {c}" for c in PMC_COMMANDS] + [
-             "#   python bench.py --pmc-summary gpurun_out/prof_fetch gpurun_out/prof_write "
-             "gpurun_out/prof_copy_fetch gpurun_out/prof_copy_write", "#",
+             "# commands (from the repo root):"] + [f"#   {c}" for c in commands] + [
+             f"#   python bench.py --workload {workload} --pmc-summary {fetch_dir} {write_dir} {copy_fetch_dir} "
+             f"{copy_write_dir}", "#",
              f"# calibration, 1 GiB device copy: FETCH_SIZE {copy_f:.0f} KiB -> factor {ff:.4f}; "
              f"WRITE_SIZE {copy_w:.0f} KiB -> factor {wf:.4f}", "",
              "| op | kernel | dispatches | FETCH_SIZE KiB | WRITE_SIZE KiB | traffic bytes | algorithmic bytes | ratio |",
              "|---|---|---|---|---|---|---|---|"]
     traffic = {}
-    for op in OPS:
-        fk = [(k, v) for k, v in fe.items() if k[1] == "FETCH_SIZE" and _match(k[0], op)]
-        wk = [(k, v) for k, v in wr.items() if k[1] == "WRITE_SIZE" and _match(k[0], op)]
+    for op in kernels:
+        fk = [(k, v) for k, v in fe.items() if k[1] == "FETCH_SIZE" and _match(k[0], op, kernels)]
+        wk = [(k, v) for k, v in wr.items() if k[1] == "WRITE_SIZE" and _match(k[0], op, kernels)]
         if not fk or not wk:
             continue
         (kname, _), (n, f) = fk[0]
         _, (_, w_) = wk[0]
         t = round((f * ff + w_ * wf) * 1024)
         traffic[op] = t
-        short = kname.split("(")[0].replace("void ", "")
-        lines.append(f"| {op} | `{short}` | {n} | {f:.0f} | {w_:.0f} | {t} | {ob[op]} | {t / ob[op]:.4f} |")
+        short = kname.replace("(anonymous namespace)::", "").split("(")[0].replace("void ", "")
+        ratio = f"{t / ob[op]:.4f}" if ob[op] else "-"
+        lines.append(f"| {op} | `{short}` | {n} | {f:.0f} | {w_:.0f} | {t} | {ob[op]} | {ratio} |")
     lines += ["", "traffic_json: " + json.dumps(dict(workload=workload, fetch_factor=round(ff, 6),
                                                       write_factor=round(wf, 6), bytes_per_dispatch=traffic))]
     return "\n".join(lines)
@@ -408,7 +486,7 @@ def trace_summary(d, command, top=10):
     share kernel names, their grids tell them apart)."""
     rows = _csv_rows(d, "kernel_stats.csv")
     rows.sort(key=lambda r: -float(r["TotalDurationNs"]))
-    short = lambda n: n.split("(")[0].replace("void ", "")
+    short = lambda n: n.replace("(anonymous namespace)::", "").split("(")[0].replace("void ", "")
     lines = ["# rocprofv3 --kernel-trace --stats", "#", f"# command (from the repo root): {command}", "",
              "## busiest kernels (kernel_stats.csv)", "",
              "| kernel | calls | avg us | min us | max us | share % |", "|---|---|---|---|---|---|"]
@@ -449,12 +527,14 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default=HEADLINE, choices=sorted(WORKLOADS))
+    ap.add_argument("--workload", default=HEADLINE, choices=sorted(WORKLOADS) + sorted(ATTN_WORKLOADS),
+                    help="op-chain workload to run (attention names only select --pmc-summary kernels)")
     ap.add_argument("--cpu-seconds", type=float, default=8.0, help="CPU time budget of the headline baseline")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--headline-only", action="store_true", help="skip the other configurations")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only time a 1 GiB device-to-device copy (reference for rocprof byte counters)")
+    ap.add_argument("--only", default=None, help="measure only this named configuration and print it")
     ap.add_argument("--pmc-summary", nargs=4, metavar=("FETCH", "WRITE", "COPY_FETCH", "COPY_WRITE"),
                     help="print the traffic summary of four rocprofv3 --pmc output directories and exit")
     ap.add_argument("--trace-summary", nargs=2, metavar=("DIR", "COMMAND"),
@@ -484,6 +564,19 @@ def main():
         return
 
     anelm.lib()
+    if args.only:
+        if args.only in ATTN_WORKLOADS:
+            r = measure_attention(anelm, ATTN_WORKLOADS[args.only], max(args.steps, 20))
+        elif args.only == "sampling-64x151936":
+            r = measure_sampler(anelm, max(args.steps, 20))
+        elif args.only == "convert-qwen3-8b-bf16":
+            r = measure_convert(anelm)
+        else:
+            r = measure_chain(WORKLOADS[args.only], args.steps, args.warmup, per_op=True)
+        print(json.dumps({args.only: r}))
+        return
+    if args.workload not in WORKLOADS:
+        raise SystemExit(f"--workload {args.workload}: an op-chain workload is needed here ({', '.join(WORKLOADS)})")
     w = WORKLOADS[args.workload]
     head = measure_chain(w, args.steps, args.warmup, per_op=True)
     ob = op_bytes(w)
@@ -499,6 +592,8 @@ def main():
             if name != args.workload:
                 configs[name] = measure_chain(wl, max(args.steps, 20), args.warmup, per_op=False)
         configs["sampling-64x151936"] = measure_sampler(anelm, max(args.steps, 20))
+        for name, aw in ATTN_WORKLOADS.items():
+            configs[name] = measure_attention(anelm, aw, max(args.steps, 20))
         configs["convert-qwen3-8b-bf16"] = measure_convert(anelm)
     cpu = None
     cpu_configs = {}
@@ -509,6 +604,7 @@ def main():
                 if name != args.workload:
                     cpu_configs[name] = cpu_chain(wl, 1.5, max_tokens=256, layers=2)
             cpu_configs["sampling-64x151936"] = cpu_sampler(1.5)
+            cpu_configs["attention-qwen3-8b-decode"] = cpu_attention(ATTN_WORKLOADS["attention-qwen3-8b-decode-b1"], 1.5)
             cpu_configs["convert-qwen3-8b-bf16"] = cpu_convert(1.5)
     out = {
         "metric": METRIC,

@@ -182,6 +182,53 @@ int anelm_sample(int32_t* ids, float* probs, long ld_probs, const float* logits,
                  const int32_t* hist_len, const anelm_sampling_params* params, const float* r,
                  void* workspace, size_t workspace_bytes, void* stream);
 
+/* ------------------------------------------------ KV ring and attention */
+
+/* Per-sequence KV rings: for sequence b, k_cache/v_cache + b*cache_seq_stride
+ * each hold [capacity, n_kv_heads, head_dim] fp32 (the layout of the
+ * reference's KVCache, models/llm/qwen3.cpp:227-231); ring_start[b] /
+ * ring_len[b] (device int32) name the live rows start, start+1, ...
+ * (mod capacity), len of them.  Out-of-range state is clamped on the device
+ * (0 <= len <= capacity, start taken mod capacity) so no access leaves the
+ * caches. */
+
+/* Appends row b of k and v (n_kv_heads*head_dim floats at k + b*k_ld,
+ * v + b*v_ld) to ring b and advances its state, as models/llm/qwen3.cpp:475-488:
+ * while len < capacity the row goes to slot start+len (mod capacity) and len
+ * grows; afterwards it overwrites slot start and start advances. */
+int anelm_kv_ring_append(float* k_cache, float* v_cache, int32_t* ring_start, int32_t* ring_len,
+                         const float* k, const float* v, long k_ld, long v_ld, long batch,
+                         int n_kv_heads, int head_dim, int capacity, long cache_seq_stride,
+                         void* stream);
+
+/* GQA decode attention (ane_lm::gqa_attention, core/cpu_ops.cpp:173-240,
+ * core/cpu_ops.h:53-56) for `batch` sequences at once: q head h of sequence b
+ * at q + b*q_ld + h*q_head_stride attends over ring b with kv head
+ * h / (n_heads/n_kv_heads):
+ *   score_t = dot(q_h, k_t) * (1/sqrtf(head_dim)), p = softmax(score),
+ *   out[b*out_ld + h*head_dim + d] = sum_t p_t v_t[d];
+ * an empty ring gives zeros (cpu_ops.cpp:177-180).  head_dim 64, 128 or 256;
+ * n_heads a multiple of n_kv_heads; q and the caches 16-byte aligned with
+ * strides that are multiples of 4.  Needs
+ * anelm_gqa_workspace_size(batch, n_heads, n_kv_heads, head_dim, capacity)
+ * bytes of device workspace (0 is possible: then workspace may be NULL). */
+size_t anelm_gqa_workspace_size(long batch, int n_heads, int n_kv_heads, int head_dim, int capacity);
+int anelm_gqa_attention(float* out, const float* q, const float* k_cache, const float* v_cache,
+                        const int32_t* ring_start, const int32_t* ring_len, long batch, int n_heads,
+                        int n_kv_heads, int head_dim, long q_ld, int q_head_stride, long out_ld,
+                        int capacity, long cache_seq_stride, void* workspace, size_t workspace_bytes,
+                        void* stream);
+/* The reference's own single-sequence form, with the ring state as host
+ * integers (its exact argument list, core/cpu_ops.h:53-56); caches
+ * [cache_capacity, n_kv_heads, head_dim]; out [n_heads, head_dim].
+ * cache_len <= 0 gives zeros; cache_len > cache_capacity or a start outside
+ * [0, capacity) is ANELM_ERR_RANGE.  Workspace as anelm_gqa_attention with
+ * batch 1. */
+int anelm_gqa_attention_ring(float* out, const float* q, const float* k_cache, const float* v_cache,
+                             int n_heads, int n_kv_heads, int head_dim, int q_head_stride,
+                             int cache_start, int cache_len, int cache_capacity, void* workspace,
+                             size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

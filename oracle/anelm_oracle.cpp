@@ -356,6 +356,68 @@ extern "C" void orc_softmax(float* x, int n) {
     for (int i = 0; i < n; i++) x[i] = x[i] * inv;                 // vDSP_vsmul :98
 }
 
+// ------------------------------------------------------- KV ring, attention
+
+// models/llm/qwen3.cpp:475-488
+extern "C" int orc_kv_ring_append(float* k_cache, float* v_cache, const float* k, const float* v,
+                                  int kv_stride, int* start, int* len, int capacity) {
+    int slot;
+    if (*len < capacity) {                       // :476-479
+        slot = *start + *len;
+        if (slot >= capacity) slot -= capacity;
+        (*len)++;
+    } else {                                     // :480-484
+        slot = *start;
+        (*start)++;
+        if (*start >= capacity) *start = 0;
+    }
+    std::memcpy(k_cache + (size_t)slot * kv_stride, k, (size_t)kv_stride * sizeof(float));  // :487
+    std::memcpy(v_cache + (size_t)slot * kv_stride, v, (size_t)kv_stride * sizeof(float));  // :488
+    return slot;
+}
+
+// core/cpu_ops.cpp:173-240
+extern "C" void orc_gqa_attention(float* out, const float* q, const float* k_cache, const float* v_cache,
+                                  int n_heads, int n_kv_heads, int head_dim, int q_head_stride,
+                                  int cache_start, int cache_len, int cache_capacity) {
+    if (cache_len <= 0) {                                           // :177-180
+        std::memset(out, 0, (size_t)n_heads * head_dim * sizeof(float));
+        return;
+    }
+    const int groups = n_heads / n_kv_heads;                        // :182
+    const float scale = 1.0f / sqrtf((float)head_dim);              // :183
+    const size_t kv_step = (size_t)n_kv_heads * head_dim;           // :184
+    int first_span = cache_capacity - cache_start;                  // :186-188
+    if (first_span > cache_len) first_span = cache_len;
+    // heads are independent; the reference runs them in parallel for
+    // cache_len >= 128 and n_heads >= 4 (:229-236)
+#pragma omp parallel for schedule(static) if (cache_len >= 128 && n_heads >= 4)
+    for (int h = 0; h < n_heads; h++) {
+        std::vector<float> scores(cache_len);
+        const int kv_h = h / groups;
+        const float* qh = q + (size_t)h * q_head_stride;
+        float* oh = out + (size_t)h * head_dim;
+        const size_t off = (size_t)kv_h * head_dim;
+        auto row = [&](int t) {                                     // ring order :199-209
+            const size_t slot = t < first_span ? (size_t)(cache_start + t) : (size_t)(t - first_span);
+            return slot * kv_step + off;
+        };
+        for (int t = 0; t < cache_len; t++) {
+            const float* kh = k_cache + row(t);
+            double dot = 0.0;
+            for (int d = 0; d < head_dim; d++) dot += (double)qh[d] * (double)kh[d];
+            scores[t] = (float)dot * scale;
+        }
+        orc_softmax(scores.data(), cache_len);                      // :211
+        for (int d = 0; d < head_dim; d++) oh[d] = 0.0f;            // :213
+        for (int t = 0; t < cache_len; t++) {                       // cblas_saxpy :214-223
+            const float* vh = v_cache + row(t);
+            const float p = scores[t];
+            for (int d = 0; d < head_dim; d++) oh[d] = oh[d] + p * vh[d];
+        }
+    }
+}
+
 // ---------------------------------------------------------------- sampling
 // core/sampling.cpp:58-65 (after r is drawn): sequential fp32 cumulative sum.
 extern "C" int orc_cdf_walk(const float* p, int V, float r) {

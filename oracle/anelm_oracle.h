@@ -120,6 +120,30 @@ int orc_sample_token(const float* logits, int V, float temperature, float rep_pe
 /* the CDF walk alone (sampling.cpp:58-65) on given probabilities */
 int orc_cdf_walk(const float* p, int V, float r);
 
+/* ---- KV ring and GQA decode attention ---- */
+/* Append one token's k, v rows (kv_stride = n_kv_heads*head_dim floats each)
+ * to a ring of `capacity` rows, models/llm/qwen3.cpp:475-488: while
+ * len < capacity the slot is start+len (mod capacity) and len grows;
+ * afterwards the oldest row (slot start) is overwritten and start advances.
+ * Returns the slot written.  pinned: a Python list model of the ring over
+ * more appends than the capacity (tests/test_oracle_attention.py). */
+int orc_kv_ring_append(float* k_cache, float* v_cache, const float* k, const float* v, int kv_stride,
+                       int* start, int* len, int capacity);
+/* core/cpu_ops.cpp:173-240 for one token: k_cache / v_cache [capacity,
+ * n_kv_heads, head_dim]; the cache_len positions in ring order start,
+ * start+1, ... (mod capacity); q head h at q + h*q_head_stride uses kv head
+ * h / (n_heads / n_kv_heads); out [n_heads, head_dim].
+ *   score_t = fl(dot(q_h, k_t)) * fl(1/sqrtf(head_dim))     :182, :196-209
+ *   p = softmax(score)  (orc_softmax, as :211 calls softmax)
+ *   out_h = sum_t p_t * v_t, accumulated in ring order     :213-223
+ * vDSP_dotpr's summation order is unspecified; the oracle uses the
+ * correctly rounded dot (double accumulation).  cache_len <= 0 -> out = 0
+ * (:177-180).  pinned: len 1 -> out = v exactly, uniform keys, fp64 brute
+ * force with an independent ring enumeration, ring-rotation identity. */
+void orc_gqa_attention(float* out, const float* q, const float* k_cache, const float* v_cache,
+                       int n_heads, int n_kv_heads, int head_dim, int q_head_stride, int cache_start,
+                       int cache_len, int cache_capacity);
+
 /* ---- one layer of the fused op chain over T tokens, per token as the
  * reference's forward() runs it (qwen3.cpp:502-528):
  *   (1) xn = rmsnorm(x, w_in)                       :503

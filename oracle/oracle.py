@@ -45,6 +45,8 @@ _SIGS = {
     "orc_layer_chain": (None, [_L, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                                _P, _P, _I, _F, _F, _I]),
     "orc_max_threads": (_I, []),
+    "orc_kv_ring_append": (_I, [_P, _P, _P, _P, _I, _P, _P, _I]),
+    "orc_gqa_attention": (None, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I]),
 }
 
 _lib = None
@@ -242,6 +244,30 @@ def layer_chain(T, H, nq, nk, D, I, x, xn, attn_out, mlp_out, q, k, g, u, h, w_i
     lib().orc_layer_chain(T, H, nq, nk, D, I, _p(x), _p(xn), _p(attn_out), _p(mlp_out), _p(q), _p(k), _p(g), _p(u),
                           _p(h), _p(w_in), _p(w_post), _p(wq), _p(wk), _p(pos), _p(cos_tab), _p(sin_tab),
                           cos_tab.shape[0], theta, eps, nthreads)
+
+
+def kv_ring_append(k_cache, v_cache, k, v, state):
+    """Append rows k, v ([n_kv_heads*head_dim] each) to the ring caches
+    [capacity, kv_stride] in place; state = [start, len] (np.int32, updated).
+    Returns the slot written."""
+    cap, stride = k_cache.shape
+    assert state.dtype == np.int32 and state.size == 2 and state.flags.c_contiguous
+    assert k_cache.flags.c_contiguous and v_cache.flags.c_contiguous and k_cache.dtype == np.float32
+    return lib().orc_kv_ring_append(_p(k_cache), _p(v_cache), _p(_c(k, np.float32)), _p(_c(v, np.float32)), stride,
+                                    ctypes.c_void_p(state.ctypes.data), ctypes.c_void_p(state.ctypes.data + 4), cap)
+
+
+def gqa_attention(q, k_cache, v_cache, n_heads, n_kv_heads, head_dim, cache_start, cache_len, q_head_stride=None):
+    """q: flat [>= (n_heads-1)*q_head_stride + head_dim]; caches [capacity,
+    n_kv_heads*head_dim] (or any shape of that size).  Returns [n_heads, head_dim]."""
+    q = _c(q, np.float32).ravel()
+    kc, vc = _c(k_cache, np.float32), _c(v_cache, np.float32)
+    cap = kc.size // (n_kv_heads * head_dim)
+    qs = head_dim if q_head_stride is None else q_head_stride
+    out = np.empty((n_heads, head_dim), np.float32)
+    lib().orc_gqa_attention(_p(out), _p(q), _p(kc), _p(vc), n_heads, n_kv_heads, head_dim, qs, cache_start,
+                            cache_len, cap)
+    return out
 
 
 def max_threads() -> int:

@@ -188,6 +188,29 @@ int main() {
         report(max_rel(h.data(), hr.data(), 3072) <= 1e-5, "silu_mul", max_rel(h.data(), hr.data(), 3072));
     }
 
+    // KV ring + GQA attention as qwen3.cpp:475-492 calls them (host ring state)
+    {
+        const int nq = 16, nk = 8, hd = 128, cap = 64, row = nk * hd;
+        std::vector<float> kc((size_t)cap * row, 0.f), vc((size_t)cap * row, 0.f);
+        int start = 0, len = 0;
+        double worst = 0;
+        for (int step = 0; step < 70; step++) {                   // past the capacity: wraps
+            auto k = randv(row), v = randv(row), q = randv((size_t)nq * hd);
+            orc_kv_ring_append(kc.data(), vc.data(), k.data(), v.data(), row, &start, &len, cap);
+            if (step % 10 != 9) continue;
+            std::vector<float> out((size_t)nq * hd), ref((size_t)nq * hd);
+            ane_lm::gqa_attention(out.data(), q.data(), kc.data(), vc.data(), nq, nk, hd, hd, start, len, cap);
+            orc_gqa_attention(ref.data(), q.data(), kc.data(), vc.data(), nq, nk, hd, hd, start, len, cap);
+            for (size_t i = 0; i < out.size(); i++) worst = std::fmax(worst, std::fabs((double)out[i] - ref[i]));
+        }
+        report(worst <= 1e-5, "gqa_attention over a wrapped ring", worst);
+        std::vector<float> out((size_t)nq * hd, 1.f);
+        ane_lm::gqa_attention(out.data(), kc.data(), kc.data(), vc.data(), nq, nk, hd, hd, 0, 0, cap);
+        bool zero = true;
+        for (float x : out) zero = zero && x == 0.f;
+        report(zero, "gqa_attention empty cache", 0);
+    }
+
     printf("%s: %d failure(s)\n", g_fail ? "FAILED" : "OK", g_fail);
     return g_fail ? 1 : 0;
 }

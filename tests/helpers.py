@@ -24,6 +24,31 @@ def assert_bitexact(got, ref, what=""):
     assert bad.size == 0, f"{what}: {bad.size} mismatches, first at {bad[:5]}: {g.ravel()[bad[:5]]} vs {r.ravel()[bad[:5]]}"
 
 
+def attention_fp64(q, kc, vc, nq, nk, D, start, length, qs=None):
+    """float64 GQA attention over ring positions (start + t) mod capacity.
+    q flat (head h at h*qs); caches [capacity, nk*D].  Returns (out, bound):
+    out [nq, D] and bound = sum_t p_t |v_t|, the scale of the terms summed,
+    which the attention tolerances are relative to."""
+    qs = D if qs is None else qs
+    cap = kc.shape[0]
+    if length <= 0:
+        return np.zeros((nq, D)), np.zeros((nq, D))
+    slots = (start + np.arange(length)) % cap
+    K = kc.reshape(cap, nk, D)[slots].astype(np.float64)
+    V = vc.reshape(cap, nk, D)[slots].astype(np.float64)
+    out = np.zeros((nq, D))
+    bound = np.zeros((nq, D))
+    for h in range(nq):
+        kv = h // (nq // nk)
+        qh = q[h * qs:h * qs + D].astype(np.float64)
+        s = (K[:, kv, :] @ qh) / np.sqrt(D)
+        p = np.exp(s - s.max())
+        p /= p.sum()
+        out[h] = p @ V[:, kv, :]
+        bound[h] = p @ np.abs(V[:, kv, :])
+    return out, bound
+
+
 # ---------------------------------------------------------------- GPU plumbing
 
 def dev(a):

@@ -58,7 +58,8 @@ def test_dropin_cpp_symbols_exported():
                 "ane_lm::apply_rope_cached(float*, float*, int, int, int, int, int, int, int, float, float const*, float const*)",
                 "ane_lm::sample_token(float const*, int, ane_lm::SamplingParams const&, std::vector<int, std::allocator<int> > const&)",
                 "ane_lm::hip::bf16_to_f16_vec(unsigned short*, unsigned short const*, int)",
-                "ane_lm::hip::residual_add(float*, float const*, int)"]:
+                "ane_lm::hip::residual_add(float*, float const*, int)",
+                "ane_lm::gqa_attention(float*, float const*, float const*, float const*, int, int, int, int, int, int, int)"]:
         assert sig in out, sig
 
 
@@ -118,3 +119,37 @@ def test_error_string_is_per_thread(lib):
     t.join()
     assert seen["msg"] == b""
     assert b"null" in lib.anelm_last_error()
+
+
+def test_attention_argument_checks(lib):
+    """Validation of the KV-ring / attention entry points (no launch happens)."""
+    P = ctypes.c_void_p
+    fake = P(0x1000)
+    ws = lib.anelm_gqa_workspace_size
+    # one (sequence, kv head) pair per 32 positions at most -> the chunk is 512
+    # once there are >= 2048 workgroups, else it shrinks towards 32
+    assert ws(64, 32, 8, 128, 2048) == 64 * 32 * 4 * 130 * 4
+    assert ws(1, 32, 8, 128, 2048) == 32 * 64 * 130 * 4
+    assert ws(512, 16, 8, 128, 512) == 0                        # one chunk: no partials
+    assert ws(0, 32, 8, 128, 2048) == 0
+    g = lib.anelm_gqa_attention
+    ok = dict(q_ld=32 * 128, qs=128, out_ld=32 * 128, cap=2048, seq=2048 * 8 * 128)
+
+    def call(nh=32, nkv=8, d=128, ring=fake, batch=2, ws_bytes=1 << 30, **kw):
+        a = dict(ok, **kw)
+        return g(fake, fake, fake, fake, ring, ring, batch, nh, nkv, d, a["q_ld"], a["qs"], a["out_ld"], a["cap"],
+                 a["seq"], fake, ws_bytes, None)
+
+    assert call(d=96) == -1 and b"head_dim" in lib.anelm_last_error()
+    assert call(nh=30) == -1                                    # not a multiple of n_kv_heads
+    assert call(ring=None) == -1
+    assert call(seq=100) == -1                                  # sequences' caches overlap
+    assert call(qs=130) == -1                                   # stride not a multiple of 4
+    assert call(ws_bytes=16) == -4                              # workspace too small
+    r = lib.anelm_gqa_attention_ring
+    assert r(fake, fake, fake, fake, 32, 8, 128, 128, 0, 2049, 2048, fake, 1 << 30, None) == -2  # len > capacity
+    assert r(fake, fake, fake, fake, 32, 8, 128, 128, 2048, 5, 2048, fake, 1 << 30, None) == -2  # start outside
+    assert r(fake, fake, fake, fake, 32, 8, 128, 128, -1, 5, 2048, fake, 1 << 30, None) == -2
+    a = lib.anelm_kv_ring_append
+    assert a(fake, fake, None, fake, fake, fake, 1024, 1024, 4, 8, 128, 2048, 2048 * 1024, None) == -1
+    assert a(fake, fake, fake, fake, fake, fake, 1000, 1024, 4, 8, 128, 2048, 2048 * 1024, None) == -1  # k_ld < row

@@ -1,0 +1,162 @@
+"""GQA decode attention over KV rings (core/cpu_ops.cpp:173-240) and the ring
+append (models/llm/qwen3.cpp:475-488) on the GPU, against the oracle on the
+same inputs.  Attention outputs must be within 1e-5 relative to
+sum_t p_t |v_t[d]| (the magnitude of the terms the output sums; the output
+itself can cancel to ~0); the ring append is bit-exact."""
+import numpy as np
+import pytest
+
+from helpers import assert_bitexact, attention_fp64, dev, host
+
+pytestmark = pytest.mark.gpu
+ATTN_TOL = 1e-5
+
+
+def ring_call(hip, q, kc, vc, nq, nk, D, start, length, qs=None):
+    import torch
+
+    out = torch.full((nq, D), float("nan"), device="cuda")
+    n = hip.gqa_workspace_size(1, nq, nk, D, kc.shape[0])
+    ws = torch.empty(max(n, 1), dtype=torch.uint8, device="cuda")
+    hip.gqa_attention_ring(out, dev(q), dev(kc), dev(vc), nq, nk, D, start, length, ws, q_head_stride=qs)
+    return host(out)
+
+
+def check(got, q, kc, vc, nq, nk, D, start, length, orc, qs=None):
+    ref = orc.gqa_attention(q, kc, vc, nq, nk, D, start, length, q_head_stride=qs)
+    _, bound = attention_fp64(q, kc, vc, nq, nk, D, start, length, qs)
+    err = np.abs(got.astype(np.float64) - ref) / np.maximum(bound, 1e-30)
+    assert float(err.max()) <= ATTN_TOL, float(err.max())
+
+
+@pytest.mark.parametrize("nq,nk,D,cap,start,length,qs", [
+    (16, 8, 128, 2048, 0, 1, None),          # one position
+    (16, 8, 128, 2048, 2047, 2, None),       # wraps right away
+    (32, 8, 128, 2048, 1500, 2048, None),    # full ring, 8B shapes
+    (32, 8, 128, 2048, 3, 700, 256),         # q head stride 2*head_dim
+    (40, 8, 128, 512, 100, 500, None),       # groups of 5
+    (64, 8, 128, 256, 200, 256, None),       # groups of 8
+    (16, 2, 256, 300, 290, 299, None),       # head_dim 256, groups of 8 in two passes
+    (8, 8, 64, 100, 50, 77, None),           # head_dim 64, no sharing
+    (16, 1, 64, 4096, 4000, 4096, None),     # one kv head, long ring
+])
+def test_ring_form_matches_oracle(hip, orc, rng, nq, nk, D, cap, start, length, qs):
+    qsz = (nq - 1) * (qs or D) + D
+    q = rng.standard_normal(qsz).astype(np.float32)
+    kc = rng.standard_normal((cap, nk * D)).astype(np.float32)
+    vc = rng.standard_normal((cap, nk * D)).astype(np.float32)
+    got = ring_call(hip, q, kc, vc, nq, nk, D, start, length, qs)
+    check(got, q, kc, vc, nq, nk, D, start, length, orc, qs)
+
+
+def test_empty_and_single(hip, rng):
+    nq, nk, D, cap = 32, 8, 128, 64
+    q = rng.standard_normal(nq * D).astype(np.float32)
+    kc = rng.standard_normal((cap, nk * D)).astype(np.float32)
+    vc = rng.standard_normal((cap, nk * D)).astype(np.float32)
+    assert np.array_equal(ring_call(hip, q, kc, vc, nq, nk, D, 5, 0), np.zeros((nq, D), np.float32))
+    assert np.array_equal(ring_call(hip, q, kc, vc, nq, nk, D, 5, -4), np.zeros((nq, D), np.float32))
+    one = ring_call(hip, q, kc, vc, nq, nk, D, 9, 1)   # p = 1 exactly: out = v
+    for h in range(nq):
+        assert np.array_equal(one[h], vc[9].reshape(nk, D)[h // 4])
+
+
+def test_peaked_and_uniform_scores(hip, orc, rng):
+    """A dominant key (weights underflow to 0 elsewhere) and identical keys
+    (all weights equal), the two extremes of the softmax."""
+    nq, nk, D, cap = 8, 2, 128, 1024
+    kc = np.tile(rng.standard_normal(nk * D).astype(np.float32), (cap, 1))
+    vc = rng.standard_normal((cap, nk * D)).astype(np.float32)
+    q = rng.standard_normal(nq * D).astype(np.float32)
+    check(ring_call(hip, q, kc, vc, nq, nk, D, 77, 1000), q, kc, vc, nq, nk, D, 77, 1000, orc)
+    kc = (0.01 * rng.standard_normal((cap, nk * D))).astype(np.float32)
+    kc[500] = 8.0
+    q = np.ones(nq * D, np.float32)
+    got = ring_call(hip, q, kc, vc, nq, nk, D, 0, 1024)
+    for h in range(nq):
+        assert np.array_equal(got[h], vc[500].reshape(nk, D)[h // 4])
+
+
+def batched(hip, B, nq, nk, D, cap, starts, lens, rng, qs=None):
+    import torch
+
+    qs = qs or D
+    q = rng.standard_normal((B, (nq - 1) * qs + D)).astype(np.float32)
+    kc = rng.standard_normal((B, cap, nk * D)).astype(np.float32)
+    vc = rng.standard_normal((B, cap, nk * D)).astype(np.float32)
+    out = torch.full((B, nq * D), float("nan"), device="cuda")
+    ws = torch.empty(max(hip.gqa_workspace_size(B, nq, nk, D, cap), 1), dtype=torch.uint8, device="cuda")
+    hip.gqa_attention(out, dev(q), dev(kc), dev(vc), dev(np.array(starts, np.int32)), dev(np.array(lens, np.int32)),
+                      nq, nk, D, ws, q_head_stride=qs)
+    return host(out).reshape(B, nq, D), q, kc, vc
+
+
+def test_batched_decode_b64_full_shape(hip, orc, rng):
+    """64 sequences at the Qwen3-8B decode shape (32 q heads, 8 kv heads,
+    head_dim 128, capacity 2048) with different ring states."""
+    B, nq, nk, D, cap = 64, 32, 8, 128, 2048
+    starts = rng.integers(0, cap, B)
+    lens = rng.integers(1, cap + 1, B)
+    lens[:4] = [0, 1, cap, cap]
+    starts[3] = 0
+    got, q, kc, vc = batched(hip, B, nq, nk, D, cap, starts, lens, rng)
+    for b in range(B):
+        check(got[b], q[b], kc[b], vc[b], nq, nk, D, int(starts[b]), int(lens[b]), orc)
+
+
+@pytest.mark.parametrize("B,nq,nk,D,cap", [(3, 16, 8, 128, 4096), (600, 16, 8, 128, 64), (5, 8, 4, 64, 333)])
+def test_batched_other_shapes(hip, orc, rng, B, nq, nk, D, cap):
+    starts = rng.integers(0, cap, B)
+    lens = rng.integers(0, cap + 1, B)
+    got, q, kc, vc = batched(hip, B, nq, nk, D, cap, starts, lens, rng)
+    for b in range(min(B, 40)):
+        check(got[b], q[b], kc[b], vc[b], nq, nk, D, int(starts[b]), int(lens[b]), orc)
+
+
+def test_ring_append_matches_oracle(hip, orc, rng):
+    import torch
+
+    B, nk, D, cap = 6, 8, 128, 16
+    row = nk * D
+    kc = rng.standard_normal((B, cap, row)).astype(np.float32)
+    vc = rng.standard_normal((B, cap, row)).astype(np.float32)
+    st = np.array([[0, 0], [3, 5], [15, 2], [0, 16], [9, 16], [7, 15]], np.int32)
+    dk, dv = dev(kc), dev(vc)
+    ds, dl = dev(st[:, 0].copy()), dev(st[:, 1].copy())
+    for step in range(20):                                     # wraps every ring
+        k = rng.standard_normal((B, row)).astype(np.float32)
+        v = rng.standard_normal((B, row)).astype(np.float32)
+        hip.kv_ring_append(dk, dv, ds, dl, dev(k), dev(v))
+        for b in range(B):
+            orc.kv_ring_append(kc[b], vc[b], k[b], v[b], st[b])
+    assert np.array_equal(host(ds), st[:, 0]) and np.array_equal(host(dl), st[:, 1])
+    assert_bitexact(host(dk), kc, "k cache")
+    assert_bitexact(host(dv), vc, "v cache")
+
+
+def test_append_then_attend_decode_loop(hip, orc, rng):
+    """The decode loop of qwen3.cpp:475-492 for 2 sequences past the ring's
+    capacity: append the token's k/v, then attend over the ring."""
+    import torch
+
+    B, nq, nk, D, cap = 2, 16, 8, 128, 24
+    row = nk * D
+    dk = torch.zeros(B, cap, row, device="cuda")
+    dv = torch.zeros(B, cap, row, device="cuda")
+    ds = torch.zeros(B, dtype=torch.int32, device="cuda")
+    dl = torch.zeros(B, dtype=torch.int32, device="cuda")
+    kc = np.zeros((B, cap, row), np.float32)
+    vc = np.zeros((B, cap, row), np.float32)
+    st = np.zeros((B, 2), np.int32)
+    out = torch.empty(B, nq * D, device="cuda")
+    ws = torch.empty(max(hip.gqa_workspace_size(B, nq, nk, D, cap), 1), dtype=torch.uint8, device="cuda")
+    for step in range(30):
+        k = rng.standard_normal((B, row)).astype(np.float32)
+        v = rng.standard_normal((B, row)).astype(np.float32)
+        q = rng.standard_normal((B, nq * D)).astype(np.float32)
+        hip.kv_ring_append(dk, dv, ds, dl, dev(k), dev(v))
+        hip.gqa_attention(out, dev(q), dk, dv, ds, dl, nq, nk, D, ws)
+        got = host(out).reshape(B, nq, D)
+        for b in range(B):
+            orc.kv_ring_append(kc[b], vc[b], k[b], v[b], st[b])
+            check(got[b], q[b], kc[b], vc[b], nq, nk, D, int(st[b, 0]), int(st[b, 1]), orc)
