@@ -70,6 +70,11 @@ _SIGS = {
     "anelm_gqa_attention": (_I, [_P, _P, _P, _P, _P, _P, _L, _I, _I, _I, _L, _I, _L, _I, _L, _P, _S, _P]),
     "anelm_gqa_attention_ring": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _S, _P]),
     "anelm_kv_ring_append": (_I, [_P, _P, _P, _P, _P, _P, _L, _L, _L, _I, _I, _I, _L, _P]),
+    "anelm_rmsnorm_gated": (_I, [_P, _P, _P, _P, _I, _L, _I, _I, _L, _L, _L, _F, _P]),
+    "anelm_l2_normalize": (_I, [_P, _L, _I, _I, _L, _F, _P]),
+    "anelm_conv1d_update": (_I, [_P, _P, _P, _P, _P, _L, _I, _I, _L, _L, _L, _P]),
+    "anelm_ssm_step": (_I, [_P, _P, _P, _P, _P, _P, _P, _L, _I, _I, _I, _I, _L, _L, _L, _L, _P]),
+    "anelm_matvec": (_I, [_P, _P, _P, _L, _I, _P]),
 }
 
 EXPORTED = tuple(_SIGS)
@@ -284,3 +289,45 @@ def kv_ring_append(k_cache, v_cache, ring_start, ring_len, k, v, stream=None):
     _need(k.shape[1] == row and v.shape[1] == row and k_cache.stride() == v_cache.stride(), "kv_ring_append: shapes")
     _check(lib().anelm_kv_ring_append(_ptr(k_cache), _ptr(v_cache), _ptr(ring_start), _ptr(ring_len), _ptr(k),
                                       _ptr(v), _ld(k), _ld(v), B, 1, row, cap, k_cache.stride(0), _stream(stream)))
+
+
+def rmsnorm_gated(out, x, z, w, eps=1e-6, heads=1, stream=None):
+    """x, z, out: [rows, >= heads*dim] (row slices allowed); w: [dim]."""
+    rows, span, ldx = _rows(x)
+    _, _, ldz = _rows(z)
+    _, _, ldo = _rows(out)
+    dim = w.shape[0]
+    _need(span >= heads * dim, "rmsnorm_gated: row shorter than heads*dim")
+    _check(lib().anelm_rmsnorm_gated(_ptr(out), _ptr(x), _ptr(z), _ptr(w), _dtype_code(w), rows, heads, dim, ldx, ldz,
+                                     ldo, eps, _stream(stream)))
+
+
+def l2_normalize(x, scale=1.0, heads=1, stream=None):
+    """x: [rows, >= heads*dim] with dim = x.shape[1] // heads (row slices allowed)."""
+    rows, span, ld = _rows(x)
+    _check(lib().anelm_l2_normalize(_ptr(x), rows, heads, span // heads, ld, scale, _stream(stream)))
+
+
+def conv1d_update(y, conv_state, state_pos, x, w, stream=None):
+    """y, x: [B, channels]; conv_state: [B, channels, K-1]; state_pos: int32 [B]; w: [channels, K]."""
+    B, ch, sl = conv_state.shape
+    _need(w.shape == (ch, sl + 1) and w.is_contiguous() and conv_state.stride(2) == 1 and conv_state.stride(1) == sl,
+          "conv1d_update: shapes")
+    _check(lib().anelm_conv1d_update(_ptr(y), _ptr(conv_state), _ptr(state_pos), _ptr(x), _ptr(w), B, ch, sl + 1,
+                                     _ld(x), _ld(y), conv_state.stride(0), _stream(stream)))
+
+
+def ssm_step(y, state, q, k, v, decay, beta, n_key_heads, stream=None):
+    """state: [B, n_heads, key_dim, value_dim]; q, k: [B, n_key_heads*key_dim];
+    v, y: [B, n_heads*value_dim]; decay, beta: [B, n_heads]."""
+    B, nh, kd, vd = state.shape
+    _need(state.stride(3) == 1 and state.stride(2) == vd and state.stride(1) == kd * vd, "ssm_step: state layout")
+    _need(q.stride() == k.stride() and decay.is_contiguous() and beta.is_contiguous(), "ssm_step: layouts")
+    _check(lib().anelm_ssm_step(_ptr(y), _ptr(state), _ptr(q), _ptr(k), _ptr(v), _ptr(decay), _ptr(beta), B, nh,
+                                n_key_heads, kd, vd, _ld(q), _ld(v), _ld(y), state.stride(0), _stream(stream)))
+
+
+def matvec(y, W, x, stream=None):
+    out_dim, in_dim = W.shape
+    _need(W.is_contiguous() and x.is_contiguous() and y.numel() >= out_dim, "matvec: shapes")
+    _check(lib().anelm_matvec(_ptr(y), _ptr(W), _ptr(x), out_dim, in_dim, _stream(stream)))

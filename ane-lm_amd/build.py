@@ -28,6 +28,7 @@ SOURCES = [
     os.path.join(CSRC, "elementwise.hip"),
     os.path.join(CSRC, "sampling.hip"),
     os.path.join(CSRC, "attention.hip"),
+    os.path.join(CSRC, "deltanet.hip"),
     os.path.join(HOST, "dropin.hip"),
 ]
 

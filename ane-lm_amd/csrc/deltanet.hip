@@ -1,0 +1,359 @@
+// Qwen3.5 linear-attention (DeltaNet) ops and matvec for gfx950: gated
+// RMSNorm, L2 normalisation, the causal conv1d state update, the delta-rule
+// state step, and y = W x.  Replaces core/cpu_ops.cpp:33-39 and :100-171 as
+// models/llm/qwen3_5.cpp:493-549 calls them, batched over sequences.
+//
+// All are HBM- or latency-bound.  The dominant one at batch is the state
+// step: each (sequence, value head) state [key_dim, value_dim] is read once
+// and written once per token, held in registers in between.
+#include <cmath>
+
+#include "anelm_common.hpp"
+
+namespace anelm {
+namespace {
+
+constexpr int kRowThreads = 256;  // 4 rows per workgroup, one wave each
+
+// ------------------------------------------------------------ gated RMSNorm
+// core/cpu_ops.cpp:33-39: out = rmsnorm(x)*w (cpu_ops.cpp:25-31 rounding
+// steps), then out = out / (1 + expf(-z)), then out *= z.
+// Vector v = (row, head) of rows x heads, at row*ld + head*dim.
+template <int DT>
+__global__ __launch_bounds__(kRowThreads) void rmsnorm_gated_kernel(float* out, const float* x, const float* z,
+                                                                    const void* w, long rows, int heads, int dim,
+                                                                    long ld_x, long ld_z, long ld_out, float eps) {
+    const long vi = (long)blockIdx.x * (kRowThreads / kWave) + threadIdx.x / kWave;
+    const int lane = threadIdx.x % kWave;
+    if (vi >= rows * heads) return;
+    const long row = vi / heads, h = vi % heads;
+    const float* xr = x + row * ld_x + h * dim;
+    const float* zr = z + row * ld_z + h * dim;
+    float* orow = out + row * ld_out + h * dim;
+    float ss = 0.0f;
+    for (int i = lane; i < dim; i += kWave) ss = fmaf(xr[i], xr[i], ss);
+    ss = wave_sum(ss);
+    const float s = 1.0f / sqrtf(ss / (float)dim + eps);
+    for (int i = lane; i < dim; i += kWave) {
+        float o = (xr[i] * s) * load_w<DT>(w, i);
+        const float zi = zr[i];
+        o = o / (1.0f + expf(-zi));
+        orow[i] = o * zi;
+    }
+}
+
+// ------------------------------------------------------------ L2 normalise
+// core/cpu_ops.cpp:105-110: x *= 1/sqrtf(sum x^2 + 1e-12); then x *= scale
+// (the caller's separate vDSP_vsmul, qwen3_5.cpp:530-531; 1 is exact).
+__global__ __launch_bounds__(kRowThreads) void l2_normalize_kernel(float* x, long rows, int heads, int dim, long ld,
+                                                                   float scale) {
+    const long vi = (long)blockIdx.x * (kRowThreads / kWave) + threadIdx.x / kWave;
+    const int lane = threadIdx.x % kWave;
+    if (vi >= rows * heads) return;
+    float* xr = x + (vi / heads) * ld + (vi % heads) * dim;
+    float ss = 0.0f;
+    for (int i = lane; i < dim; i += kWave) ss = fmaf(xr[i], xr[i], ss);
+    ss = wave_sum(ss);
+    const float norm = 1.0f / sqrtf(ss + 1e-12f);
+    for (int i = lane; i < dim; i += kWave) xr[i] = (xr[i] * norm) * scale;
+}
+
+// ------------------------------------------------------------ conv1d update
+// core/cpu_ops.cpp:112-150, one workgroup per sequence: every thread reads
+// the sequence's ring position before the barrier, thread 0 advances it
+// after.  Fused multiply-adds in the reference's order, so results are
+// bit-identical to the oracle's.
+__global__ __launch_bounds__(1024) void conv1d_update_kernel(float* y, float* state, int32_t* state_pos,
+                                                             const float* x, const float* w, int channels,
+                                                             int kernel_size, long ld_x, long ld_y,
+                                                             long state_stride) {
+    const long b = blockIdx.x;
+    const int state_len = kernel_size - 1;
+    int pos = state_pos[b];
+    pos = pos < 0 ? 0 : (pos >= state_len ? 0 : pos);   // keeps every access in the ring
+    float* st = state + b * state_stride;
+    const float* xb = x + b * ld_x;
+    float* yb = y + b * ld_y;
+    if (kernel_size == 4) {
+        // the common case: every load of a batch of channels is issued
+        // before the first is used (ring indices pos, pos+1, pos+2 mod 3)
+        const int i1 = pos + 1 == 3 ? 0 : pos + 1;
+        const int i2 = i1 + 1 == 3 ? 0 : i1 + 1;
+        constexpr int kB = 8;
+        for (int c0 = threadIdx.x; c0 < channels; c0 += kB * 1024) {
+            float s0[kB], s1[kB], s2[kB], xc[kB];
+            float4 wc[kB];
+#pragma unroll
+            for (int u = 0; u < kB; u++) {
+                const int c = c0 + u * 1024;
+                if (c < channels) {
+                    const float* sc = st + (long)c * 3;
+                    s0[u] = sc[pos];
+                    s1[u] = sc[i1];
+                    s2[u] = sc[i2];
+                    xc[u] = xb[c];
+                    wc[u] = *reinterpret_cast<const float4*>(w + (long)c * 4);
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < kB; u++) {
+                const int c = c0 + u * 1024;
+                if (c < channels) {
+                    const float sum = fmaf(s2[u], wc[u].z, fmaf(s1[u], wc[u].y, fmaf(s0[u], wc[u].x, 0.0f)));
+                    yb[c] = fmaf(xc[u], wc[u].w, sum);
+                    st[(long)c * 3 + pos] = xc[u];
+                }
+            }
+        }
+    } else {
+        for (int c = threadIdx.x; c < channels; c += blockDim.x) {
+            float* sc = st + (long)c * state_len;
+            const float* wc = w + (long)c * kernel_size;
+            float sum = 0.0f;
+            for (int j = 0; j < state_len; j++) {
+                int idx = pos + j;
+                if (idx >= state_len) idx -= state_len;
+                sum = fmaf(sc[idx], wc[j], sum);
+            }
+            const float xv = xb[c];
+            yb[c] = fmaf(xv, wc[state_len], sum);
+            sc[pos] = xv;
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) state_pos[b] = pos + 1 == state_len ? 0 : pos + 1;
+}
+
+// ------------------------------------------------------------ delta-rule step
+// core/cpu_ops.cpp:152-171 for one (sequence, value head) per workgroup:
+//   Sk = S^T k;  delta = v - Sk;  S = decay*S + beta*k*delta^T;  y = S^T q.
+// 256 threads: VD/4 column groups of 4 columns (float4) x RG row groups of
+// RPT consecutive rows.  The state is read once (non-temporal), kept in
+// registers for both reductions and the update, and written once.
+struct SsmArgs {
+    float* y;
+    float* state;
+    const float* q;
+    const float* k;
+    const float* v;
+    const float* decay;   // [batch * nvh]
+    const float* beta;    // [batch * nvh]
+    int nvh, nkh;         // value heads, key heads (value head h uses key head h / (nvh/nkh))
+    long ld_qk, ld_v, ld_y, state_stride;  // per-sequence strides
+};
+
+template <int KD, int VD>
+__global__ __launch_bounds__(256) void ssm_step_kernel(SsmArgs a) {
+    constexpr int CG = VD / 4;          // column groups
+    constexpr int RG = 256 / CG;        // row groups
+    constexpr int RPT = KD / RG;        // rows per thread
+    __shared__ float sk[KD], sq[KD], sdelta[VD];
+    __shared__ float red[RG][VD];
+    const int tid = threadIdx.x;
+    const int cg = tid % CG, rg = tid / CG;
+    const long bh = blockIdx.x;
+    const long b = bh / a.nvh;
+    const int vh = (int)(bh % a.nvh);
+    const int kh = vh / (a.nvh / a.nkh);
+    const float* kp = a.k + b * a.ld_qk + (long)kh * KD;
+    const float* qp = a.q + b * a.ld_qk + (long)kh * KD;
+    const float* vp = a.v + b * a.ld_v + (long)vh * VD;
+    float* S = a.state + b * a.state_stride + (long)vh * KD * VD;
+    const float decay = a.decay[bh], beta = a.beta[bh];
+
+    float4 s[RPT];
+#pragma unroll
+    for (int r = 0; r < RPT; r++) s[r] = ld_nt(reinterpret_cast<const float4*>(S + (long)(rg * RPT + r) * VD) + cg);
+    for (int i = tid; i < KD; i += 256) {
+        sk[i] = kp[i];
+        sq[i] = qp[i];
+    }
+    __syncthreads();
+    // Sk = S^T k
+    float4 p = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int r = 0; r < RPT; r++) {
+        const float kr = sk[rg * RPT + r];
+        p.x = fmaf(s[r].x, kr, p.x);
+        p.y = fmaf(s[r].y, kr, p.y);
+        p.z = fmaf(s[r].z, kr, p.z);
+        p.w = fmaf(s[r].w, kr, p.w);
+    }
+    *reinterpret_cast<float4*>(&red[rg][4 * cg]) = p;
+    __syncthreads();
+    for (int j = tid; j < VD; j += 256) {
+        float t = red[0][j];
+#pragma unroll
+        for (int g = 1; g < RG; g++) t += red[g][j];
+        sdelta[j] = vp[j] - t;
+    }
+    __syncthreads();
+    // S = decay*S + beta*k*delta^T, then y = S^T q
+    const float4 d = *reinterpret_cast<const float4*>(&sdelta[4 * cg]);
+    p = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int r = 0; r < RPT; r++) {
+        const float bk = beta * sk[rg * RPT + r];
+        s[r].x = fmaf(bk, d.x, s[r].x * decay);
+        s[r].y = fmaf(bk, d.y, s[r].y * decay);
+        s[r].z = fmaf(bk, d.z, s[r].z * decay);
+        s[r].w = fmaf(bk, d.w, s[r].w * decay);
+        const float qr = sq[rg * RPT + r];
+        p.x = fmaf(s[r].x, qr, p.x);
+        p.y = fmaf(s[r].y, qr, p.y);
+        p.z = fmaf(s[r].z, qr, p.z);
+        p.w = fmaf(s[r].w, qr, p.w);
+        st_nt(reinterpret_cast<float4*>(S + (long)(rg * RPT + r) * VD) + cg, s[r]);
+    }
+    *reinterpret_cast<float4*>(&red[rg][4 * cg]) = p;   // red was last read before the previous barrier
+    __syncthreads();
+    float* yp = a.y + b * a.ld_y + (long)vh * VD;
+    for (int j = tid; j < VD; j += 256) {
+        float t = red[0][j];
+#pragma unroll
+        for (int g = 1; g < RG; g++) t += red[g][j];
+        yp[j] = t;
+    }
+}
+
+// ------------------------------------------------------------ matvec
+// core/cpu_ops.cpp:100-103: y = W x, W [out_dim, in_dim] row-major fp32.
+// One wave per row; W is streamed once (non-temporal), x comes from cache.
+template <bool VEC>
+__global__ __launch_bounds__(kRowThreads) void matvec_kernel(float* y, const float* W, const float* x, long out_dim,
+                                                             int in_dim) {
+    const long row = (long)blockIdx.x * (kRowThreads / kWave) + threadIdx.x / kWave;
+    const int lane = threadIdx.x % kWave;
+    if (row >= out_dim) return;
+    const float* wr = W + row * (long)in_dim;
+    float acc = 0.0f;
+    if (VEC) {
+        const int n4 = in_dim / 4;
+        constexpr int U = 4;
+        for (int c0 = 0; c0 < n4; c0 += kWave * U) {
+            float4 wv[U], xv[U];
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const int c = c0 + u * kWave + lane;
+                wv[u] = c < n4 ? ld_nt(reinterpret_cast<const float4*>(wr) + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+                xv[u] = c < n4 ? reinterpret_cast<const float4*>(x)[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                acc = fmaf(wv[u].x, xv[u].x, acc);
+                acc = fmaf(wv[u].y, xv[u].y, acc);
+                acc = fmaf(wv[u].z, xv[u].z, acc);
+                acc = fmaf(wv[u].w, xv[u].w, acc);
+            }
+        }
+    } else {
+        for (int c = lane; c < in_dim; c += kWave) acc = fmaf(wr[c], x[c], acc);
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) y[row] = acc;
+}
+
+long row_blocks(long rows) { return (rows + kRowThreads / kWave - 1) / (kRowThreads / kWave); }
+
+template <int KD, int VD>
+void launch_ssm(const SsmArgs& a, long n, hipStream_t st) {
+    hipLaunchKernelGGL((ssm_step_kernel<KD, VD>), dim3(n), dim3(256), 0, st, a);
+}
+
+}  // namespace
+}  // namespace anelm
+
+using namespace anelm;
+
+extern "C" int anelm_rmsnorm_gated(float* out, const float* x, const float* z, const void* w, int w_dtype, long rows,
+                                   int heads, int dim, long ld_x, long ld_z, long ld_out, float eps, void* stream) {
+    clear_error();
+    if (!out || !x || !z || !w) return fail(ANELM_ERR_INVALID, "rmsnorm_gated: null pointer");
+    const long span = (long)heads * dim;
+    if (rows < 0 || heads <= 0 || dim <= 0 || (rows > 1 && (ld_x < span || ld_z < span || ld_out < span)))
+        return fail(ANELM_ERR_INVALID, "rmsnorm_gated: bad sizes or strides");
+    if (w_dtype != ANELM_F32 && w_dtype != ANELM_F16 && w_dtype != ANELM_BF16)
+        return fail(ANELM_ERR_INVALID, "rmsnorm_gated: weight dtype %d", w_dtype);
+    if (rows == 0) return ANELM_OK;
+    const dim3 grid(row_blocks(rows * heads));
+    hipStream_t st = as_stream(stream);
+    if (w_dtype == ANELM_F32)
+        hipLaunchKernelGGL((rmsnorm_gated_kernel<ANELM_F32>), grid, dim3(kRowThreads), 0, st, out, x, z, w, rows, heads, dim, ld_x, ld_z, ld_out, eps);
+    else if (w_dtype == ANELM_F16)
+        hipLaunchKernelGGL((rmsnorm_gated_kernel<ANELM_F16>), grid, dim3(kRowThreads), 0, st, out, x, z, w, rows, heads, dim, ld_x, ld_z, ld_out, eps);
+    else
+        hipLaunchKernelGGL((rmsnorm_gated_kernel<ANELM_BF16>), grid, dim3(kRowThreads), 0, st, out, x, z, w, rows, heads, dim, ld_x, ld_z, ld_out, eps);
+    return launch_status("rmsnorm_gated");
+}
+
+extern "C" int anelm_l2_normalize(float* x, long rows, int heads, int dim, long ld, float scale, void* stream) {
+    clear_error();
+    if (!x) return fail(ANELM_ERR_INVALID, "l2_normalize: null pointer");
+    if (rows < 0 || heads <= 0 || dim <= 0 || (rows > 1 && ld < (long)heads * dim))
+        return fail(ANELM_ERR_INVALID, "l2_normalize: bad sizes");
+    if (rows == 0) return ANELM_OK;
+    hipLaunchKernelGGL(l2_normalize_kernel, dim3(row_blocks(rows * heads)), dim3(kRowThreads), 0, as_stream(stream), x,
+                       rows, heads, dim, ld, scale);
+    return launch_status("l2_normalize");
+}
+
+extern "C" int anelm_conv1d_update(float* y, float* conv_state, int32_t* state_pos, const float* x, const float* w,
+                                   long batch, int channels, int kernel_size, long ld_x, long ld_y,
+                                   long state_stride, void* stream) {
+    clear_error();
+    if (!y || !conv_state || !state_pos || !x || !w) return fail(ANELM_ERR_INVALID, "conv1d_update: null pointer");
+    if (batch < 0 || channels <= 0 || kernel_size < 2)
+        return fail(ANELM_ERR_INVALID, "conv1d_update: bad sizes (kernel_size >= 2)");
+    if (batch > 1 && (ld_x < channels || ld_y < channels || state_stride < (long)channels * (kernel_size - 1)))
+        return fail(ANELM_ERR_INVALID, "conv1d_update: strides overlap");
+    if (kernel_size == 4 && !aligned16(w)) return fail(ANELM_ERR_INVALID, "conv1d_update: w not 16-byte aligned");
+    if (batch == 0) return ANELM_OK;
+    hipLaunchKernelGGL(conv1d_update_kernel, dim3(batch), dim3(1024), 0, as_stream(stream), y, conv_state, state_pos, x,
+                       w, channels, kernel_size, ld_x, ld_y, state_stride);
+    return launch_status("conv1d_update");
+}
+
+extern "C" int anelm_ssm_step(float* y, float* state, const float* q, const float* k, const float* v,
+                              const float* decay, const float* beta, long batch, int n_heads, int n_key_heads,
+                              int key_dim, int value_dim, long ld_qk, long ld_v, long ld_y, long state_stride,
+                              void* stream) {
+    clear_error();
+    if (!y || !state || !q || !k || !v || !decay || !beta) return fail(ANELM_ERR_INVALID, "ssm_step: null pointer");
+    if (batch < 0 || n_heads <= 0 || n_key_heads <= 0 || n_heads % n_key_heads)
+        return fail(ANELM_ERR_INVALID, "ssm_step: n_heads must be a positive multiple of n_key_heads");
+    const bool kd_ok = key_dim == 64 || key_dim == 128 || key_dim == 256;
+    if (!kd_ok || (value_dim != 64 && value_dim != 128))
+        return fail(ANELM_ERR_INVALID, "ssm_step: key_dim %d / value_dim %d (64/128/256 and 64/128)", key_dim, value_dim);
+    if (batch > 1 && (ld_qk < (long)n_key_heads * key_dim || ld_v < (long)n_heads * value_dim ||
+                      ld_y < (long)n_heads * value_dim || state_stride < (long)n_heads * key_dim * value_dim))
+        return fail(ANELM_ERR_INVALID, "ssm_step: strides overlap");
+    if (!aligned16(state) || (state_stride & 3)) return fail(ANELM_ERR_INVALID, "ssm_step: state not 16-byte aligned");
+    if (batch == 0) return ANELM_OK;
+    SsmArgs a{y, state, q, k, v, decay, beta, n_heads, n_key_heads, ld_qk, ld_v, ld_y, state_stride};
+    const long n = batch * n_heads;
+    hipStream_t st = as_stream(stream);
+    if (value_dim == 128) {
+        if (key_dim == 64) launch_ssm<64, 128>(a, n, st);
+        else if (key_dim == 128) launch_ssm<128, 128>(a, n, st);
+        else launch_ssm<256, 128>(a, n, st);
+    } else {
+        if (key_dim == 64) launch_ssm<64, 64>(a, n, st);
+        else if (key_dim == 128) launch_ssm<128, 64>(a, n, st);
+        else launch_ssm<256, 64>(a, n, st);
+    }
+    return launch_status("ssm_step");
+}
+
+extern "C" int anelm_matvec(float* y, const float* W, const float* x, long out_dim, int in_dim, void* stream) {
+    clear_error();
+    if (!y || !W || !x) return fail(ANELM_ERR_INVALID, "matvec: null pointer");
+    if (out_dim < 0 || in_dim <= 0) return fail(ANELM_ERR_INVALID, "matvec: bad sizes");
+    if (out_dim == 0) return ANELM_OK;
+    const dim3 grid(row_blocks(out_dim));
+    const bool vec = !(in_dim & 3) && aligned16(W) && aligned16(x);
+    if (vec)
+        hipLaunchKernelGGL((matvec_kernel<true>), grid, dim3(kRowThreads), 0, as_stream(stream), y, W, x, out_dim, in_dim);
+    else
+        hipLaunchKernelGGL((matvec_kernel<false>), grid, dim3(kRowThreads), 0, as_stream(stream), y, W, x, out_dim, in_dim);
+    return launch_status("matvec");
+}

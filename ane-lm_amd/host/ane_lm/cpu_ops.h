@@ -5,9 +5,8 @@
 // On any device error the call prints the library's message to stderr and
 // aborts: there is no CPU fallback.
 //
-// Only the functions on the fused layer-op path and the decode attention are
-// provided here; matvec, l2_normalize, conv1d_update, ssm_step and
-// rmsnorm_gated keep their reference definitions.
+// Every function of core/cpu_ops.h is provided, so core/cpu_ops.cpp can be
+// dropped from the build.
 #pragma once
 
 #include <cmath>
@@ -27,6 +26,9 @@ void mul_sigmoid_inplace(float* y, const float* z, int n, float* tmp);
 
 // core/cpu_ops.h:21 -- out may equal x
 void rmsnorm(float* out, const float* x, const float* weight, int dim, float eps = 1e-6f);
+// core/cpu_ops.h:22
+void rmsnorm_gated(float* out, const float* x, const float* z,
+                   const float* weight, int dim);
 
 // core/cpu_ops.h:26-29
 void apply_rope_cached(float* q, float* k, int n_q_heads, int n_kv_heads,
@@ -36,6 +38,20 @@ void apply_rope_cached(float* q, float* k, int n_q_heads, int n_kv_heads,
 
 // core/cpu_ops.h:33
 void softmax(float* x, int n);
+
+// core/cpu_ops.h:37
+void matvec(float* y, const float* W, const float* x, int out_dim, int in_dim);
+
+// core/cpu_ops.h:41
+void l2_normalize(float* x, int dim);
+
+// core/cpu_ops.h:45-46 -- state_pos is the caller's host int, advanced
+void conv1d_update(float* y, float* conv_state, int* state_pos, const float* x,
+                   const float* w, int channels, int kernel_size);
+
+// core/cpu_ops.h:49-50
+void ssm_step(float* y, float* state, const float* q, const float* k,
+              const float* v, float decay, float beta, int key_dim, int value_dim);
 
 // core/cpu_ops.h:53-56 -- caches [cache_capacity, n_kv_heads, head_dim]
 // (host memory, staged to the device on every call)

@@ -157,6 +157,107 @@ void softmax(float* x, int n) {
     S.sync();
 }
 
+// core/cpu_ops.cpp:33-39
+void rmsnorm_gated(float* out, const float* x, const float* z, const float* weight, int dim) {
+    if (dim <= 0) return;
+    Staging& S = t_stage;
+    const size_t n = (size_t)dim * 4;
+    const size_t sz[4] = {n, n, n, n};
+    char* d[4];
+    S.get(sz, d);
+    S.h2d(d[0], x, n);
+    S.h2d(d[1], z, n);
+    S.h2d(d[2], weight, n);
+    check_rc(anelm_rmsnorm_gated(reinterpret_cast<float*>(d[3]), reinterpret_cast<const float*>(d[0]),
+                                 reinterpret_cast<const float*>(d[1]), d[2], ANELM_F32, 1, 1, dim, dim, dim, dim,
+                                 1e-6f, S.s()),
+             "rmsnorm_gated");
+    S.d2h(out, d[3], n);
+    S.sync();
+}
+
+// core/cpu_ops.cpp:100-103
+void matvec(float* y, const float* W, const float* x, int out_dim, int in_dim) {
+    if (out_dim <= 0 || in_dim <= 0) return;
+    Staging& S = t_stage;
+    const size_t sz[3] = {(size_t)out_dim * in_dim * 4, (size_t)in_dim * 4, (size_t)out_dim * 4};
+    char* d[3];
+    S.get(sz, d);
+    S.h2d(d[0], W, sz[0]);
+    S.h2d(d[1], x, sz[1]);
+    check_rc(anelm_matvec(reinterpret_cast<float*>(d[2]), reinterpret_cast<const float*>(d[0]),
+                          reinterpret_cast<const float*>(d[1]), out_dim, in_dim, S.s()),
+             "matvec");
+    S.d2h(y, d[2], sz[2]);
+    S.sync();
+}
+
+// core/cpu_ops.cpp:105-110
+void l2_normalize(float* x, int dim) {
+    if (dim <= 0) return;
+    Staging& S = t_stage;
+    const size_t sz[1] = {(size_t)dim * 4};
+    char* d[1];
+    S.get(sz, d);
+    S.h2d(d[0], x, sz[0]);
+    check_rc(anelm_l2_normalize(reinterpret_cast<float*>(d[0]), 1, 1, dim, dim, 1.0f, S.s()), "l2_normalize");
+    S.d2h(x, d[0], sz[0]);
+    S.sync();
+}
+
+// core/cpu_ops.cpp:112-150
+void conv1d_update(float* y, float* conv_state, int* state_pos, const float* x, const float* w, int channels,
+                   int kernel_size) {
+    if (channels <= 0 || kernel_size < 2) return;
+    Staging& S = t_stage;
+    const size_t sn = (size_t)channels * (kernel_size - 1) * 4;
+    const size_t sz[5] = {(size_t)channels * 4, sn, 4, (size_t)channels * 4, (size_t)channels * kernel_size * 4};
+    char* d[5];
+    S.get(sz, d);
+    const int32_t pos = *state_pos;
+    S.h2d(d[1], conv_state, sn);
+    S.h2d(d[2], &pos, 4);
+    S.h2d(d[3], x, sz[3]);
+    S.h2d(d[4], w, sz[4]);
+    check_rc(anelm_conv1d_update(reinterpret_cast<float*>(d[0]), reinterpret_cast<float*>(d[1]),
+                                 reinterpret_cast<int32_t*>(d[2]), reinterpret_cast<const float*>(d[3]),
+                                 reinterpret_cast<const float*>(d[4]), 1, channels, kernel_size, channels, channels,
+                                 (long)channels * (kernel_size - 1), S.s()),
+             "conv1d_update");
+    int32_t npos = 0;
+    S.d2h(y, d[0], sz[0]);
+    S.d2h(conv_state, d[1], sn);
+    S.d2h(&npos, d[2], 4);
+    S.sync();
+    *state_pos = npos;
+}
+
+// core/cpu_ops.cpp:152-171
+void ssm_step(float* y, float* state, const float* q, const float* k, const float* v, float decay, float beta,
+              int key_dim, int value_dim) {
+    Staging& S = t_stage;
+    const size_t sn = (size_t)key_dim * value_dim * 4;
+    const size_t sz[7] = {(size_t)value_dim * 4, sn, (size_t)key_dim * 4, (size_t)key_dim * 4,
+                          (size_t)value_dim * 4, 4, 4};
+    char* d[7];
+    S.get(sz, d);
+    S.h2d(d[1], state, sn);
+    S.h2d(d[2], q, sz[2]);
+    S.h2d(d[3], k, sz[3]);
+    S.h2d(d[4], v, sz[4]);
+    S.h2d(d[5], &decay, 4);
+    S.h2d(d[6], &beta, 4);
+    check_rc(anelm_ssm_step(reinterpret_cast<float*>(d[0]), reinterpret_cast<float*>(d[1]),
+                            reinterpret_cast<const float*>(d[2]), reinterpret_cast<const float*>(d[3]),
+                            reinterpret_cast<const float*>(d[4]), reinterpret_cast<const float*>(d[5]),
+                            reinterpret_cast<const float*>(d[6]), 1, 1, 1, key_dim, value_dim, key_dim, value_dim,
+                            value_dim, (long)key_dim * value_dim, S.s()),
+             "ssm_step");
+    S.d2h(y, d[0], sz[0]);
+    S.d2h(state, d[1], sn);
+    S.sync();
+}
+
 // core/cpu_ops.cpp:173-240
 void gqa_attention(float* out, const float* q, const float* k_cache, const float* v_cache, int n_heads,
                    int n_kv_heads, int head_dim, int q_head_stride, int cache_start, int cache_len,

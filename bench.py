@@ -288,6 +288,72 @@ def measure_attention(hip, w, steps, layers=8):
                 note="per layer; algorithmic bytes = full K and V rings read once + q and out")
 
 
+DN_WORKLOADS = {
+    # Qwen3.5-0.8B linear-attention layer shapes (models/llm/qwen3_5.h:40-44): 16 key and
+    # 16 value heads of 128, conv kernel 4 over 2*2048 + 2048 channels
+    "deltanet-qwen3.5-0.8b-decode-b64": dict(B=64, nvh=16, nkh=16, kd=128, vd=128, K=4),
+    "deltanet-qwen3.5-0.8b-decode-b1": dict(B=1, nvh=16, nkh=16, kd=128, vd=128, K=4),
+}
+
+
+def dn_bytes(w):
+    """Per layer and token: the delta-rule states read and written once (the
+    dominant term), conv rings read and written, q/k/v/z/x/y activations and
+    the conv weights once."""
+    B, nvh, nkh, kd, vd, K = w["B"], w["nvh"], w["nkh"], w["kd"], w["vd"], w["K"]
+    ch = 2 * nkh * kd + nvh * vd
+    state = B * nvh * kd * vd * 4 * 2
+    conv = B * ch * (K - 1) * 4 * 2 + ch * K * 4 + B * ch * 4 * 2
+    acts = B * (2 * nkh * kd * 4 * 2 + nvh * vd * 4 * 3 + nvh * vd * 4 * 2)
+    return dict(ssm_step=state + B * (2 * nkh * kd + 2 * nvh * vd) * 4, layer=state + conv + acts)
+
+
+def measure_deltanet(hip, w, steps, layers=8):
+    """One decode step of the linear-attention layer ops (qwen3_5.cpp:513-549:
+    conv1d_update, SiLU, L2-normalised and scaled q, L2-normalised k, the
+    delta-rule step, gated RMSNorm) over `layers` distinct layers' states,
+    graph-replayed; plus the state step alone."""
+    import torch
+
+    B, nvh, nkh, kd, vd, K = w["B"], w["nvh"], w["nkh"], w["kd"], w["vd"], w["K"]
+    ch = 2 * nkh * kd + nvh * vd
+    g = torch.Generator(device="cuda").manual_seed(41)
+    rn = lambda *s: torch.randn(*s, generator=g, device="cuda")
+    lay = [dict(S=0.05 * rn(B, nvh, kd, vd), conv=rn(B, ch, K - 1), cw=rn(ch, K), pos=torch.zeros(B, dtype=torch.int32, device="cuda"),
+                decay=torch.rand(B, nvh, generator=g, device="cuda"), beta=torch.rand(B, nvh, generator=g, device="cuda"),
+                nw=1.0 + 0.02 * rn(vd)) for _ in range(layers)]
+    x = rn(B, ch)
+    z = rn(B, nvh * vd)
+    mixed = torch.empty(B, ch, device="cuda")
+    y = torch.empty(B, nvh * vd, device="cuda")
+    out = torch.empty(B, nvh * vd, device="cuda")
+    qs = float(1.0 / (kd ** 0.5))
+
+    def layer(L):
+        hip.conv1d_update(mixed, L["conv"], L["pos"], x, L["cw"])               # :513
+        hip.silu(mixed)                                                         # :514
+        hip.l2_normalize(mixed[:, :nkh * kd], qs, heads=nkh)                     # :528, :530-531
+        hip.l2_normalize(mixed[:, nkh * kd:2 * nkh * kd], 1.0, heads=nkh)        # :529
+        hip.ssm_step(y, L["S"], mixed[:, :nkh * kd], mixed[:, nkh * kd:2 * nkh * kd], mixed[:, 2 * nkh * kd:],
+                     L["decay"], L["beta"], nkh)                                # :533-542
+        hip.rmsnorm_gated(out, y, z, L["nw"], heads=nvh)                         # :545-549
+
+    gr = capture(lambda: [layer(L) for L in lay])
+    gr.replay()
+    ms = time_region(gr.replay, steps) / layers
+    gs = capture(lambda: [hip.ssm_step(y, L["S"], mixed[:, :nkh * kd], mixed[:, nkh * kd:2 * nkh * kd],
+                                       mixed[:, 2 * nkh * kd:], L["decay"], L["beta"], nkh) for L in lay])
+    gs.replay()
+    ms_s = time_region(gs.replay, steps) / layers
+    b = dn_bytes(w)
+    del lay, gr, gs
+    torch.cuda.empty_cache()
+    f = lambda byt, ms: dict(us=round(ms * 1e3, 2), GBps=round(byt / ms / 1e6, 1),
+                             frac=round(byt / ms / 1e6 / HBM_PEAK_GBPS, 4), bytes=byt)
+    return dict(layer=dict(f(b["layer"], ms), tokens_per_s=round(B / (ms / 1e3), 1)), ssm_step=f(b["ssm_step"], ms_s),
+                note="per layer; algorithmic bytes = delta-rule states read+written once, conv rings, activations")
+
+
 def cpu_attention(w, target_s):
     """The oracle's gqa_attention (heads in parallel, as the reference runs
     them) for one sequence, repeated for about target_s seconds."""
@@ -567,6 +633,8 @@ def main():
     if args.only:
         if args.only in ATTN_WORKLOADS:
             r = measure_attention(anelm, ATTN_WORKLOADS[args.only], max(args.steps, 20))
+        elif args.only in DN_WORKLOADS:
+            r = measure_deltanet(anelm, DN_WORKLOADS[args.only], max(args.steps, 20))
         elif args.only == "sampling-64x151936":
             r = measure_sampler(anelm, max(args.steps, 20))
         elif args.only == "convert-qwen3-8b-bf16":
@@ -594,6 +662,8 @@ def main():
         configs["sampling-64x151936"] = measure_sampler(anelm, max(args.steps, 20))
         for name, aw in ATTN_WORKLOADS.items():
             configs[name] = measure_attention(anelm, aw, max(args.steps, 20))
+        for name, dw in DN_WORKLOADS.items():
+            configs[name] = measure_deltanet(anelm, dw, max(args.steps, 20))
         configs["convert-qwen3-8b-bf16"] = measure_convert(anelm)
     cpu = None
     cpu_configs = {}

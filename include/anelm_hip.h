@@ -229,6 +229,52 @@ int anelm_gqa_attention_ring(float* out, const float* q, const float* k_cache, c
                              int cache_start, int cache_len, int cache_capacity, void* workspace,
                              size_t workspace_bytes, void* stream);
 
+/* ------------------------------ Qwen3.5 linear-attention ops and matvec */
+
+/* Gated RMSNorm of rows x heads vectors of `dim` (vector (r, h) at
+ * r*ld + h*dim of each operand): out = rmsnorm(x)*w (the anelm_rmsnorm
+ * rounding steps), then out = out/(1 + expf(-z)), then out *= z.  Replaces ane_lm::rmsnorm_gated (core/cpu_ops.cpp:33-39,
+ * cpu_ops.h:22; the reference passes no eps, so its default 1e-6 applies),
+ * called per value head at models/llm/qwen3_5.cpp:545-549.  out may equal x. */
+int anelm_rmsnorm_gated(float* out, const float* x, const float* z, const void* w, int w_dtype, long rows,
+                        int heads, int dim, long ld_x, long ld_z, long ld_out, float eps, void* stream);
+
+/* v = (v * (1/sqrtf(sum v^2 + 1e-12))) * scale, in place, for the rows x
+ * heads vectors v of `dim` at x + r*ld + h*dim (ane_lm::l2_normalize,
+ * core/cpu_ops.cpp:105-110, cpu_ops.h:41).  scale = 1
+ * is the reference function itself (the second product is exact); the
+ * q path of models/llm/qwen3_5.cpp:528-531 passes 1/sqrtf(key_dim). */
+int anelm_l2_normalize(float* x, long rows, int heads, int dim, long ld, float scale, void* stream);
+
+/* Causal depthwise conv1d step for `batch` sequences (ane_lm::conv1d_update,
+ * core/cpu_ops.cpp:112-150, cpu_ops.h:45-46): per sequence b a ring
+ * conv_state + b*state_stride of [channels, kernel_size-1] past inputs whose
+ * oldest entry is at state_pos[b] (device int32); y = sum_j
+ * state[(pos+j) mod (K-1)]*w[c*K+j] + x*w[c*K+K-1] as fused multiply-adds
+ * in that order, then the oldest entry becomes x and state_pos[b] advances.
+ * A state_pos outside [0, K-1) is taken as 0. */
+int anelm_conv1d_update(float* y, float* conv_state, int32_t* state_pos, const float* x, const float* w,
+                        long batch, int channels, int kernel_size, long ld_x, long ld_y, long state_stride,
+                        void* stream);
+
+/* Delta-rule state step (ane_lm::ssm_step, core/cpu_ops.cpp:152-171,
+ * cpu_ops.h:49-50) for `batch` sequences x n_heads value heads: head h of
+ * sequence b has state + b*state_stride + h*key_dim*value_dim
+ * ([key_dim, value_dim] row-major), q/k from key head h/(n_heads/n_key_heads)
+ * at q/k + b*ld_qk, v at v + b*ld_v + h*value_dim, decay/beta[b*n_heads+h]:
+ *   Sk = S^T k; delta = v - Sk; S = decay*S + beta*k*delta^T; y = S^T q.
+ * The loop of models/llm/qwen3_5.cpp:524-543 in one launch.  key_dim 64, 128
+ * or 256; value_dim 64 or 128; state 16-byte aligned. */
+int anelm_ssm_step(float* y, float* state, const float* q, const float* k, const float* v,
+                   const float* decay, const float* beta, long batch, int n_heads, int n_key_heads,
+                   int key_dim, int value_dim, long ld_qk, long ld_v, long ld_y, long state_stride,
+                   void* stream);
+
+/* y = W x, W [out_dim, in_dim] row-major fp32 (ane_lm::matvec,
+ * core/cpu_ops.cpp:100-103, cpu_ops.h:37; the reference's CPU LM head and
+ * DeltaNet a/b projections, models/llm/qwen3_5.cpp:509-510, :689). */
+int anelm_matvec(float* y, const float* W, const float* x, long out_dim, int in_dim, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

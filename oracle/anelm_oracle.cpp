@@ -356,6 +356,79 @@ extern "C" void orc_softmax(float* x, int n) {
     for (int i = 0; i < n; i++) x[i] = x[i] * inv;                 // vDSP_vsmul :98
 }
 
+// ------------------------------------------------ Qwen3.5 linear attention
+
+// core/cpu_ops.cpp:33-39
+extern "C" void orc_rmsnorm_gated(float* out, const float* x, const float* z, const float* w, int dim) {
+    orc_rmsnorm(out, x, w, dim, 1e-6f);                                      // :35 (default eps)
+    for (int i = 0; i < dim; i++) out[i] = out[i] / (1.0f + expf(-z[i]));   // mul_sigmoid_inplace :37
+    for (int i = 0; i < dim; i++) out[i] = out[i] * z[i];                   // vDSP_vmul :38
+}
+
+// core/cpu_ops.cpp:105-110
+extern "C" void orc_l2_normalize(float* x, int dim) {
+    double ss = 0.0;
+    for (int i = 0; i < dim; i++) ss += (double)x[i] * (double)x[i];      // vDSP_svesq :107
+    const float norm = 1.0f / sqrtf((float)ss + 1e-12f);                   // :108
+    for (int i = 0; i < dim; i++) x[i] = x[i] * norm;                      // vDSP_vsmul :109
+}
+
+// core/cpu_ops.cpp:112-150 (the kernel_size 4 branch :117-133 is this loop unrolled)
+extern "C" void orc_conv1d_update(float* y, float* conv_state, int* state_pos, const float* x, const float* w,
+                                  int channels, int kernel_size) {
+    const int state_len = kernel_size - 1;
+    int pos = *state_pos;
+    for (int c = 0; c < channels; c++) {
+        float* st = conv_state + (size_t)c * state_len;
+        const float* wc = w + (size_t)c * kernel_size;
+        float sum = 0.0f;
+        for (int j = 0; j < state_len; j++) {
+            int idx = pos + j;
+            if (idx >= state_len) idx -= state_len;
+            sum = fmaf(st[idx], wc[j], sum);
+        }
+        y[c] = fmaf(x[c], wc[state_len], sum);
+        st[pos] = x[c];
+    }
+    pos++;
+    if (pos == state_len) pos = 0;
+    *state_pos = pos;
+}
+
+// core/cpu_ops.cpp:152-171
+extern "C" void orc_ssm_step(float* y, float* state, const float* q, const float* k, const float* v, float decay,
+                             float beta, int key_dim, int value_dim) {
+    std::vector<float> delta(value_dim);
+    for (int j = 0; j < value_dim; j++) {                       // Sk = state^T k   :154-155
+        double sk = 0.0;
+        for (int i = 0; i < key_dim; i++) sk += (double)state[(size_t)i * value_dim + j] * k[i];
+        delta[j] = v[j] - (float)sk;                            // :158
+    }
+    for (int i = 0; i < key_dim; i++) {                         // sscal :160, sger :161-162
+        for (int j = 0; j < value_dim; j++) {
+            float& s = state[(size_t)i * value_dim + j];
+            const float scaled = s * decay;
+            s = (float)((double)scaled + (double)beta * (double)k[i] * (double)delta[j]);
+        }
+    }
+    for (int j = 0; j < value_dim; j++) {                       // y = state^T q   :164-165
+        double acc = 0.0;
+        for (int i = 0; i < key_dim; i++) acc += (double)state[(size_t)i * value_dim + j] * q[i];
+        y[j] = (float)acc;
+    }
+}
+
+// core/cpu_ops.cpp:100-103
+extern "C" void orc_matvec(float* y, const float* W, const float* x, int out_dim, int in_dim) {
+#pragma omp parallel for schedule(static) if (out_dim >= 1024)
+    for (int r = 0; r < out_dim; r++) {
+        const float* wr = W + (size_t)r * in_dim;
+        double acc = 0.0;
+        for (int c = 0; c < in_dim; c++) acc += (double)wr[c] * x[c];
+        y[r] = (float)acc;
+    }
+}
+
 // ------------------------------------------------------- KV ring, attention
 
 // models/llm/qwen3.cpp:475-488

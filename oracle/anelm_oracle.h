@@ -144,6 +144,36 @@ void orc_gqa_attention(float* out, const float* q, const float* k_cache, const f
                        int n_heads, int n_kv_heads, int head_dim, int q_head_stride, int cache_start,
                        int cache_len, int cache_capacity);
 
+/* ---- Qwen3.5 linear-attention (DeltaNet) ops, core/cpu_ops.cpp:33-39, :100-171 ---- */
+/* rmsnorm (eps 1e-6, the default argument) then out = out/(1+expf(-z)),
+ * out *= z  (cpu_ops.cpp:33-39).  pinned: z = 0 gives exact zeros,
+ * equals rmsnorm * silu(z) in fp64, constant-row closed form. */
+void orc_rmsnorm_gated(float* out, const float* x, const float* z, const float* w, int dim);
+/* x *= 1/sqrtf(sum x^2 + 1e-12)  (cpu_ops.cpp:105-110; the sum correctly
+ * rounded).  pinned: unit norm, exact power-of-two scale invariance,
+ * constant-vector closed form, zero vector stays zero. */
+void orc_l2_normalize(float* x, int dim);
+/* Depthwise causal conv over a ring of the last kernel_size-1 inputs per
+ * channel (cpu_ops.cpp:112-150): conv_state [channels, kernel_size-1], the
+ * oldest entry at *state_pos; y = sum_j state[(pos+j) mod (K-1)]*w[j] +
+ * x*w[K-1], as fused multiply-adds in that order (what clang's default
+ * -ffp-contract=on makes of :131 and :140-145 on the reference's arm64
+ * target); then the oldest entry becomes x and pos advances.
+ * pinned: float64 direct convolution over the input history. */
+void orc_conv1d_update(float* y, float* conv_state, int* state_pos, const float* x, const float* w,
+                       int channels, int kernel_size);
+/* Delta-rule state step (cpu_ops.cpp:152-171): state [key_dim, value_dim];
+ * Sk = state^T k; delta = v - Sk; state = decay*state + beta*k*delta^T;
+ * y = state^T q.  BLAS summation order is unspecified: the oracle rounds
+ * each dot and each updated element once from double.
+ * pinned: float64 brute force; decay 1 beta 0 leaves the state; the delta
+ * rule recalls v for a unit key. */
+void orc_ssm_step(float* y, float* state, const float* q, const float* k, const float* v, float decay,
+                  float beta, int key_dim, int value_dim);
+/* y = W x, W [out_dim, in_dim] row-major (cpu_ops.cpp:100-103, cblas_sgemv);
+ * each dot correctly rounded.  pinned: identity matrix, fp64 brute force. */
+void orc_matvec(float* y, const float* W, const float* x, int out_dim, int in_dim);
+
 /* ---- one layer of the fused op chain over T tokens, per token as the
  * reference's forward() runs it (qwen3.cpp:502-528):
  *   (1) xn = rmsnorm(x, w_in)                       :503

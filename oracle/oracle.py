@@ -46,6 +46,11 @@ _SIGS = {
                                _P, _P, _I, _F, _F, _I]),
     "orc_max_threads": (_I, []),
     "orc_kv_ring_append": (_I, [_P, _P, _P, _P, _I, _P, _P, _I]),
+    "orc_rmsnorm_gated": (None, [_P, _P, _P, _P, _I]),
+    "orc_l2_normalize": (None, [_P, _I]),
+    "orc_conv1d_update": (None, [_P, _P, _P, _P, _P, _I, _I]),
+    "orc_ssm_step": (None, [_P, _P, _P, _P, _P, _F, _F, _I, _I]),
+    "orc_matvec": (None, [_P, _P, _P, _I, _I]),
     "orc_gqa_attention": (None, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I]),
 }
 
@@ -268,6 +273,48 @@ def gqa_attention(q, k_cache, v_cache, n_heads, n_kv_heads, head_dim, cache_star
     lib().orc_gqa_attention(_p(out), _p(q), _p(kc), _p(vc), n_heads, n_kv_heads, head_dim, qs, cache_start,
                             cache_len, cap)
     return out
+
+
+def rmsnorm_gated(x, z, w):
+    x, z, w = _c(x, np.float32), _c(z, np.float32), _c(w, np.float32)
+    out = np.empty_like(x)
+    lib().orc_rmsnorm_gated(_p(out), _p(x), _p(z), _p(w), x.size)
+    return out
+
+
+def l2_normalize(x):
+    y = _c(x, np.float32).copy()
+    lib().orc_l2_normalize(_p(y), y.size)
+    return y
+
+
+def conv1d_update(conv_state, state_pos, x, w):
+    """conv_state [channels, K-1] float32 (updated in place); state_pos an
+    np.int32 array of one element (updated); w [channels, K]. Returns y."""
+    ch, K = w.shape
+    assert conv_state.flags.c_contiguous and conv_state.dtype == np.float32 and conv_state.shape == (ch, K - 1)
+    assert state_pos.dtype == np.int32 and state_pos.size == 1
+    y = np.empty(ch, np.float32)
+    lib().orc_conv1d_update(_p(y), _p(conv_state), ctypes.c_void_p(state_pos.ctypes.data), _p(_c(x, np.float32)),
+                            _p(_c(w, np.float32)), ch, K)
+    return y
+
+
+def ssm_step(state, q, k, v, decay, beta):
+    """state [key_dim, value_dim] float32, updated in place. Returns y."""
+    kd, vd = state.shape
+    assert state.flags.c_contiguous and state.dtype == np.float32
+    y = np.empty(vd, np.float32)
+    lib().orc_ssm_step(_p(y), _p(state), _p(_c(q, np.float32)), _p(_c(k, np.float32)), _p(_c(v, np.float32)),
+                       decay, beta, kd, vd)
+    return y
+
+
+def matvec(W, x):
+    W, x = _c(W, np.float32), _c(x, np.float32)
+    y = np.empty(W.shape[0], np.float32)
+    lib().orc_matvec(_p(y), _p(W), _p(x), W.shape[0], W.shape[1])
+    return y
 
 
 def max_threads() -> int:

@@ -211,6 +211,53 @@ int main() {
         report(zero, "gqa_attention empty cache", 0);
     }
 
+    // Qwen3.5 DeltaNet ops and matvec as qwen3_5.cpp:509-549 calls them
+    {
+        const int kd = 128, vd = 128, ch = 6144, K = 4;
+        auto x = randv(vd), z = randv(vd), w = randv(vd, 0.1f);
+        for (auto& e : w) e += 1.f;
+        std::vector<float> out(vd), ref(vd);
+        ane_lm::rmsnorm_gated(out.data(), x.data(), z.data(), w.data(), vd);
+        orc_rmsnorm_gated(ref.data(), x.data(), z.data(), w.data(), vd);
+        report(max_rel(out.data(), ref.data(), vd) <= 1e-5, "rmsnorm_gated", max_rel(out.data(), ref.data(), vd));
+
+        auto q = randv(kd), qr = q;
+        ane_lm::l2_normalize(q.data(), kd);
+        orc_l2_normalize(qr.data(), kd);
+        report(max_rel(q.data(), qr.data(), kd) <= 1e-5, "l2_normalize", max_rel(q.data(), qr.data(), kd));
+
+        auto cw = randv((size_t)ch * K);
+        std::vector<float> st((size_t)ch * (K - 1), 0.f), sr(st), y(ch), yr(ch);
+        int pos = 0, posr = 0;
+        bool same = true;
+        for (int step = 0; step < 5; step++) {
+            auto cx = randv(ch);
+            ane_lm::conv1d_update(y.data(), st.data(), &pos, cx.data(), cw.data(), ch, K);
+            orc_conv1d_update(yr.data(), sr.data(), &posr, cx.data(), cw.data(), ch, K);
+            same = same && same_bits(y.data(), yr.data(), (size_t)ch * 4) && pos == posr;
+        }
+        same = same && same_bits(st.data(), sr.data(), st.size() * 4);
+        report(same, "conv1d_update bit-exact over 5 steps", same ? 0 : 1);
+
+        auto S = randv((size_t)kd * vd, 0.1f), Sr = S, k = randv(kd), v = randv(vd), qq = randv(kd);
+        std::vector<float> ys(vd), ysr(vd);
+        ane_lm::ssm_step(ys.data(), S.data(), qq.data(), k.data(), v.data(), 0.9f, 0.3f, kd, vd);
+        orc_ssm_step(ysr.data(), Sr.data(), qq.data(), k.data(), v.data(), 0.9f, 0.3f, kd, vd);
+        double es = 0, ey = 0;
+        for (size_t i = 0; i < S.size(); i++) es = std::fmax(es, std::fabs((double)S[i] - Sr[i]));
+        for (int j = 0; j < vd; j++) ey = std::fmax(ey, std::fabs((double)ys[j] - ysr[j]));
+        report(es <= 1e-5 && ey <= 1e-4, "ssm_step", std::fmax(es, ey));
+
+        const int od = 151936 / 8, id = 1024;
+        auto W = randv((size_t)od * id), xv = randv(id);
+        std::vector<float> mv(od), mvr(od);
+        ane_lm::matvec(mv.data(), W.data(), xv.data(), od, id);
+        orc_matvec(mvr.data(), W.data(), xv.data(), od, id);
+        double em = 0;
+        for (int i = 0; i < od; i++) em = std::fmax(em, std::fabs((double)mv[i] - mvr[i]));
+        report(em <= 1e-3, "matvec", em);
+    }
+
     printf("%s: %d failure(s)\n", g_fail ? "FAILED" : "OK", g_fail);
     return g_fail ? 1 : 0;
 }

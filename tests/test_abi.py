@@ -59,7 +59,12 @@ def test_dropin_cpp_symbols_exported():
                 "ane_lm::sample_token(float const*, int, ane_lm::SamplingParams const&, std::vector<int, std::allocator<int> > const&)",
                 "ane_lm::hip::bf16_to_f16_vec(unsigned short*, unsigned short const*, int)",
                 "ane_lm::hip::residual_add(float*, float const*, int)",
-                "ane_lm::gqa_attention(float*, float const*, float const*, float const*, int, int, int, int, int, int, int)"]:
+                "ane_lm::gqa_attention(float*, float const*, float const*, float const*, int, int, int, int, int, int, int)",
+                "ane_lm::rmsnorm_gated(float*, float const*, float const*, float const*, int)",
+                "ane_lm::matvec(float*, float const*, float const*, int, int)",
+                "ane_lm::l2_normalize(float*, int)",
+                "ane_lm::conv1d_update(float*, float*, int*, float const*, float const*, int, int)",
+                "ane_lm::ssm_step(float*, float*, float const*, float const*, float const*, float, float, int, int)"]:
         assert sig in out, sig
 
 
@@ -153,3 +158,21 @@ def test_attention_argument_checks(lib):
     a = lib.anelm_kv_ring_append
     assert a(fake, fake, None, fake, fake, fake, 1024, 1024, 4, 8, 128, 2048, 2048 * 1024, None) == -1
     assert a(fake, fake, fake, fake, fake, fake, 1000, 1024, 4, 8, 128, 2048, 2048 * 1024, None) == -1  # k_ld < row
+
+
+def test_deltanet_argument_checks(lib):
+    fake = ctypes.c_void_p(0x1000)
+    assert lib.anelm_rmsnorm_gated(fake, fake, fake, fake, 5, 4, 1, 128, 128, 128, 128, 1e-6, None) == -1  # dtype
+    assert lib.anelm_rmsnorm_gated(fake, fake, None, fake, 0, 4, 1, 128, 128, 128, 128, 1e-6, None) == -1
+    assert lib.anelm_rmsnorm_gated(fake, fake, fake, fake, 0, 4, 16, 128, 1024, 2048, 2048, 1e-6, None) == -1  # ld
+    assert lib.anelm_l2_normalize(fake, 4, 1, 128, 64, 1.0, None) == -1                                    # ld < dim
+    assert lib.anelm_l2_normalize(fake, 4, 0, 128, 4096, 1.0, None) == -1                                  # heads
+    assert lib.anelm_conv1d_update(fake, fake, fake, fake, fake, 2, 6144, 1, 6144, 6144, 6144 * 3, None) == -1
+    assert lib.anelm_conv1d_update(fake, fake, None, fake, fake, 2, 6144, 4, 6144, 6144, 6144 * 3, None) == -1
+    assert lib.anelm_conv1d_update(fake, fake, fake, fake, fake, 2, 6144, 4, 6144, 6144, 100, None) == -1  # overlap
+    s = lib.anelm_ssm_step
+    assert s(fake, fake, fake, fake, fake, fake, fake, 1, 16, 16, 96, 128, 2048, 2048, 2048, 16 * 128 * 128, None) == -1
+    assert s(fake, fake, fake, fake, fake, fake, fake, 1, 16, 5, 128, 128, 2048, 2048, 2048, 16 * 128 * 128, None) == -1
+    assert b"key_dim" in lib.anelm_last_error() or b"multiple" in lib.anelm_last_error()
+    assert lib.anelm_matvec(None, fake, fake, 4, 4, None) == -1
+    assert lib.anelm_matvec(fake, fake, fake, 4, 0, None) == -1
