@@ -75,6 +75,17 @@ _SIGS = {
     "anelm_conv1d_update": (_I, [_P, _P, _P, _P, _P, _L, _I, _I, _L, _L, _L, _P]),
     "anelm_ssm_step": (_I, [_P, _P, _P, _P, _P, _P, _P, _L, _I, _I, _I, _I, _L, _L, _L, _L, _P]),
     "anelm_matvec": (_I, [_P, _P, _P, _L, _I, _P]),
+    "anelm_st_open": (_P, [ctypes.c_char_p]),
+    "anelm_st_close": (None, [_P]),
+    "anelm_st_count": (_L, [_P]),
+    "anelm_st_find": (_L, [_P, ctypes.c_char_p]),
+    "anelm_st_info": (_I, [_P, _L, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(_I), ctypes.POINTER(_I),
+                           ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_uint64),
+                           ctypes.POINTER(ctypes.c_uint64)]),
+    "anelm_st_host_data": (_P, [_P, _L]),
+    "anelm_st_load": (_I, [_P, _L, _P, _I, _P]),
+    "anelm_ane_blob_header": (None, [_P, ctypes.c_uint64]),
+    "anelm_write_ane_blobs": (_L, [ctypes.c_char_p, ctypes.c_char_p, _P]),
 }
 
 EXPORTED = tuple(_SIGS)
@@ -331,3 +342,61 @@ def matvec(y, W, x, stream=None):
     out_dim, in_dim = W.shape
     _need(W.is_contiguous() and x.is_contiguous() and y.numel() >= out_dim, "matvec: shapes")
     _check(lib().anelm_matvec(_ptr(y), _ptr(W), _ptr(x), out_dim, in_dim, _stream(stream)))
+
+
+ST_F64, ST_I32, ST_I64, ST_U8, ST_UNKNOWN = 3, 4, 5, 6, -1
+
+
+class SafeTensorsFile:
+    """A safetensors file opened by the library (core/safetensors.cpp:193-244).
+    info(i) -> (name, dtype code, shape, offset, nbytes); load(i, dst, dtype)
+    copies tensor i into device tensor dst (widened / converted on the device)."""
+
+    def __init__(self, path):
+        self._h = lib().anelm_st_open(os.fsencode(path))
+        if not self._h:
+            raise AnelmError(ERR_INVALID, last_error())
+
+    def close(self):
+        if self._h:
+            lib().anelm_st_close(self._h)
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def __len__(self):
+        return lib().anelm_st_count(self._h)
+
+    def find(self, name):
+        return lib().anelm_st_find(self._h, name.encode())
+
+    def info(self, i):
+        name, dt, nd = ctypes.c_char_p(), _I(), _I()
+        shape = (ctypes.c_int64 * 8)()
+        off, nb = ctypes.c_uint64(), ctypes.c_uint64()
+        _check(lib().anelm_st_info(self._h, i, ctypes.byref(name), ctypes.byref(dt), ctypes.byref(nd), shape,
+                                   ctypes.byref(off), ctypes.byref(nb)))
+        return name.value.decode(), dt.value, tuple(shape[:nd.value]), off.value, nb.value
+
+    def host_data(self, i):
+        return lib().anelm_st_host_data(self._h, i)
+
+    def load(self, i, dst, dtype, stream=None):
+        _check(lib().anelm_st_load(self._h, i, _ptr(dst), dtype, _stream(stream)))
+
+
+def ane_blob_header(num_elements) -> bytes:
+    buf = (ctypes.c_uint8 * 128)()
+    lib().anelm_ane_blob_header(buf, num_elements)
+    return bytes(buf)
+
+
+def write_ane_blobs(safetensors_path, output_dir, stream=None) -> int:
+    n = lib().anelm_write_ane_blobs(os.fsencode(safetensors_path), os.fsencode(output_dir), _stream(stream))
+    if n < 0:
+        raise AnelmError(n, last_error())
+    return n

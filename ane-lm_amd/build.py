@@ -30,6 +30,7 @@ SOURCES = [
     os.path.join(CSRC, "attention.hip"),
     os.path.join(CSRC, "deltanet.hip"),
     os.path.join(HOST, "dropin.hip"),
+    os.path.join(HOST, "safetensors.hip"),
 ]
 
 ARCH = "gfx950"

@@ -46,6 +46,12 @@ extern "C" {
 #define ANELM_F32  0
 #define ANELM_F16  1
 #define ANELM_BF16 2
+/* further safetensors file dtypes (anelm_st_info) */
+#define ANELM_ST_F64 3
+#define ANELM_ST_I32 4
+#define ANELM_ST_I64 5
+#define ANELM_ST_U8  6
+#define ANELM_ST_UNKNOWN (-1)
 
 /* Description of the last error on the calling thread ("" if none). */
 const char* anelm_last_error(void);
@@ -274,6 +280,44 @@ int anelm_ssm_step(float* y, float* state, const float* q, const float* k, const
  * core/cpu_ops.cpp:100-103, cpu_ops.h:37; the reference's CPU LM head and
  * DeltaNet a/b projections, models/llm/qwen3_5.cpp:509-510, :689). */
 int anelm_matvec(float* y, const float* W, const float* x, long out_dim, int in_dim, void* stream);
+
+/* ------------------------------------------- safetensors and ANE weight blobs */
+
+/* A safetensors file opened for reading (core/safetensors.h:27-59,
+ * core/safetensors.cpp:193-244): the file is memory-mapped and its JSON
+ * header parsed (every tensor, no count limit; "__metadata__" skipped;
+ * names are the raw text between the key's quotes, as the reference keeps
+ * them).  A tensor whose data_offsets disagree with dtype x shape or leave
+ * the file is an error.  NULL on error (anelm_last_error). A handle is not
+ * thread-safe; host calls, they may allocate. */
+typedef struct anelm_st anelm_st;
+anelm_st* anelm_st_open(const char* path);
+void anelm_st_close(anelm_st* st);
+long anelm_st_count(const anelm_st* st);
+/* index of the tensor with this name, or -1 (SafeTensors::find, :246-253) */
+long anelm_st_find(const anelm_st* st, const char* name);
+/* name (valid until close), dtype (ANELM_F32/F16/BF16/ST_*), ndims, shape
+ * (up to 8 entries), byte offset in the data block and byte size; any output
+ * pointer may be NULL. */
+int anelm_st_info(const anelm_st* st, long i, const char** name, int* dtype, int* ndims, int64_t* shape,
+                  uint64_t* offset, uint64_t* nbytes);
+/* host pointer to tensor i's bytes in the mapping (SafeTensors::data / get_bf16_ptr) */
+const void* anelm_st_host_data(const anelm_st* st, long i);
+/* Tensor i into DEVICE memory dst as dst_dtype: its own dtype (a copy; the
+ * reference's load_f32_direct :283-297), or for a BF16 tensor ANELM_F32
+ * (exact widening on the device: load_bf16_to_f32 :266-281) or ANELM_F16
+ * (the truncating convert on the device, the blobs' data).  Staged through
+ * pinned memory on `stream`; returns when the tensor is in place. */
+int anelm_st_load(const anelm_st* st, long i, void* dst, int dst_dtype, void* stream);
+
+/* The 128-byte ANE blob header for num_elements fp16 values
+ * (core/safetensors.cpp:322-331, core/ane_runtime.cpp:199-205). */
+void anelm_ane_blob_header(uint8_t* header128, uint64_t num_elements);
+/* The `convert` command (SafeTensors::write_ane_blobs, core/safetensors.cpp:
+ * 345-383): every BF16 tensor becomes <output_dir>/<name, '.' -> '/'>.bin =
+ * header + truncating fp16 data (converted on the GPU), directories created
+ * as needed.  Returns the number of blobs written or a negative status. */
+long anelm_write_ane_blobs(const char* safetensors_path, const char* output_dir, void* stream);
 
 #ifdef __cplusplus
 }

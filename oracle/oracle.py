@@ -319,3 +319,68 @@ def matvec(W, x):
 
 def max_threads() -> int:
     return lib().orc_max_threads()
+
+
+# ------------------------------------------------------------ safetensors, ANE blobs
+
+ST_DTYPES = {"BF16": (np.uint16, 2), "F16": (np.uint16, 2), "F32": (np.float32, 4), "F64": (np.float64, 8),
+             "I32": (np.int32, 4), "I64": (np.int64, 8), "U8": (np.uint8, 1)}
+
+
+def read_safetensors(path):
+    """{name: (dtype string, shape, raw data as a numpy array)} in header
+    order: an 8-byte little-endian header length, a JSON header, then the
+    data block (the format core/safetensors.cpp:193-244 reads).  BF16/F16
+    data are returned as uint16 bit patterns; "__metadata__" is skipped."""
+    import json
+
+    with open(path, "rb") as f:
+        blob = f.read()
+    hlen = int.from_bytes(blob[:8], "little")
+    header = json.loads(blob[8:8 + hlen])
+    base = 8 + hlen
+    out = {}
+    for name, info in header.items():
+        if name == "__metadata__":
+            continue
+        a, b = info["data_offsets"]
+        dt, size = ST_DTYPES.get(info["dtype"], (np.uint8, 1))
+        out[name] = (info["dtype"], tuple(info["shape"]), np.frombuffer(blob[base + a:base + b], dtype=dt))
+    return out
+
+
+def ane_blob(bf16_bits):
+    """The ANE weight blob of a BF16 tensor, core/safetensors.cpp:316-343
+    (same bytes as core/ane_runtime.cpp:195-209): a 64-byte global header
+    with byte 0 = 1 and byte 4 = 2, a 64-byte chunk header with magic
+    EF BE AD DE, version 1 at +4, the fp16 data size (u32 LE) at +8 and the
+    data offset 128 (u32 LE) at +16, zeros elsewhere; then the truncating
+    fp16 convert of the data (common.h:81-83)."""
+    bits = np.ascontiguousarray(bf16_bits, dtype=np.uint16).ravel()
+    hdr = bytearray(128)
+    hdr[0] = 0x01
+    hdr[4] = 0x02
+    hdr[64:68] = bytes([0xEF, 0xBE, 0xAD, 0xDE])
+    hdr[68] = 0x01
+    hdr[72:76] = (bits.size * 2 & 0xFFFFFFFF).to_bytes(4, "little")
+    hdr[80:84] = (128).to_bytes(4, "little")
+    return bytes(hdr) + bf16_to_f16(bits).tobytes()
+
+
+def blob_relpath(name):
+    """core/safetensors.cpp:355-361: dots become directory separators, plus ".bin"."""
+    return name.replace(".", "/") + ".bin"
+
+
+def write_ane_blobs(st_path, out_dir):
+    """core/safetensors.cpp:345-383: one blob per BF16 tensor.  Returns the count."""
+    n = 0
+    for name, (dt, shape, data) in read_safetensors(st_path).items():
+        if dt != "BF16":
+            continue
+        p = os.path.join(out_dir, blob_relpath(name))
+        os.makedirs(os.path.dirname(p), exist_ok=True)
+        with open(p, "wb") as f:
+            f.write(ane_blob(data))
+        n += 1
+    return n
