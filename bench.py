@@ -380,6 +380,66 @@ def cpu_attention(w, target_s):
                 sample=f"{done} single-sequence calls (capacity {cap}, full ring) on {oracle.max_threads()} threads")
 
 
+def qwen3_06b_tensors():
+    """Tensor names and shapes of a Qwen3-0.6B checkpoint (tied LM head)."""
+    H, I, L = 1024, 3072, 28
+    t = {"model.embed_tokens.weight": (VOCAB, H), "model.norm.weight": (H,)}
+    for l in range(L):
+        p = f"model.layers.{l}."
+        t.update({p + "self_attn.q_proj.weight": (2048, H), p + "self_attn.k_proj.weight": (1024, H),
+                  p + "self_attn.v_proj.weight": (1024, H), p + "self_attn.o_proj.weight": (H, 2048),
+                  p + "self_attn.q_norm.weight": (D,), p + "self_attn.k_norm.weight": (D,),
+                  p + "mlp.gate_proj.weight": (I, H), p + "mlp.up_proj.weight": (I, H),
+                  p + "mlp.down_proj.weight": (H, I), p + "input_layernorm.weight": (H,),
+                  p + "post_attention_layernorm.weight": (H,)})
+    return t
+
+
+def make_blob_checkpoint(path):
+    """A synthetic bf16 safetensors file of Qwen3-0.6B shapes (~1.2 GB)."""
+    import torch
+    from safetensors.torch import save_file
+
+    g = torch.Generator().manual_seed(13)
+    ts = {n: (0.02 * torch.randn(*s, generator=g)).bfloat16() for n, s in qwen3_06b_tensors().items()}
+    save_file(ts, path)
+    return sum(t.numel() for t in ts.values())
+
+
+def measure_blobs(hip, workdir, reps=2):
+    """The `convert` command (core/safetensors.cpp:345-383) on a Qwen3-0.6B-shaped
+    checkpoint: parse, convert on the GPU, write every blob; wall clock
+    including the file writes (best of reps)."""
+    import shutil
+
+    src = os.path.join(workdir, "qwen3-0.6b-shaped.safetensors")
+    n = make_blob_checkpoint(src)
+    best = None
+    for r in range(reps):
+        out = os.path.join(workdir, f"blobs{r}")
+        t0 = time.perf_counter()
+        k = hip.write_ane_blobs(src, out)
+        el = time.perf_counter() - t0
+        best = el if best is None else min(best, el)
+        shutil.rmtree(out, ignore_errors=True)
+    return src, dict(seconds=round(best, 3), params=n, blobs=k, params_per_s=round(n / best, 1),
+                     GBps_in_out=round(4 * n / best / 1e9, 2),
+                     note="wall clock of anelm_write_ane_blobs incl. page-cache reads and file writes")
+
+
+def cpu_blobs(src, workdir):
+    import shutil
+
+    oracle = _oracle()
+    out = os.path.join(workdir, "blobs_cpu")
+    t0 = time.perf_counter()
+    k = oracle.write_ane_blobs(src, out)
+    el = time.perf_counter() - t0
+    shutil.rmtree(out, ignore_errors=True)
+    return dict(seconds=round(el, 3), blobs=k, cores=oracle.max_threads(), kind="port",
+                sample="the oracle's write_ane_blobs (numpy reader, C convert) on the same file")
+
+
 # ------------------------------------------------------------------ CPU baseline
 
 def _oracle():
@@ -639,6 +699,13 @@ def main():
             r = measure_sampler(anelm, max(args.steps, 20))
         elif args.only == "convert-qwen3-8b-bf16":
             r = measure_convert(anelm)
+        elif args.only == "blobs-qwen3-0.6b":
+            import tempfile
+
+            with tempfile.TemporaryDirectory() as wd:
+                src, r = measure_blobs(anelm, wd)
+                if not args.no_cpu:
+                    r["cpu"] = cpu_blobs(src, wd)
         else:
             r = measure_chain(WORKLOADS[args.only], args.steps, args.warmup, per_op=True)
         print(json.dumps({args.only: r}))
@@ -655,6 +722,7 @@ def main():
                 traffic_source=f"profiles/pmc_traffic_{args.workload}.txt (FETCH_SIZE, WRITE_SIZE per dispatch, "
                                f"copy-calibrated)")
     configs = {}
+    cpu_configs = {}
     if not args.headline_only:
         for name, wl in WORKLOADS.items():
             if name != args.workload:
@@ -664,9 +732,14 @@ def main():
             configs[name] = measure_attention(anelm, aw, max(args.steps, 20))
         for name, dw in DN_WORKLOADS.items():
             configs[name] = measure_deltanet(anelm, dw, max(args.steps, 20))
+        import tempfile
+
+        with tempfile.TemporaryDirectory() as wd:
+            src, configs["blobs-qwen3-0.6b"] = measure_blobs(anelm, wd)
+            if not args.no_cpu:
+                cpu_configs["blobs-qwen3-0.6b"] = cpu_blobs(src, wd)
         configs["convert-qwen3-8b-bf16"] = measure_convert(anelm)
     cpu = None
-    cpu_configs = {}
     if not args.no_cpu:
         cpu = cpu_chain(w, args.cpu_seconds)
         if not args.headline_only:
