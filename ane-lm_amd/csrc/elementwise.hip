@@ -13,7 +13,7 @@
 
 namespace anelm {
 
-constexpr int kU_add = 4;   // residual add
+constexpr int kU_add = 1;   // residual add
 constexpr int kU_silu = 1;  // SwiGLU
 constexpr int kU_cvt = 2;   // bf16 -> fp16
 

@@ -129,8 +129,9 @@ static int launch_rmsnorm_dt(float* out, float* x, const float* y, const void* w
                      (!ADD || ((ld_y % 4 == 0) && aligned16(y)));
     const int nvec = dim / 4;  // float4 per row
     if (vec && nvec <= 1024 * 4) {
-        // two float4 per lane where the row allows it, at most 16 waves
-        int nv = nvec <= 1024 * 2 ? (nvec <= 64 ? 1 : 2) : 4;
+        // two float4 per lane where the row allows it, at most 16 waves;
+        // one per lane for few rows (decode), where more lanes per row win
+        int nv = nvec <= 1024 * 2 ? (nvec <= 64 || (rows < 256 && nvec <= 1024) ? 1 : 2) : 4;
         int threads = ((nvec + nv - 1) / nv + 63) / 64 * 64;
         const dim3 grd((unsigned)rows);
         if (nv == 1)
@@ -172,75 +173,101 @@ static int launch_rmsnorm(float* out, float* x, const float* y, const void* w, i
 // one lane and the sum of squares is a 16-lane shuffle reduction.  A head is
 // read once and written once (non-temporal); its token's cos/sin row and
 // the gammas are shared by all heads and come from cache.
-template <int DT>
+//
+// HPG heads per group: group g of G handles heads g, g+G, ..., so each round
+// of the grid covers consecutive heads; all loads of the HPG heads (heads,
+// then positions, then the table rows that depend on them) are issued before
+// the first is used, which matters when a launch is only a few rounds deep.
+template <int DT, int HPG>
 __global__ __launch_bounds__(256) void qknorm_rope128_kernel(
     float* q, float* k, long q_ld, long k_ld, const void* wq, const void* wk, const int32_t* pos,
     const float* cos_tab, const float* sin_tab, int tab_len, const InvFreq inv, long T, int nq,
     int nk, float eps) {
-    const long gh = ((long)blockIdx.x * 256 + threadIdx.x) >> 4;
+    const uint32_t nqh = (uint32_t)T * (uint32_t)nq;            // heads < 2^31 (checked on the host)
+    const uint32_t heads = nqh + (uint32_t)T * (uint32_t)nk;
+    const uint32_t G = gridDim.x * 16u;
+    const uint32_t g = blockIdx.x * 16u + (threadIdx.x >> 4);
     const int j0 = 4 * (threadIdx.x & 15);
-    const long nqh = T * nq;
-    if (gh >= nqh + T * nk) return;
-    const bool isq = gh < nqh;
-    long t;
-    float* v;
-    if (isq) {
-        t = gh / nq;
-        v = q + t * q_ld + (gh - t * nq) * 128;
-    } else {
-        const long g2 = gh - nqh;
-        t = g2 / nk;
-        v = k + t * k_ld + (g2 - t * nk) * 128;
+    float* v[HPG];
+    float4 lo[HPG], hi[HPG], c[HPG], s[HPG];
+    int p[HPG];
+    bool isq[HPG];
+#pragma unroll
+    for (int i = 0; i < HPG; i++) {
+        const uint32_t gh = g + (uint32_t)i * G;
+        v[i] = nullptr;
+        isq[i] = gh < nqh;
+        lo[i] = hi[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+        p[i] = 0;
+        if (gh < heads) {
+            uint32_t t;
+            if (isq[i]) {
+                t = gh / (uint32_t)nq;
+                v[i] = q + (long)t * q_ld + (long)(gh - t * (uint32_t)nq) * 128;
+            } else {
+                const uint32_t g2 = gh - nqh;
+                t = g2 / (uint32_t)nk;
+                v[i] = k + (long)t * k_ld + (long)(g2 - t * (uint32_t)nk) * 128;
+            }
+            lo[i] = ld_nt(reinterpret_cast<const float4*>(v[i] + j0));
+            hi[i] = ld_nt(reinterpret_cast<const float4*>(v[i] + 64 + j0));
+            p[i] = pos[t];
+        }
     }
-    float4 lo = ld_nt(reinterpret_cast<const float4*>(v + j0));
-    float4 hi = ld_nt(reinterpret_cast<const float4*>(v + 64 + j0));
-    const int p = pos[t];
-    float4 c, s;
-    if (p >= 0 && p < tab_len) {
-        c = *reinterpret_cast<const float4*>(cos_tab + (long)p * 64 + j0);
-        s = *reinterpret_cast<const float4*>(sin_tab + (long)p * 64 + j0);
-    } else {
-        const float pf = (float)p;
-        const float a0 = pf * inv.v[j0], a1 = pf * inv.v[j0 + 1];
-        const float a2 = pf * inv.v[j0 + 2], a3 = pf * inv.v[j0 + 3];
-        c = make_float4(cosf(a0), cosf(a1), cosf(a2), cosf(a3));
-        s = make_float4(sinf(a0), sinf(a1), sinf(a2), sinf(a3));
+#pragma unroll
+    for (int i = 0; i < HPG; i++) {
+        if (p[i] >= 0 && p[i] < tab_len) {
+            c[i] = *reinterpret_cast<const float4*>(cos_tab + (long)p[i] * 64 + j0);
+            s[i] = *reinterpret_cast<const float4*>(sin_tab + (long)p[i] * 64 + j0);
+        } else {
+            const float pf = (float)p[i];
+            const float a0 = pf * inv.v[j0], a1 = pf * inv.v[j0 + 1];
+            const float a2 = pf * inv.v[j0 + 2], a3 = pf * inv.v[j0 + 3];
+            c[i] = make_float4(cosf(a0), cosf(a1), cosf(a2), cosf(a3));
+            s[i] = make_float4(sinf(a0), sinf(a1), sinf(a2), sinf(a3));
+        }
     }
-    float ss = 0.f;
-    ss = fmaf(lo.x, lo.x, ss);
-    ss = fmaf(lo.y, lo.y, ss);
-    ss = fmaf(lo.z, lo.z, ss);
-    ss = fmaf(lo.w, lo.w, ss);
-    ss = fmaf(hi.x, hi.x, ss);
-    ss = fmaf(hi.y, hi.y, ss);
-    ss = fmaf(hi.z, hi.z, ss);
-    ss = fmaf(hi.w, hi.w, ss);
-    ss = group16_sum(ss);
-    const void* w = isq ? wq : wk;
-    if (w) {
-        const float sc = 1.0f / sqrtf(ss / 128.0f + eps);
-        const float4 wl = load_w4<DT>(w, j0);
-        const float4 wh = load_w4<DT>(w, j0 + 64);
-        lo.x = (lo.x * sc) * wl.x;
-        lo.y = (lo.y * sc) * wl.y;
-        lo.z = (lo.z * sc) * wl.z;
-        lo.w = (lo.w * sc) * wl.w;
-        hi.x = (hi.x * sc) * wh.x;
-        hi.y = (hi.y * sc) * wh.y;
-        hi.z = (hi.z * sc) * wh.z;
-        hi.w = (hi.w * sc) * wh.w;
+#pragma unroll
+    for (int i = 0; i < HPG; i++) {
+        float4 l = lo[i], h = hi[i];
+        float ss = 0.f;
+        ss = fmaf(l.x, l.x, ss);
+        ss = fmaf(l.y, l.y, ss);
+        ss = fmaf(l.z, l.z, ss);
+        ss = fmaf(l.w, l.w, ss);
+        ss = fmaf(h.x, h.x, ss);
+        ss = fmaf(h.y, h.y, ss);
+        ss = fmaf(h.z, h.z, ss);
+        ss = fmaf(h.w, h.w, ss);
+        ss = group16_sum(ss);   // every lane takes part (dead heads contribute zeros)
+        const void* w = isq[i] ? wq : wk;
+        if (w) {
+            const float sc = 1.0f / sqrtf(ss / 128.0f + eps);
+            const float4 wl = load_w4<DT>(w, j0);
+            const float4 wh = load_w4<DT>(w, j0 + 64);
+            l.x = (l.x * sc) * wl.x;
+            l.y = (l.y * sc) * wl.y;
+            l.z = (l.z * sc) * wl.z;
+            l.w = (l.w * sc) * wl.w;
+            h.x = (h.x * sc) * wh.x;
+            h.y = (h.y * sc) * wh.y;
+            h.z = (h.z * sc) * wh.z;
+            h.w = (h.w * sc) * wh.w;
+        }
+        if (v[i]) {
+            float4 ol, oh;
+            ol.x = l.x * c[i].x - h.x * s[i].x;
+            ol.y = l.y * c[i].y - h.y * s[i].y;
+            ol.z = l.z * c[i].z - h.z * s[i].z;
+            ol.w = l.w * c[i].w - h.w * s[i].w;
+            oh.x = h.x * c[i].x + l.x * s[i].x;
+            oh.y = h.y * c[i].y + l.y * s[i].y;
+            oh.z = h.z * c[i].z + l.z * s[i].z;
+            oh.w = h.w * c[i].w + l.w * s[i].w;
+            st_nt(reinterpret_cast<float4*>(v[i] + j0), ol);
+            st_nt(reinterpret_cast<float4*>(v[i] + 64 + j0), oh);
+        }
     }
-    float4 ol, oh;
-    ol.x = lo.x * c.x - hi.x * s.x;
-    ol.y = lo.y * c.y - hi.y * s.y;
-    ol.z = lo.z * c.z - hi.z * s.z;
-    ol.w = lo.w * c.w - hi.w * s.w;
-    oh.x = hi.x * c.x + lo.x * s.x;
-    oh.y = hi.y * c.y + lo.y * s.y;
-    oh.z = hi.z * c.z + lo.z * s.z;
-    oh.w = hi.w * c.w + lo.w * s.w;
-    st_nt(reinterpret_cast<float4*>(v + j0), ol);
-    st_nt(reinterpret_cast<float4*>(v + 64 + j0), oh);
 }
 
 // Any even head_dim <= 1024: one wave per (token, head), two passes.
@@ -366,8 +393,11 @@ static int launch_qknorm(float* q, float* k, long q_ld, long k_ld, const void* w
                       (!wq || (DT == ANELM_F32 ? aligned16(wq) : aligned8(wq))) &&
                       (!wk || (DT == ANELM_F32 ? aligned16(wk) : aligned8(wk)));
     if (fast) {
+        // one head per group measured fastest at every shape from T=1 to the
+        // 8B prefill (two or four per group: equal at best, slower at decode)
         const long heads = T * (nq + nk);
-        qknorm_rope128_kernel<DT><<<dim3((unsigned)((heads * 16 + 255) / 256)), dim3(256), 0, st>>>(
+        const unsigned blocks = (unsigned)((heads * 16 + 255) / 256);
+        qknorm_rope128_kernel<DT, 1><<<dim3(blocks), dim3(256), 0, st>>>(
             q, k, q_ld, k_ld, wq, wk, pos, cos_tab, sin_tab, tab_len, inv, T, nq, nk, eps);
     } else {
         const long waves = T * (nq + nk);
@@ -388,7 +418,7 @@ extern "C" int anelm_qknorm_rope(float* q, float* k, long q_ld, long k_ld, const
     if ((nq > 0 && q_ld < (long)nq * head_dim) || (nk > 0 && k_ld < (long)nk * head_dim))
         return fail(ANELM_ERR_INVALID, "anelm_qknorm_rope: token stride too small");
     if (tab_len < 0 || (tab_len > 0 && (!cos_tab || !sin_tab))) return fail(ANELM_ERR_INVALID, "anelm_qknorm_rope: table");
-    if (T * (nq + nk) / 4 + 1 > 0x7FFFFFFFL || T > (1L << 40)) return fail(ANELM_ERR_INVALID, "anelm_qknorm_rope: too large");
+    if (T > (1L << 40) || T * (nq + nk) > 0x7FFFFFFFL) return fail(ANELM_ERR_INVALID, "anelm_qknorm_rope: too large");
     if (w_dtype < ANELM_F32 || w_dtype > ANELM_BF16) return fail(ANELM_ERR_INVALID, "anelm_qknorm_rope: dtype");
     InvFreq inv;
     rope_inv_freq(&inv, head_dim, theta);
