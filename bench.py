@@ -449,11 +449,12 @@ def _oracle():
     return oracle
 
 
-def cpu_chain(w, target_s, max_tokens=512, layers=4):
+def cpu_chain(w, target_s, max_tokens=512, layers=4, threads=None):
     """The oracle's per-token layer chain (looping per token as the reference
-    does) on the host's cores, over a bounded sample: up to max_tokens tokens
-    x `layers` distinct layers of the workload's shapes, repeated for about
-    target_s seconds.  Reported in the GPU figure's unit (algorithmic GB/s)."""
+    does) on the host's cores (or `threads` of them), over a bounded sample:
+    up to max_tokens tokens x `layers` distinct layers of the workload's
+    shapes, repeated for about target_s seconds.  Reported in the GPU
+    figure's unit (algorithmic GB/s)."""
     import numpy as np
 
     oracle = _oracle()
@@ -468,7 +469,7 @@ def cpu_chain(w, target_s, max_tokens=512, layers=4):
     x, xn, h = rn(T, H), np.empty((T, H), np.float32), np.empty((T, I), np.float32)
     pos = (np.arange(T) % w["pmax"]).astype(np.int32)
     c, s = oracle.rope_table(16384, D, THETA)
-    threads = oracle.max_threads()
+    threads = threads or oracle.max_threads()
     t0 = time.perf_counter()
     passes = 0
     while True:
@@ -543,7 +544,14 @@ def _csv_rows(d, suffix):
 ATTN_KERNELS = {"gqa_decode": ("gqa_decode_kernel", ""), "gqa_combine": ("gqa_combine_kernel", "")}
 
 
+SAMPLE_KERNELS = {"stage1": ("sample_stage1_kernel", ""), "stage2": ("sample_stage2_kernel", ""),
+                  "stage3": ("sample_stage3_kernel", ""), "walk": ("sample_walk_kernel", "")}
+SAMPLER = "sampling-64x151936"
+
+
 def _kernels_of(workload):
+    if workload == SAMPLER:
+        return SAMPLE_KERNELS
     return ATTN_KERNELS if workload in ATTN_WORKLOADS else OP_KERNELS
 
 
@@ -576,9 +584,14 @@ def pmc_summary(fetch_dir, write_dir, copy_fetch_dir, copy_write_dir, workload=H
         w = ATTN_WORKLOADS[workload]
         ob = {"gqa_decode": attn_bytes(w), "gqa_combine": 0}
         run_args = f"--only {workload} --steps 1"
+    elif workload == SAMPLER:
+        lv = 64 * VOCAB * 4   # logits read (stages 1, 2), + probabilities written (stage 3)
+        ob = {"stage1": lv, "stage2": lv, "stage3": 2 * lv, "walk": 0}
+        run_args = f"--only {workload} --steps 1"
     else:
         ob = op_bytes(WORKLOADS[workload])
-        run_args = f"--workload {workload} --headline-only --no-cpu --steps 1 --warmup 0"
+        run_args = (f"--workload {workload} --headline-only --no-cpu --steps 1 --warmup 0" if workload == HEADLINE
+                    else f"--only {workload} --steps 1 --warmup 0")
     commands = pmc_commands(fetch_dir, write_dir, copy_fetch_dir, copy_write_dir, run_args)
     lines = [f"# HBM traffic per dispatch, workload {workload} (rocprofv3 --pmc, one counter per run)", "#",
              "# commands (from the repo root):"] + [f"#   {c}" for c in commands] + [
@@ -653,7 +666,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default=HEADLINE, choices=sorted(WORKLOADS) + sorted(ATTN_WORKLOADS),
+    ap.add_argument("--workload", default=HEADLINE, choices=sorted(WORKLOADS) + sorted(ATTN_WORKLOADS) + [SAMPLER],
                     help="op-chain workload to run (attention names only select --pmc-summary kernels)")
     ap.add_argument("--cpu-seconds", type=float, default=8.0, help="CPU time budget of the headline baseline")
     ap.add_argument("--no-cpu", action="store_true")
@@ -742,6 +755,8 @@ def main():
     cpu = None
     if not args.no_cpu:
         cpu = cpu_chain(w, args.cpu_seconds)
+        one = cpu_chain(w, max(2.0, args.cpu_seconds / 4), max_tokens=64, layers=2, threads=1)
+        cpu["single_thread"] = {k: one[k] for k in ("value", "unit", "cores", "us_per_layer_chain", "sample")}
         if not args.headline_only:
             for name, wl in WORKLOADS.items():
                 if name != args.workload:
