@@ -62,6 +62,7 @@ _SIGS = {
     "anelm_bf16_to_f16": (_I, [_P, _P, _S, _P]),
     "anelm_bf16_to_f32": (_I, [_P, _P, _S, _P]),
     "anelm_f16_to_f32": (_I, [_P, _P, _S, _P]),
+    "anelm_f32_to_f16": (_I, [_P, _P, _S, _P]),
     "anelm_softmax_workspace_size": (_S, [_L, _L]),
     "anelm_softmax": (_I, [_P, _L, _L, _L, _P, _S, _P]),
     "anelm_sample_workspace_size": (_S, [_L, _L]),
@@ -86,6 +87,14 @@ _SIGS = {
     "anelm_st_load": (_I, [_P, _L, _P, _I, _P]),
     "anelm_ane_blob_header": (None, [_P, ctypes.c_uint64]),
     "anelm_write_ane_blobs": (_L, [ctypes.c_char_p, ctypes.c_char_p, _P]),
+    "anelm_blas_create": (_P, []),
+    "anelm_blas_destroy": (None, [_P]),
+    "anelm_linear_f16": (_I, [_P, _P, _P, _P, _L, _I, _I, _L, _L, _P]),
+    "anelm_proj_f16": (_I, [_P, _P, _P, _L, _I, _I, _L, _L, _P]),
+    "anelm_qwen3_load": (_P, [ctypes.c_char_p, _P, _I, _I, _P]),
+    "anelm_qwen3_free": (None, [_P]),
+    "anelm_qwen3_reset": (_I, [_P, _P]),
+    "anelm_qwen3_forward": (_I, [_P, _P, _P, _L, _P, _L, _P, _P]),
 }
 
 EXPORTED = tuple(_SIGS)
@@ -229,6 +238,10 @@ def bf16_to_f16(dst, src, stream=None):
 
 def bf16_to_f32(dst, src, stream=None):
     _check(lib().anelm_bf16_to_f32(_ptr(dst), _ptr(src), src.numel(), _stream(stream)))
+
+
+def f32_to_f16(dst, src, stream=None):
+    _check(lib().anelm_f32_to_f16(_ptr(dst), _ptr(src), src.numel(), _stream(stream)))
 
 
 def f16_to_f32(dst, src, stream=None):
@@ -400,3 +413,72 @@ def write_ane_blobs(safetensors_path, output_dir, stream=None) -> int:
     if n < 0:
         raise AnelmError(n, last_error())
     return n
+
+
+class Qwen3Config(ctypes.Structure):
+    _fields_ = [("hidden", ctypes.c_int), ("layers", ctypes.c_int), ("n_q_heads", ctypes.c_int),
+                ("n_kv_heads", ctypes.c_int), ("head_dim", ctypes.c_int), ("intermediate", ctypes.c_int),
+                ("vocab", ctypes.c_int), ("rope_theta", ctypes.c_float), ("rms_eps", ctypes.c_float)]
+
+
+class Blas:
+    """A rocBLAS context for linear_f16."""
+
+    def __init__(self):
+        self._h = lib().anelm_blas_create()
+        if not self._h:
+            raise AnelmError(ERR_HIP, last_error())
+
+    def linear_f16(self, y16, x16, w16, stream=None):
+        """y16 [B, out] = fp16(x16 [B, in] . w16 [out, in]^T)."""
+        batch, in_dim = x16.shape
+        out_dim = w16.shape[0]
+        _check(lib().anelm_linear_f16(self._h, _ptr(y16), _ptr(x16), _ptr(w16), batch, out_dim, in_dim, _ld(x16),
+                                      _ld(y16), _stream(stream)))
+
+    def __del__(self):
+        try:
+            if getattr(self, "_h", None) and _lib is not None:
+                _lib.anelm_blas_destroy(self._h)
+        except Exception:   # interpreter shutdown
+            pass
+        self._h = None
+
+
+def proj_f16(y, x, w16, stream=None):
+    """y [B, out] fp32 = fp16(fp16(x) [B, in] . w16 [out, in]^T), B <= 8."""
+    batch, in_dim = x.shape
+    out_dim = w16.shape[0]
+    _check(lib().anelm_proj_f16(_ptr(y), _ptr(x), _ptr(w16), batch, out_dim, in_dim, _ld(x), _ld(y),
+                                _stream(stream)))
+
+
+class Qwen3Model:
+    """A Qwen3 checkpoint in HBM with per-sequence KV rings (anelm_qwen3_*)."""
+
+    def __init__(self, path, cfg: Qwen3Config, max_batch: int, kv_capacity: int = 2048, stream=None):
+        self.cfg = cfg
+        self._h = lib().anelm_qwen3_load(os.fsencode(path), ctypes.byref(cfg), max_batch, kv_capacity,
+                                         _stream(stream))
+        if not self._h:
+            raise AnelmError(ERR_INVALID, last_error())
+
+    def reset(self, stream=None):
+        _check(lib().anelm_qwen3_reset(self._h, _stream(stream)))
+
+    def forward(self, ids, pos, logits, bad_ids=None, stream=None):
+        _check(lib().anelm_qwen3_forward(self._h, _ptr(ids), _ptr(pos), ids.shape[0], _ptr(logits), _ld(logits),
+                                         _ptr(bad_ids), _stream(stream)))
+
+    def close(self):
+        if getattr(self, "_h", None):
+            lib().anelm_qwen3_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            if getattr(self, "_h", None) and _lib is not None:
+                _lib.anelm_qwen3_free(self._h)
+        except Exception:   # interpreter shutdown
+            pass
+        self._h = None

@@ -31,6 +31,7 @@ SOURCES = [
     os.path.join(CSRC, "deltanet.hip"),
     os.path.join(HOST, "dropin.hip"),
     os.path.join(HOST, "safetensors.hip"),
+    os.path.join(HOST, "qwen3.hip"),
 ]
 
 ARCH = "gfx950"
@@ -82,7 +83,7 @@ def build_lib(jobs: int = 8) -> str:
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
         list(ex.map(_run, cmds))
     tmp = LIB + ".tmp"
-    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs])
+    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs, "-lrocblas"])
     os.replace(tmp, LIB)
     return LIB
 

@@ -147,6 +147,26 @@ __global__ __launch_bounds__(256) void widen_kernel(float* dst, const uint16_t* 
         dst[i] = F16 ? f16_to_f32_exact(src[i]) : bf16_to_f32(src[i]);
 }
 
+// fp32 -> fp16 round to nearest even (the activation conversion at the ANE
+// kernel inputs, core/ane_runtime.cpp:604-612, where arm64's __fp16 cast
+// rounds to nearest even): the hardware conversion, whose mode is RNE.
+__device__ __forceinline__ uint32_t f16_rne(float x) {
+    const _Float16 h = (_Float16)x;
+    return (uint32_t)__builtin_bit_cast(uint16_t, h);
+}
+
+__global__ __launch_bounds__(256) void narrow_vec_kernel(uint2* dst, const float4* src, size_t n4) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (size_t)gridDim.x * 256) {
+        const float4 v = src[i];
+        dst[i] = make_uint2(f16_rne(v.x) | (f16_rne(v.y) << 16), f16_rne(v.z) | (f16_rne(v.w) << 16));
+    }
+}
+
+__global__ __launch_bounds__(256) void narrow_kernel(uint16_t* dst, const float* src, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256)
+        dst[i] = (uint16_t)f16_rne(src[i]);
+}
+
 // ------------------------------------------------------------ gather
 // qwen3.cpp:498: x = E[id].  gridDim.y = ids; each block moves a slice of
 // the row.  A bad id leaves its row unwritten and bumps *bad once.
@@ -288,6 +308,18 @@ extern "C" int anelm_bf16_to_f32(float* dst, const uint16_t* src, size_t n, void
     clear_error();
     widen_kernel<false><<<grid_stride_blocks(n), 256, 0, as_stream(stream)>>>(dst, src, n);
     return launch_status("bf16_to_f32");
+}
+
+extern "C" int anelm_f32_to_f16(uint16_t* dst, const float* src, size_t n, void* stream) {
+    if (!dst || !src) return fail(ANELM_ERR_INVALID, "anelm_f32_to_f16: null pointer");
+    if (n == 0) return fail(ANELM_ERR_INVALID, "anelm_f32_to_f16: n == 0");
+    clear_error();
+    if (n % 4 == 0 && aligned16(src) && aligned8(dst))
+        narrow_vec_kernel<<<grid_stride_blocks(n / 4), 256, 0, as_stream(stream)>>>(
+            reinterpret_cast<uint2*>(dst), reinterpret_cast<const float4*>(src), n / 4);
+    else
+        narrow_kernel<<<grid_stride_blocks(n), 256, 0, as_stream(stream)>>>(dst, src, n);
+    return launch_status("f32_to_f16");
 }
 
 extern "C" int anelm_f16_to_f32(float* dst, const uint16_t* src, size_t n, void* stream) {

@@ -1,0 +1,427 @@
+// Device-resident Qwen3 decode step: the forward glue of
+// models/llm/qwen3.cpp:497-564 with every activation kept in HBM, the
+// library's layer-op kernels between the contractions, and the ANE
+// contractions (core/ane_runtime.cpp:265-408: fused q|k|v, o_proj,
+// gate|up -> down, the LM head) as rocBLAS fp16 GEMMs with fp32
+// accumulation.  The ANE's interface numerics are kept: weights are the
+// truncating fp16 convert of the bf16 checkpoint (the blobs), activations
+// enter a projection as round-to-nearest fp16 and leave it as fp16
+// (core/ane_runtime.cpp:600-640).
+//
+// A step processes one token of each of `batch` sequences; every sequence
+// has its own KV ring per layer (qwen3.cpp:227-231, 475-488).
+#include <hip/hip_runtime.h>
+#include <rocblas/rocblas.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "anelm_common.hpp"
+
+using anelm::fail;
+using anelm::clear_error;
+
+extern "C" int anelm_proj_f16(float* y, const float* x, const uint16_t* w16, long batch, int out_dim, int in_dim,
+                              long ld_x, long ld_y, void* stream);
+
+struct anelm_blas {
+    rocblas_handle h = nullptr;
+};
+
+extern "C" anelm_blas* anelm_blas_create(void) {
+    clear_error();
+    anelm_blas* b = new anelm_blas();
+    if (rocblas_create_handle(&b->h) != rocblas_status_success) {
+        delete b;
+        fail(ANELM_ERR_HIP, "blas_create: rocblas_create_handle failed");
+        return nullptr;
+    }
+    return b;
+}
+
+extern "C" void anelm_blas_destroy(anelm_blas* b) {
+    if (!b) return;
+    if (b->h) rocblas_destroy_handle(b->h);
+    delete b;
+}
+
+// y16 [batch, out_dim] (row stride ld_y) = fp16(x16 [batch, in_dim] (ld_x) . W16^T),
+// W16 [out_dim, in_dim] row-major; fp32 accumulation, one rounding to fp16.
+extern "C" int anelm_linear_f16(anelm_blas* b, uint16_t* y16, const uint16_t* x16, const uint16_t* w16, long batch,
+                                int out_dim, int in_dim, long ld_x, long ld_y, void* stream) {
+    clear_error();
+    if (!b || !y16 || !x16 || !w16) return fail(ANELM_ERR_INVALID, "linear_f16: null pointer");
+    if (batch <= 0 || out_dim <= 0 || in_dim <= 0 || ld_x < in_dim || ld_y < out_dim || batch > 0x7FFFFFFFL ||
+        ld_x > 0x7FFFFFFFL || ld_y > 0x7FFFFFFFL)
+        return fail(ANELM_ERR_INVALID, "linear_f16: bad sizes or strides");
+    if (rocblas_set_stream(b->h, anelm::as_stream(stream)) != rocblas_status_success)
+        return fail(ANELM_ERR_HIP, "linear_f16: rocblas_set_stream failed");
+    const float alpha = 1.0f, beta = 0.0f;
+    // column-major view: Y^T (out x batch) = W (in x out)^T . X^T (in x batch)
+    const rocblas_status st = rocblas_gemm_ex(
+        b->h, rocblas_operation_transpose, rocblas_operation_none, out_dim, (rocblas_int)batch, in_dim, &alpha, w16,
+        rocblas_datatype_f16_r, in_dim, x16, rocblas_datatype_f16_r, (rocblas_int)ld_x, &beta, y16,
+        rocblas_datatype_f16_r, (rocblas_int)ld_y, y16, rocblas_datatype_f16_r, (rocblas_int)ld_y,
+        rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
+    if (st != rocblas_status_success) return fail(ANELM_ERR_HIP, "linear_f16: rocblas_gemm_ex status %d", (int)st);
+    return anelm::launch_status("linear_f16");
+}
+
+namespace {
+template <int BT>
+void launch_proj(float* y, const float* x, const uint16_t* W, int out_dim, int in_dim, long ld_x, long ld_y,
+                 int batch, hipStream_t st);
+}
+
+// fp32 in, fp32 out (holding fp16 values): the whole fp16 projection of
+// anelm_linear_f16 including the conversions, for batch <= 8.
+extern "C" int anelm_proj_f16(float* y, const float* x, const uint16_t* w16, long batch, int out_dim, int in_dim,
+                              long ld_x, long ld_y, void* stream) {
+    clear_error();
+    if (!y || !x || !w16) return fail(ANELM_ERR_INVALID, "proj_f16: null pointer");
+    if (batch <= 0 || batch > 8 || out_dim <= 0 || in_dim <= 0 || in_dim % 8 || ld_x < in_dim || ld_y < out_dim ||
+        ld_x % 4)
+        return fail(ANELM_ERR_INVALID, "proj_f16: batch 1..8, in_dim a multiple of 8, ld_x a multiple of 4");
+    if (!anelm::aligned16(x) || !anelm::aligned16(w16)) return fail(ANELM_ERR_INVALID, "proj_f16: alignment");
+    hipStream_t st = anelm::as_stream(stream);
+    const int b = (int)batch;
+    if (b == 1) launch_proj<1>(y, x, w16, out_dim, in_dim, ld_x, ld_y, b, st);
+    else if (b == 2) launch_proj<2>(y, x, w16, out_dim, in_dim, ld_x, ld_y, b, st);
+    else if (b <= 4) launch_proj<4>(y, x, w16, out_dim, in_dim, ld_x, ld_y, b, st);
+    else launch_proj<8>(y, x, w16, out_dim, in_dim, ld_x, ld_y, b, st);
+    return anelm::launch_status("proj_f16");
+}
+
+namespace {
+
+// ---- small-batch projection ------------------------------------------------
+// y[b, o] = fp16(sum_i fp16(x[b, i]) * W16[o, i]) for batch <= 8, written as
+// fp32: the input rounding, fp32 accumulation and output rounding of the
+// fp16 path in one kernel, reading each weight once.  One wave per output
+// row; lanes cover 512 consecutive inputs per chunk (8 halves, one 16-byte
+// load each), and the weight loads of up to 8 chunks are issued before the
+// first is used, so a row of up to 4096 inputs is in flight at once.  The
+// inputs x are tiny and shared by every row: they come from cache.
+__device__ __forceinline__ float r16(float v) { return (float)(_Float16)v; }
+
+template <int BT>
+__global__ __launch_bounds__(256) void proj_f16_kernel(float* y, const float* x, const uint16_t* W, int out_dim,
+                                                       int in_dim, long ld_x, long ld_y, int batch) {
+    constexpr int NC = 8;   // chunks of 512 inputs in flight
+    const int lane = threadIdx.x & 63;
+    const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= out_dim) return;
+    const uint16_t* wr = W + row * in_dim;
+    float acc[BT];
+#pragma unroll
+    for (int b = 0; b < BT; b++) acc[b] = 0.0f;
+    for (int c0 = 0; c0 < in_dim; c0 += NC * 512) {
+        uint4 wv[NC];
+#pragma unroll
+        for (int k = 0; k < NC; k++) {
+            const int c = c0 + k * 512 + lane * 8;
+            wv[k] = c < in_dim ? anelm::ld_nt(reinterpret_cast<const uint4*>(wr + c)) : make_uint4(0u, 0u, 0u, 0u);
+        }
+#pragma unroll
+        for (int k = 0; k < NC; k++) {
+            const int c = c0 + k * 512 + lane * 8;
+            if (c >= in_dim) break;   // this lane is past the end of the row (inputs are not read there)
+            const uint32_t u[4] = {wv[k].x, wv[k].y, wv[k].z, wv[k].w};
+            float wf[8];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                wf[2 * e] = anelm::f16_to_f32_exact(u[e] & 0xFFFFu);
+                wf[2 * e + 1] = anelm::f16_to_f32_exact(u[e] >> 16);
+            }
+#pragma unroll
+            for (int b = 0; b < BT; b++) {
+                if (b < batch) {
+                    const float4 a = reinterpret_cast<const float4*>(x + b * ld_x + c)[0];
+                    const float4 d = reinterpret_cast<const float4*>(x + b * ld_x + c)[1];
+                    float t = acc[b];
+                    t = fmaf(r16(a.x), wf[0], t);
+                    t = fmaf(r16(a.y), wf[1], t);
+                    t = fmaf(r16(a.z), wf[2], t);
+                    t = fmaf(r16(a.w), wf[3], t);
+                    t = fmaf(r16(d.x), wf[4], t);
+                    t = fmaf(r16(d.y), wf[5], t);
+                    t = fmaf(r16(d.z), wf[6], t);
+                    t = fmaf(r16(d.w), wf[7], t);
+                    acc[b] = t;
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int b = 0; b < BT; b++) {
+        const float s = anelm::wave_sum(acc[b]);
+        if (lane == 0 && b < batch) y[b * ld_y + row] = r16(s);
+    }
+}
+
+template <int BT>
+void launch_proj(float* y, const float* x, const uint16_t* W, int out_dim, int in_dim, long ld_x, long ld_y,
+                 int batch, hipStream_t st) {
+    hipLaunchKernelGGL((proj_f16_kernel<BT>), dim3((unsigned)((out_dim + 3) / 4)), dim3(256), 0, st, y, x, W,
+                       out_dim, in_dim, ld_x, ld_y, batch);
+}
+
+constexpr int kRopeRows = 16384;   // min(max_position_embeddings, 16384), qwen3.cpp:201
+
+struct DevBuf {
+    void* p = nullptr;
+    ~DevBuf() {
+        if (p) hipFree(p);
+    }
+};
+
+}  // namespace
+
+struct anelm_qwen3 {
+    anelm_qwen3_config c{};
+    int max_batch = 0, cap = 0, qdim = 0, kvdim = 0, qkvdim = 0;
+    anelm_blas* blas = nullptr;
+    std::vector<DevBuf*> bufs;   // every device allocation, freed at the end
+    // weights
+    uint16_t* embed = nullptr;       // bf16 [V, H] (widened exactly by the gather)
+    uint16_t* final_norm = nullptr;  // bf16 [H]
+    uint16_t* lm16 = nullptr;        // fp16 [V, H]
+    struct Layer {
+        uint16_t *qkv16, *o16, *gu16, *down16;   // fp16 projections
+        uint16_t *qn, *kn, *w_in, *w_post;       // bf16 gammas
+        float *kc, *vc;                          // [max_batch][cap][kvdim]
+        int32_t *start, *len;                    // [max_batch]
+    };
+    std::vector<Layer> layers;
+    float *cos_tab = nullptr, *sin_tab = nullptr;
+    // activations
+    float *x, *xn, *qkv, *attn, *o, *gu, *h;
+    uint16_t *a16, *y16;
+    void* attn_ws = nullptr;
+    size_t attn_ws_bytes = 0;
+
+    void* alloc(size_t bytes) {
+        DevBuf* d = new DevBuf();
+        if (hipMalloc(&d->p, bytes ? bytes : 16) != hipSuccess) {
+            delete d;
+            return nullptr;
+        }
+        bufs.push_back(d);
+        return d->p;
+    }
+    ~anelm_qwen3() {
+        for (DevBuf* d : bufs) delete d;
+        anelm_blas_destroy(blas);
+    }
+};
+
+namespace {
+
+// tensor `name` of the checkpoint into device memory as dtype, with a shape check
+int load_tensor(anelm_st* st, const char* name, const std::vector<int64_t>& shape, void* dst, int dtype,
+                void* stream) {
+    const long i = anelm_st_find(st, name);
+    if (i < 0) return fail(ANELM_ERR_INVALID, "qwen3_load: tensor %s not found", name);
+    int dt, nd;
+    int64_t sh[8];
+    anelm_st_info(st, i, nullptr, &dt, &nd, sh, nullptr, nullptr);
+    if (dt != ANELM_BF16) return fail(ANELM_ERR_INVALID, "qwen3_load: %s is not BF16", name);
+    bool ok = nd == (int)shape.size();
+    for (int d = 0; ok && d < nd; d++) ok = sh[d] == shape[d];
+    if (!ok) return fail(ANELM_ERR_INVALID, "qwen3_load: %s has an unexpected shape", name);
+    return anelm_st_load(st, i, dst, dtype, stream);
+}
+
+}  // namespace
+
+extern "C" anelm_qwen3* anelm_qwen3_load(const char* path, const anelm_qwen3_config* cfg, int max_batch,
+                                         int kv_capacity, void* stream) {
+    clear_error();
+    if (!path || !cfg || max_batch <= 0 || kv_capacity <= 0) {
+        fail(ANELM_ERR_INVALID, "qwen3_load: bad arguments");
+        return nullptr;
+    }
+    const anelm_qwen3_config& c = *cfg;
+    if (c.hidden <= 0 || c.layers <= 0 || c.n_q_heads <= 0 || c.n_kv_heads <= 0 || c.intermediate <= 0 ||
+        c.vocab <= 0 || (c.head_dim != 64 && c.head_dim != 128 && c.head_dim != 256) ||
+        c.n_q_heads % c.n_kv_heads || c.hidden % 4 || c.intermediate % 4) {
+        fail(ANELM_ERR_INVALID, "qwen3_load: unsupported configuration");
+        return nullptr;
+    }
+    anelm_st* st = anelm_st_open(path);
+    if (!st) return nullptr;
+    anelm_qwen3* m = new anelm_qwen3();
+    m->c = c;
+    m->max_batch = max_batch;
+    m->cap = kv_capacity;
+    const long H = c.hidden, D = c.head_dim, I = c.intermediate, V = c.vocab, B = max_batch;
+    m->qdim = c.n_q_heads * c.head_dim;
+    m->kvdim = c.n_kv_heads * c.head_dim;
+    m->qkvdim = m->qdim + 2 * m->kvdim;
+    int rc = ANELM_OK;
+    auto bail = [&](const char* what) {
+        if (rc == ANELM_OK) rc = fail(ANELM_ERR_HIP, "qwen3_load: %s", what);
+        anelm_st_close(st);
+        delete m;
+        return (anelm_qwen3*)nullptr;
+    };
+    m->blas = anelm_blas_create();
+    if (!m->blas) return bail("blas");
+#define ALLOC(ptr, T, n)                                                   \
+    do {                                                                   \
+        ptr = static_cast<T*>(m->alloc((size_t)(n) * sizeof(T)));          \
+        if (!ptr) return bail("out of device memory");                     \
+    } while (0)
+    ALLOC(m->embed, uint16_t, V * H);
+    ALLOC(m->final_norm, uint16_t, H);
+    ALLOC(m->lm16, uint16_t, V * H);
+    if ((rc = load_tensor(st, "model.embed_tokens.weight", {V, H}, m->embed, ANELM_BF16, stream)) ||
+        (rc = load_tensor(st, "model.norm.weight", {H}, m->final_norm, ANELM_BF16, stream)))
+        return bail("");
+    const bool tied = anelm_st_find(st, "lm_head.weight") < 0;   // qwen3.cpp:259-263, :383
+    if ((rc = load_tensor(st, tied ? "model.embed_tokens.weight" : "lm_head.weight", {V, H}, m->lm16, ANELM_F16,
+                          stream)))
+        return bail("");
+    m->layers.resize(c.layers);
+    char name[256];
+    for (int L = 0; L < c.layers; L++) {
+        anelm_qwen3::Layer& l = m->layers[L];
+        ALLOC(l.qkv16, uint16_t, (long)m->qkvdim * H);
+        ALLOC(l.o16, uint16_t, H * m->qdim);
+        ALLOC(l.gu16, uint16_t, 2 * I * H);
+        ALLOC(l.down16, uint16_t, H * I);
+        ALLOC(l.qn, uint16_t, D);
+        ALLOC(l.kn, uint16_t, D);
+        ALLOC(l.w_in, uint16_t, H);
+        ALLOC(l.w_post, uint16_t, H);
+        ALLOC(l.kc, float, B * m->cap * m->kvdim);
+        ALLOC(l.vc, float, B * m->cap * m->kvdim);
+        ALLOC(l.start, int32_t, B);
+        ALLOC(l.len, int32_t, B);
+        struct Item {
+            const char* n;
+            std::vector<int64_t> shape;
+            void* dst;
+            int dt;
+        } items[] = {
+            {"self_attn.q_proj.weight", {m->qdim, H}, l.qkv16, ANELM_F16},
+            {"self_attn.k_proj.weight", {m->kvdim, H}, l.qkv16 + (long)m->qdim * H, ANELM_F16},
+            {"self_attn.v_proj.weight", {m->kvdim, H}, l.qkv16 + (long)(m->qdim + m->kvdim) * H, ANELM_F16},
+            {"self_attn.o_proj.weight", {H, m->qdim}, l.o16, ANELM_F16},
+            {"self_attn.q_norm.weight", {D}, l.qn, ANELM_BF16},
+            {"self_attn.k_norm.weight", {D}, l.kn, ANELM_BF16},
+            {"mlp.gate_proj.weight", {I, H}, l.gu16, ANELM_F16},
+            {"mlp.up_proj.weight", {I, H}, l.gu16 + I * H, ANELM_F16},
+            {"mlp.down_proj.weight", {H, I}, l.down16, ANELM_F16},
+            {"input_layernorm.weight", {H}, l.w_in, ANELM_BF16},
+            {"post_attention_layernorm.weight", {H}, l.w_post, ANELM_BF16},
+        };
+        for (const Item& it : items) {
+            snprintf(name, sizeof(name), "model.layers.%d.%s", L, it.n);
+            if ((rc = load_tensor(st, name, it.shape, it.dst, it.dt, stream))) return bail("");
+        }
+    }
+    anelm_st_close(st);
+    st = nullptr;
+    ALLOC(m->cos_tab, float, (long)kRopeRows * (D / 2));
+    ALLOC(m->sin_tab, float, (long)kRopeRows * (D / 2));
+    const long amax = std::max({H, (long)m->qdim, I});
+    ALLOC(m->x, float, B * H);
+    ALLOC(m->xn, float, B * H);
+    ALLOC(m->qkv, float, B * m->qkvdim);
+    ALLOC(m->attn, float, B * m->qdim);
+    ALLOC(m->o, float, B * H);
+    ALLOC(m->gu, float, B * 2 * I);
+    ALLOC(m->h, float, B * I);
+    ALLOC(m->a16, uint16_t, B * amax);
+    ALLOC(m->y16, uint16_t, B * std::max({(long)m->qkvdim, 2 * I, H, V}));
+#undef ALLOC
+    m->attn_ws_bytes = anelm_gqa_workspace_size(B, c.n_q_heads, c.n_kv_heads, c.head_dim, m->cap);
+    if (m->attn_ws_bytes && !(m->attn_ws = m->alloc(m->attn_ws_bytes))) {
+        rc = fail(ANELM_ERR_HIP, "qwen3_load: out of device memory");
+        delete m;
+        return nullptr;
+    }
+    if ((rc = anelm_rope_table(m->cos_tab, m->sin_tab, kRopeRows, c.head_dim, c.rope_theta, stream)) ||
+        (rc = anelm_qwen3_reset(m, stream))) {
+        delete m;
+        return nullptr;
+    }
+    if (hipStreamSynchronize(anelm::as_stream(stream)) != hipSuccess) {
+        fail(ANELM_ERR_HIP, "qwen3_load: synchronisation failed");
+        delete m;
+        return nullptr;
+    }
+    return m;
+}
+
+extern "C" void anelm_qwen3_free(anelm_qwen3* m) { delete m; }
+
+extern "C" int anelm_qwen3_reset(anelm_qwen3* m, void* stream) {
+    clear_error();
+    if (!m) return fail(ANELM_ERR_INVALID, "qwen3_reset: null model");
+    for (auto& l : m->layers) {
+        if (hipMemsetAsync(l.start, 0, sizeof(int32_t) * m->max_batch, anelm::as_stream(stream)) != hipSuccess ||
+            hipMemsetAsync(l.len, 0, sizeof(int32_t) * m->max_batch, anelm::as_stream(stream)) != hipSuccess)
+            return fail(ANELM_ERR_HIP, "qwen3_reset: hipMemsetAsync failed");
+    }
+    return ANELM_OK;
+}
+
+// models/llm/qwen3.cpp:497-564 for `batch` sequences, one token each.
+extern "C" int anelm_qwen3_forward(anelm_qwen3* m, const int32_t* ids, const int32_t* pos, long batch,
+                                   float* logits, long ld_logits, int32_t* bad_ids, void* stream) {
+    clear_error();
+    if (!m || !ids || !pos || !logits) return fail(ANELM_ERR_INVALID, "qwen3_forward: null pointer");
+    const anelm_qwen3_config& c = m->c;
+    if (batch <= 0 || batch > m->max_batch || ld_logits < c.vocab)
+        return fail(ANELM_ERR_INVALID, "qwen3_forward: batch %ld (max %d) or ld_logits", batch, m->max_batch);
+    const long H = c.hidden, I = c.intermediate, V = c.vocab, B = batch;
+    const int D = c.head_dim;
+    const long seq = (long)m->cap * m->kvdim;
+    int rc;
+#define CK(call)                      \
+    do {                              \
+        if ((rc = (call)) != ANELM_OK) return rc; \
+    } while (0)
+    // x16 = RNE fp16 of the [B, n] fp32 input; y16 = the projection; out = widened y16
+    auto project = [&](float* out, long ld_out, const float* in, long n_in, const uint16_t* w16, long n_out) -> int {
+        int r;
+        if (B <= 8) return anelm_proj_f16(out, in, w16, B, (int)n_out, (int)n_in, n_in, ld_out, stream);
+        if ((r = anelm_f32_to_f16(m->a16, in, (size_t)(B * n_in), stream))) return r;
+        if ((r = anelm_linear_f16(m->blas, m->y16, m->a16, w16, B, (int)n_out, (int)n_in, n_in, n_out, stream)))
+            return r;
+        if (ld_out == n_out) return anelm_f16_to_f32(out, m->y16, (size_t)(B * n_out), stream);
+        for (long b = 0; b < B; b++)   // strided destination (the caller's logits rows)
+            if ((r = anelm_f16_to_f32(out + b * ld_out, m->y16 + b * n_out, (size_t)n_out, stream))) return r;
+        return ANELM_OK;
+    };
+    CK(anelm_embed_gather(m->x, m->embed, ANELM_BF16, ids, B, H, V, bad_ids, stream));             // :498
+    for (int L = 0; L < c.layers; L++) {
+        const anelm_qwen3::Layer& l = m->layers[L];
+        CK(anelm_rmsnorm(m->xn, m->x, l.w_in, ANELM_BF16, B, (int)H, H, H, c.rms_eps, stream));    // :503
+        CK(project(m->qkv, m->qkvdim, m->xn, H, l.qkv16, m->qkvdim));                             // first_proj
+        CK(anelm_qknorm_rope(m->qkv, m->qkv + m->qdim, m->qkvdim, m->qkvdim, l.qn, l.kn, ANELM_BF16, pos,
+                             m->cos_tab, m->sin_tab, kRopeRows, c.rope_theta, B, c.n_q_heads, c.n_kv_heads, D,
+                             c.rms_eps, stream));                                                 // :444-472
+        CK(anelm_kv_ring_append(l.kc, l.vc, l.start, l.len, m->qkv + m->qdim, m->qkv + m->qdim + m->kvdim,
+                                m->qkvdim, m->qkvdim, B, c.n_kv_heads, D, m->cap, seq, stream));  // :475-488
+        CK(anelm_gqa_attention(m->attn, m->qkv, l.kc, l.vc, l.start, l.len, B, c.n_q_heads, c.n_kv_heads, D,
+                               m->qkvdim, D, m->qdim, m->cap, seq, m->attn_ws, m->attn_ws_bytes, stream));  // :490
+        CK(project(m->o, H, m->attn, m->qdim, l.o16, H));                                         // o_proj
+        CK(anelm_add_rmsnorm(m->x, m->o, m->xn, l.w_post, ANELM_BF16, B, (int)H, H, H, H, c.rms_eps,
+                             stream));                                                            // :516-518
+        CK(project(m->gu, 2 * I, m->xn, H, l.gu16, 2 * I));                                       // fused_ffn: gate|up
+        CK(anelm_silu_mul(m->h, m->gu, m->gu + I, B, I, I, 2 * I, 2 * I, stream));
+        CK(project(m->o, H, m->h, I, l.down16, H));                                               // fused_ffn: down
+        CK(anelm_residual_add(m->x, m->o, (size_t)(B * H), stream));                             // :527
+    }
+    CK(anelm_rmsnorm(m->x, m->x, m->final_norm, ANELM_BF16, B, (int)H, H, H, c.rms_eps, stream));  // :530
+    CK(project(logits, ld_logits, m->x, H, m->lm16, V));                                          // LM head
+#undef CK
+    return ANELM_OK;
+}

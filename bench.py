@@ -427,6 +427,76 @@ def measure_blobs(hip, workdir, reps=2):
                      note="wall clock of anelm_write_ane_blobs incl. page-cache reads and file writes")
 
 
+Q3_WORKLOADS = {
+    # one decode step of a Qwen3-0.6B-shaped model (random weights) for B
+    # sequences: every layer op, the attention over 2048-row rings and the
+    # fp16 projections (the reference's ANE contractions) with the LM head
+    "qwen3-0.6b-decode-step-b1": dict(B=1),
+    "qwen3-0.6b-decode-step-b64": dict(B=64),
+}
+Q3_06B = dict(hidden=1024, layers=28, n_q_heads=16, n_kv_heads=8, head_dim=D, intermediate=3072, vocab=VOCAB)
+
+
+def q3_weight_bytes():
+    """fp16 projection and LM-head bytes one step reads (the norms and the
+    gathered embedding rows are negligible)."""
+    c = Q3_06B
+    per_layer = ((c["n_q_heads"] + 2 * c["n_kv_heads"]) * D * c["hidden"] + c["hidden"] * c["n_q_heads"] * D +
+                 3 * c["intermediate"] * c["hidden"])
+    return 2 * (c["layers"] * per_layer + c["vocab"] * c["hidden"])
+
+
+def measure_qwen3(hip, src, w, steps=30):
+    """Graph-replayed decode steps (positions advance inside the graph) from
+    empty rings; tokens/s = B x steps / time."""
+    import torch
+
+    B = w["B"]
+    cfg = hip.Qwen3Config(*[Q3_06B[k] for k in ("hidden", "layers", "n_q_heads", "n_kv_heads", "head_dim",
+                                                 "intermediate", "vocab")], THETA, EPS)
+    model = hip.Qwen3Model(src, cfg, max_batch=B, kv_capacity=2048)
+    g = torch.Generator(device="cuda").manual_seed(17)
+    ids = torch.randint(0, VOCAB, (B,), generator=g, device="cuda", dtype=torch.int32)
+    pos = torch.zeros(B, dtype=torch.int32, device="cuda")
+    logits = torch.empty(B, VOCAB, device="cuda")
+
+    def step():
+        model.forward(ids, pos, logits)
+        pos.add_(1)
+    step()
+    gr = capture(step)
+    for _ in range(3):
+        gr.replay()
+    ms = time_region(gr.replay, steps)
+    byt = q3_weight_bytes()
+    del gr
+    model.close()
+    torch.cuda.empty_cache()
+    return dict(ms_per_step=round(ms, 4), tokens_per_s=round(B / (ms / 1e3), 1),
+                weight_GBps=round(byt / ms / 1e6, 1), weight_frac=round(byt / ms / 1e6 / HBM_PEAK_GBPS, 4),
+                weight_bytes=byt, steps=steps,
+                note="decode steps from empty 2048-row rings; weight_GBps = fp16 projection + LM-head bytes / step time")
+
+
+def cpu_qwen3(src, steps=2):
+    """The oracle's decode step (one sequence) on the same checkpoint."""
+    oracle = _oracle()
+    t = {k: v[2] for k, v in oracle.read_safetensors(src).items()}
+    c = Q3_06B
+    cfg = oracle.Qwen3Config(c["hidden"], c["layers"], c["n_q_heads"], c["n_kv_heads"], c["head_dim"],
+                             c["intermediate"], c["vocab"], THETA, EPS)
+    m = oracle.Qwen3(cfg, t, 1, 2048)
+    import numpy as np
+
+    m.forward(np.array([1], np.int32), np.array([0], np.int32))
+    t0 = time.perf_counter()
+    for s in range(steps):
+        m.forward(np.array([7 + s], np.int32), np.array([1 + s], np.int32))
+    el = (time.perf_counter() - t0) / steps
+    return dict(ms_per_step=round(el * 1e3, 1), tokens_per_s=round(1 / el, 2), cores=oracle.max_threads(),
+                kind="port", sample=f"{steps} single-sequence steps of the oracle's decode step (fp64 projections)")
+
+
 def cpu_blobs(src, workdir):
     import shutil
 
@@ -712,6 +782,15 @@ def main():
             r = measure_sampler(anelm, max(args.steps, 20))
         elif args.only == "convert-qwen3-8b-bf16":
             r = measure_convert(anelm)
+        elif args.only in Q3_WORKLOADS:
+            import tempfile
+
+            with tempfile.TemporaryDirectory() as wd:
+                src = os.path.join(wd, "qwen3-0.6b-shaped.safetensors")
+                make_blob_checkpoint(src)
+                r = measure_qwen3(anelm, src, Q3_WORKLOADS[args.only])
+                if not args.no_cpu:
+                    r["cpu"] = cpu_qwen3(src)
         elif args.only == "blobs-qwen3-0.6b":
             import tempfile
 
@@ -751,6 +830,10 @@ def main():
             src, configs["blobs-qwen3-0.6b"] = measure_blobs(anelm, wd)
             if not args.no_cpu:
                 cpu_configs["blobs-qwen3-0.6b"] = cpu_blobs(src, wd)
+            for name, qw in Q3_WORKLOADS.items():
+                configs[name] = measure_qwen3(anelm, src, qw)
+            if not args.no_cpu:
+                cpu_configs["qwen3-0.6b-decode-step"] = cpu_qwen3(src)
         configs["convert-qwen3-8b-bf16"] = measure_convert(anelm)
     cpu = None
     if not args.no_cpu:

@@ -145,6 +145,9 @@ int anelm_bf16_to_f16(uint16_t* dst, const uint16_t* src, size_t n, void* stream
 int anelm_bf16_to_f32(float* dst, const uint16_t* src, size_t n, void* stream);
 /* fp16 -> fp32 exact widening (f16_to_f32, common.h:35-56). */
 int anelm_f16_to_f32(float* dst, const uint16_t* src, size_t n, void* stream);
+/* fp32 -> fp16 rounded to nearest even: the activation conversion at the ANE
+ * kernel inputs (core/ane_runtime.cpp:604-612, arm64 __fp16). */
+int anelm_f32_to_f16(uint16_t* dst, const float* src, size_t n, void* stream);
 
 /* ---------------------------------------------------- softmax / sampling */
 
@@ -318,6 +321,51 @@ void anelm_ane_blob_header(uint8_t* header128, uint64_t num_elements);
  * header + truncating fp16 data (converted on the GPU), directories created
  * as needed.  Returns the number of blobs written or a negative status. */
 long anelm_write_ane_blobs(const char* safetensors_path, const char* output_dir, void* stream);
+
+/* ------------------------------ contractions and the device-resident step */
+
+/* A rocBLAS handle for the projections (host object; creating it allocates). */
+typedef struct anelm_blas anelm_blas;
+anelm_blas* anelm_blas_create(void);
+void anelm_blas_destroy(anelm_blas* blas);
+/* One ANE projection for `batch` rows (the conv-as-matvec kernels of
+ * core/ane_runtime.cpp:265-408 with ane_matvec's fp16 interface, :600-640):
+ * y16[b, o] = fp16(sum_i x16[b, i] * W16[o, i]), W16 [out_dim, in_dim]
+ * row-major fp16, fp32 accumulation, one rounding to nearest. */
+int anelm_linear_f16(anelm_blas* blas, uint16_t* y16, const uint16_t* x16, const uint16_t* w16, long batch,
+                     int out_dim, int in_dim, long ld_x, long ld_y, void* stream);
+
+/* The same projection with the conversions fused, for batch <= 8 (decode):
+ * y[b, o] = fp16(sum_i fp16_rne(x[b, i]) * W16[o, i]) stored as fp32, x fp32;
+ * each weight is read once.  in_dim a multiple of 8, ld_x a multiple of 4,
+ * x and W16 16-byte aligned. */
+int anelm_proj_f16(float* y, const float* x, const uint16_t* w16, long batch, int out_dim, int in_dim, long ld_x,
+                   long ld_y, void* stream);
+
+/* Qwen3 model shape (the config.json fields of models/llm/qwen3.cpp:55-80). */
+typedef struct anelm_qwen3_config {
+    int hidden, layers, n_q_heads, n_kv_heads, head_dim, intermediate, vocab;
+    float rope_theta, rms_eps;
+} anelm_qwen3_config;
+/* A Qwen3 checkpoint loaded into HBM for device-resident decoding
+ * (models/llm/qwen3.cpp:150-300): projections as the truncating fp16 convert
+ * (the reference's ANE blobs), the embedding and norms as bf16 (widened
+ * exactly on use), the LM head from lm_head.weight or, when absent, the tied
+ * embedding; per layer a KV ring of kv_capacity rows for each of max_batch
+ * sequences.  Host object; loading allocates and synchronises `stream`. */
+typedef struct anelm_qwen3 anelm_qwen3;
+anelm_qwen3* anelm_qwen3_load(const char* safetensors_path, const anelm_qwen3_config* cfg, int max_batch,
+                              int kv_capacity, void* stream);
+void anelm_qwen3_free(anelm_qwen3* model);
+/* Empties every KV ring (not for graph capture: it records memsets). */
+int anelm_qwen3_reset(anelm_qwen3* model, void* stream);
+/* One decode step (Qwen3Model::forward, models/llm/qwen3.cpp:497-564) for
+ * `batch` sequences: token ids[b] at position pos[b] (device int32) appended
+ * to sequence b's rings; logits [batch, ld_logits] fp32 (device) receive the
+ * LM head's fp16 outputs widened.  Asynchronous on `stream`; bad ids are
+ * counted in *bad_ids (device, may be NULL) and leave their rows unset. */
+int anelm_qwen3_forward(anelm_qwen3* model, const int32_t* ids, const int32_t* pos, long batch, float* logits,
+                        long ld_logits, int32_t* bad_ids, void* stream);
 
 #ifdef __cplusplus
 }

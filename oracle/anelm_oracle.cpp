@@ -429,6 +429,161 @@ extern "C" void orc_matvec(float* y, const float* W, const float* x, int out_dim
     }
 }
 
+// ------------------------------------------- ANE contractions, Qwen3 decode step
+
+// Round-to-nearest-even fp32 -> fp16 (IEEE 754 binary16), in integers.
+extern "C" uint16_t orc_f32_to_f16_rne(float f) {
+    uint32_t x;
+    std::memcpy(&x, &f, 4);
+    const uint32_t sign = (x >> 16) & 0x8000u;
+    const uint32_t ax = x & 0x7FFFFFFFu;
+    if (ax > 0x7F800000u) return (uint16_t)(sign | 0x7E00u | ((ax >> 13) & 0x3FFu));  // NaN, quiet
+    if (ax >= 0x477FF000u) return (uint16_t)(sign | 0x7C00u);                           // rounds to >= 2^16: Inf
+    if (ax < 0x38800000u) {                                  // below 2^-14: fp16 subnormal or zero
+        if (ax < 0x33000000u) return (uint16_t)sign;         // below 2^-25: rounds to zero (tie -> even 0)
+        const uint32_t m = (ax & 0x7FFFFFu) | 0x800000u;
+        const int e = (int)(ax >> 23);                       // value = m * 2^(e-150)
+        const int sh = 126 - e;                              // m >> sh = value / 2^-24
+        uint32_t q = m >> sh;
+        const uint32_t rem = m & ((1u << sh) - 1u), half = 1u << (sh - 1);
+        if (rem > half || (rem == half && (q & 1u))) q++;
+        return (uint16_t)(sign | q);
+    }
+    uint32_t h = ((ax >> 13) - (112u << 10));                // rebias exponent, keep 10 mantissa bits
+    const uint32_t rem = ax & 0x1FFFu;
+    if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h++;
+    return (uint16_t)(sign | h);
+}
+
+extern "C" void orc_linear_f16(uint16_t* y16, const uint16_t* x16, const uint16_t* w16, long batch, int out_dim,
+                               int in_dim) {
+    std::vector<double> xd((size_t)in_dim);
+    for (long b = 0; b < batch; b++) {
+        for (int i = 0; i < in_dim; i++) xd[i] = orc_f16_to_f32(x16[(size_t)b * in_dim + i]);
+#pragma omp parallel for schedule(static) if (out_dim >= 256)
+        for (int o = 0; o < out_dim; o++) {
+            const uint16_t* wr = w16 + (size_t)o * in_dim;
+            double acc = 0.0;
+            for (int i = 0; i < in_dim; i++) acc += xd[i] * (double)orc_f16_to_f32(wr[i]);
+            y16[(size_t)b * out_dim + o] = orc_f32_to_f16_rne((float)acc);
+        }
+    }
+}
+
+namespace {
+struct OrcQwen3 {
+    orc_qwen3_config c;
+    int batch, cap, qdim, kvdim, qkvdim;
+    std::vector<float> embed, final_norm, cos_tab, sin_tab;
+    std::vector<uint16_t> lm16;
+    struct Layer {
+        std::vector<uint16_t> qkv16, o16, gu16, down16;
+        std::vector<float> qn, kn, w_in, w_post;
+        std::vector<float> kc, vc;   // [batch][cap][kvdim]
+        std::vector<int> start, len;
+    };
+    std::vector<Layer> layers;
+};
+
+std::vector<float> widen_bf16(const uint16_t* p, size_t n) {
+    std::vector<float> v(n);
+    for (size_t i = 0; i < n; i++) v[i] = orc_bf16_to_f32(p[i]);
+    return v;
+}
+
+std::vector<uint16_t> to_f16(const uint16_t* bf16, size_t n) {
+    std::vector<uint16_t> v(n);
+    orc_bf16_to_f16_vec(v.data(), bf16, n, 0);
+    return v;
+}
+
+// y = fp16 projection of the fp32 vector x (RNE in, fp16 out, widened)
+void project(float* y, const float* x, const uint16_t* w16, int out_dim, int in_dim) {
+    std::vector<uint16_t> x16((size_t)in_dim), y16((size_t)out_dim);
+    for (int i = 0; i < in_dim; i++) x16[i] = orc_f32_to_f16_rne(x[i]);
+    orc_linear_f16(y16.data(), x16.data(), w16, 1, out_dim, in_dim);
+    for (int o = 0; o < out_dim; o++) y[o] = orc_f16_to_f32(y16[o]);
+}
+}  // namespace
+
+extern "C" void* orc_qwen3_create(const orc_qwen3_config* c, int batch, int kv_capacity, const uint16_t* embed,
+                                  const uint16_t* const* lt, const uint16_t* final_norm, const uint16_t* lm_head) {
+    OrcQwen3* m = new OrcQwen3();
+    m->c = *c;
+    m->batch = batch;
+    m->cap = kv_capacity;
+    const int H = c->hidden, D = c->head_dim, I = c->intermediate;
+    m->qdim = c->n_q_heads * D;
+    m->kvdim = c->n_kv_heads * D;
+    m->qkvdim = m->qdim + 2 * m->kvdim;
+    m->embed = widen_bf16(embed, (size_t)c->vocab * H);                          // qwen3.cpp:255-256
+    m->final_norm = widen_bf16(final_norm, (size_t)H);
+    m->lm16 = to_f16(lm_head ? lm_head : embed, (size_t)c->vocab * H);          // tied: qwen3.cpp:259-260, :383
+    const int tab = 16384;                                                       // min(max_pos, 16384), :201
+    m->cos_tab.resize((size_t)tab * (D / 2));
+    m->sin_tab.resize((size_t)tab * (D / 2));
+    orc_rope_table(m->cos_tab.data(), m->sin_tab.data(), tab, D, c->rope_theta);
+    m->layers.resize(c->layers);
+    for (int L = 0; L < c->layers; L++) {
+        const uint16_t* const* t = lt + 11 * L;
+        OrcQwen3::Layer& l = m->layers[L];
+        l.qkv16.resize((size_t)m->qkvdim * H);                                  // fused_3: [q | k | v]
+        orc_bf16_to_f16_vec(l.qkv16.data(), t[0], (size_t)m->qdim * H, 0);
+        orc_bf16_to_f16_vec(l.qkv16.data() + (size_t)m->qdim * H, t[1], (size_t)m->kvdim * H, 0);
+        orc_bf16_to_f16_vec(l.qkv16.data() + (size_t)(m->qdim + m->kvdim) * H, t[2], (size_t)m->kvdim * H, 0);
+        l.o16 = to_f16(t[3], (size_t)H * m->qdim);
+        l.qn = widen_bf16(t[4], (size_t)D);
+        l.kn = widen_bf16(t[5], (size_t)D);
+        l.gu16.resize((size_t)2 * I * H);                                       // fused_ffn: gate, up
+        orc_bf16_to_f16_vec(l.gu16.data(), t[6], (size_t)I * H, 0);
+        orc_bf16_to_f16_vec(l.gu16.data() + (size_t)I * H, t[7], (size_t)I * H, 0);
+        l.down16 = to_f16(t[8], (size_t)H * I);
+        l.w_in = widen_bf16(t[9], (size_t)H);
+        l.w_post = widen_bf16(t[10], (size_t)H);
+        l.kc.assign((size_t)batch * kv_capacity * m->kvdim, 0.0f);
+        l.vc.assign((size_t)batch * kv_capacity * m->kvdim, 0.0f);
+        l.start.assign(batch, 0);
+        l.len.assign(batch, 0);
+    }
+    return m;
+}
+
+// models/llm/qwen3.cpp:497-564 for each sequence b (ids[b] at position pos[b])
+extern "C" void orc_qwen3_forward(void* mp, const int32_t* ids, const int32_t* pos, float* logits) {
+    OrcQwen3* m = static_cast<OrcQwen3*>(mp);
+    const orc_qwen3_config& c = m->c;
+    const int H = c.hidden, D = c.head_dim, I = c.intermediate;
+    std::vector<float> x(H), xn(H), qkv(m->qkvdim), attn(m->qdim), o(H), gu(2 * I), h(I);
+    for (int b = 0; b < m->batch; b++) {
+        std::memcpy(x.data(), m->embed.data() + (size_t)ids[b] * H, (size_t)H * 4);            // :498
+        for (int L = 0; L < c.layers; L++) {
+            OrcQwen3::Layer& l = m->layers[L];
+            orc_rmsnorm(xn.data(), x.data(), l.w_in.data(), H, c.rms_eps);                    // :503
+            project(qkv.data(), xn.data(), l.qkv16.data(), m->qkvdim, H);                     // first_proj
+            orc_qknorm_rope(qkv.data(), qkv.data() + m->qdim, m->qkvdim, m->qkvdim, l.qn.data(), l.kn.data(),
+                            &pos[b], m->cos_tab.data(), m->sin_tab.data(), 16384, c.rope_theta, 1,
+                            c.n_q_heads, c.n_kv_heads, D, c.rms_eps, 1);                      // :444-472
+            float* kc = l.kc.data() + (size_t)b * m->cap * m->kvdim;
+            float* vc = l.vc.data() + (size_t)b * m->cap * m->kvdim;
+            orc_kv_ring_append(kc, vc, qkv.data() + m->qdim, qkv.data() + m->qdim + m->kvdim, m->kvdim,
+                               &l.start[b], &l.len[b], m->cap);                               // :475-488
+            orc_gqa_attention(attn.data(), qkv.data(), kc, vc, c.n_q_heads, c.n_kv_heads, D, D, l.start[b],
+                              l.len[b], m->cap);                                              // :490-492
+            project(o.data(), attn.data(), l.o16.data(), H, m->qdim);                         // o_proj
+            for (int i = 0; i < H; i++) x[i] = x[i] + o[i];                                   // :516
+            orc_rmsnorm(xn.data(), x.data(), l.w_post.data(), H, c.rms_eps);                 // :518
+            project(gu.data(), xn.data(), l.gu16.data(), 2 * I, H);                           // fused_ffn: gate|up
+            orc_silu_mul(h.data(), gu.data(), gu.data() + I, (size_t)I, 1);
+            project(o.data(), h.data(), l.down16.data(), H, I);                               // fused_ffn: down
+            for (int i = 0; i < H; i++) x[i] = x[i] + o[i];                                   // :527
+        }
+        orc_rmsnorm(x.data(), x.data(), m->final_norm.data(), H, c.rms_eps);                 // :530
+        project(logits + (size_t)b * c.vocab, x.data(), m->lm16.data(), c.vocab, H);          // LM head
+    }
+}
+
+extern "C" void orc_qwen3_free(void* m) { delete static_cast<OrcQwen3*>(m); }
+
 // ------------------------------------------------------- KV ring, attention
 
 // models/llm/qwen3.cpp:475-488

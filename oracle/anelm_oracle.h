@@ -174,6 +174,39 @@ void orc_ssm_step(float* y, float* state, const float* q, const float* k, const 
  * each dot correctly rounded.  pinned: identity matrix, fp64 brute force. */
 void orc_matvec(float* y, const float* W, const float* x, int out_dim, int in_dim);
 
+/* ---- device-resident forward: the ANE contractions and a Qwen3 decode step ---- */
+/* fp32 -> fp16 rounded to nearest even (arm64's __fp16 cast at the ANE
+ * inputs, core/ane_runtime.cpp:604-612).  pinned: numpy's float16 cast
+ * (round to nearest even) over every fp16 boundary and random values. */
+uint16_t orc_f32_to_f16_rne(float f);
+/* One ANE projection (core/ane_runtime.cpp:265-290 conv as a matvec, with
+ * ane_matvec's fp16 input and output, :600-640) for `batch` rows:
+ * y16[b,o] = fp16_rne(sum_i x16[b,i] * w16[o,i]) with the sum exact (double
+ * accumulation, rounded once).  W [out_dim, in_dim] fp16 bits.
+ * pinned: float64 matmul of the same fp16 values. */
+void orc_linear_f16(uint16_t* y16, const uint16_t* x16, const uint16_t* w16, long batch, int out_dim,
+                    int in_dim);
+
+/* Qwen3 decode step (models/llm/qwen3.cpp:497-564) for `batch` independent
+ * sequences, each with its own KV rings (capacity kv_capacity, qwen3.cpp:
+ * 227-231), with the reference's ANE projections: weights are the truncating
+ * fp16 convert of the bf16 checkpoint (the blobs), activations enter each
+ * projection as RNE fp16 and leave it as fp16 (q|k|v fused, o_proj,
+ * gate|up, down, LM head); everything else is the oracle functions above
+ * (norms, q/k norm + RoPE with the min(max_pos,16384)-row table, ring,
+ * attention, SiLU*up in fp32, residual adds).  Per layer the tensors are, in
+ * order: q_proj, k_proj, v_proj, o_proj, q_norm, k_norm, gate_proj, up_proj,
+ * down_proj, input_layernorm, post_attention_layernorm (bf16 bits). */
+typedef struct orc_qwen3_config {
+    int hidden, layers, n_q_heads, n_kv_heads, head_dim, intermediate, vocab;
+    float rope_theta, rms_eps;
+} orc_qwen3_config;
+void* orc_qwen3_create(const orc_qwen3_config* c, int batch, int kv_capacity, const uint16_t* embed,
+                       const uint16_t* const* layer_tensors, const uint16_t* final_norm,
+                       const uint16_t* lm_head);
+void orc_qwen3_forward(void* m, const int32_t* ids, const int32_t* pos, float* logits);
+void orc_qwen3_free(void* m);
+
 /* ---- one layer of the fused op chain over T tokens, per token as the
  * reference's forward() runs it (qwen3.cpp:502-528):
  *   (1) xn = rmsnorm(x, w_in)                       :503

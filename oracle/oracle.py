@@ -51,6 +51,11 @@ _SIGS = {
     "orc_conv1d_update": (None, [_P, _P, _P, _P, _P, _I, _I]),
     "orc_ssm_step": (None, [_P, _P, _P, _P, _P, _F, _F, _I, _I]),
     "orc_matvec": (None, [_P, _P, _P, _I, _I]),
+    "orc_f32_to_f16_rne": (_U16, [_F]),
+    "orc_linear_f16": (None, [_P, _P, _P, _L, _I, _I]),
+    "orc_qwen3_create": (_P, [_P, _I, _I, _P, _P, _P, _P]),
+    "orc_qwen3_forward": (None, [_P, _P, _P, _P]),
+    "orc_qwen3_free": (None, [_P]),
     "orc_gqa_attention": (None, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I]),
 }
 
@@ -384,3 +389,65 @@ def write_ane_blobs(st_path, out_dir):
             f.write(ane_blob(data))
         n += 1
     return n
+
+
+# ------------------------------------------------------------ ANE contractions, Qwen3 step
+
+class Qwen3Config(ctypes.Structure):
+    _fields_ = [("hidden", ctypes.c_int), ("layers", ctypes.c_int), ("n_q_heads", ctypes.c_int),
+                ("n_kv_heads", ctypes.c_int), ("head_dim", ctypes.c_int), ("intermediate", ctypes.c_int),
+                ("vocab", ctypes.c_int), ("rope_theta", ctypes.c_float), ("rms_eps", ctypes.c_float)]
+
+
+def f32_to_f16_rne(x: np.ndarray) -> np.ndarray:
+    x = _c(x, np.float32).ravel()
+    f = lib().orc_f32_to_f16_rne
+    return np.array([f(float(v)) for v in x], np.uint16)
+
+
+def linear_f16(x16, w16):
+    """y16 [batch, out] = fp16_rne(x16 @ w16.T) with exact accumulation (fp16 bit arrays)."""
+    x16 = _c(x16, np.uint16)
+    w16 = _c(w16, np.uint16)
+    batch = x16.shape[0] if x16.ndim == 2 else 1
+    out_dim, in_dim = w16.shape
+    y = np.empty((batch, out_dim), np.uint16)
+    lib().orc_linear_f16(_p(y), _p(x16), _p(w16), batch, out_dim, in_dim)
+    return y
+
+
+QWEN3_LAYER_TENSORS = ["self_attn.q_proj.weight", "self_attn.k_proj.weight", "self_attn.v_proj.weight",
+                       "self_attn.o_proj.weight", "self_attn.q_norm.weight", "self_attn.k_norm.weight",
+                       "mlp.gate_proj.weight", "mlp.up_proj.weight", "mlp.down_proj.weight",
+                       "input_layernorm.weight", "post_attention_layernorm.weight"]
+
+
+class Qwen3:
+    """The oracle's Qwen3 decode step over `batch` sequences from a dict of
+    bf16 bit arrays keyed by the checkpoint's tensor names."""
+
+    def __init__(self, cfg: Qwen3Config, tensors: dict, batch: int, kv_capacity: int):
+        self._keep = {k: _c(v, np.uint16) for k, v in tensors.items()}
+        ptrs = []
+        for L in range(cfg.layers):
+            for n in QWEN3_LAYER_TENSORS:
+                ptrs.append(self._keep[f"model.layers.{L}.{n}"].ctypes.data)
+        arr = (ctypes.c_void_p * len(ptrs))(*ptrs)
+        self._arr = arr
+        self.cfg, self.batch = cfg, batch
+        lm = self._keep.get("lm_head.weight")
+        self._h = lib().orc_qwen3_create(ctypes.byref(cfg), batch, kv_capacity,
+                                         _p(self._keep["model.embed_tokens.weight"]), arr,
+                                         _p(self._keep["model.norm.weight"]), _p(lm) if lm is not None else None)
+
+    def forward(self, ids, pos):
+        ids = _c(ids, np.int32)
+        pos = _c(pos, np.int32)
+        out = np.empty((self.batch, self.cfg.vocab), np.float32)
+        lib().orc_qwen3_forward(self._h, _p(ids), _p(pos), _p(out))
+        return out
+
+    def __del__(self):
+        if getattr(self, "_h", None):
+            lib().orc_qwen3_free(self._h)
+            self._h = None

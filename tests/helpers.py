@@ -49,6 +49,48 @@ def attention_fp64(q, kc, vc, nq, nk, D, start, length, qs=None):
     return out, bound
 
 
+# ---------------------------------------------------------------- tiny Qwen3 checkpoints
+
+def bf16(a):
+    """bf16 bits of the truncation of a float32 array (the model-building convention)"""
+    return (np.ascontiguousarray(a, np.float32).view(np.uint32) >> 16).astype(np.uint16)
+
+
+def from_bf16(b):
+    return (b.astype(np.uint32) << 16).view(np.float32)
+
+
+def tiny_qwen3(rng, H=256, L=2, nq=4, nk=2, D=128, I=384, V=300, tied=True):
+    t = {"model.embed_tokens.weight": bf16(0.5 * rng.standard_normal((V, H))),
+         "model.norm.weight": bf16(1 + 0.1 * rng.standard_normal(H))}
+    for l in range(L):
+        p = f"model.layers.{l}."
+        t[p + "self_attn.q_proj.weight"] = bf16(0.06 * rng.standard_normal((nq * D, H)))
+        t[p + "self_attn.k_proj.weight"] = bf16(0.06 * rng.standard_normal((nk * D, H)))
+        t[p + "self_attn.v_proj.weight"] = bf16(0.06 * rng.standard_normal((nk * D, H)))
+        t[p + "self_attn.o_proj.weight"] = bf16(0.06 * rng.standard_normal((H, nq * D)))
+        t[p + "self_attn.q_norm.weight"] = bf16(1 + 0.1 * rng.standard_normal(D))
+        t[p + "self_attn.k_norm.weight"] = bf16(1 + 0.1 * rng.standard_normal(D))
+        t[p + "mlp.gate_proj.weight"] = bf16(0.06 * rng.standard_normal((I, H)))
+        t[p + "mlp.up_proj.weight"] = bf16(0.06 * rng.standard_normal((I, H)))
+        t[p + "mlp.down_proj.weight"] = bf16(0.06 * rng.standard_normal((H, I)))
+        t[p + "input_layernorm.weight"] = bf16(1 + 0.1 * rng.standard_normal(H))
+        t[p + "post_attention_layernorm.weight"] = bf16(1 + 0.1 * rng.standard_normal(H))
+    if not tied:
+        t["lm_head.weight"] = bf16(0.06 * rng.standard_normal((V, H)))
+    return t, dict(H=H, L=L, nq=nq, nk=nk, D=D, I=I, V=V)
+
+
+
+def save_qwen3(path, tensors):
+    """Write bf16 bit arrays as a safetensors checkpoint."""
+    import torch
+    from safetensors.torch import save_file
+
+    save_file({k: torch.from_numpy(np.ascontiguousarray(v).view(np.int16)).view(torch.bfloat16)
+               for k, v in tensors.items()}, str(path))
+
+
 # ---------------------------------------------------------------- GPU plumbing
 
 def dev(a):
