@@ -182,22 +182,39 @@ def measure_chain(w, steps, warmup, per_op):
              GBps=round(chain_bytes / ms / 1e6, 1), frac=round(chain_bytes / ms / 1e6 / HBM_PEAK_GBPS, 4),
              tokens_per_s=round(w["T"] / (ms / 1e3), 1), chain_bytes=chain_bytes)
     if per_op:
+        # Each op alone over all layers.  The residual stream x and the
+        # outputs xn, h rotate over 4 sets, so no launch reads or rewrites
+        # what the launch before it left in the 256 MB Infinity Cache (one
+        # op's launch touches >= 256 MB at the 8B prefill shapes).
+        T, H, I = w["T"], w["H"], w["I"]
+        sets = [(chain.x, chain.xn, chain.h)] + [
+            (torch.randn(T, H, device="cuda"), torch.empty(T, H, device="cuda"), torch.empty(T, I, device="cuda"))
+            for _ in range(3)]
+
+        def alone(name):
+            for li, Ld in enumerate(chain.layers):
+                chain.x, chain.xn, chain.h = sets[li % 4]
+                chain.op(name, Ld)
+            chain.x, chain.xn, chain.h = sets[0]
+
         ops = {}
         for name in OPS:
-            go = capture(lambda: [chain.op(name, Ld) for Ld in chain.layers])
+            go = capture(lambda: alone(name))
             go.replay()
-            t = time_region(go.replay, 3 if w["T"] >= 1024 else 20) / len(chain.layers)
+            t = time_region(go.replay, 10 if w["T"] >= 1024 else 20) / len(chain.layers)
             ops[name] = dict(us=round(t * 1e3, 2), GBps=round(ob[name] / t / 1e6, 1),
                              frac=round(ob[name] / t / 1e6 / HBM_PEAK_GBPS, 4), bytes=ob[name])
             del go
         r["ops"] = ops
+        del sets
     del g, chain
     torch.cuda.empty_cache()
     return r
 
 
-def measure_sampler(hip, steps, rows=64, vocab=VOCAB):
-    """Logits [64, 151936] ~N(0,3), history [64, 256], rep 1.2, T 0.6, freq 0.1."""
+def measure_sampler(hip, steps, rows=64, vocab=VOCAB, freq=0.1):
+    """Logits [64, 151936] ~N(0,3), history [64, 256], rep 1.2, T 0.6, freq
+    0.1 (the reference default) or as given."""
     import torch
 
     g = torch.Generator(device="cuda").manual_seed(21)
@@ -207,7 +224,7 @@ def measure_sampler(hip, steps, rows=64, vocab=VOCAB):
     ids = torch.empty(rows, dtype=torch.int32, device="cuda")
     probs = torch.empty(rows, vocab, device="cuda")
     ws = torch.empty(hip.sample_workspace_size(rows, vocab), dtype=torch.uint8, device="cuda")
-    p = hip.SamplingParams()
+    p = hip.SamplingParams(frequency_penalty=freq)
     call = lambda: hip.sample(ids, probs, logits, hist, None, p, r, ws)
     gr = capture(call)
     gr.replay()
@@ -559,7 +576,7 @@ def cpu_chain(w, target_s, max_tokens=512, layers=4, threads=None):
                        f"of the workload's shapes, {passes} passes in {el:.1f} s on {threads} OpenMP threads")
 
 
-def cpu_sampler(target_s, rows=64, vocab=VOCAB):
+def cpu_sampler(target_s, rows=64, vocab=VOCAB, freq=0.1):
     import numpy as np
 
     oracle = _oracle()
@@ -569,7 +586,7 @@ def cpu_sampler(target_s, rows=64, vocab=VOCAB):
     t0 = time.perf_counter()
     done = 0
     while True:
-        oracle.sample_token(logits[done % rows], recent=hist[done % rows], r=0.5)
+        oracle.sample_token(logits[done % rows], recent=hist[done % rows], r=0.5, frequency_penalty=freq)
         done += 1
         el = time.perf_counter() - t0
         if el >= target_s:
@@ -780,6 +797,7 @@ def main():
             r = measure_deltanet(anelm, DN_WORKLOADS[args.only], max(args.steps, 20))
         elif args.only == "sampling-64x151936":
             r = measure_sampler(anelm, max(args.steps, 20))
+            r["frequency_penalty_0"] = measure_sampler(anelm, max(args.steps, 20), freq=0.0)
         elif args.only == "convert-qwen3-8b-bf16":
             r = measure_convert(anelm)
         elif args.only in Q3_WORKLOADS:
@@ -820,6 +838,8 @@ def main():
             if name != args.workload:
                 configs[name] = measure_chain(wl, max(args.steps, 20), args.warmup, per_op=False)
         configs["sampling-64x151936"] = measure_sampler(anelm, max(args.steps, 20))
+        configs["sampling-64x151936"]["frequency_penalty_0"] = {
+            k: v for k, v in measure_sampler(anelm, max(args.steps, 20), freq=0.0).items() if k != "note"}
         for name, aw in ATTN_WORKLOADS.items():
             configs[name] = measure_attention(anelm, aw, max(args.steps, 20))
         for name, dw in DN_WORKLOADS.items():
@@ -845,6 +865,8 @@ def main():
                 if name != args.workload:
                     cpu_configs[name] = cpu_chain(wl, 1.5, max_tokens=256, layers=2)
             cpu_configs["sampling-64x151936"] = cpu_sampler(1.5)
+            cpu_configs["sampling-64x151936"]["frequency_penalty_0"] = {
+                k: v for k, v in cpu_sampler(1.0, freq=0.0).items() if k in ("us", "GBps")}
             cpu_configs["attention-qwen3-8b-decode"] = cpu_attention(ATTN_WORKLOADS["attention-qwen3-8b-decode-b1"], 1.5)
             cpu_configs["convert-qwen3-8b-bf16"] = cpu_convert(1.5)
     out = {
