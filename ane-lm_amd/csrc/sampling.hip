@@ -258,20 +258,21 @@ __device__ __forceinline__ Binade binade_of(float cum) {
 }
 
 // The map of adding p inside binade b (saturated if the sum may leave it).
+// Straight-line code: a branch per element costs more than the select.
 __device__ __forceinline__ Fn elem_map(float p, const Binade& b) {
-    Fn f;
-    if (!(p < b.U)) {  // leaves the binade (or NaN): exact add at walk time
-        f.a0 = f.a1 = kSat;
-        return f;
-    }
-    const float t = ldexpf(p, b.sh);  // exact: p/u < 2^24
+    // exact below 2^24 (p < U); clamped above so the conversion is defined
+    // for the sums that leave the binade, whose map is replaced anyway
+    const float t = fminf(ldexpf(p, b.sh), 0x1p30f);
     const float fl = floorf(t);
-    const float fr = t - fl;          // exact
+    const float fr = t - fl;  // exact
     const uint32_t qi = (uint32_t)fl;
     const uint32_t q = qi + (fr > 0.5f ? 1u : 0u);
-    const bool tie = fr == 0.5f;
-    f.a0 = q + ((tie && (qi & 1u)) ? 1u : 0u);
-    f.a1 = q + ((tie && !(qi & 1u)) ? 1u : 0u);
+    const uint32_t tie = fr == 0.5f ? 1u : 0u;
+    const uint32_t odd = qi & 1u;
+    const bool leave = !(p < b.U);  // leaves the binade (or NaN): exact add at walk time
+    Fn f;
+    f.a0 = leave ? kSat : q + (tie & odd);
+    f.a1 = leave ? kSat : q + (tie & (odd ^ 1u));
     return f;
 }
 
@@ -536,22 +537,33 @@ __global__ __launch_bounds__(256) void sample_stage3_kernel(SampleArgs a, int ve
 constexpr int kSumCache = 4096;  // sub-tile summaries cached in LDS per row
 constexpr uint32_t kNoEv = 0xFFFFFFFFu;
 
-// n words from global memory to LDS by one wave, eight loads in flight per
-// lane before the first store (a plain loop would wait out the memory
-// latency once per iteration).
-__device__ __forceinline__ void copy_to_lds(int32_t* dst, const int32_t* src, int n) {
+// The row's three sub-tile summary arrays (n words each) from global memory
+// to LDS by one wave, 16 loads per array and lane in flight before the first
+// store: at V = 151936 (594 sub-tiles) that is one memory round trip.  The
+// loads use clamped indices (always in bounds, n >= 1), so none waits on a
+// branch; only the LDS stores are guarded.
+__device__ __forceinline__ void copy3_to_lds(int32_t* d0, const int32_t* s0, int32_t* d1, const int32_t* s1,
+                                             int32_t* d2, const int32_t* s2, int n) {
+    constexpr int K = 16;
     const int lane = threadIdx.x;
-    for (int b = 0; b < n; b += 64 * 8) {
-        int32_t t[8];
+    for (int b = 0; b < n; b += 64 * K) {
+        int32_t t0[K], t1[K], t2[K];
 #pragma unroll
-        for (int k = 0; k < 8; k++) {
+        for (int k = 0; k < K; k++) {
             const int j = b + k * 64 + lane;
-            t[k] = j < n ? src[j] : 0;
+            const int jj = j < n ? j : n - 1;
+            t0[k] = s0[jj];
+            t1[k] = s1[jj];
+            t2[k] = s2[jj];
         }
 #pragma unroll
-        for (int k = 0; k < 8; k++) {
+        for (int k = 0; k < K; k++) {
             const int j = b + k * 64 + lane;
-            if (j < n) dst[j] = t[k];
+            if (j < n) {
+                d0[j] = t0[k];
+                d1[j] = t1[k];
+                d2[j] = t2[k];
+            }
         }
     }
 }
@@ -582,15 +594,20 @@ __device__ bool walk_subtile(const SampleArgs& a, long st, const float* prow, fl
 #pragma unroll
         for (int e = 0; e < 4; e++) p[e] = i0 + e < V ? prow[i0 + e] : 0.0f;
     }
-    long s = base;  // first unprocessed index
+    // offsets inside the sub-tile: first unprocessed element, end of the row
+    const int nvalid = V - base < kSub ? (int)(V - base) : kSub;
+    int s = 0;
     while (true) {
         const Binade b = binade_of(__uint_as_float(cb));
         Fn f[4];
         Fn acc = {0u, 0u};
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-            const long i = i0 + e;
-            f[e] = (i >= s && i < V) ? elem_map(p[e], b) : Fn{0u, 0u};
+            const int o = 4 * lane + e;
+            const Fn m = elem_map(p[e], b);
+            const bool in = o >= s && o < nvalid;
+            f[e].a0 = in ? m.a0 : 0u;
+            f[e].a1 = in ? m.a1 : 0u;
             acc = compose(acc, f[e]);
         }
         const Fn incl = wave_scan(acc);
@@ -602,18 +619,16 @@ __device__ bool walk_subtile(const SampleArgs& a, long st, const float* prow, fl
         float evp = 0.0f;
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-            const long i = i0 + e;
-            if (ev == kNoEv && i >= s && i < V) {
-                const uint32_t inc = pick(f[e], mm);
-                if (mm >= b.mhi || inc >= b.mhi - mm) {
-                    ev = ((uint32_t)(4 * lane + e) << 1) | 1u;  // leaves the binade
-                    evm = mm;
-                    evp = p[e];
-                } else {
-                    mm += inc;
-                    if (ldexpf((float)mm, -b.sh) >= r) ev = (uint32_t)(4 * lane + e) << 1;  // hit
-                }
-            }
+            const int o = 4 * lane + e;
+            const bool act = ev == kNoEv && o >= s && o < nvalid;
+            const uint32_t inc = pick(f[e], mm);
+            const bool leave = mm >= b.mhi || inc >= b.mhi - mm;  // leaves the binade
+            const uint32_t mn = mm + inc;                          // no wrap: mm < 2^24, inc <= 2^30
+            const bool hit = !leave && ldexpf((float)mn, -b.sh) >= r;
+            evm = act && leave ? mm : evm;
+            evp = act && leave ? p[e] : evp;
+            ev = act && leave ? (((uint32_t)o << 1) | 1u) : (act && hit ? (uint32_t)o << 1 : ev);
+            mm = act && !leave ? mn : mm;
         }
         const unsigned long long bal = __ballot(ev != kNoEv);
         if (bal == 0) {
@@ -640,7 +655,7 @@ __device__ bool walk_subtile(const SampleArgs& a, long st, const float* prow, fl
             return true;
         }
         cb = __float_as_uint(c);
-        s = ei + 1;
+        s = (int)(e0 >> 1) + 1;
     }
 }
 
@@ -653,9 +668,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1))) void
     const long V = a.vocab;
     const float* prow = a.probs + row * a.ld_probs;
     const int ncache = a.nsub < kSumCache ? a.nsub : kSumCache;
-    copy_to_lds(reinterpret_cast<int32_t*>(sh.sm0), reinterpret_cast<const int32_t*>(a.ws_map0 + row * a.nsub), ncache);
-    copy_to_lds(reinterpret_cast<int32_t*>(sh.sm1), reinterpret_cast<const int32_t*>(a.ws_map1 + row * a.nsub), ncache);
-    copy_to_lds(sh.scls, a.ws_cls + row * a.nsub, ncache);
+    copy3_to_lds(reinterpret_cast<int32_t*>(sh.sm0), reinterpret_cast<const int32_t*>(a.ws_map0 + row * a.nsub),
+                 reinterpret_cast<int32_t*>(sh.sm1), reinterpret_cast<const int32_t*>(a.ws_map1 + row * a.nsub),
+                 sh.scls, a.ws_cls + row * a.nsub, ncache);
     __syncthreads();
     // "cum < r" on bit patterns: cum >= 0, so cum < r <=> bits(cum) < bits(r)
     // for r > 0; for r <= 0 or NaN no sub-tile is passed without a walk
