@@ -8,15 +8,16 @@
 // Pipeline per call (rows x vocab; chunks of kCH = 4096 logits, sub-tiles of
 // kSub = 256):
 //   stage1  grid (chunks, rows): penalties + 1/T, per-chunk max (or argmax)
-//   stage2  grid (chunks, rows): exp(x - rowmax), exact fixed-point chunk sums
-//   stage3  grid (chunks, rows): p = e * (1/sum) (written to probs if asked),
-//           and for every sub-tile the exact running-sum map under the
-//           binade its start is predicted to lie in (see "categorical draw")
+//   stage2  grid (chunks, rows): e = exp(x - rowmax) into the probability
+//           buffer, exact fixed-point chunk sums
+//   stage3  grid (chunks, rows): p = e * (1/sum) in place, and for every
+//           sub-tile the exact running-sum map under the binade its start is
+//           predicted to lie in (see "categorical draw")
 //   walk    grid (rows), one wave each: the sequential fp32 CDF walk, passing
 //           up to 64 sub-tiles per step where the predictions hold and
 //           walking the others exactly, with no barriers
-// Every stage recomputes the adjusted logit from the input (a few flops)
-// instead of storing intermediates.
+// Stages 1 and 2 recompute the adjusted logit from the input (a few flops)
+// instead of storing it; stage 3 reads the exponentials stage 2 stored.
 #pragma clang fp contract(off)
 
 #include <climits>
@@ -406,8 +407,11 @@ __global__ __launch_bounds__(64) void sample_argmax_final_kernel(SampleArgs a) {
 
 // ---- stage 2: exact fixed-point sum of exp(x - max) per chunk ---------------
 // floor(e * 2^shift) summed as integers (associative, so independent of the
-// reduction order); any NaN term flags the row.
-__global__ __launch_bounds__(256) void sample_stage2_kernel(SampleArgs a, int vec) {
+// reduction order); any NaN term flags the row.  The values e are stored in
+// the probability buffer (in place over the logits for softmax: every
+// workgroup reads its own chunk before writing it), where stage 3 scales them
+// into probabilities without recomputing them.
+__global__ __launch_bounds__(256) void sample_stage2_kernel(SampleArgs a, int vec, int vec_out) {
     __shared__ uint32_t cnt[kCH];
     __shared__ float red[4];
     __shared__ uint64_t red_s[4];
@@ -419,18 +423,30 @@ __global__ __launch_bounds__(256) void sample_stage2_kernel(SampleArgs a, int ve
     build_counts(cnt, kCH, a, row, c0);
     const float neg = -row_max(a, row, red);
     const float scale = ldexpf(1.0f, a.shift);
+    float* out = a.probs + row * a.ld_probs;
     uint64_t acc = 0;
     int nan = 0;
 #pragma unroll
     for (int k = 0; k < 4; k++) {
+        float ev[4];
 #pragma unroll
         for (int e = 0; e < 4; e++) {
             const int li = k * 1024 + 4 * threadIdx.x + e;
+            ev[e] = 0.0f;
             if (c0 + li < a.vocab) {
                 const float x = sampler_expf(adjust(v[4 * k + e], cnt[li], a) + neg);
+                ev[e] = x;
                 if (x >= 0.0f && x <= 1.0f) acc += (uint64_t)(x * scale);
                 else nan = 1;
             }
+        }
+        const long i = c0 + k * 1024 + 4 * threadIdx.x;
+        if (vec_out && i + 3 < a.vocab) {  // cached store: stage 3 reads these back
+            *reinterpret_cast<float4*>(out + i) = make_float4(ev[0], ev[1], ev[2], ev[3]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                if (i + e < a.vocab) out[i + e] = ev[e];
         }
     }
     acc = wave_sum_u64(acc);
@@ -454,9 +470,7 @@ __global__ __launch_bounds__(256) void sample_stage2_kernel(SampleArgs a, int ve
 // the in-order composition of its elements' maps under that binade.  The walk
 // uses a map only if the actual running sum turns out to lie in that binade
 // and the map shows no element leaving it; otherwise it walks exactly.
-__global__ __launch_bounds__(256) void sample_stage3_kernel(SampleArgs a, int vec, int vec_out) {
-    __shared__ uint32_t cnt[kCH];
-    __shared__ float red[4];
+__global__ __launch_bounds__(256) void sample_stage3_kernel(SampleArgs a, int vec_out) {
     __shared__ uint64_t red_s[4];
     __shared__ int red_f[4];
     __shared__ float ksum[4][4];  // [k][wave] fp32 sums of exp (prediction only)
@@ -464,10 +478,8 @@ __global__ __launch_bounds__(256) void sample_stage3_kernel(SampleArgs a, int ve
     const long row = blockIdx.y;
     const long c0 = (long)blockIdx.x * kCH;
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-    float v[16];
-    load_chunk16(v, a.logits + row * a.ld_logits, c0, a.vocab, vec != 0);
-    build_counts(cnt, kCH, a, row, c0);
-    const float neg = -row_max(a, row, red);
+    float v[16];  // exp(adjusted - max), as stage 2 stored them
+    load_chunk16(v, a.probs + row * a.ld_probs, c0, a.vocab, vec_out != 0);
     const float inv = row_inv_sum(a, row, red_s, red_f);
     // exact prefix of the earlier chunks' sums (prediction of the running sum)
     if (wid == 0) {
@@ -477,28 +489,25 @@ __global__ __launch_bounds__(256) void sample_stage3_kernel(SampleArgs a, int ve
         if (lane == 0) s_prefix = ldexpf((float)pre, -a.shift);
     }
     float p[16];
-    float* out = a.probs ? a.probs + row * a.ld_probs : nullptr;
+    float* out = a.probs + row * a.ld_probs;
 #pragma unroll
     for (int k = 0; k < 4; k++) {
         float ks = 0.f;
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            const int li = k * 1024 + 4 * threadIdx.x + j;
-            const float e = c0 + li < a.vocab ? sampler_expf(adjust(v[4 * k + j], cnt[li], a) + neg) : 0.0f;
+            const float e = v[4 * k + j];  // 0 past the end of the row
             ks += e;
             p[4 * k + j] = e * inv;
         }
         ks = wave_sum(ks);
         if (lane == 0) ksum[k][wid] = ks;
         const long i = c0 + k * 1024 + 4 * threadIdx.x;
-        if (out) {
-            if (vec_out && i + 3 < a.vocab) {  // cached store: the walk reads these back
-                *reinterpret_cast<float4*>(out + i) = make_float4(p[4 * k], p[4 * k + 1], p[4 * k + 2], p[4 * k + 3]);
-            } else {
+        if (vec_out && i + 3 < a.vocab) {  // cached store: the walk reads these back
+            *reinterpret_cast<float4*>(out + i) = make_float4(p[4 * k], p[4 * k + 1], p[4 * k + 2], p[4 * k + 3]);
+        } else {
 #pragma unroll
-                for (int j = 0; j < 4; j++)
-                    if (i + j < a.vocab) out[i + j] = p[4 * k + j];
-            }
+            for (int j = 0; j < 4; j++)
+                if (i + j < a.vocab) out[i + j] = p[4 * k + j];
         }
     }
     __syncthreads();
@@ -797,8 +806,8 @@ extern "C" int anelm_softmax(float* x, long rows, long n, long ld, void* workspa
     const int vec = (ld % 4 == 0) && aligned16(x);
     const dim3 grd((unsigned)a.nchunk, (unsigned)rows);
     sample_stage1_kernel<false><<<grd, 256, 0, st>>>(a, vec);
-    sample_stage2_kernel<<<grd, 256, 0, st>>>(a, vec);
-    sample_stage3_kernel<<<grd, 256, 0, st>>>(a, vec, vec);
+    sample_stage2_kernel<<<grd, 256, 0, st>>>(a, vec, vec);
+    sample_stage3_kernel<<<grd, 256, 0, st>>>(a, vec);
     return launch_status("softmax");
 }
 
@@ -847,8 +856,8 @@ extern "C" int anelm_sample(int32_t* ids, float* probs, long ld_probs, const flo
     const int vec_out = probs && (ld_probs % 4 == 0) && aligned16(probs);
     a.vec_probs = vec_out;
     sample_stage1_kernel<false><<<grd, 256, 0, st>>>(a, vec);
-    sample_stage2_kernel<<<grd, 256, 0, st>>>(a, vec);
-    sample_stage3_kernel<<<grd, 256, 0, st>>>(a, vec, vec_out);
+    sample_stage2_kernel<<<grd, 256, 0, st>>>(a, vec, vec_out);
+    sample_stage3_kernel<<<grd, 256, 0, st>>>(a, vec_out);
     sample_walk_kernel<<<dim3((unsigned)rows), 64, 0, st>>>(a);
     return launch_status("sample");
 }
