@@ -55,8 +55,10 @@ struct SampleArgs {
     uint32_t* ws_map0;    // [rows, nsub] sub-tile map, even start
     uint32_t* ws_map1;    // [rows, nsub] sub-tile map, odd start
     int32_t* ws_cls;      // [rows, nsub] predicted binade class (-1: none)
+    uint32_t* ws_xing;    // [rows, nsub, kXWords] predicted crossing (see predict_crossing)
     int nchunk;
     int nsub;
+    int nsub_ld;          // row stride of the sub-tile arrays: nsub rounded up to 4 (16-byte rows)
     int shift;
     int vec_probs;        // probs rows are 16-byte aligned
 };
@@ -71,12 +73,12 @@ struct SampleArgs {
 __device__ __forceinline__ float pow2i(int k) { return __uint_as_float((uint32_t)(k + 127) << 23); }
 
 __device__ __forceinline__ float sampler_expf(float x) {
-    if (x != x) return x;
-    if (x < -104.0f) return 0.0f;
-    if (x > 89.0f) return INFINITY;
-    const float kf = rintf(x * 0x1.715476p+0f);
+    // Straight-line: the special cases are selected at the end.  The clamp
+    // keeps the body finite (maxnum ignores a NaN); x itself decides.
+    const float xc = fminf(fmaxf(x, -104.0f), 89.0f);
+    const float kf = rintf(xc * 0x1.715476p+0f);
     const int k = (int)kf;
-    float r = fmaf(-kf, 0x1.63p-1f, x);
+    float r = fmaf(-kf, 0x1.63p-1f, xc);
     r = fmaf(-kf, -0x1.bd0106p-13f, r);
     float p = 0x1.a01a02p-13f;
     p = fmaf(p, r, 0x1.6c16c2p-10f);
@@ -86,9 +88,12 @@ __device__ __forceinline__ float sampler_expf(float x) {
     p = fmaf(p, r, 0x1p-1f);
     p = fmaf(p, r, 1.0f);
     p = fmaf(p, r, 1.0f);
-    if (k < -126) return (p * pow2i(k + 64)) * pow2i(-64);
-    if (k > 127) return (p * pow2i(k - 1)) * 2.0f;
-    return p * pow2i(k);
+    const float sub = (p * pow2i(k + 64)) * pow2i(-64);  // k < -126: rounded once, as a subnormal
+    const float big = (p * pow2i(k - 1)) * 2.0f;         // k > 127
+    float y = k < -126 ? sub : (k > 127 ? big : p * pow2i(k));
+    y = x < -104.0f ? 0.0f : y;
+    y = x > 89.0f ? INFINITY : y;
+    return x != x ? x : y;
 }
 
 // ---- history counts --------------------------------------------------------
@@ -124,6 +129,21 @@ __device__ __forceinline__ float adjust(float l, uint32_t n, const SampleArgs& a
     return l;
 }
 
+// The 16 adjusted logits of this thread in place (the element order of
+// load_chunk16); the counts come in four 16-byte LDS reads before any use.
+__device__ __forceinline__ void adjust16(float v[16], const uint32_t* cnt, const SampleArgs& a) {
+    uint4 n[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) n[k] = *reinterpret_cast<const uint4*>(cnt + k * 1024 + 4 * threadIdx.x);
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        v[4 * k] = adjust(v[4 * k], n[k].x, a);
+        v[4 * k + 1] = adjust(v[4 * k + 1], n[k].y, a);
+        v[4 * k + 2] = adjust(v[4 * k + 2], n[k].z, a);
+        v[4 * k + 3] = adjust(v[4 * k + 3], n[k].w, a);
+    }
+}
+
 // The 16 logits of thread tid in chunk c0 (4 float4 slots k*1024 + 4*tid).
 __device__ __forceinline__ void load_chunk16(float v[16], const float* row_ptr, long c0, long vocab, bool vec) {
 #pragma unroll
@@ -142,10 +162,20 @@ __device__ __forceinline__ void load_chunk16(float v[16], const float* row_ptr, 
     }
 }
 
-// max over the row's chunk maxima (any block size, all threads get it)
-__device__ float row_max(const SampleArgs& a, long row, float* red) {
+// The row's chunk maxima and chunk sums are read by every workgroup of the
+// next stage.  Each thread loads its share first (the loads do not depend on
+// the chunk's own data, so their latency overlaps the chunk loads), and the
+// workgroup reduces the shares later.
+
+// this thread's share of the row max
+__device__ __forceinline__ float max_share(const SampleArgs& a, long row) {
     float m = -INFINITY;
     for (int c = threadIdx.x; c < a.nchunk; c += blockDim.x) m = fmaxf(m, a.ws_max[row * a.nchunk + c]);
+    return m;
+}
+
+// the row max from the shares (any block size, all threads get it)
+__device__ float reduce_max(float m, float* red) {
     m = wave_max(m);
     const int nw = blockDim.x >> 6;
     if (nw == 1) return m;
@@ -157,35 +187,53 @@ __device__ float row_max(const SampleArgs& a, long row, float* red) {
     return m;
 }
 
-// 1 / (row sum) from the chunk sums: exact integer total, one rounding to
-// float, exact power-of-two scaling, correctly rounded reciprocal
-// (cpu_ops.cpp:95-97).  Any block size; the value does not depend on it.
-__device__ float row_inv_sum(const SampleArgs& a, long row, uint64_t* red_s, int* red_f) {
-    uint64_t s = 0;
-    int f = 0;
+// this thread's share of the row sum, of the sum of the chunks before chunk
+// `before`, and of the NaN flags
+struct SumShare {
+    uint64_t all, pre;
+    int flag;
+};
+
+__device__ __forceinline__ SumShare sum_share(const SampleArgs& a, long row, int before) {
+    SumShare sh = {0, 0, 0};
     for (int c = threadIdx.x; c < a.nchunk; c += blockDim.x) {
-        s += a.ws_sum[row * a.nchunk + c];
-        f |= a.ws_flag[row * a.nchunk + c];
+        const uint64_t w = a.ws_sum[row * a.nchunk + c];
+        sh.all += w;
+        sh.pre += c < before ? w : 0;
+        sh.flag |= a.ws_flag[row * a.nchunk + c];
     }
-    s = wave_sum_u64(s);
-    f = __any(f) ? 1 : 0;
+    return sh;
+}
+
+// 1 / (row sum) from the shares: exact integer total, one rounding to float,
+// exact power-of-two scaling, correctly rounded reciprocal (cpu_ops.cpp:95-97),
+// and the prefix as a float (a prediction only).  Any block size; the values
+// do not depend on it.
+__device__ void reduce_sums(SumShare sh, const SampleArgs& a, uint64_t* red_s, uint64_t* red_p, int* red_f,
+                            float& inv, float& prefix) {
+    uint64_t s = wave_sum_u64(sh.all), pre = wave_sum_u64(sh.pre);
+    int f = __any(sh.flag) ? 1 : 0;
     const int nw = blockDim.x >> 6;
     if (nw > 1) {
         __syncthreads();
         if ((threadIdx.x & 63) == 0) {
             red_s[threadIdx.x >> 6] = s;
+            red_p[threadIdx.x >> 6] = pre;
             red_f[threadIdx.x >> 6] = f;
         }
         __syncthreads();
         s = 0;
+        pre = 0;
         f = 0;
         for (int w = 0; w < nw; w++) {
             s += red_s[w];
+            pre += red_p[w];
             f |= red_f[w];
         }
     }
     const float sum = f ? NAN : ldexpf((float)s, -a.shift);
-    return 1.0f / sum;
+    inv = 1.0f / sum;
+    prefix = ldexpf((float)pre, -a.shift);
 }
 
 // ---- the categorical draw: exact sequential running sums -----------------
@@ -302,7 +350,7 @@ __device__ __forceinline__ Fn wave_scan(Fn v) {
 // ---- stage 1: penalties, 1/T, chunk max (T > 0) or chunk argmax (T <= 0) ----
 template <bool ARGMAX>
 __global__ __launch_bounds__(256) void sample_stage1_kernel(SampleArgs a, int vec) {
-    __shared__ uint32_t cnt[kCH];
+    __shared__ __align__(16) uint32_t cnt[kCH];
     __shared__ float red_v[4];
     __shared__ int red_i[4];
     const long row = blockIdx.y;
@@ -310,6 +358,8 @@ __global__ __launch_bounds__(256) void sample_stage1_kernel(SampleArgs a, int ve
     float v[16];
     load_chunk16(v, a.logits + row * a.ld_logits, c0, a.vocab, vec != 0);
     build_counts(cnt, kCH, a, row, c0);
+    adjust16(v, cnt, a);
+    const int nvalid = a.vocab - c0 < kCH ? (int)(a.vocab - c0) : kCH;
     float best = -INFINITY;
     int besti = INT_MAX;
 #pragma unroll
@@ -317,18 +367,16 @@ __global__ __launch_bounds__(256) void sample_stage1_kernel(SampleArgs a, int ve
 #pragma unroll
         for (int e = 0; e < 4; e++) {
             const int li = k * 1024 + 4 * threadIdx.x + e;
-            const long i = c0 + li;
-            if (i < a.vocab) {
-                const float x = adjust(v[4 * k + e], cnt[li], a);
-                if (ARGMAX) {
-                    // first index of the maximum among non-NaN values
-                    if (x == x && (x > best || (x == best && (int)i < besti))) {
-                        best = x;
-                        besti = (int)i;
-                    }
-                } else {
-                    best = fmaxf(best, x);
+            const float x = v[4 * k + e];
+            if (ARGMAX) {
+                // first index of the maximum among non-NaN values
+                const int i = (int)c0 + li;
+                if (li < nvalid && x == x && (x > best || (x == best && i < besti))) {
+                    best = x;
+                    besti = i;
                 }
+            } else {
+                best = li < nvalid ? fmaxf(best, x) : best;
             }
         }
     }
@@ -412,7 +460,7 @@ __global__ __launch_bounds__(64) void sample_argmax_final_kernel(SampleArgs a) {
 // workgroup reads its own chunk before writing it), where stage 3 scales them
 // into probabilities without recomputing them.
 __global__ __launch_bounds__(256) void sample_stage2_kernel(SampleArgs a, int vec, int vec_out) {
-    __shared__ uint32_t cnt[kCH];
+    __shared__ __align__(16) uint32_t cnt[kCH];
     __shared__ float red[4];
     __shared__ uint64_t red_s[4];
     __shared__ int red_f[4];
@@ -420,8 +468,11 @@ __global__ __launch_bounds__(256) void sample_stage2_kernel(SampleArgs a, int ve
     const long c0 = (long)blockIdx.x * kCH;
     float v[16];
     load_chunk16(v, a.logits + row * a.ld_logits, c0, a.vocab, vec != 0);
+    const float mshare = max_share(a, row);
     build_counts(cnt, kCH, a, row, c0);
-    const float neg = -row_max(a, row, red);
+    adjust16(v, cnt, a);
+    const int nvalid = a.vocab - c0 < kCH ? (int)(a.vocab - c0) : kCH;
+    const float neg = -reduce_max(mshare, red);
     const float scale = ldexpf(1.0f, a.shift);
     float* out = a.probs + row * a.ld_probs;
     uint64_t acc = 0;
@@ -432,13 +483,11 @@ __global__ __launch_bounds__(256) void sample_stage2_kernel(SampleArgs a, int ve
 #pragma unroll
         for (int e = 0; e < 4; e++) {
             const int li = k * 1024 + 4 * threadIdx.x + e;
-            ev[e] = 0.0f;
-            if (c0 + li < a.vocab) {
-                const float x = sampler_expf(adjust(v[4 * k + e], cnt[li], a) + neg);
-                ev[e] = x;
-                if (x >= 0.0f && x <= 1.0f) acc += (uint64_t)(x * scale);
-                else nan = 1;
-            }
+            const float x = li < nvalid ? sampler_expf(v[4 * k + e] + neg) : 0.0f;
+            ev[e] = x;
+            const bool ok = x >= 0.0f && x <= 1.0f;
+            acc += ok ? (uint64_t)(x * scale) : 0u;
+            nan |= ok ? 0 : 1;
         }
         const long i = c0 + k * 1024 + 4 * threadIdx.x;
         if (vec_out && i + 3 < a.vocab) {  // cached store: stage 3 reads these back
@@ -462,6 +511,93 @@ __global__ __launch_bounds__(256) void sample_stage2_kernel(SampleArgs a, int ve
     }
 }
 
+// ---- crossings: a sub-tile in which the running sum enters the next binade ----
+// Inside such a sub-tile the single-binade map cannot pass the walk.  Stage 3
+// predicts where the crossing happens (from its prediction of the running
+// sum at the sub-tile's start) and stores what the walk needs to pass the
+// sub-tile in O(1) if the prediction holds for the actual running sum:
+//   pre  the map of the elements before the crossing element j, under the
+//        start binade;
+//   pj   the crossing element's probability (added with one fp32 add);
+//   sfx  the map of the elements after j, under the binade the sum enters;
+//   info j | (that binade's class << 8), or -1 when there is no single
+//        predicted crossing (none, or a second one in the same sub-tile).
+// The walk checks every assumption against the exact running sum and walks
+// the sub-tile exactly when one fails, so a wrong prediction costs time only.
+constexpr int kXWords = 6;  // words per sub-tile: pre.a0, pre.a1, sfx.a0, sfx.a1, pj, info
+
+struct Crossing {
+    Fn pre, sfx;
+    float pj;
+    int info;
+};
+
+// acc: the inclusive scan of the lanes' maps under binade b (class cls);
+// f: this lane's four element maps; p: its four probabilities; nv: valid
+// elements in the sub-tile; cb: bits of the predicted running sum at its
+// start.  Wave-uniform control flow.
+__device__ __forceinline__ Crossing predict_crossing(Fn acc, const Fn f[4], const float p[4], int nv, bool ok,
+                                                     uint32_t cb, int cls, const Binade& b) {
+    Crossing x = {{0u, 0u}, {0u, 0u}, 0.0f, -1};
+    const int lane = threadIdx.x & 63;
+    const uint32_t t0 = (uint32_t)__builtin_amdgcn_readlane((int)acc.a0, 63);
+    const uint32_t t1 = (uint32_t)__builtin_amdgcn_readlane((int)acc.a1, 63);
+    const uint32_t mp = cls == 0 ? cb : ((cb & 0x7FFFFFu) | 0x800000u);  // predicted start multiple
+    const uint32_t tinc = (mp & 1u) ? t1 : t0;
+    if (!ok || tinc < b.mhi - mp) return x;  // no crossing predicted
+    // the first element at which the predicted sum leaves binade b
+    const Fn ex = dpp_fn<0x138, 0xF>(acc);  // composition of the lanes before this one
+    uint32_t mm = mp + pick(ex, mp);
+    Fn run = ex, pre = {0u, 0u};
+    int ev = kSub;
+    uint32_t mb = 0;
+    float pe = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int o = 4 * lane + j;
+        const bool act = ev == kSub && o < nv;
+        const uint32_t inc = pick(f[j], mm);
+        const bool leave = mm >= b.mhi || inc >= b.mhi - mm;
+        if (act && leave) {
+            ev = o;
+            mb = mm;
+            pe = p[j];
+            pre = run;
+        }
+        mm = act && !leave ? mm + inc : mm;
+        run = compose(run, f[j]);
+    }
+    const unsigned long long bal = __ballot(ev != kSub);
+    if (bal == 0) return x;
+    const int L = __ffsll((long long)bal) - 1;
+    const int jstar = __builtin_amdgcn_readlane(ev, L);
+    x.pre.a0 = (uint32_t)__builtin_amdgcn_readlane((int)pre.a0, L);
+    x.pre.a1 = (uint32_t)__builtin_amdgcn_readlane((int)pre.a1, L);
+    x.pj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pe), L));
+    const uint32_t mbs = (uint32_t)__builtin_amdgcn_readlane((int)mb, L);
+    // the predicted sum after the crossing add, and the elements after it
+    const float c = ldexpf((float)mbs, -b.sh) + x.pj;
+    if (!(c < INFINITY)) return x;  // NaN or overflow: no prediction
+    const uint32_t c2 = __float_as_uint(c);
+    const int cls2 = c2 < 0x00800000u ? 0 : (int)(c2 >> 23);
+    const Binade b2 = binade_of_class(cls2);
+    Fn g = {0u, 0u};
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int o = 4 * lane + j;
+        const Fn m = elem_map(p[j], b2);
+        const bool in = o > jstar && o < nv;
+        g = compose(g, Fn{in ? m.a0 : 0u, in ? m.a1 : 0u});
+    }
+    g = wave_scan(g);
+    x.sfx.a0 = (uint32_t)__builtin_amdgcn_readlane((int)g.a0, 63);
+    x.sfx.a1 = (uint32_t)__builtin_amdgcn_readlane((int)g.a1, 63);
+    const uint32_t m2 = cls2 == 0 ? c2 : ((c2 & 0x7FFFFFu) | 0x800000u);
+    const uint32_t sinc = (m2 & 1u) ? x.sfx.a1 : x.sfx.a0;
+    if (sinc < b2.mhi - m2) x.info = jstar | (cls2 << 8);  // else a second crossing: walk exactly
+    return x;
+}
+
 // ---- stage 3: probabilities and sub-tile maps --------------------------------
 // Wave w's part of k-slice k is the 256 consecutive logits c0 + k*1024 + w*256 +
 // [0, 256): sub-tile 16*chunk + 4k + w.  For each, the wave predicts the binade
@@ -471,23 +607,19 @@ __global__ __launch_bounds__(256) void sample_stage2_kernel(SampleArgs a, int ve
 // uses a map only if the actual running sum turns out to lie in that binade
 // and the map shows no element leaving it; otherwise it walks exactly.
 __global__ __launch_bounds__(256) void sample_stage3_kernel(SampleArgs a, int vec_out) {
-    __shared__ uint64_t red_s[4];
+    __shared__ uint64_t red_s[4], red_p[4];
     __shared__ int red_f[4];
     __shared__ float ksum[4][4];  // [k][wave] fp32 sums of exp (prediction only)
-    __shared__ float s_prefix;
     const long row = blockIdx.y;
     const long c0 = (long)blockIdx.x * kCH;
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
     float v[16];  // exp(adjusted - max), as stage 2 stored them
     load_chunk16(v, a.probs + row * a.ld_probs, c0, a.vocab, vec_out != 0);
-    const float inv = row_inv_sum(a, row, red_s, red_f);
-    // exact prefix of the earlier chunks' sums (prediction of the running sum)
-    if (wid == 0) {
-        uint64_t pre = 0;
-        for (int c = lane; c < (int)blockIdx.x; c += 64) pre += a.ws_sum[row * a.nchunk + c];
-        pre = wave_sum_u64(pre);
-        if (lane == 0) s_prefix = ldexpf((float)pre, -a.shift);
-    }
+    const SumShare share = sum_share(a, row, (int)blockIdx.x);
+    // 1/sum, and the exact prefix of the earlier chunks' sums (the prediction
+    // of the running sum at this chunk's start)
+    float inv, prefix;
+    reduce_sums(share, a, red_s, red_p, red_f, inv, prefix);
     float p[16];
     float* out = a.probs + row * a.ld_probs;
 #pragma unroll
@@ -511,7 +643,7 @@ __global__ __launch_bounds__(256) void sample_stage3_kernel(SampleArgs a, int ve
         }
     }
     __syncthreads();
-    float run = s_prefix;  // running prediction, the same order of additions in every wave
+    float run = prefix;  // running prediction, the same order of additions in every wave
 #pragma unroll
     for (int k = 0; k < 4; k++) {
         float here = run;
@@ -521,18 +653,32 @@ __global__ __launch_bounds__(256) void sample_stage3_kernel(SampleArgs a, int ve
         const bool ok = cpred == cpred && cpred < INFINITY;
         const int cls = ok ? (cb < 0x00800000u ? 0 : (int)(cb >> 23)) : -1;
         const Binade b = binade_of_class(ok ? cls : 0);
+        const int nv = a.vocab - (c0 + k * 1024 + 256 * wid) < kSub ? (int)(a.vocab - (c0 + k * 1024 + 256 * wid))
+                                                                     : kSub;  // valid elements of the sub-tile
+        Fn f[4];
         Fn acc = {0u, 0u};
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            const long i = c0 + k * 1024 + 4 * threadIdx.x + j;
-            acc = compose(acc, i < a.vocab ? elem_map(p[4 * k + j], b) : Fn{0u, 0u});
+            const Fn m = elem_map(p[4 * k + j], b);
+            const bool in = 4 * lane + j < nv;
+            f[j].a0 = in ? m.a0 : 0u;
+            f[j].a1 = in ? m.a1 : 0u;
+            acc = compose(acc, f[j]);
         }
         acc = wave_scan(acc);
         const long st = (long)blockIdx.x * 16 + 4 * k + wid;
+        const Crossing x = predict_crossing(acc, f, &p[4 * k], nv, ok, cb, cls, b);
         if (lane == 63 && st < a.nsub) {
-            a.ws_map0[row * a.nsub + st] = acc.a0;
-            a.ws_map1[row * a.nsub + st] = acc.a1;
-            a.ws_cls[row * a.nsub + st] = cls;
+            a.ws_map0[row * a.nsub_ld + st] = acc.a0;
+            a.ws_map1[row * a.nsub_ld + st] = acc.a1;
+            a.ws_cls[row * a.nsub_ld + st] = cls;
+            uint32_t* xw = a.ws_xing + (row * a.nsub_ld + st) * kXWords;
+            xw[0] = x.pre.a0;
+            xw[1] = x.pre.a1;
+            xw[2] = x.sfx.a0;
+            xw[3] = x.sfx.a1;
+            xw[4] = __float_as_uint(x.pj);
+            xw[5] = (uint32_t)x.info;
         }
         run = run + ((ksum[k][0] + ksum[k][1]) + (ksum[k][2] + ksum[k][3]));
     }
@@ -546,41 +692,102 @@ __global__ __launch_bounds__(256) void sample_stage3_kernel(SampleArgs a, int ve
 constexpr int kSumCache = 4096;  // sub-tile summaries cached in LDS per row
 constexpr uint32_t kNoEv = 0xFFFFFFFFu;
 
-// The row's three sub-tile summary arrays (n words each) from global memory
-// to LDS by one wave, 16 loads per array and lane in flight before the first
-// store: at V = 151936 (594 sub-tiles) that is one memory round trip.  The
-// loads use clamped indices (always in bounds, n >= 1), so none waits on a
-// branch; only the LDS stores are guarded.
-__device__ __forceinline__ void copy3_to_lds(int32_t* d0, const int32_t* s0, int32_t* d1, const int32_t* s1,
-                                             int32_t* d2, const int32_t* s2, int n) {
-    constexpr int K = 16;
+constexpr int kXCache = 2048;  // sub-tiles whose crossing data is cached in LDS per row
+
+struct __align__(16) WalkShared {
+    uint32_t sm0[kSumCache], sm1[kSumCache];  // sub-tile maps
+    int32_t scls[kSumCache];                   // predicted binade classes
+    uint32_t xing[kXCache * kXWords];          // predicted crossings
+};
+
+// One memory round of the cache fill: K 16-byte loads per lane from a
+// source of nq quads (16-byte aligned rows), every load issued before the
+// first LDS store.  Loads and stores both use the clamped index, so neither
+// sits behind a branch (a guarded store lets the compiler sink its load into
+// the branch, one memory latency per quad); lanes past the end rewrite the
+// last quad with its own value.  The source row stride is a multiple of 4
+// words, so the last quad is in bounds; the LDS destination holds whole quads.
+template <int K>
+__device__ __forceinline__ void fill_round(const int4* src, int nq, int b, int4 t[K]) {
     const int lane = threadIdx.x;
-    for (int b = 0; b < n; b += 64 * K) {
-        int32_t t0[K], t1[K], t2[K];
 #pragma unroll
-        for (int k = 0; k < K; k++) {
-            const int j = b + k * 64 + lane;
-            const int jj = j < n ? j : n - 1;
-            t0[k] = s0[jj];
-            t1[k] = s1[jj];
-            t2[k] = s2[jj];
-        }
+    for (int k = 0; k < K; k++) {
+        const int j = b + k * 64 + lane;
+        t[k] = src[j < nq ? j : nq - 1];
+    }
+}
+template <int K>
+__device__ __forceinline__ void drain_round(int4* d, int nq, int b, const int4 t[K]) {
+    const int lane = threadIdx.x;
 #pragma unroll
-        for (int k = 0; k < K; k++) {
-            const int j = b + k * 64 + lane;
-            if (j < n) {
-                d0[j] = t0[k];
-                d1[j] = t1[k];
-                d2[j] = t2[k];
-            }
-        }
+    for (int k = 0; k < K; k++) {
+        const int j = b + k * 64 + lane;
+        d[j < nq ? j : nq - 1] = t[k];
     }
 }
 
-struct WalkShared {
-    uint32_t sm0[kSumCache], sm1[kSumCache];  // sub-tile maps
-    int32_t scls[kSumCache];                   // predicted binade classes
-};
+// The row's sub-tile summaries (maps and classes: nm sub-tiles; crossings:
+// nx sub-tiles) from global memory to LDS by one wave.  At V = 151936 (594
+// sub-tiles) everything arrives in one memory round trip.
+__device__ void fill_walk_cache(WalkShared& sh, const SampleArgs& a, long row, int nm, int nx) {
+    constexpr int KM = 4, KX = 16;  // quads per lane and round
+    const int4* s0 = reinterpret_cast<const int4*>(a.ws_map0 + row * a.nsub_ld);
+    const int4* s1 = reinterpret_cast<const int4*>(a.ws_map1 + row * a.nsub_ld);
+    const int4* s2 = reinterpret_cast<const int4*>(a.ws_cls + row * a.nsub_ld);
+    const int4* sx = reinterpret_cast<const int4*>(a.ws_xing + row * a.nsub_ld * kXWords);
+    const int qm = (nm + 3) / 4, qx = (nx * kXWords + 3) / 4;
+    int4 t0[KM], t1[KM], t2[KM], tx[KX];
+    fill_round<KM>(s0, qm, 0, t0);
+    fill_round<KM>(s1, qm, 0, t1);
+    fill_round<KM>(s2, qm, 0, t2);
+    fill_round<KX>(sx, qx, 0, tx);
+    drain_round<KM>(reinterpret_cast<int4*>(sh.sm0), qm, 0, t0);
+    drain_round<KM>(reinterpret_cast<int4*>(sh.sm1), qm, 0, t1);
+    drain_round<KM>(reinterpret_cast<int4*>(sh.scls), qm, 0, t2);
+    drain_round<KX>(reinterpret_cast<int4*>(sh.xing), qx, 0, tx);
+    for (int b = 64 * KM; b < qm; b += 64 * KM) {  // larger vocabularies
+        fill_round<KM>(s0, qm, b, t0);
+        fill_round<KM>(s1, qm, b, t1);
+        fill_round<KM>(s2, qm, b, t2);
+        drain_round<KM>(reinterpret_cast<int4*>(sh.sm0), qm, b, t0);
+        drain_round<KM>(reinterpret_cast<int4*>(sh.sm1), qm, b, t1);
+        drain_round<KM>(reinterpret_cast<int4*>(sh.scls), qm, b, t2);
+    }
+    for (int b = 64 * KX; b < qx; b += 64 * KX) {
+        fill_round<KX>(sx, qx, b, tx);
+        drain_round<KX>(reinterpret_cast<int4*>(sh.xing), qx, b, tx);
+    }
+}
+
+// Pass a crossing sub-tile in O(1) from the exact running sum at its start
+// (bits cb, binade class ccls) with its stored crossing x, if every stored
+// prediction holds: the sum stays in its binade up to element j, leaves it
+// at j, the fp32 sum after j lies in the binade the suffix map was made for
+// and stays there, and no running sum reaches r.  Returns false (nothing
+// changed) otherwise; the caller then walks the sub-tile exactly.
+__device__ __forceinline__ bool pass_crossing(uint32_t& cb, const uint32_t* x, int pcls, float r) {
+    const int info = (int)x[5];
+    if (info < 0) return false;
+    const Binade b = binade_of(__uint_as_float(cb));
+    if (b.cls != pcls) return false;  // pre was made under the predicted start binade
+    const uint32_t inc = (b.m0 & 1u) ? x[1] : x[0];
+    if (!(inc < b.mhi - b.m0)) return false;  // leaves before element j
+    const uint32_t mb = b.m0 + inc;
+    if (!(ldexpf((float)mb, -b.sh) < r)) return false;  // the draw ends before j
+    const float pj = __uint_as_float(x[4]);
+    const uint32_t incj = pick(elem_map(pj, b), mb);
+    if (incj < b.mhi - mb) return false;  // does not leave at j
+    const float c = ldexpf((float)mb, -b.sh) + pj;  // the reference's fp32 add of element j
+    if (!(c < r)) return false;                      // the draw ends at j (or NaN)
+    const Binade b2 = binade_of(c);
+    if (b2.cls != (info >> 8)) return false;
+    const uint32_t inc2 = (b2.m0 & 1u) ? x[3] : x[2];
+    if (!(inc2 < b2.mhi - b2.m0)) return false;  // leaves again
+    const float end = ldexpf((float)(b2.m0 + inc2), -b2.sh);
+    if (!(end < r)) return false;  // the draw ends after j
+    cb = __float_as_uint(end);
+    return true;
+}
 
 // Exact walk of sub-tile st from the running sum with bits cb.  Inside one
 // binade the running sums of all 256 elements follow from one in-order wave
@@ -677,9 +884,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1))) void
     const long V = a.vocab;
     const float* prow = a.probs + row * a.ld_probs;
     const int ncache = a.nsub < kSumCache ? a.nsub : kSumCache;
-    copy3_to_lds(reinterpret_cast<int32_t*>(sh.sm0), reinterpret_cast<const int32_t*>(a.ws_map0 + row * a.nsub),
-                 reinterpret_cast<int32_t*>(sh.sm1), reinterpret_cast<const int32_t*>(a.ws_map1 + row * a.nsub),
-                 sh.scls, a.ws_cls + row * a.nsub, ncache);
+    const int nxcache = a.nsub < kXCache ? a.nsub : kXCache;
+    fill_walk_cache(sh, a, row, ncache, nxcache);
     __syncthreads();
     // "cum < r" on bit patterns: cum >= 0, so cum < r <=> bits(cum) < bits(r)
     // for r > 0; for r <= 0 or NaN no sub-tile is passed without a walk
@@ -698,10 +904,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1))) void
         const uint32_t mhi = ccls ? (1u << 24) : (1u << 23);
         Fn f = {kSat, kSat};
         if (idx < a.nsub) {
-            const int pc = idx < kSumCache ? sh.scls[idx] : a.ws_cls[row * a.nsub + idx];
+            const int pc = idx < kSumCache ? sh.scls[idx] : a.ws_cls[row * a.nsub_ld + idx];
             if (pc == ccls) {
-                f.a0 = idx < kSumCache ? sh.sm0[idx] : a.ws_map0[row * a.nsub + idx];
-                f.a1 = idx < kSumCache ? sh.sm1[idx] : a.ws_map1[row * a.nsub + idx];
+                f.a0 = idx < kSumCache ? sh.sm0[idx] : a.ws_map0[row * a.nsub_ld + idx];
+                f.a1 = idx < kSumCache ? sh.sm1[idx] : a.ws_map1[row * a.nsub_ld + idx];
             }
         }
         const Fn pre = wave_scan(f);
@@ -716,7 +922,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1))) void
             st += npass;
         }
         if (npass < 64 && st < a.nsub) {
-            if (walk_subtile(a, st, prow, r, cb, result)) break;
+            // a predicted crossing passes in O(1); anything else is walked exactly
+            const int pc = st < kSumCache ? sh.scls[st] : a.ws_cls[row * a.nsub_ld + st];
+            const bool passed = st < nxcache && pass_crossing(cb, &sh.xing[st * kXWords], pc, r);
+            if (!passed && walk_subtile(a, st, prow, r, cb, result)) break;
             st += 1;
         }
     }
@@ -730,7 +939,7 @@ static int ceil_log2(long n) {
 }
 
 struct WsLayout {
-    size_t off_sum, off_max, off_arg, off_flag, off_m0, off_m1, off_cls, total;
+    size_t off_sum, off_max, off_arg, off_flag, off_m0, off_m1, off_cls, off_x, total;
 };
 
 static size_t al16(size_t x) { return (x + 15) & ~(size_t)15; }
@@ -738,7 +947,7 @@ static size_t al16(size_t x) { return (x + 15) & ~(size_t)15; }
 static WsLayout ws_layout(long rows, long vocab) {
     const size_t nch = (size_t)((vocab + kCH - 1) / kCH);
     const size_t nsub = (size_t)((vocab + kSub - 1) / kSub);
-    const size_t n = (size_t)rows * nch, ns = (size_t)rows * nsub;
+    const size_t n = (size_t)rows * nch, ns = (size_t)rows * ((nsub + 3) & ~(size_t)3);
     WsLayout l;
     l.off_sum = 0;
     l.off_max = l.off_sum + al16(n * sizeof(uint64_t));
@@ -747,7 +956,8 @@ static WsLayout ws_layout(long rows, long vocab) {
     l.off_m0 = l.off_flag + al16(n * sizeof(int32_t));
     l.off_m1 = l.off_m0 + al16(ns * sizeof(uint32_t));
     l.off_cls = l.off_m1 + al16(ns * sizeof(uint32_t));
-    l.total = l.off_cls + al16(ns * sizeof(int32_t));
+    l.off_x = l.off_cls + al16(ns * sizeof(int32_t));
+    l.total = l.off_x + al16(ns * kXWords * sizeof(uint32_t));
     return l;
 }
 
@@ -765,8 +975,10 @@ static int bind_workspace(SampleArgs& a, void* ws, size_t ws_bytes, long rows, l
     a.ws_map0 = reinterpret_cast<uint32_t*>(b + l.off_m0);
     a.ws_map1 = reinterpret_cast<uint32_t*>(b + l.off_m1);
     a.ws_cls = reinterpret_cast<int32_t*>(b + l.off_cls);
+    a.ws_xing = reinterpret_cast<uint32_t*>(b + l.off_x);
     a.nchunk = (int)((vocab + kCH - 1) / kCH);
     a.nsub = (int)((vocab + kSub - 1) / kSub);
+    a.nsub_ld = (a.nsub + 3) & ~3;
     a.shift = 63 - ceil_log2(vocab);
     return ANELM_OK;
 }
