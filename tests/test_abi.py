@@ -102,10 +102,11 @@ def test_invalid_arguments_return_status_and_message(lib):
 
 def test_workspace_sizes(lib):
     # 64 rows x 38 chunks of 4096 logits (u64 sums, f32 maxima, i32 argmax, i32 flags)
-    # + 64 rows x 594 sub-tiles of 256 (two u32 map words, i32 binade class), 16-byte aligned
+    # + 64 rows x 594 sub-tiles of 256, rows padded to 596 (two u32 map words, i32
+    # binade class, six u32 words of the predicted crossing), 16-byte aligned
     al = lambda b: (b + 15) // 16 * 16
-    n, ns = 64 * 38, 64 * 594
-    assert lib.anelm_sample_workspace_size(64, 151936) == al(n * 8) + 3 * al(n * 4) + 3 * al(ns * 4)
+    n, ns = 64 * 38, 64 * 596
+    assert lib.anelm_sample_workspace_size(64, 151936) == al(n * 8) + 3 * al(n * 4) + 3 * al(ns * 4) + al(ns * 24)
     assert lib.anelm_sample_workspace_size(0, 10) == 0
     assert lib.anelm_softmax_workspace_size(1, 4096) > 0
 
