@@ -69,6 +69,8 @@ _SIGS = {
     "anelm_sample": (_I, [_P, _P, _L, _P, _L, _L, _L, _P, _L, _P, ctypes.POINTER(SamplingParams), _P, _P, _S, _P]),
     "anelm_gqa_workspace_size": (_S, [_L, _I, _I, _I, _I]),
     "anelm_gqa_attention": (_I, [_P, _P, _P, _P, _P, _P, _L, _I, _I, _I, _L, _I, _L, _I, _L, _P, _S, _P]),
+    "anelm_gqa_attention_bounded": (_I, [_P, _P, _P, _P, _P, _P, _L, _I, _I, _I, _L, _I, _L, _I, _L, _I, _P, _S,
+                                         _P]),
     "anelm_gqa_attention_ring": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _S, _P]),
     "anelm_kv_ring_append": (_I, [_P, _P, _P, _P, _P, _P, _L, _L, _L, _I, _I, _I, _L, _P]),
     "anelm_rmsnorm_gated": (_I, [_P, _P, _P, _P, _I, _L, _I, _I, _L, _L, _L, _F, _P]),
@@ -91,6 +93,8 @@ _SIGS = {
     "anelm_blas_destroy": (None, [_P]),
     "anelm_linear_f16": (_I, [_P, _P, _P, _P, _L, _I, _I, _L, _L, _P]),
     "anelm_proj_f16": (_I, [_P, _P, _P, _L, _I, _I, _L, _L, _P]),
+    "anelm_proj_f16_x16": (_I, [_P, _P, _P, _L, _I, _I, _L, _L, _P]),
+    "anelm_proj_f16_fused": (_I, [_P, _P, _P, _L, _I, _I, _L, _L, _P, _F, _I, _P]),
     "anelm_qwen3_load": (_P, [ctypes.c_char_p, _P, _I, _I, _P]),
     "anelm_qwen3_free": (None, [_P]),
     "anelm_qwen3_reset": (_I, [_P, _P]),
@@ -295,6 +299,20 @@ def gqa_attention(out, q, k_cache, v_cache, ring_start, ring_len, n_heads, n_kv_
                                      k_cache.stride(0), _ptr(workspace), _nbytes(workspace), _stream(stream)))
 
 
+def gqa_attention_bounded(out, q, k_cache, v_cache, ring_start, ring_len, n_heads, n_kv_heads, head_dim, len_bound,
+                          workspace, q_head_stride=None, stream=None):
+    """gqa_attention when every ring length is known to be <= len_bound."""
+    B = q.shape[0]
+    cap = k_cache.shape[1]
+    _need(k_cache.stride() == v_cache.stride() and k_cache.stride(2) == 1 and k_cache.stride(1) == n_kv_heads * head_dim,
+          "gqa_attention: cache layout")
+    _check(lib().anelm_gqa_attention_bounded(_ptr(out), _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(ring_start),
+                                             _ptr(ring_len), B, n_heads, n_kv_heads, head_dim, _ld(q),
+                                             head_dim if q_head_stride is None else q_head_stride, _ld(out), cap,
+                                             k_cache.stride(0), len_bound, _ptr(workspace), _nbytes(workspace),
+                                             _stream(stream)))
+
+
 def gqa_attention_ring(out, q, k_cache, v_cache, n_heads, n_kv_heads, head_dim, cache_start, cache_len, workspace,
                        q_head_stride=None, stream=None):
     """The reference's single-sequence form (core/cpu_ops.cpp:173-240) with
@@ -446,11 +464,32 @@ class Blas:
 
 
 def proj_f16(y, x, w16, stream=None):
-    """y [B, out] fp32 = fp16(fp16(x) [B, in] . w16 [out, in]^T), B <= 8."""
+    """y [B, out] fp32 = fp16(fp16(x) [B, in] . w16 [out, in]^T)."""
     batch, in_dim = x.shape
     out_dim = w16.shape[0]
     _check(lib().anelm_proj_f16(_ptr(y), _ptr(x), _ptr(w16), batch, out_dim, in_dim, _ld(x), _ld(y),
                                 _stream(stream)))
+
+
+def proj_f16_x16(y, x16, w16, stream=None):
+    """proj_f16 with x16 [B, in] already rounded to fp16 (int16 or float16 tensor)."""
+    batch, in_dim = x16.shape
+    out_dim = w16.shape[0]
+    _check(lib().anelm_proj_f16_x16(_ptr(y), _ptr(x16), _ptr(w16), batch, out_dim, in_dim, _ld(x16), _ld(y),
+                                    _stream(stream)))
+
+
+PROJ_STORE, PROJ_ADD, PROJ_SWIGLU = 0, 1, 2
+
+
+def proj_f16_fused(y, x, w16, norm=None, eps=1e-6, epilogue=PROJ_STORE, stream=None):
+    """Decode projection (B <= 16) with an optional RMSNorm prologue (norm:
+    bf16 gamma as int16/bfloat16 tensor) and a store / residual-add / SwiGLU
+    epilogue; for SwiGLU w16 holds the gate rows then the up rows."""
+    batch, in_dim = x.shape
+    out_dim = w16.shape[0] // 2 if epilogue == PROJ_SWIGLU else w16.shape[0]
+    _check(lib().anelm_proj_f16_fused(_ptr(y), _ptr(x), _ptr(w16), batch, out_dim, in_dim, _ld(x), _ld(y),
+                                      _ptr(norm), eps, epilogue, _stream(stream)))
 
 
 class Qwen3Model:

@@ -29,6 +29,7 @@ SOURCES = [
     os.path.join(CSRC, "sampling.hip"),
     os.path.join(CSRC, "attention.hip"),
     os.path.join(CSRC, "deltanet.hip"),
+    os.path.join(CSRC, "projection.hip"),
     os.path.join(HOST, "dropin.hip"),
     os.path.join(HOST, "safetensors.hip"),
     os.path.join(HOST, "qwen3.hip"),

@@ -143,6 +143,14 @@ __device__ __forceinline__ float4 load_w4<ANELM_BF16>(const void* w, long i) {
                        bf16_to_f32(v.y & 0xFFFFu), bf16_to_f32(v.y >> 16));
 }
 
+// core/cpu_ops.cpp:7-14 form: silu(g) = g / (1 + expf(-g)) with a correctly
+// rounded divide.  Shared by the SwiGLU kernel and the projection epilogue
+// that fuses it, so both give the same bits.
+__device__ __forceinline__ float silu_ref(float g) {
+    const float t = expf(-g) + 1.0f;
+    return g / t;
+}
+
 // Non-temporal 16-byte loads / stores (streamed data that is touched once).
 typedef float nat_f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int nat_u32x4 __attribute__((ext_vector_type(4)));

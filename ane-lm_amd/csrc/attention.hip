@@ -430,7 +430,7 @@ int check_common(const void* out, const void* q, const void* kc, const void* vc,
 int run(AttnArgs a, long batch, int D, int bound, void* ws, size_t ws_bytes, hipStream_t st) {
     a.groups = a.nh / a.nkv;
     a.scale = 1.0f / sqrtf((float)D);   // core/cpu_ops.cpp:183
-    a.chunk = pick_chunk(batch * a.nkv, a.cap);
+    a.chunk = pick_chunk(batch * a.nkv, a.cap);  // from the capacity, so the workspace size holds for any bound
     a.nsplit = (bound + a.chunk - 1) / a.chunk;
     if (a.nsplit < 1) a.nsplit = 1;
     if (a.nsplit > 1) {
@@ -474,6 +474,27 @@ extern "C" int anelm_gqa_attention(float* out, const float* q, const float* k_ca
     a.q_ld = q_ld; a.q_hs = q_head_stride; a.out_ld = out_ld;
     a.cap = capacity; a.seq_stride = cache_seq_stride;
     return run(a, batch, head_dim, capacity, workspace, workspace_bytes, as_stream(stream));
+}
+
+extern "C" int anelm_gqa_attention_bounded(float* out, const float* q, const float* k_cache, const float* v_cache,
+                                           const int32_t* ring_start, const int32_t* ring_len, long batch,
+                                           int n_heads, int n_kv_heads, int head_dim, long q_ld, int q_head_stride,
+                                           long out_ld, int capacity, long cache_seq_stride, int len_bound,
+                                           void* workspace, size_t workspace_bytes, void* stream) {
+    clear_error();
+    int rc = check_common(out, q, k_cache, v_cache, batch, n_heads, n_kv_heads, head_dim, q_ld, q_head_stride,
+                          out_ld, capacity, cache_seq_stride);
+    if (rc) return rc;
+    if (!ring_start || !ring_len) return fail(ANELM_ERR_INVALID, "gqa_attention: null ring state");
+    if (len_bound <= 0) return fail(ANELM_ERR_INVALID, "gqa_attention: len_bound %d", len_bound);
+    AttnArgs a{};
+    a.out = out; a.q = q; a.kc = k_cache; a.vc = v_cache;
+    a.ring_start = ring_start; a.ring_len = ring_len;
+    a.nh = n_heads; a.nkv = n_kv_heads;
+    a.q_ld = q_ld; a.q_hs = q_head_stride; a.out_ld = out_ld;
+    a.cap = capacity; a.seq_stride = cache_seq_stride;
+    return run(a, batch, head_dim, len_bound < capacity ? len_bound : capacity, workspace, workspace_bytes,
+               as_stream(stream));
 }
 
 extern "C" int anelm_gqa_attention_ring(float* out, const float* q, const float* k_cache, const float* v_cache,

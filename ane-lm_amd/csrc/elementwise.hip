@@ -51,12 +51,8 @@ __global__ __launch_bounds__(256) void residual_add_scalar_kernel(float* x, cons
 }
 
 // ------------------------------------------------------------ SiLU family
-// core/cpu_ops.cpp:7-14 form: silu(g) = g / (1 + expf(-g)) with a correctly
-// rounded divide; SwiGLU multiplies by up (core/ane_runtime.cpp:393-395).
-__device__ __forceinline__ float silu_ref(float g) {
-    const float t = expf(-g) + 1.0f;
-    return g / t;
-}
+// silu_ref (anelm_common.hpp); SwiGLU multiplies by up
+// (core/ane_runtime.cpp:393-395).
 
 __device__ __forceinline__ float4 silu_mul4(float4 g, float4 u) {
     float4 r;

@@ -1,0 +1,442 @@
+// The ANE projections with their interface numerics (the conv-as-matvec
+// kernels of core/ane_runtime.cpp:265-408, fp16 in and out, :600-640):
+//     y[b, o] = fp16(sum_i fp16_rne(x[b, i]) * W16[o, i])   stored as fp32,
+// W16 [out_dim, in_dim] row-major fp16 (the truncating convert of the bf16
+// checkpoint), fp32 accumulation.  Decode-shaped: a handful to 64 rows of x
+// against a weight matrix that is read once, so the kernels are built
+// around streaming W at HBM speed, not around reusing it.
+//
+// MFMA path (in_dim a multiple of 32): v_mfma_f32_16x16x32_f16 with A = a
+// 16-row tile of W and B = 16 rows of x (transposed), both fed 8 fp16 per
+// lane.  Lane l supplies row (l % 16) of its operand and the 8 inputs
+// 8*(l/16) .. +7 of the current 32-input step; D holds output rows
+// 4*(l/16) + i (i = 0..3) for batch row l % 16.  A workgroup of 4 waves owns
+// 16*RT output rows and 16*NB batch rows; its waves take interleaved 32-input
+// steps (so the four read neighbouring 64-byte pieces of each weight row),
+// every wave issues the loads of R steps before its first MFMA, and the four
+// partial tiles are summed in LDS in a fixed order.  (Splitting the input
+// dimension over several workgroups per tile, with the last to finish summing
+// the partials behind a device-scope fence, measured 20 us slower per call:
+// the fence writes back the L2.  Small out_dim runs on fewer workgroups.)
+//
+// Small path (batch <= 8, any in_dim multiple of 8): one wave per output row.
+#include <hip/hip_runtime.h>
+
+#include "anelm_common.hpp"
+
+namespace anelm {
+
+namespace {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float float4v __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float r16(float v) { return (float)(_Float16)v; }
+
+__device__ __forceinline__ half8 to_half8(float4 a, float4 b) {
+    half8 r;
+    r[0] = (_Float16)a.x;
+    r[1] = (_Float16)a.y;
+    r[2] = (_Float16)a.z;
+    r[3] = (_Float16)a.w;
+    r[4] = (_Float16)b.x;
+    r[5] = (_Float16)b.y;
+    r[6] = (_Float16)b.z;
+    r[7] = (_Float16)b.w;
+    return r;
+}
+
+__device__ __forceinline__ half8 as_half8(uint4 u) {
+    half8 r;
+    __builtin_memcpy(&r, &u, 16);
+    return r;
+}
+
+struct ProjArgs {
+    float* y;
+    const void* x;  // fp32, or fp16 already rounded (XH)
+    const uint16_t* w;
+    int out_dim, in_dim, batch;
+    long ld_x, ld_y;
+    // fused prologue (kNorm): x replaced by rmsnorm(x) * gamma, gamma bf16 [in_dim]
+    const uint16_t* gamma;
+    float eps;
+    // SwiGLU epilogue (kSwiGLU): the up rows follow the gate rows at this offset
+    long pair_rows;
+};
+
+// What the epilogue does with the rounded projection p = fp16(sum) (as fp32):
+enum Epilogue {
+    kStore = 0,   // y = p
+    kAdd = 1,     // y = y + p  (the residual add of qwen3.cpp:516, :527)
+    kSwiGLU = 2,  // y = silu(p_gate) * p_up  (core/ane_runtime.cpp:393-395)
+};
+
+// kNorm (fp32 x, NB = 1): the workgroup first computes the RMSNorm scale
+// 1/sqrtf(ss/dim + eps) of each of its batch rows (core/cpu_ops.cpp:25-31),
+// and every input is formed as (x * s) * gamma before its fp16 rounding,
+// exactly the separate RMSNorm's output.  kSwiGLU needs RT = 2: tile 0 holds
+// gate rows, tile 1 the up rows pair_rows further on, and out_dim counts the
+// gate rows.
+template <bool XH, int NB, int RT, int R, bool NORM = false, int EPI = kStore, int NW = 4>
+__global__ __launch_bounds__(64 * NW) void proj_mfma_kernel(ProjArgs a) {
+    static_assert(!NORM || (!XH && NB == 1), "the fused norm reads fp32 x, one batch block");
+    static_assert(EPI != kSwiGLU || RT == 2, "SwiGLU pairs a gate tile with an up tile");
+    __shared__ float4v part[NW][RT * NB][64];
+    __shared__ float s_scale[16];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int g = lane >> 4, c = lane & 15;
+    const long row0 = (long)blockIdx.x * 16 * (EPI == kSwiGLU ? 1 : RT);
+    const int b0 = blockIdx.y * 16 * NB;
+    // operand rows, clamped: rows past the end compute values that are never stored
+    const uint16_t* wp[RT];
+#pragma unroll
+    for (int t = 0; t < RT; t++) {
+        const long r0 = EPI == kSwiGLU ? row0 + c : row0 + 16 * t + c;
+        const long r = (r0 < a.out_dim ? r0 : a.out_dim - 1) + (EPI == kSwiGLU && t == 1 ? a.pair_rows : 0);
+        wp[t] = a.w + r * a.in_dim + 8 * g;
+    }
+    long xoff[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; nb++) {
+        const int b = b0 + nb * 16 + c;
+        xoff[nb] = (long)(b < a.batch ? b : a.batch - 1) * a.ld_x + 8 * g;
+    }
+    const float* xf = static_cast<const float*>(a.x);
+    const uint16_t* xh = static_cast<const uint16_t*>(a.x);
+    const int s_end = a.in_dim / 32;  // 32-input steps
+
+    // the loads of R steps of this wave, starting at step s0
+    uint4 wr[R][RT];
+    float4 xr[R][XH ? 1 : NB][2];
+    uint4 xq[R][XH ? NB : 1];
+    uint4 gq[NORM ? R : 1];
+    auto issue = [&](int s0) {
+#pragma unroll
+        for (int j = 0; j < R; j++) {
+            const int s = s0 + NW * j;
+            const int k = 32 * (s < s_end ? s : s_end - 1);  // clamped: in bounds, result unused
+#pragma unroll
+            for (int t = 0; t < RT; t++) wr[j][t] = ld_nt(reinterpret_cast<const uint4*>(wp[t] + k));
+            if constexpr (NORM) gq[j] = *reinterpret_cast<const uint4*>(a.gamma + k + 8 * g);
+#pragma unroll
+            for (int nb = 0; nb < NB; nb++) {
+                if constexpr (XH) {
+                    xq[j][nb] = *reinterpret_cast<const uint4*>(xh + xoff[nb] + k);
+                } else {
+                    xr[j][nb][0] = *reinterpret_cast<const float4*>(xf + xoff[nb] + k);
+                    xr[j][nb][1] = *reinterpret_cast<const float4*>(xf + xoff[nb] + k + 4);
+                }
+            }
+        }
+    };
+    // the first round's loads go out before the RMSNorm prologue, whose own
+    // loads then overlap them
+    issue(wv);
+
+    if constexpr (NORM) {
+        // wave w: the tile's batch rows w, w+NW, ... that exist; each lane has
+        // four 16-byte loads in flight per round (a 1024-wide row in one)
+        const int nrows = a.batch - b0 < 16 ? a.batch - b0 : 16;
+        if (threadIdx.x < 16 && (int)threadIdx.x >= nrows) s_scale[threadIdx.x] = 0.0f;  // unused columns
+        for (int i = wv; i < nrows; i += NW) {
+            const float* xrow = xf + (long)(b0 + i) * a.ld_x;
+            float sp[4] = {0.f, 0.f, 0.f, 0.f};
+            for (int k = 4 * lane; k < a.in_dim; k += 1024) {
+                float4 v[4];
+#pragma unroll
+                for (int u = 0; u < 4; u++)
+                    v[u] = k + 256 * u < a.in_dim ? *reinterpret_cast<const float4*>(xrow + k + 256 * u)
+                                                  : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    sp[u] = fmaf(v[u].x, v[u].x, sp[u]);
+                    sp[u] = fmaf(v[u].y, v[u].y, sp[u]);
+                    sp[u] = fmaf(v[u].z, v[u].z, sp[u]);
+                    sp[u] = fmaf(v[u].w, v[u].w, sp[u]);
+                }
+            }
+            const float ss = wave_sum((sp[0] + sp[1]) + (sp[2] + sp[3]));
+            if (lane == 0) s_scale[i] = 1.0f / sqrtf(ss / (float)a.in_dim + a.eps);
+        }
+        __syncthreads();
+    }
+    const float my_scale = NORM ? s_scale[c] : 1.0f;
+
+    float4v acc[RT][NB];
+#pragma unroll
+    for (int t = 0; t < RT; t++)
+#pragma unroll
+        for (int nb = 0; nb < NB; nb++) acc[t][nb] = float4v{0.f, 0.f, 0.f, 0.f};
+    for (int s0 = wv; s0 < s_end; s0 += NW * R) {
+        if (s0 != wv) issue(s0);
+#pragma unroll
+        for (int j = 0; j < R; j++) {
+            if (s0 + NW * j < s_end) {  // wave-uniform
+#pragma unroll
+                for (int nb = 0; nb < NB; nb++) {
+                    half8 xb;
+                    if constexpr (XH) {
+                        xb = as_half8(xq[j][nb]);
+                    } else if constexpr (NORM) {
+                        const float4 u = xr[j][nb][0], v = xr[j][nb][1];
+                        const uint4 q = gq[j];
+                        float4 lo, hi;
+                        lo.x = (u.x * my_scale) * bf16_to_f32(q.x & 0xFFFFu);
+                        lo.y = (u.y * my_scale) * bf16_to_f32(q.x >> 16);
+                        lo.z = (u.z * my_scale) * bf16_to_f32(q.y & 0xFFFFu);
+                        lo.w = (u.w * my_scale) * bf16_to_f32(q.y >> 16);
+                        hi.x = (v.x * my_scale) * bf16_to_f32(q.z & 0xFFFFu);
+                        hi.y = (v.y * my_scale) * bf16_to_f32(q.z >> 16);
+                        hi.z = (v.z * my_scale) * bf16_to_f32(q.w & 0xFFFFu);
+                        hi.w = (v.w * my_scale) * bf16_to_f32(q.w >> 16);
+                        xb = to_half8(lo, hi);
+                    } else {
+                        xb = to_half8(xr[j][nb][0], xr[j][nb][1]);
+                    }
+#pragma unroll
+                    for (int t = 0; t < RT; t++)
+                        acc[t][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(wr[j][t]), xb, acc[t][nb], 0, 0, 0);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < RT; t++)
+#pragma unroll
+        for (int nb = 0; nb < NB; nb++) part[wv][t * NB + nb][lane] = acc[t][nb];
+    __syncthreads();
+    if constexpr (EPI == kSwiGLU) {
+        for (int nb = wv; nb < NB; nb += NW) {
+            float4v gs = part[0][nb][lane], us = part[0][NB + nb][lane];
+            for (int w = 1; w < NW; w++) {
+                gs += part[w][nb][lane];
+                us += part[w][NB + nb][lane];
+            }
+            const int b = b0 + nb * 16 + c;
+            const long r = row0 + 4 * g;
+            if (b < a.batch) {
+                float* yr = a.y + (long)b * a.ld_y;
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    if (r + i < a.out_dim) yr[r + i] = silu_ref(r16(gs[i])) * r16(us[i]);
+            }
+        }
+    } else {
+        for (int q = wv; q < RT * NB; q += NW) {
+            float4v s = part[0][q][lane];
+            for (int w = 1; w < NW; w++) s += part[w][q][lane];
+            const int t = q / NB, nb = q % NB;
+            const int b = b0 + nb * 16 + c;
+            const long r = row0 + 16 * t + 4 * g;
+            if (b < a.batch) {
+                float* yr = a.y + (long)b * a.ld_y;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    if (r + i < a.out_dim) {
+                        if constexpr (EPI == kAdd) yr[r + i] = yr[r + i] + r16(s[i]);
+                        else yr[r + i] = r16(s[i]);
+                    }
+                }
+            }
+        }
+    }
+}
+
+// ---- small batches, any in_dim multiple of 8 -------------------------------
+// One wave per output row; lanes cover 512 consecutive inputs per chunk (8
+// halves, one 16-byte load each), and the weight loads of up to 8 chunks are
+// issued before the first is used.  The inputs x are tiny and shared by
+// every row: they come from cache.
+template <int BT>
+__global__ __launch_bounds__(256) void proj_rows_kernel(float* y, const float* x, const uint16_t* W, int out_dim,
+                                                        int in_dim, long ld_x, long ld_y, int batch) {
+    constexpr int NC = 8;  // chunks of 512 inputs in flight
+    const int lane = threadIdx.x & 63;
+    const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= out_dim) return;
+    const uint16_t* wr = W + row * in_dim;
+    float acc[BT];
+#pragma unroll
+    for (int b = 0; b < BT; b++) acc[b] = 0.0f;
+    for (int c0 = 0; c0 < in_dim; c0 += NC * 512) {
+        uint4 wv[NC];
+#pragma unroll
+        for (int k = 0; k < NC; k++) {
+            const int c = c0 + k * 512 + lane * 8;
+            wv[k] = c < in_dim ? ld_nt(reinterpret_cast<const uint4*>(wr + c)) : make_uint4(0u, 0u, 0u, 0u);
+        }
+#pragma unroll
+        for (int k = 0; k < NC; k++) {
+            const int c = c0 + k * 512 + lane * 8;
+            if (c >= in_dim) break;  // this lane is past the end of the row (inputs are not read there)
+            const uint32_t u[4] = {wv[k].x, wv[k].y, wv[k].z, wv[k].w};
+            float wf[8];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                wf[2 * e] = f16_to_f32_exact(u[e] & 0xFFFFu);
+                wf[2 * e + 1] = f16_to_f32_exact(u[e] >> 16);
+            }
+#pragma unroll
+            for (int b = 0; b < BT; b++) {
+                if (b < batch) {
+                    const float4 p = reinterpret_cast<const float4*>(x + b * ld_x + c)[0];
+                    const float4 d = reinterpret_cast<const float4*>(x + b * ld_x + c)[1];
+                    float t = acc[b];
+                    t = fmaf(r16(p.x), wf[0], t);
+                    t = fmaf(r16(p.y), wf[1], t);
+                    t = fmaf(r16(p.z), wf[2], t);
+                    t = fmaf(r16(p.w), wf[3], t);
+                    t = fmaf(r16(d.x), wf[4], t);
+                    t = fmaf(r16(d.y), wf[5], t);
+                    t = fmaf(r16(d.z), wf[6], t);
+                    t = fmaf(r16(d.w), wf[7], t);
+                    acc[b] = t;
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int b = 0; b < BT; b++) {
+        const float s = wave_sum(acc[b]);
+        if (lane == 0 && b < batch) y[b * ld_y + row] = r16(s);
+    }
+}
+
+template <int BT>
+void launch_rows(float* y, const float* x, const uint16_t* W, int out_dim, int in_dim, long ld_x, long ld_y,
+                 int batch, hipStream_t st) {
+    proj_rows_kernel<BT><<<dim3((unsigned)((out_dim + 3) / 4)), dim3(256), 0, st>>>(y, x, W, out_dim, in_dim, ld_x,
+                                                                                     ld_y, batch);
+}
+
+// ---- MFMA launch shapes -----------------------------------------------------
+template <bool XH, int NB, int RT, int R, bool NORM = false, int EPI = kStore, int NW = 4>
+void launch_mfma(const ProjArgs& a, hipStream_t st) {
+    const int rows = 16 * (EPI == kSwiGLU ? 1 : RT);
+    const dim3 grid((unsigned)((a.out_dim + rows - 1) / rows), (unsigned)((a.batch + 16 * NB - 1) / (16 * NB)));
+    proj_mfma_kernel<XH, NB, RT, R, NORM, EPI, NW><<<grid, dim3(64 * NW), 0, st>>>(a);
+}
+
+// Up to 16 rows: one 16-row batch block, one row tile per workgroup (the
+// most workgroups), 8 steps of loads in flight per wave.  More rows: 32-row
+// batch blocks and two row tiles per workgroup, so each input fetched from
+// cache feeds twice the MFMAs.
+// Past 16 rows, 32-row batch blocks with two row tiles per workgroup (each
+// input fetched from cache feeds four MFMA tiles) where that still leaves
+// enough workgroups; shapes with few output tiles (out_dim 1024 at 64 rows:
+// 64 such workgroups) keep 16x16 tiles and four times the workgroups, which
+// measured 1.6x faster there.  (8 waves per workgroup for the few-tile
+// shapes measured 10% slower than 4.)
+template <bool XH>
+int proj_mfma(const ProjArgs& a, hipStream_t st) {
+    const long tiles16 = (long)((a.out_dim + 15) / 16) * ((a.batch + 15) / 16);
+    if (a.batch <= 16 || tiles16 < 512) launch_mfma<XH, 1, 1, 8>(a, st);
+    else launch_mfma<XH, 2, 2, XH ? 8 : 4>(a, st);
+    return launch_status("proj_f16");
+}
+
+bool mfma_ok(const void* x, bool x_f16, const uint16_t* w16, int in_dim, long ld_x) {
+    return in_dim % 32 == 0 && aligned16(x) && aligned16(w16) && ld_x % (x_f16 ? 8 : 4) == 0;
+}
+
+bool sizes_ok(long batch, int out_dim, int in_dim, long ld_x, long ld_y) {
+    return batch > 0 && batch <= 65535 * 32L && out_dim > 0 && in_dim > 0 && ld_x >= in_dim && ld_y >= out_dim &&
+           (long)out_dim * in_dim <= (1L << 40);
+}
+
+ProjArgs args(float* y, const void* x, const uint16_t* w16, long batch, int out_dim, int in_dim, long ld_x,
+              long ld_y) {
+    ProjArgs a = {};
+    a.y = y;
+    a.x = x;
+    a.w = w16;
+    a.out_dim = out_dim;
+    a.in_dim = in_dim;
+    a.batch = (int)batch;
+    a.ld_x = ld_x;
+    a.ld_y = ld_y;
+    return a;
+}
+
+}  // namespace
+
+}  // namespace anelm
+
+using namespace anelm;
+
+// fp32 in, fp32 out (holding fp16 values): the whole fp16 projection,
+// conversions included, with each weight read once.
+extern "C" int anelm_proj_f16(float* y, const float* x, const uint16_t* w16, long batch, int out_dim, int in_dim,
+                              long ld_x, long ld_y, void* stream) {
+    clear_error();
+    if (!y || !x || !w16) return fail(ANELM_ERR_INVALID, "proj_f16: null pointer");
+    if (!sizes_ok(batch, out_dim, in_dim, ld_x, ld_y)) return fail(ANELM_ERR_INVALID, "proj_f16: bad sizes or strides");
+    hipStream_t st = as_stream(stream);
+    if (mfma_ok(x, false, w16, in_dim, ld_x))
+        return proj_mfma<false>(args(y, x, w16, batch, out_dim, in_dim, ld_x, ld_y), st);
+    if (batch > 8 || in_dim % 8 || ld_x % 4 || !aligned16(x) || !aligned16(w16))
+        return fail(ANELM_ERR_INVALID,
+                    "proj_f16: needs in_dim a multiple of 32 (or batch <= 8 and in_dim a multiple of 8), "
+                    "ld_x a multiple of 4, 16-byte aligned x and W");
+    const int b = (int)batch;
+    if (b == 1) launch_rows<1>(y, x, w16, out_dim, in_dim, ld_x, ld_y, b, st);
+    else if (b == 2) launch_rows<2>(y, x, w16, out_dim, in_dim, ld_x, ld_y, b, st);
+    else if (b <= 4) launch_rows<4>(y, x, w16, out_dim, in_dim, ld_x, ld_y, b, st);
+    else launch_rows<8>(y, x, w16, out_dim, in_dim, ld_x, ld_y, b, st);
+    return launch_status("proj_f16");
+}
+
+// The same with x already rounded to fp16 (e.g. by anelm_f32_to_f16): for
+// larger batches, where rounding x once beats rounding it in every workgroup.
+extern "C" int anelm_proj_f16_x16(float* y, const uint16_t* x16, const uint16_t* w16, long batch, int out_dim,
+                                  int in_dim, long ld_x, long ld_y, void* stream) {
+    clear_error();
+    if (!y || !x16 || !w16) return fail(ANELM_ERR_INVALID, "proj_f16_x16: null pointer");
+    if (!sizes_ok(batch, out_dim, in_dim, ld_x, ld_y))
+        return fail(ANELM_ERR_INVALID, "proj_f16_x16: bad sizes or strides");
+    if (!mfma_ok(x16, true, w16, in_dim, ld_x))
+        return fail(ANELM_ERR_INVALID,
+                    "proj_f16_x16: needs in_dim a multiple of 32, ld_x a multiple of 8, 16-byte aligned x and W");
+    return proj_mfma<true>(args(y, x16, w16, batch, out_dim, in_dim, ld_x, ld_y), as_stream(stream));
+}
+
+// Decode-step projections with the neighbouring layer ops fused in, for up
+// to 16 rows (see the header): the RMSNorm before a projection, the residual
+// add after one, the SwiGLU between the gate|up and down projections.
+extern "C" int anelm_proj_f16_fused(float* y, const float* x, const uint16_t* w16, long batch, int out_dim,
+                                    int in_dim, long ld_x, long ld_y, const uint16_t* norm_bf16, float eps,
+                                    int epilogue, void* stream) {
+    clear_error();
+    if (!y || !x || !w16) return fail(ANELM_ERR_INVALID, "proj_f16_fused: null pointer");
+    if (batch > 16 || !sizes_ok(batch, out_dim, in_dim, ld_x, ld_y))
+        return fail(ANELM_ERR_INVALID, "proj_f16_fused: batch 1..16, sizes and strides");
+    if (!mfma_ok(x, false, w16, in_dim, ld_x) || (norm_bf16 && !aligned16(norm_bf16)))
+        return fail(ANELM_ERR_INVALID,
+                    "proj_f16_fused: needs in_dim a multiple of 32, ld_x a multiple of 4, 16-byte aligned x, W, gamma");
+    if (epilogue < ANELM_PROJ_STORE || epilogue > ANELM_PROJ_SWIGLU)
+        return fail(ANELM_ERR_INVALID, "proj_f16_fused: unknown epilogue %d", epilogue);
+    if (epilogue == ANELM_PROJ_ADD && (const void*)y == (const void*)x)
+        return fail(ANELM_ERR_INVALID, "proj_f16_fused: the residual add needs y distinct from x");
+    ProjArgs a = args(y, x, w16, batch, out_dim, in_dim, ld_x, ld_y);
+    a.gamma = norm_bf16;
+    a.eps = eps;
+    a.pair_rows = out_dim;  // SwiGLU: W holds out_dim gate rows, then out_dim up rows
+    hipStream_t st = as_stream(stream);
+    const bool norm = norm_bf16 != nullptr;
+    switch (epilogue) {
+        case ANELM_PROJ_STORE:
+            if (norm) launch_mfma<false, 1, 1, 8, true, kStore>(a, st);
+            else launch_mfma<false, 1, 1, 8, false, kStore>(a, st);
+            break;
+        case ANELM_PROJ_ADD:
+            if (norm) launch_mfma<false, 1, 1, 8, true, kAdd>(a, st);
+            else launch_mfma<false, 1, 1, 8, false, kAdd>(a, st);
+            break;
+        default:
+            if (norm) launch_mfma<false, 1, 2, 8, true, kSwiGLU>(a, st);
+            else launch_mfma<false, 1, 2, 8, false, kSwiGLU>(a, st);
+            break;
+    }
+    return launch_status("proj_f16_fused");
+}

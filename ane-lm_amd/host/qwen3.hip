@@ -2,11 +2,13 @@
 // models/llm/qwen3.cpp:497-564 with every activation kept in HBM, the
 // library's layer-op kernels between the contractions, and the ANE
 // contractions (core/ane_runtime.cpp:265-408: fused q|k|v, o_proj,
-// gate|up -> down, the LM head) as rocBLAS fp16 GEMMs with fp32
-// accumulation.  The ANE's interface numerics are kept: weights are the
-// truncating fp16 convert of the bf16 checkpoint (the blobs), activations
-// enter a projection as round-to-nearest fp16 and leave it as fp16
-// (core/ane_runtime.cpp:600-640).
+// gate|up -> down, the LM head) as fp16 MFMA projections with fp32
+// accumulation (projection.hip; rocBLAS for shapes it does not take).  The
+// ANE's interface numerics are kept: weights are the truncating fp16 convert
+// of the bf16 checkpoint (the blobs), activations enter a projection as
+// round-to-nearest fp16 and leave it as fp16 (core/ane_runtime.cpp:600-640).
+// Up to 16 sequences, the RMSNorms, residual adds and the SwiGLU are fused
+// into the projections: 7 launches per layer instead of 13.
 //
 // A step processes one token of each of `batch` sequences; every sequence
 // has its own KV ring per layer (qwen3.cpp:227-231, 475-488).
@@ -72,103 +74,6 @@ extern "C" int anelm_linear_f16(anelm_blas* b, uint16_t* y16, const uint16_t* x1
 }
 
 namespace {
-template <int BT>
-void launch_proj(float* y, const float* x, const uint16_t* W, int out_dim, int in_dim, long ld_x, long ld_y,
-                 int batch, hipStream_t st);
-}
-
-// fp32 in, fp32 out (holding fp16 values): the whole fp16 projection of
-// anelm_linear_f16 including the conversions, for batch <= 8.
-extern "C" int anelm_proj_f16(float* y, const float* x, const uint16_t* w16, long batch, int out_dim, int in_dim,
-                              long ld_x, long ld_y, void* stream) {
-    clear_error();
-    if (!y || !x || !w16) return fail(ANELM_ERR_INVALID, "proj_f16: null pointer");
-    if (batch <= 0 || batch > 8 || out_dim <= 0 || in_dim <= 0 || in_dim % 8 || ld_x < in_dim || ld_y < out_dim ||
-        ld_x % 4)
-        return fail(ANELM_ERR_INVALID, "proj_f16: batch 1..8, in_dim a multiple of 8, ld_x a multiple of 4");
-    if (!anelm::aligned16(x) || !anelm::aligned16(w16)) return fail(ANELM_ERR_INVALID, "proj_f16: alignment");
-    hipStream_t st = anelm::as_stream(stream);
-    const int b = (int)batch;
-    if (b == 1) launch_proj<1>(y, x, w16, out_dim, in_dim, ld_x, ld_y, b, st);
-    else if (b == 2) launch_proj<2>(y, x, w16, out_dim, in_dim, ld_x, ld_y, b, st);
-    else if (b <= 4) launch_proj<4>(y, x, w16, out_dim, in_dim, ld_x, ld_y, b, st);
-    else launch_proj<8>(y, x, w16, out_dim, in_dim, ld_x, ld_y, b, st);
-    return anelm::launch_status("proj_f16");
-}
-
-namespace {
-
-// ---- small-batch projection ------------------------------------------------
-// y[b, o] = fp16(sum_i fp16(x[b, i]) * W16[o, i]) for batch <= 8, written as
-// fp32: the input rounding, fp32 accumulation and output rounding of the
-// fp16 path in one kernel, reading each weight once.  One wave per output
-// row; lanes cover 512 consecutive inputs per chunk (8 halves, one 16-byte
-// load each), and the weight loads of up to 8 chunks are issued before the
-// first is used, so a row of up to 4096 inputs is in flight at once.  The
-// inputs x are tiny and shared by every row: they come from cache.
-__device__ __forceinline__ float r16(float v) { return (float)(_Float16)v; }
-
-template <int BT>
-__global__ __launch_bounds__(256) void proj_f16_kernel(float* y, const float* x, const uint16_t* W, int out_dim,
-                                                       int in_dim, long ld_x, long ld_y, int batch) {
-    constexpr int NC = 8;   // chunks of 512 inputs in flight
-    const int lane = threadIdx.x & 63;
-    const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (row >= out_dim) return;
-    const uint16_t* wr = W + row * in_dim;
-    float acc[BT];
-#pragma unroll
-    for (int b = 0; b < BT; b++) acc[b] = 0.0f;
-    for (int c0 = 0; c0 < in_dim; c0 += NC * 512) {
-        uint4 wv[NC];
-#pragma unroll
-        for (int k = 0; k < NC; k++) {
-            const int c = c0 + k * 512 + lane * 8;
-            wv[k] = c < in_dim ? anelm::ld_nt(reinterpret_cast<const uint4*>(wr + c)) : make_uint4(0u, 0u, 0u, 0u);
-        }
-#pragma unroll
-        for (int k = 0; k < NC; k++) {
-            const int c = c0 + k * 512 + lane * 8;
-            if (c >= in_dim) break;   // this lane is past the end of the row (inputs are not read there)
-            const uint32_t u[4] = {wv[k].x, wv[k].y, wv[k].z, wv[k].w};
-            float wf[8];
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                wf[2 * e] = anelm::f16_to_f32_exact(u[e] & 0xFFFFu);
-                wf[2 * e + 1] = anelm::f16_to_f32_exact(u[e] >> 16);
-            }
-#pragma unroll
-            for (int b = 0; b < BT; b++) {
-                if (b < batch) {
-                    const float4 a = reinterpret_cast<const float4*>(x + b * ld_x + c)[0];
-                    const float4 d = reinterpret_cast<const float4*>(x + b * ld_x + c)[1];
-                    float t = acc[b];
-                    t = fmaf(r16(a.x), wf[0], t);
-                    t = fmaf(r16(a.y), wf[1], t);
-                    t = fmaf(r16(a.z), wf[2], t);
-                    t = fmaf(r16(a.w), wf[3], t);
-                    t = fmaf(r16(d.x), wf[4], t);
-                    t = fmaf(r16(d.y), wf[5], t);
-                    t = fmaf(r16(d.z), wf[6], t);
-                    t = fmaf(r16(d.w), wf[7], t);
-                    acc[b] = t;
-                }
-            }
-        }
-    }
-#pragma unroll
-    for (int b = 0; b < BT; b++) {
-        const float s = anelm::wave_sum(acc[b]);
-        if (lane == 0 && b < batch) y[b * ld_y + row] = r16(s);
-    }
-}
-
-template <int BT>
-void launch_proj(float* y, const float* x, const uint16_t* W, int out_dim, int in_dim, long ld_x, long ld_y,
-                 int batch, hipStream_t st) {
-    hipLaunchKernelGGL((proj_f16_kernel<BT>), dim3((unsigned)((out_dim + 3) / 4)), dim3(256), 0, st, y, x, W,
-                       out_dim, in_dim, ld_x, ld_y, batch);
-}
 
 constexpr int kRopeRows = 16384;   // min(max_position_embeddings, 16384), qwen3.cpp:201
 
@@ -203,6 +108,7 @@ struct anelm_qwen3 {
     uint16_t *a16, *y16;
     void* attn_ws = nullptr;
     size_t attn_ws_bytes = 0;
+
 
     void* alloc(size_t bytes) {
         DevBuf* d = new DevBuf();
@@ -391,6 +297,15 @@ extern "C" int anelm_qwen3_forward(anelm_qwen3* m, const int32_t* ids, const int
     // x16 = RNE fp16 of the [B, n] fp32 input; y16 = the projection; out = widened y16
     auto project = [&](float* out, long ld_out, const float* in, long n_in, const uint16_t* w16, long n_out) -> int {
         int r;
+        // MFMA kernel; past 16 rows the inputs are rounded to fp16 once instead
+        // of in every workgroup.  rocBLAS keeps the LM head past 16 rows: with
+        // 151936 outputs its tiles reuse each input row better (77 us against
+        // 200 us at 64 rows).
+        if (n_in % 32 == 0 && (B <= 16 || n_out <= 65536)) {
+            if (B <= 16) return anelm_proj_f16(out, in, w16, B, (int)n_out, (int)n_in, n_in, ld_out, stream);
+            if ((r = anelm_f32_to_f16(m->a16, in, (size_t)(B * n_in), stream))) return r;
+            return anelm_proj_f16_x16(out, m->a16, w16, B, (int)n_out, (int)n_in, n_in, ld_out, stream);
+        }
         if (B <= 8) return anelm_proj_f16(out, in, w16, B, (int)n_out, (int)n_in, n_in, ld_out, stream);
         if ((r = anelm_f32_to_f16(m->a16, in, (size_t)(B * n_in), stream))) return r;
         if ((r = anelm_linear_f16(m->blas, m->y16, m->a16, w16, B, (int)n_out, (int)n_in, n_in, n_out, stream)))
@@ -401,6 +316,32 @@ extern "C" int anelm_qwen3_forward(anelm_qwen3* m, const int32_t* ids, const int
         return ANELM_OK;
     };
     CK(anelm_embed_gather(m->x, m->embed, ANELM_BF16, ids, B, H, V, bad_ids, stream));             // :498
+    const bool fused = B <= 16 && H % 32 == 0 && I % 32 == 0 && m->qdim % 32 == 0;
+    if (fused) {
+        // 7 launches per layer: the RMSNorms, residual adds and the SwiGLU
+        // ride in the projections (anelm_proj_f16_fused)
+        for (int L = 0; L < c.layers; L++) {
+            const anelm_qwen3::Layer& l = m->layers[L];
+            CK(anelm_proj_f16_fused(m->qkv, m->x, l.qkv16, B, m->qkvdim, (int)H, H, m->qkvdim, l.w_in, c.rms_eps,
+                                    ANELM_PROJ_STORE, stream));                                   // :503 + first_proj
+            CK(anelm_qknorm_rope(m->qkv, m->qkv + m->qdim, m->qkvdim, m->qkvdim, l.qn, l.kn, ANELM_BF16, pos,
+                                 m->cos_tab, m->sin_tab, kRopeRows, c.rope_theta, B, c.n_q_heads, c.n_kv_heads, D,
+                                 c.rms_eps, stream));                                             // :444-472
+            CK(anelm_kv_ring_append(l.kc, l.vc, l.start, l.len, m->qkv + m->qdim, m->qkv + m->qdim + m->kvdim,
+                                    m->qkvdim, m->qkvdim, B, c.n_kv_heads, D, m->cap, seq, stream));  // :475-488
+            CK(anelm_gqa_attention(m->attn, m->qkv, l.kc, l.vc, l.start, l.len, B, c.n_q_heads, c.n_kv_heads, D,
+                                   m->qkvdim, D, m->qdim, m->cap, seq, m->attn_ws, m->attn_ws_bytes, stream));  // :490
+            CK(anelm_proj_f16_fused(m->x, m->attn, l.o16, B, (int)H, m->qdim, m->qdim, H, nullptr, 0.0f,
+                                    ANELM_PROJ_ADD, stream));                                     // o_proj + :516
+            CK(anelm_proj_f16_fused(m->h, m->x, l.gu16, B, (int)I, (int)H, H, I, l.w_post, c.rms_eps,
+                                    ANELM_PROJ_SWIGLU, stream));                                  // :518 + fused_ffn
+            CK(anelm_proj_f16_fused(m->x, m->h, l.down16, B, (int)H, (int)I, I, H, nullptr, 0.0f, ANELM_PROJ_ADD,
+                                    stream));                                                     // down + :527
+        }
+        CK(anelm_proj_f16_fused(logits, m->x, m->lm16, B, (int)V, (int)H, H, ld_logits, m->final_norm, c.rms_eps,
+                                ANELM_PROJ_STORE, stream));                                       // :530 + LM head
+        return ANELM_OK;
+    }
     for (int L = 0; L < c.layers; L++) {
         const anelm_qwen3::Layer& l = m->layers[L];
         CK(anelm_rmsnorm(m->xn, m->x, l.w_in, ANELM_BF16, B, (int)H, H, H, c.rms_eps, stream));    // :503

@@ -227,6 +227,17 @@ int anelm_gqa_attention(float* out, const float* q, const float* k_cache, const 
                         int n_kv_heads, int head_dim, long q_ld, int q_head_stride, long out_ld,
                         int capacity, long cache_seq_stride, void* workspace, size_t workspace_bytes,
                         void* stream);
+/* anelm_gqa_attention for callers that know an upper bound on every ring's
+ * length (len_bound >= ring_len[b] for all b; e.g. the tokens decoded since
+ * the rings were emptied): only ceil(len_bound / chunk) chunks per sequence
+ * are launched, and with one chunk no merge kernel runs.  A ring longer than
+ * len_bound is only partly attended.  No counterpart in the reference (its
+ * loop already runs over the live rows only, core/cpu_ops.cpp:186-188). */
+int anelm_gqa_attention_bounded(float* out, const float* q, const float* k_cache, const float* v_cache,
+                                const int32_t* ring_start, const int32_t* ring_len, long batch, int n_heads,
+                                int n_kv_heads, int head_dim, long q_ld, int q_head_stride, long out_ld,
+                                int capacity, long cache_seq_stride, int len_bound, void* workspace,
+                                size_t workspace_bytes, void* stream);
 /* The reference's own single-sequence form, with the ring state as host
  * integers (its exact argument list, core/cpu_ops.h:53-56); caches
  * [cache_capacity, n_kv_heads, head_dim]; out [n_heads, head_dim].
@@ -335,12 +346,40 @@ void anelm_blas_destroy(anelm_blas* blas);
 int anelm_linear_f16(anelm_blas* blas, uint16_t* y16, const uint16_t* x16, const uint16_t* w16, long batch,
                      int out_dim, int in_dim, long ld_x, long ld_y, void* stream);
 
-/* The same projection with the conversions fused, for batch <= 8 (decode):
+/* The same projection with the conversions fused (decode batches):
  * y[b, o] = fp16(sum_i fp16_rne(x[b, i]) * W16[o, i]) stored as fp32, x fp32;
- * each weight is read once.  in_dim a multiple of 8, ld_x a multiple of 4,
+ * each weight is read once.  in_dim a multiple of 32 (MFMA kernel, any
+ * batch), or batch <= 8 and in_dim a multiple of 8; ld_x a multiple of 4;
  * x and W16 16-byte aligned. */
 int anelm_proj_f16(float* y, const float* x, const uint16_t* w16, long batch, int out_dim, int in_dim, long ld_x,
                    long ld_y, void* stream);
+/* anelm_proj_f16 with x already rounded to fp16 (x16 [batch, in_dim], row
+ * stride ld_x a multiple of 8, e.g. from anelm_f32_to_f16): for larger
+ * batches, where rounding x once beats rounding it in every workgroup.
+ * in_dim a multiple of 32.  No counterpart in the reference (the ANE runtime
+ * has no batched projection). */
+int anelm_proj_f16_x16(float* y, const uint16_t* x16, const uint16_t* w16, long batch, int out_dim, int in_dim,
+                       long ld_x, long ld_y, void* stream);
+
+/* Decode-step projections (batch <= 16, fp32 x, in_dim a multiple of 32)
+ * with the neighbouring layer ops of models/llm/qwen3.cpp:497-530 fused in,
+ * so a layer is 7 launches instead of 13.  With p the rounded projection of
+ * anelm_proj_f16:
+ *   norm_bf16 != NULL: x is first replaced by rmsnorm(x) * norm_bf16
+ *     (core/cpu_ops.cpp:25-31 with eps; norm_bf16 [in_dim], 16-byte aligned);
+ *   ANELM_PROJ_STORE:  y = p;
+ *   ANELM_PROJ_ADD:    y = y + p (the residual add; y distinct from x);
+ *   ANELM_PROJ_SWIGLU: W16 holds out_dim gate rows then out_dim up rows, and
+ *     y = silu(p_gate) * p_up (the SwiGLU of core/ane_runtime.cpp:393-395 in
+ *     the fp32 form of core/cpu_ops.cpp:7-14).
+ * Each result equals the separate kernels' to within the RMSNorm's
+ * summation order.  No counterpart in the reference: the ANE runtime fuses
+ * these inside its own fp16 programs. */
+#define ANELM_PROJ_STORE 0
+#define ANELM_PROJ_ADD 1
+#define ANELM_PROJ_SWIGLU 2
+int anelm_proj_f16_fused(float* y, const float* x, const uint16_t* w16, long batch, int out_dim, int in_dim,
+                         long ld_x, long ld_y, const uint16_t* norm_bf16, float eps, int epilogue, void* stream);
 
 /* Qwen3 model shape (the config.json fields of models/llm/qwen3.cpp:55-80). */
 typedef struct anelm_qwen3_config {

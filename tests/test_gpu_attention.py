@@ -113,6 +113,28 @@ def test_batched_other_shapes(hip, orc, rng, B, nq, nk, D, cap):
         check(got[b], q[b], kc[b], vc[b], nq, nk, D, int(starts[b]), int(lens[b]), orc)
 
 
+@pytest.mark.parametrize("B,cap,bound", [(1, 2048, 30), (1, 2048, 700), (64, 2048, 33), (3, 4096, 4096)])
+def test_bounded_launch(hip, orc, rng, B, cap, bound):
+    """Every ring no longer than the bound: the bounded launch (fewer chunks;
+    no merge kernel when one chunk suffices) matches the oracle like the full
+    one does."""
+    import torch
+
+    nq, nk, D = 16, 8, 128
+    starts = rng.integers(0, cap, B).astype(np.int32)
+    lens = rng.integers(0, bound + 1, B).astype(np.int32)
+    lens[0] = bound
+    q = rng.standard_normal((B, nq * D)).astype(np.float32)
+    kc = rng.standard_normal((B, cap, nk * D)).astype(np.float32)
+    vc = rng.standard_normal((B, cap, nk * D)).astype(np.float32)
+    ws = torch.empty(max(hip.gqa_workspace_size(B, nq, nk, D, cap), 16), dtype=torch.uint8, device="cuda")
+    out = torch.empty(B, nq * D, device="cuda")
+    hip.gqa_attention_bounded(out, dev(q), dev(kc), dev(vc), dev(starts), dev(lens), nq, nk, D, bound, ws)
+    got = host(out).reshape(B, nq, D)
+    for b in range(min(B, 8)):
+        check(got[b], q[b], kc[b], vc[b], nq, nk, D, int(starts[b]), int(lens[b]), orc)
+
+
 def test_ring_append_matches_oracle(hip, orc, rng):
     import torch
 

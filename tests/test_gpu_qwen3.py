@@ -8,7 +8,7 @@ KV rings (the fp16 rounding points are where the two can part by an ulp)."""
 import numpy as np
 import pytest
 
-from helpers import assert_bitexact, dev, host, save_qwen3, tiny_qwen3
+from helpers import assert_bitexact, bf16, dev, from_bf16, host, save_qwen3, tiny_qwen3
 
 pytestmark = pytest.mark.gpu
 
@@ -50,8 +50,23 @@ def test_linear_f16_within_one_ulp(hip, orc, rng, B, out_dim, in_dim):
     assert np.mean(got != ref) < 0.01
 
 
+def check_projection(orc, x, w, got):
+    """got (float64 of the fp32 outputs) against the oracle's fp16 projection:
+    the outputs are fp16 values, within one fp16 ulp of the exactly rounded
+    result plus what an fp32 accumulation may differ from the exact sum by."""
+    B, in_dim = x.shape
+    x16 = orc.f32_to_f16_rne(x).reshape(B, in_dim)
+    ref = orc.linear_f16(x16, w).view(np.float16).astype(np.float64)
+    assert np.array_equal(got.astype(np.float16).astype(np.float64), got)      # outputs are fp16 values
+    ulp = np.spacing(np.abs(ref).astype(np.float16)).astype(np.float64)
+    mag = np.abs(x16.view(np.float16).astype(np.float64)) @ np.abs(w.view(np.float16).astype(np.float64)).T
+    assert np.all(np.abs(got - ref) <= ulp + mag * 2.0 ** -21 * 4)
+
+
+# (in_dim % 32 == 0: MFMA kernel; otherwise the row kernel for batch <= 8)
 @pytest.mark.parametrize("B,out_dim,in_dim", [(1, 4096, 1024), (3, 1024, 3072), (8, 6144, 1024), (2, 77, 1000),
-                                               (1, 151936, 1024), (5, 1024, 2048)])
+                                               (1, 151936, 1024), (5, 1024, 2048), (16, 1000, 96), (17, 3072, 1024),
+                                               (64, 4096, 1024), (33, 100, 32), (4, 64, 1000)])
 def test_proj_f16_fused_conversions(hip, orc, rng, B, out_dim, in_dim):
     import torch
 
@@ -59,13 +74,93 @@ def test_proj_f16_fused_conversions(hip, orc, rng, B, out_dim, in_dim):
     w = (0.03 * rng.standard_normal((out_dim, in_dim))).astype(np.float16).view(np.uint16)
     y = torch.empty(B, out_dim, device="cuda")
     hip.proj_f16(y, dev(x), dev(w))
-    got = host(y).astype(np.float64)
-    x16 = orc.f32_to_f16_rne(x).reshape(B, in_dim)
+    check_projection(orc, x, w, host(y).astype(np.float64))
+
+
+@pytest.mark.parametrize("B,out_dim,in_dim", [(64, 1024, 3072), (40, 6144, 1024), (17, 2560, 9728),
+                                               (64, 151936, 1024), (1, 48, 64), (33, 100, 32)])
+def test_proj_f16_x16_inputs(hip, orc, rng, B, out_dim, in_dim):
+    """Inputs rounded to fp16 beforehand (the oracle's RNE convert) give the
+    same projection as fp32 inputs rounded inside; two calls in a row, the
+    second with a smaller batch."""
+    import torch
+
+    w = (0.03 * rng.standard_normal((out_dim, in_dim))).astype(np.float16).view(np.uint16)
+    dw = dev(w)
+    for b in (B, max(1, B // 3)):
+        x = rng.standard_normal((b, in_dim)).astype(np.float32)
+        x16 = dev(orc.f32_to_f16_rne(x).reshape(b, in_dim).view(np.int16))
+        y = torch.full((b, out_dim), float("nan"), device="cuda")
+        hip.proj_f16_x16(y, x16, dw)
+        check_projection(orc, x, w, host(y).astype(np.float64))
+
+
+def _proj_ref(orc, x, w):
+    """The oracle's rounded projection (float64 of fp16 values) and the term
+    magnitudes sum |x16| |w| that bound an fp32 accumulation's error."""
+    B, in_dim = x.shape
+    x16 = orc.f32_to_f16_rne(np.ascontiguousarray(x, np.float32)).reshape(B, in_dim)
     ref = orc.linear_f16(x16, w).view(np.float16).astype(np.float64)
-    assert np.array_equal(got.astype(np.float16).astype(np.float64), got)      # outputs are fp16 values
-    ulp = np.spacing(np.abs(ref).astype(np.float16)).astype(np.float64)
     mag = np.abs(x16.view(np.float16).astype(np.float64)) @ np.abs(w.view(np.float16).astype(np.float64)).T
-    assert np.all(np.abs(got - ref) <= ulp + mag * 2.0 ** -21 * 4)
+    return ref, mag
+
+
+def _ulp16(v):
+    return np.spacing(np.abs(v).astype(np.float16)).astype(np.float64)
+
+
+@pytest.mark.parametrize("B,out_dim,in_dim", [(1, 1024, 1024), (11, 4096, 1024), (16, 300, 256), (3, 151936, 1024)])
+def test_proj_fused_rmsnorm_prologue(hip, orc, rng, B, out_dim, in_dim):
+    """The fused RMSNorm equals the oracle's RMSNorm followed by the
+    projection (the normalised row rounded to fp16 on the way in)."""
+    import torch
+
+    x = (2 * rng.standard_normal((B, in_dim))).astype(np.float32)
+    gamma = bf16(1 + 0.1 * rng.standard_normal(in_dim))
+    w = (0.03 * rng.standard_normal((out_dim, in_dim))).astype(np.float16).view(np.uint16)
+    y = torch.full((B, out_dim), float("nan"), device="cuda")
+    hip.proj_f16_fused(y, dev(x), dev(w), norm=dev(gamma.view(np.int16)), eps=1e-6)
+    xn = np.stack([orc.rmsnorm(x[b], from_bf16(gamma), 1e-6) for b in range(B)])
+    check_projection(orc, xn, w, host(y).astype(np.float64))
+
+
+@pytest.mark.parametrize("B,out_dim,in_dim", [(1, 1024, 2048), (7, 1024, 3072), (16, 256, 512)])
+def test_proj_fused_residual_add(hip, orc, rng, B, out_dim, in_dim):
+    import torch
+
+    x = rng.standard_normal((B, in_dim)).astype(np.float32)
+    w = (0.03 * rng.standard_normal((out_dim, in_dim))).astype(np.float16).view(np.uint16)
+    r0 = rng.standard_normal((B, out_dim)).astype(np.float32)
+    y = dev(r0)
+    hip.proj_f16_fused(y, dev(x), dev(w), epilogue=hip.PROJ_ADD)
+    ref, mag = _proj_ref(orc, x, w)
+    want = r0.astype(np.float64) + ref
+    got = host(y).astype(np.float64)
+    tol = _ulp16(ref) + mag * 2.0 ** -21 * 4 + np.spacing(np.abs(want).astype(np.float32))
+    assert np.all(np.abs(got - want) <= tol)
+
+
+@pytest.mark.parametrize("B,inter,in_dim,norm", [(1, 3072, 1024, True), (5, 384, 256, True), (16, 160, 64, False)])
+def test_proj_fused_swiglu(hip, orc, rng, B, inter, in_dim, norm):
+    """gate|up projection with the SwiGLU epilogue: silu(g) * u of the rounded
+    gate and up projections, in the fp32 form of core/cpu_ops.cpp:7-14."""
+    import torch
+
+    x = (2 * rng.standard_normal((B, in_dim))).astype(np.float32)
+    gamma = bf16(1 + 0.1 * rng.standard_normal(in_dim))
+    w = (0.05 * rng.standard_normal((2 * inter, in_dim))).astype(np.float16).view(np.uint16)
+    h = torch.full((B, inter), float("nan"), device="cuda")
+    hip.proj_f16_fused(h, dev(x), dev(w), norm=dev(gamma.view(np.int16)) if norm else None, eps=1e-6,
+                       epilogue=hip.PROJ_SWIGLU)
+    xn = np.stack([orc.rmsnorm(x[b], from_bf16(gamma), 1e-6) for b in range(B)]) if norm else x
+    gu, mag = _proj_ref(orc, xn, w)
+    g, u, mg, mu = gu[:, :inter], gu[:, inter:], mag[:, :inter], mag[:, inter:]
+    want = g / (1 + np.exp(-g)) * u
+    # each rounded projection may be off by its tolerance; silu' <= 1.1
+    eg = _ulp16(g) + mg * 2.0 ** -21 * 4
+    eu = _ulp16(u) + mu * 2.0 ** -21 * 4
+    tol = 1.1 * eg * np.abs(u) + np.abs(g / (1 + np.exp(-g))) * eu + eg * eu + np.abs(want) * 1e-6 + 1e-30
+    assert np.all(np.abs(host(h).astype(np.float64) - want) <= tol)
 
 
 @pytest.mark.parametrize("tied,B", [(True, 3), (False, 3), (True, 11)])
