@@ -161,6 +161,28 @@ def test_attention_argument_checks(lib):
     assert a(fake, fake, fake, fake, fake, fake, 1000, 1024, 4, 8, 128, 2048, 2048 * 1024, None) == -1  # k_ld < row
 
 
+def test_projection_argument_checks(lib):
+    """Validation of the projection entry points (no launch happens)."""
+    P = ctypes.c_void_p
+    fake, odd = P(0x1000), P(0x1008)
+    f, x16, fu = lib.anelm_proj_f16, lib.anelm_proj_f16_x16, lib.anelm_proj_f16_fused
+    assert f(fake, None, fake, 1, 64, 64, 64, 64, None) == -1
+    assert f(fake, fake, fake, 0, 64, 64, 64, 64, None) == -1                   # batch 0
+    assert f(fake, fake, fake, 2, 64, 64, 32, 64, None) == -1                   # ld_x < in_dim
+    assert f(fake, fake, fake, 9, 64, 72, 72, 64, None) == -1                   # in_dim % 32 and batch > 8
+    assert f(fake, odd, fake, 2, 64, 40, 40, 64, None) == -1                    # unaligned x, row path
+    assert x16(fake, fake, fake, 4, 64, 48, 48, 64, None) == -1                 # in_dim not a multiple of 32
+    assert x16(fake, fake, fake, 4, 64, 64, 68, 64, None) == -1                 # fp16 row stride not 16 bytes
+    assert fu(fake, fake, fake, 17, 64, 64, 64, 64, None, 1e-6, 0, None) == -1  # batch > 16
+    assert fu(fake, fake, fake, 1, 64, 64, 64, 64, None, 1e-6, 3, None) == -1   # no such epilogue
+    assert fu(fake, fake, fake, 1, 64, 64, 64, 64, odd, 1e-6, 0, None) == -1    # unaligned gamma
+    assert fu(fake, fake, fake, 1, 64, 64, 64, 64, None, 1e-6, 1, None) == -1   # residual add onto its own input
+    assert b"residual" in lib.anelm_last_error()
+    b = lib.anelm_gqa_attention_bounded
+    assert b(fake, fake, fake, fake, fake, fake, 1, 32, 8, 128, 4096, 128, 4096, 2048, 2048 * 1024, 0, fake,
+             1 << 30, None) == -1                                               # bound 0
+
+
 def test_deltanet_argument_checks(lib):
     fake = ctypes.c_void_p(0x1000)
     assert lib.anelm_rmsnorm_gated(fake, fake, fake, fake, 5, 4, 1, 128, 128, 128, 128, 1e-6, None) == -1  # dtype
