@@ -56,6 +56,7 @@ struct SampleArgs {
     uint32_t* ws_map1;    // [rows, nsub] sub-tile map, odd start
     int32_t* ws_cls;      // [rows, nsub] predicted binade class (-1: none)
     uint32_t* ws_xing;    // [rows, nsub, kXWords] predicted crossing (see predict_crossing)
+    int32_t* ws_first;    // [rows, 2] sub-tile 0 walked by stage 3: hit index or -1, end bits
     int nchunk;
     int nsub;
     int nsub_ld;          // row stride of the sub-tile arrays: nsub rounded up to 4 (16-byte rows)
@@ -598,6 +599,9 @@ __device__ __forceinline__ Crossing predict_crossing(Fn acc, const Fn f[4], cons
     return x;
 }
 
+__device__ bool walk_subtile_p(const float p[4], long base, long V, float r, uint32_t& cb, long& result);
+__device__ bool walk_serial_p(const float p[4], long base, long V, float r, uint32_t& cb, long& result);
+
 // ---- stage 3: probabilities and sub-tile maps --------------------------------
 // Wave w's part of k-slice k is the 256 consecutive logits c0 + k*1024 + w*256 +
 // [0, 256): sub-tile 16*chunk + 4k + w.  For each, the wave predicts the binade
@@ -610,12 +614,16 @@ __global__ __launch_bounds__(256) void sample_stage3_kernel(SampleArgs a, int ve
     __shared__ uint64_t red_s[4], red_p[4];
     __shared__ int red_f[4];
     __shared__ float ksum[4][4];  // [k][wave] fp32 sums of exp (prediction only)
-    const long row = blockIdx.y;
-    const long c0 = (long)blockIdx.x * kCH;
+    // Workgroups in dispatch order take chunk 0 of every row first: those
+    // also walk sub-tile 0 (below), the longest job, so it starts early.
+    const long lin = (long)blockIdx.y * gridDim.x + blockIdx.x;
+    const long row = lin % a.rows;
+    const int chunk = (int)(lin / a.rows);
+    const long c0 = (long)chunk * kCH;
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
     float v[16];  // exp(adjusted - max), as stage 2 stored them
     load_chunk16(v, a.probs + row * a.ld_probs, c0, a.vocab, vec_out != 0);
-    const SumShare share = sum_share(a, row, (int)blockIdx.x);
+    const SumShare share = sum_share(a, row, chunk);
     // 1/sum, and the exact prefix of the earlier chunks' sums (the prediction
     // of the running sum at this chunk's start)
     float inv, prefix;
@@ -642,6 +650,22 @@ __global__ __launch_bounds__(256) void sample_stage3_kernel(SampleArgs a, int ve
                 if (i + j < a.vocab) out[i + j] = p[4 * k + j];
         }
     }
+    // Sub-tile 0 starts from an exact running sum, 0, and crosses a binade
+    // at about every doubling of its element count: a dozen restarts of the
+    // exact walk.  The first wave of each row's first workgroup (dispatched
+    // first) walks it here, at raised issue priority, while the rest of the
+    // grid runs, instead of on the walk kernel's one-wave critical path.
+    if (chunk == 0 && wid == 0 && a.r) {
+        __builtin_amdgcn_s_setprio(3);
+        uint32_t cb = 0u;
+        long result = -1;
+        const bool done = walk_serial_p(&p[0], 0, a.vocab, a.r[row], cb, result);
+        if (lane == 0) {
+            a.ws_first[2 * row] = done ? (int32_t)result : -1;
+            a.ws_first[2 * row + 1] = (int32_t)cb;
+        }
+        __builtin_amdgcn_s_setprio(0);
+    }
     __syncthreads();
     float run = prefix;  // running prediction, the same order of additions in every wave
 #pragma unroll
@@ -666,7 +690,7 @@ __global__ __launch_bounds__(256) void sample_stage3_kernel(SampleArgs a, int ve
             acc = compose(acc, f[j]);
         }
         acc = wave_scan(acc);
-        const long st = (long)blockIdx.x * 16 + 4 * k + wid;
+        const long st = (long)chunk * 16 + 4 * k + wid;
         const Crossing x = predict_crossing(acc, f, &p[4 * k], nv, ok, cb, cls, b);
         if (lane == 63 && st < a.nsub) {
             a.ws_map0[row * a.nsub_ld + st] = acc.a0;
@@ -794,22 +818,46 @@ __device__ __forceinline__ bool pass_crossing(uint32_t& cb, const uint32_t* x, i
 // scan of their maps; an element that leaves the binade is added with an
 // ordinary fp32 add and the scan restarts after it.  Returns true when the
 // draw is decided (result set), else updates cb to the sub-tile's end.
-__device__ bool walk_subtile(const SampleArgs& a, long st, const float* prow, float r, uint32_t& cb, long& result) {
-    const int lane = threadIdx.x;
-    const long V = a.vocab;
-    const long base = st * kSub;
-    const long i0 = base + 4 * lane;
-    float p[4];
-    if (i0 + 3 < V && a.vec_probs) {
-        const float4 q = *reinterpret_cast<const float4*>(prow + i0);
-        p[0] = q.x;
-        p[1] = q.y;
-        p[2] = q.z;
-        p[3] = q.w;
-    } else {
+// The whole sub-tile one fp32 add at a time in index order (the reference's
+// loop itself), four per step from one lane's registers; p, base, V as below.
+__device__ bool walk_serial_p(const float p[4], long base, long V, float r, uint32_t& cb, long& result) {
+    const int nvalid = V - base < kSub ? (int)(V - base) : kSub;
+    float cum = __uint_as_float(cb);
+    for (int L = 0; L < 64 && 4 * L < nvalid; L++) {
+        float c[4];
+        float run = cum;
 #pragma unroll
-        for (int e = 0; e < 4; e++) p[e] = i0 + e < V ? prow[i0 + e] : 0.0f;
+        for (int e = 0; e < 4; e++) {
+            const float q = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p[e]), L));
+            run = run + (4 * L + e < nvalid ? q : 0.0f);
+            c[e] = run;
+        }
+        if (!(c[3] < r)) {  // the draw ends in this quad, or the sum became NaN
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int o = 4 * L + e;
+                if (o < nvalid) {
+                    if (c[e] >= r) {
+                        result = base + o;
+                        return true;
+                    }
+                    if (c[e] != c[e]) {  // no later sum can reach r
+                        result = V - 1;
+                        return true;
+                    }
+                }
+            }
+        }
+        cum = c[3];
     }
+    cb = __float_as_uint(cum);
+    return false;
+}
+
+// p: this lane's four probabilities of the sub-tile starting at index base
+// (elements base + 4*lane ..); one wave.
+__device__ bool walk_subtile_p(const float p[4], long base, long V, float r, uint32_t& cb, long& result) {
+    const int lane = threadIdx.x & 63;
     // offsets inside the sub-tile: first unprocessed element, end of the row
     const int nvalid = V - base < kSub ? (int)(V - base) : kSub;
     int s = 0;
@@ -875,6 +923,24 @@ __device__ bool walk_subtile(const SampleArgs& a, long st, const float* prow, fl
     }
 }
 
+__device__ bool walk_subtile(const SampleArgs& a, long st, const float* prow, float r, uint32_t& cb, long& result) {
+    const int lane = threadIdx.x & 63;
+    const long V = a.vocab;
+    const long i0 = st * kSub + 4 * lane;
+    float p[4];
+    if (i0 + 3 < V && a.vec_probs) {
+        const float4 q = *reinterpret_cast<const float4*>(prow + i0);
+        p[0] = q.x;
+        p[1] = q.y;
+        p[2] = q.z;
+        p[3] = q.w;
+    } else {
+#pragma unroll
+        for (int e = 0; e < 4; e++) p[e] = i0 + e < V ? prow[i0 + e] : 0.0f;
+    }
+    return walk_subtile_p(p, st * kSub, V, r, cb, result);
+}
+
 // one wave per row and per CU: all of the register file is available to it
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1))) void sample_walk_kernel(SampleArgs a) {
     __shared__ WalkShared sh;
@@ -883,6 +949,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1))) void
     const float r = a.r[row];
     const long V = a.vocab;
     const float* prow = a.probs + row * a.ld_probs;
+    const int first_hit = a.ws_first[2 * row];  // sub-tile 0, walked by stage 3
+    const uint32_t first_end = (uint32_t)a.ws_first[2 * row + 1];
     const int ncache = a.nsub < kSumCache ? a.nsub : kSumCache;
     const int nxcache = a.nsub < kXCache ? a.nsub : kXCache;
     fill_walk_cache(sh, a, row, ncache, nxcache);
@@ -890,9 +958,13 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1))) void
     // "cum < r" on bit patterns: cum >= 0, so cum < r <=> bits(cum) < bits(r)
     // for r > 0; for r <= 0 or NaN no sub-tile is passed without a walk
     const uint32_t rb = r > 0.0f ? __float_as_uint(r) : 0u;
-    uint32_t cb = 0u;  // bits of the running sum
+    if (first_hit >= 0) {
+        if (lane == 0) a.ids[row] = first_hit;
+        return;
+    }
+    uint32_t cb = first_end;  // bits of the running sum
     long result = V - 1;
-    long st = 0;
+    long st = 1;
     while (st < a.nsub) {
         // Pass as many sub-tiles as possible at once: lane j holds sub-tile
         // st + j; the in-order scan of their maps gives each one's end value
@@ -939,7 +1011,7 @@ static int ceil_log2(long n) {
 }
 
 struct WsLayout {
-    size_t off_sum, off_max, off_arg, off_flag, off_m0, off_m1, off_cls, off_x, total;
+    size_t off_sum, off_max, off_arg, off_flag, off_m0, off_m1, off_cls, off_x, off_first, total;
 };
 
 static size_t al16(size_t x) { return (x + 15) & ~(size_t)15; }
@@ -957,7 +1029,8 @@ static WsLayout ws_layout(long rows, long vocab) {
     l.off_m1 = l.off_m0 + al16(ns * sizeof(uint32_t));
     l.off_cls = l.off_m1 + al16(ns * sizeof(uint32_t));
     l.off_x = l.off_cls + al16(ns * sizeof(int32_t));
-    l.total = l.off_x + al16(ns * kXWords * sizeof(uint32_t));
+    l.off_first = l.off_x + al16(ns * kXWords * sizeof(uint32_t));
+    l.total = l.off_first + al16((size_t)rows * 2 * sizeof(int32_t));
     return l;
 }
 
@@ -976,6 +1049,7 @@ static int bind_workspace(SampleArgs& a, void* ws, size_t ws_bytes, long rows, l
     a.ws_map1 = reinterpret_cast<uint32_t*>(b + l.off_m1);
     a.ws_cls = reinterpret_cast<int32_t*>(b + l.off_cls);
     a.ws_xing = reinterpret_cast<uint32_t*>(b + l.off_x);
+    a.ws_first = reinterpret_cast<int32_t*>(b + l.off_first);
     a.nchunk = (int)((vocab + kCH - 1) / kCH);
     a.nsub = (int)((vocab + kSub - 1) / kSub);
     a.nsub_ld = (a.nsub + 3) & ~3;

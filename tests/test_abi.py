@@ -106,7 +106,8 @@ def test_workspace_sizes(lib):
     # binade class, six u32 words of the predicted crossing), 16-byte aligned
     al = lambda b: (b + 15) // 16 * 16
     n, ns = 64 * 38, 64 * 596
-    assert lib.anelm_sample_workspace_size(64, 151936) == al(n * 8) + 3 * al(n * 4) + 3 * al(ns * 4) + al(ns * 24)
+    assert lib.anelm_sample_workspace_size(64, 151936) == (al(n * 8) + 3 * al(n * 4) + 3 * al(ns * 4) + al(ns * 24)
+                                                           + al(64 * 8))   # + sub-tile 0 result per row
     assert lib.anelm_sample_workspace_size(0, 10) == 0
     assert lib.anelm_softmax_workspace_size(1, 4096) > 0
 
