@@ -268,19 +268,33 @@ __global__ __launch_bounds__(kAttnThreads) void gqa_decode_kernel(AttnArgs a) {
 
 // Merges the per-chunk partials of one (sequence, q head): one wave; lane j
 // owns chunks j, j+64, ... for the (max, sum) merge, then every lane sums its
-// head_dim/64 outputs over all chunks with independent loads.
+// head_dim/64 outputs over all chunks.  The first kBatch chunks' output
+// partials are loaded together with the (max, sum) pairs, before the max is
+// known, so a ring of up to kBatch chunks costs one memory round trip.
+// Loads use clamped indices (chunk nsplit-1 re-read, then discarded) so
+// none sits behind a branch.
 template <int D>
 __global__ __launch_bounds__(kWave) void gqa_combine_kernel(AttnArgs a) {
+    constexpr int kBatch = D <= 128 ? 64 : 32;  // chunks whose partials are in flight at once
     const int lane = threadIdx.x;
     const long bh = blockIdx.x;
     const long b = bh / a.nh;
     const int h = (int)(bh % a.nh);
-    const float* p = a.ws + bh * a.nsplit * (long)(D + 2);
-    // lane j holds chunk s0 + j's (max, sum); the first 64 stay in registers
-    const float m0 = lane < a.nsplit ? p[lane * (D + 2) + D] : -INFINITY;
-    const float l0 = lane < a.nsplit ? p[lane * (D + 2) + D + 1] : 0.0f;
+    const int ns = a.nsplit;
+    const float* p = a.ws + bh * ns * (long)(D + 2);
+    auto clampc = [&](int s) { return s < ns ? s : ns - 1; };
+    // lane j holds chunk j's (max, sum); the first 64 stay in registers
+    const float m0r = p[clampc(lane) * (D + 2) + D];
+    const float l0r = p[clampc(lane) * (D + 2) + D + 1];
+    float v[kBatch][D / kWave];
+#pragma unroll
+    for (int j = 0; j < kBatch; j++)
+#pragma unroll
+        for (int i = 0; i < D / kWave; i++) v[j][i] = p[clampc(j) * (D + 2) + lane + i * kWave];
+    const float m0 = lane < ns ? m0r : -INFINITY;
+    const float l0 = lane < ns ? l0r : 0.0f;
     float M = l0 > 0.0f ? m0 : -INFINITY;
-    for (int s = lane + kWave; s < a.nsplit; s += kWave) {
+    for (int s = lane + kWave; s < ns; s += kWave) {
         if (p[s * (D + 2) + D + 1] > 0.0f) M = fmaxf(M, p[s * (D + 2) + D]);
     }
     M = wave_max(M);
@@ -288,30 +302,33 @@ __global__ __launch_bounds__(kWave) void gqa_combine_kernel(AttnArgs a) {
     float o[D / kWave];
 #pragma unroll
     for (int i = 0; i < D / kWave; i++) o[i] = 0.0f;
-    constexpr int kBatch = 32;   // partials loaded before they are used
-    for (int s0 = 0; s0 < a.nsplit; s0 += kWave) {
+    for (int s0 = 0; s0 < ns; s0 += kWave) {
         const int s = s0 + lane;
         float ms = m0, ls = l0;
         if (s0 > 0) {
-            ms = s < a.nsplit ? p[s * (D + 2) + D] : -INFINITY;
-            ls = s < a.nsplit ? p[s * (D + 2) + D + 1] : 0.0f;
+            ms = s < ns ? p[s * (D + 2) + D] : -INFINITY;
+            ls = s < ns ? p[s * (D + 2) + D + 1] : 0.0f;
         }
         // an empty chunk (sum 0) contributes nothing; NaN sums propagate
         const float c = (!(ls > 0.0f) && ls == ls) ? 0.0f : expf(ms - M);
         L = fmaf(ls, c, L);
-        const int cnt = min(kWave, a.nsplit - s0);
+        const int cnt = min(kWave, ns - s0);
         for (int j0 = 0; j0 < cnt; j0 += kBatch) {
-            float v[kBatch][D / kWave];
+            if (s0 + j0 > 0) {  // chunks past the first batch
 #pragma unroll
-            for (int j = 0; j < kBatch; j++)
+                for (int j = 0; j < kBatch; j++)
 #pragma unroll
-                for (int i = 0; i < D / kWave; i++)
-                    v[j][i] = j0 + j < cnt ? p[(s0 + j0 + j) * (D + 2) + lane + i * kWave] : 0.0f;
+                    for (int i = 0; i < D / kWave; i++)
+                        v[j][i] = p[clampc(s0 + j0 + j) * (D + 2) + lane + i * kWave];
+            }
 #pragma unroll
             for (int j = 0; j < kBatch; j++) {
+                // past the last chunk: weight 0 and value 0 (not the re-read
+                // chunk's value, which could be infinite)
+                const bool live = j0 + j < cnt;
                 const float cj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(c), j0 + j));
 #pragma unroll
-                for (int i = 0; i < D / kWave; i++) o[i] = fmaf(v[j][i], cj, o[i]);
+                for (int i = 0; i < D / kWave; i++) o[i] = fmaf(live ? v[j][i] : 0.0f, live ? cj : 0.0f, o[i]);
             }
         }
     }
