@@ -146,7 +146,24 @@ __device__ __forceinline__ void adjust16(float v[16], const uint32_t* cnt, const
 }
 
 // The 16 logits of thread tid in chunk c0 (4 float4 slots k*1024 + 4*tid).
+// A whole chunk of an aligned row (every chunk but a row's last) takes one
+// uniform branch with its four 16-byte loads in flight together; per-lane
+// conditions around each load made the compiler wait for each one before
+// issuing the next.
 __device__ __forceinline__ void load_chunk16(float v[16], const float* row_ptr, long c0, long vocab, bool vec) {
+    if (vec && c0 + kCH <= vocab) {
+        float4 f[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) f[k] = ld_nt(reinterpret_cast<const float4*>(row_ptr + c0 + k * 1024 + 4 * threadIdx.x));
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            v[4 * k] = f[k].x;
+            v[4 * k + 1] = f[k].y;
+            v[4 * k + 2] = f[k].z;
+            v[4 * k + 3] = f[k].w;
+        }
+        return;
+    }
 #pragma unroll
     for (int k = 0; k < 4; k++) {
         const long i = c0 + k * 1024 + 4 * threadIdx.x;
