@@ -672,8 +672,10 @@ def pmc_summary(fetch_dir, write_dir, copy_fetch_dir, copy_write_dir, workload=H
         ob = {"gqa_decode": attn_bytes(w), "gqa_combine": 0}
         run_args = f"--only {workload} --steps 1"
     elif workload == SAMPLER:
-        lv = 64 * VOCAB * 4   # logits read (stages 1, 2), + probabilities written (stage 3)
-        ob = {"stage1": lv, "stage2": lv, "stage3": 2 * lv, "walk": 0}
+        # stage 1 reads the logits; stage 2 reads them again and writes exp(x - max)
+        # into the probability buffer; stage 3 reads that and writes the probabilities
+        lv = 64 * VOCAB * 4
+        ob = {"stage1": lv, "stage2": 2 * lv, "stage3": 2 * lv, "walk": 0}
         run_args = f"--only {workload} --steps 1"
     else:
         ob = op_bytes(WORKLOADS[workload])
