@@ -61,6 +61,7 @@ _SIGS = {
     "anelm_embed_gather": (_I, [_P, _P, _I, _P, _L, _L, _L, _P, _P]),
     "anelm_bf16_to_f16": (_I, [_P, _P, _S, _P]),
     "anelm_bf16_to_f32": (_I, [_P, _P, _S, _P]),
+    "anelm_bf16_to_f32_plus1": (_I, [_P, _P, _S, _P]),
     "anelm_f16_to_f32": (_I, [_P, _P, _S, _P]),
     "anelm_f32_to_f16": (_I, [_P, _P, _S, _P]),
     "anelm_softmax_workspace_size": (_S, [_L, _L]),
@@ -87,6 +88,7 @@ _SIGS = {
                            ctypes.POINTER(ctypes.c_uint64)]),
     "anelm_st_host_data": (_P, [_P, _L]),
     "anelm_st_load": (_I, [_P, _L, _P, _I, _P]),
+    "anelm_st_load_norm": (_I, [_P, _L, _P, _L, _P]),
     "anelm_ane_blob_header": (None, [_P, ctypes.c_uint64]),
     "anelm_write_ane_blobs": (_L, [ctypes.c_char_p, ctypes.c_char_p, _P]),
     "anelm_blas_create": (_P, []),
@@ -242,6 +244,11 @@ def bf16_to_f16(dst, src, stream=None):
 
 def bf16_to_f32(dst, src, stream=None):
     _check(lib().anelm_bf16_to_f32(_ptr(dst), _ptr(src), src.numel(), _stream(stream)))
+
+
+def bf16_to_f32_plus1(dst, src, stream=None):
+    """The Qwen3.5 (1+w) norm weight: dst = widen(src) + 1.0f."""
+    _check(lib().anelm_bf16_to_f32_plus1(_ptr(dst), _ptr(src), src.numel(), _stream(stream)))
 
 
 def f32_to_f16(dst, src, stream=None):
@@ -418,6 +425,10 @@ class SafeTensorsFile:
 
     def load(self, i, dst, dtype, stream=None):
         _check(lib().anelm_st_load(self._h, i, _ptr(dst), dtype, _stream(stream)))
+
+    def load_norm(self, i, dst, expected_numel, stream=None):
+        """SafeTensors::load_norm_weight: BF16 tensor i as fp32 (1+w)."""
+        _check(lib().anelm_st_load_norm(self._h, i, _ptr(dst), expected_numel, _stream(stream)))
 
 
 def ane_blob_header(num_elements) -> bytes:

@@ -143,6 +143,20 @@ __global__ __launch_bounds__(256) void widen_kernel(float* dst, const uint16_t* 
         dst[i] = F16 ? f16_to_f32_exact(src[i]) : bf16_to_f32(src[i]);
 }
 
+// The Qwen3.5 (1+w) norm weight (core/safetensors.cpp:299-306): bf16 widened
+// exactly, then + 1.0f in fp32, rounded to nearest even as the reference's
+// `w[i] += 1.0f` is.  +-Inf stays +-Inf; a NaN comes out quieted with its
+// sign and payload kept, which is what an IEEE add of a NaN operand returns
+// on the CPUs the reference runs on, written out so it does not depend on
+// the GPU's NaN propagation.
+__global__ __launch_bounds__(256) void widen_plus1_kernel(float* dst, const uint16_t* src, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
+        const uint32_t b = (uint32_t)src[i] << 16;
+        const bool nan = (b & 0x7FFFFFFFu) > 0x7F800000u;
+        dst[i] = nan ? __uint_as_float(b | 0x00400000u) : __uint_as_float(b) + 1.0f;
+    }
+}
+
 // fp32 -> fp16 round to nearest even (the activation conversion at the ANE
 // kernel inputs, core/ane_runtime.cpp:604-612, where arm64's __fp16 cast
 // rounds to nearest even): the hardware conversion, whose mode is RNE.
@@ -304,6 +318,14 @@ extern "C" int anelm_bf16_to_f32(float* dst, const uint16_t* src, size_t n, void
     clear_error();
     widen_kernel<false><<<grid_stride_blocks(n), 256, 0, as_stream(stream)>>>(dst, src, n);
     return launch_status("bf16_to_f32");
+}
+
+extern "C" int anelm_bf16_to_f32_plus1(float* dst, const uint16_t* src, size_t n, void* stream) {
+    if (!dst || !src) return fail(ANELM_ERR_INVALID, "anelm_bf16_to_f32_plus1: null pointer");
+    if (n == 0) return fail(ANELM_ERR_INVALID, "anelm_bf16_to_f32_plus1: n == 0");
+    clear_error();
+    widen_plus1_kernel<<<grid_stride_blocks(n), 256, 0, as_stream(stream)>>>(dst, src, n);
+    return launch_status("bf16_to_f32_plus1");
 }
 
 extern "C" int anelm_f32_to_f16(uint16_t* dst, const float* src, size_t n, void* stream) {

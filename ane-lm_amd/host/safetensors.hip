@@ -352,18 +352,11 @@ extern "C" const void* anelm_st_host_data(const anelm_st* h, long i) {
     return h->data + h->t[i].offset;
 }
 
-// Tensor i to device memory dst as dst_dtype: the tensor's own dtype (a
-// copy), or for a BF16 tensor ANELM_F32 (exact widening, the reference's
-// load_bf16_to_f32) or ANELM_F16 (the truncating convert of the blobs).
-extern "C" int anelm_st_load(const anelm_st* h, long i, void* dst, int dst_dtype, void* stream) {
-    clear_error();
-    if (!h || i < 0 || i >= (long)h->t.size()) return fail(ANELM_ERR_RANGE, "st_load: no tensor %ld", i);
-    if (!dst) return fail(ANELM_ERR_INVALID, "st_load: null destination");
-    const StTensor& t = h->t[i];
-    const bool widen = t.dtype == ANELM_BF16 && dst_dtype == ANELM_F32;
-    const bool to_f16 = t.dtype == ANELM_BF16 && dst_dtype == ANELM_F16;
-    if (!widen && !to_f16 && dst_dtype != t.dtype)
-        return fail(ANELM_ERR_INVALID, "st_load: %s cannot be loaded as dtype %d", t.name.c_str(), dst_dtype);
+namespace {
+
+// Staged upload of tensor t (already validated) to dst: a copy, or for a BF16
+// tensor the widening to fp32 (plus 1.0f when plus1) or the fp16 convert.
+int load_tensor(const anelm_st* h, const StTensor& t, void* dst, bool widen, bool plus1, bool to_f16, void* stream) {
     if (t.nbytes == 0) return ANELM_OK;
     hipStream_t st = anelm::as_stream(stream);
     anelm_st* hm = const_cast<anelm_st*>(h);
@@ -389,8 +382,9 @@ extern "C" int anelm_st_load(const anelm_st* h, long i, void* dst, int dst_dtype
         if (widen) {   // staged bf16 chunk, widened into place
             if ((e = hipMemcpyAsync(p.dev[k], p.hin[k], n, hipMemcpyHostToDevice, st)) != hipSuccess)
                 return hip_fail(e, "st_load H2D");
-            rc = anelm_bf16_to_f32(static_cast<float*>(dst) + off / 2, reinterpret_cast<const uint16_t*>(p.dev[k]),
-                                   n / 2, stream);
+            float* d = static_cast<float*>(dst) + off / 2;
+            const uint16_t* s16 = reinterpret_cast<const uint16_t*>(p.dev[k]);
+            rc = plus1 ? anelm_bf16_to_f32_plus1(d, s16, n / 2, stream) : anelm_bf16_to_f32(d, s16, n / 2, stream);
         } else {
             char* d = static_cast<char*>(dst) + off;
             if ((e = hipMemcpyAsync(d, p.hin[k], n, hipMemcpyHostToDevice, st)) != hipSuccess)
@@ -404,6 +398,38 @@ extern "C" int anelm_st_load(const anelm_st* h, long i, void* dst, int dst_dtype
     }
     if ((e = hipStreamSynchronize(st)) != hipSuccess) return hip_fail(e, "st_load");
     return ANELM_OK;
+}
+
+}  // namespace
+
+// Tensor i to device memory dst as dst_dtype: the tensor's own dtype (a
+// copy), or for a BF16 tensor ANELM_F32 (exact widening, the reference's
+// load_bf16_to_f32) or ANELM_F16 (the truncating convert of the blobs).
+extern "C" int anelm_st_load(const anelm_st* h, long i, void* dst, int dst_dtype, void* stream) {
+    clear_error();
+    if (!h || i < 0 || i >= (long)h->t.size()) return fail(ANELM_ERR_RANGE, "st_load: no tensor %ld", i);
+    if (!dst) return fail(ANELM_ERR_INVALID, "st_load: null destination");
+    const StTensor& t = h->t[i];
+    const bool widen = t.dtype == ANELM_BF16 && dst_dtype == ANELM_F32;
+    const bool to_f16 = t.dtype == ANELM_BF16 && dst_dtype == ANELM_F16;
+    if (!widen && !to_f16 && dst_dtype != t.dtype)
+        return fail(ANELM_ERR_INVALID, "st_load: %s cannot be loaded as dtype %d", t.name.c_str(), dst_dtype);
+    return load_tensor(h, t, dst, widen, false, to_f16, stream);
+}
+
+// core/safetensors.cpp:299-306 (load_norm_weight): the widened BF16 weight
+// plus 1.0f.  The reference adds the offset for i < expected_numel, so a
+// non-positive count (no shape check there either) gives the plain widening.
+extern "C" int anelm_st_load_norm(const anelm_st* h, long i, float* dst, long expected_numel, void* stream) {
+    clear_error();
+    if (!h || i < 0 || i >= (long)h->t.size()) return fail(ANELM_ERR_RANGE, "st_load_norm: no tensor %ld", i);
+    if (!dst) return fail(ANELM_ERR_INVALID, "st_load_norm: null destination");
+    const StTensor& t = h->t[i];
+    if (t.dtype != ANELM_BF16) return fail(ANELM_ERR_INVALID, "st_load_norm: %s is not BF16", t.name.c_str());
+    if (expected_numel > 0 && t.numel != expected_numel)
+        return fail(ANELM_ERR_INVALID, "st_load_norm: shape mismatch for %s: expected %ld, got %lld", t.name.c_str(),
+                    expected_numel, (long long)t.numel);
+    return load_tensor(h, t, dst, true, expected_numel > 0, false, stream);
 }
 
 // core/safetensors.cpp:316-331 / core/ane_runtime.cpp:197-205

@@ -143,6 +143,9 @@ int anelm_bf16_to_f16(uint16_t* dst, const uint16_t* src, size_t n, void* stream
 /* bf16 -> fp32 (bf16_to_f32_vec, common.h:77-79; used by load_bf16_to_f32,
  * core/safetensors.cpp:266-281). */
 int anelm_bf16_to_f32(float* dst, const uint16_t* src, size_t n, void* stream);
+/* bf16 -> fp32 plus 1.0f (round to nearest even): the Qwen3.5 (1+w) RMSNorm
+ * weight of SafeTensors::load_norm_weight, core/safetensors.cpp:299-306. */
+int anelm_bf16_to_f32_plus1(float* dst, const uint16_t* src, size_t n, void* stream);
 /* fp16 -> fp32 exact widening (f16_to_f32, common.h:35-56). */
 int anelm_f16_to_f32(float* dst, const uint16_t* src, size_t n, void* stream);
 /* fp32 -> fp16 rounded to nearest even: the activation conversion at the ANE
@@ -323,6 +326,15 @@ const void* anelm_st_host_data(const anelm_st* st, long i);
  * (the truncating convert on the device, the blobs' data).  Staged through
  * pinned memory on `stream`; returns when the tensor is in place. */
 int anelm_st_load(const anelm_st* st, long i, void* dst, int dst_dtype, void* stream);
+/* The Qwen3.5 (1+w) norm weight into DEVICE memory dst as fp32
+ * (SafeTensors::load_norm_weight, core/safetensors.cpp:299-306): BF16 tensor i
+ * widened and offset by 1.0f on the device.  expected_numel > 0 must equal the
+ * tensor's element count (else ANELM_ERR_INVALID, the reference's "Shape
+ * mismatch" null return); as in the reference, whose offset loop runs to
+ * expected_numel, a non-positive count loads the widened weight without the
+ * offset.  A tensor that is not BF16 is an error (the reference would read
+ * its bytes as bf16). */
+int anelm_st_load_norm(const anelm_st* st, long i, float* dst, long expected_numel, void* stream);
 
 /* The 128-byte ANE blob header for num_elements fp16 values
  * (core/safetensors.cpp:322-331, core/ane_runtime.cpp:199-205). */

@@ -91,6 +91,13 @@ extern "C" void orc_f16_to_f32_vec(float* out, const uint16_t* in, size_t n) {
     for (size_t i = 0; i < n; i++) out[i] = orc_f16_to_f32(in[i]);
 }
 
+// core/safetensors.cpp:299-306: widen, then the (1+w) offset over the first
+// expected_numel entries
+extern "C" void orc_norm_weight_vec(float* out, const uint16_t* in, size_t n, long expected_numel) {
+    orc_bf16_to_f32_vec(out, in, n);
+    for (long i = 0; i < expected_numel && (size_t)i < n; i++) out[i] += 1.0f;
+}
+
 // ---------------------------------------------------------------- RMSNorm
 // core/cpu_ops.cpp:25-31:
 //   vDSP_svesq(x, &ss)            ss = sum x^2

@@ -38,6 +38,14 @@ void orc_bf16_to_f16_vec(uint16_t* out, const uint16_t* in, size_t n, int nthrea
 void orc_bf16_to_f32_vec(float* out, const uint16_t* in, size_t n);
 void orc_f16_to_f32_vec(float* out, const uint16_t* in, size_t n);
 
+/* ---- Qwen3.5 norm weights: core/safetensors.cpp:299-306 (load_norm_weight)
+ * out = bf16 widened to fp32 (load_bf16_to_f32 :266-281), then out[i] += 1.0f
+ * for i < expected_numel, rounded to nearest even.  The reference's loop runs
+ * to expected_numel, so a non-positive count widens only.
+ * pinned: all 65,536 patterns against an exact-rational round-to-nearest-even
+ * of w + 1 (tests/test_oracle_convert.py). */
+void orc_norm_weight_vec(float* out, const uint16_t* in, size_t n, long expected_numel);
+
 /* ---- RMSNorm: core/cpu_ops.cpp:25-31 ----
  * ss = sum(x^2); s = 1/sqrtf(ss/dim + eps); out = x*s; out *= w.
  * vDSP_svesq's summation order is unspecified; the oracle uses the

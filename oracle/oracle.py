@@ -25,6 +25,7 @@ _SIGS = {
     "orc_bf16_to_f16_vec": (None, [_P, _P, _S, _I]),
     "orc_bf16_to_f32_vec": (None, [_P, _P, _S]),
     "orc_f16_to_f32_vec": (None, [_P, _P, _S]),
+    "orc_norm_weight_vec": (None, [_P, _P, _S, _L]),
     "orc_rmsnorm": (None, [_P, _P, _P, _I, _F]),
     "orc_rmsnorm_rows": (None, [_P, _P, _P, _L, _I, _L, _L, _F, _I]),
     "orc_silu_vec": (None, [_P, _S]),
@@ -105,6 +106,15 @@ def bf16_to_f32(bits: np.ndarray) -> np.ndarray:
     src = _c(bits, np.uint16)
     out = np.empty(src.shape, np.float32)
     lib().orc_bf16_to_f32_vec(_p(out), _p(src), src.size)
+    return out
+
+
+def norm_weight(bits: np.ndarray, expected_numel: int | None = None) -> np.ndarray:
+    """Qwen3.5 (1+w) norm weight (core/safetensors.cpp:299-306): bf16 widened
+    to fp32 plus 1.0f over the first expected_numel entries (default: all)."""
+    src = _c(bits, np.uint16)
+    out = np.empty(src.shape, np.float32)
+    lib().orc_norm_weight_vec(_p(out), _p(src), src.size, src.size if expected_numel is None else expected_numel)
     return out
 
 

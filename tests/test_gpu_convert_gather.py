@@ -139,3 +139,16 @@ def test_gather_ragged_hidden_and_bad_ids(hip, orc, rng):
     good = [0, 2, 4]
     assert_bitexact(o[good], orc.embed_gather(table, ids[good], 1), "good rows")
     assert np.all(o[[1, 3]] == 123.0), "rows with bad ids must not be written"
+
+
+@pytest.mark.parametrize("n", [65536, 4096, 1, 3_000_017])
+def test_norm_weight_plus1(hip, orc, rng, n):
+    """Qwen3.5 (1+w) norm weight (core/safetensors.cpp:299-306): bit-exact with
+    the oracle over all 65,536 bf16 patterns (NaN payloads included) and at
+    ragged sizes."""
+    import torch
+
+    pats = np.arange(65536, dtype=np.uint16) if n == 65536 else rng.integers(0, 65536, n, dtype=np.uint32).astype(np.uint16)
+    dst = torch.empty(n, device="cuda")
+    hip.bf16_to_f32_plus1(dst, dev(pats))
+    assert_bitexact(host(dst), orc.norm_weight(pats), f"n={n}")

@@ -44,6 +44,13 @@ def test_device_loads(hip, orc, tmp_path, rng):
                 out32 = torch.empty(max(n, 1), device="cuda")
                 f.load(i, out32, hip.F32)
                 assert_bitexact(host(out32)[:n], orc.bf16_to_f32(data), name + " as f32")
+                f.load_norm(i, out32, n)
+                assert_bitexact(host(out32)[:n], orc.norm_weight(data), name + " as (1+w) norm weight")
+                f.load_norm(i, out32, 0)                        # count <= 0: no offset, as the reference
+                assert_bitexact(host(out32)[:n], orc.bf16_to_f32(data), name + " norm weight, count 0")
+                if n:
+                    with pytest.raises(hip.AnelmError, match="shape mismatch"):
+                        f.load_norm(i, out32, n + 1)
                 out16 = torch.empty(max(n, 1), dtype=torch.int16, device="cuda")
                 f.load(i, out16, hip.F16)
                 assert_bitexact(host(out16)[:n], orc.bf16_to_f16(data), name + " as f16")
@@ -56,6 +63,8 @@ def test_device_loads(hip, orc, tmp_path, rng):
                 assert_bitexact(host(out), data, name)
                 with pytest.raises(hip.AnelmError):
                     f.load(i, out, hip.F16)                     # only BF16 converts
+                with pytest.raises(hip.AnelmError, match="not BF16"):
+                    f.load_norm(i, out, n)
 
 
 def _tree(root):

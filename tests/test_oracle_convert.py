@@ -77,3 +77,59 @@ def test_bf16_to_f32_is_high_half(orc):
     pats = np.arange(65536, dtype=np.uint16)
     got = orc.bf16_to_f32(pats).view(np.uint32)
     assert np.array_equal(got, pats.astype(np.uint32) << 16)
+
+
+def _rne_f32(x):
+    """Exact rational x rounded to nearest-even fp32 (normal range), derived
+    from the definition: scale to a 24-bit significand, round half to even."""
+    from fractions import Fraction
+
+    if x == 0:
+        return 0.0
+    sign = -1 if x < 0 else 1
+    a = abs(x)
+    k = a.numerator.bit_length() - a.denominator.bit_length()
+    if Fraction(2) ** k > a:
+        k -= 1
+    m = a / Fraction(2) ** (k - 23)          # in [2^23, 2^24)
+    q, r = divmod(m.numerator, m.denominator)
+    twice = 2 * r
+    if twice > m.denominator or (twice == m.denominator and q & 1):
+        q += 1
+    return sign * float(Fraction(q) * Fraction(2) ** (k - 23))
+
+
+def test_norm_weight_exhaustive_against_exact_rounding(orc):
+    """core/safetensors.cpp:299-306: w + 1.0f for every bf16 w, checked
+    against the exact sum rounded to nearest even (ties included: w = 2^-24
+    rounds to 1, w = 3*2^-25 to 1 + 2^-23)."""
+    from fractions import Fraction
+
+    pats = np.arange(65536, dtype=np.uint16)
+    got = orc.norm_weight(pats)
+    w = orc.bf16_to_f32(pats)
+    want = np.empty(65536, np.float32)
+    for i in range(65536):
+        wi = float(w[i])
+        if not np.isfinite(wi):
+            want[i] = wi
+            continue
+        want[i] = _rne_f32(Fraction(wi) + 1)
+    fin = np.isfinite(w)
+    assert_bitexact(got[fin], want[fin], "norm weight")
+    assert np.array_equal(got[np.isinf(w)], w[np.isinf(w)])
+    nan = np.isnan(w)                                  # quieted, sign and payload kept (IEEE 754 6.2.3)
+    assert np.array_equal(got[nan].view(np.uint32), w[nan].view(np.uint32) | 0x00400000)
+    one = lambda bits: float(orc.norm_weight(np.array([bits], np.uint16))[0])
+    assert one(0x3380) == 1.0                          # 2^-24: tie, stays at 1 (even)
+    assert one(0x33C0) == 1.0 + 2.0 ** -23             # 1.5 * 2^-24: above the tie
+    assert one(0xBF80) == 0.0                          # -1 + 1
+    assert one(0x8000) == 1.0                          # -0 + 1
+
+
+def test_norm_weight_count_bounds_the_offset(orc):
+    """The reference adds 1 for i < expected_numel only: a non-positive count
+    widens only (core/safetensors.cpp:302-303)."""
+    bits = np.array([0x3F80, 0x4000, 0xC000], np.uint16)
+    assert np.array_equal(orc.norm_weight(bits, 0), orc.bf16_to_f32(bits))
+    assert np.array_equal(orc.norm_weight(bits, 2), np.array([2.0, 3.0, -2.0], np.float32))
