@@ -19,7 +19,8 @@
 // the partials behind a device-scope fence, measured 20 us slower per call:
 // the fence writes back the L2.  Small out_dim runs on fewer workgroups.)
 //
-// Small path (batch <= 8, any in_dim multiple of 8): one wave per output row.
+// Dot path (one or two rows of x, up to eight for narrow out_dim; in_dim any
+// multiple of 8): one wave per output row, v_dot2_f32_f16 into fp32.
 #include <hip/hip_runtime.h>
 
 #include "anelm_common.hpp"
@@ -243,71 +244,203 @@ __global__ __launch_bounds__(64 * NW) void proj_mfma_kernel(ProjArgs a) {
     }
 }
 
-// ---- small batches, any in_dim multiple of 8 -------------------------------
-// One wave per output row; lanes cover 512 consecutive inputs per chunk (8
-// halves, one 16-byte load each), and the weight loads of up to 8 chunks are
-// issued before the first is used.  The inputs x are tiny and shared by
-// every row: they come from cache.
-template <int BT>
-__global__ __launch_bounds__(256) void proj_rows_kernel(float* y, const float* x, const uint16_t* W, int out_dim,
-                                                        int in_dim, long ld_x, long ld_y, int batch) {
-    constexpr int NC = 8;  // chunks of 512 inputs in flight
-    const int lane = threadIdx.x & 63;
-    const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (row >= out_dim) return;
-    const uint16_t* wr = W + row * in_dim;
-    float acc[BT];
+// ---- one or two rows of x: one wave per output row ------------------------
+// Below a few rows of x the 16-column MFMA tile is mostly idle and the work
+// is a matrix-vector product bound by how fast W streams in.  Here each wave
+// owns RPW output rows (2*RPW with the SwiGLU's up rows) for BT rows of x;
+// lane l covers inputs 8l .. 8l+7 of every 512-input chunk, one 16-byte load
+// of each weight row, and the loads of NCH chunks are in flight together.
+// Products are v_dot2_f32_f16 of fp16 pairs into fp32 (a fp16 x fp16
+// product is exact in fp32), a wave sum closes each row, and lane t of the
+// wave writes row t's result.  x comes from cache and is rounded to fp16 (after
+// the fused RMSNorm, if any) on the way in, the same x16 the MFMA path uses.
+// Small out_dim gets the most from it: 1024 output rows are 64 MFMA
+// workgroups but 1024 waves here.
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ half2v as_half2(uint32_t u) {
+    half2v r;
+    __builtin_memcpy(&r, &u, 4);
+    return r;
+}
+
+__device__ __forceinline__ float4 norm_scale(float4 v, float s, uint32_t g01, uint32_t g23) {
+    v.x = (v.x * s) * bf16_to_f32(g01 & 0xFFFFu);
+    v.y = (v.y * s) * bf16_to_f32(g01 >> 16);
+    v.z = (v.z * s) * bf16_to_f32(g23 & 0xFFFFu);
+    v.w = (v.w * s) * bf16_to_f32(g23 >> 16);
+    return v;
+}
+
+template <int BT, int RPW, int NCH, bool NORM, int EPI>
+__global__ __launch_bounds__(256) void proj_dot_kernel(ProjArgs a) {
+    constexpr int NR = EPI == kSwiGLU ? 2 * RPW : RPW;  // weight rows per wave
+    __shared__ float s_part[4][BT];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const long r0 = ((long)blockIdx.x * 4 + wv) * RPW;
+    // operand rows, clamped: rows past the end compute values that are never stored
+    const uint16_t* wp[NR];
 #pragma unroll
-    for (int b = 0; b < BT; b++) acc[b] = 0.0f;
-    for (int c0 = 0; c0 < in_dim; c0 += NC * 512) {
-        uint4 wv[NC];
+    for (int t = 0; t < NR; t++) {
+        const long r = r0 + t % RPW;
+        wp[t] = a.w + ((r < a.out_dim ? r : a.out_dim - 1) + (t >= RPW ? a.pair_rows : 0)) * a.in_dim;
+    }
+    const float* xf = static_cast<const float*>(a.x);
+    uint4 wr[NCH][NR];
+    int idx[NCH];  // this lane's first input in each chunk, clamped into the row
+    auto issue = [&](int c0) {
 #pragma unroll
-        for (int k = 0; k < NC; k++) {
-            const int c = c0 + k * 512 + lane * 8;
-            wv[k] = c < in_dim ? ld_nt(reinterpret_cast<const uint4*>(wr + c)) : make_uint4(0u, 0u, 0u, 0u);
+        for (int k = 0; k < NCH; k++) {
+            const int i = c0 + 512 * k + 8 * lane;
+            idx[k] = i < a.in_dim ? i : a.in_dim - 8;
+#pragma unroll
+            for (int t = 0; t < NR; t++) wr[k][t] = ld_nt(reinterpret_cast<const uint4*>(wp[t] + idx[k]));
+        }
+    };
+    // the first chunks' weight loads go out before the RMSNorm prologue
+    issue(0);
+
+    float scale[BT];
+#pragma unroll
+    for (int b = 0; b < BT; b++) scale[b] = 1.0f;
+    if constexpr (NORM) {
+        // the workgroup's 256 lanes share each row's sum of squares
+#pragma unroll
+        for (int b = 0; b < BT; b++) {
+            float sp = 0.f;
+            if (b < a.batch)
+                for (int k = 4 * (int)threadIdx.x; k < a.in_dim; k += 1024) {
+                    const float4 v = *reinterpret_cast<const float4*>(xf + (long)b * a.ld_x + k);
+                    sp = fmaf(v.x, v.x, sp);
+                    sp = fmaf(v.y, v.y, sp);
+                    sp = fmaf(v.z, v.z, sp);
+                    sp = fmaf(v.w, v.w, sp);
+                }
+            sp = wave_sum(sp);
+            if (lane == 0) s_part[wv][b] = sp;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int b = 0; b < BT; b++) {
+            const float ss = (s_part[0][b] + s_part[1][b]) + (s_part[2][b] + s_part[3][b]);
+            scale[b] = 1.0f / sqrtf(ss / (float)a.in_dim + a.eps);
+        }
+    }
+    if (r0 >= a.out_dim) return;  // whole wave, after the workgroup's barrier
+
+    float acc[NR][BT];
+#pragma unroll
+    for (int t = 0; t < NR; t++)
+#pragma unroll
+        for (int b = 0; b < BT; b++) acc[t][b] = 0.f;
+    for (int c0 = 0; c0 < a.in_dim; c0 += 512 * NCH) {
+        if (c0) issue(c0);
+        uint4 gq[NORM ? NCH : 1];
+        if constexpr (NORM) {
+#pragma unroll
+            for (int k = 0; k < NCH; k++) gq[k] = *reinterpret_cast<const uint4*>(a.gamma + idx[k]);
         }
 #pragma unroll
-        for (int k = 0; k < NC; k++) {
-            const int c = c0 + k * 512 + lane * 8;
-            if (c >= in_dim) break;  // this lane is past the end of the row (inputs are not read there)
-            const uint32_t u[4] = {wv[k].x, wv[k].y, wv[k].z, wv[k].w};
-            float wf[8];
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                wf[2 * e] = f16_to_f32_exact(u[e] & 0xFFFFu);
-                wf[2 * e + 1] = f16_to_f32_exact(u[e] >> 16);
-            }
+        for (int k = 0; k < NCH; k++) {
+            const bool live = c0 + 512 * k + 8 * lane < a.in_dim;
 #pragma unroll
             for (int b = 0; b < BT; b++) {
-                if (b < batch) {
-                    const float4 p = reinterpret_cast<const float4*>(x + b * ld_x + c)[0];
-                    const float4 d = reinterpret_cast<const float4*>(x + b * ld_x + c)[1];
-                    float t = acc[b];
-                    t = fmaf(r16(p.x), wf[0], t);
-                    t = fmaf(r16(p.y), wf[1], t);
-                    t = fmaf(r16(p.z), wf[2], t);
-                    t = fmaf(r16(p.w), wf[3], t);
-                    t = fmaf(r16(d.x), wf[4], t);
-                    t = fmaf(r16(d.y), wf[5], t);
-                    t = fmaf(r16(d.z), wf[6], t);
-                    t = fmaf(r16(d.w), wf[7], t);
-                    acc[b] = t;
+                const float* xp = xf + (long)(b < a.batch ? b : a.batch - 1) * a.ld_x + idx[k];
+                float4 p = reinterpret_cast<const float4*>(xp)[0];
+                float4 q = reinterpret_cast<const float4*>(xp)[1];
+                if constexpr (NORM) {
+                    p = norm_scale(p, scale[b], gq[k].x, gq[k].y);
+                    q = norm_scale(q, scale[b], gq[k].z, gq[k].w);
+                }
+                const _Float16 z = (_Float16)0.0f;
+                const half2v x0 = live ? half2v{(_Float16)p.x, (_Float16)p.y} : half2v{z, z};
+                const half2v x1 = live ? half2v{(_Float16)p.z, (_Float16)p.w} : half2v{z, z};
+                const half2v x2 = live ? half2v{(_Float16)q.x, (_Float16)q.y} : half2v{z, z};
+                const half2v x3 = live ? half2v{(_Float16)q.z, (_Float16)q.w} : half2v{z, z};
+#pragma unroll
+                for (int t = 0; t < NR; t++) {
+                    float s = acc[t][b];
+                    s = __builtin_amdgcn_fdot2(as_half2(wr[k][t].x), x0, s, false);
+                    s = __builtin_amdgcn_fdot2(as_half2(wr[k][t].y), x1, s, false);
+                    s = __builtin_amdgcn_fdot2(as_half2(wr[k][t].z), x2, s, false);
+                    s = __builtin_amdgcn_fdot2(as_half2(wr[k][t].w), x3, s, false);
+                    acc[t][b] = s;
                 }
             }
         }
     }
 #pragma unroll
-    for (int b = 0; b < BT; b++) {
-        const float s = wave_sum(acc[b]);
-        if (lane == 0 && b < batch) y[b * ld_y + row] = r16(s);
+    for (int t = 0; t < NR; t++)
+#pragma unroll
+        for (int b = 0; b < BT; b++) acc[t][b] = wave_sum(acc[t][b]);
+    // lane b*RPW + t stores row r0 + t of x row b
+    float s = 0.f, u = 0.f;
+#pragma unroll
+    for (int t = 0; t < RPW; t++)
+#pragma unroll
+        for (int b = 0; b < BT; b++)
+            if (lane == b * RPW + t) {
+                s = acc[t][b];
+                if constexpr (EPI == kSwiGLU) u = acc[RPW + t][b];
+            }
+    const int t = lane % RPW, b = lane / RPW;
+    if (lane < RPW * BT && b < a.batch && r0 + t < a.out_dim) {
+        float* yp = a.y + (long)b * a.ld_y + r0 + t;
+        if constexpr (EPI == kAdd) *yp = *yp + r16(s);
+        else if constexpr (EPI == kSwiGLU) *yp = silu_ref(r16(s)) * r16(u);
+        else *yp = r16(s);
     }
 }
 
-template <int BT>
-void launch_rows(float* y, const float* x, const uint16_t* W, int out_dim, int in_dim, long ld_x, long ld_y,
-                 int batch, hipStream_t st) {
-    proj_rows_kernel<BT><<<dim3((unsigned)((out_dim + 3) / 4)), dim3(256), 0, st>>>(y, x, W, out_dim, in_dim, ld_x,
-                                                                                     ld_y, batch);
+template <int BT, int RPW, int NCH, bool NORM, int EPI>
+void launch_dot(const ProjArgs& a, hipStream_t st) {
+    const long waves = (a.out_dim + RPW - 1) / RPW;
+    proj_dot_kernel<BT, RPW, NCH, NORM, EPI><<<dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, st>>>(a);
+}
+
+// Launch shape: all of a 1024-input row in one round of loads (NCH = 2),
+// longer rows in rounds of up to six 512-input chunks; two output rows per
+// wave from 4096 rows up and four from 32768 (the LM head), so that each
+// wave has several loads in flight, one row per wave for the SwiGLU's row
+// pairs and for narrow out_dim, so that there are enough waves.
+template <int BT, bool NORM, int EPI>
+void dot_shape(const ProjArgs& a, hipStream_t st) {
+    const int chunks = (a.in_dim + 511) / 512;
+    if (chunks > 2) {
+        if (chunks <= 4) launch_dot<BT, 1, 4, NORM, EPI>(a, st);
+        else launch_dot<BT, 1, 6, NORM, EPI>(a, st);
+    } else if (BT == 1 && EPI != kSwiGLU && a.out_dim >= 32768) {
+        launch_dot<1, 4, 2, NORM, EPI>(a, st);
+    } else if (EPI != kSwiGLU && a.out_dim >= 4096) {
+        launch_dot<BT, 2, 2, NORM, EPI>(a, st);
+    } else {
+        launch_dot<BT, 1, 2, NORM, EPI>(a, st);
+    }
+}
+
+template <bool NORM, int EPI>
+void proj_dot(const ProjArgs& a, hipStream_t st) {
+    if (a.batch == 1) dot_shape<1, NORM, EPI>(a, st);
+    else if (a.batch == 2) dot_shape<2, NORM, EPI>(a, st);
+    else if (a.batch <= 4) dot_shape<4, NORM, EPI>(a, st);
+    else dot_shape<8, NORM, EPI>(a, st);
+}
+
+// Where the dot kernel beats the MFMA kernel (measured at the Qwen3-0.6B
+// decode shapes): one or two rows of x everywhere, up to eight for narrow
+// out_dim (1024 rows: 64 MFMA workgroups).
+bool dot_wins(long batch, int out_dim) { return batch <= 2 || (batch <= 8 && out_dim <= 1024); }
+
+// y and x must not share memory: workgroups write y while others still read x.
+bool overlaps(const void* y, long ld_y, int out_dim, const void* x, long ld_x, int in_dim, int x_bytes, long batch) {
+    const uintptr_t y0 = reinterpret_cast<uintptr_t>(y), x0 = reinterpret_cast<uintptr_t>(x);
+    const uintptr_t y1 = y0 + (uintptr_t)((batch - 1) * ld_y + out_dim) * 4u;
+    const uintptr_t x1 = x0 + (uintptr_t)((batch - 1) * ld_x + in_dim) * (uintptr_t)x_bytes;
+    return x0 < y1 && y0 < x1;
+}
+
+bool dot_ok(const float* x, const uint16_t* w16, long batch, int in_dim, long ld_x) {
+    return batch <= 8 && in_dim % 8 == 0 && ld_x % 4 == 0 && aligned16(x) && aligned16(w16);
 }
 
 // ---- MFMA launch shapes -----------------------------------------------------
@@ -372,18 +505,17 @@ extern "C" int anelm_proj_f16(float* y, const float* x, const uint16_t* w16, lon
     clear_error();
     if (!y || !x || !w16) return fail(ANELM_ERR_INVALID, "proj_f16: null pointer");
     if (!sizes_ok(batch, out_dim, in_dim, ld_x, ld_y)) return fail(ANELM_ERR_INVALID, "proj_f16: bad sizes or strides");
+    if (overlaps(y, ld_y, out_dim, x, ld_x, in_dim, 4, batch))
+        return fail(ANELM_ERR_INVALID, "proj_f16: y overlaps x (y is written while x is still read)");
     hipStream_t st = as_stream(stream);
-    if (mfma_ok(x, false, w16, in_dim, ld_x))
-        return proj_mfma<false>(args(y, x, w16, batch, out_dim, in_dim, ld_x, ld_y), st);
-    if (batch > 8 || in_dim % 8 || ld_x % 4 || !aligned16(x) || !aligned16(w16))
+    const ProjArgs a = args(y, x, w16, batch, out_dim, in_dim, ld_x, ld_y);
+    const bool dot = dot_ok(x, w16, batch, in_dim, ld_x);
+    if (mfma_ok(x, false, w16, in_dim, ld_x) && !(dot && dot_wins(batch, out_dim))) return proj_mfma<false>(a, st);
+    if (!dot)
         return fail(ANELM_ERR_INVALID,
                     "proj_f16: needs in_dim a multiple of 32 (or batch <= 8 and in_dim a multiple of 8), "
                     "ld_x a multiple of 4, 16-byte aligned x and W");
-    const int b = (int)batch;
-    if (b == 1) launch_rows<1>(y, x, w16, out_dim, in_dim, ld_x, ld_y, b, st);
-    else if (b == 2) launch_rows<2>(y, x, w16, out_dim, in_dim, ld_x, ld_y, b, st);
-    else if (b <= 4) launch_rows<4>(y, x, w16, out_dim, in_dim, ld_x, ld_y, b, st);
-    else launch_rows<8>(y, x, w16, out_dim, in_dim, ld_x, ld_y, b, st);
+    proj_dot<false, kStore>(a, st);
     return launch_status("proj_f16");
 }
 
@@ -395,6 +527,8 @@ extern "C" int anelm_proj_f16_x16(float* y, const uint16_t* x16, const uint16_t*
     if (!y || !x16 || !w16) return fail(ANELM_ERR_INVALID, "proj_f16_x16: null pointer");
     if (!sizes_ok(batch, out_dim, in_dim, ld_x, ld_y))
         return fail(ANELM_ERR_INVALID, "proj_f16_x16: bad sizes or strides");
+    if (overlaps(y, ld_y, out_dim, x16, ld_x, in_dim, 2, batch))
+        return fail(ANELM_ERR_INVALID, "proj_f16_x16: y overlaps x (y is written while x is still read)");
     if (!mfma_ok(x16, true, w16, in_dim, ld_x))
         return fail(ANELM_ERR_INVALID,
                     "proj_f16_x16: needs in_dim a multiple of 32, ld_x a multiple of 8, 16-byte aligned x and W");
@@ -416,14 +550,33 @@ extern "C" int anelm_proj_f16_fused(float* y, const float* x, const uint16_t* w1
                     "proj_f16_fused: needs in_dim a multiple of 32, ld_x a multiple of 4, 16-byte aligned x, W, gamma");
     if (epilogue < ANELM_PROJ_STORE || epilogue > ANELM_PROJ_SWIGLU)
         return fail(ANELM_ERR_INVALID, "proj_f16_fused: unknown epilogue %d", epilogue);
-    if (epilogue == ANELM_PROJ_ADD && (const void*)y == (const void*)x)
-        return fail(ANELM_ERR_INVALID, "proj_f16_fused: the residual add needs y distinct from x");
+    if (overlaps(y, ld_y, out_dim, x, ld_x, in_dim, 4, batch))
+        return fail(ANELM_ERR_INVALID,
+                    "proj_f16_fused: y overlaps x (y is written while x is still read; the residual add takes the "
+                    "residual stream as y and the projection input as a separate x)");
     ProjArgs a = args(y, x, w16, batch, out_dim, in_dim, ld_x, ld_y);
     a.gamma = norm_bf16;
     a.eps = eps;
     a.pair_rows = out_dim;  // SwiGLU: W holds out_dim gate rows, then out_dim up rows
     hipStream_t st = as_stream(stream);
     const bool norm = norm_bf16 != nullptr;
+    if (dot_ok(x, w16, batch, in_dim, ld_x) && dot_wins(batch, out_dim)) {
+        switch (epilogue) {
+            case ANELM_PROJ_STORE:
+                if (norm) proj_dot<true, kStore>(a, st);
+                else proj_dot<false, kStore>(a, st);
+                break;
+            case ANELM_PROJ_ADD:
+                if (norm) proj_dot<true, kAdd>(a, st);
+                else proj_dot<false, kAdd>(a, st);
+                break;
+            default:
+                if (norm) proj_dot<true, kSwiGLU>(a, st);
+                else proj_dot<false, kSwiGLU>(a, st);
+                break;
+        }
+        return launch_status("proj_f16_fused");
+    }
     switch (epilogue) {
         case ANELM_PROJ_STORE:
             if (norm) launch_mfma<false, 1, 1, 8, true, kStore>(a, st);

@@ -360,16 +360,16 @@ int anelm_linear_f16(anelm_blas* blas, uint16_t* y16, const uint16_t* x16, const
 
 /* The same projection with the conversions fused (decode batches):
  * y[b, o] = fp16(sum_i fp16_rne(x[b, i]) * W16[o, i]) stored as fp32, x fp32;
- * each weight is read once.  in_dim a multiple of 32 (MFMA kernel, any
- * batch), or batch <= 8 and in_dim a multiple of 8; ld_x a multiple of 4;
- * x and W16 16-byte aligned. */
+ * each weight is read once.  in_dim a multiple of 32 (any batch), or
+ * batch <= 8 and in_dim a multiple of 8; ld_x a multiple of 4; x and W16
+ * 16-byte aligned; y must not overlap x. */
 int anelm_proj_f16(float* y, const float* x, const uint16_t* w16, long batch, int out_dim, int in_dim, long ld_x,
                    long ld_y, void* stream);
 /* anelm_proj_f16 with x already rounded to fp16 (x16 [batch, in_dim], row
  * stride ld_x a multiple of 8, e.g. from anelm_f32_to_f16): for larger
  * batches, where rounding x once beats rounding it in every workgroup.
- * in_dim a multiple of 32.  No counterpart in the reference (the ANE runtime
- * has no batched projection). */
+ * in_dim a multiple of 32; y must not overlap x16.  No counterpart in the
+ * reference (the ANE runtime has no batched projection). */
 int anelm_proj_f16_x16(float* y, const uint16_t* x16, const uint16_t* w16, long batch, int out_dim, int in_dim,
                        long ld_x, long ld_y, void* stream);
 
@@ -380,12 +380,12 @@ int anelm_proj_f16_x16(float* y, const uint16_t* x16, const uint16_t* w16, long 
  *   norm_bf16 != NULL: x is first replaced by rmsnorm(x) * norm_bf16
  *     (core/cpu_ops.cpp:25-31 with eps; norm_bf16 [in_dim], 16-byte aligned);
  *   ANELM_PROJ_STORE:  y = p;
- *   ANELM_PROJ_ADD:    y = y + p (the residual add; y distinct from x);
+ *   ANELM_PROJ_ADD:    y = y + p (the residual add);
  *   ANELM_PROJ_SWIGLU: W16 holds out_dim gate rows then out_dim up rows, and
  *     y = silu(p_gate) * p_up (the SwiGLU of core/ane_runtime.cpp:393-395 in
  *     the fp32 form of core/cpu_ops.cpp:7-14).
- * Each result equals the separate kernels' to within the RMSNorm's
- * summation order.  No counterpart in the reference: the ANE runtime fuses
+ * y must not overlap x.  Each result equals the separate kernels' to within
+ * the RMSNorm's summation order.  No counterpart in the reference: the ANE runtime fuses
  * these inside its own fp16 programs. */
 #define ANELM_PROJ_STORE 0
 #define ANELM_PROJ_ADD 1

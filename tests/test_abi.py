@@ -179,6 +179,9 @@ def test_projection_argument_checks(lib):
     assert fu(fake, fake, fake, 1, 64, 64, 64, 64, odd, 1e-6, 0, None) == -1    # unaligned gamma
     assert fu(fake, fake, fake, 1, 64, 64, 64, 64, None, 1e-6, 1, None) == -1   # residual add onto its own input
     assert b"residual" in lib.anelm_last_error()
+    assert f(fake, P(0x10F0), fake, 1, 64, 64, 64, 64, None) == -1             # x starts inside y (64 floats at 0x1000)
+    assert b"overlaps" in lib.anelm_last_error()
+    assert x16(P(0x1040), fake, fake, 1, 64, 64, 64, 64, None) == -1           # y starts inside the fp16 x
     b = lib.anelm_gqa_attention_bounded
     assert b(fake, fake, fake, fake, fake, fake, 1, 32, 8, 128, 4096, 128, 4096, 2048, 2048 * 1024, 0, fake,
              1 << 30, None) == -1                                               # bound 0

@@ -63,10 +63,17 @@ def check_projection(orc, x, w, got):
     assert np.all(np.abs(got - ref) <= ulp + mag * 2.0 ** -21 * 4)
 
 
-# (in_dim % 32 == 0: MFMA kernel; otherwise the row kernel for batch <= 8)
+# One or two rows of x (up to eight for out_dim <= 1024) take the dot kernel,
+# the rest the MFMA kernel; in_dim not a multiple of 32 needs the dot kernel.
+# The dot kernel's launch shapes: one output row per wave (1024-input rows in
+# one round of loads, longer ones in rounds of 4 or 6 chunks, 4096 inputs in
+# two rounds), two per wave from 4096 rows (odd counts leave a half-used
+# wave), four from 32768 rows, and ragged in_dim (masked lanes).
 @pytest.mark.parametrize("B,out_dim,in_dim", [(1, 4096, 1024), (3, 1024, 3072), (8, 6144, 1024), (2, 77, 1000),
                                                (1, 151936, 1024), (5, 1024, 2048), (16, 1000, 96), (17, 3072, 1024),
-                                               (64, 4096, 1024), (33, 100, 32), (4, 64, 1000)])
+                                               (64, 4096, 1024), (33, 100, 32), (4, 64, 1000), (1, 4097, 1024),
+                                               (2, 4101, 992), (1, 32771, 512), (1, 1023, 4096), (2, 1000, 2056),
+                                               (8, 1024, 200), (1, 33, 8)])
 def test_proj_f16_fused_conversions(hip, orc, rng, B, out_dim, in_dim):
     import torch
 
@@ -109,7 +116,9 @@ def _ulp16(v):
     return np.spacing(np.abs(v).astype(np.float16)).astype(np.float64)
 
 
-@pytest.mark.parametrize("B,out_dim,in_dim", [(1, 1024, 1024), (11, 4096, 1024), (16, 300, 256), (3, 151936, 1024)])
+@pytest.mark.parametrize("B,out_dim,in_dim", [(1, 1024, 1024), (11, 4096, 1024), (16, 300, 256), (3, 151936, 1024),
+                                               (1, 4097, 1024), (2, 4101, 992), (1, 32771, 512), (1, 151936, 1024),
+                                               (4, 777, 3072)])
 def test_proj_fused_rmsnorm_prologue(hip, orc, rng, B, out_dim, in_dim):
     """The fused RMSNorm equals the oracle's RMSNorm followed by the
     projection (the normalised row rounded to fp16 on the way in)."""
@@ -124,7 +133,8 @@ def test_proj_fused_rmsnorm_prologue(hip, orc, rng, B, out_dim, in_dim):
     check_projection(orc, xn, w, host(y).astype(np.float64))
 
 
-@pytest.mark.parametrize("B,out_dim,in_dim", [(1, 1024, 2048), (7, 1024, 3072), (16, 256, 512)])
+@pytest.mark.parametrize("B,out_dim,in_dim", [(1, 1024, 2048), (7, 1024, 3072), (16, 256, 512), (2, 1023, 4096),
+                                               (1, 1024, 3072), (8, 1000, 992)])
 def test_proj_fused_residual_add(hip, orc, rng, B, out_dim, in_dim):
     import torch
 
@@ -140,7 +150,8 @@ def test_proj_fused_residual_add(hip, orc, rng, B, out_dim, in_dim):
     assert np.all(np.abs(got - want) <= tol)
 
 
-@pytest.mark.parametrize("B,inter,in_dim,norm", [(1, 3072, 1024, True), (5, 384, 256, True), (16, 160, 64, False)])
+@pytest.mark.parametrize("B,inter,in_dim,norm", [(1, 3072, 1024, True), (5, 384, 256, True), (16, 160, 64, False),
+                                                   (2, 3072, 1024, True), (1, 1001, 4096, False), (8, 512, 1024, True)])
 def test_proj_fused_swiglu(hip, orc, rng, B, inter, in_dim, norm):
     """gate|up projection with the SwiGLU epilogue: silu(g) * u of the rounded
     gate and up projections, in the fp32 form of core/cpu_ops.cpp:7-14."""
@@ -163,7 +174,7 @@ def test_proj_fused_swiglu(hip, orc, rng, B, inter, in_dim, norm):
     assert np.all(np.abs(host(h).astype(np.float64) - want) <= tol)
 
 
-@pytest.mark.parametrize("tied,B", [(True, 3), (False, 3), (True, 11)])
+@pytest.mark.parametrize("tied,B", [(True, 3), (False, 3), (True, 11), (True, 1)])
 def test_decode_steps_match_oracle(hip, orc, rng, tmp_path, tied, B):
     import torch
 
