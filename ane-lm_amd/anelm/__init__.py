@@ -50,6 +50,7 @@ _SIGS = {
     "anelm_last_error": (ctypes.c_char_p, []),
     "anelm_version": (_I, []),
     "anelm_rmsnorm": (_I, [_P, _P, _P, _I, _L, _I, _L, _L, _F, _P]),
+    "anelm_rmsnorm_f16": (_I, [_P, _P, _P, _I, _L, _I, _L, _L, _F, _P]),
     "anelm_add_rmsnorm": (_I, [_P, _P, _P, _P, _I, _L, _I, _L, _L, _L, _F, _P]),
     "anelm_qknorm_rope": (_I, [_P, _P, _L, _L, _P, _P, _I, _P, _P, _P, _I, _F, _L, _I, _I, _I, _F, _P]),
     "anelm_rope_cached": (_I, [_P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _P, _P, _P]),
@@ -97,6 +98,7 @@ _SIGS = {
     "anelm_proj_f16": (_I, [_P, _P, _P, _L, _I, _I, _L, _L, _P]),
     "anelm_proj_f16_x16": (_I, [_P, _P, _P, _L, _I, _I, _L, _L, _P]),
     "anelm_proj_f16_fused": (_I, [_P, _P, _P, _L, _I, _I, _L, _L, _P, _F, _I, _P]),
+    "anelm_proj_f16_x16_fused": (_I, [_P, _P, _P, _L, _I, _I, _L, _L, _I, _P]),
     "anelm_qwen3_load": (_P, [ctypes.c_char_p, _P, _I, _I, _P]),
     "anelm_qwen3_free": (None, [_P]),
     "anelm_qwen3_reset": (_I, [_P, _P]),
@@ -175,6 +177,14 @@ def rmsnorm(out, x, w, eps=1e-6, stream=None):
     _, _, ldo = _rows(out)
     _check(lib().anelm_rmsnorm(_ptr(out), _ptr(x), _ptr(w), _dtype_code(w), rows, dim, ldx, ldo, eps,
                                _stream(stream)))
+
+
+def rmsnorm_f16(out16, x, w, eps=1e-6, stream=None):
+    """out16 (int16/float16 tensor, fp16 bits) = fp16 RNE of rmsnorm(x) * w."""
+    rows, dim, ldx = _rows(x)
+    _, _, ldo = _rows(out16)
+    _check(lib().anelm_rmsnorm_f16(_ptr(out16), _ptr(x), _ptr(w), _dtype_code(w), rows, dim, ldx, ldo, eps,
+                                   _stream(stream)))
 
 
 def add_rmsnorm(x, y, out, w, eps=1e-6, stream=None):
@@ -490,17 +500,26 @@ def proj_f16_x16(y, x16, w16, stream=None):
                                     _stream(stream)))
 
 
-PROJ_STORE, PROJ_ADD, PROJ_SWIGLU = 0, 1, 2
+PROJ_STORE, PROJ_ADD, PROJ_SWIGLU, PROJ_SWIGLU_F16 = 0, 1, 2, 3
 
 
 def proj_f16_fused(y, x, w16, norm=None, eps=1e-6, epilogue=PROJ_STORE, stream=None):
-    """Decode projection (B <= 16) with an optional RMSNorm prologue (norm:
+    """Decode projection with an optional RMSNorm prologue (norm:
     bf16 gamma as int16/bfloat16 tensor) and a store / residual-add / SwiGLU
     epilogue; for SwiGLU w16 holds the gate rows then the up rows."""
     batch, in_dim = x.shape
     out_dim = w16.shape[0] // 2 if epilogue == PROJ_SWIGLU else w16.shape[0]
     _check(lib().anelm_proj_f16_fused(_ptr(y), _ptr(x), _ptr(w16), batch, out_dim, in_dim, _ld(x), _ld(y),
                                       _ptr(norm), eps, epilogue, _stream(stream)))
+
+
+def proj_f16_x16_fused(y, x16, w16, epilogue=PROJ_STORE, stream=None):
+    """The fused epilogues on fp16 rows x16 (int16/float16 tensor of fp16
+    bits); y fp32, or fp16 bits with PROJ_SWIGLU_F16."""
+    batch, in_dim = x16.shape
+    out_dim = w16.shape[0] // 2 if epilogue in (PROJ_SWIGLU, PROJ_SWIGLU_F16) else w16.shape[0]
+    _check(lib().anelm_proj_f16_x16_fused(_ptr(y), _ptr(x16), _ptr(w16), batch, out_dim, in_dim, _ld(x16), _ld(y),
+                                          epilogue, _stream(stream)))
 
 
 class Qwen3Model:

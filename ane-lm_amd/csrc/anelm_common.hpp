@@ -151,6 +151,17 @@ __device__ __forceinline__ float silu_ref(float g) {
     return g / t;
 }
 
+// fp32 -> fp16 rounded to nearest even, of the value as already rounded to
+// fp32.  Without the empty asm the compiler folds a preceding multiply or
+// add into v_fma_mixlo_f16, which rounds the exact result once, straight to
+// fp16 (it does so even under -ffp-contract=off), so a product such as
+// (x * s) * gamma could land one fp16 ulp away from the reference's fp32
+// result rounded to fp16.
+__device__ __forceinline__ _Float16 to_f16(float v) {
+    __asm__("" : "+v"(v));
+    return (_Float16)v;
+}
+
 // Non-temporal 16-byte loads / stores (streamed data that is touched once).
 typedef float nat_f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int nat_u32x4 __attribute__((ext_vector_type(4)));

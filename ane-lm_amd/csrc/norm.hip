@@ -23,8 +23,15 @@ namespace anelm {
 // H=4096) keep many rows in flight per CU, which measured faster than one
 // wave per row holding the whole row.  The row is entirely in registers
 // before anything is written, so out may alias x and y may alias out.
-template <int NV, int DT, bool ADD>
-__global__ __launch_bounds__(1024) void rmsnorm_row_kernel(float* out, float* x, const float* y,
+// With O16 the output is fp16 rounded to nearest even: the activation
+// conversion at the ANE kernel inputs (core/ane_runtime.cpp:604-612) applied
+// to the RMSNorm's fp32 result, for a projection that takes fp16 inputs.
+__device__ __forceinline__ uint32_t f16_bits_rne(float v) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, to_f16(v));
+}
+
+template <int NV, int DT, bool ADD, bool O16 = false>
+__global__ __launch_bounds__(1024) void rmsnorm_row_kernel(void* out, float* x, const float* y,
                                                            const void* w, long rows, int dim,
                                                            long ld_x, long ld_y, long ld_out,
                                                            float eps) {
@@ -74,7 +81,6 @@ __global__ __launch_bounds__(1024) void rmsnorm_row_kernel(float* out, float* x,
         for (int k = 1; k < nw; k++) ss += part[k];
     }
     const float s = 1.0f / sqrtf(ss / (float)dim + eps);
-    float* orow = out + row * ld_out;
 #pragma unroll
     for (int i = 0; i < NV; i++) {
         const int c = (i * nthr + tid) * 4;
@@ -85,15 +91,21 @@ __global__ __launch_bounds__(1024) void rmsnorm_row_kernel(float* out, float* x,
             o.y = (v[i].y * s) * wv.y;
             o.z = (v[i].z * s) * wv.z;
             o.w = (v[i].w * s) * wv.w;
-            st_nt(reinterpret_cast<float4*>(orow + c), o);
+            if constexpr (O16) {
+                uint16_t* orow = static_cast<uint16_t*>(out) + row * ld_out;
+                *reinterpret_cast<uint2*>(orow + c) = make_uint2(f16_bits_rne(o.x) | (f16_bits_rne(o.y) << 16),
+                                                                 f16_bits_rne(o.z) | (f16_bits_rne(o.w) << 16));
+            } else {
+                st_nt(reinterpret_cast<float4*>(static_cast<float*>(out) + row * ld_out + c), o);
+            }
         }
     }
 }
 
 // Any dim / alignment: one 256-thread block per row, two passes over the row
 // (the second re-reads x, which the same thread wrote in the ADD case).
-template <int DT, bool ADD>
-__global__ __launch_bounds__(256) void rmsnorm_block_kernel(float* out, float* x, const float* y,
+template <int DT, bool ADD, bool O16 = false>
+__global__ __launch_bounds__(256) void rmsnorm_block_kernel(void* out, float* x, const float* y,
                                                             const void* w, long rows, int dim,
                                                             long ld_x, long ld_y, long ld_out,
                                                             float eps) {
@@ -115,16 +127,19 @@ __global__ __launch_bounds__(256) void rmsnorm_block_kernel(float* out, float* x
     __syncthreads();
     ss = (part[0] + part[1]) + (part[2] + part[3]);
     const float s = 1.0f / sqrtf(ss / (float)dim + eps);
-    float* orow = out + row * ld_out;
-    for (int c = threadIdx.x; c < dim; c += 256) orow[c] = (xr[c] * s) * load_w<DT>(w, c);
+    for (int c = threadIdx.x; c < dim; c += 256) {
+        const float o = (xr[c] * s) * load_w<DT>(w, c);
+        if constexpr (O16) static_cast<uint16_t*>(out)[row * ld_out + c] = (uint16_t)f16_bits_rne(o);
+        else static_cast<float*>(out)[row * ld_out + c] = o;
+    }
 }
 
-template <int DT, bool ADD>
-static int launch_rmsnorm_dt(float* out, float* x, const float* y, const void* w, long rows,
+template <int DT, bool ADD, bool O16 = false>
+static int launch_rmsnorm_dt(void* out, float* x, const float* y, const void* w, long rows,
                              int dim, long ld_x, long ld_y, long ld_out, float eps,
                              hipStream_t st) {
     const bool vec = (dim % 4 == 0) && (ld_x % 4 == 0) && (ld_out % 4 == 0) && aligned16(x) &&
-                     aligned16(out) &&
+                     (O16 ? aligned8(out) : aligned16(out)) &&
                      (DT == ANELM_F32 ? aligned16(w) : aligned8(w)) &&
                      (!ADD || ((ld_y % 4 == 0) && aligned16(y)));
     const int nvec = dim / 4;  // float4 per row
@@ -135,25 +150,25 @@ static int launch_rmsnorm_dt(float* out, float* x, const float* y, const void* w
         int threads = ((nvec + nv - 1) / nv + 63) / 64 * 64;
         const dim3 grd((unsigned)rows);
         if (nv == 1)
-            rmsnorm_row_kernel<1, DT, ADD><<<grd, threads, 0, st>>>(out, x, y, w, rows, dim, ld_x, ld_y, ld_out, eps);
+            rmsnorm_row_kernel<1, DT, ADD, O16><<<grd, threads, 0, st>>>(out, x, y, w, rows, dim, ld_x, ld_y, ld_out, eps);
         else if (nv == 2)
-            rmsnorm_row_kernel<2, DT, ADD><<<grd, threads, 0, st>>>(out, x, y, w, rows, dim, ld_x, ld_y, ld_out, eps);
+            rmsnorm_row_kernel<2, DT, ADD, O16><<<grd, threads, 0, st>>>(out, x, y, w, rows, dim, ld_x, ld_y, ld_out, eps);
         else
-            rmsnorm_row_kernel<4, DT, ADD><<<grd, threads, 0, st>>>(out, x, y, w, rows, dim, ld_x, ld_y, ld_out, eps);
+            rmsnorm_row_kernel<4, DT, ADD, O16><<<grd, threads, 0, st>>>(out, x, y, w, rows, dim, ld_x, ld_y, ld_out, eps);
         return launch_status("rmsnorm");
     }
-    rmsnorm_block_kernel<DT, ADD><<<dim3((unsigned)rows), dim3(256), 0, st>>>(out, x, y, w, rows, dim, ld_x,
-                                                                              ld_y, ld_out, eps);
+    rmsnorm_block_kernel<DT, ADD, O16><<<dim3((unsigned)rows), dim3(256), 0, st>>>(out, x, y, w, rows, dim, ld_x,
+                                                                                   ld_y, ld_out, eps);
     return launch_status("rmsnorm");
 }
 
-template <bool ADD>
-static int launch_rmsnorm(float* out, float* x, const float* y, const void* w, int dt, long rows,
+template <bool ADD, bool O16 = false>
+static int launch_rmsnorm(void* out, float* x, const float* y, const void* w, int dt, long rows,
                           int dim, long ld_x, long ld_y, long ld_out, float eps, hipStream_t st) {
     switch (dt) {
-        case ANELM_F32: return launch_rmsnorm_dt<ANELM_F32, ADD>(out, x, y, w, rows, dim, ld_x, ld_y, ld_out, eps, st);
-        case ANELM_F16: return launch_rmsnorm_dt<ANELM_F16, ADD>(out, x, y, w, rows, dim, ld_x, ld_y, ld_out, eps, st);
-        case ANELM_BF16: return launch_rmsnorm_dt<ANELM_BF16, ADD>(out, x, y, w, rows, dim, ld_x, ld_y, ld_out, eps, st);
+        case ANELM_F32: return launch_rmsnorm_dt<ANELM_F32, ADD, O16>(out, x, y, w, rows, dim, ld_x, ld_y, ld_out, eps, st);
+        case ANELM_F16: return launch_rmsnorm_dt<ANELM_F16, ADD, O16>(out, x, y, w, rows, dim, ld_x, ld_y, ld_out, eps, st);
+        case ANELM_BF16: return launch_rmsnorm_dt<ANELM_BF16, ADD, O16>(out, x, y, w, rows, dim, ld_x, ld_y, ld_out, eps, st);
         default: return fail(ANELM_ERR_INVALID, "rmsnorm: unknown weight dtype %d", dt);
     }
 }
@@ -368,6 +383,20 @@ extern "C" int anelm_rmsnorm(float* out, const float* x, const void* w, int w_dt
     clear_error();
     return launch_rmsnorm<false>(out, const_cast<float*>(x), nullptr, w, w_dtype, rows, dim, ld_x, 0,
                                  ld_out, eps, as_stream(stream));
+}
+
+extern "C" int anelm_rmsnorm_f16(uint16_t* out16, const float* x, const void* w, int w_dtype, long rows, int dim,
+                                 long ld_x, long ld_out, float eps, void* stream) {
+    if (!out16 || !x || !w) return fail(ANELM_ERR_INVALID, "anelm_rmsnorm_f16: null pointer");
+    if (rows <= 0 || dim <= 0) return fail(ANELM_ERR_INVALID, "anelm_rmsnorm_f16: rows=%ld dim=%d", rows, dim);
+    if (ld_x < dim || ld_out < dim) return fail(ANELM_ERR_INVALID, "anelm_rmsnorm_f16: ld < dim");
+    if (rows > 0x7FFFFFFFL) return fail(ANELM_ERR_INVALID, "anelm_rmsnorm_f16: too many rows");
+    const uintptr_t o0 = reinterpret_cast<uintptr_t>(out16), x0 = reinterpret_cast<uintptr_t>(x);
+    if (o0 < x0 + (uintptr_t)((rows - 1) * ld_x + dim) * 4u && x0 < o0 + (uintptr_t)((rows - 1) * ld_out + dim) * 2u)
+        return fail(ANELM_ERR_INVALID, "anelm_rmsnorm_f16: out16 overlaps x");
+    clear_error();
+    return launch_rmsnorm<false, true>(out16, const_cast<float*>(x), nullptr, w, w_dtype, rows, dim, ld_x, 0, ld_out,
+                                       eps, as_stream(stream));
 }
 
 extern "C" int anelm_add_rmsnorm(float* x, const float* y, float* out, const void* w, int w_dtype,

@@ -32,18 +32,18 @@ namespace {
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float float4v __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ float r16(float v) { return (float)(_Float16)v; }
+__device__ __forceinline__ float r16(float v) { return (float)to_f16(v); }
 
 __device__ __forceinline__ half8 to_half8(float4 a, float4 b) {
     half8 r;
-    r[0] = (_Float16)a.x;
-    r[1] = (_Float16)a.y;
-    r[2] = (_Float16)a.z;
-    r[3] = (_Float16)a.w;
-    r[4] = (_Float16)b.x;
-    r[5] = (_Float16)b.y;
-    r[6] = (_Float16)b.z;
-    r[7] = (_Float16)b.w;
+    r[0] = to_f16(a.x);
+    r[1] = to_f16(a.y);
+    r[2] = to_f16(a.z);
+    r[3] = to_f16(a.w);
+    r[4] = to_f16(b.x);
+    r[5] = to_f16(b.y);
+    r[6] = to_f16(b.z);
+    r[7] = to_f16(b.w);
     return r;
 }
 
@@ -51,6 +51,16 @@ __device__ __forceinline__ half8 as_half8(uint4 u) {
     half8 r;
     __builtin_memcpy(&r, &u, 16);
     return r;
+}
+
+// (x * s) * gamma for four inputs, gamma as two packed bf16 pairs: the fused
+// RMSNorm's output, before its fp16 rounding
+__device__ __forceinline__ float4 norm_scale(float4 v, float s, uint32_t g01, uint32_t g23) {
+    v.x = (v.x * s) * bf16_to_f32(g01 & 0xFFFFu);
+    v.y = (v.y * s) * bf16_to_f32(g01 >> 16);
+    v.z = (v.z * s) * bf16_to_f32(g23 & 0xFFFFu);
+    v.w = (v.w * s) * bf16_to_f32(g23 >> 16);
+    return v;
 }
 
 struct ProjArgs {
@@ -62,8 +72,10 @@ struct ProjArgs {
     // fused prologue (kNorm): x replaced by rmsnorm(x) * gamma, gamma bf16 [in_dim]
     const uint16_t* gamma;
     float eps;
-    // SwiGLU epilogue (kSwiGLU): the up rows follow the gate rows at this offset
+    // SwiGLU epilogue (kSwiGLU, kSwiGLU16): the up rows follow the gate rows at this offset
     long pair_rows;
+    // kSwiGLU16: the output as fp16 bits (row stride ld_y) instead of y
+    uint16_t* y16;
 };
 
 // What the epilogue does with the rounded projection p = fp16(sum) (as fp32):
@@ -71,9 +83,11 @@ enum Epilogue {
     kStore = 0,   // y = p
     kAdd = 1,     // y = y + p  (the residual add of qwen3.cpp:516, :527)
     kSwiGLU = 2,  // y = silu(p_gate) * p_up  (core/ane_runtime.cpp:393-395)
+    kSwiGLU16 = 3,  // the same rounded to fp16 (nearest even) into y16: the next projection's input
 };
+constexpr bool is_swiglu(int epi) { return epi == kSwiGLU || epi == kSwiGLU16; }
 
-// kNorm (fp32 x, NB = 1): the workgroup first computes the RMSNorm scale
+// kNorm (fp32 x): the workgroup first computes the RMSNorm scale
 // 1/sqrtf(ss/dim + eps) of each of its batch rows (core/cpu_ops.cpp:25-31),
 // and every input is formed as (x * s) * gamma before its fp16 rounding,
 // exactly the separate RMSNorm's output.  kSwiGLU needs RT = 2: tile 0 holds
@@ -81,20 +95,20 @@ enum Epilogue {
 // gate rows.
 template <bool XH, int NB, int RT, int R, bool NORM = false, int EPI = kStore, int NW = 4>
 __global__ __launch_bounds__(64 * NW) void proj_mfma_kernel(ProjArgs a) {
-    static_assert(!NORM || (!XH && NB == 1), "the fused norm reads fp32 x, one batch block");
-    static_assert(EPI != kSwiGLU || RT == 2, "SwiGLU pairs a gate tile with an up tile");
+    static_assert(!NORM || !XH, "the fused norm reads fp32 x");
+    static_assert(!is_swiglu(EPI) || RT == 2, "SwiGLU pairs a gate tile with an up tile");
     __shared__ float4v part[NW][RT * NB][64];
-    __shared__ float s_scale[16];
+    __shared__ float s_scale[16 * NB];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int g = lane >> 4, c = lane & 15;
-    const long row0 = (long)blockIdx.x * 16 * (EPI == kSwiGLU ? 1 : RT);
+    const long row0 = (long)blockIdx.x * 16 * (is_swiglu(EPI) ? 1 : RT);
     const int b0 = blockIdx.y * 16 * NB;
     // operand rows, clamped: rows past the end compute values that are never stored
     const uint16_t* wp[RT];
 #pragma unroll
     for (int t = 0; t < RT; t++) {
-        const long r0 = EPI == kSwiGLU ? row0 + c : row0 + 16 * t + c;
-        const long r = (r0 < a.out_dim ? r0 : a.out_dim - 1) + (EPI == kSwiGLU && t == 1 ? a.pair_rows : 0);
+        const long r0 = is_swiglu(EPI) ? row0 + c : row0 + 16 * t + c;
+        const long r = (r0 < a.out_dim ? r0 : a.out_dim - 1) + (is_swiglu(EPI) && t == 1 ? a.pair_rows : 0);
         wp[t] = a.w + r * a.in_dim + 8 * g;
     }
     long xoff[NB];
@@ -136,10 +150,10 @@ __global__ __launch_bounds__(64 * NW) void proj_mfma_kernel(ProjArgs a) {
     issue(wv);
 
     if constexpr (NORM) {
-        // wave w: the tile's batch rows w, w+NW, ... that exist; each lane has
-        // four 16-byte loads in flight per round (a 1024-wide row in one)
-        const int nrows = a.batch - b0 < 16 ? a.batch - b0 : 16;
-        if (threadIdx.x < 16 && (int)threadIdx.x >= nrows) s_scale[threadIdx.x] = 0.0f;  // unused columns
+        // wave w: the workgroup's batch rows w, w+NW, ... that exist; each
+        // lane has four 16-byte loads in flight per round (a 1024-wide row in one)
+        const int nrows = a.batch - b0 < 16 * NB ? a.batch - b0 : 16 * NB;
+        if ((int)threadIdx.x < 16 * NB && (int)threadIdx.x >= nrows) s_scale[threadIdx.x] = 0.0f;  // unused columns
         for (int i = wv; i < nrows; i += NW) {
             const float* xrow = xf + (long)(b0 + i) * a.ld_x;
             float sp[4] = {0.f, 0.f, 0.f, 0.f};
@@ -162,7 +176,9 @@ __global__ __launch_bounds__(64 * NW) void proj_mfma_kernel(ProjArgs a) {
         }
         __syncthreads();
     }
-    const float my_scale = NORM ? s_scale[c] : 1.0f;
+    float my_scale[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; nb++) my_scale[nb] = NORM ? s_scale[16 * nb + c] : 1.0f;
 
     float4v acc[RT][NB];
 #pragma unroll
@@ -183,15 +199,7 @@ __global__ __launch_bounds__(64 * NW) void proj_mfma_kernel(ProjArgs a) {
                         const float4 u = xr[j][nb][0], v = xr[j][nb][1];
                         const uint4 q = gq[j];
                         float4 lo, hi;
-                        lo.x = (u.x * my_scale) * bf16_to_f32(q.x & 0xFFFFu);
-                        lo.y = (u.y * my_scale) * bf16_to_f32(q.x >> 16);
-                        lo.z = (u.z * my_scale) * bf16_to_f32(q.y & 0xFFFFu);
-                        lo.w = (u.w * my_scale) * bf16_to_f32(q.y >> 16);
-                        hi.x = (v.x * my_scale) * bf16_to_f32(q.z & 0xFFFFu);
-                        hi.y = (v.y * my_scale) * bf16_to_f32(q.z >> 16);
-                        hi.z = (v.z * my_scale) * bf16_to_f32(q.w & 0xFFFFu);
-                        hi.w = (v.w * my_scale) * bf16_to_f32(q.w >> 16);
-                        xb = to_half8(lo, hi);
+                        xb = to_half8(norm_scale(u, my_scale[nb], q.x, q.y), norm_scale(v, my_scale[nb], q.z, q.w));
                     } else {
                         xb = to_half8(xr[j][nb][0], xr[j][nb][1]);
                     }
@@ -207,7 +215,7 @@ __global__ __launch_bounds__(64 * NW) void proj_mfma_kernel(ProjArgs a) {
 #pragma unroll
         for (int nb = 0; nb < NB; nb++) part[wv][t * NB + nb][lane] = acc[t][nb];
     __syncthreads();
-    if constexpr (EPI == kSwiGLU) {
+    if constexpr (is_swiglu(EPI)) {
         for (int nb = wv; nb < NB; nb += NW) {
             float4v gs = part[0][nb][lane], us = part[0][NB + nb][lane];
             for (int w = 1; w < NW; w++) {
@@ -217,10 +225,16 @@ __global__ __launch_bounds__(64 * NW) void proj_mfma_kernel(ProjArgs a) {
             const int b = b0 + nb * 16 + c;
             const long r = row0 + 4 * g;
             if (b < a.batch) {
-                float* yr = a.y + (long)b * a.ld_y;
 #pragma unroll
-                for (int i = 0; i < 4; i++)
-                    if (r + i < a.out_dim) yr[r + i] = silu_ref(r16(gs[i])) * r16(us[i]);
+                for (int i = 0; i < 4; i++) {
+                    if (r + i < a.out_dim) {
+                        const float h = silu_ref(r16(gs[i])) * r16(us[i]);
+                        if constexpr (EPI == kSwiGLU16)
+                            a.y16[(long)b * a.ld_y + r + i] = __builtin_bit_cast(uint16_t, to_f16(h));
+                        else
+                            a.y[(long)b * a.ld_y + r + i] = h;
+                    }
+                }
             }
         }
     } else {
@@ -262,14 +276,6 @@ __device__ __forceinline__ half2v as_half2(uint32_t u) {
     half2v r;
     __builtin_memcpy(&r, &u, 4);
     return r;
-}
-
-__device__ __forceinline__ float4 norm_scale(float4 v, float s, uint32_t g01, uint32_t g23) {
-    v.x = (v.x * s) * bf16_to_f32(g01 & 0xFFFFu);
-    v.y = (v.y * s) * bf16_to_f32(g01 >> 16);
-    v.z = (v.z * s) * bf16_to_f32(g23 & 0xFFFFu);
-    v.w = (v.w * s) * bf16_to_f32(g23 >> 16);
-    return v;
 }
 
 template <int BT, int RPW, int NCH, bool NORM, int EPI>
@@ -353,10 +359,10 @@ __global__ __launch_bounds__(256) void proj_dot_kernel(ProjArgs a) {
                     q = norm_scale(q, scale[b], gq[k].z, gq[k].w);
                 }
                 const _Float16 z = (_Float16)0.0f;
-                const half2v x0 = live ? half2v{(_Float16)p.x, (_Float16)p.y} : half2v{z, z};
-                const half2v x1 = live ? half2v{(_Float16)p.z, (_Float16)p.w} : half2v{z, z};
-                const half2v x2 = live ? half2v{(_Float16)q.x, (_Float16)q.y} : half2v{z, z};
-                const half2v x3 = live ? half2v{(_Float16)q.z, (_Float16)q.w} : half2v{z, z};
+                const half2v x0 = live ? half2v{to_f16(p.x), to_f16(p.y)} : half2v{z, z};
+                const half2v x1 = live ? half2v{to_f16(p.z), to_f16(p.w)} : half2v{z, z};
+                const half2v x2 = live ? half2v{to_f16(q.x), to_f16(q.y)} : half2v{z, z};
+                const half2v x3 = live ? half2v{to_f16(q.z), to_f16(q.w)} : half2v{z, z};
 #pragma unroll
                 for (int t = 0; t < NR; t++) {
                     float s = acc[t][b];
@@ -432,9 +438,10 @@ void proj_dot(const ProjArgs& a, hipStream_t st) {
 bool dot_wins(long batch, int out_dim) { return batch <= 2 || (batch <= 8 && out_dim <= 1024); }
 
 // y and x must not share memory: workgroups write y while others still read x.
-bool overlaps(const void* y, long ld_y, int out_dim, const void* x, long ld_x, int in_dim, int x_bytes, long batch) {
+bool overlaps(const void* y, long ld_y, int out_dim, int y_bytes, const void* x, long ld_x, int in_dim, int x_bytes,
+              long batch) {
     const uintptr_t y0 = reinterpret_cast<uintptr_t>(y), x0 = reinterpret_cast<uintptr_t>(x);
-    const uintptr_t y1 = y0 + (uintptr_t)((batch - 1) * ld_y + out_dim) * 4u;
+    const uintptr_t y1 = y0 + (uintptr_t)((batch - 1) * ld_y + out_dim) * (uintptr_t)y_bytes;
     const uintptr_t x1 = x0 + (uintptr_t)((batch - 1) * ld_x + in_dim) * (uintptr_t)x_bytes;
     return x0 < y1 && y0 < x1;
 }
@@ -446,7 +453,7 @@ bool dot_ok(const float* x, const uint16_t* w16, long batch, int in_dim, long ld
 // ---- MFMA launch shapes -----------------------------------------------------
 template <bool XH, int NB, int RT, int R, bool NORM = false, int EPI = kStore, int NW = 4>
 void launch_mfma(const ProjArgs& a, hipStream_t st) {
-    const int rows = 16 * (EPI == kSwiGLU ? 1 : RT);
+    const int rows = 16 * (is_swiglu(EPI) ? 1 : RT);
     const dim3 grid((unsigned)((a.out_dim + rows - 1) / rows), (unsigned)((a.batch + 16 * NB - 1) / (16 * NB)));
     proj_mfma_kernel<XH, NB, RT, R, NORM, EPI, NW><<<grid, dim3(64 * NW), 0, st>>>(a);
 }
@@ -505,7 +512,7 @@ extern "C" int anelm_proj_f16(float* y, const float* x, const uint16_t* w16, lon
     clear_error();
     if (!y || !x || !w16) return fail(ANELM_ERR_INVALID, "proj_f16: null pointer");
     if (!sizes_ok(batch, out_dim, in_dim, ld_x, ld_y)) return fail(ANELM_ERR_INVALID, "proj_f16: bad sizes or strides");
-    if (overlaps(y, ld_y, out_dim, x, ld_x, in_dim, 4, batch))
+    if (overlaps(y, ld_y, out_dim, 4, x, ld_x, in_dim, 4, batch))
         return fail(ANELM_ERR_INVALID, "proj_f16: y overlaps x (y is written while x is still read)");
     hipStream_t st = as_stream(stream);
     const ProjArgs a = args(y, x, w16, batch, out_dim, in_dim, ld_x, ld_y);
@@ -527,12 +534,61 @@ extern "C" int anelm_proj_f16_x16(float* y, const uint16_t* x16, const uint16_t*
     if (!y || !x16 || !w16) return fail(ANELM_ERR_INVALID, "proj_f16_x16: null pointer");
     if (!sizes_ok(batch, out_dim, in_dim, ld_x, ld_y))
         return fail(ANELM_ERR_INVALID, "proj_f16_x16: bad sizes or strides");
-    if (overlaps(y, ld_y, out_dim, x16, ld_x, in_dim, 2, batch))
+    if (overlaps(y, ld_y, out_dim, 4, x16, ld_x, in_dim, 2, batch))
         return fail(ANELM_ERR_INVALID, "proj_f16_x16: y overlaps x (y is written while x is still read)");
     if (!mfma_ok(x16, true, w16, in_dim, ld_x))
         return fail(ANELM_ERR_INVALID,
                     "proj_f16_x16: needs in_dim a multiple of 32, ld_x a multiple of 8, 16-byte aligned x and W");
     return proj_mfma<true>(args(y, x16, w16, batch, out_dim, in_dim, ld_x, ld_y), as_stream(stream));
+}
+
+// fp32 inputs with the fused RMSNorm and epilogues: one 16-row batch block
+// per workgroup up to 16 rows, and past that wherever there are few output
+// tiles; otherwise 32-row batch blocks and two row tiles per workgroup.
+template <bool NORM, int EPI>
+void f32_fused(const ProjArgs& a, hipStream_t st) {
+    const long tiles16 = (long)((a.out_dim + 15) / 16) * ((a.batch + 15) / 16);
+    constexpr int RT = is_swiglu(EPI) ? 2 : 1;
+    if (a.batch <= 16 || (!is_swiglu(EPI) && tiles16 < 512)) launch_mfma<false, 1, RT, 8, NORM, EPI>(a, st);
+    else launch_mfma<false, 2, 2, 4, NORM, EPI>(a, st);
+}
+
+// The fused epilogues on fp16 inputs (x16 from anelm_rmsnorm_f16 or a
+// previous fp16 SwiGLU): the decode step past a few rows, where the fp32
+// inputs' extra bytes and per-workgroup rounding cost more than the
+// separate conversion.
+template <int EPI>
+void x16_fused(const ProjArgs& a, hipStream_t st) {
+    const long tiles16 = (long)((a.out_dim + 15) / 16) * ((a.batch + 15) / 16);
+    constexpr int RT = is_swiglu(EPI) ? 2 : 1;
+    if (a.batch <= 16 || (!is_swiglu(EPI) && tiles16 < 512)) launch_mfma<true, 1, RT, 8, false, EPI>(a, st);
+    else launch_mfma<true, 2, 2, 8, false, EPI>(a, st);
+}
+
+extern "C" int anelm_proj_f16_x16_fused(void* y, const uint16_t* x16, const uint16_t* w16, long batch, int out_dim,
+                                        int in_dim, long ld_x, long ld_y, int epilogue, void* stream) {
+    clear_error();
+    if (!y || !x16 || !w16) return fail(ANELM_ERR_INVALID, "proj_f16_x16_fused: null pointer");
+    if (!sizes_ok(batch, out_dim, in_dim, ld_x, ld_y))
+        return fail(ANELM_ERR_INVALID, "proj_f16_x16_fused: bad sizes or strides");
+    if (!mfma_ok(x16, true, w16, in_dim, ld_x))
+        return fail(ANELM_ERR_INVALID,
+                    "proj_f16_x16_fused: needs in_dim a multiple of 32, ld_x a multiple of 8, 16-byte aligned x and W");
+    if (epilogue < ANELM_PROJ_STORE || epilogue > ANELM_PROJ_SWIGLU_F16)
+        return fail(ANELM_ERR_INVALID, "proj_f16_x16_fused: unknown epilogue %d", epilogue);
+    if (overlaps(y, ld_y, out_dim, epilogue == ANELM_PROJ_SWIGLU_F16 ? 2 : 4, x16, ld_x, in_dim, 2, batch))
+        return fail(ANELM_ERR_INVALID, "proj_f16_x16_fused: y overlaps x (y is written while x is still read)");
+    ProjArgs a = args(static_cast<float*>(y), x16, w16, batch, out_dim, in_dim, ld_x, ld_y);
+    a.y16 = static_cast<uint16_t*>(y);
+    a.pair_rows = out_dim;
+    hipStream_t st = as_stream(stream);
+    switch (epilogue) {
+        case ANELM_PROJ_STORE: x16_fused<kStore>(a, st); break;
+        case ANELM_PROJ_ADD: x16_fused<kAdd>(a, st); break;
+        case ANELM_PROJ_SWIGLU: x16_fused<kSwiGLU>(a, st); break;
+        default: x16_fused<kSwiGLU16>(a, st); break;
+    }
+    return launch_status("proj_f16_x16_fused");
 }
 
 // Decode-step projections with the neighbouring layer ops fused in, for up
@@ -543,14 +599,14 @@ extern "C" int anelm_proj_f16_fused(float* y, const float* x, const uint16_t* w1
                                     int epilogue, void* stream) {
     clear_error();
     if (!y || !x || !w16) return fail(ANELM_ERR_INVALID, "proj_f16_fused: null pointer");
-    if (batch > 16 || !sizes_ok(batch, out_dim, in_dim, ld_x, ld_y))
-        return fail(ANELM_ERR_INVALID, "proj_f16_fused: batch 1..16, sizes and strides");
+    if (!sizes_ok(batch, out_dim, in_dim, ld_x, ld_y))
+        return fail(ANELM_ERR_INVALID, "proj_f16_fused: bad sizes or strides");
     if (!mfma_ok(x, false, w16, in_dim, ld_x) || (norm_bf16 && !aligned16(norm_bf16)))
         return fail(ANELM_ERR_INVALID,
                     "proj_f16_fused: needs in_dim a multiple of 32, ld_x a multiple of 4, 16-byte aligned x, W, gamma");
     if (epilogue < ANELM_PROJ_STORE || epilogue > ANELM_PROJ_SWIGLU)
         return fail(ANELM_ERR_INVALID, "proj_f16_fused: unknown epilogue %d", epilogue);
-    if (overlaps(y, ld_y, out_dim, x, ld_x, in_dim, 4, batch))
+    if (overlaps(y, ld_y, out_dim, 4, x, ld_x, in_dim, 4, batch))
         return fail(ANELM_ERR_INVALID,
                     "proj_f16_fused: y overlaps x (y is written while x is still read; the residual add takes the "
                     "residual stream as y and the projection input as a separate x)");
@@ -579,16 +635,16 @@ extern "C" int anelm_proj_f16_fused(float* y, const float* x, const uint16_t* w1
     }
     switch (epilogue) {
         case ANELM_PROJ_STORE:
-            if (norm) launch_mfma<false, 1, 1, 8, true, kStore>(a, st);
-            else launch_mfma<false, 1, 1, 8, false, kStore>(a, st);
+            if (norm) f32_fused<true, kStore>(a, st);
+            else f32_fused<false, kStore>(a, st);
             break;
         case ANELM_PROJ_ADD:
-            if (norm) launch_mfma<false, 1, 1, 8, true, kAdd>(a, st);
-            else launch_mfma<false, 1, 1, 8, false, kAdd>(a, st);
+            if (norm) f32_fused<true, kAdd>(a, st);
+            else f32_fused<false, kAdd>(a, st);
             break;
         default:
-            if (norm) launch_mfma<false, 1, 2, 8, true, kSwiGLU>(a, st);
-            else launch_mfma<false, 1, 2, 8, false, kSwiGLU>(a, st);
+            if (norm) f32_fused<true, kSwiGLU>(a, st);
+            else f32_fused<false, kSwiGLU>(a, st);
             break;
     }
     return launch_status("proj_f16_fused");

@@ -7,8 +7,10 @@
 // ANE's interface numerics are kept: weights are the truncating fp16 convert
 // of the bf16 checkpoint (the blobs), activations enter a projection as
 // round-to-nearest fp16 and leave it as fp16 (core/ane_runtime.cpp:600-640).
-// Up to 16 sequences, the RMSNorms, residual adds and the SwiGLU are fused
-// into the projections: 7 launches per layer instead of 13.
+// The RMSNorms, residual adds and the SwiGLU are fused into the
+// projections: up to 16 sequences as the projections' own prologue and
+// epilogues (7 launches per layer instead of 13), past that with the norms
+// writing the projections' fp16 inputs (8 launches).
 //
 // A step processes one token of each of `batch` sequences; every sequence
 // has its own KV ring per layer (qwen3.cpp:227-231, 475-488).
@@ -27,8 +29,6 @@
 using anelm::fail;
 using anelm::clear_error;
 
-extern "C" int anelm_proj_f16(float* y, const float* x, const uint16_t* w16, long batch, int out_dim, int in_dim,
-                              long ld_x, long ld_y, void* stream);
 
 struct anelm_blas {
     rocblas_handle h = nullptr;
@@ -316,8 +316,45 @@ extern "C" int anelm_qwen3_forward(anelm_qwen3* m, const int32_t* ids, const int
         return ANELM_OK;
     };
     CK(anelm_embed_gather(m->x, m->embed, ANELM_BF16, ids, B, H, V, bad_ids, stream));             // :498
-    const bool fused = B <= 16 && H % 32 == 0 && I % 32 == 0 && m->qdim % 32 == 0;
-    if (fused) {
+    const bool dims32 = H % 32 == 0 && I % 32 == 0 && m->qdim % 32 == 0;
+    if (dims32 && B > 16) {
+        // Past 16 rows the RMSNorms round their output to fp16 once
+        // (anelm_rmsnorm_f16) and the projections read fp16 rows; the SwiGLU
+        // writes the down projection's fp16 input and the residual adds ride
+        // in the o and down projections: 8 launches per layer
+        for (int L = 0; L < c.layers; L++) {
+            const anelm_qwen3::Layer& l = m->layers[L];
+            CK(anelm_rmsnorm_f16(m->a16, m->x, l.w_in, ANELM_BF16, B, (int)H, H, H, c.rms_eps, stream));  // :503
+            CK(anelm_proj_f16_x16_fused(m->qkv, m->a16, l.qkv16, B, m->qkvdim, (int)H, H, m->qkvdim,
+                                        ANELM_PROJ_STORE, stream));                               // first_proj
+            CK(anelm_qknorm_rope(m->qkv, m->qkv + m->qdim, m->qkvdim, m->qkvdim, l.qn, l.kn, ANELM_BF16, pos,
+                                 m->cos_tab, m->sin_tab, kRopeRows, c.rope_theta, B, c.n_q_heads, c.n_kv_heads, D,
+                                 c.rms_eps, stream));                                             // :444-472
+            CK(anelm_kv_ring_append(l.kc, l.vc, l.start, l.len, m->qkv + m->qdim, m->qkv + m->qdim + m->kvdim,
+                                    m->qkvdim, m->qkvdim, B, c.n_kv_heads, D, m->cap, seq, stream));  // :475-488
+            CK(anelm_gqa_attention(m->attn, m->qkv, l.kc, l.vc, l.start, l.len, B, c.n_q_heads, c.n_kv_heads, D,
+                                   m->qkvdim, D, m->qdim, m->cap, seq, m->attn_ws, m->attn_ws_bytes, stream));  // :490
+            CK(anelm_proj_f16_fused(m->x, m->attn, l.o16, B, (int)H, m->qdim, m->qdim, H, nullptr, 0.0f,
+                                    ANELM_PROJ_ADD, stream));                                     // o_proj + :516
+            CK(anelm_rmsnorm_f16(m->a16, m->x, l.w_post, ANELM_BF16, B, (int)H, H, H, c.rms_eps, stream));  // :518
+            CK(anelm_proj_f16_x16_fused(m->y16, m->a16, l.gu16, B, (int)I, (int)H, H, I, ANELM_PROJ_SWIGLU_F16,
+                                        stream));                                                 // fused_ffn
+            CK(anelm_proj_f16_x16_fused(m->x, m->y16, l.down16, B, (int)H, (int)I, I, H, ANELM_PROJ_ADD,
+                                        stream));                                                 // down + :527
+        }
+        CK(anelm_rmsnorm_f16(m->a16, m->x, m->final_norm, ANELM_BF16, B, (int)H, H, H, c.rms_eps, stream));  // :530
+        if (V <= 65536)
+            return anelm_proj_f16_x16_fused(logits, m->a16, m->lm16, B, (int)V, (int)H, H, ld_logits, ANELM_PROJ_STORE,
+                                            stream);
+        // rocBLAS keeps the LM head: with 151936 outputs its tiles reuse each
+        // input row better (80 us against 140 us at 64 rows)
+        CK(anelm_linear_f16(m->blas, m->y16, m->a16, m->lm16, B, (int)V, (int)H, H, V, stream));
+        if (ld_logits == V) return anelm_f16_to_f32(logits, m->y16, (size_t)(B * V), stream);
+        for (long b = 0; b < B; b++)   // strided destination (the caller's logits rows)
+            CK(anelm_f16_to_f32(logits + b * ld_logits, m->y16 + b * V, (size_t)V, stream));
+        return ANELM_OK;
+    }
+    if (dims32) {
         // 7 launches per layer: the RMSNorms, residual adds and the SwiGLU
         // ride in the projections (anelm_proj_f16_fused)
         for (int L = 0; L < c.layers; L++) {

@@ -68,6 +68,15 @@ int anelm_version(void);
 int anelm_rmsnorm(float* out, const float* x, const void* w, int w_dtype, long rows, int dim,
                   long ld_x, long ld_out, float eps, void* stream);
 
+/* anelm_rmsnorm with the result rounded to fp16 (nearest even), the ANE
+ * kernels' input conversion (core/ane_runtime.cpp:604-612) fused into the
+ * norm: out16 = fp16(rmsnorm(x) * w), the same fp32 values as anelm_rmsnorm
+ * (bit-identical to it followed by anelm_f32_to_f16 wherever both take the
+ * vector path: dim a multiple of 4, 16-byte aligned rows).  The input of a projection that takes fp16 rows
+ * (anelm_proj_f16_x16, anelm_proj_f16_x16_fused); out16 must not overlap x.
+ * No counterpart in the reference. */
+int anelm_rmsnorm_f16(uint16_t* out16, const float* x, const void* w, int w_dtype, long rows, int dim, long ld_x,
+                      long ld_out, float eps, void* stream);
 /* Fused residual add + RMSNorm:  x[r,:] += y[r,:];  out[r,:] = rmsnorm(x[r,:]).
  * Replaces the pair vDSP_vadd(x_, attn_out, x_) + rmsnorm(x_norm_, x_, ...)
  * of models/llm/qwen3.cpp:516-518.  y may equal out (the reference's
@@ -373,9 +382,11 @@ int anelm_proj_f16(float* y, const float* x, const uint16_t* w16, long batch, in
 int anelm_proj_f16_x16(float* y, const uint16_t* x16, const uint16_t* w16, long batch, int out_dim, int in_dim,
                        long ld_x, long ld_y, void* stream);
 
-/* Decode-step projections (batch <= 16, fp32 x, in_dim a multiple of 32)
- * with the neighbouring layer ops of models/llm/qwen3.cpp:497-530 fused in,
- * so a layer is 7 launches instead of 13.  With p the rounded projection of
+/* Decode-step projections (fp32 x, in_dim a multiple of 32) with the
+ * neighbouring layer ops of models/llm/qwen3.cpp:497-530 fused in, so a
+ * layer is 7 launches instead of 13.  Any batch; past 16 rows
+ * anelm_rmsnorm_f16 with anelm_proj_f16_x16_fused is faster where a norm
+ * precedes the projection.  With p the rounded projection of
  * anelm_proj_f16:
  *   norm_bf16 != NULL: x is first replaced by rmsnorm(x) * norm_bf16
  *     (core/cpu_ops.cpp:25-31 with eps; norm_bf16 [in_dim], 16-byte aligned);
@@ -392,6 +403,17 @@ int anelm_proj_f16_x16(float* y, const uint16_t* x16, const uint16_t* w16, long 
 #define ANELM_PROJ_SWIGLU 2
 int anelm_proj_f16_fused(float* y, const float* x, const uint16_t* w16, long batch, int out_dim, int in_dim,
                          long ld_x, long ld_y, const uint16_t* norm_bf16, float eps, int epilogue, void* stream);
+/* The epilogues of anelm_proj_f16_fused on inputs already rounded to fp16
+ * (x16 [batch, in_dim], row stride ld_x a multiple of 8: anelm_rmsnorm_f16's
+ * output, or a previous ANELM_PROJ_SWIGLU_F16), any batch: the decode step
+ * past a few sequences, where one conversion of x beats one per workgroup.
+ * y is fp32 (STORE, ADD, SWIGLU) or, with ANELM_PROJ_SWIGLU_F16, fp16: the
+ * SwiGLU result rounded to nearest even, i.e. the down projection's input;
+ * ld_y counts y's elements; y must not overlap x16.  in_dim a multiple of 32.
+ * No counterpart in the reference (see anelm_proj_f16_fused). */
+#define ANELM_PROJ_SWIGLU_F16 3
+int anelm_proj_f16_x16_fused(void* y, const uint16_t* x16, const uint16_t* w16, long batch, int out_dim,
+                             int in_dim, long ld_x, long ld_y, int epilogue, void* stream);
 
 /* Qwen3 model shape (the config.json fields of models/llm/qwen3.cpp:55-80). */
 typedef struct anelm_qwen3_config {

@@ -174,7 +174,7 @@ def test_projection_argument_checks(lib):
     assert f(fake, odd, fake, 2, 64, 40, 40, 64, None) == -1                    # unaligned x, row path
     assert x16(fake, fake, fake, 4, 64, 48, 48, 64, None) == -1                 # in_dim not a multiple of 32
     assert x16(fake, fake, fake, 4, 64, 64, 68, 64, None) == -1                 # fp16 row stride not 16 bytes
-    assert fu(fake, fake, fake, 17, 64, 64, 64, 64, None, 1e-6, 0, None) == -1  # batch > 16
+    assert fu(fake, fake, fake, 17, 64, 64, 64, 60, None, 1e-6, 0, None) == -1  # ld_y < out_dim
     assert fu(fake, fake, fake, 1, 64, 64, 64, 64, None, 1e-6, 3, None) == -1   # no such epilogue
     assert fu(fake, fake, fake, 1, 64, 64, 64, 64, odd, 1e-6, 0, None) == -1    # unaligned gamma
     assert fu(fake, fake, fake, 1, 64, 64, 64, 64, None, 1e-6, 1, None) == -1   # residual add onto its own input
@@ -182,6 +182,12 @@ def test_projection_argument_checks(lib):
     assert f(fake, P(0x10F0), fake, 1, 64, 64, 64, 64, None) == -1             # x starts inside y (64 floats at 0x1000)
     assert b"overlaps" in lib.anelm_last_error()
     assert x16(P(0x1040), fake, fake, 1, 64, 64, 64, 64, None) == -1           # y starts inside the fp16 x
+    xf = lib.anelm_proj_f16_x16_fused
+    assert xf(fake, fake, fake, 1, 64, 64, 64, 64, 4, None) == -1              # no such epilogue
+    assert xf(fake, fake, fake, 1, 64, 48, 48, 64, 0, None) == -1              # in_dim not a multiple of 32
+    assert xf(P(0x1040), fake, fake, 1, 64, 64, 64, 64, 3, None) == -1         # fp16 y inside x16
+    assert xf(P(0x0F90), fake, fake, 1, 64, 64, 64, 64, 0, None) == -1         # fp32 y runs into x16
+    assert lib.anelm_rmsnorm_f16(P(0x10C0), fake, fake, 2, 1, 64, 64, 64, 1e-6, None) == -1  # out16 inside x
     b = lib.anelm_gqa_attention_bounded
     assert b(fake, fake, fake, fake, fake, fake, 1, 32, 8, 128, 4096, 128, 4096, 2048, 2048 * 1024, 0, fake,
              1 << 30, None) == -1                                               # bound 0

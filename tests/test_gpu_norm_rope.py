@@ -38,6 +38,30 @@ def test_rmsnorm(hip, orc, rng, rows, dim, dt):
     assert max_rel_err(host(out), orc.rmsnorm_rows(x, w32, EPS)) <= REL_TOL
 
 
+@pytest.mark.parametrize("rows,dim", [(1, 1024), (64, 1024), (64, 2560), (3, 1000), (5, 7), (2, 8192)])
+@pytest.mark.parametrize("dt", ["f16", "bf16"])
+def test_rmsnorm_f16_output(hip, orc, rng, rows, dim, dt):
+    """The fp16-output RMSNorm: bit-identical to the fp32 RMSNorm followed by
+    the RNE narrowing (same kernel layout, dim a multiple of 4) and within one
+    fp16 ulp (plus the norm's tolerance) of the oracle's RMSNorm rounded."""
+    import torch
+
+    x = (3 * rng.standard_normal((rows, dim))).astype(np.float32)
+    wt, w32 = _gamma(rng, dim, dt)
+    out16 = torch.empty(rows, dim, dtype=torch.int16, device="cuda")
+    hip.rmsnorm_f16(out16, dev(x), wt, EPS)
+    got = host(out16).view(np.float16).astype(np.float64)
+    if dim % 4 == 0:
+        ref32 = torch.empty(rows, dim, device="cuda")
+        hip.rmsnorm(ref32, dev(x), wt, EPS)
+        ref16 = torch.empty(rows, dim, dtype=torch.int16, device="cuda")
+        hip.f32_to_f16(ref16, ref32)
+        assert_bitexact(host(out16), host(ref16), "rmsnorm_f16 vs rmsnorm + narrow")
+    want = orc.rmsnorm_rows(x, w32, EPS).astype(np.float64)
+    ulp = np.spacing(np.abs(want).astype(np.float16)).astype(np.float64)
+    assert np.all(np.abs(got - want) <= ulp + np.abs(want) * REL_TOL)
+
+
 def test_rmsnorm_in_place_and_strided(hip, orc, rng):
     import torch
 

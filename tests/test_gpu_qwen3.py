@@ -102,6 +102,66 @@ def test_proj_f16_x16_inputs(hip, orc, rng, B, out_dim, in_dim):
         check_projection(orc, x, w, host(y).astype(np.float64))
 
 
+@pytest.mark.parametrize("B,out_dim,in_dim", [(17, 4096, 1024), (64, 1024, 2048), (40, 3072, 1024), (64, 1000, 96)])
+@pytest.mark.parametrize("norm", [False, True])
+def test_proj_f16_fused_past_16_rows(hip, orc, rng, B, out_dim, in_dim, norm):
+    """The fp32-input fused projection past 16 rows (two batch blocks per
+    workgroup with the norm prologue over 32 rows), store and residual add."""
+    import torch
+
+    x = (2 * rng.standard_normal((B, in_dim))).astype(np.float32)
+    gamma = bf16(1 + 0.1 * rng.standard_normal(in_dim))
+    w = (0.03 * rng.standard_normal((out_dim, in_dim))).astype(np.float16).view(np.uint16)
+    y = torch.full((B, out_dim), float("nan"), device="cuda")
+    g = dev(gamma.view(np.int16)) if norm else None
+    hip.proj_f16_fused(y, dev(x), dev(w), norm=g, eps=1e-6)
+    xn = np.stack([orc.rmsnorm(x[b], from_bf16(gamma), 1e-6) for b in range(B)]) if norm else x
+    check_projection(orc, xn, w, host(y).astype(np.float64))
+    r0 = rng.standard_normal((B, out_dim)).astype(np.float32)
+    y = dev(r0)
+    hip.proj_f16_fused(y, dev(x), dev(w), norm=g, eps=1e-6, epilogue=hip.PROJ_ADD)
+    ref, mag = _proj_ref(orc, xn, w)
+    want = r0.astype(np.float64) + ref
+    tol = _ulp16(ref) + mag * 2.0 ** -21 * 4 + np.spacing(np.abs(want).astype(np.float32))
+    assert np.all(np.abs(host(y).astype(np.float64) - want) <= tol)
+
+
+@pytest.mark.parametrize("B,out_dim,in_dim", [(17, 4096, 1024), (64, 1024, 3072), (3, 1024, 2048), (64, 160, 64)])
+def test_proj_f16_x16_fused_epilogues(hip, orc, rng, B, out_dim, in_dim):
+    """fp16 rows in (the fp16 RMSNorm's output), each epilogue: store and
+    residual add against the oracle, the SwiGLU in fp32 and rounded to fp16
+    (the down projection's input), the latter bit-identical to the fp32
+    SwiGLU narrowed."""
+    import torch
+
+    x = (2 * rng.standard_normal((B, in_dim))).astype(np.float32)
+    x16 = dev(orc.f32_to_f16_rne(x).reshape(B, in_dim).view(np.int16))
+    w = (0.03 * rng.standard_normal((out_dim, in_dim))).astype(np.float16).view(np.uint16)
+    y = torch.full((B, out_dim), float("nan"), device="cuda")
+    hip.proj_f16_x16_fused(y, x16, dev(w))
+    check_projection(orc, x, w, host(y).astype(np.float64))
+    r0 = rng.standard_normal((B, out_dim)).astype(np.float32)
+    y = dev(r0)
+    hip.proj_f16_x16_fused(y, x16, dev(w), epilogue=hip.PROJ_ADD)
+    ref, mag = _proj_ref(orc, x, w)
+    want = r0.astype(np.float64) + ref
+    tol = _ulp16(ref) + mag * 2.0 ** -21 * 4 + np.spacing(np.abs(want).astype(np.float32))
+    assert np.all(np.abs(host(y).astype(np.float64) - want) <= tol)
+    inter = out_dim // 2
+    h = torch.full((B, inter), float("nan"), device="cuda")
+    hip.proj_f16_x16_fused(h, x16, dev(w[:2 * inter]), epilogue=hip.PROJ_SWIGLU)
+    gu, mg = ref[:, :2 * inter], mag[:, :2 * inter]
+    g, u, m_g, m_u = gu[:, :inter], gu[:, inter:], mg[:, :inter], mg[:, inter:]
+    want = g / (1 + np.exp(-g)) * u
+    eg = _ulp16(g) + m_g * 2.0 ** -21 * 4
+    eu = _ulp16(u) + m_u * 2.0 ** -21 * 4
+    tol = 1.1 * eg * np.abs(u) + np.abs(g / (1 + np.exp(-g))) * eu + eg * eu + np.abs(want) * 1e-6 + 1e-30
+    assert np.all(np.abs(host(h).astype(np.float64) - want) <= tol)
+    h16 = torch.empty(B, inter, dtype=torch.int16, device="cuda")
+    hip.proj_f16_x16_fused(h16, x16, dev(w[:2 * inter]), epilogue=hip.PROJ_SWIGLU_F16)
+    assert_bitexact(host(h16), orc.f32_to_f16_rne(host(h)).reshape(B, inter), "fp16 SwiGLU vs fp32 SwiGLU rounded")
+
+
 def _proj_ref(orc, x, w):
     """The oracle's rounded projection (float64 of fp16 values) and the term
     magnitudes sum |x16| |w| that bound an fp32 accumulation's error."""
@@ -174,7 +234,7 @@ def test_proj_fused_swiglu(hip, orc, rng, B, inter, in_dim, norm):
     assert np.all(np.abs(host(h).astype(np.float64) - want) <= tol)
 
 
-@pytest.mark.parametrize("tied,B", [(True, 3), (False, 3), (True, 11), (True, 1)])
+@pytest.mark.parametrize("tied,B", [(True, 3), (False, 3), (True, 11), (True, 1), (True, 20), (False, 33)])
 def test_decode_steps_match_oracle(hip, orc, rng, tmp_path, tied, B):
     import torch
 
@@ -187,7 +247,7 @@ def test_decode_steps_match_oracle(hip, orc, rng, tmp_path, tied, B):
     model = hip.Qwen3Model(path, cfg, max_batch=B, kv_capacity=cap)
     ref = orc.Qwen3(ocfg, t, B, cap)
     logits = torch.empty(B, d["V"], device="cuda")
-    pos0 = np.array([0, 100, 20000] * 4)[:B]    # every third sequence uses the RoPE fallback
+    pos0 = np.resize(np.array([0, 100, 20000]), B)    # every third sequence uses the RoPE fallback
     worst = 0.0
     for s in range(steps):
         ids = rng.integers(0, d["V"], B).astype(np.int32)
