@@ -53,6 +53,8 @@ _SIGS = {
     "anelm_rmsnorm_f16": (_I, [_P, _P, _P, _I, _L, _I, _L, _L, _F, _P]),
     "anelm_add_rmsnorm": (_I, [_P, _P, _P, _P, _I, _L, _I, _L, _L, _L, _F, _P]),
     "anelm_qknorm_rope": (_I, [_P, _P, _L, _L, _P, _P, _I, _P, _P, _P, _I, _F, _L, _I, _I, _I, _F, _P]),
+    "anelm_qknorm_rope_append": (_I, [_P, _P, _P, _L, _L, _L, _P, _P, _I, _P, _P, _P, _I, _F, _L, _I, _I, _F, _P, _P,
+                                      _P, _P, _I, _L, _P]),
     "anelm_rope_cached": (_I, [_P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _P, _P, _P]),
     "anelm_rope_table": (_I, [_P, _P, _I, _I, _F, _P]),
     "anelm_residual_add": (_I, [_P, _P, _S, _P]),
@@ -207,6 +209,23 @@ def qknorm_rope(q, k, wq, wk, pos, cos_tab, sin_tab, theta=1e6, eps=1e-6, nq=Non
     tab_len = cos_tab.shape[0] if cos_tab is not None else 0
     _check(lib().anelm_qknorm_rope(_ptr(q), _ptr(k), q_ld, k_ld, _ptr(wq), _ptr(wk), wdt, _ptr(pos), _ptr(cos_tab),
                                    _ptr(sin_tab), tab_len, theta, T, nq, nk, head_dim, eps, _stream(stream)))
+
+
+def qknorm_rope_append(q, k, v, wq, wk, pos, cos_tab, sin_tab, k_cache, v_cache, ring_start, ring_len, theta=1e6,
+                       eps=1e-6, nq=None, nk=None, stream=None):
+    """Decode step: q/k norm + RoPE of token b (pos[b]) in place, then k and v
+    appended to ring b; head_dim 128; caches [B, capacity, nk*128]."""
+    B = pos.shape[0]
+    nq = q.shape[1] // 128 if nq is None else nq
+    nk = k.shape[1] // 128 if nk is None else nk
+    _, cap, row = k_cache.shape
+    _need(row == nk * 128 and k_cache.stride() == v_cache.stride(), "qknorm_rope_append: cache shapes")
+    wdt = _dtype_code(wq if wq is not None else (wk if wk is not None else q))
+    tab_len = cos_tab.shape[0] if cos_tab is not None else 0
+    _check(lib().anelm_qknorm_rope_append(_ptr(q), _ptr(k), _ptr(v), _ld(q), _ld(k), _ld(v), _ptr(wq), _ptr(wk), wdt,
+                                          _ptr(pos), _ptr(cos_tab), _ptr(sin_tab), tab_len, theta, B, nq, nk, eps,
+                                          _ptr(k_cache), _ptr(v_cache), _ptr(ring_start), _ptr(ring_len), cap,
+                                          k_cache.stride(0), _stream(stream)))
 
 
 def rope_cached(q, k, n_q_heads, n_kv_heads, head_dim, q_head_stride, k_head_stride, rot_dim, pos, theta,

@@ -151,6 +151,31 @@ __device__ __forceinline__ float silu_ref(float g) {
     return g / t;
 }
 
+// One KV ring step for a sequence's state (start, len), models/llm/qwen3.cpp
+// :475-488, with the state clamped into range first (0 <= len <= cap, start
+// mod cap): while len < cap the row goes to slot start+len (mod cap) and len
+// grows, afterwards it overwrites slot start and start advances.  Returns the
+// slot and stores the advanced state.
+__device__ __forceinline__ int ring_advance(int32_t* rs, int32_t* rl, int cap) {
+    int s = *rs, l = *rl;
+    l = l < 0 ? 0 : (l > cap ? cap : l);
+    s %= cap;
+    if (s < 0) s += cap;
+    int slot;
+    if (l < cap) {
+        slot = s + l;
+        if (slot >= cap) slot -= cap;
+        l++;
+    } else {
+        slot = s;
+        s++;
+        if (s >= cap) s = 0;
+    }
+    *rs = s;
+    *rl = l;
+    return slot;
+}
+
 // fp32 -> fp16 rounded to nearest even, of the value as already rounded to
 // fp32.  Without the empty asm the compiler folds a preceding multiply or
 // add into v_fma_mixlo_f16, which rounds the exact result once, straight to

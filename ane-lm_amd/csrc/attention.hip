@@ -344,25 +344,7 @@ __global__ __launch_bounds__(256) void kv_append_kernel(float* kc, float* vc, in
                                                         int row, int cap, long seq_stride, int vec) {
     __shared__ int s_slot;
     const long b = blockIdx.x;
-    if (threadIdx.x == 0) {
-        int s = rs[b], l = rl[b];
-        l = l < 0 ? 0 : (l > cap ? cap : l);
-        s %= cap;
-        if (s < 0) s += cap;
-        int slot;
-        if (l < cap) {                   // qwen3.cpp:476-479
-            slot = s + l;
-            if (slot >= cap) slot -= cap;
-            l++;
-        } else {                         // qwen3.cpp:480-484
-            slot = s;
-            s++;
-            if (s >= cap) s = 0;
-        }
-        s_slot = slot;
-        rs[b] = s;
-        rl[b] = l;
-    }
+    if (threadIdx.x == 0) s_slot = ring_advance(rs + b, rl + b, cap);   // qwen3.cpp:475-484
     __syncthreads();
     float* kd = kc + b * seq_stride + (long)s_slot * row;
     float* vd = vc + b * seq_stride + (long)s_slot * row;

@@ -4,6 +4,7 @@
 // All of these are HBM-bound (< 1 flop/byte): every activation is read
 // from HBM once and written once, with 16-byte accesses, and reductions are
 // wave shuffles plus at most one LDS exchange of per-wave partials.
+#include <algorithm>
 #include <cmath>
 
 #include "anelm_common.hpp"
@@ -193,6 +194,64 @@ static int launch_rmsnorm(void* out, float* x, const float* y, const void* w, in
 // of the grid covers consecutive heads; all loads of the HPG heads (heads,
 // then positions, then the table rows that depend on them) are issued before
 // the first is used, which matters when a launch is only a few rounds deep.
+// cos/sin of the rotation angles j0 .. j0+3 at position p: table row p when
+// 0 <= p < tab_len (qwen3.cpp:463-469), else the fallback angle
+// p * inv_freq[j] (qwen3.cpp:39-49).
+__device__ __forceinline__ void rope_cs4(int p, int j0, const float* cos_tab, const float* sin_tab, int tab_len,
+                                         const InvFreq& inv, float4& c, float4& s) {
+    if (p >= 0 && p < tab_len) {
+        c = *reinterpret_cast<const float4*>(cos_tab + (long)p * 64 + j0);
+        s = *reinterpret_cast<const float4*>(sin_tab + (long)p * 64 + j0);
+    } else {
+        const float pf = (float)p;
+        const float a0 = pf * inv.v[j0], a1 = pf * inv.v[j0 + 1];
+        const float a2 = pf * inv.v[j0 + 2], a3 = pf * inv.v[j0 + 3];
+        c = make_float4(cosf(a0), cosf(a1), cosf(a2), cosf(a3));
+        s = make_float4(sinf(a0), sinf(a1), sinf(a2), sinf(a3));
+    }
+}
+
+// One 128-wide head held by an aligned group of 16 lanes, lane l holding
+// elements j0 = 4*(l%16) .. j0+3 in `l` and j0+64 .. j0+67 in `h`: the
+// RMSNorm with gamma w (skipped when w is null), then the half-split
+// rotation; returns the rotated halves in ol / oh.  Every lane of the group
+// calls it (the sum of squares is a group reduction).
+template <int DT>
+__device__ __forceinline__ void norm_rope128(float4 l, float4 h, const void* w, float4 c, float4 s, int j0,
+                                             float eps, float4& ol, float4& oh) {
+    float ss = 0.f;
+    ss = fmaf(l.x, l.x, ss);
+    ss = fmaf(l.y, l.y, ss);
+    ss = fmaf(l.z, l.z, ss);
+    ss = fmaf(l.w, l.w, ss);
+    ss = fmaf(h.x, h.x, ss);
+    ss = fmaf(h.y, h.y, ss);
+    ss = fmaf(h.z, h.z, ss);
+    ss = fmaf(h.w, h.w, ss);
+    ss = group16_sum(ss);
+    if (w) {
+        const float sc = 1.0f / sqrtf(ss / 128.0f + eps);
+        const float4 wl = load_w4<DT>(w, j0);
+        const float4 wh = load_w4<DT>(w, j0 + 64);
+        l.x = (l.x * sc) * wl.x;
+        l.y = (l.y * sc) * wl.y;
+        l.z = (l.z * sc) * wl.z;
+        l.w = (l.w * sc) * wl.w;
+        h.x = (h.x * sc) * wh.x;
+        h.y = (h.y * sc) * wh.y;
+        h.z = (h.z * sc) * wh.z;
+        h.w = (h.w * sc) * wh.w;
+    }
+    ol.x = l.x * c.x - h.x * s.x;
+    ol.y = l.y * c.y - h.y * s.y;
+    ol.z = l.z * c.z - h.z * s.z;
+    ol.w = l.w * c.w - h.w * s.w;
+    oh.x = h.x * c.x + l.x * s.x;
+    oh.y = h.y * c.y + l.y * s.y;
+    oh.z = h.z * c.z + l.z * s.z;
+    oh.w = h.w * c.w + l.w * s.w;
+}
+
 template <int DT, int HPG>
 __global__ __launch_bounds__(256) void qknorm_rope128_kernel(
     float* q, float* k, long q_ld, long k_ld, const void* wq, const void* wk, const int32_t* pos,
@@ -230,57 +289,66 @@ __global__ __launch_bounds__(256) void qknorm_rope128_kernel(
         }
     }
 #pragma unroll
-    for (int i = 0; i < HPG; i++) {
-        if (p[i] >= 0 && p[i] < tab_len) {
-            c[i] = *reinterpret_cast<const float4*>(cos_tab + (long)p[i] * 64 + j0);
-            s[i] = *reinterpret_cast<const float4*>(sin_tab + (long)p[i] * 64 + j0);
-        } else {
-            const float pf = (float)p[i];
-            const float a0 = pf * inv.v[j0], a1 = pf * inv.v[j0 + 1];
-            const float a2 = pf * inv.v[j0 + 2], a3 = pf * inv.v[j0 + 3];
-            c[i] = make_float4(cosf(a0), cosf(a1), cosf(a2), cosf(a3));
-            s[i] = make_float4(sinf(a0), sinf(a1), sinf(a2), sinf(a3));
-        }
-    }
+    for (int i = 0; i < HPG; i++) rope_cs4(p[i], j0, cos_tab, sin_tab, tab_len, inv, c[i], s[i]);
 #pragma unroll
     for (int i = 0; i < HPG; i++) {
-        float4 l = lo[i], h = hi[i];
-        float ss = 0.f;
-        ss = fmaf(l.x, l.x, ss);
-        ss = fmaf(l.y, l.y, ss);
-        ss = fmaf(l.z, l.z, ss);
-        ss = fmaf(l.w, l.w, ss);
-        ss = fmaf(h.x, h.x, ss);
-        ss = fmaf(h.y, h.y, ss);
-        ss = fmaf(h.z, h.z, ss);
-        ss = fmaf(h.w, h.w, ss);
-        ss = group16_sum(ss);   // every lane takes part (dead heads contribute zeros)
-        const void* w = isq[i] ? wq : wk;
-        if (w) {
-            const float sc = 1.0f / sqrtf(ss / 128.0f + eps);
-            const float4 wl = load_w4<DT>(w, j0);
-            const float4 wh = load_w4<DT>(w, j0 + 64);
-            l.x = (l.x * sc) * wl.x;
-            l.y = (l.y * sc) * wl.y;
-            l.z = (l.z * sc) * wl.z;
-            l.w = (l.w * sc) * wl.w;
-            h.x = (h.x * sc) * wh.x;
-            h.y = (h.y * sc) * wh.y;
-            h.z = (h.z * sc) * wh.z;
-            h.w = (h.w * sc) * wh.w;
-        }
+        float4 ol, oh;   // every lane takes part (dead heads contribute zeros)
+        norm_rope128<DT>(lo[i], hi[i], isq[i] ? wq : wk, c[i], s[i], j0, eps, ol, oh);
         if (v[i]) {
-            float4 ol, oh;
-            ol.x = l.x * c[i].x - h.x * s[i].x;
-            ol.y = l.y * c[i].y - h.y * s[i].y;
-            ol.z = l.z * c[i].z - h.z * s[i].z;
-            ol.w = l.w * c[i].w - h.w * s[i].w;
-            oh.x = h.x * c[i].x + l.x * s[i].x;
-            oh.y = h.y * c[i].y + l.y * s[i].y;
-            oh.z = h.z * c[i].z + l.z * s[i].z;
-            oh.w = h.w * c[i].w + l.w * s[i].w;
             st_nt(reinterpret_cast<float4*>(v[i] + j0), ol);
             st_nt(reinterpret_cast<float4*>(v[i] + 64 + j0), oh);
+        }
+    }
+}
+
+// The decode step's q/k norm + RoPE and KV ring append in one launch
+// (qwen3.cpp:444-488): token b of sequence b, one workgroup per sequence.
+// Groups of 16 lanes take the heads in turn (q heads, then k heads); q and k
+// are rewritten in place as anelm_qknorm_rope does, and k, with v copied as
+// it is, also goes to the ring slot that anelm_kv_ring_append would pick.
+// The ring state is read and advanced by one lane while the first heads'
+// loads are in flight.
+template <int DT>
+__global__ __launch_bounds__(1024) void qknorm_rope_append128_kernel(
+    float* q, float* k, const float* v, long q_ld, long k_ld, long v_ld, const void* wq, const void* wk,
+    const int32_t* pos, const float* cos_tab, const float* sin_tab, int tab_len, const InvFreq inv, int nq, int nk,
+    float eps, float* kc, float* vc, int32_t* rs, int32_t* rl, int cap, long seq_stride) {
+    __shared__ int s_slot;
+    const long b = blockIdx.x;
+    const int grp = threadIdx.x >> 4, ngrp = blockDim.x >> 4;
+    const int j0 = 4 * (threadIdx.x & 15);
+    const int nh = nq + nk;
+    auto head = [&](int hh) {
+        return hh < nq ? q + b * q_ld + (long)hh * 128 : k + b * k_ld + (long)(hh - nq) * 128;
+    };
+    float4 lo = make_float4(0.f, 0.f, 0.f, 0.f), hi = lo;
+    if (grp < nh) {
+        lo = ld_nt(reinterpret_cast<const float4*>(head(grp) + j0));
+        hi = ld_nt(reinterpret_cast<const float4*>(head(grp) + 64 + j0));
+    }
+    if (threadIdx.x == 0) s_slot = ring_advance(rs + b, rl + b, cap);
+    float4 c, s;
+    rope_cs4(pos[b], j0, cos_tab, sin_tab, tab_len, inv, c, s);
+    __syncthreads();
+    const long row = (long)nk * 128;
+    float* kd = kc + b * seq_stride + (long)s_slot * row;
+    float4* vd = reinterpret_cast<float4*>(vc + b * seq_stride + (long)s_slot * row);
+    const float4* vs = reinterpret_cast<const float4*>(v + b * v_ld);
+    for (int i = threadIdx.x; i < nk * 32; i += blockDim.x) vd[i] = vs[i];
+    for (int hh = grp; hh < nh; hh += ngrp) {   // uniform within the 16-lane group
+        if (hh != grp) {
+            lo = ld_nt(reinterpret_cast<const float4*>(head(hh) + j0));
+            hi = ld_nt(reinterpret_cast<const float4*>(head(hh) + 64 + j0));
+        }
+        float4 ol, oh;
+        norm_rope128<DT>(lo, hi, hh < nq ? wq : wk, c, s, j0, eps, ol, oh);
+        float* dst = head(hh);
+        *reinterpret_cast<float4*>(dst + j0) = ol;
+        *reinterpret_cast<float4*>(dst + 64 + j0) = oh;
+        if (hh >= nq) {
+            float* kr = kd + (long)(hh - nq) * 128;
+            *reinterpret_cast<float4*>(kr + j0) = ol;
+            *reinterpret_cast<float4*>(kr + 64 + j0) = oh;
         }
     }
 }
@@ -460,6 +528,50 @@ extern "C" int anelm_qknorm_rope(float* q, float* k, long q_ld, long k_ld, const
         case ANELM_F16: return launch_qknorm<ANELM_F16>(q, k, q_ld, k_ld, wq, wk, pos, cos_tab, sin_tab, tab_len, inv, T, nq, nk, head_dim, eps, st);
         default: return launch_qknorm<ANELM_BF16>(q, k, q_ld, k_ld, wq, wk, pos, cos_tab, sin_tab, tab_len, inv, T, nq, nk, head_dim, eps, st);
     }
+}
+
+extern "C" int anelm_qknorm_rope_append(float* q, float* k, const float* v, long q_ld, long k_ld, long v_ld,
+                                        const void* wq, const void* wk, int w_dtype, const int32_t* pos,
+                                        const float* cos_tab, const float* sin_tab, int tab_len, float theta,
+                                        long batch, int nq, int nk, float eps, float* k_cache, float* v_cache,
+                                        int32_t* ring_start, int32_t* ring_len, int capacity, long cache_seq_stride,
+                                        void* stream) {
+    const char* fn = "anelm_qknorm_rope_append";
+    if (!k || !v || !pos || !k_cache || !v_cache || !ring_start || !ring_len || (nq > 0 && !q))
+        return fail(ANELM_ERR_INVALID, "%s: null pointer", fn);
+    if (batch <= 0 || batch > 0x7FFFFFFFL || nq < 0 || nk <= 0 || capacity <= 0 || nq + nk > (1 << 20))
+        return fail(ANELM_ERR_INVALID, "%s: bad sizes", fn);
+    const long row = (long)nk * 128;
+    if (batch > 1 && ((nq > 0 && q_ld < (long)nq * 128) || k_ld < row || v_ld < row ||
+                      cache_seq_stride < (long)capacity * row))
+        return fail(ANELM_ERR_INVALID, "%s: strides overlap", fn);
+    if (tab_len < 0 || (tab_len > 0 && (!cos_tab || !sin_tab))) return fail(ANELM_ERR_INVALID, "%s: table", fn);
+    if (w_dtype < ANELM_F32 || w_dtype > ANELM_BF16) return fail(ANELM_ERR_INVALID, "%s: dtype", fn);
+    const bool wal = w_dtype == ANELM_F32 ? (!wq || aligned16(wq)) && (!wk || aligned16(wk))
+                                          : (!wq || aligned8(wq)) && (!wk || aligned8(wk));
+    if (!aligned16(k) || !aligned16(v) || (nq > 0 && !aligned16(q)) || !aligned16(k_cache) || !aligned16(v_cache) ||
+        (q_ld | k_ld | v_ld | cache_seq_stride) & 3 || !wal ||
+        (tab_len > 0 && (!aligned16(cos_tab) || !aligned16(sin_tab))))
+        return fail(ANELM_ERR_INVALID, "%s: needs 16-byte aligned rows (strides multiples of 4)", fn);
+    InvFreq inv;
+    rope_inv_freq(&inv, 128, theta);
+    clear_error();
+    if (nq == 0) q = k;  // never dereferenced
+    const int threads = (int)std::min<long>(1024, ((long)(nq + nk) * 16 + 63) / 64 * 64);
+    const dim3 grid((unsigned)batch), block((unsigned)threads);
+    hipStream_t st = as_stream(stream);
+#define LAUNCH(DT)                                                                                            \
+    qknorm_rope_append128_kernel<DT><<<grid, block, 0, st>>>(q, k, v, q_ld, k_ld, v_ld, wq, wk, pos, cos_tab, \
+                                                             sin_tab, tab_len, inv, nq, nk, eps, k_cache,     \
+                                                             v_cache, ring_start, ring_len, capacity,         \
+                                                             cache_seq_stride)
+    switch (w_dtype) {
+        case ANELM_F32: LAUNCH(ANELM_F32); break;
+        case ANELM_F16: LAUNCH(ANELM_F16); break;
+        default: LAUNCH(ANELM_BF16); break;
+    }
+#undef LAUNCH
+    return launch_status("qknorm_rope_append");
 }
 
 extern "C" int anelm_rope_cached(float* q, float* k, int n_q_heads, int n_kv_heads, int head_dim,

@@ -9,8 +9,9 @@
 // round-to-nearest fp16 and leave it as fp16 (core/ane_runtime.cpp:600-640).
 // The RMSNorms, residual adds and the SwiGLU are fused into the
 // projections: up to 16 sequences as the projections' own prologue and
-// epilogues (7 launches per layer instead of 13), past that with the norms
-// writing the projections' fp16 inputs (8 launches).
+// epilogues (6 library calls per layer instead of 12), past that with the
+// norms writing the projections' fp16 inputs (8 calls); the q/k norm, RoPE
+// and ring append are one kernel throughout.
 //
 // A step processes one token of each of `batch` sequences; every sequence
 // has its own KV ring per layer (qwen3.cpp:227-231, 475-488).
@@ -315,23 +316,26 @@ extern "C" int anelm_qwen3_forward(anelm_qwen3* m, const int32_t* ids, const int
             if ((r = anelm_f16_to_f32(out + b * ld_out, m->y16 + b * n_out, (size_t)n_out, stream))) return r;
         return ANELM_OK;
     };
+    // q/k norm + RoPE and the KV ring append, one launch (head_dim 128)
+    auto qk_append = [&](const anelm_qwen3::Layer& l) -> int {
+        return anelm_qknorm_rope_append(m->qkv, m->qkv + m->qdim, m->qkv + m->qdim + m->kvdim, m->qkvdim, m->qkvdim,
+                                        m->qkvdim, l.qn, l.kn, ANELM_BF16, pos, m->cos_tab, m->sin_tab, kRopeRows,
+                                        c.rope_theta, B, c.n_q_heads, c.n_kv_heads, c.rms_eps, l.kc, l.vc, l.start,
+                                        l.len, m->cap, seq, stream);
+    };
     CK(anelm_embed_gather(m->x, m->embed, ANELM_BF16, ids, B, H, V, bad_ids, stream));             // :498
     const bool dims32 = H % 32 == 0 && I % 32 == 0 && m->qdim % 32 == 0;
     if (dims32 && B > 16) {
         // Past 16 rows the RMSNorms round their output to fp16 once
         // (anelm_rmsnorm_f16) and the projections read fp16 rows; the SwiGLU
         // writes the down projection's fp16 input and the residual adds ride
-        // in the o and down projections: 8 launches per layer
+        // in the o and down projections: 8 calls per layer
         for (int L = 0; L < c.layers; L++) {
             const anelm_qwen3::Layer& l = m->layers[L];
             CK(anelm_rmsnorm_f16(m->a16, m->x, l.w_in, ANELM_BF16, B, (int)H, H, H, c.rms_eps, stream));  // :503
             CK(anelm_proj_f16_x16_fused(m->qkv, m->a16, l.qkv16, B, m->qkvdim, (int)H, H, m->qkvdim,
                                         ANELM_PROJ_STORE, stream));                               // first_proj
-            CK(anelm_qknorm_rope(m->qkv, m->qkv + m->qdim, m->qkvdim, m->qkvdim, l.qn, l.kn, ANELM_BF16, pos,
-                                 m->cos_tab, m->sin_tab, kRopeRows, c.rope_theta, B, c.n_q_heads, c.n_kv_heads, D,
-                                 c.rms_eps, stream));                                             // :444-472
-            CK(anelm_kv_ring_append(l.kc, l.vc, l.start, l.len, m->qkv + m->qdim, m->qkv + m->qdim + m->kvdim,
-                                    m->qkvdim, m->qkvdim, B, c.n_kv_heads, D, m->cap, seq, stream));  // :475-488
+            CK(qk_append(l));                                                                      // :444-488
             CK(anelm_gqa_attention(m->attn, m->qkv, l.kc, l.vc, l.start, l.len, B, c.n_q_heads, c.n_kv_heads, D,
                                    m->qkvdim, D, m->qdim, m->cap, seq, m->attn_ws, m->attn_ws_bytes, stream));  // :490
             CK(anelm_proj_f16_fused(m->x, m->attn, l.o16, B, (int)H, m->qdim, m->qdim, H, nullptr, 0.0f,
@@ -355,17 +359,13 @@ extern "C" int anelm_qwen3_forward(anelm_qwen3* m, const int32_t* ids, const int
         return ANELM_OK;
     }
     if (dims32) {
-        // 7 launches per layer: the RMSNorms, residual adds and the SwiGLU
+        // 6 calls per layer: the RMSNorms, residual adds and the SwiGLU
         // ride in the projections (anelm_proj_f16_fused)
         for (int L = 0; L < c.layers; L++) {
             const anelm_qwen3::Layer& l = m->layers[L];
             CK(anelm_proj_f16_fused(m->qkv, m->x, l.qkv16, B, m->qkvdim, (int)H, H, m->qkvdim, l.w_in, c.rms_eps,
                                     ANELM_PROJ_STORE, stream));                                   // :503 + first_proj
-            CK(anelm_qknorm_rope(m->qkv, m->qkv + m->qdim, m->qkvdim, m->qkvdim, l.qn, l.kn, ANELM_BF16, pos,
-                                 m->cos_tab, m->sin_tab, kRopeRows, c.rope_theta, B, c.n_q_heads, c.n_kv_heads, D,
-                                 c.rms_eps, stream));                                             // :444-472
-            CK(anelm_kv_ring_append(l.kc, l.vc, l.start, l.len, m->qkv + m->qdim, m->qkv + m->qdim + m->kvdim,
-                                    m->qkvdim, m->qkvdim, B, c.n_kv_heads, D, m->cap, seq, stream));  // :475-488
+            CK(qk_append(l));                                                                      // :444-488
             CK(anelm_gqa_attention(m->attn, m->qkv, l.kc, l.vc, l.start, l.len, B, c.n_q_heads, c.n_kv_heads, D,
                                    m->qkvdim, D, m->qdim, m->cap, seq, m->attn_ws, m->attn_ws_bytes, stream));  // :490
             CK(anelm_proj_f16_fused(m->x, m->attn, l.o16, B, (int)H, m->qdim, m->qdim, H, nullptr, 0.0f,
@@ -383,11 +383,7 @@ extern "C" int anelm_qwen3_forward(anelm_qwen3* m, const int32_t* ids, const int
         const anelm_qwen3::Layer& l = m->layers[L];
         CK(anelm_rmsnorm(m->xn, m->x, l.w_in, ANELM_BF16, B, (int)H, H, H, c.rms_eps, stream));    // :503
         CK(project(m->qkv, m->qkvdim, m->xn, H, l.qkv16, m->qkvdim));                             // first_proj
-        CK(anelm_qknorm_rope(m->qkv, m->qkv + m->qdim, m->qkvdim, m->qkvdim, l.qn, l.kn, ANELM_BF16, pos,
-                             m->cos_tab, m->sin_tab, kRopeRows, c.rope_theta, B, c.n_q_heads, c.n_kv_heads, D,
-                             c.rms_eps, stream));                                                 // :444-472
-        CK(anelm_kv_ring_append(l.kc, l.vc, l.start, l.len, m->qkv + m->qdim, m->qkv + m->qdim + m->kvdim,
-                                m->qkvdim, m->qkvdim, B, c.n_kv_heads, D, m->cap, seq, stream));  // :475-488
+        CK(qk_append(l));                                                                          // :444-488
         CK(anelm_gqa_attention(m->attn, m->qkv, l.kc, l.vc, l.start, l.len, B, c.n_q_heads, c.n_kv_heads, D,
                                m->qkvdim, D, m->qdim, m->cap, seq, m->attn_ws, m->attn_ws_bytes, stream));  // :490
         CK(project(m->o, H, m->attn, m->qdim, l.o16, H));                                         // o_proj

@@ -98,6 +98,20 @@ int anelm_qknorm_rope(float* q, float* k, long q_ld, long k_ld, const void* wq, 
                       int tab_len, float theta, long T, int nq, int nk, int head_dim, float eps,
                       void* stream);
 
+/* The decode step's anelm_qknorm_rope then anelm_kv_ring_append in one
+ * launch (models/llm/qwen3.cpp:444-488), head_dim 128: token b of `batch` is
+ * sequence b's (position pos[b]); its q heads (q + b*q_ld, nq of them) and k
+ * heads (k + b*k_ld, nk) are normalised and rotated in place exactly as
+ * anelm_qknorm_rope does, and its k (as rotated) and v (v + b*v_ld, copied)
+ * are appended to ring b exactly as anelm_kv_ring_append does.  q, k, v, the
+ * caches and the tables 16-byte aligned, strides multiples of 4.  No
+ * counterpart in the reference (there the three steps are separate loops). */
+int anelm_qknorm_rope_append(float* q, float* k, const float* v, long q_ld, long k_ld, long v_ld, const void* wq,
+                             const void* wk, int w_dtype, const int32_t* pos, const float* cos_tab,
+                             const float* sin_tab, int tab_len, float theta, long batch, int nq, int nk, float eps,
+                             float* k_cache, float* v_cache, int32_t* ring_start, int32_t* ring_len, int capacity,
+                             long cache_seq_stride, void* stream);
+
 /* ane_lm::apply_rope_cached semantics (core/cpu_ops.h:26-29,
  * core/cpu_ops.cpp:56-80) for ONE token: heads at q + h*q_head_stride and
  * k + h*k_head_stride, the first rot_dim elements rotated.  With a table row

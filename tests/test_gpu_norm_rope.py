@@ -218,3 +218,46 @@ def test_rope_table(hip, orc, n_pos):
     gc, gs = host(c), host(s)
     assert np.all(gc[0] == 1.0) and np.all(gs[0] == 0.0)
     assert np.max(np.abs(gc - rc)) <= 2.0 ** -22 and np.max(np.abs(gs - rs)) <= 2.0 ** -22
+
+
+@pytest.mark.parametrize("B,nq,nk,cap,fill,dt", [(1, 16, 8, 64, 0, "bf16"), (64, 16, 8, 64, 10, "bf16"),
+                                                 (5, 32, 8, 16, 16, "f16"), (3, 4, 2, 8, 40, "f32"),
+                                                 (2, 64, 8, 4, 3, "bf16"), (7, 0, 4, 32, 31, "f16")])
+def test_qknorm_rope_append_matches_separate_kernels(hip, orc, rng, B, nq, nk, cap, fill, dt):
+    """The decode step's fused q/k norm + RoPE + ring append equals
+    anelm_qknorm_rope followed by anelm_kv_ring_append bit for bit: rotated
+    q/k in the fused [q|k|v] rows, cache contents and ring state, over rings
+    empty, part-full, full and wrapped (fill appends before the step), with
+    some positions past the table (the fallback angle)."""
+    import torch
+
+    D = 128
+    row = (nq + 2 * nk) * D
+    qkv = rng.standard_normal((B, row), dtype=np.float32)
+    pos = rng.integers(0, 3000, B).astype(np.int32)
+    wq, _ = _gamma(rng, D, dt)
+    wk, _ = _gamma(rng, D, dt)
+    c_tab, s_tab = orc.rope_table(2048, D, THETA)
+    caches = []
+    for _ in range(2):
+        kc = torch.zeros(B, cap, nk * D, device="cuda")
+        vc = torch.zeros(B, cap, nk * D, device="cuda")
+        rs = torch.zeros(B, dtype=torch.int32, device="cuda")
+        rl = torch.zeros(B, dtype=torch.int32, device="cuda")
+        for f in range(fill):   # the same history in both
+            kv = dev(np.full((B, 2 * nk * D), float(f + 1), np.float32))
+            hip.kv_ring_append(kc, vc, rs, rl, kv[:, :nk * D], kv[:, nk * D:])
+        caches.append((kc, vc, rs, rl))
+    a, b = dev(qkv), dev(qkv)
+    q_of = lambda t: t[:, :nq * D] if nq else None
+    kc, vc, rs, rl = caches[0]
+    hip.qknorm_rope(q_of(a), a[:, nq * D:(nq + nk) * D], wq, wk, dev(pos), dev(c_tab), dev(s_tab), THETA, EPS,
+                    nq=nq, nk=nk)
+    hip.kv_ring_append(kc, vc, rs, rl, a[:, nq * D:(nq + nk) * D], a[:, (nq + nk) * D:])
+    kc2, vc2, rs2, rl2 = caches[1]
+    hip.qknorm_rope_append(q_of(b) if nq else b[:, :0], b[:, nq * D:(nq + nk) * D], b[:, (nq + nk) * D:], wq, wk,
+                           dev(pos), dev(c_tab), dev(s_tab), kc2, vc2, rs2, rl2, THETA, EPS, nq=nq, nk=nk)
+    assert_bitexact(host(b), host(a), "q|k|v rows")
+    assert_bitexact(host(kc2), host(kc), "k cache")
+    assert_bitexact(host(vc2), host(vc), "v cache")
+    assert np.array_equal(host(rs2), host(rs)) and np.array_equal(host(rl2), host(rl))
