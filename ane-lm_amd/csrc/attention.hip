@@ -29,6 +29,8 @@ constexpr int kMinChunk = 32;
 constexpr int kMaxGD = 1024;          // group heads x head_dim per workgroup
 constexpr long kTargetBlocks = 2048;  // 8 workgroups per CU on 256 CUs
 constexpr int kMaxSplit = 4096;       // chunks per sequence (capacity <= 4096*32)
+constexpr int kWholeRows = 128;       // rings up to this long (or one chunk) are done by one workgroup
+static_assert(kWholeRows <= kMaxChunk, "a whole ring's scores fit the LDS rows");
 
 struct AttnArgs {
     float* out;
@@ -45,6 +47,7 @@ struct AttnArgs {
     int cap;
     long seq_stride;            // between sequences' caches
     int chunk, nsplit;
+    int whole;                  // split launches: rings of at most this many rows are done by chunk 0 alone
     int g0, gcount;             // q heads g0 .. g0+gcount-1 of every group
     float scale;
     float* ws;                  // [batch*nh][nsplit][head_dim + 2] partials
@@ -119,8 +122,15 @@ __global__ __launch_bounds__(kAttnThreads) void gqa_decode_kernel(AttnArgs a) {
     const long b = blockIdx.z;
     int start, len;
     ring_state(a, b, start, len);
+    // In a split launch a ring that is short (len <= a.whole, at most one
+    // chunk's worth of LDS) is done by chunk 0 alone, which then writes the
+    // normalised output itself; the merge kernel skips that sequence.  The
+    // ring lengths live on the device, so this is decided per sequence here.
+    const bool whole = !FINAL && len <= a.whole;
+    if (whole && split > 0) return;
+    const bool fin = FINAL || whole;
     const int t0 = split * a.chunk;
-    const int n = min(t0 + a.chunk, len) - t0;     // positions of this chunk (may be <= 0)
+    const int n = whole ? len : min(t0 + a.chunk, len) - t0;     // positions of this chunk (may be <= 0)
     const int ps = wid * PPW + lane / LP;          // position slot within a round
     const int ds = lane % LP;                      // this lane's 8-float slice
     const int row = a.nkv * D;                     // cap * row < 2^31 (checked on the host)
@@ -193,7 +203,7 @@ __global__ __launch_bounds__(kAttnThreads) void gqa_decode_kernel(AttnArgs a) {
             l += e;
         }
         l = wave_sum(l);
-        if (FINAL) {  // the reference's p = e * (1/sum) (core/cpu_ops.cpp:97-98)
+        if (fin) {  // the reference's p = e * (1/sum) (core/cpu_ops.cpp:97-98)
             const float inv = 1.0f / l;
             for (int i = lane; i < n; i += kWave) sc[g][i] = sc[g][i] * inv;
         }
@@ -253,7 +263,7 @@ __global__ __launch_bounds__(kAttnThreads) void gqa_decode_kernel(AttnArgs a) {
 #pragma unroll
         for (int w = 1; w < kAttnWaves; w++) s += red[w][g][d];
         const int h = kvh * a.groups + a.g0 + g;
-        if (FINAL) {
+        if (fin) {
             a.out[b * a.out_ld + (long)h * D + d] = s;
         } else {
             float* p = a.ws + ((b * a.nh + h) * a.nsplit + split) * (long)(D + 2);
@@ -266,7 +276,8 @@ __global__ __launch_bounds__(kAttnThreads) void gqa_decode_kernel(AttnArgs a) {
     }
 }
 
-// Merges the per-chunk partials of one (sequence, q head): one wave; lane j
+// Merges the per-chunk partials of one (sequence, q head), for rings longer
+// than a.whole (chunk 0 wrote the shorter ones' output): one wave; lane j
 // owns chunks j, j+64, ... for the (max, sum) merge, then every lane sums its
 // head_dim/64 outputs over all chunks.  The first kBatch chunks' output
 // partials are loaded together with the (max, sum) pairs, before the max is
@@ -280,6 +291,9 @@ __global__ __launch_bounds__(kWave) void gqa_combine_kernel(AttnArgs a) {
     const long bh = blockIdx.x;
     const long b = bh / a.nh;
     const int h = (int)(bh % a.nh);
+    int start, len;
+    ring_state(a, b, start, len);
+    if (len <= a.whole) return;   // chunk 0 did the whole ring and wrote the output
     const int ns = a.nsplit;
     const float* p = a.ws + bh * ns * (long)(D + 2);
     auto clampc = [&](int s) { return s < ns ? s : ns - 1; };
@@ -432,6 +446,7 @@ int run(AttnArgs a, long batch, int D, int bound, void* ws, size_t ws_bytes, hip
     a.chunk = pick_chunk(batch * a.nkv, a.cap);  // from the capacity, so the workspace size holds for any bound
     a.nsplit = (bound + a.chunk - 1) / a.chunk;
     if (a.nsplit < 1) a.nsplit = 1;
+    a.whole = a.chunk > kWholeRows ? a.chunk : kWholeRows;   // <= kMaxChunk, the LDS score rows
     if (a.nsplit > 1) {
         const size_t need = (size_t)batch * a.nh * a.nsplit * (D + 2) * sizeof(float);
         if (!ws || ws_bytes < need)

@@ -104,6 +104,18 @@ def test_batched_decode_b64_full_shape(hip, orc, rng):
         check(got[b], q[b], kc[b], vc[b], nq, nk, D, int(starts[b]), int(lens[b]), orc)
 
 
+def test_whole_ring_threshold(hip, orc, rng):
+    """Rings short enough for one workgroup (128 rows at this shape: 32-row
+    chunks) are done by chunk 0 alone, longer ones split and merged; lengths
+    on both sides of the threshold in one launch, some wrapping."""
+    B, nq, nk, D, cap = 6, 16, 8, 128, 2048
+    lens = [0, 1, 127, 128, 129, 2048]
+    starts = [5, 2047, 1990, 0, 1950, 700]
+    got, q, kc, vc = batched(hip, B, nq, nk, D, cap, starts, lens, rng)
+    for b in range(B):
+        check(got[b], q[b], kc[b], vc[b], nq, nk, D, starts[b], lens[b], orc)
+
+
 @pytest.mark.parametrize("B,nq,nk,D,cap", [(3, 16, 8, 128, 4096), (600, 16, 8, 128, 64), (5, 8, 4, 64, 333)])
 def test_batched_other_shapes(hip, orc, rng, B, nq, nk, D, cap):
     starts = rng.integers(0, cap, B)
