@@ -446,10 +446,14 @@ def measure_blobs(hip, workdir, reps=2):
 
 Q3_WORKLOADS = {
     # one decode step of a Qwen3-0.6B-shaped model (random weights) for B
-    # sequences: every layer op, the attention over 2048-row rings and the
-    # fp16 projections (the reference's ANE contractions) with the LM head
+    # sequences: every layer op, the attention over rings of capacity 2048
+    # and the fp16 projections (the reference's ANE contractions) with the LM
+    # head.  The rings start empty (a few dozen rows by the timed steps) or,
+    # with ctx, hold that many rows from earlier steps.
     "qwen3-0.6b-decode-step-b1": dict(B=1),
     "qwen3-0.6b-decode-step-b64": dict(B=64),
+    "qwen3-0.6b-decode-step-b1-ctx1024": dict(B=1, ctx=1024),
+    "qwen3-0.6b-decode-step-b64-ctx1024": dict(B=64, ctx=1024),
 }
 Q3_06B = dict(hidden=1024, layers=28, n_q_heads=16, n_kv_heads=8, head_dim=D, intermediate=3072, vocab=VOCAB)
 
@@ -465,7 +469,7 @@ def q3_weight_bytes():
 
 def measure_qwen3(hip, src, w, steps=30):
     """Graph-replayed decode steps (positions advance inside the graph) from
-    empty rings; tokens/s = B x steps / time."""
+    empty rings, or after w["ctx"] eager steps; tokens/s = B x steps / time."""
     import torch
 
     B = w["B"]
@@ -480,19 +484,29 @@ def measure_qwen3(hip, src, w, steps=30):
     def step():
         model.forward(ids, pos, logits)
         pos.add_(1)
-    step()
+    for _ in range(max(1, w.get("ctx", 0))):
+        step()
     gr = capture(step)
     for _ in range(3):
         gr.replay()
     ms = time_region(gr.replay, steps)
     byt = q3_weight_bytes()
+    # K and V rows each timed step reads: the rings hold ctx rows (at least
+    # one step) + 1 (capture's run) + 3 (warm replays), plus one more per step
+    c = Q3_06B
+    rows = max(1, w.get("ctx", 0)) + 4 + (steps + 1) / 2
+    kv = int(c["layers"] * B * rows * c["n_kv_heads"] * D * 4 * 2)
     del gr
     model.close()
     torch.cuda.empty_cache()
     return dict(ms_per_step=round(ms, 4), tokens_per_s=round(B / (ms / 1e3), 1),
                 weight_GBps=round(byt / ms / 1e6, 1), weight_frac=round(byt / ms / 1e6 / HBM_PEAK_GBPS, 4),
                 weight_bytes=byt, steps=steps,
-                note="decode steps from empty 2048-row rings; weight_GBps = fp16 projection + LM-head bytes / step time")
+                ring_rows=f"{w.get('ctx', 0)}+ (capacity 2048)", kv_bytes=kv,
+                total_GBps=round((byt + kv) / ms / 1e6, 1), total_frac=round((byt + kv) / ms / 1e6 / HBM_PEAK_GBPS, 4),
+                note="weight_GBps = fp16 projection + LM-head bytes / step time; ring_rows = rows in each ring when "
+                     "the timed steps start; total_GBps adds the K and V rows the attention reads (kv_bytes, "
+                     "averaged over the timed steps)")
 
 
 def cpu_qwen3(src, steps=2):
