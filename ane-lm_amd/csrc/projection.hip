@@ -148,6 +148,22 @@ __global__ __launch_bounds__(64 * NW) void proj_mfma_kernel(ProjArgs a) {
     // the first round's loads go out before the RMSNorm prologue, whose own
     // loads then overlap them
     issue(wv);
+    // the residual add's y values are loaded now, with the weights, not after
+    // the reduction (addresses clamped: lanes without an output load a valid
+    // element and never use it)
+    constexpr int QPW = (RT * NB + NW - 1) / NW;  // epilogue tiles per wave
+    float yprev[EPI == kAdd ? QPW : 1][4];
+    if constexpr (EPI == kAdd) {
+#pragma unroll
+        for (int j = 0; j < QPW; j++) {
+            const int q = wv + j * NW < RT * NB ? wv + j * NW : RT * NB - 1;
+            const int b = b0 + (q % NB) * 16 + c;
+            const float* yr = a.y + (long)(b < a.batch ? b : a.batch - 1) * a.ld_y;
+            const long r = row0 + 16 * (q / NB) + 4 * g;
+#pragma unroll
+            for (int i = 0; i < 4; i++) yprev[j][i] = yr[r + i < a.out_dim ? r + i : a.out_dim - 1];
+        }
+    }
 
     if constexpr (NORM) {
         // wave w: the workgroup's batch rows w, w+NW, ... that exist; each
@@ -238,7 +254,10 @@ __global__ __launch_bounds__(64 * NW) void proj_mfma_kernel(ProjArgs a) {
             }
         }
     } else {
-        for (int q = wv; q < RT * NB; q += NW) {
+#pragma unroll
+        for (int j = 0; j < QPW; j++) {
+            const int q = wv + j * NW;
+            if (q >= RT * NB) break;
             float4v s = part[0][q][lane];
             for (int w = 1; w < NW; w++) s += part[w][q][lane];
             const int t = q / NB, nb = q % NB;
@@ -249,7 +268,7 @@ __global__ __launch_bounds__(64 * NW) void proj_mfma_kernel(ProjArgs a) {
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     if (r + i < a.out_dim) {
-                        if constexpr (EPI == kAdd) yr[r + i] = yr[r + i] + r16(s[i]);
+                        if constexpr (EPI == kAdd) yr[r + i] = yprev[j][i] + r16(s[i]);
                         else yr[r + i] = r16(s[i]);
                     }
                 }
@@ -303,8 +322,16 @@ __global__ __launch_bounds__(256) void proj_dot_kernel(ProjArgs a) {
             for (int t = 0; t < NR; t++) wr[k][t] = ld_nt(reinterpret_cast<const uint4*>(wp[t] + idx[k]));
         }
     };
-    // the first chunks' weight loads go out before the RMSNorm prologue
+    // the first chunks' weight loads go out before the RMSNorm prologue, and
+    // the residual add's y value with them (lane b*RPW + t: row r0 + t of x
+    // row b; clamped, unused where the lane stores nothing)
     issue(0);
+    float yprev = 0.f;
+    if constexpr (EPI == kAdd) {
+        const int t = lane % RPW, b = lane / RPW < a.batch ? lane / RPW : a.batch - 1;
+        const long r = r0 + t < a.out_dim ? r0 + t : a.out_dim - 1;
+        yprev = a.y[(long)b * a.ld_y + r];
+    }
 
     float scale[BT];
 #pragma unroll
@@ -392,7 +419,7 @@ __global__ __launch_bounds__(256) void proj_dot_kernel(ProjArgs a) {
     const int t = lane % RPW, b = lane / RPW;
     if (lane < RPW * BT && b < a.batch && r0 + t < a.out_dim) {
         float* yp = a.y + (long)b * a.ld_y + r0 + t;
-        if constexpr (EPI == kAdd) *yp = *yp + r16(s);
+        if constexpr (EPI == kAdd) *yp = yprev + r16(s);
         else if constexpr (EPI == kSwiGLU) *yp = silu_ref(r16(s)) * r16(u);
         else *yp = r16(s);
     }
