@@ -65,6 +65,7 @@ _SIGS = {
     "anelm_bf16_to_f16": (_I, [_P, _P, _S, _P]),
     "anelm_bf16_to_f32": (_I, [_P, _P, _S, _P]),
     "anelm_bf16_to_f32_plus1": (_I, [_P, _P, _S, _P]),
+    "anelm_bf16_to_f16_multi": (_I, [_P, _P, _P, _I, _P]),
     "anelm_f16_to_f32": (_I, [_P, _P, _S, _P]),
     "anelm_f32_to_f16": (_I, [_P, _P, _S, _P]),
     "anelm_softmax_workspace_size": (_S, [_L, _L]),
@@ -273,6 +274,16 @@ def bf16_to_f16(dst, src, stream=None):
 
 def bf16_to_f32(dst, src, stream=None):
     _check(lib().anelm_bf16_to_f32(_ptr(dst), _ptr(src), src.numel(), _stream(stream)))
+
+
+def bf16_to_f16_multi(dsts, srcs, stream=None):
+    """anelm_bf16_to_f16 over lists of tensors (uint16/int16 views), a few launches in all."""
+    _need(len(dsts) == len(srcs), "bf16_to_f16_multi: list lengths")
+    k = len(srcs)
+    d = (ctypes.c_void_p * max(k, 1))(*[t.data_ptr() for t in dsts])
+    sp = (ctypes.c_void_p * max(k, 1))(*[t.data_ptr() for t in srcs])
+    n = (ctypes.c_size_t * max(k, 1))(*[t.numel() for t in srcs])
+    _check(lib().anelm_bf16_to_f16_multi(d, sp, n, k, _stream(stream)))
 
 
 def bf16_to_f32_plus1(dst, src, stream=None):

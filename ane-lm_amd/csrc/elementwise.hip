@@ -132,6 +132,55 @@ __global__ __launch_bounds__(256) void bf16_to_f16_vec_kernel(uint4* dst, const 
     }
 }
 
+// Many tensors in one launch: the table of up to kCvtBatch tensors travels
+// in the kernel arguments, so no device-side list is needed.  Each tensor is
+// cut into tiles of 256 * 8 * kU elements; workgroup w finds its tensor by a
+// binary search over the tile prefix (uniform, scalar) and converts its
+// tile, the last tile of a tensor also taking the n % 8 tail element-wise.
+constexpr int kCvtBatch = 128;
+struct CvtTable {
+    const uint16_t* src[kCvtBatch];
+    uint16_t* dst[kCvtBatch];
+    unsigned long long n[kCvtBatch];
+    unsigned tile0[kCvtBatch + 1];  // first tile of each tensor; tile0[count] = tiles in the launch
+    int count;
+};
+
+template <int kU>
+__global__ __launch_bounds__(256) void bf16_to_f16_multi_kernel(const CvtTable t) {
+    const unsigned tile = blockIdx.x;
+    int lo = 0, hi = t.count - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (t.tile0[mid] <= tile) lo = mid;
+        else hi = mid - 1;
+    }
+    const size_t n = t.n[lo], n8 = n / 8;
+    const uint4* src = reinterpret_cast<const uint4*>(t.src[lo]);
+    uint4* dst = reinterpret_cast<uint4*>(t.dst[lo]);
+    const size_t base = (size_t)(tile - t.tile0[lo]) * (256 * kU) + threadIdx.x;
+    uint4 a[kU];
+#pragma unroll
+    for (int i = 0; i < kU; i++) {
+        const size_t idx = base + (size_t)i * 256;
+        if (idx < n8) a[i] = ld_nt(src + idx);
+    }
+#pragma unroll
+    for (int i = 0; i < kU; i++) {
+        const size_t idx = base + (size_t)i * 256;
+        if (idx < n8) {
+            uint4 r;
+            r.x = cvt_pair(a[i].x);
+            r.y = cvt_pair(a[i].y);
+            r.z = cvt_pair(a[i].z);
+            r.w = cvt_pair(a[i].w);
+            st_nt(dst + idx, r);
+        }
+    }
+    const size_t tail = n8 * 8 + threadIdx.x;  // the last tile: elements n8*8 .. n-1
+    if (tile + 1 == t.tile0[lo + 1] && tail < n) t.dst[lo][tail] = (uint16_t)bf16_to_f16_trunc(t.src[lo][tail]);
+}
+
 __global__ __launch_bounds__(256) void bf16_to_f16_scalar_kernel(uint16_t* dst, const uint16_t* src, size_t n) {
     for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256)
         dst[i] = (uint16_t)bf16_to_f16_trunc(src[i]);
@@ -310,6 +359,46 @@ extern "C" int anelm_bf16_to_f16(uint16_t* dst, const uint16_t* src, size_t n, v
         bf16_to_f16_scalar_kernel<<<grid_stride_blocks(n), 256, 0, st>>>(dst, src, n);
     }
     return launch_status("bf16_to_f16");
+}
+
+extern "C" int anelm_bf16_to_f16_multi(uint16_t* const* dst, const uint16_t* const* src, const size_t* n, int count,
+                                       void* stream) {
+    if (count < 0 || (count > 0 && (!dst || !src || !n))) return fail(ANELM_ERR_INVALID, "anelm_bf16_to_f16_multi: arguments");
+    for (int i = 0; i < count; i++)
+        if (n[i] > 0 && (!dst[i] || !src[i])) return fail(ANELM_ERR_INVALID, "anelm_bf16_to_f16_multi: null tensor %d", i);
+    clear_error();
+    hipStream_t st = as_stream(stream);
+    constexpr size_t kTile = 256 * 8 * kU_cvt;
+    CvtTable t;
+    t.count = 0;
+    t.tile0[0] = 0;
+    auto flush = [&]() -> int {
+        if (t.count == 0) return ANELM_OK;
+        bf16_to_f16_multi_kernel<kU_cvt><<<dim3(t.tile0[t.count]), dim3(256), 0, st>>>(t);
+        t.count = 0;
+        return launch_status("bf16_to_f16_multi");
+    };
+    for (int i = 0; i < count; i++) {
+        if (n[i] == 0) continue;
+        if (!aligned16(dst[i]) || !aligned16(src[i])) {  // rare: its own launch, element-wise
+            int rc = flush();
+            if (rc) return rc;
+            if ((rc = anelm_bf16_to_f16(dst[i], src[i], n[i], stream))) return rc;
+            continue;
+        }
+        const size_t tiles = (n[i] + kTile - 1) / kTile;
+        if (tiles > 0x7FFFFFFFu) return fail(ANELM_ERR_INVALID, "anelm_bf16_to_f16_multi: tensor %d too large", i);
+        if (t.count == kCvtBatch || (size_t)t.tile0[t.count] + tiles > 0x7FFFFFFFu) {
+            const int rc = flush();
+            if (rc) return rc;
+        }
+        t.src[t.count] = src[i];
+        t.dst[t.count] = dst[i];
+        t.n[t.count] = n[i];
+        t.tile0[t.count + 1] = t.tile0[t.count] + (unsigned)tiles;
+        t.count++;
+    }
+    return flush();
 }
 
 extern "C" int anelm_bf16_to_f32(float* dst, const uint16_t* src, size_t n, void* stream) {

@@ -237,7 +237,8 @@ def measure_sampler(hip, steps, rows=64, vocab=VOCAB, freq=0.1):
 
 def measure_convert(hip, reps=3):
     """bf16->fp16 of the 8,190,735,360-parameter Qwen3-8B set: one call over the
-    contiguous set, and one call per tensor (399 launches, graph-replayed)."""
+    contiguous set, one call per tensor (399 launches, graph-replayed), and
+    the tensors through the multi-tensor call (4 launches)."""
     import torch
 
     sizes = qwen3_8b_tensor_sizes()
@@ -261,10 +262,16 @@ def measure_convert(hip, reps=3):
     gr = capture(lambda: [hip.bf16_to_f16(d, s) for d, s in views])
     gr.replay()
     ms_per = time_region(gr.replay, reps)
-    del src, dst, views, gr
+    dl, sl = [d for d, _ in views], [s for _, s in views]
+    multi = lambda: hip.bf16_to_f16_multi(dl, sl)
+    multi()
+    ms_multi = time_region(multi, reps)
+    del src, dst, views, gr, dl, sl
     torch.cuda.empty_cache()
     f = lambda ms: dict(ms=round(ms, 4), GBps=round(byt / ms / 1e6, 1), frac=round(byt / ms / 1e6 / HBM_PEAK_GBPS, 4))
-    return dict(params=n, bytes=byt, contiguous_set=f(ms_one), per_tensor=dict(f(ms_per), launches=len(sizes)))
+    return dict(params=n, bytes=byt, contiguous_set=f(ms_one), per_tensor=dict(f(ms_per), launches=len(sizes)),
+                per_tensor_batched=dict(f(ms_multi), launches=-(-len(sizes) // 128),
+                                        note="anelm_bf16_to_f16_multi: the same tensors, up to 128 per launch"))
 
 
 ATTN_WORKLOADS = {

@@ -163,6 +163,15 @@ int anelm_embed_gather(float* out, const void* table, int table_dtype, const int
  * Replaces the per-weight loop at core/safetensors.cpp:335 (write_ane_blob)
  * and core/ane_runtime.cpp:207 (build_weight_blob).  dst may equal src. */
 int anelm_bf16_to_f16(uint16_t* dst, const uint16_t* src, size_t n, void* stream);
+/* anelm_bf16_to_f16 over many tensors: tensor i is n[i] elements from src[i]
+ * to dst[i] (dst[i] may equal src[i]).  dst, src and n are HOST arrays (of
+ * device pointers); up to 128 tensors share one launch, so converting a
+ * checkpoint tensor by tensor (core/safetensors.cpp:335 in write_ane_blobs'
+ * loop, core/ane_runtime.cpp:207 per weight) costs a few launches, not one
+ * per tensor.  Tensors whose pointers are not 16-byte aligned get their own
+ * launch.  Bit-identical to anelm_bf16_to_f16 per tensor. */
+int anelm_bf16_to_f16_multi(uint16_t* const* dst, const uint16_t* const* src, const size_t* n, int count,
+                            void* stream);
 /* bf16 -> fp32 (bf16_to_f32_vec, common.h:77-79; used by load_bf16_to_f32,
  * core/safetensors.cpp:266-281). */
 int anelm_bf16_to_f32(float* dst, const uint16_t* src, size_t n, void* stream);

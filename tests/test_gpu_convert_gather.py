@@ -152,3 +152,33 @@ def test_norm_weight_plus1(hip, orc, rng, n):
     dst = torch.empty(n, device="cuda")
     hip.bf16_to_f32_plus1(dst, dev(pats))
     assert_bitexact(host(dst), orc.norm_weight(pats), f"n={n}")
+
+
+def test_convert_many_tensors_one_call(hip, orc, rng):
+    """anelm_bf16_to_f16_multi: 300 tensors (three launches of up to 128),
+    sizes 1 .. 70,000 including tails that are not a multiple of 8, empty
+    tensors, one in place and two not 16-byte aligned (own launches); every
+    output bit-exact, and the bytes between tensors untouched."""
+    import torch
+
+    sizes = [int(x) for x in rng.integers(1, 70_000, 300)]
+    sizes[:6] = [1, 7, 8, 4096, 4097, 0]
+    pad = 64                                      # untouched gap (elements) after each tensor
+    offs = np.cumsum([0] + [((m + 7) // 8) * 8 + pad for m in sizes])
+    bits = rng.integers(0, 65536, int(offs[-1]), dtype=np.uint32).astype(np.uint16)
+    src = dev(bits)
+    out = torch.full((int(offs[-1]),), 0x5A5A, dtype=torch.int16, device="cuda")
+    srcs = [src[o:o + m] for o, m in zip(offs[:-1], sizes)]
+    dsts = [out[o:o + m] for o, m in zip(offs[:-1], sizes)]
+    dsts[10] = srcs[10]                           # in place
+    srcs[20], dsts[20] = src[offs[20] + 1:offs[20] + 1 + sizes[20]], out[offs[20] + 3:offs[20] + 3 + sizes[20]]
+    hip.bf16_to_f16_multi(dsts, srcs)
+    got_out, got_src = host(out), host(src)
+    for i, (o, m) in enumerate(zip(offs[:-1], sizes)):
+        if i == 20:
+            assert_bitexact(got_out[o + 3:o + 3 + m], orc.bf16_to_f16(bits[o + 1:o + 1 + m]), "unaligned tensor")
+            continue
+        ref = orc.bf16_to_f16(bits[o:o + m])
+        assert_bitexact((got_src if i == 10 else got_out)[o:o + m], ref, f"tensor {i} ({m} elements)")
+        if i not in (10, 20):
+            assert np.all(got_out[o + m:int(offs[i + 1])].view(np.uint16) == 0x5A5A), f"gap after tensor {i}"
