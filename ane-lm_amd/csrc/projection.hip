@@ -584,11 +584,15 @@ void f32_fused(const ProjArgs& a, hipStream_t st) {
 // previous fp16 SwiGLU): the decode step past a few rows, where the fp32
 // inputs' extra bytes and per-workgroup rounding cost more than the
 // separate conversion.
+// The SwiGLU past 32 rows takes all 64 batch rows of a workgroup (each
+// gate|up tile read by one workgroup): 9.8 us against 11.8 us with 32 at the
+// Qwen3-0.6B shape and 64 rows; the other shapes measured no better so.
 template <int EPI>
 void x16_fused(const ProjArgs& a, hipStream_t st) {
     const long tiles16 = (long)((a.out_dim + 15) / 16) * ((a.batch + 15) / 16);
     constexpr int RT = is_swiglu(EPI) ? 2 : 1;
     if (a.batch <= 16 || (!is_swiglu(EPI) && tiles16 < 512)) launch_mfma<true, 1, RT, 8, false, EPI>(a, st);
+    else if (is_swiglu(EPI) && a.batch > 32) launch_mfma<true, 4, 2, 4, false, EPI>(a, st);
     else launch_mfma<true, 2, 2, 8, false, EPI>(a, st);
 }
 

@@ -126,7 +126,8 @@ def test_proj_f16_fused_past_16_rows(hip, orc, rng, B, out_dim, in_dim, norm):
     assert np.all(np.abs(host(y).astype(np.float64) - want) <= tol)
 
 
-@pytest.mark.parametrize("B,out_dim,in_dim", [(17, 4096, 1024), (64, 1024, 3072), (3, 1024, 2048), (64, 160, 64)])
+@pytest.mark.parametrize("B,out_dim,in_dim", [(17, 4096, 1024), (64, 1024, 3072), (3, 1024, 2048), (64, 160, 64),
+                                               (40, 512, 256), (100, 2048, 1024)])
 def test_proj_f16_x16_fused_epilogues(hip, orc, rng, B, out_dim, in_dim):
     """fp16 rows in (the fp16 RMSNorm's output), each epilogue: store and
     residual add against the oracle, the SwiGLU in fp32 and rounded to fp16
