@@ -182,3 +182,19 @@ def test_convert_many_tensors_one_call(hip, orc, rng):
         assert_bitexact((got_src if i == 10 else got_out)[o:o + m], ref, f"tensor {i} ({m} elements)")
         if i not in (10, 20):
             assert np.all(got_out[o + m:int(offs[i + 1])].view(np.uint16) == 0x5A5A), f"gap after tensor {i}"
+
+
+@pytest.mark.parametrize("n,offset", [(65536, 0), (8 * 1000, 0), (1, 0), (13, 0), (8 * 777, 2), (3_000_000, 0)])
+@pytest.mark.parametrize("kind", ["f16", "bf16"])
+def test_widen_to_f32(hip, orc, rng, n, offset, kind):
+    """fp16 -> fp32 (common.h:35-56) and bf16 -> fp32 (common.h:21-26): exact,
+    NaN payloads kept; the 8-wide path (aligned, n % 8 == 0) and the
+    element-wise one (ragged or misaligned)."""
+    import torch
+
+    bits = np.arange(65536, dtype=np.uint16) if n == 65536 else rng.integers(0, 65536, n, dtype=np.uint32).astype(np.uint16)
+    src = dev(np.concatenate([np.zeros(offset, np.uint16), bits]))[offset:]
+    dst = torch.empty(n + offset, device="cuda")[offset:]
+    (hip.f16_to_f32 if kind == "f16" else hip.bf16_to_f32)(dst, src)
+    want = orc.f16_to_f32(bits) if kind == "f16" else orc.bf16_to_f32(bits)
+    assert_bitexact(host(dst), want, f"{kind} n={n} offset={offset}")
