@@ -17,7 +17,7 @@
 // partial tiles are summed in LDS in a fixed order.  (Splitting the input
 // dimension over several workgroups per tile, with the last to finish summing
 // the partials behind a device-scope fence, measured 20 us slower per call:
-// the fence writes back the L2.  Small out_dim runs on fewer workgroups.)
+// the fence writes back the L2.)
 //
 // Dot path (one or two rows of x, up to eight for narrow out_dim; in_dim any
 // multiple of 8): one wave per output row, v_dot2_f32_f16 into fp32.
@@ -486,15 +486,13 @@ void launch_mfma(const ProjArgs& a, hipStream_t st) {
 }
 
 // Up to 16 rows: one 16-row batch block, one row tile per workgroup (the
-// most workgroups), 8 steps of loads in flight per wave.  More rows: 32-row
-// batch blocks and two row tiles per workgroup, so each input fetched from
-// cache feeds twice the MFMAs.
-// Past 16 rows, 32-row batch blocks with two row tiles per workgroup (each
-// input fetched from cache feeds four MFMA tiles) where that still leaves
-// enough workgroups; shapes with few output tiles (out_dim 1024 at 64 rows:
-// 64 such workgroups) keep 16x16 tiles and four times the workgroups, which
-// measured 1.6x faster there.  (8 waves per workgroup for the few-tile
-// shapes measured 10% slower than 4.)
+// most workgroups), 8 steps of loads in flight per wave.  Past 16 rows,
+// 32-row batch blocks with two row tiles per workgroup (each input fetched
+// from cache feeds four MFMA tiles) where that still leaves enough
+// workgroups; shapes with few output tiles (out_dim 1024 at 64 rows: 64 such
+// workgroups) keep 16x16 tiles and four times the workgroups, which measured
+// 1.6x faster there.  (8 waves per workgroup for the few-tile shapes
+// measured 10% slower than 4.)
 template <bool XH>
 int proj_mfma(const ProjArgs& a, hipStream_t st) {
     const long tiles16 = (long)((a.out_dim + 15) / 16) * ((a.batch + 15) / 16);
