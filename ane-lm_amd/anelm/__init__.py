@@ -82,6 +82,9 @@ _SIGS = {
     "anelm_l2_normalize": (_I, [_P, _L, _I, _I, _L, _F, _P]),
     "anelm_conv1d_update": (_I, [_P, _P, _P, _P, _P, _L, _I, _I, _L, _L, _L, _P]),
     "anelm_ssm_step": (_I, [_P, _P, _P, _P, _P, _P, _P, _L, _I, _I, _I, _I, _L, _L, _L, _L, _P]),
+    "anelm_ssm_step_gated_norm": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _L, _I, _I, _I, _I, _L, _L, _L, _L,
+                                       _L, _F, _P]),
+    "anelm_conv1d_silu_l2norm": (_I, [_P, _P, _P, _P, _P, _L, _I, _I, _L, _L, _L, _F, _P]),
     "anelm_matvec": (_I, [_P, _P, _P, _L, _I, _P]),
     "anelm_st_open": (_P, [ctypes.c_char_p]),
     "anelm_st_close": (None, [_P]),
@@ -414,6 +417,27 @@ def ssm_step(y, state, q, k, v, decay, beta, n_key_heads, stream=None):
     _need(q.stride() == k.stride() and decay.is_contiguous() and beta.is_contiguous(), "ssm_step: layouts")
     _check(lib().anelm_ssm_step(_ptr(y), _ptr(state), _ptr(q), _ptr(k), _ptr(v), _ptr(decay), _ptr(beta), B, nh,
                                 n_key_heads, kd, vd, _ld(q), _ld(v), _ld(y), state.stride(0), _stream(stream)))
+
+
+def ssm_step_gated_norm(out, state, q, k, v, decay, beta, z, norm_w, n_key_heads, eps=1e-6, stream=None):
+    """ssm_step, then rmsnorm_gated of each head's y with gate z and weight
+    norm_w ([value_dim]); out, z: [B, n_heads*value_dim]."""
+    B, nh, kd, vd = state.shape
+    _need(state.stride(3) == 1 and state.stride(2) == vd and state.stride(1) == kd * vd, "ssm_step: state layout")
+    _need(q.stride() == k.stride() and decay.is_contiguous() and beta.is_contiguous(), "ssm_step: layouts")
+    _check(lib().anelm_ssm_step_gated_norm(_ptr(out), _ptr(state), _ptr(q), _ptr(k), _ptr(v), _ptr(decay), _ptr(beta),
+                                           _ptr(z), _ptr(norm_w), _dtype_code(norm_w), B, nh, n_key_heads, kd, vd, _ld(q),
+                                           _ld(v), _ld(z), _ld(out), state.stride(0), eps, _stream(stream)))
+
+
+def conv1d_silu_l2norm(y, conv_state, state_pos, x, w, n_key_heads, q_scale, stream=None):
+    """conv1d_update (kernel size 4), SiLU and the q/k L2 normalisation of the
+    decode step; channels [q heads | k heads | v], key heads of 128."""
+    B, ch, sl = conv_state.shape
+    _need(sl == 3 and w.shape == (ch, 4) and w.is_contiguous() and conv_state.stride(2) == 1 and
+          conv_state.stride(1) == sl, "conv1d_silu_l2norm: shapes")
+    _check(lib().anelm_conv1d_silu_l2norm(_ptr(y), _ptr(conv_state), _ptr(state_pos), _ptr(x), _ptr(w), B, ch,
+                                          n_key_heads, _ld(x), _ld(y), conv_state.stride(0), q_scale, _stream(stream)))
 
 
 def matvec(y, W, x, stream=None):

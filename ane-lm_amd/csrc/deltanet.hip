@@ -124,6 +124,59 @@ __global__ __launch_bounds__(1024) void conv1d_update_kernel(float* y, float* st
     if (threadIdx.x == 0) state_pos[b] = pos + 1 == state_len ? 0 : pos + 1;
 }
 
+// ---------------------------------------- conv1d + SiLU + q/k L2 normalise
+// The decode step's qwen3_5.cpp:513-531 for kernel size 4 and 128-wide key
+// heads, one workgroup per sequence: channels are [q heads | k heads | v],
+// each q/k head 128 channels.  Wave w takes the 128-channel blocks w, w+16,
+// ...; lane l computes channels 128*blk + l and 128*blk + 64 + l, so every
+// value is produced by the same operations in the same order as
+// anelm_conv1d_update, anelm_silu and anelm_l2_normalize (whose wave per
+// head sums element l, then l + 64, in lane l) produce it one after the other.
+__device__ __forceinline__ float conv4(const float* st, int pos, int i1, int i2, float xc, float4 wc, long c) {
+    const float* sc = st + c * 3;
+    const float sum = fmaf(sc[i2], wc.z, fmaf(sc[i1], wc.y, fmaf(sc[pos], wc.x, 0.0f)));
+    return fmaf(xc, wc.w, sum);
+}
+
+__global__ __launch_bounds__(1024) void conv_silu_l2_kernel(float* y, float* state, int32_t* state_pos, const float* x,
+                                                            const float* w, int channels, int nq_ch, long ld_x,
+                                                            long ld_y, long state_stride, float q_scale) {
+    const long b = blockIdx.x;
+    int pos = state_pos[b];
+    pos = pos < 0 ? 0 : (pos >= 3 ? 0 : pos);   // keeps every access in the ring
+    const int i1 = pos + 1 == 3 ? 0 : pos + 1;
+    const int i2 = i1 + 1 == 3 ? 0 : i1 + 1;
+    float* st = state + b * state_stride;
+    const float* xb = x + b * ld_x;
+    float* yb = y + b * ld_y;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    for (int blk = wv; blk < channels / 128; blk += nw) {   // uniform within the wave
+        const long c0 = (long)blk * 128 + lane, c1 = c0 + 64;
+        const float x0 = xb[c0], x1 = xb[c1];
+        const float4 w0 = *reinterpret_cast<const float4*>(w + c0 * 4);
+        const float4 w1 = *reinterpret_cast<const float4*>(w + c1 * 4);
+        float y0 = conv4(st, pos, i1, i2, x0, w0, c0);
+        float y1 = conv4(st, pos, i1, i2, x1, w1, c1);
+        st[c0 * 3 + pos] = x0;
+        st[c1 * 3 + pos] = x1;
+        y0 = y0 / (expf(-y0) + 1.0f);   // SiLU, qwen3_5.cpp:514
+        y1 = y1 / (expf(-y1) + 1.0f);
+        if (blk * 128 < 2 * nq_ch) {      // a q or k head: L2 normalise (x scale)
+            float ss = fmaf(y0, y0, 0.0f);
+            ss = fmaf(y1, y1, ss);
+            ss = wave_sum(ss);
+            const float norm = 1.0f / sqrtf(ss + 1e-12f);
+            const float scale = blk * 128 < nq_ch ? q_scale : 1.0f;
+            y0 = (y0 * norm) * scale;
+            y1 = (y1 * norm) * scale;
+        }
+        yb[c0] = y0;
+        yb[c1] = y1;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) state_pos[b] = pos + 1 == 3 ? 0 : pos + 1;
+}
+
 // ------------------------------------------------------------ delta-rule step
 // core/cpu_ops.cpp:152-171 for one (sequence, value head) per workgroup:
 //   Sk = S^T k;  delta = v - Sk;  S = decay*S + beta*k*delta^T;  y = S^T q.
@@ -140,9 +193,19 @@ struct SsmArgs {
     const float* beta;    // [batch * nvh]
     int nvh, nkh;         // value heads, key heads (value head h uses key head h / (nvh/nkh))
     long ld_qk, ld_v, ld_y, state_stride;  // per-sequence strides
+    // gated RMSNorm epilogue (GATED): out = rmsnorm(y)*w / (1 + expf(-z)) * z
+    const float* z;
+    const void* nw;
+    float* out;
+    long ld_z, ld_out;
+    float eps;
 };
 
-template <int KD, int VD>
+// With GATED the head's y is not stored: the epilogue applies
+// anelm_rmsnorm_gated to it (qwen3_5.cpp:545-549) with that kernel's
+// operations in its order (wave 0, lane l: elements l, l+64, ...) and stores
+// the result.
+template <int KD, int VD, int GATED = -1>
 __global__ __launch_bounds__(256) void ssm_step_kernel(SsmArgs a) {
     constexpr int CG = VD / 4;          // column groups
     constexpr int RG = 256 / CG;        // row groups
@@ -207,12 +270,36 @@ __global__ __launch_bounds__(256) void ssm_step_kernel(SsmArgs a) {
     }
     *reinterpret_cast<float4*>(&red[rg][4 * cg]) = p;   // red was last read before the previous barrier
     __syncthreads();
-    float* yp = a.y + b * a.ld_y + (long)vh * VD;
-    for (int j = tid; j < VD; j += 256) {
-        float t = red[0][j];
+    if constexpr (GATED < 0) {
+        float* yp = a.y + b * a.ld_y + (long)vh * VD;
+        for (int j = tid; j < VD; j += 256) {
+            float t = red[0][j];
 #pragma unroll
-        for (int g = 1; g < RG; g++) t += red[g][j];
-        yp[j] = t;
+            for (int g = 1; g < RG; g++) t += red[g][j];
+            yp[j] = t;
+        }
+    } else {
+        for (int j = tid; j < VD; j += 256) {   // y into sdelta (last read before the previous barrier)
+            float t = red[0][j];
+#pragma unroll
+            for (int g = 1; g < RG; g++) t += red[g][j];
+            sdelta[j] = t;
+        }
+        __syncthreads();
+        if (tid < kWave) {
+            float ss = 0.0f;
+            for (int i = tid; i < VD; i += kWave) ss = fmaf(sdelta[i], sdelta[i], ss);
+            ss = wave_sum(ss);
+            const float sc = 1.0f / sqrtf(ss / (float)VD + a.eps);
+            const float* zr = a.z + b * a.ld_z + (long)vh * VD;
+            float* orow = a.out + b * a.ld_out + (long)vh * VD;
+            for (int i = tid; i < VD; i += kWave) {
+                float o = (sdelta[i] * sc) * load_w<GATED>(a.nw, i);
+                const float zi = zr[i];
+                o = o / (1.0f + expf(-zi));
+                orow[i] = o * zi;
+            }
+        }
     }
 }
 
@@ -256,8 +343,42 @@ __global__ __launch_bounds__(kRowThreads) void matvec_kernel(float* y, const flo
 long row_blocks(long rows) { return (rows + kRowThreads / kWave - 1) / (kRowThreads / kWave); }
 
 template <int KD, int VD>
-void launch_ssm(const SsmArgs& a, long n, hipStream_t st) {
-    hipLaunchKernelGGL((ssm_step_kernel<KD, VD>), dim3(n), dim3(256), 0, st, a);
+void launch_ssm(const SsmArgs& a, long n, hipStream_t st, int gated_dtype = -1) {
+    switch (gated_dtype) {
+        case -1: hipLaunchKernelGGL((ssm_step_kernel<KD, VD>), dim3(n), dim3(256), 0, st, a); break;
+        case ANELM_F32: hipLaunchKernelGGL((ssm_step_kernel<KD, VD, ANELM_F32>), dim3(n), dim3(256), 0, st, a); break;
+        case ANELM_F16: hipLaunchKernelGGL((ssm_step_kernel<KD, VD, ANELM_F16>), dim3(n), dim3(256), 0, st, a); break;
+        default: hipLaunchKernelGGL((ssm_step_kernel<KD, VD, ANELM_BF16>), dim3(n), dim3(256), 0, st, a); break;
+    }
+}
+
+int ssm_check(const char* fn, long batch, int n_heads, int n_key_heads, int key_dim, int value_dim, long ld_qk,
+              long ld_v, long ld_y, long state_stride, const float* state) {
+    if (batch < 0 || n_heads <= 0 || n_key_heads <= 0 || n_heads % n_key_heads)
+        return fail(ANELM_ERR_INVALID, "%s: n_heads must be a positive multiple of n_key_heads", fn);
+    const bool kd_ok = key_dim == 64 || key_dim == 128 || key_dim == 256;
+    if (!kd_ok || (value_dim != 64 && value_dim != 128))
+        return fail(ANELM_ERR_INVALID, "%s: key_dim %d / value_dim %d (64/128/256 and 64/128)", fn, key_dim, value_dim);
+    if (batch > 1 && (ld_qk < (long)n_key_heads * key_dim || ld_v < (long)n_heads * value_dim ||
+                      ld_y < (long)n_heads * value_dim || state_stride < (long)n_heads * key_dim * value_dim))
+        return fail(ANELM_ERR_INVALID, "%s: strides overlap", fn);
+    if (!aligned16(state) || (state_stride & 3)) return fail(ANELM_ERR_INVALID, "%s: state not 16-byte aligned", fn);
+    return ANELM_OK;
+}
+
+int ssm_launch(const SsmArgs& a, long batch, int n_heads, int key_dim, int value_dim, int gated_dtype,
+               hipStream_t st) {
+    const long n = batch * n_heads;
+    if (value_dim == 128) {
+        if (key_dim == 64) launch_ssm<64, 128>(a, n, st, gated_dtype);
+        else if (key_dim == 128) launch_ssm<128, 128>(a, n, st, gated_dtype);
+        else launch_ssm<256, 128>(a, n, st, gated_dtype);
+    } else {
+        if (key_dim == 64) launch_ssm<64, 64>(a, n, st, gated_dtype);
+        else if (key_dim == 128) launch_ssm<128, 64>(a, n, st, gated_dtype);
+        else launch_ssm<256, 64>(a, n, st, gated_dtype);
+    }
+    return launch_status("ssm_step");
 }
 
 }  // namespace
@@ -319,29 +440,54 @@ extern "C" int anelm_ssm_step(float* y, float* state, const float* q, const floa
                               void* stream) {
     clear_error();
     if (!y || !state || !q || !k || !v || !decay || !beta) return fail(ANELM_ERR_INVALID, "ssm_step: null pointer");
-    if (batch < 0 || n_heads <= 0 || n_key_heads <= 0 || n_heads % n_key_heads)
-        return fail(ANELM_ERR_INVALID, "ssm_step: n_heads must be a positive multiple of n_key_heads");
-    const bool kd_ok = key_dim == 64 || key_dim == 128 || key_dim == 256;
-    if (!kd_ok || (value_dim != 64 && value_dim != 128))
-        return fail(ANELM_ERR_INVALID, "ssm_step: key_dim %d / value_dim %d (64/128/256 and 64/128)", key_dim, value_dim);
-    if (batch > 1 && (ld_qk < (long)n_key_heads * key_dim || ld_v < (long)n_heads * value_dim ||
-                      ld_y < (long)n_heads * value_dim || state_stride < (long)n_heads * key_dim * value_dim))
-        return fail(ANELM_ERR_INVALID, "ssm_step: strides overlap");
-    if (!aligned16(state) || (state_stride & 3)) return fail(ANELM_ERR_INVALID, "ssm_step: state not 16-byte aligned");
+    int rc = ssm_check("ssm_step", batch, n_heads, n_key_heads, key_dim, value_dim, ld_qk, ld_v, ld_y, state_stride,
+                       state);
+    if (rc) return rc;
     if (batch == 0) return ANELM_OK;
-    SsmArgs a{y, state, q, k, v, decay, beta, n_heads, n_key_heads, ld_qk, ld_v, ld_y, state_stride};
-    const long n = batch * n_heads;
-    hipStream_t st = as_stream(stream);
-    if (value_dim == 128) {
-        if (key_dim == 64) launch_ssm<64, 128>(a, n, st);
-        else if (key_dim == 128) launch_ssm<128, 128>(a, n, st);
-        else launch_ssm<256, 128>(a, n, st);
-    } else {
-        if (key_dim == 64) launch_ssm<64, 64>(a, n, st);
-        else if (key_dim == 128) launch_ssm<128, 64>(a, n, st);
-        else launch_ssm<256, 64>(a, n, st);
-    }
-    return launch_status("ssm_step");
+    SsmArgs a{};
+    a.y = y; a.state = state; a.q = q; a.k = k; a.v = v; a.decay = decay; a.beta = beta;
+    a.nvh = n_heads; a.nkh = n_key_heads; a.ld_qk = ld_qk; a.ld_v = ld_v; a.ld_y = ld_y; a.state_stride = state_stride;
+    return ssm_launch(a, batch, n_heads, key_dim, value_dim, -1, as_stream(stream));
+}
+
+extern "C" int anelm_ssm_step_gated_norm(float* out, float* state, const float* q, const float* k, const float* v,
+                                         const float* decay, const float* beta, const float* z, const void* norm_w,
+                                         int w_dtype, long batch, int n_heads, int n_key_heads, int key_dim,
+                                         int value_dim, long ld_qk, long ld_v, long ld_z, long ld_out,
+                                         long state_stride, float eps, void* stream) {
+    clear_error();
+    if (!out || !state || !q || !k || !v || !decay || !beta || !z || !norm_w)
+        return fail(ANELM_ERR_INVALID, "ssm_step_gated_norm: null pointer");
+    if (w_dtype != ANELM_F32 && w_dtype != ANELM_F16 && w_dtype != ANELM_BF16)
+        return fail(ANELM_ERR_INVALID, "ssm_step_gated_norm: weight dtype %d", w_dtype);
+    int rc = ssm_check("ssm_step_gated_norm", batch, n_heads, n_key_heads, key_dim, value_dim, ld_qk, ld_v, ld_out,
+                       state_stride, state);
+    if (rc) return rc;
+    if (batch > 1 && ld_z < (long)n_heads * value_dim)
+        return fail(ANELM_ERR_INVALID, "ssm_step_gated_norm: strides overlap");
+    if (batch == 0) return ANELM_OK;
+    SsmArgs a{};
+    a.state = state; a.q = q; a.k = k; a.v = v; a.decay = decay; a.beta = beta;
+    a.nvh = n_heads; a.nkh = n_key_heads; a.ld_qk = ld_qk; a.ld_v = ld_v; a.state_stride = state_stride;
+    a.z = z; a.nw = norm_w; a.out = out; a.ld_z = ld_z; a.ld_out = ld_out; a.eps = eps;
+    return ssm_launch(a, batch, n_heads, key_dim, value_dim, w_dtype, as_stream(stream));
+}
+
+extern "C" int anelm_conv1d_silu_l2norm(float* y, float* conv_state, int32_t* state_pos, const float* x,
+                                        const float* w, long batch, int channels, int n_key_heads, long ld_x,
+                                        long ld_y, long state_stride, float q_scale, void* stream) {
+    clear_error();
+    if (!y || !conv_state || !state_pos || !x || !w) return fail(ANELM_ERR_INVALID, "conv1d_silu_l2norm: null pointer");
+    if (batch < 0 || channels <= 0 || channels % 128 || n_key_heads < 0 || 2L * n_key_heads * 128 > channels)
+        return fail(ANELM_ERR_INVALID, "conv1d_silu_l2norm: channels a multiple of 128 holding 2*n_key_heads heads");
+    if (batch > 1 && (ld_x < channels || ld_y < channels || state_stride < (long)channels * 3))
+        return fail(ANELM_ERR_INVALID, "conv1d_silu_l2norm: strides overlap");
+    if (!aligned16(w)) return fail(ANELM_ERR_INVALID, "conv1d_silu_l2norm: w not 16-byte aligned");
+    if (batch == 0) return ANELM_OK;
+    const int waves = channels / 128 < 16 ? channels / 128 : 16;
+    hipLaunchKernelGGL(conv_silu_l2_kernel, dim3(batch), dim3(64 * waves), 0, as_stream(stream), y, conv_state,
+                       state_pos, x, w, channels, n_key_heads * 128, ld_x, ld_y, state_stride, q_scale);
+    return launch_status("conv1d_silu_l2norm");
 }
 
 extern "C" int anelm_matvec(float* y, const float* W, const float* x, long out_dim, int in_dim, void* stream) {

@@ -336,7 +336,8 @@ def measure_deltanet(hip, w, steps, layers=8):
     """One decode step of the linear-attention layer ops (qwen3_5.cpp:513-549:
     conv1d_update, SiLU, L2-normalised and scaled q, L2-normalised k, the
     delta-rule step, gated RMSNorm) over `layers` distinct layers' states,
-    graph-replayed; plus the state step alone."""
+    graph-replayed: through the two fused calls and as six separate calls;
+    plus the state step alone."""
     import torch
 
     B, nvh, nkh, kd, vd, K = w["B"], w["nvh"], w["nkh"], w["kd"], w["vd"], w["K"]
@@ -353,7 +354,7 @@ def measure_deltanet(hip, w, steps, layers=8):
     out = torch.empty(B, nvh * vd, device="cuda")
     qs = float(1.0 / (kd ** 0.5))
 
-    def layer(L):
+    def layer_separate(L):
         hip.conv1d_update(mixed, L["conv"], L["pos"], x, L["cw"])               # :513
         hip.silu(mixed)                                                         # :514
         hip.l2_normalize(mixed[:, :nkh * kd], qs, heads=nkh)                     # :528, :530-531
@@ -362,20 +363,31 @@ def measure_deltanet(hip, w, steps, layers=8):
                      L["decay"], L["beta"], nkh)                                # :533-542
         hip.rmsnorm_gated(out, y, z, L["nw"], heads=nvh)                         # :545-549
 
+    def layer(L):   # the same in two launches
+        hip.conv1d_silu_l2norm(mixed, L["conv"], L["pos"], x, L["cw"], nkh, qs)  # :513-531
+        hip.ssm_step_gated_norm(out, L["S"], mixed[:, :nkh * kd], mixed[:, nkh * kd:2 * nkh * kd],
+                                mixed[:, 2 * nkh * kd:], L["decay"], L["beta"], z, L["nw"], nkh)  # :533-549
+
     gr = capture(lambda: [layer(L) for L in lay])
     gr.replay()
     ms = time_region(gr.replay, steps) / layers
+    g6 = capture(lambda: [layer_separate(L) for L in lay])
+    g6.replay()
+    ms6 = time_region(g6.replay, steps) / layers
     gs = capture(lambda: [hip.ssm_step(y, L["S"], mixed[:, :nkh * kd], mixed[:, nkh * kd:2 * nkh * kd],
                                        mixed[:, 2 * nkh * kd:], L["decay"], L["beta"], nkh) for L in lay])
     gs.replay()
     ms_s = time_region(gs.replay, steps) / layers
     b = dn_bytes(w)
-    del lay, gr, gs
+    del lay, gr, gs, g6
     torch.cuda.empty_cache()
     f = lambda byt, ms: dict(us=round(ms * 1e3, 2), GBps=round(byt / ms / 1e6, 1),
                              frac=round(byt / ms / 1e6 / HBM_PEAK_GBPS, 4), bytes=byt)
-    return dict(layer=dict(f(b["layer"], ms), tokens_per_s=round(B / (ms / 1e3), 1)), ssm_step=f(b["ssm_step"], ms_s),
-                note="per layer; algorithmic bytes = delta-rule states read+written once, conv rings, activations")
+    return dict(layer=dict(f(b["layer"], ms), tokens_per_s=round(B / (ms / 1e3), 1)),
+                layer_six_calls=f(b["layer"], ms6), ssm_step=f(b["ssm_step"], ms_s),
+                note="per layer; algorithmic bytes = delta-rule states read+written once, conv rings, activations; "
+                     "layer = anelm_conv1d_silu_l2norm + anelm_ssm_step_gated_norm, layer_six_calls = the six "
+                     "separate ops")
 
 
 def cpu_attention(w, target_s):

@@ -312,6 +312,18 @@ int anelm_conv1d_update(float* y, float* conv_state, int32_t* state_pos, const f
                         long batch, int channels, int kernel_size, long ld_x, long ld_y, long state_stride,
                         void* stream);
 
+/* The decode step's conv1d update, SiLU and q/k L2 normalisation in one
+ * launch (models/llm/qwen3_5.cpp:513-531; kernel size 4, 128-wide key heads):
+ * anelm_conv1d_update, then anelm_silu over all channels, then
+ * anelm_l2_normalize of the n_key_heads q heads (channels [0, 128*nkh), times
+ * q_scale) and of the k heads (the next 128*nkh channels, scale 1).  Each
+ * output is bit-identical to the three calls'.  channels a multiple of 128;
+ * w 16-byte aligned.  No counterpart in the reference, which runs the steps
+ * one after the other. */
+int anelm_conv1d_silu_l2norm(float* y, float* conv_state, int32_t* state_pos, const float* x, const float* w,
+                             long batch, int channels, int n_key_heads, long ld_x, long ld_y, long state_stride,
+                             float q_scale, void* stream);
+
 /* Delta-rule state step (ane_lm::ssm_step, core/cpu_ops.cpp:152-171,
  * cpu_ops.h:49-50) for `batch` sequences x n_heads value heads: head h of
  * sequence b has state + b*state_stride + h*key_dim*value_dim
@@ -324,6 +336,15 @@ int anelm_ssm_step(float* y, float* state, const float* q, const float* k, const
                    const float* decay, const float* beta, long batch, int n_heads, int n_key_heads,
                    int key_dim, int value_dim, long ld_qk, long ld_v, long ld_y, long state_stride,
                    void* stream);
+/* anelm_ssm_step with anelm_rmsnorm_gated applied to each head's y
+ * (models/llm/qwen3_5.cpp:545-549, gate z at z + b*ld_z + h*value_dim, weight
+ * norm_w [value_dim] of w_dtype) before it is stored: out = rmsnorm(y)*w,
+ * then out/(1 + expf(-z)), then out*z, bit-identical to the two calls; y
+ * itself is not stored.  No counterpart in the reference. */
+int anelm_ssm_step_gated_norm(float* out, float* state, const float* q, const float* k, const float* v,
+                              const float* decay, const float* beta, const float* z, const void* norm_w, int w_dtype,
+                              long batch, int n_heads, int n_key_heads, int key_dim, int value_dim, long ld_qk,
+                              long ld_v, long ld_z, long ld_out, long state_stride, float eps, void* stream);
 
 /* y = W x, W [out_dim, in_dim] row-major fp32 (ane_lm::matvec,
  * core/cpu_ops.cpp:100-103, cpu_ops.h:37; the reference's CPU LM head and

@@ -144,3 +144,59 @@ def test_head_slices_of_fused_rows(hip, orc, rng):
     ref = np.stack([np.concatenate([orc.rmsnorm_gated(y[b, h * vd:(h + 1) * vd], z[b, h * vd:(h + 1) * vd], w)
                                     for h in range(nvh)]) for b in range(B)])
     assert max_rel_err(host(out), ref) <= REL_TOL
+
+
+@pytest.mark.parametrize("B,nkh,nvh,steps", [(1, 16, 16, 5), (64, 16, 16, 4), (3, 2, 4, 7), (2, 0, 3, 2)])
+def test_conv_silu_l2norm_matches_separate_calls(hip, rng, B, nkh, nvh, steps):
+    """The fused conv1d update + SiLU + q/k L2 norm equals anelm_conv1d_update,
+    anelm_silu and two anelm_l2_normalize calls bit for bit (outputs, ring
+    states and positions), over several steps so the ring wraps."""
+    import torch
+
+    ch = (2 * nkh + nvh) * 128
+    qs = float(1.0 / np.sqrt(128.0))
+    w = dev((0.5 * rng.standard_normal((ch, 4))).astype(np.float32))
+    st0 = rng.standard_normal((B, ch, 3)).astype(np.float32)
+    pos0 = rng.integers(-1, 4, B).astype(np.int32)        # out-of-range positions are taken as 0
+    sa, pa, sb, pb = dev(st0), dev(pos0), dev(st0), dev(pos0)
+    for _ in range(steps):
+        x = dev((2 * rng.standard_normal((B, ch))).astype(np.float32))
+        ya = torch.empty(B, ch, device="cuda")
+        hip.conv1d_update(ya, sa, pa, x, w)
+        hip.silu(ya)
+        if nkh:
+            hip.l2_normalize(ya[:, :nkh * 128], qs, heads=nkh)
+            hip.l2_normalize(ya[:, nkh * 128:2 * nkh * 128], 1.0, heads=nkh)
+        yb = torch.empty(B, ch, device="cuda")
+        hip.conv1d_silu_l2norm(yb, sb, pb, x, w, nkh, qs)
+        assert_bitexact(host(yb), host(ya), "outputs")
+        assert_bitexact(host(sb), host(sa), "conv states")
+        assert np.array_equal(host(pb), host(pa))
+
+
+@pytest.mark.parametrize("B,nvh,nkh,kd,vd,wdt", [(64, 16, 16, 128, 128, "f32"), (1, 16, 16, 128, 128, "bf16"),
+                                                 (3, 8, 2, 64, 64, "f16"), (2, 4, 4, 256, 128, "f32")])
+def test_ssm_step_gated_norm_matches_separate_calls(hip, rng, B, nvh, nkh, kd, vd, wdt):
+    """The state step with the gated RMSNorm fused in equals anelm_ssm_step
+    then anelm_rmsnorm_gated bit for bit (outputs and states)."""
+    import torch
+
+    S0 = (0.05 * rng.standard_normal((B, nvh, kd, vd))).astype(np.float32)
+    q = dev(rng.standard_normal((B, nkh * kd)).astype(np.float32))
+    k = dev(rng.standard_normal((B, nkh * kd)).astype(np.float32))
+    v = dev(rng.standard_normal((B, nvh * vd)).astype(np.float32))
+    z = dev((2 * rng.standard_normal((B, nvh * vd))).astype(np.float32))
+    decay = dev(rng.uniform(0.5, 1.0, (B, nvh)).astype(np.float32))
+    beta = dev(rng.uniform(0.0, 1.0, (B, nvh)).astype(np.float32))
+    w32 = (1 + 0.1 * rng.standard_normal(vd)).astype(np.float32)
+    nw = {"f32": torch.from_numpy(w32), "f16": torch.from_numpy(w32).half(),
+          "bf16": torch.from_numpy(w32).bfloat16()}[wdt].cuda()
+    Sa, Sb = dev(S0), dev(S0)
+    y = torch.empty(B, nvh * vd, device="cuda")
+    outa = torch.empty(B, nvh * vd, device="cuda")
+    hip.ssm_step(y, Sa, q, k, v, decay, beta, nkh)
+    hip.rmsnorm_gated(outa, y, z, nw, heads=nvh)
+    outb = torch.full((B, nvh * vd), float("nan"), device="cuda")
+    hip.ssm_step_gated_norm(outb, Sb, q, k, v, decay, beta, z, nw, nkh)
+    assert_bitexact(host(outb), host(outa), "gated outputs")
+    assert_bitexact(host(Sb), host(Sa), "states")
