@@ -213,8 +213,8 @@ def measure_chain(w, steps, warmup, per_op):
 
 
 def measure_sampler(hip, steps, rows=64, vocab=VOCAB, freq=0.1):
-    """Logits [64, 151936] ~N(0,3), history [64, 256], rep 1.2, T 0.6, freq
-    0.1 (the reference default) or as given."""
+    """Logits [rows, 151936] ~N(0,3), history [rows, 256], rep 1.2, T 0.6,
+    freq 0.1 (the reference default) or as given."""
     import torch
 
     g = torch.Generator(device="cuda").manual_seed(21)
@@ -833,6 +833,8 @@ def main():
         elif args.only == "sampling-64x151936":
             r = measure_sampler(anelm, max(args.steps, 20))
             r["frequency_penalty_0"] = measure_sampler(anelm, max(args.steps, 20), freq=0.0)
+        elif args.only == "sampling-1x151936":
+            r = measure_sampler(anelm, max(args.steps, 20), rows=1)
         elif args.only == "convert-qwen3-8b-bf16":
             r = measure_convert(anelm)
         elif args.only in Q3_WORKLOADS:
@@ -875,6 +877,8 @@ def main():
         configs["sampling-64x151936"] = measure_sampler(anelm, max(args.steps, 20))
         configs["sampling-64x151936"]["frequency_penalty_0"] = {
             k: v for k, v in measure_sampler(anelm, max(args.steps, 20), freq=0.0).items() if k != "note"}
+        # one row: what the reference samples per decode step (generate.cpp:80-129)
+        configs["sampling-1x151936"] = measure_sampler(anelm, max(args.steps, 20), rows=1)
         for name, aw in ATTN_WORKLOADS.items():
             configs[name] = measure_attention(anelm, aw, max(args.steps, 20))
         for name, dw in DN_WORKLOADS.items():
@@ -902,6 +906,7 @@ def main():
             cpu_configs["sampling-64x151936"] = cpu_sampler(1.5)
             cpu_configs["sampling-64x151936"]["frequency_penalty_0"] = {
                 k: v for k, v in cpu_sampler(1.0, freq=0.0).items() if k in ("us", "GBps")}
+            cpu_configs["sampling-1x151936"] = cpu_sampler(0.5, rows=1)
             cpu_configs["attention-qwen3-8b-decode"] = cpu_attention(ATTN_WORKLOADS["attention-qwen3-8b-decode-b1"], 1.5)
             cpu_configs["convert-qwen3-8b-bf16"] = cpu_convert(1.5)
     out = {
