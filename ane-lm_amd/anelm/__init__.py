@@ -473,8 +473,10 @@ class SafeTensorsFile:
     def __len__(self):
         return lib().anelm_st_count(self._h)
 
+    # names are the raw bytes between the header's quotes (not necessarily
+    # UTF-8); surrogateescape carries any byte through str and back
     def find(self, name):
-        return lib().anelm_st_find(self._h, name.encode())
+        return lib().anelm_st_find(self._h, name.encode("utf-8", "surrogateescape"))
 
     def info(self, i):
         name, dt, nd = ctypes.c_char_p(), _I(), _I()
@@ -482,7 +484,7 @@ class SafeTensorsFile:
         off, nb = ctypes.c_uint64(), ctypes.c_uint64()
         _check(lib().anelm_st_info(self._h, i, ctypes.byref(name), ctypes.byref(dt), ctypes.byref(nd), shape,
                                    ctypes.byref(off), ctypes.byref(nb)))
-        return name.value.decode(), dt.value, tuple(shape[:nd.value]), off.value, nb.value
+        return name.value.decode("utf-8", "surrogateescape"), dt.value, tuple(shape[:nd.value]), off.value, nb.value
 
     def host_data(self, i):
         return lib().anelm_st_host_data(self._h, i)

@@ -304,7 +304,10 @@ extern "C" anelm_st* anelm_st_open(const char* path) {
                 break;
             }
             const int es = dtype_size(t.dtype);
-            if (t.offset + t.nbytes > h->data_size || (es && (uint64_t)t.numel * es != t.nbytes)) {
+            // (numel * es could wrap; offset + nbytes = the end offset <= INT64_MAX cannot)
+            const bool size_ok =
+                !es || (t.nbytes % (uint64_t)es == 0 && (uint64_t)t.numel == t.nbytes / (uint64_t)es);
+            if (t.offset + t.nbytes > h->data_size || !size_ok) {
                 fail(ANELM_ERR_INVALID, "st_open: tensor %s: data_offsets and shape disagree or leave the file",
                      t.name.c_str());
                 delete h;

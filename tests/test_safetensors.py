@@ -118,3 +118,81 @@ def test_blob_header_layout(orc, n):
 
 def test_blob_paths(orc):
     assert orc.blob_relpath("model.layers.0.mlp.gate_proj.weight") == "model/layers/0/mlp/gate_proj/weight.bin"
+
+
+_SIZES = {"BF16": 2, "F16": 2, "F32": 4, "F64": 8, "I32": 4, "I64": 8, "U8": 1}
+
+
+def _check_open(path):
+    """Open a possibly malformed file: either an AnelmError, or a handle whose
+    every tensor lies inside the data block with bytes = numel x dtype size."""
+    import anelm
+
+    raw = path.read_bytes()
+    try:
+        f = anelm.SafeTensorsFile(path)
+    except anelm.AnelmError:
+        return False
+    with f:
+        hlen = struct.unpack("<Q", raw[:8])[0]
+        data = len(raw) - 8 - hlen
+        assert data >= 0
+        for i in range(len(f)):
+            name, dt, shape, off, nb = f.info(i)
+            assert off + nb <= data, (name, off, nb, data)
+            assert all(d >= 0 for d in shape)
+            size = {anelm.BF16: 2, anelm.F16: 2, anelm.F32: 4, anelm.ST_F64: 8, anelm.ST_I32: 4, anelm.ST_I64: 8,
+                    anelm.ST_U8: 1}.get(dt)
+            if size is not None:
+                assert int(np.prod(shape, dtype=np.int64)) * size == nb, (name, shape, nb)
+    return True
+
+
+def test_fuzz_mutated_and_truncated_files(tmp_path, rng):
+    """Byte mutations inside the header, length-field changes and
+    truncations of a valid file never crash the parser, and whatever it
+    accepts is consistent (no tensor outside the data block)."""
+    p = tmp_path / "m.safetensors"
+    make_file(p, rng)
+    good = p.read_bytes()
+    hlen = struct.unpack("<Q", good[:8])[0]
+    q = tmp_path / "fuzz.safetensors"
+    accepted = 0
+    for trial in range(400):
+        b = bytearray(good)
+        kind = trial % 4
+        if kind == 0:      # flip bytes inside the JSON header
+            for _ in range(int(rng.integers(1, 4))):
+                b[8 + int(rng.integers(0, hlen))] = int(rng.integers(0, 256))
+        elif kind == 1:    # digits changed: offsets and shapes
+            digits = [i for i in range(8, 8 + hlen) if chr(b[i]).isdigit()]
+            for _ in range(int(rng.integers(1, 3))):
+                b[digits[int(rng.integers(0, len(digits)))]] = ord(str(int(rng.integers(0, 10))))
+        elif kind == 2:    # the header length field
+            b[:8] = struct.pack("<Q", int(rng.integers(0, len(good) + 64)))
+        else:              # truncation
+            b = b[:int(rng.integers(0, len(good)))]
+        q.write_bytes(bytes(b))
+        accepted += _check_open(q)
+    assert accepted > 0   # some mutations (e.g. inside names) stay valid
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_fuzz_random_headers(tmp_path, seed):
+    """Structured random headers: unknown dtypes, negative, zero and huge
+    dimensions, offsets out of order, overlapping or past the end, odd
+    metadata."""
+    r = np.random.default_rng(100 + seed)
+    q = tmp_path / "h.safetensors"
+    for _ in range(60):
+        hdr = {}
+        for t in range(int(r.integers(0, 5))):
+            dt = str(r.choice(["BF16", "F16", "F32", "F64", "I32", "I64", "U8", "BOOL", "F8_E4M3", ""]))
+            shape = [int(x) for x in r.choice([0, 1, 3, 4, -1, 1 << 31, 1 << 62], int(r.integers(0, 4)))]
+            a = int(r.choice([0, 4, 8, 16, 1 << 40, -8]))
+            b = a + int(r.choice([0, 2, 8, 24, -2]))
+            hdr[f"t{t}"] = {"dtype": dt, "shape": shape, "data_offsets": [a, b]}
+        if r.random() < 0.3:
+            hdr["__metadata__"] = {"k": str(r.integers(0, 9))}
+        _write_raw(q, hdr, bytes(int(r.integers(0, 64))))
+        _check_open(q)
