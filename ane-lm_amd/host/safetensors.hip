@@ -218,15 +218,17 @@ struct Pipeline {
         recorded[k] = e == hipSuccess;
         return e;
     }
+    // teardown: a failure here has nowhere to go (the call that owns the
+    // pipeline has already returned its status), so results are dropped
     ~Pipeline() {
         for (int k = 0; k < 2; k++) {
             if (ev[k]) {
-                wait(k);
-                hipEventDestroy(ev[k]);
+                (void)wait(k);
+                (void)hipEventDestroy(ev[k]);
             }
-            if (hin[k]) hipHostFree(hin[k]);
-            if (hout[k]) hipHostFree(hout[k]);
-            if (dev[k]) hipFree(dev[k]);
+            if (hin[k]) (void)hipHostFree(hin[k]);
+            if (hout[k]) (void)hipHostFree(hout[k]);
+            if (dev[k]) (void)hipFree(dev[k]);
         }
     }
 };
@@ -550,8 +552,8 @@ extern "C" long anelm_write_ane_blobs(const char* safetensors_path, const char* 
         }
         // drain in chunk order: the older slot first
         for (int s = 0; s < 2 && rc == ANELM_OK; s++) rc = flush((int)((c + s) & 1));
-        if (rc != ANELM_OK) {   // close every file still open, once
-            hipStreamSynchronize(st);
+        if (rc != ANELM_OK) {   // close every file still open, once (rc already holds the error)
+            (void)hipStreamSynchronize(st);
             FILE* open_files[3] = {pend[0].busy ? pend[0].f : nullptr, pend[1].busy ? pend[1].f : nullptr, cur};
             for (int a = 0; a < 3; a++) {
                 if (!open_files[a]) continue;
