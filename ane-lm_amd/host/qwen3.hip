@@ -81,7 +81,7 @@ constexpr int kRopeRows = 16384;   // min(max_position_embeddings, 16384), qwen3
 struct DevBuf {
     void* p = nullptr;
     ~DevBuf() {
-        if (p) hipFree(p);
+        if (p) (void)hipFree(p);   // teardown: nothing left to report to
     }
 };
 
