@@ -74,6 +74,7 @@ _SIGS = {
     "anelm_sample": (_I, [_P, _P, _L, _P, _L, _L, _L, _P, _L, _P, ctypes.POINTER(SamplingParams), _P, _P, _S, _P]),
     "anelm_gqa_workspace_size": (_S, [_L, _I, _I, _I, _I]),
     "anelm_gqa_attention": (_I, [_P, _P, _P, _P, _P, _P, _L, _I, _I, _I, _L, _I, _L, _I, _L, _P, _S, _P]),
+    "anelm_gqa_attention_f16": (_I, [_P, _P, _P, _P, _P, _P, _L, _I, _I, _I, _L, _I, _L, _I, _L, _P, _S, _P]),
     "anelm_gqa_attention_bounded": (_I, [_P, _P, _P, _P, _P, _P, _L, _I, _I, _I, _L, _I, _L, _I, _L, _I, _P, _S,
                                          _P]),
     "anelm_gqa_attention_ring": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _S, _P]),
@@ -337,16 +338,17 @@ def _nbytes(t):
 def gqa_attention(out, q, k_cache, v_cache, ring_start, ring_len, n_heads, n_kv_heads, head_dim, workspace,
                   q_head_stride=None, stream=None):
     """Batched decode attention.  q: [B, >= (n_heads-1)*q_head_stride + head_dim];
-    out: [B, >= n_heads*head_dim]; caches: [B, capacity, n_kv_heads*head_dim]
-    (any per-sequence stride); ring_start / ring_len: int32 [B]."""
+    out: [B, >= n_heads*head_dim], fp32 or (int16/float16) fp16; caches: [B,
+    capacity, n_kv_heads*head_dim] (any per-sequence stride); ring_start /
+    ring_len: int32 [B]."""
     B = q.shape[0]
     cap = k_cache.shape[1]
     _need(k_cache.stride() == v_cache.stride() and k_cache.stride(2) == 1 and k_cache.stride(1) == n_kv_heads * head_dim,
           "gqa_attention: cache layout")
-    _check(lib().anelm_gqa_attention(_ptr(out), _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(ring_start),
-                                     _ptr(ring_len), B, n_heads, n_kv_heads, head_dim, _ld(q),
-                                     head_dim if q_head_stride is None else q_head_stride, _ld(out), cap,
-                                     k_cache.stride(0), _ptr(workspace), _nbytes(workspace), _stream(stream)))
+    fn = lib().anelm_gqa_attention_f16 if out.element_size() == 2 else lib().anelm_gqa_attention   # fp16 output
+    _check(fn(_ptr(out), _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(ring_start), _ptr(ring_len), B, n_heads,
+              n_kv_heads, head_dim, _ld(q), head_dim if q_head_stride is None else q_head_stride, _ld(out), cap,
+              k_cache.stride(0), _ptr(workspace), _nbytes(workspace), _stream(stream)))
 
 
 def gqa_attention_bounded(out, q, k_cache, v_cache, ring_start, ring_len, n_heads, n_kv_heads, head_dim, len_bound,

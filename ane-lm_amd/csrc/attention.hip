@@ -34,6 +34,7 @@ static_assert(kWholeRows <= kMaxChunk, "a whole ring's scores fit the LDS rows")
 
 struct AttnArgs {
     float* out;
+    uint16_t* out16;            // when set, outputs go here as fp16 (nearest even) instead of to out
     const float* q;
     const float* kc;
     const float* vc;
@@ -52,6 +53,13 @@ struct AttnArgs {
     float scale;
     float* ws;                  // [batch*nh][nsplit][head_dim + 2] partials
 };
+
+// An attention output: fp32, or fp16 rounded to nearest even (the input
+// rounding of the projection that follows, done once here).
+__device__ __forceinline__ void put_out(const AttnArgs& a, long i, float v) {
+    if (a.out16) a.out16[i] = __builtin_bit_cast(uint16_t, to_f16(v));
+    else a.out[i] = v;
+}
 
 // The ring state of sequence b, clamped so that every access stays inside
 // the caches: 0 <= len <= cap, 0 <= start < cap.
@@ -264,7 +272,7 @@ __global__ __launch_bounds__(kAttnThreads) void gqa_decode_kernel(AttnArgs a) {
         for (int w = 1; w < kAttnWaves; w++) s += red[w][g][d];
         const int h = kvh * a.groups + a.g0 + g;
         if (fin) {
-            a.out[b * a.out_ld + (long)h * D + d] = s;
+            put_out(a, b * a.out_ld + (long)h * D + d, s);
         } else {
             float* p = a.ws + ((b * a.nh + h) * a.nsplit + split) * (long)(D + 2);
             p[d] = s;
@@ -349,7 +357,7 @@ __global__ __launch_bounds__(kWave) void gqa_combine_kernel(AttnArgs a) {
     L = wave_sum(L);
     const float inv = L == 0.0f ? 0.0f : 1.0f / L;   // no live position: zeros (cpu_ops.cpp:177-180)
 #pragma unroll
-    for (int i = 0; i < D / kWave; i++) a.out[b * a.out_ld + (long)h * D + lane + i * kWave] = o[i] * inv;
+    for (int i = 0; i < D / kWave; i++) put_out(a, b * a.out_ld + (long)h * D + lane + i * kWave, o[i] * inv);
 }
 
 // Ring append: one workgroup per sequence.
@@ -483,6 +491,25 @@ extern "C" int anelm_gqa_attention(float* out, const float* q, const float* k_ca
     if (!ring_start || !ring_len) return fail(ANELM_ERR_INVALID, "gqa_attention: null ring state");
     AttnArgs a{};
     a.out = out; a.q = q; a.kc = k_cache; a.vc = v_cache;
+    a.ring_start = ring_start; a.ring_len = ring_len;
+    a.nh = n_heads; a.nkv = n_kv_heads;
+    a.q_ld = q_ld; a.q_hs = q_head_stride; a.out_ld = out_ld;
+    a.cap = capacity; a.seq_stride = cache_seq_stride;
+    return run(a, batch, head_dim, capacity, workspace, workspace_bytes, as_stream(stream));
+}
+
+extern "C" int anelm_gqa_attention_f16(uint16_t* out16, const float* q, const float* k_cache, const float* v_cache,
+                                       const int32_t* ring_start, const int32_t* ring_len, long batch, int n_heads,
+                                       int n_kv_heads, int head_dim, long q_ld, int q_head_stride, long out_ld,
+                                       int capacity, long cache_seq_stride, void* workspace, size_t workspace_bytes,
+                                       void* stream) {
+    clear_error();
+    int rc = check_common(out16, q, k_cache, v_cache, batch, n_heads, n_kv_heads, head_dim, q_ld, q_head_stride,
+                          out_ld, capacity, cache_seq_stride);
+    if (rc) return rc;
+    if (!ring_start || !ring_len) return fail(ANELM_ERR_INVALID, "gqa_attention: null ring state");
+    AttnArgs a{};
+    a.out16 = out16; a.q = q; a.kc = k_cache; a.vc = v_cache;
     a.ring_start = ring_start; a.ring_len = ring_len;
     a.nh = n_heads; a.nkv = n_kv_heads;
     a.q_ld = q_ld; a.q_hs = q_head_stride; a.out_ld = out_ld;

@@ -336,10 +336,12 @@ extern "C" int anelm_qwen3_forward(anelm_qwen3* m, const int32_t* ids, const int
             CK(anelm_proj_f16_x16_fused(m->qkv, m->a16, l.qkv16, B, m->qkvdim, (int)H, H, m->qkvdim,
                                         ANELM_PROJ_STORE, stream));                               // first_proj
             CK(qk_append(l));                                                                      // :444-488
-            CK(anelm_gqa_attention(m->attn, m->qkv, l.kc, l.vc, l.start, l.len, B, c.n_q_heads, c.n_kv_heads, D,
-                                   m->qkvdim, D, m->qdim, m->cap, seq, m->attn_ws, m->attn_ws_bytes, stream));  // :490
-            CK(anelm_proj_f16_fused(m->x, m->attn, l.o16, B, (int)H, m->qdim, m->qdim, H, nullptr, 0.0f,
-                                    ANELM_PROJ_ADD, stream));                                     // o_proj + :516
+            // the attention writes the o projection's fp16 input (y16 is free until the SwiGLU)
+            CK(anelm_gqa_attention_f16(m->y16, m->qkv, l.kc, l.vc, l.start, l.len, B, c.n_q_heads, c.n_kv_heads, D,
+                                       m->qkvdim, D, m->qdim, m->cap, seq, m->attn_ws, m->attn_ws_bytes,
+                                       stream));                                                  // :490
+            CK(anelm_proj_f16_x16_fused(m->x, m->y16, l.o16, B, (int)H, m->qdim, m->qdim, H, ANELM_PROJ_ADD,
+                                        stream));                                                 // o_proj + :516
             CK(anelm_rmsnorm_f16(m->a16, m->x, l.w_post, ANELM_BF16, B, (int)H, H, H, c.rms_eps, stream));  // :518
             CK(anelm_proj_f16_x16_fused(m->y16, m->a16, l.gu16, B, (int)I, (int)H, H, I, ANELM_PROJ_SWIGLU_F16,
                                         stream));                                                 // fused_ffn

@@ -262,6 +262,15 @@ int anelm_gqa_attention(float* out, const float* q, const float* k_cache, const 
                         int n_kv_heads, int head_dim, long q_ld, int q_head_stride, long out_ld,
                         int capacity, long cache_seq_stride, void* workspace, size_t workspace_bytes,
                         void* stream);
+/* anelm_gqa_attention with the outputs rounded to fp16 (nearest even) into
+ * out16 (row stride out_ld elements): the o projection's input, rounded once
+ * here instead of in every projection workgroup (anelm_proj_f16_x16_fused).
+ * Each value equals anelm_gqa_attention's then anelm_f32_to_f16.  No
+ * counterpart in the reference. */
+int anelm_gqa_attention_f16(uint16_t* out16, const float* q, const float* k_cache, const float* v_cache,
+                            const int32_t* ring_start, const int32_t* ring_len, long batch, int n_heads,
+                            int n_kv_heads, int head_dim, long q_ld, int q_head_stride, long out_ld, int capacity,
+                            long cache_seq_stride, void* workspace, size_t workspace_bytes, void* stream);
 /* anelm_gqa_attention for callers that know an upper bound on every ring's
  * length (len_bound >= ring_len[b] for all b; e.g. the tokens decoded since
  * the rings were emptied): only ceil(len_bound / chunk) chunks per sequence

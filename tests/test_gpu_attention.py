@@ -116,6 +116,28 @@ def test_whole_ring_threshold(hip, orc, rng):
         check(got[b], q[b], kc[b], vc[b], nq, nk, D, starts[b], lens[b], orc)
 
 
+@pytest.mark.parametrize("B,cap,lens", [(6, 2048, [0, 1, 127, 128, 129, 2048]), (3, 100, [1, 50, 100]),
+                                       (3, 32, [1, 20, 32])])
+def test_fp16_output_is_fp32_output_rounded(hip, orc, rng, B, cap, lens):
+    """The fp16-output attention writes the fp32 attention's values rounded
+    to nearest even, bit for bit: whole rings written by chunk 0, split rings
+    through the merge, and a single-chunk launch."""
+    import torch
+
+    nq, nk, D = 16, 8, 128
+    starts = [int(x) for x in rng.integers(0, cap, B)]
+    q = dev(rng.standard_normal((B, nq * D)).astype(np.float32))
+    kc = dev(rng.standard_normal((B, cap, nk * D)).astype(np.float32))
+    vc = dev(rng.standard_normal((B, cap, nk * D)).astype(np.float32))
+    ws = torch.empty(max(hip.gqa_workspace_size(B, nq, nk, D, cap), 1), dtype=torch.uint8, device="cuda")
+    st, ln = dev(np.array(starts, np.int32)), dev(np.array(lens, np.int32))
+    o32 = torch.empty(B, nq * D, device="cuda")
+    hip.gqa_attention(o32, q, kc, vc, st, ln, nq, nk, D, ws)
+    o16 = torch.empty(B, nq * D, dtype=torch.int16, device="cuda")
+    hip.gqa_attention(o16, q, kc, vc, st, ln, nq, nk, D, ws)
+    assert_bitexact(host(o16), orc.f32_to_f16_rne(host(o32)).reshape(B, nq * D), "fp16 attention output")
+
+
 @pytest.mark.parametrize("B,nq,nk,D,cap", [(3, 16, 8, 128, 4096), (600, 16, 8, 128, 64), (5, 8, 4, 64, 333)])
 def test_batched_other_shapes(hip, orc, rng, B, nq, nk, D, cap):
     starts = rng.integers(0, cap, B)
