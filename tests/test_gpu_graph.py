@@ -94,3 +94,41 @@ def test_sampler_graph_replays_match_eager(hip, rng):
         torch.cuda.synchronize()
         assert np.array_equal(host(ids_e), host(ids_g)), f"replay {rep}: ids"
         assert np.array_equal(host(pr_e).view(np.uint32), host(pr_g).view(np.uint32)), f"replay {rep}: probs"
+
+
+@pytest.mark.parametrize("B,steps", [(1, 140), (3, 30), (20, 24)])
+def test_decode_step_graph_replays_match_eager(hip, rng, tmp_path, B, steps):
+    """The Qwen3 decode step captured once (positions advanced inside the
+    graph, as bench.py runs it) gives on every replay the logits of the same
+    step run eagerly on a twin model, bit for bit: one sequence (dot-kernel
+    projections; its rings pass the 128-row whole-ring limit of the
+    attention), three (MFMA) and twenty (fp16-row projections, fp16
+    attention output)."""
+    import torch
+
+    from helpers import save_qwen3, tiny_qwen3
+
+    t, d = tiny_qwen3(rng, tied=False)
+    path = tmp_path / "tiny.safetensors"
+    save_qwen3(path, t)
+    cfg = hip.Qwen3Config(d["H"], d["L"], d["nq"], d["nk"], d["D"], d["I"], d["V"], 1e6, 1e-6)
+    eager = hip.Qwen3Model(path, cfg, max_batch=B, kv_capacity=256)
+    graph = hip.Qwen3Model(path, cfg, max_batch=B, kv_capacity=256)
+    ids = dev(rng.integers(0, d["V"], B).astype(np.int32))
+    pos_e = dev(np.resize(np.array([0, 7, 20000], np.int32), B))
+    pos_g = pos_e.clone()
+    le = torch.empty(B, d["V"], device="cuda")
+    lg = torch.empty(B, d["V"], device="cuda")
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        graph.forward(ids, pos_g, lg)
+        pos_g.add_(1)
+    for s in range(steps):
+        eager.forward(ids, pos_e, le)
+        pos_e.add_(1)
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(host(le).view(np.uint32), host(lg).view(np.uint32)), f"step {s}"
+    eager.close()
+    graph.close()
