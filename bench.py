@@ -668,10 +668,28 @@ SAMPLE_KERNELS = {"stage1": ("sample_stage1_kernel", ""), "stage2": ("sample_sta
                   "stage3": ("sample_stage3_kernel", ""), "walk": ("sample_walk_kernel", "")}
 SAMPLER = "sampling-64x151936"
 
+# The one-sequence decode step's projections, told apart by their launch
+# shapes (rows per wave, chunks in flight, fused norm, epilogue)
+Q3_B1 = "qwen3-0.6b-decode-step-b1"
+Q3_KERNELS = {"qkv": ("proj_dot_kernel", "<1, 2, 2, true, 0>"), "o_proj": ("proj_dot_kernel", "<1, 1, 4, false, 1>"),
+              "gate_up": ("proj_dot_kernel", "<1, 1, 2, true, 2>"), "down": ("proj_dot_kernel", "<1, 1, 6, false, 1>"),
+              "lm_head": ("proj_dot_kernel", "<1, 4, 2, true, 0>")}
+
+
+def q3_b1_bytes():
+    """fp16 weight bytes each projection of the one-sequence step reads (its
+    activations are a few KB)."""
+    c = Q3_06B
+    H, I, qd = c["hidden"], c["intermediate"], c["n_q_heads"] * D
+    return {"qkv": 2 * (qd + 2 * c["n_kv_heads"] * D) * H, "o_proj": 2 * H * qd, "gate_up": 2 * 2 * I * H,
+            "down": 2 * H * I, "lm_head": 2 * c["vocab"] * H}
+
 
 def _kernels_of(workload):
     if workload == SAMPLER:
         return SAMPLE_KERNELS
+    if workload == Q3_B1:
+        return Q3_KERNELS
     return ATTN_KERNELS if workload in ATTN_WORKLOADS else OP_KERNELS
 
 
@@ -704,6 +722,9 @@ def pmc_summary(fetch_dir, write_dir, copy_fetch_dir, copy_write_dir, workload=H
         w = ATTN_WORKLOADS[workload]
         ob = {"gqa_decode": attn_bytes(w), "gqa_combine": 0}
         run_args = f"--only {workload} --steps 1"
+    elif workload == Q3_B1:
+        ob = q3_b1_bytes()
+        run_args = f"--only {workload} --no-cpu"
     elif workload == SAMPLER:
         # stage 1 reads the logits; stage 2 reads them again and writes exp(x - max)
         # into the probability buffer; stage 3 reads that and writes the probabilities
@@ -788,7 +809,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default=HEADLINE, choices=sorted(WORKLOADS) + sorted(ATTN_WORKLOADS) + [SAMPLER],
+    ap.add_argument("--workload", default=HEADLINE, choices=sorted(WORKLOADS) + sorted(ATTN_WORKLOADS) + [SAMPLER, Q3_B1],
                     help="op-chain workload to run (attention names only select --pmc-summary kernels)")
     ap.add_argument("--cpu-seconds", type=float, default=8.0, help="CPU time budget of the headline baseline")
     ap.add_argument("--no-cpu", action="store_true")
