@@ -269,3 +269,31 @@ def test_bad_config_and_missing_file(hip, tmp_path):
     cfg = hip.Qwen3Config(256, 2, 4, 2, 128, 384, 300, 1e6, 1e-6)
     with pytest.raises(hip.AnelmError):
         hip.Qwen3Model(tmp_path / "absent.safetensors", cfg, 1)
+
+
+@pytest.mark.parametrize("B,out_dim,in_dim", [(2, 1024, 2048), (20, 512, 256), (1, 3000, 1024)])
+def test_proj_fused_strided_rows(hip, orc, rng, B, out_dim, in_dim):
+    """x and y as column slices of wider row-major buffers (row strides
+    larger than the rows, offsets inside the rows), for the dot kernel
+    (B <= 2) and the MFMA kernel, store and residual add; the columns
+    outside the slices stay untouched."""
+    import torch
+
+    x = rng.standard_normal((B, in_dim)).astype(np.float32)
+    w = (0.03 * rng.standard_normal((out_dim, in_dim))).astype(np.float16).view(np.uint16)
+    xb = torch.full((B, in_dim + 40), float("nan"), device="cuda")
+    xb[:, 8:8 + in_dim] = dev(x)
+    yb = torch.full((B, out_dim + 24), -7.0, device="cuda")
+    hip.proj_f16_fused(yb[:, 4:4 + out_dim], xb[:, 8:8 + in_dim], dev(w))
+    got = host(yb)
+    check_projection(orc, x, w, got[:, 4:4 + out_dim].astype(np.float64))
+    assert np.all(got[:, :4] == -7.0) and np.all(got[:, 4 + out_dim:] == -7.0)
+    r0 = rng.standard_normal((B, out_dim)).astype(np.float32)
+    yb[:, 4:4 + out_dim] = dev(r0)
+    hip.proj_f16_fused(yb[:, 4:4 + out_dim], xb[:, 8:8 + in_dim], dev(w), epilogue=hip.PROJ_ADD)
+    ref, mag = _proj_ref(orc, x, w)
+    want = r0.astype(np.float64) + ref
+    tol = _ulp16(ref) + mag * 2.0 ** -21 * 4 + np.spacing(np.abs(want).astype(np.float32))
+    got = host(yb)
+    assert np.all(np.abs(got[:, 4:4 + out_dim].astype(np.float64) - want) <= tol)
+    assert np.all(got[:, :4] == -7.0) and np.all(got[:, 4 + out_dim:] == -7.0)
