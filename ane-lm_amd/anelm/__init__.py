@@ -79,6 +79,9 @@ _SIGS = {
                                          _P]),
     "anelm_gqa_attention_ring": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _S, _P]),
     "anelm_kv_ring_append": (_I, [_P, _P, _P, _P, _P, _P, _L, _L, _L, _I, _I, _I, _L, _P]),
+    "anelm_kv_ring_advance": (_I, [_P, _P, _L, _I, _L, _I, _P]),
+    "anelm_gqa_attention_qk": (_I, [_P, _I, _P, _P, _P, _L, _L, _L, _P, _P, _I, _P, _P, _P, _I, _F, _F, _P, _P, _P, _P,
+                                    _L, _I, _I, _L, _I, _L, _P, _S, _P]),
     "anelm_rmsnorm_gated": (_I, [_P, _P, _P, _P, _I, _L, _I, _I, _L, _L, _L, _F, _P]),
     "anelm_l2_normalize": (_I, [_P, _L, _I, _I, _L, _F, _P]),
     "anelm_conv1d_update": (_I, [_P, _P, _P, _P, _P, _L, _I, _I, _L, _L, _L, _P]),
@@ -383,6 +386,38 @@ def kv_ring_append(k_cache, v_cache, ring_start, ring_len, k, v, stream=None):
     _need(k.shape[1] == row and v.shape[1] == row and k_cache.stride() == v_cache.stride(), "kv_ring_append: shapes")
     _check(lib().anelm_kv_ring_append(_ptr(k_cache), _ptr(v_cache), _ptr(ring_start), _ptr(ring_len), _ptr(k),
                                       _ptr(v), _ld(k), _ld(v), B, 1, row, cap, k_cache.stride(0), _stream(stream)))
+
+
+def kv_ring_advance(ring_start, ring_len, capacity, batch=None, stream=None):
+    """Advance rings by one row each (state only).  ring_start / ring_len:
+    int32 [B] or [groups, >= B] (row stride = group stride)."""
+    _need(ring_start.shape == ring_len.shape and ring_start.stride() == ring_len.stride(), "kv_ring_advance: shapes")
+    if ring_start.dim() == 1:
+        groups, gstride, B = 1, ring_start.shape[0], ring_start.shape[0]
+    else:
+        groups, gstride, B = ring_start.shape[0], ring_start.stride(0), ring_start.shape[1]
+    B = B if batch is None else batch
+    _check(lib().anelm_kv_ring_advance(_ptr(ring_start), _ptr(ring_len), B, groups, gstride, capacity,
+                                       _stream(stream)))
+
+
+def gqa_attention_qk(out, q, k, v, wq, wk, pos, cos_tab, sin_tab, k_cache, v_cache, ring_start, ring_len, n_heads,
+                     n_kv_heads, workspace, theta=1e6, eps=1e-6, stream=None):
+    """qknorm_rope_append + gqa_attention in one launch (head_dim 128) for rings
+    already advanced by kv_ring_advance.  q: [B, >= n_heads*128], k, v: [B, >=
+    n_kv_heads*128] (row slices of the qkv projection allowed, left as they
+    are); out fp32 or fp16; caches [B, capacity, n_kv_heads*128]."""
+    B = q.shape[0]
+    cap = k_cache.shape[1]
+    _need(k_cache.stride() == v_cache.stride() and k_cache.stride(2) == 1 and k_cache.stride(1) == n_kv_heads * 128,
+          "gqa_attention_qk: cache layout")
+    wdt = _dtype_code(wq if wq is not None else (wk if wk is not None else q))
+    tab_len = cos_tab.shape[0] if cos_tab is not None else 0
+    _check(lib().anelm_gqa_attention_qk(_ptr(out), int(out.element_size() == 2), _ptr(q), _ptr(k), _ptr(v), _ld(q),
+                                        _ld(k), _ld(v), _ptr(wq), _ptr(wk), wdt, _ptr(pos), _ptr(cos_tab),
+                                        _ptr(sin_tab), tab_len, theta, eps, _ptr(k_cache), _ptr(v_cache),
+                                        _ptr(ring_start), _ptr(ring_len), B, n_heads, n_kv_heads, _ld(out), cap,
+                                        k_cache.stride(0), _ptr(workspace), _nbytes(workspace), _stream(stream)))
 
 
 def rmsnorm_gated(out, x, z, w, eps=1e-6, heads=1, stream=None):

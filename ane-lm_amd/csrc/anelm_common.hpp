@@ -208,4 +208,95 @@ __device__ __forceinline__ void st_nt(uint4* p, uint4 v) {
     __builtin_nontemporal_store(n, reinterpret_cast<nat_u32x4*>(p));
 }
 
+// ---------------------------------------------- per-head q/k norm + RoPE
+// Shared by the q/k norm kernels and the attention that applies them on the
+// fly, so both produce the same bits.
+// cos/sin of the rotation angles j0 .. j0+3 at position p: table row p when
+// 0 <= p < tab_len (qwen3.cpp:463-469), else the fallback angle
+// p * inv_freq[j] (qwen3.cpp:39-49).
+__device__ __noinline__ float2 cos_sin_cold(float ang) { return make_float2(cosf(ang), sinf(ang)); }
+
+__device__ __forceinline__ void rope_cs4(int p, int j0, const float* cos_tab, const float* sin_tab, int tab_len,
+                                         const float* inv, float4& c, float4& s) {
+    if (p >= 0 && p < tab_len) {
+        c = *reinterpret_cast<const float4*>(cos_tab + (long)p * 64 + j0);
+        s = *reinterpret_cast<const float4*>(sin_tab + (long)p * 64 + j0);
+    } else {
+        // one angle per trip through an out-of-line cosf/sinf: keeps the
+        // code of the kernels that share this small (it is not the common path)
+        const float pf = (float)p;
+#pragma unroll 1
+        for (int i = 0; i < 4; i++) {
+            const float2 cs = cos_sin_cold(pf * inv[j0 + i]);
+            const float cv = cs.x, sv = cs.y;
+            c.x = i == 0 ? cv : c.x;
+            c.y = i == 1 ? cv : c.y;
+            c.z = i == 2 ? cv : c.z;
+            c.w = i == 3 ? cv : c.w;
+            s.x = i == 0 ? sv : s.x;
+            s.y = i == 1 ? sv : s.y;
+            s.z = i == 2 ? sv : s.z;
+            s.w = i == 3 ? sv : s.w;
+        }
+    }
+}
+
+// One 128-wide head held by an aligned group of 16 lanes, lane l holding
+// elements j0 = 4*(l%16) .. j0+3 in `l` and j0+64 .. j0+67 in `h`: the
+// RMSNorm with gamma wl / wh (this lane's gammas; skipped when !has_w), then
+// the half-split rotation; returns the rotated halves in ol / oh.  Every lane
+// of the group calls it (the sum of squares is a group reduction).
+__device__ __forceinline__ void norm_rope128_w(float4 l, float4 h, bool has_w, float4 wl, float4 wh, float4 c,
+                                               float4 s, float eps, float4& ol, float4& oh) {
+    float ss = 0.f;
+    ss = fmaf(l.x, l.x, ss);
+    ss = fmaf(l.y, l.y, ss);
+    ss = fmaf(l.z, l.z, ss);
+    ss = fmaf(l.w, l.w, ss);
+    ss = fmaf(h.x, h.x, ss);
+    ss = fmaf(h.y, h.y, ss);
+    ss = fmaf(h.z, h.z, ss);
+    ss = fmaf(h.w, h.w, ss);
+    ss = group16_sum(ss);
+    if (has_w) {
+        const float sc = 1.0f / sqrtf(ss / 128.0f + eps);
+        l.x = (l.x * sc) * wl.x;
+        l.y = (l.y * sc) * wl.y;
+        l.z = (l.z * sc) * wl.z;
+        l.w = (l.w * sc) * wl.w;
+        h.x = (h.x * sc) * wh.x;
+        h.y = (h.y * sc) * wh.y;
+        h.z = (h.z * sc) * wh.z;
+        h.w = (h.w * sc) * wh.w;
+    }
+    ol.x = l.x * c.x - h.x * s.x;
+    ol.y = l.y * c.y - h.y * s.y;
+    ol.z = l.z * c.z - h.z * s.z;
+    ol.w = l.w * c.w - h.w * s.w;
+    oh.x = h.x * c.x + l.x * s.x;
+    oh.y = h.y * c.y + l.y * s.y;
+    oh.z = h.z * c.z + l.z * s.z;
+    oh.w = h.w * c.w + l.w * s.w;
+}
+
+// The gammas of lane slice j0 of a 128-wide head (ones when w is null).
+template <int DT>
+__device__ __forceinline__ void head_gamma128(const void* w, int j0, float4& wl, float4& wh) {
+    wl = wh = make_float4(1.f, 1.f, 1.f, 1.f);
+    if (w) {
+        wl = load_w4<DT>(w, j0);
+        wh = load_w4<DT>(w, j0 + 64);
+    }
+}
+
+// norm_rope128_w with the gammas read from w (element type DT; null skips
+// the norm).
+template <int DT>
+__device__ __forceinline__ void norm_rope128(float4 l, float4 h, const void* w, float4 c, float4 s, int j0,
+                                             float eps, float4& ol, float4& oh) {
+    float4 wl, wh;
+    head_gamma128<DT>(w, j0, wl, wh);
+    norm_rope128_w(l, h, w != nullptr, wl, wh, c, s, eps, ol, oh);
+}
+
 }  // namespace anelm

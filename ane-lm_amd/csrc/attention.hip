@@ -52,6 +52,22 @@ struct AttnArgs {
     int g0, gcount;             // q heads g0 .. g0+gcount-1 of every group
     float scale;
     float* ws;                  // [batch*nh][nsplit][head_dim + 2] partials
+    // QK launches (head_dim 128): q (at q, q_ld, q_hs = 128) and the new k and
+    // v rows are the raw projection outputs.  q is normalised and rotated on
+    // the fly; the workgroup whose chunk holds the ring's newest row (the
+    // rings were advanced before the launch) makes that row from k and v and
+    // writes it to the caches.
+    const float* kraw;
+    const float* vraw;
+    long k_ld, v_ld;
+    const void* wq;
+    const void* wk;
+    const int32_t* pos;
+    const float* cos_tab;
+    const float* sin_tab;
+    int tab_len;
+    float eps;
+    float inv[64];              // RoPE inverse frequencies of the 64 pairs
 };
 
 // An attention output: fp32, or fp16 rounded to nearest even (the input
@@ -114,8 +130,9 @@ __device__ __forceinline__ void load8(float (&x)[8], const float* p) {
 template <int D>
 __device__ __forceinline__ int elem_of(int ds, int i) { return (i < 4 ? 0 : D / 2 - 4) + 4 * ds + i; }
 
-template <int D, int GM, bool FINAL>
+template <int D, int GM, bool FINAL, int QK = -1>
 __global__ __launch_bounds__(kAttnThreads) void gqa_decode_kernel(AttnArgs a) {
+    static_assert(QK < 0 || D == 128, "the fused q/k norm + RoPE is for 128-wide heads");
     constexpr int LP = D / 8;                  // lanes per position
     constexpr int PPW = kWave / LP;            // positions per wave per round
     constexpr int PPB = PPW * kAttnWaves;      // positions per workgroup per round
@@ -128,6 +145,7 @@ __global__ __launch_bounds__(kAttnThreads) void gqa_decode_kernel(AttnArgs a) {
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wid = tid / kWave;
     const int split = blockIdx.x, kvh = blockIdx.y;
     const long b = blockIdx.z;
+    const int qpos = QK >= 0 ? a.pos[b] : 0;   // read beside the ring state
     int start, len;
     ring_state(a, b, start, len);
     // In a split launch a ring that is short (len <= a.whole, at most one
@@ -151,9 +169,45 @@ __global__ __launch_bounds__(kAttnThreads) void gqa_decode_kernel(AttnArgs a) {
     // registers: the next batch's loads are in flight while this one is
     // used.  Positions past the chunk re-read its last row (n >= 1 inside
     // the loops) and are discarded.
+    // QK: the newest row (position len-1) is made here, in this lane's slice
+    // layout, by the workgroup whose chunk holds it, substituted for what the
+    // caches held at its slot, and written to the caches at the end.  The
+    // RoPE angles, gammas, raw k and v, the q heads and the first K batch are
+    // all loaded before any of them is used, so the loads overlap.
+    float knew[8], vnew[8], kr[8];
+    float4 rc, rs, gql, gqh, gkl, gkh;   // cos/sin of this lane's four angles; q and k gammas
+    const int tnew = QK >= 0 ? len - 1 - t0 : -1;   // its position in this chunk
+    const bool owns = QK >= 0 && tnew >= 0 && tnew < n;
+    // The loads are unconditional (a branch around a load makes the wave
+    // wait for it at the branch's end): a table row (the clamped position's;
+    // replaced below when the position is past the table), both gammas (non-
+    // null, checked on the host), and the raw k and v of every workgroup.
+    const int rpos = QK >= 0 ? min(max(qpos, 0), a.tab_len - 1) : 0;   // tab_len >= 1
+    if constexpr (QK >= 0) {
+        constexpr int WT = QK < 0 ? ANELM_F32 : QK;
+        rc = *reinterpret_cast<const float4*>(a.cos_tab + (long)rpos * 64 + 4 * ds);
+        rs = *reinterpret_cast<const float4*>(a.sin_tab + (long)rpos * 64 + 4 * ds);
+        gql = load_w4<WT>(a.wq, 4 * ds);
+        gqh = load_w4<WT>(a.wq, 4 * ds + 64);
+        gkl = load_w4<WT>(a.wk, 4 * ds);
+        gkh = load_w4<WT>(a.wk, 4 * ds + 64);
+        load8<D, false>(kr, a.kraw + b * a.k_ld + (long)kvh * D + 4 * ds);
+        load8<D, false>(vnew, a.vraw + b * a.v_ld + (long)kvh * D + 4 * ds);
+    }
     auto load_batch = [&](float (&buf)[U][8], const float* base, int r0) {
 #pragma unroll
         for (int u = 0; u < U; u++) load8<D, true>(buf[u], base + ring_slot(a, start, t0, r0 + u * PPB + ps, n) * row);
+    };
+    // the newest row in place of the slot's old contents (K: knew, V: vnew)
+    auto fix_batch = [&](float (&buf)[U][8], const float (&nw)[8], int r0) {
+        if constexpr (QK >= 0) {
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const bool hit = owns && r0 + u * PPB + ps == tnew;
+#pragma unroll
+                for (int i = 0; i < 8; i++) buf[u][i] = hit ? nw[i] : buf[u][i];
+            }
+        }
     };
 
     // phase 1: scores
@@ -161,11 +215,42 @@ __global__ __launch_bounds__(kAttnThreads) void gqa_decode_kernel(AttnArgs a) {
         float qv[GM][8];
 #pragma unroll
         for (int g = 0; g < GM; g++) {
-            if (g < gc) {
+            if constexpr (QK >= 0) {   // branch-free: heads past gc re-read the last one, then zeroed
+                const int gg = g < gc ? g : gc - 1;
+                load8<D, false>(qv[g], a.q + b * a.q_ld + (long)(kvh * a.groups + a.g0 + gg) * a.q_hs + 4 * ds);
+            } else if (g < gc) {
                 load8<D, false>(qv[g], a.q + b * a.q_ld + (long)(kvh * a.groups + a.g0 + g) * a.q_hs + 4 * ds);
             } else {
 #pragma unroll
                 for (int i = 0; i < 8; i++) qv[g][i] = 0.0f;
+            }
+        }
+        float ka[U][8], kb[U][8];
+        if (n > 0) load_batch(ka, kbase, 0);
+        if constexpr (QK >= 0) {
+            if (qpos != rpos) {   // past the table (uniform): the angles themselves
+                float4 fc, fs;
+                rope_cs4(qpos, 4 * ds, nullptr, nullptr, 0, a.inv, fc, fs);
+                rc = fc;
+                rs = fs;
+            }
+            // the q heads' norm + RoPE, every lane of each 16-lane group
+#pragma unroll
+            for (int g = 0; g < GM; g++) {
+                float4 ol, oh;
+                norm_rope128_w(make_float4(qv[g][0], qv[g][1], qv[g][2], qv[g][3]),
+                               make_float4(qv[g][4], qv[g][5], qv[g][6], qv[g][7]), true, gql, gqh, rc, rs, a.eps,
+                               ol, oh);
+                if (g >= gc) ol = oh = make_float4(0.f, 0.f, 0.f, 0.f);   // heads past gc
+                qv[g][0] = ol.x; qv[g][1] = ol.y; qv[g][2] = ol.z; qv[g][3] = ol.w;
+                qv[g][4] = oh.x; qv[g][5] = oh.y; qv[g][6] = oh.z; qv[g][7] = oh.w;
+            }
+            if (owns) {   // uniform across the workgroup
+                float4 ol, oh;
+                norm_rope128_w(make_float4(kr[0], kr[1], kr[2], kr[3]), make_float4(kr[4], kr[5], kr[6], kr[7]), true,
+                               gkl, gkh, rc, rs, a.eps, ol, oh);
+                knew[0] = ol.x; knew[1] = ol.y; knew[2] = ol.z; knew[3] = ol.w;
+                knew[4] = oh.x; knew[5] = oh.y; knew[6] = oh.z; knew[7] = oh.w;
             }
         }
         auto scores = [&](const float (&kx)[U][8], int r0) {
@@ -184,13 +269,13 @@ __global__ __launch_bounds__(kAttnThreads) void gqa_decode_kernel(AttnArgs a) {
                 if (t < n && ds < gc) sc[ds][t] = mine * a.scale;
             }
         };
-        float ka[U][8], kb[U][8];
-        if (n > 0) load_batch(ka, kbase, 0);
         for (int r0 = 0; r0 < n; r0 += 2 * STEP) {
             if (r0 + STEP < n) load_batch(kb, kbase, r0 + STEP);
+            fix_batch(ka, knew, r0);
             scores(ka, r0);
             if (r0 + STEP >= n) break;
             if (r0 + 2 * STEP < n) load_batch(ka, kbase, r0 + 2 * STEP);
+            fix_batch(kb, knew, r0 + STEP);
             scores(kb, r0 + STEP);
         }
     }
@@ -246,9 +331,11 @@ __global__ __launch_bounds__(kAttnThreads) void gqa_decode_kernel(AttnArgs a) {
     };
     for (int r0 = 0; r0 < n; r0 += 2 * STEP) {
         if (r0 + STEP < n) load_batch(vb, vbase, r0 + STEP);
+        fix_batch(va, vnew, r0);
         accumulate(va, r0);
         if (r0 + STEP >= n) break;
         if (r0 + 2 * STEP < n) load_batch(va, vbase, r0 + 2 * STEP);
+        fix_batch(vb, vnew, r0 + STEP);
         accumulate(vb, r0 + STEP);
     }
     // reduce over the position slots of the wave (lanes with the same slice)
@@ -280,6 +367,19 @@ __global__ __launch_bounds__(kAttnThreads) void gqa_decode_kernel(AttnArgs a) {
                 p[D] = hm[g];
                 p[D + 1] = hl[g];
             }
+        }
+    }
+    // QK: the new row goes to the caches last, once this workgroup's own
+    // reads of the chunk (which may cover its slot) are done
+    if constexpr (QK >= 0) {
+        if (owns && tid < LP) {   // one 16-lane group stores the row
+            const long slot = ring_slot(a, start, t0, tnew, n);
+            float* kd = const_cast<float*>(kbase) + slot * row;
+            float* vd = const_cast<float*>(vbase) + slot * row;
+            *reinterpret_cast<float4*>(kd) = make_float4(knew[0], knew[1], knew[2], knew[3]);
+            *reinterpret_cast<float4*>(kd + D / 2) = make_float4(knew[4], knew[5], knew[6], knew[7]);
+            *reinterpret_cast<float4*>(vd) = make_float4(vnew[0], vnew[1], vnew[2], vnew[3]);
+            *reinterpret_cast<float4*>(vd + D / 2) = make_float4(vnew[4], vnew[5], vnew[6], vnew[7]);
         }
     }
 }
@@ -385,6 +485,17 @@ __global__ __launch_bounds__(256) void kv_append_kernel(float* kc, float* vc, in
     }
 }
 
+// Rings [g][b] (g < groups, b < batch, ring g*group_stride + b) each take one
+// row: the state update of the append (qwen3.cpp:475-484) without the copy.
+__global__ __launch_bounds__(256) void kv_ring_advance_kernel(int32_t* rs, int32_t* rl, long batch, long n,
+                                                              long group_stride, int cap) {
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const long g = i / batch;
+    const long r = g * group_stride + (i - g * batch);
+    ring_advance(rs + r, rl + r, cap);
+}
+
 // Positions per workgroup for a ring of `bound` positions and `pairs`
 // (sequence, kv head) pairs: the largest chunk that still gives about
 // kTargetBlocks workgroups, at least kMinChunk.
@@ -397,26 +508,30 @@ int pick_chunk(long pairs, int bound) {
 
 int group_max(int D) { return kMaxGD / D < 8 ? kMaxGD / D : 8; }
 
-template <int D, int GM>
+template <int D, int GM, int QK>
 void launch_gm(const AttnArgs& a, long batch, hipStream_t st) {
     const dim3 grid(a.nsplit, a.nkv, batch);
     if (a.nsplit == 1) {
-        hipLaunchKernelGGL((gqa_decode_kernel<D, GM, true>), grid, dim3(kAttnThreads), 0, st, a);
+        hipLaunchKernelGGL((gqa_decode_kernel<D, GM, true, QK>), grid, dim3(kAttnThreads), 0, st, a);
     } else {
-        hipLaunchKernelGGL((gqa_decode_kernel<D, GM, false>), grid, dim3(kAttnThreads), 0, st, a);
+        hipLaunchKernelGGL((gqa_decode_kernel<D, GM, false, QK>), grid, dim3(kAttnThreads), 0, st, a);
     }
 }
 
-template <int D>
+// One launch per slice of at most group_max(D) q heads of each kv head.  A
+// QK launch writes the newest cache row in every slice's launch (the same
+// bits each time) and uses it from registers, so no launch depends on the
+// order of the others.
+template <int D, int QK = -1>
 void launch_d(AttnArgs a, long batch, hipStream_t st) {
     const int gmax = group_max(D);
     for (int g0 = 0; g0 < a.groups; g0 += gmax) {
         a.g0 = g0;
         a.gcount = a.groups - g0 < gmax ? a.groups - g0 : gmax;
-        if (a.gcount <= 1) launch_gm<D, 1>(a, batch, st);
-        else if (a.gcount <= 2) launch_gm<D, 2>(a, batch, st);
-        else if (a.gcount <= 4) launch_gm<D, 4>(a, batch, st);
-        else launch_gm<D, (kMaxGD / D < 8 ? kMaxGD / D : 8)>(a, batch, st);
+        if (a.gcount <= 1) launch_gm<D, 1, QK>(a, batch, st);
+        else if (a.gcount <= 2) launch_gm<D, 2, QK>(a, batch, st);
+        else if (a.gcount <= 4) launch_gm<D, 4, QK>(a, batch, st);
+        else launch_gm<D, (kMaxGD / D < 8 ? kMaxGD / D : 8), QK>(a, batch, st);
     }
     if (a.nsplit > 1) {
         hipLaunchKernelGGL((gqa_combine_kernel<D>), dim3(batch * a.nh), dim3(kWave), 0, st, a);
@@ -448,7 +563,8 @@ int check_common(const void* out, const void* q, const void* kc, const void* vc,
     return ANELM_OK;
 }
 
-int run(AttnArgs a, long batch, int D, int bound, void* ws, size_t ws_bytes, hipStream_t st) {
+// qk: -1, or the weight dtype of a QK launch (head_dim 128)
+int run(AttnArgs a, long batch, int D, int bound, void* ws, size_t ws_bytes, hipStream_t st, int qk = -1) {
     a.groups = a.nh / a.nkv;
     a.scale = 1.0f / sqrtf((float)D);   // core/cpu_ops.cpp:183
     a.chunk = pick_chunk(batch * a.nkv, a.cap);  // from the capacity, so the workspace size holds for any bound
@@ -463,7 +579,10 @@ int run(AttnArgs a, long batch, int D, int bound, void* ws, size_t ws_bytes, hip
     }
     a.ws = static_cast<float*>(ws);
     if (batch == 0) return ANELM_OK;
-    if (D == 64) launch_d<64>(a, batch, st);
+    if (qk == ANELM_F32) launch_d<128, ANELM_F32>(a, batch, st);
+    else if (qk == ANELM_F16) launch_d<128, ANELM_F16>(a, batch, st);
+    else if (qk == ANELM_BF16) launch_d<128, ANELM_BF16>(a, batch, st);
+    else if (D == 64) launch_d<64>(a, batch, st);
     else if (D == 128) launch_d<128>(a, batch, st);
     else launch_d<256>(a, batch, st);
     return launch_status("gqa_attention");
@@ -578,4 +697,56 @@ extern "C" int anelm_kv_ring_append(float* k_cache, float* v_cache, int32_t* rin
     hipLaunchKernelGGL(kv_append_kernel, dim3(batch), dim3(256), 0, as_stream(stream), k_cache, v_cache, ring_start,
                        ring_len, k, v, k_ld, v_ld, (int)row, capacity, cache_seq_stride, vec);
     return launch_status("kv_ring_append");
+}
+
+extern "C" int anelm_kv_ring_advance(int32_t* ring_start, int32_t* ring_len, long batch, int groups,
+                                     long group_stride, int capacity, void* stream) {
+    clear_error();
+    if (!ring_start || !ring_len) return fail(ANELM_ERR_INVALID, "kv_ring_advance: null pointer");
+    if (batch < 0 || groups < 0 || capacity <= 0 || (groups > 1 && group_stride < batch))
+        return fail(ANELM_ERR_INVALID, "kv_ring_advance: bad sizes");
+    const long n = batch * groups;
+    if (n == 0) return ANELM_OK;
+    if (n > (1L << 31)) return fail(ANELM_ERR_INVALID, "kv_ring_advance: too many rings");
+    hipLaunchKernelGGL(kv_ring_advance_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, as_stream(stream),
+                       ring_start, ring_len, batch, n, group_stride, capacity);
+    return launch_status("kv_ring_advance");
+}
+
+extern "C" int anelm_gqa_attention_qk(void* out, int out_f16, const float* q, const float* k, const float* v,
+                                      long q_ld, long k_ld, long v_ld, const void* wq, const void* wk, int w_dtype,
+                                      const int32_t* pos, const float* cos_tab, const float* sin_tab, int tab_len,
+                                      float theta, float eps, float* k_cache, float* v_cache,
+                                      const int32_t* ring_start, const int32_t* ring_len, long batch, int n_heads,
+                                      int n_kv_heads, long out_ld, int capacity, long cache_seq_stride,
+                                      void* workspace, size_t workspace_bytes, void* stream) {
+    const char* fn = "gqa_attention_qk";
+    clear_error();
+    int rc = check_common(out, q, k_cache, v_cache, batch, n_heads, n_kv_heads, 128, q_ld, 128, out_ld, capacity,
+                          cache_seq_stride);
+    if (rc) return rc;
+    if (!ring_start || !ring_len || !k || !v || !pos) return fail(ANELM_ERR_INVALID, "%s: null pointer", fn);
+    const long row = (long)n_kv_heads * 128;
+    if (batch > 1 && (k_ld < row || v_ld < row)) return fail(ANELM_ERR_INVALID, "%s: k/v strides overlap", fn);
+    if (tab_len < 1 || !cos_tab || !sin_tab) return fail(ANELM_ERR_INVALID, "%s: needs a RoPE table of >= 1 row", fn);
+    if (!wq || !wk) return fail(ANELM_ERR_INVALID, "%s: needs both q and k gammas", fn);
+    if (w_dtype < ANELM_F32 || w_dtype > ANELM_BF16) return fail(ANELM_ERR_INVALID, "%s: dtype", fn);
+    const bool wal = w_dtype == ANELM_F32 ? aligned16(wq) && aligned16(wk) : aligned8(wq) && aligned8(wk);
+    if (!aligned16(k) || !aligned16(v) || ((k_ld | v_ld) & 3) || !wal || !aligned16(cos_tab) || !aligned16(sin_tab))
+        return fail(ANELM_ERR_INVALID, "%s: needs 16-byte aligned rows (strides multiples of 4)", fn);
+    InvFreq inv;
+    rope_inv_freq(&inv, 128, theta);
+    AttnArgs a{};
+    if (out_f16) a.out16 = static_cast<uint16_t*>(out);
+    else a.out = static_cast<float*>(out);
+    a.q = q; a.kc = k_cache; a.vc = v_cache;
+    a.ring_start = ring_start; a.ring_len = ring_len;
+    a.nh = n_heads; a.nkv = n_kv_heads;
+    a.q_ld = q_ld; a.q_hs = 128; a.out_ld = out_ld;
+    a.cap = capacity; a.seq_stride = cache_seq_stride;
+    a.kraw = k; a.vraw = v; a.k_ld = k_ld; a.v_ld = v_ld;
+    a.wq = wq; a.wk = wk; a.pos = pos;
+    a.cos_tab = cos_tab; a.sin_tab = sin_tab; a.tab_len = tab_len; a.eps = eps;
+    for (int j = 0; j < 64; j++) a.inv[j] = inv.v[j];
+    return run(a, batch, 128, capacity, workspace, workspace_bytes, as_stream(stream), w_dtype);
 }

@@ -194,64 +194,6 @@ static int launch_rmsnorm(void* out, float* x, const float* y, const void* w, in
 // of the grid covers consecutive heads; all loads of the HPG heads (heads,
 // then positions, then the table rows that depend on them) are issued before
 // the first is used, which matters when a launch is only a few rounds deep.
-// cos/sin of the rotation angles j0 .. j0+3 at position p: table row p when
-// 0 <= p < tab_len (qwen3.cpp:463-469), else the fallback angle
-// p * inv_freq[j] (qwen3.cpp:39-49).
-__device__ __forceinline__ void rope_cs4(int p, int j0, const float* cos_tab, const float* sin_tab, int tab_len,
-                                         const InvFreq& inv, float4& c, float4& s) {
-    if (p >= 0 && p < tab_len) {
-        c = *reinterpret_cast<const float4*>(cos_tab + (long)p * 64 + j0);
-        s = *reinterpret_cast<const float4*>(sin_tab + (long)p * 64 + j0);
-    } else {
-        const float pf = (float)p;
-        const float a0 = pf * inv.v[j0], a1 = pf * inv.v[j0 + 1];
-        const float a2 = pf * inv.v[j0 + 2], a3 = pf * inv.v[j0 + 3];
-        c = make_float4(cosf(a0), cosf(a1), cosf(a2), cosf(a3));
-        s = make_float4(sinf(a0), sinf(a1), sinf(a2), sinf(a3));
-    }
-}
-
-// One 128-wide head held by an aligned group of 16 lanes, lane l holding
-// elements j0 = 4*(l%16) .. j0+3 in `l` and j0+64 .. j0+67 in `h`: the
-// RMSNorm with gamma w (skipped when w is null), then the half-split
-// rotation; returns the rotated halves in ol / oh.  Every lane of the group
-// calls it (the sum of squares is a group reduction).
-template <int DT>
-__device__ __forceinline__ void norm_rope128(float4 l, float4 h, const void* w, float4 c, float4 s, int j0,
-                                             float eps, float4& ol, float4& oh) {
-    float ss = 0.f;
-    ss = fmaf(l.x, l.x, ss);
-    ss = fmaf(l.y, l.y, ss);
-    ss = fmaf(l.z, l.z, ss);
-    ss = fmaf(l.w, l.w, ss);
-    ss = fmaf(h.x, h.x, ss);
-    ss = fmaf(h.y, h.y, ss);
-    ss = fmaf(h.z, h.z, ss);
-    ss = fmaf(h.w, h.w, ss);
-    ss = group16_sum(ss);
-    if (w) {
-        const float sc = 1.0f / sqrtf(ss / 128.0f + eps);
-        const float4 wl = load_w4<DT>(w, j0);
-        const float4 wh = load_w4<DT>(w, j0 + 64);
-        l.x = (l.x * sc) * wl.x;
-        l.y = (l.y * sc) * wl.y;
-        l.z = (l.z * sc) * wl.z;
-        l.w = (l.w * sc) * wl.w;
-        h.x = (h.x * sc) * wh.x;
-        h.y = (h.y * sc) * wh.y;
-        h.z = (h.z * sc) * wh.z;
-        h.w = (h.w * sc) * wh.w;
-    }
-    ol.x = l.x * c.x - h.x * s.x;
-    ol.y = l.y * c.y - h.y * s.y;
-    ol.z = l.z * c.z - h.z * s.z;
-    ol.w = l.w * c.w - h.w * s.w;
-    oh.x = h.x * c.x + l.x * s.x;
-    oh.y = h.y * c.y + l.y * s.y;
-    oh.z = h.z * c.z + l.z * s.z;
-    oh.w = h.w * c.w + l.w * s.w;
-}
-
 template <int DT, int HPG>
 __global__ __launch_bounds__(256) void qknorm_rope128_kernel(
     float* q, float* k, long q_ld, long k_ld, const void* wq, const void* wk, const int32_t* pos,
@@ -289,7 +231,7 @@ __global__ __launch_bounds__(256) void qknorm_rope128_kernel(
         }
     }
 #pragma unroll
-    for (int i = 0; i < HPG; i++) rope_cs4(p[i], j0, cos_tab, sin_tab, tab_len, inv, c[i], s[i]);
+    for (int i = 0; i < HPG; i++) rope_cs4(p[i], j0, cos_tab, sin_tab, tab_len, inv.v, c[i], s[i]);
 #pragma unroll
     for (int i = 0; i < HPG; i++) {
         float4 ol, oh;   // every lane takes part (dead heads contribute zeros)
@@ -328,7 +270,7 @@ __global__ __launch_bounds__(1024) void qknorm_rope_append128_kernel(
     }
     if (threadIdx.x == 0) s_slot = ring_advance(rs + b, rl + b, cap);
     float4 c, s;
-    rope_cs4(pos[b], j0, cos_tab, sin_tab, tab_len, inv, c, s);
+    rope_cs4(pos[b], j0, cos_tab, sin_tab, tab_len, inv.v, c, s);
     __syncthreads();
     const long row = (long)nk * 128;
     float* kd = kc + b * seq_stride + (long)s_slot * row;

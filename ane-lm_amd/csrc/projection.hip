@@ -214,7 +214,6 @@ __global__ __launch_bounds__(64 * NW) void proj_mfma_kernel(ProjArgs a) {
                     } else if constexpr (NORM) {
                         const float4 u = xr[j][nb][0], v = xr[j][nb][1];
                         const uint4 q = gq[j];
-                        float4 lo, hi;
                         xb = to_half8(norm_scale(u, my_scale[nb], q.x, q.y), norm_scale(v, my_scale[nb], q.z, q.w));
                     } else {
                         xb = to_half8(xr[j][nb][0], xr[j][nb][1]);

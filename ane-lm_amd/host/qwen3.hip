@@ -9,9 +9,10 @@
 // round-to-nearest fp16 and leave it as fp16 (core/ane_runtime.cpp:600-640).
 // The RMSNorms, residual adds and the SwiGLU are fused into the
 // projections: up to 16 sequences as the projections' own prologue and
-// epilogues (6 library calls per layer instead of 12), past that with the
-// norms writing the projections' fp16 inputs (8 calls); the q/k norm, RoPE
-// and ring append are one kernel throughout.
+// epilogues (5 library calls per layer instead of 12), past that with the
+// norms writing the projections' fp16 inputs (7 calls).  The q/k norm, RoPE,
+// ring append and attention are one kernel throughout, after one launch at
+// the start of the step has advanced every layer's rings.
 //
 // A step processes one token of each of `batch` sequences; every sequence
 // has its own KV ring per layer (qwen3.cpp:227-231, 475-488).
@@ -100,9 +101,10 @@ struct anelm_qwen3 {
         uint16_t *qkv16, *o16, *gu16, *down16;   // fp16 projections
         uint16_t *qn, *kn, *w_in, *w_post;       // bf16 gammas
         float *kc, *vc;                          // [max_batch][cap][kvdim]
-        int32_t *start, *len;                    // [max_batch]
+        int32_t *start, *len;                    // [max_batch], rows of ring_start / ring_len
     };
     std::vector<Layer> layers;
+    int32_t *ring_start = nullptr, *ring_len = nullptr;   // [layers][max_batch]
     float *cos_tab = nullptr, *sin_tab = nullptr;
     // activations
     float *x, *xn, *qkv, *attn, *o, *gu, *h;
@@ -154,7 +156,7 @@ extern "C" anelm_qwen3* anelm_qwen3_load(const char* path, const anelm_qwen3_con
     }
     const anelm_qwen3_config& c = *cfg;
     if (c.hidden <= 0 || c.layers <= 0 || c.n_q_heads <= 0 || c.n_kv_heads <= 0 || c.intermediate <= 0 ||
-        c.vocab <= 0 || (c.head_dim != 64 && c.head_dim != 128 && c.head_dim != 256) ||
+        c.vocab <= 0 || c.head_dim != 128 ||   // every Qwen3 size; the fused q/k + attention kernel's width
         c.n_q_heads % c.n_kv_heads || c.hidden % 4 || c.intermediate % 4) {
         fail(ANELM_ERR_INVALID, "qwen3_load: unsupported configuration");
         return nullptr;
@@ -194,6 +196,8 @@ extern "C" anelm_qwen3* anelm_qwen3_load(const char* path, const anelm_qwen3_con
                           stream)))
         return bail("");
     m->layers.resize(c.layers);
+    ALLOC(m->ring_start, int32_t, (long)c.layers * B);
+    ALLOC(m->ring_len, int32_t, (long)c.layers * B);
     char name[256];
     for (int L = 0; L < c.layers; L++) {
         anelm_qwen3::Layer& l = m->layers[L];
@@ -207,8 +211,8 @@ extern "C" anelm_qwen3* anelm_qwen3_load(const char* path, const anelm_qwen3_con
         ALLOC(l.w_post, uint16_t, H);
         ALLOC(l.kc, float, B * m->cap * m->kvdim);
         ALLOC(l.vc, float, B * m->cap * m->kvdim);
-        ALLOC(l.start, int32_t, B);
-        ALLOC(l.len, int32_t, B);
+        l.start = m->ring_start + (long)L * B;
+        l.len = m->ring_len + (long)L * B;
         struct Item {
             const char* n;
             std::vector<int64_t> shape;
@@ -271,11 +275,10 @@ extern "C" void anelm_qwen3_free(anelm_qwen3* m) { delete m; }
 extern "C" int anelm_qwen3_reset(anelm_qwen3* m, void* stream) {
     clear_error();
     if (!m) return fail(ANELM_ERR_INVALID, "qwen3_reset: null model");
-    for (auto& l : m->layers) {
-        if (hipMemsetAsync(l.start, 0, sizeof(int32_t) * m->max_batch, anelm::as_stream(stream)) != hipSuccess ||
-            hipMemsetAsync(l.len, 0, sizeof(int32_t) * m->max_batch, anelm::as_stream(stream)) != hipSuccess)
-            return fail(ANELM_ERR_HIP, "qwen3_reset: hipMemsetAsync failed");
-    }
+    const size_t n = sizeof(int32_t) * m->layers.size() * m->max_batch;
+    if (hipMemsetAsync(m->ring_start, 0, n, anelm::as_stream(stream)) != hipSuccess ||
+        hipMemsetAsync(m->ring_len, 0, n, anelm::as_stream(stream)) != hipSuccess)
+        return fail(ANELM_ERR_HIP, "qwen3_reset: hipMemsetAsync failed");
     return ANELM_OK;
 }
 
@@ -288,7 +291,6 @@ extern "C" int anelm_qwen3_forward(anelm_qwen3* m, const int32_t* ids, const int
     if (batch <= 0 || batch > m->max_batch || ld_logits < c.vocab)
         return fail(ANELM_ERR_INVALID, "qwen3_forward: batch %ld (max %d) or ld_logits", batch, m->max_batch);
     const long H = c.hidden, I = c.intermediate, V = c.vocab, B = batch;
-    const int D = c.head_dim;
     const long seq = (long)m->cap * m->kvdim;
     int rc;
 #define CK(call)                      \
@@ -316,30 +318,30 @@ extern "C" int anelm_qwen3_forward(anelm_qwen3* m, const int32_t* ids, const int
             if ((r = anelm_f16_to_f32(out + b * ld_out, m->y16 + b * n_out, (size_t)n_out, stream))) return r;
         return ANELM_OK;
     };
-    // q/k norm + RoPE and the KV ring append, one launch (head_dim 128)
-    auto qk_append = [&](const anelm_qwen3::Layer& l) -> int {
-        return anelm_qknorm_rope_append(m->qkv, m->qkv + m->qdim, m->qkv + m->qdim + m->kvdim, m->qkvdim, m->qkvdim,
-                                        m->qkvdim, l.qn, l.kn, ANELM_BF16, pos, m->cos_tab, m->sin_tab, kRopeRows,
-                                        c.rope_theta, B, c.n_q_heads, c.n_kv_heads, c.rms_eps, l.kc, l.vc, l.start,
-                                        l.len, m->cap, seq, stream);
+    // q/k norm + RoPE, the KV ring append and the attention, one launch
+    // (head_dim 128) over the raw q|k|v rows; every layer's rings were
+    // advanced at the start of the step
+    auto attend = [&](const anelm_qwen3::Layer& l, void* out, int out_f16) -> int {
+        return anelm_gqa_attention_qk(out, out_f16, m->qkv, m->qkv + m->qdim, m->qkv + m->qdim + m->kvdim, m->qkvdim,
+                                      m->qkvdim, m->qkvdim, l.qn, l.kn, ANELM_BF16, pos, m->cos_tab, m->sin_tab,
+                                      kRopeRows, c.rope_theta, c.rms_eps, l.kc, l.vc, l.start, l.len, B, c.n_q_heads,
+                                      c.n_kv_heads, m->qdim, m->cap, seq, m->attn_ws, m->attn_ws_bytes, stream);
     };
     CK(anelm_embed_gather(m->x, m->embed, ANELM_BF16, ids, B, H, V, bad_ids, stream));             // :498
+    CK(anelm_kv_ring_advance(m->ring_start, m->ring_len, B, c.layers, m->max_batch, m->cap, stream));  // :475-484
     const bool dims32 = H % 32 == 0 && I % 32 == 0 && m->qdim % 32 == 0;
     if (dims32 && B > 16) {
         // Past 16 rows the RMSNorms round their output to fp16 once
         // (anelm_rmsnorm_f16) and the projections read fp16 rows; the SwiGLU
         // writes the down projection's fp16 input and the residual adds ride
-        // in the o and down projections: 8 calls per layer
+        // in the o and down projections: 7 calls per layer
         for (int L = 0; L < c.layers; L++) {
             const anelm_qwen3::Layer& l = m->layers[L];
             CK(anelm_rmsnorm_f16(m->a16, m->x, l.w_in, ANELM_BF16, B, (int)H, H, H, c.rms_eps, stream));  // :503
             CK(anelm_proj_f16_x16_fused(m->qkv, m->a16, l.qkv16, B, m->qkvdim, (int)H, H, m->qkvdim,
                                         ANELM_PROJ_STORE, stream));                               // first_proj
-            CK(qk_append(l));                                                                      // :444-488
             // the attention writes the o projection's fp16 input (y16 is free until the SwiGLU)
-            CK(anelm_gqa_attention_f16(m->y16, m->qkv, l.kc, l.vc, l.start, l.len, B, c.n_q_heads, c.n_kv_heads, D,
-                                       m->qkvdim, D, m->qdim, m->cap, seq, m->attn_ws, m->attn_ws_bytes,
-                                       stream));                                                  // :490
+            CK(attend(l, m->y16, 1));                                                             // :444-490
             CK(anelm_proj_f16_x16_fused(m->x, m->y16, l.o16, B, (int)H, m->qdim, m->qdim, H, ANELM_PROJ_ADD,
                                         stream));                                                 // o_proj + :516
             CK(anelm_rmsnorm_f16(m->a16, m->x, l.w_post, ANELM_BF16, B, (int)H, H, H, c.rms_eps, stream));  // :518
@@ -361,15 +363,13 @@ extern "C" int anelm_qwen3_forward(anelm_qwen3* m, const int32_t* ids, const int
         return ANELM_OK;
     }
     if (dims32) {
-        // 6 calls per layer: the RMSNorms, residual adds and the SwiGLU
+        // 5 calls per layer: the RMSNorms, residual adds and the SwiGLU
         // ride in the projections (anelm_proj_f16_fused)
         for (int L = 0; L < c.layers; L++) {
             const anelm_qwen3::Layer& l = m->layers[L];
             CK(anelm_proj_f16_fused(m->qkv, m->x, l.qkv16, B, m->qkvdim, (int)H, H, m->qkvdim, l.w_in, c.rms_eps,
                                     ANELM_PROJ_STORE, stream));                                   // :503 + first_proj
-            CK(qk_append(l));                                                                      // :444-488
-            CK(anelm_gqa_attention(m->attn, m->qkv, l.kc, l.vc, l.start, l.len, B, c.n_q_heads, c.n_kv_heads, D,
-                                   m->qkvdim, D, m->qdim, m->cap, seq, m->attn_ws, m->attn_ws_bytes, stream));  // :490
+            CK(attend(l, m->attn, 0));                                                            // :444-490
             CK(anelm_proj_f16_fused(m->x, m->attn, l.o16, B, (int)H, m->qdim, m->qdim, H, nullptr, 0.0f,
                                     ANELM_PROJ_ADD, stream));                                     // o_proj + :516
             CK(anelm_proj_f16_fused(m->h, m->x, l.gu16, B, (int)I, (int)H, H, I, l.w_post, c.rms_eps,
@@ -385,9 +385,7 @@ extern "C" int anelm_qwen3_forward(anelm_qwen3* m, const int32_t* ids, const int
         const anelm_qwen3::Layer& l = m->layers[L];
         CK(anelm_rmsnorm(m->xn, m->x, l.w_in, ANELM_BF16, B, (int)H, H, H, c.rms_eps, stream));    // :503
         CK(project(m->qkv, m->qkvdim, m->xn, H, l.qkv16, m->qkvdim));                             // first_proj
-        CK(qk_append(l));                                                                          // :444-488
-        CK(anelm_gqa_attention(m->attn, m->qkv, l.kc, l.vc, l.start, l.len, B, c.n_q_heads, c.n_kv_heads, D,
-                               m->qkvdim, D, m->qdim, m->cap, seq, m->attn_ws, m->attn_ws_bytes, stream));  // :490
+        CK(attend(l, m->attn, 0));                                                                // :444-490
         CK(project(m->o, H, m->attn, m->qdim, l.o16, H));                                         // o_proj
         CK(anelm_add_rmsnorm(m->x, m->o, m->xn, l.w_post, ANELM_BF16, B, (int)H, H, H, H, c.rms_eps,
                              stream));                                                            // :516-518

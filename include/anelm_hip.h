@@ -271,6 +271,32 @@ int anelm_gqa_attention_f16(uint16_t* out16, const float* q, const float* k_cach
                             const int32_t* ring_start, const int32_t* ring_len, long batch, int n_heads,
                             int n_kv_heads, int head_dim, long q_ld, int q_head_stride, long out_ld, int capacity,
                             long cache_seq_stride, void* workspace, size_t workspace_bytes, void* stream);
+/* The ring-state half of anelm_kv_ring_append (models/llm/qwen3.cpp:475-484)
+ * for groups x batch rings at once: ring g*group_stride + b (g < groups,
+ * b < batch) takes one row, its state advanced as the append does, the
+ * caches untouched.  With every layer's rings advanced this way before a
+ * decode step, each layer's anelm_gqa_attention_qk makes and stores the new
+ * row itself.  No counterpart in the reference. */
+int anelm_kv_ring_advance(int32_t* ring_start, int32_t* ring_len, long batch, int groups, long group_stride,
+                          int capacity, void* stream);
+/* anelm_qknorm_rope_append then anelm_gqa_attention (or _f16, out_f16 != 0)
+ * in one launch, head_dim 128, for rings that anelm_kv_ring_advance has
+ * already advanced: the new row's slot is (start + len - 1) mod capacity.
+ * q (q + b*q_ld, n_heads heads 128 apart), k and v (k + b*k_ld, v + b*v_ld,
+ * n_kv_heads heads) are the raw projection outputs and are not written; the
+ * q heads are normalised and rotated on the fly, and k (normalised, rotated)
+ * and v are stored into the new slot.  wq and wk are required and the RoPE
+ * table must hold at least one row (positions past it use the angle
+ * pos*inv_freq[j], as anelm_qknorm_rope does).  Outputs, caches and ring state equal
+ * the separate calls' bit for bit (models/llm/qwen3.cpp:444-488 then
+ * core/cpu_ops.cpp:173-240).  Workspace as anelm_gqa_attention's with
+ * head_dim 128.  No counterpart in the reference. */
+int anelm_gqa_attention_qk(void* out, int out_f16, const float* q, const float* k, const float* v, long q_ld,
+                           long k_ld, long v_ld, const void* wq, const void* wk, int w_dtype, const int32_t* pos,
+                           const float* cos_tab, const float* sin_tab, int tab_len, float theta, float eps,
+                           float* k_cache, float* v_cache, const int32_t* ring_start, const int32_t* ring_len,
+                           long batch, int n_heads, int n_kv_heads, long out_ld, int capacity,
+                           long cache_seq_stride, void* workspace, size_t workspace_bytes, void* stream);
 /* anelm_gqa_attention for callers that know an upper bound on every ring's
  * length (len_bound >= ring_len[b] for all b; e.g. the tokens decoded since
  * the rings were emptied): only ceil(len_bound / chunk) chunks per sequence
@@ -468,7 +494,8 @@ int anelm_proj_f16_fused(float* y, const float* x, const uint16_t* w16, long bat
 int anelm_proj_f16_x16_fused(void* y, const uint16_t* x16, const uint16_t* w16, long batch, int out_dim,
                              int in_dim, long ld_x, long ld_y, int epilogue, void* stream);
 
-/* Qwen3 model shape (the config.json fields of models/llm/qwen3.cpp:55-80). */
+/* Qwen3 model shape (the config.json fields of models/llm/qwen3.cpp:55-80);
+ * head_dim must be 128 (every Qwen3 size). */
 typedef struct anelm_qwen3_config {
     int hidden, layers, n_q_heads, n_kv_heads, head_dim, intermediate, vocab;
     float rope_theta, rms_eps;

@@ -157,6 +157,22 @@ def test_attention_argument_checks(lib):
     assert r(fake, fake, fake, fake, 32, 8, 128, 128, 0, 2049, 2048, fake, 1 << 30, None) == -2  # len > capacity
     assert r(fake, fake, fake, fake, 32, 8, 128, 128, 2048, 5, 2048, fake, 1 << 30, None) == -2  # start outside
     assert r(fake, fake, fake, fake, 32, 8, 128, 128, -1, 5, 2048, fake, 1 << 30, None) == -2
+    qk = lib.anelm_gqa_attention_qk
+
+    def call_qk(wq=fake, tab_len=4096, k_ld=48 * 128, batch=2, dt=2):
+        row = 48 * 128
+        return qk(fake, 1, fake, fake, fake, row, k_ld, row, wq, fake, dt, fake, fake, fake, tab_len, 1e6, 1e-6, fake,
+                  fake, fake, fake, batch, 32, 8, 32 * 128, 2048, 2048 * 8 * 128, fake, 1 << 30, None)
+
+    assert call_qk(wq=None) == -1 and b"gammas" in lib.anelm_last_error()    # the fused norm needs both gammas
+    assert call_qk(tab_len=0) == -1 and b"table" in lib.anelm_last_error()
+    assert call_qk(k_ld=1000) == -1                                            # k rows overlap
+    assert call_qk(dt=7) == -1
+    adv = lib.anelm_kv_ring_advance
+    assert adv(None, fake, 4, 2, 8, 2048, None) == -1
+    assert adv(fake, fake, 4, 2, 3, 2048, None) == -1                          # groups' rings overlap
+    assert adv(fake, fake, 4, 2, 8, 0, None) == -1
+    assert adv(fake, fake, 0, 2, 8, 2048, None) == 0                           # nothing to do
     a = lib.anelm_kv_ring_append
     assert a(fake, fake, None, fake, fake, fake, 1024, 1024, 4, 8, 128, 2048, 2048 * 1024, None) == -1
     assert a(fake, fake, fake, fake, fake, fake, 1000, 1024, 4, 8, 128, 2048, 2048 * 1024, None) == -1  # k_ld < row

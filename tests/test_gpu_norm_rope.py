@@ -261,3 +261,80 @@ def test_qknorm_rope_append_matches_separate_kernels(hip, orc, rng, B, nq, nk, c
     assert_bitexact(host(kc2), host(kc), "k cache")
     assert_bitexact(host(vc2), host(vc), "v cache")
     assert np.array_equal(host(rs2), host(rs)) and np.array_equal(host(rl2), host(rl))
+
+
+@pytest.mark.parametrize("B,nq,nk,cap,dt,out16", [
+    (1, 16, 8, 32, "bf16", False),     # one chunk (cap <= 32): the final-output launch
+    (3, 16, 8, 32, "f16", True),
+    (2, 32, 8, 4096, "bf16", False),   # split launch, short and long rings
+    (2, 16, 8, 4096, "f32", True),
+    (5, 64, 4, 512, "bf16", False),    # 16 q heads per kv head: two launches of 8
+    (4, 16, 8, 256, "f16", False),
+    (64, 16, 8, 1024, "bf16", True),   # Qwen3-0.6B attention shapes at 64 sequences
+])
+def test_gqa_attention_qk_matches_separate_kernels(hip, orc, rng, B, nq, nk, cap, dt, out16):
+    """Rings advanced once, then the fused q/k norm + RoPE + attention, equal
+    anelm_qknorm_rope_append then anelm_gqa_attention bit for bit: outputs,
+    both caches and ring state, over rings of random start and length (empty,
+    full and wrapped among them) and positions past the RoPE table; the raw
+    q|k|v rows are left unchanged."""
+    import torch
+
+    D = 128
+    row = (nq + 2 * nk) * D
+    qkv = rng.standard_normal((B, row), dtype=np.float32)
+    pos = rng.integers(0, 3000, B).astype(np.int32)
+    wq, _ = _gamma(rng, D, dt)
+    wk, _ = _gamma(rng, D, dt)
+    c_tab, s_tab = orc.rope_table(2048, D, THETA)
+    kc0 = rng.standard_normal((B, cap, nk * D), dtype=np.float32)
+    vc0 = rng.standard_normal((B, cap, nk * D), dtype=np.float32)
+    rs0 = rng.integers(-cap, 2 * cap, B).astype(np.int32)
+    rl0 = rng.integers(0, cap + 1, B).astype(np.int32)
+    rl0[0] = cap        # a full ring that wraps on this row
+    if B > 1:
+        rl0[1] = 0      # an empty ring
+    if B > 2:
+        rl0[2] = cap - 1
+    odt = torch.float16 if out16 else torch.float32
+    ws = torch.zeros(max(hip.gqa_workspace_size(B, nq, nk, D, cap), 16), dtype=torch.uint8, device="cuda")
+    tabs = (dev(pos), dev(c_tab), dev(s_tab))
+
+    a = dev(qkv)
+    kc, vc, rs, rl = dev(kc0), dev(vc0), dev(rs0), dev(rl0)
+    hip.qknorm_rope_append(a[:, :nq * D], a[:, nq * D:(nq + nk) * D], a[:, (nq + nk) * D:], wq, wk, *tabs, kc, vc,
+                           rs, rl, THETA, EPS, nq=nq, nk=nk)
+    ref = torch.full((B, nq * D), float("nan"), dtype=odt, device="cuda")
+    hip.gqa_attention(ref, a[:, :nq * D], kc, vc, rs, rl, nq, nk, D, ws)
+
+    b = dev(qkv)
+    kc2, vc2, rs2, rl2 = dev(kc0), dev(vc0), dev(rs0), dev(rl0)
+    hip.kv_ring_advance(rs2, rl2, cap)
+    got = torch.full((B, nq * D), float("nan"), dtype=odt, device="cuda")
+    hip.gqa_attention_qk(got, b[:, :nq * D], b[:, nq * D:(nq + nk) * D], b[:, (nq + nk) * D:], wq, wk, *tabs, kc2,
+                         vc2, rs2, rl2, nq, nk, ws, THETA, EPS)
+    assert_bitexact(host(got), host(ref), "attention output")
+    assert_bitexact(host(kc2), host(kc), "k cache")
+    assert_bitexact(host(vc2), host(vc), "v cache")
+    assert np.array_equal(host(rs2), host(rs)) and np.array_equal(host(rl2), host(rl))
+    assert_bitexact(host(b), qkv, "raw q|k|v rows")
+
+
+def test_kv_ring_advance_layers(hip, rng):
+    """Advancing [layers, max_batch] ring state for the first B sequences of
+    every layer equals one anelm_kv_ring_append per ring (state only), and
+    leaves the sequences past B alone."""
+    import torch
+
+    L, Bmax, B, cap, row = 5, 12, 9, 16, 8
+    rs0 = rng.integers(-cap, 2 * cap, (L, Bmax)).astype(np.int32)
+    rl0 = rng.integers(0, cap + 1, (L, Bmax)).astype(np.int32)
+    rs, rl = dev(rs0), dev(rl0)
+    hip.kv_ring_advance(rs, rl, cap, batch=B)
+    for l in range(L):
+        r_s, r_l = dev(rs0[l, :B]), dev(rl0[l, :B])
+        kc = torch.zeros(B, cap, row, device="cuda")
+        kv = torch.zeros(B, row, device="cuda")
+        hip.kv_ring_append(kc, kc.clone(), r_s, r_l, kv, kv)
+        assert np.array_equal(host(rs)[l, :B], host(r_s)) and np.array_equal(host(rl)[l, :B], host(r_l))
+    assert np.array_equal(host(rs)[:, B:], rs0[:, B:]) and np.array_equal(host(rl)[:, B:], rl0[:, B:])
