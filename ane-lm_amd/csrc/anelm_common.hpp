@@ -57,12 +57,19 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
-// sum over aligned groups of 16 lanes
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over aligned groups of 16 lanes (a DPP row), every lane of the group
+// active; each step adds a lane's value to its partner's, which holds the
+// same bits, so all 16 lanes end with the same sum.
 __device__ __forceinline__ float group16_sum(float v) {
-    v += __shfl_xor(v, 8, 16);
-    v += __shfl_xor(v, 4, 16);
-    v += __shfl_xor(v, 2, 16);
-    v += __shfl_xor(v, 1, 16);
+    v += dpp_f32<0xB1>(v);    // quad_perm [1,0,3,2]
+    v += dpp_f32<0x4E>(v);    // quad_perm [2,3,0,1]
+    v += dpp_f32<0x141>(v);   // row_half_mirror: the other quad of the half row
+    v += dpp_f32<0x140>(v);   // row_mirror: the other half row
     return v;
 }
 
