@@ -111,11 +111,25 @@ def build_dropin_check() -> str:
     return out
 
 
+def check_integration_doc() -> None:
+    """Compile every call INTEGRATION.md documents against the headers."""
+    cpp = os.path.join(ROOT, "tests", "cpp")
+    if not os.path.exists(os.path.join(cpp, "integration_doc.py")):
+        return
+    sys.path.insert(0, cpp)
+    try:
+        import integration_doc
+    finally:
+        sys.path.remove(cpp)
+    integration_doc.check()
+
+
 def build_all() -> None:
     build_oracle()
     build_lib()
     if os.path.exists(os.path.join(ROOT, "tests", "cpp", "dropin_check.cpp")):
         build_dropin_check()
+    check_integration_doc()
 
 
 if __name__ == "__main__":

@@ -7,9 +7,11 @@ A step is one pass of the op chain over all layers of the headline workload
   (1) RMSNorm  (2) q/k-norm + RoPE  (3) residual add + RMSNorm
   (4) SwiGLU   (5) residual add
 in the order of models/llm/qwen3.cpp:502-528, on synthetic device-resident
-inputs (distinct inputs per layer).  The step is captured once into a HIP
-graph and replayed, so host launch overhead is not measured.  `value` is the
-chain's algorithmic HBM bytes per step divided by the measured step time.
+inputs (distinct inputs per layer; the residual stream and the outputs rotate
+over four buffer sets, so every layer's traffic comes from HBM, not from the
+256 MB Infinity Cache).  The step is captured once into a HIP graph and
+replayed, so host launch overhead is not measured.  `value` is the chain's
+algorithmic HBM bytes per step divided by the measured step time.
 The same JSON line also reports the other configurations (0.6B decode and
 prefill, 4B batched decode, the sampling tail, the bf16->fp16 convert of the
 8.19 B-parameter set) and the CPU oracle timed on this host.
@@ -115,10 +117,20 @@ def time_region(fn, reps):
     return s.elapsed_time(e) / reps
 
 
-class Chain:
-    """Device buffers of one op-chain workload and its per-layer launches."""
+ROTATE_SETS = 4   # residual-stream / output buffer sets the prefill chains rotate over
 
-    def __init__(self, w, seed=0):
+
+class Chain:
+    """Device buffers of one op-chain workload and its per-layer launches.
+
+    With `sets` > 1 the residual stream x and the outputs xn, h rotate over
+    that many buffer sets from layer to layer (layer l uses set l % sets), so
+    no layer finds what the layer before it wrote still in the 256 MB
+    Infinity Cache: every layer's traffic then comes from HBM.  With one set
+    x is carried through all layers, as a model does, and at the 8B prefill
+    shape part of each layer's x, xn and h is then served from that cache."""
+
+    def __init__(self, w, seed=0, sets=1):
         import torch
 
         import anelm
@@ -128,9 +140,9 @@ class Chain:
         g = torch.Generator(device="cuda").manual_seed(seed)
         rn = lambda *s: torch.randn(*s, generator=g, device="cuda", dtype=torch.float32)
         gamma = lambda n: (1.0 + 0.02 * rn(n)).to(torch.float16)
-        self.x = rn(T, H)
-        self.xn = torch.empty(T, H, device="cuda")
-        self.h = torch.empty(T, I, device="cuda")
+        self.sets = [(rn(T, H), torch.empty(T, H, device="cuda"), torch.empty(T, I, device="cuda"))
+                     for _ in range(sets)]
+        self.x, self.xn, self.h = self.sets[0]
         self.layers = [dict(attn=rn(T, H), mlp=rn(T, H), q=rn(T, nq * D), k=rn(T, nk * D), g=rn(T, I), u=rn(T, I),
                             w_in=gamma(H), w_post=gamma(H), wq=gamma(D), wk=gamma(D)) for _ in range(L)]
         if w["positions"] == "sequential":
@@ -159,43 +171,69 @@ class Chain:
         else:
             hip.residual_add(self.x, Ld["mlp"])
 
-    def step(self):
+    def use_set(self, li):
+        self.x, self.xn, self.h = self.sets[li % len(self.sets)]
+
+    def step(self, rotate=True):
         if self.table is not None:
+            self.use_set(0)
             self.hip.embed_gather(self.x, self.table, self.ids)
-        for Ld in self.layers:
+        for li, Ld in enumerate(self.layers):
+            self.use_set(li if rotate else 0)
             for name in OPS:
                 self.op(name, Ld)
+        self.use_set(0)
 
 
-def measure_chain(w, steps, warmup, per_op):
+def prefill(w):
+    return w["positions"] == "sequential"
+
+
+def measure_chain(w, steps, warmup, per_op, chain_only=False):
+    """The op chain over all layers, graph-replayed.  Prefill workloads
+    rotate x, xn and h over ROTATE_SETS sets (the figures then measure HBM)
+    and also report the chain with one x carried through all layers
+    (`carried_x`, which includes Infinity-Cache reuse); decode workloads
+    carry x, as a decode step does (their buffers are cache-sized anyway)."""
     import torch
 
-    chain = Chain(w)
-    g = capture(chain.step)
-    for _ in range(warmup):
-        g.replay()
-    ms = time_region(g.replay, steps)
+    rotate = prefill(w)
+    chain = Chain(w, sets=ROTATE_SETS if rotate else 1)
     ob = op_bytes(w)
     layer_bytes = sum(ob.values())
     chain_bytes = layer_bytes * w["layers"] + gather_bytes(w)
-    r = dict(ms_per_step=round(ms, 4), us_per_layer_chain=round(ms * 1e3 / w["layers"], 3),
-             GBps=round(chain_bytes / ms / 1e6, 1), frac=round(chain_bytes / ms / 1e6 / HBM_PEAK_GBPS, 4),
-             tokens_per_s=round(w["T"] / (ms / 1e3), 1), chain_bytes=chain_bytes)
+
+    def run(rot):
+        g = capture(lambda: chain.step(rotate=rot))
+        for _ in range(warmup):
+            g.replay()
+        ms = time_region(g.replay, steps)
+        del g
+        return dict(ms_per_step=round(ms, 4), us_per_layer_chain=round(ms * 1e3 / w["layers"], 3),
+                    GBps=round(chain_bytes / ms / 1e6, 1), frac=round(chain_bytes / ms / 1e6 / HBM_PEAK_GBPS, 4),
+                    tokens_per_s=round(w["T"] / (ms / 1e3), 1))
+
+    r = run(rotate)
+    r["chain_bytes"] = chain_bytes
+    r["buffer_sets"] = len(chain.sets)
+    if rotate and not chain_only:
+        r["carried_x"] = dict(run(False), note="one x/xn/h carried through all layers: includes Infinity-Cache "
+                                              "reuse of what the previous layer wrote")
     if per_op:
-        # Each op alone over all layers.  The residual stream x and the
-        # outputs xn, h rotate over 4 sets, so no launch reads or rewrites
-        # what the launch before it left in the 256 MB Infinity Cache (one
-        # op's launch touches >= 256 MB at the 8B prefill shapes).
-        T, H, I = w["T"], w["H"], w["I"]
-        sets = [(chain.x, chain.xn, chain.h)] + [
-            (torch.randn(T, H, device="cuda"), torch.empty(T, H, device="cuda"), torch.empty(T, I, device="cuda"))
-            for _ in range(3)]
+        # Each op alone over all layers, x, xn and h rotating as in the
+        # chain: no launch reads or rewrites what the launch before it left
+        # in the 256 MB Infinity Cache (one op's launch touches >= 256 MB at
+        # the 8B prefill shapes).
+        if not rotate:
+            T, H, I = w["T"], w["H"], w["I"]
+            chain.sets += [(torch.randn(T, H, device="cuda"), torch.empty(T, H, device="cuda"),
+                            torch.empty(T, I, device="cuda")) for _ in range(ROTATE_SETS - 1)]
 
         def alone(name):
             for li, Ld in enumerate(chain.layers):
-                chain.x, chain.xn, chain.h = sets[li % 4]
+                chain.use_set(li)
                 chain.op(name, Ld)
-            chain.x, chain.xn, chain.h = sets[0]
+            chain.use_set(0)
 
         ops = {}
         for name in OPS:
@@ -206,8 +244,7 @@ def measure_chain(w, steps, warmup, per_op):
                              frac=round(ob[name] / t / 1e6 / HBM_PEAK_GBPS, 4), bytes=ob[name])
             del go
         r["ops"] = ops
-        del sets
-    del g, chain
+    del chain
     torch.cuda.empty_cache()
     return r
 
@@ -733,7 +770,7 @@ def pmc_summary(fetch_dir, write_dir, copy_fetch_dir, copy_write_dir, workload=H
         run_args = f"--only {workload} --steps 1"
     else:
         ob = op_bytes(WORKLOADS[workload])
-        run_args = (f"--workload {workload} --headline-only --no-cpu --steps 1 --warmup 0" if workload == HEADLINE
+        run_args = (f"--workload {workload} --chain-only --no-cpu --steps 1 --warmup 0" if workload == HEADLINE
                     else f"--only {workload} --steps 1 --warmup 0")
     commands = pmc_commands(fetch_dir, write_dir, copy_fetch_dir, copy_write_dir, run_args)
     lines = [f"# HBM traffic per dispatch, workload {workload} (rocprofv3 --pmc, one counter per run)", "#",
@@ -814,6 +851,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=8.0, help="CPU time budget of the headline baseline")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--headline-only", action="store_true", help="skip the other configurations")
+    ap.add_argument("--chain-only", action="store_true",
+                    help="headline: only the rotating chain (no carried-x chain, no per-op timing), for counter runs")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only time a 1 GiB device-to-device copy (reference for rocprof byte counters)")
     ap.add_argument("--only", default=None, help="measure only this named configuration and print it")
@@ -881,7 +920,10 @@ def main():
     if args.workload not in WORKLOADS:
         raise SystemExit(f"--workload {args.workload}: an op-chain workload is needed here ({', '.join(WORKLOADS)})")
     w = WORKLOADS[args.workload]
-    head = measure_chain(w, args.steps, args.warmup, per_op=True)
+    head = measure_chain(w, args.steps, args.warmup, per_op=not args.chain_only, chain_only=args.chain_only)
+    if args.chain_only:
+        print(json.dumps({args.workload: head}))
+        return
     ob = op_bytes(w)
     dom = max(OPS, key=lambda n: ob[n])
     roof = dict(bound="hbm", kernel=dom, achieved=head["ops"][dom]["GBps"], peak=HBM_PEAK_GBPS, unit="GB/s",
@@ -942,7 +984,8 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic: seeded device randn activations N(0,1), fp16 gammas 1+N(0,0.02), distinct inputs per layer",
+        "data": "synthetic: seeded device randn activations N(0,1), fp16 gammas 1+N(0,0.02), distinct inputs per "
+                "layer; residual stream and outputs rotating over 4 buffer sets (every layer's traffic from HBM)",
         "config": dict(workload=args.workload, tokens=w["T"], hidden=w["H"], q_heads=w["nq"], kv_heads=w["nk"],
                        head_dim=D, intermediate=w["I"], layers=w["layers"], rope_theta=THETA,
                        positions=w["positions"], launch="one HIP graph per step"),
@@ -950,6 +993,8 @@ def main():
         "us_per_layer_chain": head["us_per_layer_chain"],
         "tokens_per_s": head["tokens_per_s"],
         "chain_bytes_per_step": head["chain_bytes"],
+        "buffer_sets": head["buffer_sets"],
+        "carried_x": head.get("carried_x"),
         "roofline": roof,
         "cpu_baseline": cpu,
         "ops": head["ops"],

@@ -113,6 +113,14 @@ def test_full_8b_prefill_layer_sampled_rows(hip, orc, rng):
     assert_bitexact(host(x[ri]), xr, "residual stream")
     assert max_rel_err(host(xn[ri]), xnr) <= REL_TOL
     assert max_rel_err(host(h[ri]), hr) <= REL_TOL
-    # RoPE outputs: absolute error against the per-head output scale
-    for got, ref in ((host(q[ri]), qr), (host(k[ri]), kr)):
-        assert np.max(np.abs(got - ref)) <= REL_TOL * 4 * np.max(np.abs(ref))
+    # RoPE outputs, per element, relative to |a c| + |b s| of the normalised
+    # unrotated pair (a c - b s can cancel), as every other RoPE check
+    nq0, nk0 = orc.qknorm_rope(before["q"].copy(), before["k"].copy(), w32(wb["wq"]), w32(wb["wk"]),
+                               np.zeros(48, np.int32), None, None, THETA, nq, nk, D)
+    inv = orc.rope_inv_freq(D, THETA)
+    ang = (pos[rows].astype(np.float32)[:, None] * inv[None, :]).astype(np.float64)
+    c, s = np.cos(ang)[:, None, :], np.sin(ang)[:, None, :]
+    assert max_rel_err(host(q[ri]).reshape(48, nq, D), qr.reshape(48, nq, D),
+                       rope_den(nq0.reshape(48, nq, D), c, s, 64)) <= REL_TOL
+    assert max_rel_err(host(k[ri]).reshape(48, nk, D), kr.reshape(48, nk, D),
+                       rope_den(nk0.reshape(48, nk, D), c, s, 64)) <= REL_TOL

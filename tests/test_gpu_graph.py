@@ -96,19 +96,21 @@ def test_sampler_graph_replays_match_eager(hip, rng):
         assert np.array_equal(host(pr_e).view(np.uint32), host(pr_g).view(np.uint32)), f"replay {rep}: probs"
 
 
-@pytest.mark.parametrize("B,steps", [(1, 140), (3, 30), (20, 24)])
-def test_decode_step_graph_replays_match_eager(hip, rng, tmp_path, B, steps):
+@pytest.mark.parametrize("B,steps,V", [(1, 140, 300), (3, 30, 300), (20, 24, 300), (20, 8, 70000), (9, 8, 300)])
+def test_decode_step_graph_replays_match_eager(hip, rng, tmp_path, B, steps, V):
     """The Qwen3 decode step captured once (positions advanced inside the
     graph, as bench.py runs it) gives on every replay the logits of the same
     step run eagerly on a twin model, bit for bit: one sequence (dot-kernel
     projections; its rings pass the 128-row whole-ring limit of the
-    attention), three (MFMA) and twenty (fp16-row projections, fp16
-    attention output)."""
+    attention), three (MFMA), twenty (fp16-row projections, fp16
+    attention output), twenty with a 70000-row LM head (the branch of
+    Qwen3's 151936-row vocabulary), and nine with an intermediate size that
+    is not a multiple of 32 (the per-op branch)."""
     import torch
 
     from helpers import save_qwen3, tiny_qwen3
 
-    t, d = tiny_qwen3(rng, tied=False)
+    t, d = tiny_qwen3(rng, tied=False, V=V, I=336 if B == 9 else 384)
     path = tmp_path / "tiny.safetensors"
     save_qwen3(path, t)
     cfg = hip.Qwen3Config(d["H"], d["L"], d["nq"], d["nk"], d["D"], d["I"], d["V"], 1e6, 1e-6)

@@ -30,7 +30,8 @@ def test_f32_to_f16_rne_bitexact(hip, orc, rng):
     assert np.all((got[nan] & 0x7C00) == 0x7C00) and np.all(got[nan] & 0x3FF)
 
 
-@pytest.mark.parametrize("B,out_dim,in_dim", [(1, 4096, 1024), (64, 1024, 2048), (3, 77, 100), (17, 3072, 1024)])
+@pytest.mark.parametrize("B,out_dim,in_dim", [(1, 4096, 1024), (64, 1024, 2048), (3, 77, 100), (17, 3072, 1024),
+                                               (64, 151936, 1024), (20, 70000, 256)])
 def test_linear_f16_within_one_ulp(hip, orc, rng, B, out_dim, in_dim):
     import torch
 
@@ -297,3 +298,54 @@ def test_proj_fused_strided_rows(hip, orc, rng, B, out_dim, in_dim):
     got = host(yb)
     assert np.all(np.abs(got[:, 4:4 + out_dim].astype(np.float64) - want) <= tol)
     assert np.all(got[:, :4] == -7.0) and np.all(got[:, 4 + out_dim:] == -7.0)
+
+
+def _decode_vs_oracle(hip, orc, rng, path, t, d, B, steps, cap=16, ld_pad=0):
+    """`steps` decode steps of B sequences through anelm_qwen3_forward
+    against the oracle's step; logits land in a [B, V + ld_pad] buffer whose
+    padding columns must stay untouched.  Returns the worst row error
+    relative to the row's logit scale."""
+    import torch
+
+    cfg = hip.Qwen3Config(d["H"], d["L"], d["nq"], d["nk"], d["D"], d["I"], d["V"], 1e6, 1e-6)
+    ocfg = orc.Qwen3Config(d["H"], d["L"], d["nq"], d["nk"], d["D"], d["I"], d["V"], 1e6, 1e-6)
+    model = hip.Qwen3Model(path, cfg, max_batch=B, kv_capacity=cap)
+    ref = orc.Qwen3(ocfg, t, B, cap)
+    V = d["V"]
+    buf = torch.full((B, V + ld_pad), -3.0, device="cuda")
+    logits = buf[:, :V]
+    pos0 = np.resize(np.array([0, 100, 20000]), B)    # every third sequence uses the RoPE fallback
+    worst = 0.0
+    for s in range(steps):
+        ids = rng.integers(0, V, B).astype(np.int32)
+        pos = (pos0 + s).astype(np.int32)
+        model.forward(dev(ids), dev(pos), logits)
+        want = ref.forward(ids, pos)
+        got = host(buf)
+        assert np.all(got[:, V:] == -3.0), "logits padding written"
+        err = np.max(np.abs(got[:, :V] - want), axis=1) / np.max(np.abs(want), axis=1)
+        worst = max(worst, float(err.max()))
+    model.close()
+    return worst
+
+
+@pytest.mark.parametrize("B,ld_pad", [(17, 0), (20, 0), (20, 40)])
+def test_decode_big_vocab_past_16_rows(hip, orc, rng, tmp_path, B, ld_pad):
+    """The LM-head branch that Qwen3's 151936-row vocabulary takes with more
+    than 16 sequences (vocab above 65536), with the logits rows contiguous
+    (ld_logits == V) and strided (ld_logits > V); the rings wrap."""
+    t, d = tiny_qwen3(rng, V=70000, tied=False)
+    path = tmp_path / "bigvocab.safetensors"
+    save_qwen3(path, t)
+    assert _decode_vs_oracle(hip, orc, rng, path, t, d, B, steps=18, cap=16, ld_pad=ld_pad) < 4e-3
+
+
+@pytest.mark.parametrize("B", [3, 9, 20])
+def test_decode_dims_not_multiples_of_32(hip, orc, rng, tmp_path, B):
+    """Hidden and intermediate sizes that are not multiples of 32 (H 224 is,
+    I 336 is not): the decode step's per-op branch, whose projections with
+    336 inputs cannot take 32-input MFMA steps whole."""
+    t, d = tiny_qwen3(rng, H=224, I=336, V=500, tied=True)
+    path = tmp_path / "odd.safetensors"
+    save_qwen3(path, t)
+    assert _decode_vs_oracle(hip, orc, rng, path, t, d, B, steps=18, cap=16, ld_pad=8) < 4e-3
