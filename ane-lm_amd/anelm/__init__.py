@@ -72,6 +72,7 @@ _SIGS = {
     "anelm_softmax": (_I, [_P, _L, _L, _L, _P, _S, _P]),
     "anelm_sample_workspace_size": (_S, [_L, _L]),
     "anelm_sample": (_I, [_P, _P, _L, _P, _L, _L, _L, _P, _L, _P, ctypes.POINTER(SamplingParams), _P, _P, _S, _P]),
+    "anelm_sample_noalloc": (_I, [_P, _P, _L, _P, _L, _L, _L, _P, _L, _P, ctypes.POINTER(SamplingParams), _P, _P]),
     "anelm_gqa_workspace_size": (_S, [_L, _I, _I, _I, _I]),
     "anelm_gqa_attention": (_I, [_P, _P, _P, _P, _P, _P, _L, _I, _I, _I, _L, _I, _L, _I, _L, _P, _S, _P]),
     "anelm_gqa_attention_f16": (_I, [_P, _P, _P, _P, _P, _P, _L, _I, _I, _I, _L, _I, _L, _I, _L, _P, _S, _P]),
@@ -328,6 +329,17 @@ def sample(ids, probs, logits, hist, hist_len, params: SamplingParams, r, worksp
                               _ptr(hist) if hist_ld else None, hist_ld, _ptr(hist_len), ctypes.byref(params),
                               _ptr(r), _ptr(workspace), workspace.numel() * workspace.element_size(),
                               _stream(stream)))
+
+
+def sample_noalloc(ids, probs, logits, hist, hist_len, params: SamplingParams, r, stream=None):
+    """anelm_sample without a workspace: the library's static per-GPU scratch
+    (4 MiB) serves instead; calls that overlap on one GPU race."""
+    rows, vocab, ldl = _rows(logits)
+    ldp = _ld(probs) if probs is not None else 0
+    hist_ld = _ld(hist) if hist is not None and hist.numel() else 0
+    _check(lib().anelm_sample_noalloc(_ptr(ids), _ptr(probs), ldp, _ptr(logits), ldl, rows, vocab,
+                                      _ptr(hist) if hist_ld else None, hist_ld, _ptr(hist_len), ctypes.byref(params),
+                                      _ptr(r), _stream(stream)))
 
 
 def gqa_workspace_size(batch, n_heads, n_kv_heads, head_dim, capacity) -> int:

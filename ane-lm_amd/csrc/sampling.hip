@@ -22,6 +22,7 @@
 
 #include <climits>
 #include <cmath>
+#include <mutex>
 
 #include "anelm_common.hpp"
 
@@ -1114,21 +1115,24 @@ extern "C" int anelm_softmax(float* x, long rows, long n, long ld, void* workspa
     return launch_status("softmax");
 }
 
-extern "C" int anelm_sample(int32_t* ids, float* probs, long ld_probs, const float* logits, long ld_logits,
-                            long rows, long vocab, const int32_t* hist, long hist_ld, const int32_t* hist_len,
-                            const anelm_sampling_params* params, const float* r, void* workspace,
-                            size_t workspace_bytes, void* stream) {
-    if (!ids || !logits || !params) return fail(ANELM_ERR_INVALID, "anelm_sample: null pointer");
+namespace anelm {
+namespace {
+
+// The sampler behind both entry points; `who` names the caller in errors.
+int sample_impl(int32_t* ids, float* probs, long ld_probs, const float* logits, long ld_logits, long rows, long vocab,
+                const int32_t* hist, long hist_ld, const int32_t* hist_len, const anelm_sampling_params* params,
+                const float* r, void* workspace, size_t workspace_bytes, void* stream, const char* who) {
+    if (!ids || !logits || !params) return fail(ANELM_ERR_INVALID, "%s: null pointer", who);
     if (rows <= 0 || rows > 65535 || vocab <= 0 || vocab > (1L << 30))
-        return fail(ANELM_ERR_INVALID, "anelm_sample: rows=%ld vocab=%ld", rows, vocab);
-    if (ld_logits < vocab) return fail(ANELM_ERR_INVALID, "anelm_sample: ld_logits < vocab");
-    if (probs && ld_probs < vocab) return fail(ANELM_ERR_INVALID, "anelm_sample: ld_probs < vocab");
-    if (hist_ld < 0 || (hist_ld > 0 && !hist)) return fail(ANELM_ERR_INVALID, "anelm_sample: history");
+        return fail(ANELM_ERR_INVALID, "%s: rows=%ld vocab=%ld", who, rows, vocab);
+    if (ld_logits < vocab) return fail(ANELM_ERR_INVALID, "%s: ld_logits < vocab", who);
+    if (probs && ld_probs < vocab) return fail(ANELM_ERR_INVALID, "%s: ld_probs < vocab", who);
+    if (hist_ld < 0 || (hist_ld > 0 && !hist)) return fail(ANELM_ERR_INVALID, "%s: history", who);
     const bool sampling = params->temperature > 0.0f;
-    if (sampling && !r) return fail(ANELM_ERR_INVALID, "anelm_sample: r is required when temperature > 0");
-    if (sampling && !probs) return fail(ANELM_ERR_INVALID, "anelm_sample: probs is required when temperature > 0");
+    if (sampling && !r) return fail(ANELM_ERR_INVALID, "%s: r is required when temperature > 0", who);
+    if (sampling && !probs) return fail(ANELM_ERR_INVALID, "%s: probs is required when temperature > 0", who);
     SampleArgs a = {};
-    int rc = bind_workspace(a, workspace, workspace_bytes, rows, vocab, "anelm_sample");
+    int rc = bind_workspace(a, workspace, workspace_bytes, rows, vocab, who);
     if (rc) return rc;
     a.logits = logits;
     a.ld_logits = ld_logits;
@@ -1163,4 +1167,66 @@ extern "C" int anelm_sample(int32_t* ids, float* probs, long ld_probs, const flo
     sample_stage3_kernel<<<grd, 256, 0, st>>>(a, vec_out);
     sample_walk_kernel<<<dim3((unsigned)rows), 64, 0, st>>>(a);
     return launch_status("sample");
+}
+
+// ---- the allocation-free sampler's scratch ---------------------------------
+// The sampler's workspace as a static device array: every GPU the library
+// runs on holds its own copy (kScratchBytes) until the process ends.  Host
+// code never passes the array's name to a kernel or a copy (on the host it
+// is only a stand-in symbol): each device's address is looked up once with
+// hipGetSymbolAddress, with that device current, and kept in scratch_ptr.
+// Nothing in it needs clearing: every word a kernel reads is written earlier
+// in the same call.  Calls that overlap on one GPU share it, and race.
+constexpr size_t kScratchBytes = 4u << 20;   // 188 rows at Qwen3's 151936-row vocabulary
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+void* scratch_ptr[kMaxDevices];
+std::mutex scratch_mu;
+
+// this device's scratch address (looked up on its first call), or nullptr
+// with the error set
+void* device_scratch(const char* who) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        fail(ANELM_ERR_HIP, "%s: no usable current device (%d)", who, dev);
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(scratch_mu);
+    if (!scratch_ptr[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            fail(ANELM_ERR_HIP, "%s: hipGetSymbolAddress of the scratch array failed on device %d: %s", who, dev,
+                 hipGetErrorString(e));
+            return nullptr;
+        }
+        scratch_ptr[dev] = p;
+    }
+    return scratch_ptr[dev];
+}
+
+}  // namespace
+}  // namespace anelm
+
+extern "C" int anelm_sample(int32_t* ids, float* probs, long ld_probs, const float* logits, long ld_logits,
+                            long rows, long vocab, const int32_t* hist, long hist_ld, const int32_t* hist_len,
+                            const anelm_sampling_params* params, const float* r, void* workspace,
+                            size_t workspace_bytes, void* stream) {
+    return sample_impl(ids, probs, ld_probs, logits, ld_logits, rows, vocab, hist, hist_ld, hist_len, params, r,
+                       workspace, workspace_bytes, stream, "anelm_sample");
+}
+
+extern "C" int anelm_sample_noalloc(int32_t* ids, float* probs, long ld_probs, const float* logits, long ld_logits,
+                                    long rows, long vocab, const int32_t* hist, long hist_ld, const int32_t* hist_len,
+                                    const anelm_sampling_params* params, const float* r, void* stream) {
+    clear_error();
+    if (rows > 0 && vocab > 0 && rows <= 65535 && vocab <= (1L << 30) && ws_layout(rows, vocab).total > kScratchBytes)
+        return fail(ANELM_ERR_WORKSPACE,
+                    "anelm_sample_noalloc: %ld rows x %ld logits need %zu bytes of scratch; the static scratch holds "
+                    "%zu (use anelm_sample with a workspace)",
+                    rows, vocab, ws_layout(rows, vocab).total, kScratchBytes);
+    void* ws = device_scratch("anelm_sample_noalloc");
+    if (!ws) return ANELM_ERR_HIP;
+    return sample_impl(ids, probs, ld_probs, logits, ld_logits, rows, vocab, hist, hist_ld, hist_len, params, r, ws,
+                       kScratchBytes, stream, "anelm_sample_noalloc");
 }

@@ -225,6 +225,21 @@ int anelm_sample(int32_t* ids, float* probs, long ld_probs, const float* logits,
                  long rows, long vocab, const int32_t* hist, long hist_ld,
                  const int32_t* hist_len, const anelm_sampling_params* params, const float* r,
                  void* workspace, size_t workspace_bytes, void* stream);
+/* anelm_sample for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc):
+ * the same kernels and results, with the workspace taken from a static
+ * 4 MiB device array the library holds on every GPU it runs on until the
+ * process ends, so it calls no allocator.  Limit:
+ * anelm_sample_workspace_size(rows, vocab) <= 4 MiB (188 rows at a 151936-row
+ * vocabulary); larger calls return ANELM_ERR_WORKSPACE.  Every call on one GPU
+ * shares that GPU's array: calls that overlap on one GPU (on different
+ * streams, or from different threads) race and must not be issued.  The
+ * first call on a device looks the array's address up (hipGetSymbolAddress).
+ * No counterpart in the reference (its sample_token allocates per call). */
+int anelm_sample_noalloc(int32_t* ids, float* probs, long ld_probs, const float* logits, long ld_logits,
+                         long rows, long vocab, const int32_t* hist, long hist_ld,
+                         const int32_t* hist_len, const anelm_sampling_params* params, const float* r,
+                         void* stream);
 
 /* ------------------------------------------------ KV ring and attention */
 
