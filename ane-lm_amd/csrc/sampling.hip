@@ -63,6 +63,7 @@ struct SampleArgs {
     int nsub_ld;          // row stride of the sub-tile arrays: nsub rounded up to 4 (16-byte rows)
     int shift;
     int vec_probs;        // probs rows are 16-byte aligned
+    float skip_margin;    // stage 3 makes no maps for sub-tiles predicted to start this far past r
 };
 
 // ---- exp with a fixed IEEE operation sequence ----------------------------
@@ -90,9 +91,12 @@ __device__ __forceinline__ float sampler_expf(float x) {
     p = fmaf(p, r, 0x1p-1f);
     p = fmaf(p, r, 1.0f);
     p = fmaf(p, r, 1.0f);
-    const float sub = (p * pow2i(k + 64)) * pow2i(-64);  // k < -126: rounded once, as a subnormal
-    const float big = (p * pow2i(k - 1)) * 2.0f;         // k > 127
-    float y = k < -126 ? sub : (k > 127 ? big : p * pow2i(k));
+    // p * 2^k in two exact-or-once-rounded multiplies, without a branch:
+    // k < -126: (p * 2^(k+64)) * 2^-64, rounded once as a subnormal;
+    // k > 127:  (p * 2^(k-1)) * 2;  otherwise (p * 2^k) * 1
+    const int ka = k < -126 ? k + 64 : (k > 127 ? k - 1 : k);
+    const float sa = k < -126 ? 0x1p-64f : (k > 127 ? 2.0f : 1.0f);
+    float y = (p * pow2i(ka)) * sa;
     y = x < -104.0f ? 0.0f : y;
     y = x > 89.0f ? INFINITY : y;
     return x != x ? x : y;
@@ -103,15 +107,24 @@ __device__ __forceinline__ float sampler_expf(float x) {
 // sampling.cpp:17) for i in [c0, c0 + n), ids outside [0, vocab) ignored
 // (sampling.cpp:23).
 __device__ void build_counts(uint32_t* cnt, int n, const SampleArgs& a, long row, long c0) {
+    // this thread's first window entry is loaded before the LDS is cleared,
+    // so its latency overlaps the clearing and the barrier
+    long hl = 0, start = 0;
+    int id0 = -1;
+    const int32_t* h = a.hist + row * a.hist_ld;
+    if (a.use_penalty) {
+        hl = a.hist_len ? (long)a.hist_len[row] : a.hist_ld;
+        if (hl > a.hist_ld) hl = a.hist_ld;
+        start = hl - a.ctx;
+        if (start < 0) start = 0;
+        const long j = start + threadIdx.x;
+        if (j < hl) id0 = h[j];
+    }
     for (int i = threadIdx.x; i < n; i += blockDim.x) cnt[i] = 0u;
     __syncthreads();
     if (a.use_penalty) {
-        long hl = a.hist_len ? (long)a.hist_len[row] : a.hist_ld;
-        if (hl > a.hist_ld) hl = a.hist_ld;
-        long start = hl - a.ctx;
-        if (start < 0) start = 0;
-        const int32_t* h = a.hist + row * a.hist_ld;
-        for (long j = start + threadIdx.x; j < hl; j += blockDim.x) {
+        if (id0 >= 0 && id0 < a.vocab && id0 >= c0 && id0 < c0 + n) atomicAdd(&cnt[id0 - c0], 1u);
+        for (long j = start + threadIdx.x + blockDim.x; j < hl; j += blockDim.x) {
             const int id = h[j];
             if (id >= 0 && id < a.vocab && id >= c0 && id < c0 + n) atomicAdd(&cnt[id - c0], 1u);
         }
@@ -366,6 +379,48 @@ __device__ __forceinline__ Fn wave_scan(Fn v) {
     return v;
 }
 
+// The same scan when no lane's map depends on the parity (a0 == a1 in every
+// lane, i.e. no exact rounding tie): composition is then saturating
+// addition, which is associative and commutative on [0, kSat].
+template <int CTRL, int ROWMASK>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROWMASK, 0xF, false);
+}
+__device__ __forceinline__ uint32_t wave_scan_sat(uint32_t v) {
+    v = sat_add(dpp_u32<0x111, 0xF>(v), v);
+    v = sat_add(dpp_u32<0x112, 0xF>(v), v);
+    v = sat_add(dpp_u32<0x114, 0xF>(v), v);
+    v = sat_add(dpp_u32<0x118, 0xF>(v), v);
+    v = sat_add(dpp_u32<0x142, 0xA>(v), v);
+    v = sat_add(dpp_u32<0x143, 0xC>(v), v);
+    return v;
+}
+
+// In-order scan of per-lane maps, the cheap way when the wave has no tie.
+__device__ __forceinline__ Fn wave_scan_any(Fn v) {
+    if (__ballot(v.a0 != v.a1) == 0) {
+        const uint32_t t = wave_scan_sat(v.a0);
+        return Fn{t, t};
+    }
+    return wave_scan(v);
+}
+
+// A lane's four element maps composed in order, and the wave's inclusive
+// scan of those compositions; `tie` says whether any map had a0 != a1.
+__device__ __forceinline__ Fn compose4_scan(const Fn f[4]) {
+    bool tie = false;
+#pragma unroll
+    for (int j = 0; j < 4; j++) tie = tie || f[j].a0 != f[j].a1;
+    if (__ballot(tie) == 0) {
+        const uint32_t t = wave_scan_sat(sat_add(sat_add(f[0].a0, f[1].a0), sat_add(f[2].a0, f[3].a0)));
+        return Fn{t, t};
+    }
+    Fn acc = {0u, 0u};
+#pragma unroll
+    for (int j = 0; j < 4; j++) acc = compose(acc, f[j]);
+    return wave_scan(acc);
+}
+
 // ---- stage 1: penalties, 1/T, chunk max (T > 0) or chunk argmax (T <= 0) ----
 template <bool ARGMAX>
 __global__ __launch_bounds__(256) void sample_stage1_kernel(SampleArgs a, int vec) {
@@ -496,6 +551,24 @@ __global__ __launch_bounds__(256) void sample_stage2_kernel(SampleArgs a, int ve
     float* out = a.probs + row * a.ld_probs;
     uint64_t acc = 0;
     int nan = 0;
+    if (nvalid == kCH && vec_out) {
+        // a whole chunk: no per-element bounds (a guard per element compiled
+        // to an exec-mask branch per element)
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            float ev[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float x = sampler_expf(v[4 * k + e] + neg);
+                ev[e] = x;
+                const bool ok = x >= 0.0f && x <= 1.0f;
+                acc += ok ? (uint64_t)(x * scale) : 0u;
+                nan |= ok ? 0 : 1;
+            }
+            // cached store: stage 3 reads these back
+            *reinterpret_cast<float4*>(out + c0 + k * 1024 + 4 * threadIdx.x) = make_float4(ev[0], ev[1], ev[2], ev[3]);
+        }
+    } else {
 #pragma unroll
     for (int k = 0; k < 4; k++) {
         float ev[4];
@@ -516,6 +589,7 @@ __global__ __launch_bounds__(256) void sample_stage2_kernel(SampleArgs a, int ve
             for (int e = 0; e < 4; e++)
                 if (i + e < a.vocab) out[i + e] = ev[e];
         }
+    }
     }
     acc = wave_sum_u64(acc);
     nan = __any(nan) ? 1 : 0;
@@ -600,15 +674,15 @@ __device__ __forceinline__ Crossing predict_crossing(Fn acc, const Fn f[4], cons
     const uint32_t c2 = __float_as_uint(c);
     const int cls2 = c2 < 0x00800000u ? 0 : (int)(c2 >> 23);
     const Binade b2 = binade_of_class(cls2);
-    Fn g = {0u, 0u};
+    Fn gf[4];
 #pragma unroll
     for (int j = 0; j < 4; j++) {
         const int o = 4 * lane + j;
         const Fn m = elem_map(p[j], b2);
         const bool in = o > jstar && o < nv;
-        g = compose(g, Fn{in ? m.a0 : 0u, in ? m.a1 : 0u});
+        gf[j] = Fn{in ? m.a0 : 0u, in ? m.a1 : 0u};
     }
-    g = wave_scan(g);
+    const Fn g = compose4_scan(gf);
     x.sfx.a0 = (uint32_t)__builtin_amdgcn_readlane((int)g.a0, 63);
     x.sfx.a1 = (uint32_t)__builtin_amdgcn_readlane((int)g.a1, 63);
     const uint32_t m2 = cls2 == 0 ? c2 : ((c2 & 0x7FFFFFu) | 0x800000u);
@@ -618,7 +692,7 @@ __device__ __forceinline__ Crossing predict_crossing(Fn acc, const Fn f[4], cons
 }
 
 __device__ bool walk_subtile_p(const float p[4], long base, long V, float r, uint32_t& cb, long& result);
-__device__ bool walk_serial_p(const float p[4], long base, long V, float r, uint32_t& cb, long& result);
+__device__ bool walk_first_lds(const float* sp, long V, float r, uint32_t& cb, long& result);
 
 // ---- stage 3: probabilities and sub-tile maps --------------------------------
 // Wave w's part of k-slice k is the 256 consecutive logits c0 + k*1024 + w*256 +
@@ -632,6 +706,7 @@ __global__ __launch_bounds__(256) void sample_stage3_kernel(SampleArgs a, int ve
     __shared__ uint64_t red_s[4], red_p[4];
     __shared__ int red_f[4];
     __shared__ float ksum[4][4];  // [k][wave] fp32 sums of exp (prediction only)
+    __shared__ __align__(16) float s_first[kSub];  // sub-tile 0's probabilities for its one-lane walk
     // Workgroups in dispatch order take chunk 0 of every row first: those
     // also walk sub-tile 0 (below), the longest job, so it starts early.
     const long lin = (long)blockIdx.y * gridDim.x + blockIdx.x;
@@ -670,27 +745,48 @@ __global__ __launch_bounds__(256) void sample_stage3_kernel(SampleArgs a, int ve
     }
     // Sub-tile 0 starts from an exact running sum, 0, and crosses a binade
     // at about every doubling of its element count: a dozen restarts of the
-    // exact walk.  The first wave of each row's first workgroup (dispatched
-    // first) walks it here, at raised issue priority, while the rest of the
-    // grid runs, instead of on the walk kernel's one-wave critical path.
+    // map-based walk.  Lane 0 of each row's first workgroup (dispatched
+    // first) walks it here instead, one fp32 add at a time from LDS, at raised
+    // issue priority, while the rest of the grid runs (and the workgroup's
+    // other waves make their maps), off the walk kernel's critical path.
+    __syncthreads();  // ksum complete; the other waves need not wait for the walk below
     if (chunk == 0 && wid == 0 && a.r) {
         __builtin_amdgcn_s_setprio(3);
-        uint32_t cb = 0u;
-        long result = -1;
-        const bool done = walk_serial_p(&p[0], 0, a.vocab, a.r[row], cb, result);
+        *reinterpret_cast<float4*>(&s_first[4 * lane]) = make_float4(p[0], p[1], p[2], p[3]);
+        // the wave's LDS writes complete before its lane 0 reads them back
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         if (lane == 0) {
+            uint32_t cb = 0u;
+            long result = -1;
+            const bool done = walk_first_lds(s_first, a.vocab, a.r[row], cb, result);
             a.ws_first[2 * row] = done ? (int32_t)result : -1;
             a.ws_first[2 * row + 1] = (int32_t)cb;
         }
         __builtin_amdgcn_s_setprio(0);
     }
-    __syncthreads();
+    const float rdraw = a.r ? a.r[row] : 0.0f;
     float run = prefix;  // running prediction, the same order of additions in every wave
 #pragma unroll
     for (int k = 0; k < 4; k++) {
         float here = run;
         for (int w = 0; w < wid; w++) here = here + ksum[k][w];
         const float cpred = here * inv;
+        const long st = (long)chunk * 16 + 4 * k + wid;
+        // No map where the walk does not arrive: without a draw (softmax), or
+        // when the sub-tile is predicted to start more than skip_margin past
+        // r (the sequential sum is within V * 2^-25 of the exact prefix, so
+        // the draw has ended before it).  A wrong prediction costs the walk an
+        // exact walk of the sub-tile (class -1, no crossing), never a result.
+        if (!a.r || cpred >= rdraw + a.skip_margin) {   // wave-uniform
+            if (a.r && lane == 63 && st < a.nsub) {
+                a.ws_cls[row * a.nsub_ld + st] = -1;
+                a.ws_xing[(row * a.nsub_ld + st) * kXWords + 5] = 0xFFFFFFFFu;
+            }
+            run = run + ((ksum[k][0] + ksum[k][1]) + (ksum[k][2] + ksum[k][3]));
+            continue;
+        }
         const uint32_t cb = __float_as_uint(cpred);
         const bool ok = cpred == cpred && cpred < INFINITY;
         const int cls = ok ? (cb < 0x00800000u ? 0 : (int)(cb >> 23)) : -1;
@@ -698,17 +794,14 @@ __global__ __launch_bounds__(256) void sample_stage3_kernel(SampleArgs a, int ve
         const int nv = a.vocab - (c0 + k * 1024 + 256 * wid) < kSub ? (int)(a.vocab - (c0 + k * 1024 + 256 * wid))
                                                                      : kSub;  // valid elements of the sub-tile
         Fn f[4];
-        Fn acc = {0u, 0u};
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const Fn m = elem_map(p[4 * k + j], b);
             const bool in = 4 * lane + j < nv;
             f[j].a0 = in ? m.a0 : 0u;
             f[j].a1 = in ? m.a1 : 0u;
-            acc = compose(acc, f[j]);
         }
-        acc = wave_scan(acc);
-        const long st = (long)chunk * 16 + 4 * k + wid;
+        const Fn acc = compose4_scan(f);
         const Crossing x = predict_crossing(acc, f, &p[4 * k], nv, ok, cb, cls, b);
         if (lane == 63 && st < a.nsub) {
             a.ws_map0[row * a.nsub_ld + st] = acc.a0;
@@ -836,27 +929,36 @@ __device__ __forceinline__ bool pass_crossing(uint32_t& cb, const uint32_t* x, i
 // scan of their maps; an element that leaves the binade is added with an
 // ordinary fp32 add and the scan restarts after it.  Returns true when the
 // draw is decided (result set), else updates cb to the sub-tile's end.
-// The whole sub-tile one fp32 add at a time in index order (the reference's
-// loop itself), four per step from one lane's registers; p, base, V as below.
-__device__ bool walk_serial_p(const float p[4], long base, long V, float r, uint32_t& cb, long& result) {
-    const int nvalid = V - base < kSub ? (int)(V - base) : kSub;
-    float cum = __uint_as_float(cb);
-    for (int L = 0; L < 64 && 4 * L < nvalid; L++) {
-        float c[4];
+// The first sub-tile (elements 0 .. min(V, 256) - 1) one fp32 add at a time
+// in index order, from cum = 0: the reference's loop itself, run by one lane
+// over the probabilities staged in LDS (sp, 16-byte aligned).  Returns true
+// when the draw is decided (result set), else sets cb to the running sum's
+// bits at the sub-tile's end.  Adding 0.0f for the padding past V leaves the
+// sum unchanged.
+__device__ bool walk_first_lds(const float* sp, long V, float r, uint32_t& cb, long& result) {
+    const int nvalid = V < kSub ? (int)V : kSub;
+    float cum = 0.0f;
+    for (int i = 0; i < nvalid; i += 16) {
+        float4 q[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) q[u] = *reinterpret_cast<const float4*>(sp + i + 4 * u);
+        float c[16];
         float run = cum;
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-            const float q = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p[e]), L));
-            run = run + (4 * L + e < nvalid ? q : 0.0f);
-            c[e] = run;
-        }
-        if (!(c[3] < r)) {  // the draw ends in this quad, or the sum became NaN
+        for (int u = 0; u < 4; u++) {
+            const float e4[4] = {q[u].x, q[u].y, q[u].z, q[u].w};
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                const int o = 4 * L + e;
-                if (o < nvalid) {
+                run = run + (i + 4 * u + e < nvalid ? e4[e] : 0.0f);
+                c[4 * u + e] = run;
+            }
+        }
+        if (!(c[15] < r)) {  // the draw ends in these 16, or the sum became NaN (cum never decreases)
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                if (i + e < nvalid) {
                     if (c[e] >= r) {
-                        result = base + o;
+                        result = i + e;
                         return true;
                     }
                     if (c[e] != c[e]) {  // no later sum can reach r
@@ -866,7 +968,7 @@ __device__ bool walk_serial_p(const float p[4], long base, long V, float r, uint
                 }
             }
         }
-        cum = c[3];
+        cum = c[15];
     }
     cb = __float_as_uint(cum);
     return false;
@@ -882,7 +984,6 @@ __device__ bool walk_subtile_p(const float p[4], long base, long V, float r, uin
     while (true) {
         const Binade b = binade_of(__uint_as_float(cb));
         Fn f[4];
-        Fn acc = {0u, 0u};
 #pragma unroll
         for (int e = 0; e < 4; e++) {
             const int o = 4 * lane + e;
@@ -890,9 +991,8 @@ __device__ bool walk_subtile_p(const float p[4], long base, long V, float r, uin
             const bool in = o >= s && o < nvalid;
             f[e].a0 = in ? m.a0 : 0u;
             f[e].a1 = in ? m.a1 : 0u;
-            acc = compose(acc, f[e]);
         }
-        const Fn incl = wave_scan(acc);
+        const Fn incl = compose4_scan(f);
         const uint32_t tot0 = (uint32_t)__builtin_amdgcn_readlane((int)incl.a0, 63);
         const uint32_t tot1 = (uint32_t)__builtin_amdgcn_readlane((int)incl.a1, 63);
         const Fn x = dpp_fn<0x138, 0xF>(incl);  // the lanes before this one
@@ -1000,7 +1100,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1))) void
                 f.a1 = idx < kSumCache ? sh.sm1[idx] : a.ws_map1[row * a.nsub_ld + idx];
             }
         }
-        const Fn pre = wave_scan(f);
+        const Fn pre = wave_scan_any(f);
         const uint32_t inc = (m0 & 1u) ? pre.a1 : pre.a0;
         const uint32_t me = m0 + inc;  // inc <= kSat, no wrap
         const uint32_t ce = ccls ? (((uint32_t)ccls << 23) | (me & 0x7FFFFFu)) : me;
@@ -1072,6 +1172,10 @@ static int bind_workspace(SampleArgs& a, void* ws, size_t ws_bytes, long rows, l
     a.nsub = (int)((vocab + kSub - 1) / kSub);
     a.nsub_ld = (a.nsub + 3) & ~3;
     a.shift = 63 - ceil_log2(vocab);
+    // the sequential fp32 running sum of vocab probabilities is within
+    // vocab * 2^-25 of the exact prefix (each add errs by half an ulp of a
+    // sum below 1), plus slack for the prediction's own rounding
+    a.skip_margin = (float)((double)vocab * 0x1p-25 + 0x1p-10);
     return ANELM_OK;
 }
 
