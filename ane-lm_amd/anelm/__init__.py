@@ -72,6 +72,7 @@ _SIGS = {
     "anelm_softmax": (_I, [_P, _L, _L, _L, _P, _S, _P]),
     "anelm_sample_workspace_size": (_S, [_L, _L]),
     "anelm_sample": (_I, [_P, _P, _L, _P, _L, _L, _L, _P, _L, _P, ctypes.POINTER(SamplingParams), _P, _P, _S, _P]),
+    "anelm_layer_ops": (_I, [_P] * 14 + [_I, _P, _P, _P, _I, _F, _L, _I, _I, _I, _L, _F, _P]),
     "anelm_sample_noalloc": (_I, [_P, _P, _L, _P, _L, _L, _L, _P, _L, _P, ctypes.POINTER(SamplingParams), _P, _P]),
     "anelm_gqa_workspace_size": (_S, [_L, _I, _I, _I, _I]),
     "anelm_gqa_attention": (_I, [_P, _P, _P, _P, _P, _P, _L, _I, _I, _I, _L, _I, _L, _I, _L, _P, _S, _P]),
@@ -329,6 +330,19 @@ def sample(ids, probs, logits, hist, hist_len, params: SamplingParams, r, worksp
                               _ptr(hist) if hist_ld else None, hist_ld, _ptr(hist_len), ctypes.byref(params),
                               _ptr(r), _ptr(workspace), workspace.numel() * workspace.element_size(),
                               _stream(stream)))
+
+
+def layer_ops(x, xn_in, xn_post, attn, mlp, q, k, h, g, u, w_in, w_post, wq, wk, pos, cos_tab, sin_tab, theta=1e6,
+              eps=1e-6, nq=None, nk=None, stream=None):
+    """The layer's five ops in one launch (anelm_layer_ops): contiguous rows,
+    q [T, nq*128], k [T, nk*128], gammas of one dtype."""
+    T, H = x.shape
+    nq = nq if nq is not None else q.shape[1] // 128
+    nk = nk if nk is not None else k.shape[1] // 128
+    _check(lib().anelm_layer_ops(_ptr(x), _ptr(xn_in), _ptr(xn_post), _ptr(attn), _ptr(mlp), _ptr(q), _ptr(k), _ptr(h),
+                                 _ptr(g), _ptr(u), _ptr(w_in), _ptr(w_post), _ptr(wq), _ptr(wk), _dtype_code(w_in),
+                                 _ptr(pos), _ptr(cos_tab), _ptr(sin_tab), cos_tab.shape[0], theta, T, H, nq, nk,
+                                 g.shape[1], eps, _stream(stream)))
 
 
 def sample_noalloc(ids, probs, logits, hist, hist_len, params: SamplingParams, r, stream=None):

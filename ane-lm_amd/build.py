@@ -25,6 +25,7 @@ LIB = os.path.join(LIBDIR, "libanelm_hip.so")
 SOURCES = [
     os.path.join(CSRC, "status.hip"),
     os.path.join(CSRC, "norm.hip"),
+    os.path.join(CSRC, "layer.hip"),
     os.path.join(CSRC, "elementwise.hip"),
     os.path.join(CSRC, "sampling.hip"),
     os.path.join(CSRC, "attention.hip"),

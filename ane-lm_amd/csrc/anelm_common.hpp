@@ -215,6 +215,41 @@ __device__ __forceinline__ void st_nt(uint4* p, uint4 v) {
     __builtin_nontemporal_store(n, reinterpret_cast<nat_u32x4*>(p));
 }
 
+// This lane's four gammas as raw storage bits, fetched with the row (for
+// fp32 gammas the float4 itself); widened after the reduction.
+template <int DT>
+struct Gamma4 {
+    uint2 bits;
+    __device__ __forceinline__ void load(const void* w, int c) {
+        bits = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(w) + c);
+    }
+    __device__ __forceinline__ float4 get() const {
+        if constexpr (DT == ANELM_F16)
+            return make_float4(f16_to_f32_exact(bits.x & 0xFFFFu), f16_to_f32_exact(bits.x >> 16),
+                               f16_to_f32_exact(bits.y & 0xFFFFu), f16_to_f32_exact(bits.y >> 16));
+        else
+            return make_float4(bf16_to_f32(bits.x & 0xFFFFu), bf16_to_f32(bits.x >> 16), bf16_to_f32(bits.y & 0xFFFFu),
+                               bf16_to_f32(bits.y >> 16));
+    }
+};
+template <>
+struct Gamma4<ANELM_F32> {
+    float4 v;
+    __device__ __forceinline__ void load(const void* w, int c) { v = *reinterpret_cast<const float4*>(static_cast<const float*>(w) + c); }
+    __device__ __forceinline__ float4 get() const { return v; }
+};
+
+// Launch geometry of the row RMSNorm (rmsnorm_row_kernel) for rows of nvec
+// float4 (nvec <= 4096): nv float4 per lane and `threads` lanes per row.  Two
+// float4 per lane where the row allows it, at most 16 waves; one per lane for
+// few rows (decode), where more lanes per row win.  The geometry fixes the
+// order of the sum of squares, so every kernel that must reproduce the
+// RMSNorm's bits takes it from here.
+inline void rms_row_geometry(long rows, int nvec, int& nv, int& threads) {
+    nv = nvec <= 1024 * 2 ? (nvec <= 64 || (rows < 256 && nvec <= 1024) ? 1 : 2) : 4;
+    threads = ((nvec + nv - 1) / nv + 63) / 64 * 64;
+}
+
 // ---------------------------------------------- per-head q/k norm + RoPE
 // Shared by the q/k norm kernels and the attention that applies them on the
 // fly, so both produce the same bits.

@@ -31,30 +31,6 @@ __device__ __forceinline__ uint32_t f16_bits_rne(float v) {
     return (uint32_t)__builtin_bit_cast(uint16_t, to_f16(v));
 }
 
-// This lane's four gammas as raw storage bits, fetched with the row (for
-// fp32 gammas the float4 itself); widened after the reduction.
-template <int DT>
-struct Gamma4 {
-    uint2 bits;
-    __device__ __forceinline__ void load(const void* w, int c) {
-        bits = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(w) + c);
-    }
-    __device__ __forceinline__ float4 get() const {
-        if constexpr (DT == ANELM_F16)
-            return make_float4(f16_to_f32_exact(bits.x & 0xFFFFu), f16_to_f32_exact(bits.x >> 16),
-                               f16_to_f32_exact(bits.y & 0xFFFFu), f16_to_f32_exact(bits.y >> 16));
-        else
-            return make_float4(bf16_to_f32(bits.x & 0xFFFFu), bf16_to_f32(bits.x >> 16), bf16_to_f32(bits.y & 0xFFFFu),
-                               bf16_to_f32(bits.y >> 16));
-    }
-};
-template <>
-struct Gamma4<ANELM_F32> {
-    float4 v;
-    __device__ __forceinline__ void load(const void* w, int c) { v = *reinterpret_cast<const float4*>(static_cast<const float*>(w) + c); }
-    __device__ __forceinline__ float4 get() const { return v; }
-};
-
 // Every load is issued unconditionally, from a column clamped into the row
 // (lanes past its end load a valid element and discard it): a load inside a
 // branch makes the wave wait for it where the branch ends, which serialised
@@ -179,10 +155,8 @@ static int launch_rmsnorm_dt(void* out, float* x, const float* y, const void* w,
                      (!ADD || ((ld_y % 4 == 0) && aligned16(y)));
     const int nvec = dim / 4;  // float4 per row
     if (vec && nvec <= 1024 * 4) {
-        // two float4 per lane where the row allows it, at most 16 waves;
-        // one per lane for few rows (decode), where more lanes per row win
-        int nv = nvec <= 1024 * 2 ? (nvec <= 64 || (rows < 256 && nvec <= 1024) ? 1 : 2) : 4;
-        int threads = ((nvec + nv - 1) / nv + 63) / 64 * 64;
+        int nv, threads;
+        rms_row_geometry(rows, nvec, nv, threads);
         const dim3 grd((unsigned)rows);
         if (nv == 1)
             rmsnorm_row_kernel<1, DT, ADD, O16><<<grd, threads, 0, st>>>(out, x, y, w, rows, dim, ld_x, ld_y, ld_out, eps);

@@ -74,6 +74,15 @@ def op_bytes(w):
     }
 
 
+def layer_ops_bytes(w):
+    """Compulsory HBM bytes of one anelm_layer_ops launch: x read and written
+    once (it stays in registers through the three x ops), attn and mlp read,
+    both norms' outputs written, q/k in place with their cos/sin rows, g and
+    u read and h written."""
+    T, H, I, nh = w["T"], w["H"], w["I"], w["nq"] + w["nk"]
+    return 6 * T * H * 4 + 2 * T * nh * D * 4 + T * (D // 2) * 2 * 4 + 3 * T * I * 4
+
+
 def gather_bytes(w):
     return w["T"] * w["H"] * (2 + 4) if w.get("gather") else 0   # fp16 row in, fp32 row out
 
@@ -219,6 +228,36 @@ def measure_chain(w, steps, warmup, per_op, chain_only=False):
     if rotate and not chain_only:
         r["carried_x"] = dict(run(False), note="one x/xn/h carried through all layers: includes Infinity-Cache "
                                               "reuse of what the previous layer wrote")
+    if not chain_only:
+        # the same five ops per layer as one anelm_layer_ops launch (x kept in
+        # registers through its three ops); GB/s over that launch's own bytes
+        T, H = w["T"], w["H"]
+        xn_in = [torch.empty(T, H, device="cuda") for _ in chain.sets]
+
+        def one_launch():
+            if chain.table is not None:
+                chain.use_set(0)
+                chain.hip.embed_gather(chain.x, chain.table, chain.ids)
+            for li, Ld in enumerate(chain.layers):
+                si = li % len(chain.sets) if rotate else 0
+                chain.use_set(si)
+                chain.hip.layer_ops(chain.x, xn_in[si], chain.xn, Ld["attn"], Ld["mlp"], Ld["q"], Ld["k"], chain.h,
+                                    Ld["g"], Ld["u"], Ld["w_in"], Ld["w_post"], Ld["wq"], Ld["wk"], chain.pos,
+                                    chain.cos, chain.sin, THETA, EPS, nq=w["nq"], nk=w["nk"])
+            chain.use_set(0)
+        g1 = capture(one_launch)
+        for _ in range(warmup):
+            g1.replay()
+        ms1 = time_region(g1.replay, steps)
+        del g1
+        ob1 = layer_ops_bytes(w) * w["layers"] + gather_bytes(w)
+        r["one_launch_per_layer"] = dict(
+            ms_per_step=round(ms1, 4), us_per_layer_chain=round(ms1 * 1e3 / w["layers"], 3),
+            tokens_per_s=round(w["T"] / (ms1 / 1e3), 1), bytes=ob1, GBps=round(ob1 / ms1 / 1e6, 1),
+            frac=round(ob1 / ms1 / 1e6 / HBM_PEAK_GBPS, 4),
+            note="anelm_layer_ops: the five ops of a layer in one launch, outputs bit-identical to the five "
+                 "launches; bytes = that launch's own compulsory traffic (x read and written once)")
+        del xn_in
     if per_op:
         # Each op alone over all layers, x, xn and h rotating as in the
         # chain: no launch reads or rewrites what the launch before it left

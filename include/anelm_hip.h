@@ -128,6 +128,26 @@ int anelm_rope_cached(float* q, float* k, int n_q_heads, int n_kv_heads, int hea
 int anelm_rope_table(float* cos_tab, float* sin_tab, int n_pos, int rot_dim, float theta,
                      void* stream);
 
+/* The five layer ops of models/llm/qwen3.cpp:502-528 for T tokens in one
+ * launch, for a caller that holds all of the layer's op inputs at once (the
+ * op chain without contractions between its ops; e.g. decode-shaped chains,
+ * whose separate launches are each a few microseconds of latency):
+ *   xn_in = rmsnorm(x)*w_in; q, k normalised and rotated in place (head_dim
+ *   128, RoPE table required); x += attn; xn_post = rmsnorm(x)*w_post;
+ *   h = silu(g)*u; x += mlp.
+ * Every output is bit-identical to anelm_rmsnorm, anelm_qknorm_rope,
+ * anelm_add_rmsnorm, anelm_silu_mul and anelm_residual_add run in that order
+ * on the same buffers (xn_in being the first norm's output, xn_post the
+ * second's).  Row-major, contiguous: x, xn_in, xn_post, attn, mlp [T, hidden];
+ * q [T, nq*128]; k [T, nk*128]; g, u, h [T, inter]; all 16-byte aligned;
+ * gammas of w_dtype (w_in, w_post [hidden]; wq, wk [128]).  hidden and inter
+ * multiples of 4, hidden <= 16384.  x is read and written once.  No
+ * counterpart in the reference (its ops are separate steps). */
+int anelm_layer_ops(float* x, float* xn_in, float* xn_post, const float* attn, const float* mlp, float* q, float* k,
+                    float* h, const float* g, const float* u, const void* w_in, const void* w_post, const void* wq,
+                    const void* wk, int w_dtype, const int32_t* pos, const float* cos_tab, const float* sin_tab,
+                    int tab_len, float theta, long T, int hidden, int nq, int nk, long inter, float eps, void* stream);
+
 /* ---------------------------------------------------------- elementwise */
 
 /* Residual add x[i] += y[i] (one IEEE add; bit-exact).
