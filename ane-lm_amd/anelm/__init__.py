@@ -104,9 +104,7 @@ _SIGS = {
     "anelm_st_load_norm": (_I, [_P, _L, _P, _L, _P]),
     "anelm_ane_blob_header": (None, [_P, ctypes.c_uint64]),
     "anelm_write_ane_blobs": (_L, [ctypes.c_char_p, ctypes.c_char_p, _P]),
-    "anelm_blas_create": (_P, []),
-    "anelm_blas_destroy": (None, [_P]),
-    "anelm_linear_f16": (_I, [_P, _P, _P, _P, _L, _I, _I, _L, _L, _P]),
+    "anelm_linear_f16": (_I, [_P, _P, _P, _L, _I, _I, _L, _L, _P]),
     "anelm_proj_f16": (_I, [_P, _P, _P, _L, _I, _I, _L, _L, _P]),
     "anelm_proj_f16_x16": (_I, [_P, _P, _P, _L, _I, _I, _L, _L, _P]),
     "anelm_proj_f16_fused": (_I, [_P, _P, _P, _L, _I, _I, _L, _L, _P, _F, _I, _P]),
@@ -579,28 +577,12 @@ class Qwen3Config(ctypes.Structure):
                 ("vocab", ctypes.c_int), ("rope_theta", ctypes.c_float), ("rms_eps", ctypes.c_float)]
 
 
-class Blas:
-    """A rocBLAS context for linear_f16."""
-
-    def __init__(self):
-        self._h = lib().anelm_blas_create()
-        if not self._h:
-            raise AnelmError(ERR_HIP, last_error())
-
-    def linear_f16(self, y16, x16, w16, stream=None):
-        """y16 [B, out] = fp16(x16 [B, in] . w16 [out, in]^T)."""
-        batch, in_dim = x16.shape
-        out_dim = w16.shape[0]
-        _check(lib().anelm_linear_f16(self._h, _ptr(y16), _ptr(x16), _ptr(w16), batch, out_dim, in_dim, _ld(x16),
-                                      _ld(y16), _stream(stream)))
-
-    def __del__(self):
-        try:
-            if getattr(self, "_h", None) and _lib is not None:
-                _lib.anelm_blas_destroy(self._h)
-        except Exception:   # interpreter shutdown
-            pass
-        self._h = None
+def linear_f16(y16, x16, w16, stream=None):
+    """y16 [B, out] = fp16(x16 [B, in] . w16 [out, in]^T), fp32 accumulation."""
+    batch, in_dim = x16.shape
+    out_dim = w16.shape[0]
+    _check(lib().anelm_linear_f16(_ptr(y16), _ptr(x16), _ptr(w16), batch, out_dim, in_dim, _ld(x16), _ld(y16),
+                                  _stream(stream)))
 
 
 def proj_f16(y, x, w16, stream=None):

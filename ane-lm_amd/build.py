@@ -85,7 +85,7 @@ def build_lib(jobs: int = 8) -> str:
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
         list(ex.map(_run, cmds))
     tmp = LIB + ".tmp"
-    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs, "-lrocblas"])
+    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs])
     os.replace(tmp, LIB)
     return LIB
 

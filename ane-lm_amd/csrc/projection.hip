@@ -23,6 +23,8 @@
 // multiple of 8): one wave per output row, v_dot2_f32_f16 into fp32.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
 #include "anelm_common.hpp"
 
 namespace anelm {
@@ -33,6 +35,8 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float float4v __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float r16(float v) { return (float)to_f16(v); }
+// fp16 bits (low 16 of h) widened exactly
+__device__ __forceinline__ float h2f_bits(uint32_t h) { return (float)__builtin_bit_cast(_Float16, (uint16_t)h); }
 
 __device__ __forceinline__ half8 to_half8(float4 a, float4 b) {
     half8 r;
@@ -74,8 +78,10 @@ struct ProjArgs {
     float eps;
     // SwiGLU epilogue (kSwiGLU, kSwiGLU16): the up rows follow the gate rows at this offset
     long pair_rows;
-    // kSwiGLU16: the output as fp16 bits (row stride ld_y) instead of y
+    // kSwiGLU16, kStore16: the output as fp16 bits (row stride ld_y) instead of y
     uint16_t* y16;
+    // y rows 16-byte aligned (y and ld_y), for the LDS kernel's float4 stores
+    bool vec_y;
 };
 
 // What the epilogue does with the rounded projection p = fp16(sum) (as fp32):
@@ -84,6 +90,7 @@ enum Epilogue {
     kAdd = 1,     // y = y + p  (the residual add of qwen3.cpp:516, :527)
     kSwiGLU = 2,  // y = silu(p_gate) * p_up  (core/ane_runtime.cpp:393-395)
     kSwiGLU16 = 3,  // the same rounded to fp16 (nearest even) into y16: the next projection's input
+    kStore16 = 4,   // y16 = p as fp16 bits (the ANE kernels' own fp16 output)
 };
 constexpr bool is_swiglu(int epi) { return epi == kSwiGLU || epi == kSwiGLU16; }
 
@@ -268,11 +275,166 @@ __global__ __launch_bounds__(64 * NW) void proj_mfma_kernel(ProjArgs a) {
                 for (int i = 0; i < 4; i++) {
                     if (r + i < a.out_dim) {
                         if constexpr (EPI == kAdd) yr[r + i] = yprev[j][i] + r16(s[i]);
+                        else if constexpr (EPI == kStore16)
+                            a.y16[(long)b * a.ld_y + r + i] = __builtin_bit_cast(uint16_t, to_f16(s[i]));
                         else yr[r + i] = r16(s[i]);
                     }
                 }
             }
         }
+    }
+}
+
+// ---- many rows of x against a long W: x staged in LDS ------------------------
+// The LM head past 16 sequences (151936 output rows): every weight row must
+// be read from HBM once while each serves all the batch rows.  A workgroup
+// stages 16*NB rows of the fp16 x in LDS once (rows padded by 16 bytes, so
+// the 16 rows a ds_read_b128 of a wave touches fall in 16 different bank
+// groups).  Its 8 waves then take 8 adjacent 16-row tiles of W (128 output
+// rows) per round, rounds striding over the grid (about one workgroup per
+// CU, so W streams once), each wave streaming its tile over the full input
+// dimension: 8 steps of 32 inputs per load chunk, the next chunk's loads in
+// flight during the current chunk's MFMAs, each 16-byte weight load feeding
+// NB MFMAs with x from LDS.  At a round's end the waves round their sums to
+// fp16 into an LDS staging block, and the workgroup stores the 128 outputs
+// of each batch row as one contiguous run (fp32 widened, non-temporal, or
+// fp16 bits with kStore16): stored straight from the MFMA layout, each batch
+// row got 64-byte pieces, which cost a third of the kernel's time.  Weight
+// loads are cached (non-temporal measured slower here).  in_dim a multiple
+// of 256.
+constexpr int kLdsR = 8;                       // 32-input steps per load chunk
+constexpr int kLdsHalves = 64 * (1024 + 8);    // the LDS x area: 64 rows of 1024 inputs, or fewer longer rows
+constexpr int kYsLd = 128 + 8;                 // staging row stride (fp16), 128 outputs per batch row
+
+__host__ __device__ constexpr int lds_rows(int in_dim) {   // batch rows staged per workgroup
+    return 64 * (in_dim + 8) <= kLdsHalves ? 64 : (32 * (in_dim + 8) <= kLdsHalves ? 32 : 16);
+}
+
+template <int NB, int EPI>
+__global__ __launch_bounds__(512) void proj_lds_kernel(ProjArgs a) {
+    static_assert(EPI == kStore || EPI == kStore16, "store epilogues only");
+    __shared__ __align__(16) uint16_t xs[kLdsHalves];
+    __shared__ __align__(16) uint16_t ys[16 * NB * kYsLd];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int K = a.in_dim, ldx = K + 8;
+    const int b0 = blockIdx.y * 16 * NB;
+    const uint16_t* xh = static_cast<const uint16_t*>(a.x);
+    {   // stage x rows b0 .. b0 + 16*NB - 1 (zeros past the batch): 8 loads per lane before their stores
+        const int qpr = K / 8, nq = 16 * NB * qpr;
+        for (int base = 0; base < nq; base += 8 * (int)blockDim.x) {
+            uint4 t[8];
+            int dst[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int idx = base + u * (int)blockDim.x + (int)threadIdx.x;
+                const int ic = idx < nq ? idx : nq - 1;   // past the end: the last quad again
+                const int r = ic / qpr, c = ic - r * qpr;
+                const int b = b0 + r < a.batch ? b0 + r : a.batch - 1;
+                t[u] = *reinterpret_cast<const uint4*>(xh + (long)b * a.ld_x + 8 * c);
+                if (b0 + r >= a.batch) t[u] = make_uint4(0u, 0u, 0u, 0u);
+                dst[u] = r * ldx + 8 * c;
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++) *reinterpret_cast<uint4*>(xs + dst[u]) = t[u];
+        }
+    }
+    __syncthreads();
+    const int ngroup = (a.out_dim + 127) / 128;   // 128-row groups (8 tiles)
+    if ((int)blockIdx.x >= ngroup) return;        // whole workgroup
+    const int rounds = (ngroup - 1 - (int)blockIdx.x) / (int)gridDim.x + 1;
+    const int cpt = K / (32 * kLdsR);             // load chunks per tile
+    const int nq = rounds * cpt;                  // every wave runs all of them (barriers)
+    const uint16_t* wbase = a.w + 8 * (lane >> 4);
+    // the R loads of chunk q (clamped rows: tiles past the end load a valid
+    // row, computed and never stored; a chunk past nq reloads the last one)
+    auto issue = [&](uint4* w, int q) {
+        q = q < nq ? q : nq - 1;
+        const int grp = (int)blockIdx.x + (q / cpt) * (int)gridDim.x;
+        long r = 128L * grp + 16 * wv + (lane & 15);
+        r = r < a.out_dim ? r : a.out_dim - 1;
+        const uint16_t* p = wbase + r * K + (q % cpt) * (32 * kLdsR);
+#pragma unroll
+        for (int j = 0; j < kLdsR; j++) w[j] = *reinterpret_cast<const uint4*>(p + 32 * j);
+    };
+    const uint16_t* xrow = xs + (lane & 15) * ldx + 8 * (lane >> 4);
+    float4v acc[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; nb++) acc[nb] = float4v{0.f, 0.f, 0.f, 0.f};
+    auto compute = [&](const uint4* w, int q) {
+        const int s0 = (q % cpt) * kLdsR;
+#pragma unroll
+        for (int j = 0; j < kLdsR; j++) {
+#pragma unroll
+            for (int nb = 0; nb < NB; nb++) {
+                const uint4 xq = *reinterpret_cast<const uint4*>(xrow + nb * 16 * ldx + 32 * (s0 + j));
+                acc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(w[j]), as_half8(xq), acc[nb], 0, 0, 0);
+            }
+        }
+        if (q % cpt == cpt - 1) {   // the round is complete (workgroup-uniform)
+            // lane: outputs 16*wv + 4*(lane/16) + i of batch row nb*16 + lane%16
+#pragma unroll
+            for (int nb = 0; nb < NB; nb++) {
+                uint16_t h[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) h[i] = __builtin_bit_cast(uint16_t, to_f16(acc[nb][i]));
+                *reinterpret_cast<uint2*>(ys + (nb * 16 + (lane & 15)) * kYsLd + 16 * wv + 4 * (lane >> 4)) =
+                    make_uint2(h[0] | ((uint32_t)h[1] << 16), h[2] | ((uint32_t)h[3] << 16));
+                acc[nb] = float4v{0.f, 0.f, 0.f, 0.f};
+            }
+            __syncthreads();
+            // 16*NB batch rows x 32 quads of 4 outputs, 512 lanes
+            const long c0 = 128L * ((int)blockIdx.x + (q / cpt) * (int)gridDim.x);
+#pragma unroll
+            for (int u = 0; u < NB; u++) {
+                const int item = u * 512 + (int)threadIdx.x;
+                const int br = item >> 5, c4 = item & 31;
+                const int b = b0 + br;
+                const long col = c0 + 4 * c4;
+                const uint2 hv = *reinterpret_cast<const uint2*>(ys + br * kYsLd + 4 * c4);
+                if (b < a.batch) {
+                    if constexpr (EPI == kStore16) {
+                        uint16_t* yr = a.y16 + (long)b * a.ld_y;
+                        if (col + 3 < a.out_dim && a.vec_y) {
+                            *reinterpret_cast<uint2*>(yr + col) = hv;
+                        } else {
+                            const uint16_t e[4] = {(uint16_t)(hv.x & 0xFFFFu), (uint16_t)(hv.x >> 16),
+                                                   (uint16_t)(hv.y & 0xFFFFu), (uint16_t)(hv.y >> 16)};
+#pragma unroll
+                            for (int i = 0; i < 4; i++)
+                                if (col + i < a.out_dim) yr[col + i] = e[i];
+                        }
+                    } else {
+                        float* yr = a.y + (long)b * a.ld_y;
+                        const float4 f = make_float4(h2f_bits(hv.x & 0xFFFFu), h2f_bits(hv.x >> 16),
+                                                     h2f_bits(hv.y & 0xFFFFu), h2f_bits(hv.y >> 16));
+                        if (col + 3 < a.out_dim && a.vec_y) {
+                            st_nt(reinterpret_cast<float4*>(yr + col), f);   // 67.7 against 73.8 us cached
+                        } else {
+                            const float e[4] = {f.x, f.y, f.z, f.w};
+#pragma unroll
+                            for (int i = 0; i < 4; i++)
+                                if (col + i < a.out_dim) yr[col + i] = e[i];
+                        }
+                    }
+                }
+            }
+            __syncthreads();   // the staging block is reused next round
+        }
+    };
+    // The scheduling barriers keep each chunk's loads ahead of the previous
+    // chunk's MFMAs; without them the scheduler sank the loads below the
+    // MFMAs, leaving one chunk in flight.
+    uint4 wa[kLdsR], wb[kLdsR];
+    issue(wa, 0);
+    for (int q = 0; q < nq; q += 2) {
+        issue(wb, q + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(wa, q);
+        __builtin_amdgcn_sched_barrier(0);
+        issue(wa, q + 2);
+        __builtin_amdgcn_sched_barrier(0);
+        if (q + 1 < nq) compute(wb, q + 1);
+        __builtin_amdgcn_sched_barrier(0);
     }
 }
 
@@ -476,6 +638,73 @@ bool dot_ok(const float* x, const uint16_t* w16, long batch, int in_dim, long ld
     return batch <= 8 && in_dim % 8 == 0 && ld_x % 4 == 0 && aligned16(x) && aligned16(w16);
 }
 
+// ---- any shape (the fallback) ------------------------------------------------
+// One wave per (batch row, output row): lanes stride over the inputs, fp16
+// products (exact in fp32) accumulated in fp32, a wave sum, one rounding to
+// fp16.  For shapes the kernels above do not take (in_dim not a multiple of
+// 8, unaligned rows); it reads x once per output row, so it is slow on large
+// shapes, which no Qwen3 size produces.
+__device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+
+template <bool XH, int EPI>
+__global__ __launch_bounds__(256) void proj_generic_kernel(ProjArgs a) {
+    static_assert(EPI == kStore || EPI == kStore16, "store epilogues only");
+    const int lane = threadIdx.x & 63;
+    const long gwave = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const long o = gwave % a.out_dim, b = gwave / a.out_dim;
+    if (b >= a.batch) return;   // whole wave
+    const uint16_t* wr = a.w + o * a.in_dim;
+    const float* xf = static_cast<const float*>(a.x) + b * a.ld_x;
+    const uint16_t* xh = static_cast<const uint16_t*>(a.x) + b * a.ld_x;
+    float s = 0.f;
+    for (int i = lane; i < a.in_dim; i += 64) s = fmaf(XH ? h2f(xh[i]) : r16(xf[i]), h2f(wr[i]), s);
+    s = wave_sum(s);
+    if (lane == 0) {
+        if constexpr (EPI == kStore16) a.y16[b * a.ld_y + o] = __builtin_bit_cast(uint16_t, to_f16(s));
+        else a.y[b * a.ld_y + o] = r16(s);
+    }
+}
+
+template <bool XH, int EPI>
+void launch_generic(const ProjArgs& a, hipStream_t st) {
+    const long waves = (long)a.out_dim * a.batch;
+    proj_generic_kernel<XH, EPI><<<dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, st>>>(a);
+}
+
+// ---- the LDS kernel's launch -----------------------------------------------------
+// compute units of the current device (cached per device)
+int cu_count() {
+    static int cached[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cached[dev]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cached[dev] = n;
+    }
+    return cached[dev];
+}
+
+// Past 16 rows of fp16 x, against at least 8192 output rows: W streams once
+// through the LDS kernel (measured for the 151936-row LM head; narrower W is
+// better served by more, smaller workgroups).
+bool lds_ok(const ProjArgs& a) {
+    return a.batch > 16 && a.out_dim >= 8192 && a.in_dim % 256 == 0 && a.in_dim <= 4096 && a.ld_x % 8 == 0 &&
+           aligned16(a.x) && aligned16(a.w);
+}
+
+template <int EPI>
+void launch_lds(ProjArgs a, hipStream_t st) {
+    const int rows = lds_rows(a.in_dim);
+    const int ngroup = (a.out_dim + 127) / 128;
+    const int gx = std::min(cu_count(), ngroup);
+    const dim3 grid((unsigned)gx, (unsigned)((a.batch + rows - 1) / rows));
+    a.vec_y = EPI == kStore ? aligned16(a.y) && a.ld_y % 4 == 0 : aligned8(a.y16) && a.ld_y % 4 == 0;
+    if (rows == 64) proj_lds_kernel<4, EPI><<<grid, dim3(512), 0, st>>>(a);
+    else if (rows == 32) proj_lds_kernel<2, EPI><<<grid, dim3(512), 0, st>>>(a);
+    else proj_lds_kernel<1, EPI><<<grid, dim3(512), 0, st>>>(a);
+}
+
 // ---- MFMA launch shapes -----------------------------------------------------
 template <bool XH, int NB, int RT, int R, bool NORM = false, int EPI = kStore, int NW = 4>
 void launch_mfma(const ProjArgs& a, hipStream_t st) {
@@ -495,7 +724,8 @@ void launch_mfma(const ProjArgs& a, hipStream_t st) {
 template <bool XH>
 int proj_mfma(const ProjArgs& a, hipStream_t st) {
     const long tiles16 = (long)((a.out_dim + 15) / 16) * ((a.batch + 15) / 16);
-    if (a.batch <= 16 || tiles16 < 512) launch_mfma<XH, 1, 1, 8>(a, st);
+    if (XH && lds_ok(a)) launch_lds<kStore>(a, st);
+    else if (a.batch <= 16 || tiles16 < 512) launch_mfma<XH, 1, 1, 8>(a, st);
     else launch_mfma<XH, 2, 2, XH ? 8 : 4>(a, st);
     return launch_status("proj_f16");
 }
@@ -542,11 +772,12 @@ extern "C" int anelm_proj_f16(float* y, const float* x, const uint16_t* w16, lon
     const ProjArgs a = args(y, x, w16, batch, out_dim, in_dim, ld_x, ld_y);
     const bool dot = dot_ok(x, w16, batch, in_dim, ld_x);
     if (mfma_ok(x, false, w16, in_dim, ld_x) && !(dot && dot_wins(batch, out_dim))) return proj_mfma<false>(a, st);
-    if (!dot)
-        return fail(ANELM_ERR_INVALID,
-                    "proj_f16: needs in_dim a multiple of 32 (or batch <= 8 and in_dim a multiple of 8), "
-                    "ld_x a multiple of 4, 16-byte aligned x and W");
-    proj_dot<false, kStore>(a, st);
+    if (dot) {
+        proj_dot<false, kStore>(a, st);
+    } else {
+        if ((long)out_dim * batch > (1L << 33)) return fail(ANELM_ERR_INVALID, "proj_f16: too large for its shape");
+        launch_generic<false, kStore>(a, st);
+    }
     return launch_status("proj_f16");
 }
 
@@ -588,7 +819,8 @@ template <int EPI>
 void x16_fused(const ProjArgs& a, hipStream_t st) {
     const long tiles16 = (long)((a.out_dim + 15) / 16) * ((a.batch + 15) / 16);
     constexpr int RT = is_swiglu(EPI) ? 2 : 1;
-    if (a.batch <= 16 || (!is_swiglu(EPI) && tiles16 < 512)) launch_mfma<true, 1, RT, 8, false, EPI>(a, st);
+    if (EPI == kStore && lds_ok(a)) launch_lds<kStore>(a, st);
+    else if (a.batch <= 16 || (!is_swiglu(EPI) && tiles16 < 512)) launch_mfma<true, 1, RT, 8, false, EPI>(a, st);
     else if (is_swiglu(EPI) && a.batch > 32) launch_mfma<true, 4, 2, 4, false, EPI>(a, st);
     else launch_mfma<true, 2, 2, 8, false, EPI>(a, st);
 }
@@ -676,4 +908,23 @@ extern "C" int anelm_proj_f16_fused(float* y, const float* x, const uint16_t* w1
             break;
     }
     return launch_status("proj_f16_fused");
+}
+
+// The ANE projection with fp16 rows in and out: y16 = fp16(x16 . W16^T),
+// fp32 accumulation, one rounding to nearest even.
+extern "C" int anelm_linear_f16(uint16_t* y16, const uint16_t* x16, const uint16_t* w16, long batch, int out_dim,
+                                int in_dim, long ld_x, long ld_y, void* stream) {
+    clear_error();
+    if (!y16 || !x16 || !w16) return fail(ANELM_ERR_INVALID, "linear_f16: null pointer");
+    if (!sizes_ok(batch, out_dim, in_dim, ld_x, ld_y) || (long)out_dim * batch > (1L << 33))
+        return fail(ANELM_ERR_INVALID, "linear_f16: bad sizes or strides");
+    if (overlaps(y16, ld_y, out_dim, 2, x16, ld_x, in_dim, 2, batch))
+        return fail(ANELM_ERR_INVALID, "linear_f16: y overlaps x (y is written while x is still read)");
+    ProjArgs a = args(nullptr, x16, w16, batch, out_dim, in_dim, ld_x, ld_y);
+    a.y16 = y16;
+    hipStream_t st = as_stream(stream);
+    if (lds_ok(a)) launch_lds<kStore16>(a, st);
+    else if (mfma_ok(x16, true, w16, in_dim, ld_x)) launch_mfma<true, 1, 1, 8, false, kStore16>(a, st);
+    else launch_generic<true, kStore16>(a, st);
+    return launch_status("linear_f16");
 }

@@ -17,7 +17,6 @@
 // A step processes one token of each of `batch` sequences; every sequence
 // has its own KV ring per layer (qwen3.cpp:227-231, 475-488).
 #include <hip/hip_runtime.h>
-#include <rocblas/rocblas.h>
 
 #include <algorithm>
 #include <cmath>
@@ -31,49 +30,6 @@
 using anelm::fail;
 using anelm::clear_error;
 
-
-struct anelm_blas {
-    rocblas_handle h = nullptr;
-};
-
-extern "C" anelm_blas* anelm_blas_create(void) {
-    clear_error();
-    anelm_blas* b = new anelm_blas();
-    if (rocblas_create_handle(&b->h) != rocblas_status_success) {
-        delete b;
-        fail(ANELM_ERR_HIP, "blas_create: rocblas_create_handle failed");
-        return nullptr;
-    }
-    return b;
-}
-
-extern "C" void anelm_blas_destroy(anelm_blas* b) {
-    if (!b) return;
-    if (b->h) rocblas_destroy_handle(b->h);
-    delete b;
-}
-
-// y16 [batch, out_dim] (row stride ld_y) = fp16(x16 [batch, in_dim] (ld_x) . W16^T),
-// W16 [out_dim, in_dim] row-major; fp32 accumulation, one rounding to fp16.
-extern "C" int anelm_linear_f16(anelm_blas* b, uint16_t* y16, const uint16_t* x16, const uint16_t* w16, long batch,
-                                int out_dim, int in_dim, long ld_x, long ld_y, void* stream) {
-    clear_error();
-    if (!b || !y16 || !x16 || !w16) return fail(ANELM_ERR_INVALID, "linear_f16: null pointer");
-    if (batch <= 0 || out_dim <= 0 || in_dim <= 0 || ld_x < in_dim || ld_y < out_dim || batch > 0x7FFFFFFFL ||
-        ld_x > 0x7FFFFFFFL || ld_y > 0x7FFFFFFFL)
-        return fail(ANELM_ERR_INVALID, "linear_f16: bad sizes or strides");
-    if (rocblas_set_stream(b->h, anelm::as_stream(stream)) != rocblas_status_success)
-        return fail(ANELM_ERR_HIP, "linear_f16: rocblas_set_stream failed");
-    const float alpha = 1.0f, beta = 0.0f;
-    // column-major view: Y^T (out x batch) = W (in x out)^T . X^T (in x batch)
-    const rocblas_status st = rocblas_gemm_ex(
-        b->h, rocblas_operation_transpose, rocblas_operation_none, out_dim, (rocblas_int)batch, in_dim, &alpha, w16,
-        rocblas_datatype_f16_r, in_dim, x16, rocblas_datatype_f16_r, (rocblas_int)ld_x, &beta, y16,
-        rocblas_datatype_f16_r, (rocblas_int)ld_y, y16, rocblas_datatype_f16_r, (rocblas_int)ld_y,
-        rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
-    if (st != rocblas_status_success) return fail(ANELM_ERR_HIP, "linear_f16: rocblas_gemm_ex status %d", (int)st);
-    return anelm::launch_status("linear_f16");
-}
 
 namespace {
 
@@ -91,7 +47,6 @@ struct DevBuf {
 struct anelm_qwen3 {
     anelm_qwen3_config c{};
     int max_batch = 0, cap = 0, qdim = 0, kvdim = 0, qkvdim = 0;
-    anelm_blas* blas = nullptr;
     std::vector<DevBuf*> bufs;   // every device allocation, freed at the end
     // weights
     uint16_t* embed = nullptr;       // bf16 [V, H] (widened exactly by the gather)
@@ -124,7 +79,6 @@ struct anelm_qwen3 {
     }
     ~anelm_qwen3() {
         for (DevBuf* d : bufs) delete d;
-        anelm_blas_destroy(blas);
     }
 };
 
@@ -178,8 +132,6 @@ extern "C" anelm_qwen3* anelm_qwen3_load(const char* path, const anelm_qwen3_con
         delete m;
         return (anelm_qwen3*)nullptr;
     };
-    m->blas = anelm_blas_create();
-    if (!m->blas) return bail("blas");
 #define ALLOC(ptr, T, n)                                                   \
     do {                                                                   \
         ptr = static_cast<T*>(m->alloc((size_t)(n) * sizeof(T)));          \
@@ -249,7 +201,7 @@ extern "C" anelm_qwen3* anelm_qwen3_load(const char* path, const anelm_qwen3_con
     ALLOC(m->gu, float, B * 2 * I);
     ALLOC(m->h, float, B * I);
     ALLOC(m->a16, uint16_t, B * amax);
-    ALLOC(m->y16, uint16_t, B * std::max({(long)m->qkvdim, 2 * I, H, V}));
+    ALLOC(m->y16, uint16_t, B * std::max({(long)m->qkvdim, 2 * I, H}));
 #undef ALLOC
     m->attn_ws_bytes = anelm_gqa_workspace_size(B, c.n_q_heads, c.n_kv_heads, c.head_dim, m->cap);
     if (m->attn_ws_bytes && !(m->attn_ws = m->alloc(m->attn_ws_bytes))) {
@@ -297,26 +249,17 @@ extern "C" int anelm_qwen3_forward(anelm_qwen3* m, const int32_t* ids, const int
     do {                              \
         if ((rc = (call)) != ANELM_OK) return rc; \
     } while (0)
-    // x16 = RNE fp16 of the [B, n] fp32 input; y16 = the projection; out = widened y16
+    // out = the fp16 projection of the [B, n_in] fp32 rows, widened: MFMA
+    // kernels for in_dim a multiple of 32 (past 16 rows from inputs rounded
+    // to fp16 once), else the dot kernel up to 8 rows and the any-shape
+    // kernel beyond (dims no Qwen3 size has)
     auto project = [&](float* out, long ld_out, const float* in, long n_in, const uint16_t* w16, long n_out) -> int {
         int r;
-        // MFMA kernel; past 16 rows the inputs are rounded to fp16 once instead
-        // of in every workgroup.  rocBLAS keeps the LM head past 16 rows: with
-        // 151936 outputs its tiles reuse each input row better (77 us against
-        // 200 us at 64 rows).
-        if (n_in % 32 == 0 && (B <= 16 || n_out <= 65536)) {
-            if (B <= 16) return anelm_proj_f16(out, in, w16, B, (int)n_out, (int)n_in, n_in, ld_out, stream);
+        if (n_in % 32 == 0 && B > 16) {
             if ((r = anelm_f32_to_f16(m->a16, in, (size_t)(B * n_in), stream))) return r;
             return anelm_proj_f16_x16(out, m->a16, w16, B, (int)n_out, (int)n_in, n_in, ld_out, stream);
         }
-        if (B <= 8) return anelm_proj_f16(out, in, w16, B, (int)n_out, (int)n_in, n_in, ld_out, stream);
-        if ((r = anelm_f32_to_f16(m->a16, in, (size_t)(B * n_in), stream))) return r;
-        if ((r = anelm_linear_f16(m->blas, m->y16, m->a16, w16, B, (int)n_out, (int)n_in, n_in, n_out, stream)))
-            return r;
-        if (ld_out == n_out) return anelm_f16_to_f32(out, m->y16, (size_t)(B * n_out), stream);
-        for (long b = 0; b < B; b++)   // strided destination (the caller's logits rows)
-            if ((r = anelm_f16_to_f32(out + b * ld_out, m->y16 + b * n_out, (size_t)n_out, stream))) return r;
-        return ANELM_OK;
+        return anelm_proj_f16(out, in, w16, B, (int)n_out, (int)n_in, n_in, ld_out, stream);
     };
     // q/k norm + RoPE, the KV ring append and the attention, one launch
     // (head_dim 128) over the raw q|k|v rows; every layer's rings were
@@ -351,16 +294,10 @@ extern "C" int anelm_qwen3_forward(anelm_qwen3* m, const int32_t* ids, const int
                                         stream));                                                 // down + :527
         }
         CK(anelm_rmsnorm_f16(m->a16, m->x, m->final_norm, ANELM_BF16, B, (int)H, H, H, c.rms_eps, stream));  // :530
-        if (V <= 65536)
-            return anelm_proj_f16_x16_fused(logits, m->a16, m->lm16, B, (int)V, (int)H, H, ld_logits, ANELM_PROJ_STORE,
-                                            stream);
-        // rocBLAS keeps the LM head: with 151936 outputs its tiles reuse each
-        // input row better (80 us against 140 us at 64 rows)
-        CK(anelm_linear_f16(m->blas, m->y16, m->a16, m->lm16, B, (int)V, (int)H, H, V, stream));
-        if (ld_logits == V) return anelm_f16_to_f32(logits, m->y16, (size_t)(B * V), stream);
-        for (long b = 0; b < B; b++)   // strided destination (the caller's logits rows)
-            CK(anelm_f16_to_f32(logits + b * ld_logits, m->y16 + b * V, (size_t)V, stream));
-        return ANELM_OK;
+        // the LM head (a 151936-row W streams once through the LDS-staged
+        // kernel) writes the widened logits itself
+        return anelm_proj_f16_x16_fused(logits, m->a16, m->lm16, B, (int)V, (int)H, H, ld_logits, ANELM_PROJ_STORE,
+                                        stream);
     }
     if (dims32) {
         // 5 calls per layer: the RMSNorms, residual adds and the SwiGLU

@@ -470,22 +470,22 @@ long anelm_write_ane_blobs(const char* safetensors_path, const char* output_dir,
 
 /* ------------------------------ contractions and the device-resident step */
 
-/* A rocBLAS handle for the projections (host object; creating it allocates). */
-typedef struct anelm_blas anelm_blas;
-anelm_blas* anelm_blas_create(void);
-void anelm_blas_destroy(anelm_blas* blas);
 /* One ANE projection for `batch` rows (the conv-as-matvec kernels of
  * core/ane_runtime.cpp:265-408 with ane_matvec's fp16 interface, :600-640):
  * y16[b, o] = fp16(sum_i x16[b, i] * W16[o, i]), W16 [out_dim, in_dim]
- * row-major fp16, fp32 accumulation, one rounding to nearest. */
-int anelm_linear_f16(anelm_blas* blas, uint16_t* y16, const uint16_t* x16, const uint16_t* w16, long batch,
-                     int out_dim, int in_dim, long ld_x, long ld_y, void* stream);
+ * row-major fp16, fp32 accumulation, one rounding to nearest.  Any shape
+ * and alignment; in_dim a multiple of 32 with 16-byte aligned rows takes the
+ * MFMA kernels (past 16 rows against a long W, x staged in LDS so each weight
+ * row is read once for every row of x). */
+int anelm_linear_f16(uint16_t* y16, const uint16_t* x16, const uint16_t* w16, long batch, int out_dim, int in_dim,
+                     long ld_x, long ld_y, void* stream);
 
 /* The same projection with the conversions fused (decode batches):
  * y[b, o] = fp16(sum_i fp16_rne(x[b, i]) * W16[o, i]) stored as fp32, x fp32;
- * each weight is read once.  in_dim a multiple of 32 (any batch), or
- * batch <= 8 and in_dim a multiple of 8; ld_x a multiple of 4; x and W16
- * 16-byte aligned; y must not overlap x. */
+ * each weight is read once on the fast paths: in_dim a multiple of 32 (any
+ * batch), or batch <= 8 and in_dim a multiple of 8, with ld_x a multiple of
+ * 4 and x, W16 16-byte aligned.  Other shapes take a slow any-shape kernel.
+ * y must not overlap x. */
 int anelm_proj_f16(float* y, const float* x, const uint16_t* w16, long batch, int out_dim, int in_dim, long ld_x,
                    long ld_y, void* stream);
 /* anelm_proj_f16 with x already rounded to fp16 (x16 [batch, in_dim], row

@@ -38,8 +38,7 @@ def test_linear_f16_within_one_ulp(hip, orc, rng, B, out_dim, in_dim):
     x = rng.standard_normal((B, in_dim)).astype(np.float16).view(np.uint16)
     w = (0.03 * rng.standard_normal((out_dim, in_dim))).astype(np.float16).view(np.uint16)
     y = torch.empty(B, out_dim, dtype=torch.int16, device="cuda")
-    blas = hip.Blas()
-    blas.linear_f16(y, dev(x), dev(w))
+    hip.linear_f16(y, dev(x), dev(w))
     got = host(y).view(np.float16).astype(np.float64)
     ref = orc.linear_f16(x, w).view(np.float16).astype(np.float64)
     # one fp16 ulp of the result, plus what an fp32 accumulation may differ
