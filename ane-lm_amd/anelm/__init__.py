@@ -12,7 +12,8 @@ import ctypes
 import os
 
 _PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-LIB_PATH = os.path.join(_PKG, "lib", "libanelm_hip.so")
+# ANELM_LIB names another build of the same library (the host-sanitizer build)
+LIB_PATH = os.environ.get("ANELM_LIB") or os.path.join(_PKG, "lib", "libanelm_hip.so")
 
 F32, F16, BF16 = 0, 1, 2
 OK, ERR_INVALID, ERR_RANGE, ERR_HIP, ERR_WORKSPACE = 0, -1, -2, -3, -4

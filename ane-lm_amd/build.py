@@ -1,6 +1,9 @@
 """Build recipe for libanelm_hip.so (gfx950) and the C++ drop-in test driver.
 
-Run as ``python ane-lm_amd/build.py`` or through ``__graft_entry__.build()``.
+Run as ``python ane-lm_amd/build.py`` or through ``__graft_entry__.build()``;
+``python ane-lm_amd/build.py --sanitize [pytest args]`` builds the oracle and
+the library's host code with AddressSanitizer + UBSan and runs the CPU tests
+against that build.
 Every HIP source is compiled for gfx950 only, with hipcc's correctly rounded
 fp32 divide/sqrt (the default), IEEE subnormals, no fast-math, and packed
 fp32 instructions disabled in device code.
@@ -99,10 +102,11 @@ def build_oracle() -> str:
     return os.path.join(oracle, "liboracle.so")
 
 
-def build_dropin_check() -> str:
-    """C++ driver that calls the ane_lm:: drop-in functions against the oracle."""
-    src = os.path.join(ROOT, "tests", "cpp", "dropin_check.cpp")
-    out = os.path.join(ROOT, "tests", "cpp", "dropin_check")
+def build_dropin_check(name: str = "dropin_check") -> str:
+    """C++ driver that calls the ane_lm:: drop-in functions beside the oracle:
+    dropin_check compares them, dropin_timing times them."""
+    src = os.path.join(ROOT, "tests", "cpp", name + ".cpp")
+    out = os.path.join(ROOT, "tests", "cpp", name)
     oracle = os.path.join(ROOT, "oracle")
     tmp = out + ".tmp"
     _run([hipcc(), "-O2", "-std=c++17", "-I", INCLUDE, "-I", HOST, "-I", oracle, src, "-o", tmp,
@@ -125,14 +129,78 @@ def check_integration_doc() -> None:
     integration_doc.check()
 
 
+SAN_DIR = os.path.join(BUILD, "san")
+# Host code only: each -fsanitize= follows -Xarch_host, so the device code of
+# the sanitizer build is the same as the product's.
+SAN_HOST_FLAGS = "-Xarch_host -fsanitize=address -Xarch_host -fsanitize=undefined -Xarch_host -fno-sanitize-recover=undefined".split()
+
+
+def _rocm_llvm(*parts: str) -> str:
+    return os.path.join(os.environ.get("ROCM_PATH", "/opt/rocm"), "llvm", *parts)
+
+
+def asan_runtime() -> str:
+    """clang's shared AddressSanitizer runtime (it carries UBSan's too)."""
+    import glob
+
+    found = sorted(glob.glob(_rocm_llvm("lib", "clang", "*", "lib", "*", "libclang_rt.asan-x86_64.so")))
+    if not found:
+        raise RuntimeError("clang's libclang_rt.asan-x86_64.so not found under " + _rocm_llvm("lib", "clang"))
+    return found[-1]
+
+
+def build_sanitized(jobs: int = 8) -> dict:
+    """CPU sanitizer build: the oracle and the library's host code (the
+    drop-in staging, the safetensors parser and blob writer, argument
+    checks of every entry point) with AddressSanitizer and UBSan, both
+    against clang's shared runtime so one process can load the two.
+    Outputs go to ane-lm_amd/_build/san/ and are never the product."""
+    os.makedirs(SAN_DIR, exist_ok=True)
+    oracle_src = os.path.join(ROOT, "oracle", "anelm_oracle.cpp")
+    oracle_so = os.path.join(SAN_DIR, "liboracle.so")
+    clangxx = _rocm_llvm("bin", "clang++")
+    san = ["-fsanitize=address,undefined", "-fno-sanitize-recover=undefined", "-shared-libsan"]
+    _run([clangxx, "-O1", "-g", "-fno-omit-frame-pointer", "-ffp-contract=off", "-fopenmp", "-fPIC", "-std=c++17",
+          *san, "-shared", "-o", oracle_so, oracle_src, "-Wl,-rpath," + _rocm_llvm("lib")])
+    cc = hipcc()
+    objs, cmds = [], []
+    for src in SOURCES:
+        obj = os.path.join(SAN_DIR, os.path.basename(src) + ".o")
+        objs.append(obj)
+        cmds.append([cc, *COMMON_FLAGS, "-g", "-fno-omit-frame-pointer", *SAN_HOST_FLAGS, "-c", src, "-o", obj])
+    with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+        list(ex.map(_run, cmds))
+    lib = os.path.join(SAN_DIR, "libanelm_hip.so")
+    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-shared-libsan", *SAN_HOST_FLAGS, "-o", lib, *objs])
+    return dict(oracle=oracle_so, lib=lib, runtime=asan_runtime())
+
+
+def run_sanitized_tests(extra: list[str] | None = None) -> int:
+    """The CPU test suite (-m "not gpu") against the sanitizer build: the
+    runtime preloaded into the interpreter, the two libraries swapped in by
+    ANELM_LIB / ANELM_ORACLE_LIB.  Any AddressSanitizer or UBSan report
+    aborts the run.  Returns pytest's exit status."""
+    b = build_sanitized()
+    env = dict(os.environ, LD_PRELOAD=b["runtime"], ANELM_LIB=b["lib"], ANELM_ORACLE_LIB=b["oracle"],
+               # leaks of the HIP runtime and torch at exit are not this library's; everything else aborts
+               ASAN_OPTIONS="detect_leaks=0:abort_on_error=1:halt_on_error=1:detect_odr_violation=0",
+               UBSAN_OPTIONS="print_stacktrace=1:halt_on_error=1")
+    cmd = [sys.executable, "-m", "pytest", os.path.join(ROOT, "tests"), "-q", "-m", "not gpu", "-p", "no:cacheprovider",
+           *(extra or [])]
+    return subprocess.run(cmd, env=env, cwd=ROOT).returncode
+
+
 def build_all() -> None:
     build_oracle()
     build_lib()
-    if os.path.exists(os.path.join(ROOT, "tests", "cpp", "dropin_check.cpp")):
-        build_dropin_check()
+    for name in ("dropin_check", "dropin_timing"):
+        if os.path.exists(os.path.join(ROOT, "tests", "cpp", name + ".cpp")):
+            build_dropin_check(name)
     check_integration_doc()
 
 
 if __name__ == "__main__":
+    if "--sanitize" in sys.argv:
+        sys.exit(run_sanitized_tests(sys.argv[sys.argv.index("--sanitize") + 1:]))
     build_all()
     print("built", LIB)

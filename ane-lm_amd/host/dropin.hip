@@ -1,14 +1,16 @@
 // The reference-signature drop-in layer (ane_lm::rmsnorm, ane_lm::softmax,
 // ane_lm::sample_token, ...) over the C ABI.  Host pointers in, host pointers
-// out: each call stages its operands into a per-thread device buffer, runs
-// the HIP kernels on a per-thread stream and copies the results back before
-// returning, so callers that run these functions concurrently from several
-// threads (as models/llm/qwen3.cpp:451-461 does) never share state.
+// out: each call leases a staging slot (stream, pinned host buffer, device
+// buffer) from a process-wide pool, runs the HIP kernels on the slot's
+// stream and has the results in the caller's memory before returning, so
+// callers that run these functions concurrently from several threads (as
+// models/llm/qwen3.cpp:451-461 does) never share state.
 #include <hip/hip_runtime.h>
 
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <vector>
 
 #include "anelm_hip.h"
@@ -32,47 +34,118 @@ void check_hip(hipError_t e, const char* what) {
     if (e != hipSuccess) die(what, hipGetErrorString(e));
 }
 
-// Per-thread stream and growable device buffer.  They live until the
-// process ends (freed by the driver at exit), because the HIP runtime may
-// already be shut down when thread-local destructors run.
-struct Staging {
-    hipStream_t stream = nullptr;
-    char* buf = nullptr;
-    size_t cap = 0;
+// A staging slot: one HIP stream, a growable device buffer and a fixed
+// pinned host buffer.  Slots are leased to one call at a time from a
+// process-wide pool, so concurrent callers never share one, threads that
+// come and go reuse them, and the pool holds as many as were ever in use at
+// once.  Slots live until the process ends: the HIP runtime may already be
+// shut down when static destructors run, and the pinned buffers, once read
+// by kernels, are never returned.
+constexpr size_t kPinBytes = (size_t)512 << 10;
 
-    hipStream_t s() {
-        if (!stream) check_hip(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking), "hipStreamCreate");
-        return stream;
+struct Slot {
+    hipStream_t stream = nullptr;
+    char* dev = nullptr;
+    size_t dev_cap = 0;
+    char* pin = nullptr;   // kPinBytes of pinned, coherent host memory the kernels read and write directly
+};
+
+std::mutex g_pool_mu;
+std::vector<Slot*>* g_pool = new std::vector<Slot*>();
+
+Slot* acquire_slot() {
+    {
+        std::lock_guard<std::mutex> lk(g_pool_mu);
+        if (!g_pool->empty()) {
+            Slot* s = g_pool->back();
+            g_pool->pop_back();
+            return s;
+        }
     }
-    // Device memory for the given byte sizes, each 256-byte aligned.
+    Slot* s = new Slot();
+    check_hip(hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking), "hipStreamCreate");
+    check_hip(hipHostMalloc(reinterpret_cast<void**>(&s->pin), kPinBytes, hipHostMallocCoherent), "hipHostMalloc");
+    return s;
+}
+
+void release_slot(Slot* s) {
+    std::lock_guard<std::mutex> lk(g_pool_mu);
+    g_pool->push_back(s);
+}
+
+// One call's lease on a slot.  get() places the call's operands: in the
+// slot's pinned host buffer when they fit (the kernels then read and write
+// them in host memory, and h2d/d2h are host copies before the launch and
+// after the sync), else in device memory (h2d/d2h are stream copies).
+// Workspace asked for in get() is always device memory.
+class Lease {
+  public:
+    Lease() : slot_(acquire_slot()) {}
+    ~Lease() { release_slot(slot_); }
+    Lease(const Lease&) = delete;
+    Lease& operator=(const Lease&) = delete;
+
+    hipStream_t s() const { return slot_->stream; }
+
     template <size_t N>
-    void get(const size_t (&sizes)[N], char* (&out)[N]) {
+    void get(const size_t (&sizes)[N], char* (&out)[N], size_t scratch = 0, char** scratch_out = nullptr) {
         size_t off[N], total = 0;
         for (size_t i = 0; i < N; i++) {
             off[i] = total;
             total += (sizes[i] + 255) & ~(size_t)255;
         }
-        if (total > cap) {
-            if (buf) check_hip(hipFree(buf), "hipFree");
-            size_t ncap = total < ((size_t)1 << 20) ? ((size_t)1 << 20) : total;
-            check_hip(hipMalloc(reinterpret_cast<void**>(&buf), ncap), "hipMalloc");
-            cap = ncap;
+        zero_copy_ = total <= kPinBytes;
+        const size_t dev_need = (zero_copy_ ? 0 : total) + scratch;
+        if (dev_need > slot_->dev_cap) {
+            if (slot_->dev) check_hip(hipFree(slot_->dev), "hipFree");
+            const size_t ncap = dev_need < ((size_t)1 << 20) ? ((size_t)1 << 20) : dev_need;
+            check_hip(hipMalloc(reinterpret_cast<void**>(&slot_->dev), ncap), "hipMalloc");
+            slot_->dev_cap = ncap;
         }
-        for (size_t i = 0; i < N; i++) out[i] = buf + off[i];
+        char* base = zero_copy_ ? slot_->pin : slot_->dev;
+        for (size_t i = 0; i < N; i++) out[i] = base + off[i];
+        if (scratch_out) *scratch_out = slot_->dev + (zero_copy_ ? 0 : total);
     }
-    void h2d(void* d, const void* h, size_t n) { check_hip(hipMemcpyAsync(d, h, n, hipMemcpyHostToDevice, s()), "hipMemcpy H2D"); }
-    void d2h(void* h, const void* d, size_t n) { check_hip(hipMemcpyAsync(h, d, n, hipMemcpyDeviceToHost, s()), "hipMemcpy D2H"); }
-    void sync() { check_hip(hipStreamSynchronize(s()), "hipStreamSynchronize"); }
-};
+    void h2d(void* d, const void* h, size_t n) {
+        if (zero_copy_)
+            std::memcpy(d, h, n);
+        else
+            check_hip(hipMemcpyAsync(d, h, n, hipMemcpyHostToDevice, s()), "hipMemcpy H2D");
+    }
+    void d2h(void* h, const void* d, size_t n) {
+        if (!zero_copy_) {
+            check_hip(hipMemcpyAsync(h, d, n, hipMemcpyDeviceToHost, s()), "hipMemcpy D2H");
+            return;
+        }
+        if (nout_ == kMaxOut) die("drop-in staging", "too many outputs");
+        outs_[nout_++] = {h, d, n};
+    }
+    // Waits for the call's work, then copies zero-copy outputs out.
+    void sync() {
+        check_hip(hipStreamSynchronize(s()), "hipStreamSynchronize");
+        for (int i = 0; i < nout_; i++) std::memcpy(outs_[i].h, outs_[i].d, outs_[i].n);
+        nout_ = 0;
+    }
 
-thread_local Staging t_stage;
+  private:
+    static constexpr int kMaxOut = 8;
+    struct Out {
+        void* h;
+        const void* d;
+        size_t n;
+    };
+    Slot* slot_;
+    bool zero_copy_ = false;
+    Out outs_[kMaxOut];
+    int nout_ = 0;
+};
 
 }  // namespace
 
 // core/cpu_ops.cpp:7-14
 void silu_vec_inplace(float* x, int n, float* /*tmp*/) {
     if (n <= 0) return;
-    Staging& S = t_stage;
+    Lease S;
     const size_t sz[1] = {(size_t)n * 4};
     char* d[1];
     S.get(sz, d);
@@ -85,7 +158,7 @@ void silu_vec_inplace(float* x, int n, float* /*tmp*/) {
 // core/cpu_ops.cpp:16-23
 void mul_sigmoid_inplace(float* y, const float* z, int n, float* /*tmp*/) {
     if (n <= 0) return;
-    Staging& S = t_stage;
+    Lease S;
     const size_t sz[2] = {(size_t)n * 4, (size_t)n * 4};
     char* d[2];
     S.get(sz, d);
@@ -100,7 +173,7 @@ void mul_sigmoid_inplace(float* y, const float* z, int n, float* /*tmp*/) {
 // core/cpu_ops.cpp:25-31
 void rmsnorm(float* out, const float* x, const float* weight, int dim, float eps) {
     if (dim <= 0) return;
-    Staging& S = t_stage;
+    Lease S;
     const size_t sz[2] = {(size_t)dim * 4, (size_t)dim * 4};
     char* d[2];
     S.get(sz, d);
@@ -118,7 +191,7 @@ void apply_rope_cached(float* q, float* k, int n_q_heads, int n_kv_heads, int he
                        const float* sin_row) {
     const int nh = n_q_heads + n_kv_heads;
     if (nh <= 0 || rot_dim <= 0) return;
-    Staging& S = t_stage;
+    Lease S;
     // span of each operand that the rotation touches
     const size_t qn = n_q_heads > 0 ? (size_t)(n_q_heads - 1) * q_head_stride + rot_dim : 0;
     const size_t kn = n_kv_heads > 0 ? (size_t)(n_kv_heads - 1) * k_head_stride + rot_dim : 0;
@@ -146,13 +219,14 @@ void apply_rope_cached(float* q, float* k, int n_q_heads, int n_kv_heads, int he
 // core/cpu_ops.cpp:83-99
 void softmax(float* x, int n) {
     if (n <= 0) return;
-    Staging& S = t_stage;
+    Lease S;
     const size_t ws = anelm_softmax_workspace_size(1, n);
-    const size_t sz[2] = {(size_t)n * 4, ws};
-    char* d[2];
-    S.get(sz, d);
+    const size_t sz[1] = {(size_t)n * 4};
+    char* d[1];
+    char* dws = nullptr;
+    S.get(sz, d, ws, &dws);
     S.h2d(d[0], x, sz[0]);
-    check_rc(anelm_softmax(reinterpret_cast<float*>(d[0]), 1, n, n, d[1], ws, S.s()), "softmax");
+    check_rc(anelm_softmax(reinterpret_cast<float*>(d[0]), 1, n, n, dws, ws, S.s()), "softmax");
     S.d2h(x, d[0], sz[0]);
     S.sync();
 }
@@ -160,7 +234,7 @@ void softmax(float* x, int n) {
 // core/cpu_ops.cpp:33-39
 void rmsnorm_gated(float* out, const float* x, const float* z, const float* weight, int dim) {
     if (dim <= 0) return;
-    Staging& S = t_stage;
+    Lease S;
     const size_t n = (size_t)dim * 4;
     const size_t sz[4] = {n, n, n, n};
     char* d[4];
@@ -179,7 +253,7 @@ void rmsnorm_gated(float* out, const float* x, const float* z, const float* weig
 // core/cpu_ops.cpp:100-103
 void matvec(float* y, const float* W, const float* x, int out_dim, int in_dim) {
     if (out_dim <= 0 || in_dim <= 0) return;
-    Staging& S = t_stage;
+    Lease S;
     const size_t sz[3] = {(size_t)out_dim * in_dim * 4, (size_t)in_dim * 4, (size_t)out_dim * 4};
     char* d[3];
     S.get(sz, d);
@@ -195,7 +269,7 @@ void matvec(float* y, const float* W, const float* x, int out_dim, int in_dim) {
 // core/cpu_ops.cpp:105-110
 void l2_normalize(float* x, int dim) {
     if (dim <= 0) return;
-    Staging& S = t_stage;
+    Lease S;
     const size_t sz[1] = {(size_t)dim * 4};
     char* d[1];
     S.get(sz, d);
@@ -209,7 +283,7 @@ void l2_normalize(float* x, int dim) {
 void conv1d_update(float* y, float* conv_state, int* state_pos, const float* x, const float* w, int channels,
                    int kernel_size) {
     if (channels <= 0 || kernel_size < 2) return;
-    Staging& S = t_stage;
+    Lease S;
     const size_t sn = (size_t)channels * (kernel_size - 1) * 4;
     const size_t sz[5] = {(size_t)channels * 4, sn, 4, (size_t)channels * 4, (size_t)channels * kernel_size * 4};
     char* d[5];
@@ -235,7 +309,7 @@ void conv1d_update(float* y, float* conv_state, int* state_pos, const float* x, 
 // core/cpu_ops.cpp:152-171
 void ssm_step(float* y, float* state, const float* q, const float* k, const float* v, float decay, float beta,
               int key_dim, int value_dim) {
-    Staging& S = t_stage;
+    Lease S;
     const size_t sn = (size_t)key_dim * value_dim * 4;
     const size_t sz[7] = {(size_t)value_dim * 4, sn, (size_t)key_dim * 4, (size_t)key_dim * 4,
                           (size_t)value_dim * 4, 4, 4};
@@ -267,21 +341,22 @@ void gqa_attention(float* out, const float* q, const float* k_cache, const float
         std::memset(out, 0, (size_t)n_heads * head_dim * sizeof(float));
         return;
     }
-    Staging& S = t_stage;
+    Lease S;
     const size_t qn = (size_t)(n_heads - 1) * q_head_stride + head_dim;
     const size_t cn = (size_t)cache_capacity * n_kv_heads * head_dim;
     const size_t on = (size_t)n_heads * head_dim;
     const size_t ws = anelm_gqa_workspace_size(1, n_heads, n_kv_heads, head_dim, cache_capacity);
-    const size_t sz[5] = {qn * 4, cn * 4, cn * 4, on * 4, ws};
-    char* d[5];
-    S.get(sz, d);
+    const size_t sz[4] = {qn * 4, cn * 4, cn * 4, on * 4};
+    char* d[4];
+    char* dws = nullptr;
+    S.get(sz, d, ws, &dws);
     S.h2d(d[0], q, sz[0]);
     S.h2d(d[1], k_cache, sz[1]);
     S.h2d(d[2], v_cache, sz[2]);
     check_rc(anelm_gqa_attention_ring(reinterpret_cast<float*>(d[3]), reinterpret_cast<const float*>(d[0]),
                                       reinterpret_cast<const float*>(d[1]), reinterpret_cast<const float*>(d[2]),
                                       n_heads, n_kv_heads, head_dim, q_head_stride, cache_start, cache_len,
-                                      cache_capacity, ws ? d[4] : nullptr, ws, S.s()),
+                                      cache_capacity, ws ? dws : nullptr, ws, S.s()),
              "gqa_attention");
     S.d2h(out, d[3], sz[3]);
     S.sync();
@@ -291,12 +366,14 @@ void gqa_attention(float* out, const float* q, const float* k_cache, const float
 int sample_token(const float* logits, int vocab_size, const SamplingParams& params,
                  const std::vector<int>& recent_tokens) {
     if (vocab_size <= 0) die("sample_token", "vocab_size <= 0");
-    Staging& S = t_stage;
+    Lease S;
     const long nh = (long)recent_tokens.size();
     const size_t ws = anelm_sample_workspace_size(1, vocab_size);
-    const size_t sz[6] = {(size_t)vocab_size * 4, (size_t)(nh > 0 ? nh : 1) * 4, 16, 16, ws, (size_t)vocab_size * 4};
-    char* d[6];
-    S.get(sz, d);
+    // the probabilities (d[4]) are written and never read back
+    const size_t sz[5] = {(size_t)vocab_size * 4, (size_t)(nh > 0 ? nh : 1) * 4, 16, 16, (size_t)vocab_size * 4};
+    char* d[5];
+    char* dws = nullptr;
+    S.get(sz, d, ws, &dws);
     S.h2d(d[0], logits, sz[0]);
     if (nh > 0) S.h2d(d[1], recent_tokens.data(), (size_t)nh * 4);
     const bool draw = params.temperature > 0.0f;
@@ -308,10 +385,10 @@ int sample_token(const float* logits, int vocab_size, const SamplingParams& para
     p.repetition_penalty = params.repetition_penalty;
     p.repetition_context_size = params.repetition_context_size;
     p.frequency_penalty = params.frequency_penalty;
-    check_rc(anelm_sample(reinterpret_cast<int32_t*>(d[3]), reinterpret_cast<float*>(d[5]), vocab_size,
+    check_rc(anelm_sample(reinterpret_cast<int32_t*>(d[3]), reinterpret_cast<float*>(d[4]), vocab_size,
                           reinterpret_cast<const float*>(d[0]),
                           vocab_size, 1, vocab_size, nh > 0 ? reinterpret_cast<const int32_t*>(d[1]) : nullptr, nh,
-                          nullptr, &p, reinterpret_cast<const float*>(d[2]), d[4], ws, S.s()),
+                          nullptr, &p, reinterpret_cast<const float*>(d[2]), dws, ws, S.s()),
              "sample_token");
     int32_t id = 0;
     S.d2h(&id, d[3], 4);
@@ -323,7 +400,7 @@ namespace hip {
 
 void residual_add(float* x, const float* y, int n) {
     if (n <= 0) return;
-    Staging& S = t_stage;
+    Lease S;
     const size_t sz[2] = {(size_t)n * 4, (size_t)n * 4};
     char* d[2];
     S.get(sz, d);
@@ -338,7 +415,7 @@ void residual_add(float* x, const float* y, int n) {
 void qknorm_rope_qwen3(float* q, float* k, int nq, int nk, int head_dim, const float* q_norm, const float* k_norm,
                        float eps, int pos, float theta, const float* cos_row, const float* sin_row) {
     if (nq + nk <= 0 || head_dim <= 0) return;
-    Staging& S = t_stage;
+    Lease S;
     const size_t qn = (size_t)nq * head_dim, kn = (size_t)nk * head_dim, half = (size_t)head_dim / 2;
     const bool tab = cos_row && sin_row;
     const size_t sz[7] = {qn * 4, kn * 4, (size_t)head_dim * 4, (size_t)head_dim * 4, half * 4, half * 4, 4};
@@ -368,7 +445,7 @@ void qknorm_rope_qwen3(float* q, float* k, int nq, int nk, int head_dim, const f
 
 void silu_mul(float* h, const float* g, const float* u, int n) {
     if (n <= 0) return;
-    Staging& S = t_stage;
+    Lease S;
     const size_t sz[2] = {(size_t)n * 4, (size_t)n * 4};
     char* d[2];
     S.get(sz, d);
@@ -382,7 +459,7 @@ void silu_mul(float* h, const float* g, const float* u, int n) {
 
 void bf16_to_f16_vec_n(uint16_t* out, const uint16_t* in, size_t n) {
     if (n == 0) return;
-    Staging& S = t_stage;
+    Lease S;
     const size_t sz[1] = {n * 2};
     char* d[1];
     S.get(sz, d);

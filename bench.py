@@ -45,9 +45,9 @@ WORKLOADS = {
 HEADLINE = "qwen3-8b-prefill"
 OPS = ["rmsnorm", "qknorm_rope", "add_rmsnorm", "silu_mul", "residual_add"]
 # the kernel each op launches at the workload shapes: (name fragment, template fragment)
-OP_KERNELS = {"rmsnorm": ("rmsnorm_row_kernel", "false>"), "qknorm_rope": ("qknorm_rope128_kernel", ""),
-              "add_rmsnorm": ("rmsnorm_row_kernel", "true>"), "silu_mul": ("silu_mul_vec_kernel", ""),
-              "residual_add": ("residual_add_vec_kernel", "")}
+OP_KERNELS = {"rmsnorm": ("rmsnorm_row_kernel", "false, false>"), "qknorm_rope": ("qknorm_rope128_w8_kernel", ""),
+              "add_rmsnorm": ("rmsnorm_row_kernel", "true, false>"), "silu_mul": ("silu_mul_vec_kernel", ""),
+              "residual_add": ("residual_add_vec_kernel", ""), "layer_ops": ("layer_ops_kernel", "")}
 PROFILES = os.path.join(ROOT, "profiles")
 # The counter runs behind profiles/pmc_traffic_<workload>.txt (run from the repo root):
 # one counter per run over `bench.py <args>`, and the same counter over a plain
@@ -722,6 +722,26 @@ def cpu_convert(target_s):
                 sample=f"{done} parameters in chunks of 2^26 on {oracle.max_threads()} threads")
 
 
+def dropin_per_call():
+    """Per-call wall time of the unchanged-caller path: ane_lm::rmsnorm at
+    dim 1024 and 128 (and a layer's 40 head norms from 8 threads) and
+    ane_lm::sample_token at 151936, each a synchronous host-pointer call
+    through the drop-in layer, beside the oracle's single-thread CPU time of
+    the same function (tests/cpp/dropin_timing.cpp, built by build())."""
+    import subprocess
+
+    exe = os.path.join(ROOT, "tests", "cpp", "dropin_timing")
+    if not os.path.exists(exe):
+        return dict(note="tests/cpp/dropin_timing not built")
+    r = subprocess.run([exe], stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True, timeout=300)
+    if r.returncode != 0:
+        raise SystemExit(f"dropin_timing failed ({r.returncode}): {r.stderr[-2000:]}")
+    out = json.loads(r.stdout.strip().splitlines()[-1])
+    out["note"] = ("wall time per call from the host, H2D + kernels + D2H + stream sync; oracle = the same function "
+                   "on one CPU thread (the reference's cost where it runs on the CPU)")
+    return out
+
+
 # ------------------------------------------------------------ rocprofv3 summaries
 
 def _csv_rows(d, suffix):
@@ -743,6 +763,13 @@ ATTN_KERNELS = {"gqa_decode": ("gqa_decode_kernel", ""), "gqa_combine": ("gqa_co
 SAMPLE_KERNELS = {"stage1": ("sample_stage1_kernel", ""), "stage2": ("sample_stage2_kernel", ""),
                   "stage3": ("sample_stage3_kernel", ""), "walk": ("sample_walk_kernel", "")}
 SAMPLER = "sampling-64x151936"
+
+# The 64-sequence decode step's LM head (x staged in LDS) and layer kernels
+Q3_B64 = "qwen3-0.6b-decode-step-b64"
+Q3_B64_KERNELS = {"lm_head": ("proj_lds_kernel", ""), "attention": ("gqa_decode_kernel", ""),
+                  "merge": ("gqa_combine_kernel", ""), "norm_f16": ("rmsnorm_row_kernel", "true>"),
+                  "proj_add": ("proj_mfma_kernel", "false, 1, 4>"), "gate_up_swiglu": ("proj_mfma_kernel", "false, 3, 4>"),
+                  "qkv": ("proj_mfma_kernel", "false, 0, 4>")}
 
 # The one-sequence decode step's projections, told apart by their launch
 # shapes (rows per wave, chunks in flight, fused norm, epilogue)
@@ -766,7 +793,101 @@ def _kernels_of(workload):
         return SAMPLE_KERNELS
     if workload == Q3_B1:
         return Q3_KERNELS
+    if workload == Q3_B64:
+        return Q3_B64_KERNELS
     return ATTN_KERNELS if workload in ATTN_WORKLOADS else OP_KERNELS
+
+
+def _run_args(workload):
+    """bench.py arguments of the run a counter summary of `workload` is made from."""
+    if workload in ATTN_WORKLOADS or workload == SAMPLER:
+        return f"--only {workload} --steps 1"
+    if workload in (Q3_B1, Q3_B64):
+        return f"--only {workload} --no-cpu"
+    if workload == HEADLINE:
+        return f"--workload {workload} --chain-only --no-cpu --steps 1 --warmup 0"
+    return f"--only {workload} --steps 1 --warmup 0"
+
+
+# SQ counters in two passes (at most 8 SQ counters per rocprofv3 --pmc run)
+SQ_PASSES = [["SQ_WAVES", "SQ_WAVE_CYCLES", "SQ_BUSY_CU_CYCLES", "SQ_WAIT_ANY", "SQ_WAIT_INST_ANY",
+              "SQ_INSTS_VALU", "SQ_ACTIVE_INST_VALU", "SQ_INSTS_SALU"],
+             ["SQ_INSTS_VMEM_RD", "SQ_INSTS_VMEM_WR", "SQ_INSTS_LDS", "SQ_WAIT_INST_LDS", "SQ_ACTIVE_INST_ANY",
+              "GRBM_GUI_ACTIVE"],
+             # rocprofv3's derived metrics over the level counters (SQ_LEVEL_WAVES, SQ_INST_LEVEL_VMEM), which
+             # mean nothing unless accumulated: one per pass, each takes the accumulator
+             ["MeanOccupancyPerActiveCU"], ["VmemLatency"]]
+N_XCC, N_SIMD = 8, 1024   # MI355X: GRBM_GUI_ACTIVE is summed over the 8 XCCs; 256 CUs x 4 SIMDs
+
+
+def sq_commands(dirs, workload):
+    return [f"rocprofv3 --pmc {' '.join(c)} --output-format csv -d {d} -o r -- python bench.py {_run_args(workload)}"
+            for c, d in zip(SQ_PASSES, dirs)]
+
+
+def sq_summary(dirs, workload=HEADLINE):
+    """Text summary of the four SQ-counter runs of sq_commands(): per kernel,
+    per dispatch (SQ_WAVE_CYCLES, SQ_BUSY_CU_CYCLES, SQ_WAIT_*, SQ_ACTIVE_INST_*
+    count quad-cycles; GRBM_GUI_ACTIVE counts cycles on each of the 8 XCCs):
+      waves/CU    = 4 * SQ_WAVE_CYCLES / (kernel_cyc * 256 CUs)  (mean resident waves per CU over the
+                    dispatch, of 32: the numerator of rocprofv3's OccupancyPercent)
+      occ_rocprof = MeanOccupancyPerActiveCU             (rocprofv3's accumulated SQ_LEVEL_WAVES over
+                    SQ_BUSY_CU_CYCLES, which counts each SIMD of a busy CU: a per-SIMD figure, of 8)
+      wave_cyc    = 4 * SQ_WAVE_CYCLES / SQ_WAVES        (mean wave lifetime, cycles)
+      wait        = SQ_WAIT_ANY / SQ_WAVE_CYCLES         (share of wave time waiting on memory or dependencies)
+      issue_wait  = SQ_WAIT_INST_ANY / SQ_WAVE_CYCLES    (share of wave time waiting for an issue slot)
+      vmem_lat    = VmemLatency                          (mean cycles a vector memory instruction is in flight)
+      valu_util   = 4 * SQ_ACTIVE_INST_VALU / (1024 SIMDs * GRBM_GUI_ACTIVE / 8)  (VALU busy share of the chip)
+      kernel_cyc  = GRBM_GUI_ACTIVE / 8"""
+    cm = [_counter_means(d) for d in dirs]
+    kernels = _kernels_of(workload)
+    lines = [f"# SQ counters per dispatch, workload {workload} (rocprofv3 --pmc, four passes)", "#",
+             "# commands (from the repo root):"] + [
+             f"#   {c}" for c in sq_commands(dirs, workload)] + [
+             f"#   python bench.py --workload {workload} --sq-summary {' '.join(dirs)}", "#",
+             "# SQ_WAVE_CYCLES, SQ_BUSY_CU_CYCLES, SQ_WAIT_ANY, SQ_WAIT_INST_ANY, SQ_ACTIVE_INST_VALU count quad-cycles;",
+             "# GRBM_GUI_ACTIVE counts cycles on each of the 8 XCCs.",
+             "# waves/CU = 4*SQ_WAVE_CYCLES/(kernel cyc*256 CUs) (mean resident waves per CU over the dispatch, of 32); "
+             "occ_rocprof = MeanOccupancyPerActiveCU (accumulated SQ_LEVEL_WAVES/SQ_BUSY_CU_CYCLES, per SIMD, of 8);",
+             "# wave cyc = 4*SQ_WAVE_CYCLES/SQ_WAVES; wait = SQ_WAIT_ANY/SQ_WAVE_CYCLES; issue_wait = "
+             "SQ_WAIT_INST_ANY/SQ_WAVE_CYCLES; vmem_lat = VmemLatency (cycles);",
+             "# valu_util = 4*SQ_ACTIVE_INST_VALU/(1024*GRBM_GUI_ACTIVE/8); kernel cyc = GRBM_GUI_ACTIVE/8",
+             "",
+             "| op | kernel | dispatches | waves | waves/CU | occ_rocprof | kernel cyc | wave cyc | wait | issue_wait | "
+             "vmem_lat | VALU/wave | valu_util | SALU/wave | LDS/wave | VMEM rd/wr per wave |",
+             "|---|---|---|---|---|---|---|---|---|---|---|---|---|---|---|---|"]
+    out = {}
+    for op in kernels:
+        v = {}
+        n = 0
+        kname = None
+        for c in cm:
+            for (k, name), (cnt, mean) in c.items():
+                if _match(k, op, kernels):
+                    v[name] = mean
+                    n, kname = cnt, k
+        need = ("SQ_WAVES", "SQ_INSTS_VMEM_RD", "GRBM_GUI_ACTIVE", "VmemLatency")
+        if not all(x in v for x in need):
+            continue
+        wv = max(v["SQ_WAVES"], 1.0)
+        wc = max(v["SQ_WAVE_CYCLES"], 1.0)
+        kc = max(v["GRBM_GUI_ACTIVE"] / N_XCC, 1.0)
+        d = dict(waves=round(v["SQ_WAVES"]), waves_per_cu=round(4 * v["SQ_WAVE_CYCLES"] / (kc * N_SIMD / 4), 1),
+                 occ_rocprof=round(v["MeanOccupancyPerActiveCU"], 1), kernel_cycles=round(kc),
+                 wave_cycles=round(4 * v["SQ_WAVE_CYCLES"] / wv), wait=round(v["SQ_WAIT_ANY"] / wc, 3),
+                 issue_wait=round(v["SQ_WAIT_INST_ANY"] / wc, 3), vmem_lat=round(v["VmemLatency"]),
+                 valu_per_wave=round(v["SQ_INSTS_VALU"] / wv),
+                 valu_util=round(4 * v["SQ_ACTIVE_INST_VALU"] / (N_SIMD * kc), 3),
+                 salu_per_wave=round(v["SQ_INSTS_SALU"] / wv), lds_per_wave=round(v["SQ_INSTS_LDS"] / wv, 1),
+                 vmem_rd_per_wave=round(v["SQ_INSTS_VMEM_RD"] / wv, 1), vmem_wr_per_wave=round(v["SQ_INSTS_VMEM_WR"] / wv, 1))
+        out[op] = d
+        short = kname.replace("(anonymous namespace)::", "").split("(")[0].replace("void ", "")
+        lines.append(f"| {op} | `{short}` | {n} | {d['waves']} | {d['waves_per_cu']} | {d['occ_rocprof']} | "
+                     f"{d['kernel_cycles']} | {d['wave_cycles']} | {d['wait']} | {d['issue_wait']} | {d['vmem_lat']} | "
+                     f"{d['valu_per_wave']} | {d['valu_util']} | {d['salu_per_wave']} | {d['lds_per_wave']} | "
+                     f"{d['vmem_rd_per_wave']} / {d['vmem_wr_per_wave']} |")
+    lines += ["", "sq_json: " + json.dumps(dict(workload=workload, per_dispatch=out))]
+    return "\n".join(lines)
 
 
 def _match(name, op, kernels=None):
@@ -794,23 +915,23 @@ def pmc_summary(fetch_dir, write_dir, copy_fetch_dir, copy_write_dir, workload=H
     copy_w = max(v for (k, c), (n, v) in cw.items() if "copyBuffer" in k and c == "WRITE_SIZE")
     ff, wf = COPY_BYTES / 1024 / copy_f, COPY_BYTES / 1024 / copy_w
     kernels = _kernels_of(workload)
+    run_args = _run_args(workload)
     if workload in ATTN_WORKLOADS:
         w = ATTN_WORKLOADS[workload]
         ob = {"gqa_decode": attn_bytes(w), "gqa_combine": 0}
-        run_args = f"--only {workload} --steps 1"
     elif workload == Q3_B1:
         ob = q3_b1_bytes()
-        run_args = f"--only {workload} --no-cpu"
+    elif workload == Q3_B64:
+        c = Q3_06B
+        ob = {k: 0 for k in Q3_B64_KERNELS}
+        ob["lm_head"] = 2 * c["vocab"] * c["hidden"] + 64 * c["vocab"] * 4   # fp16 W once + fp32 logits
     elif workload == SAMPLER:
         # stage 1 reads the logits; stage 2 reads them again and writes exp(x - max)
         # into the probability buffer; stage 3 reads that and writes the probabilities
         lv = 64 * VOCAB * 4
         ob = {"stage1": lv, "stage2": 2 * lv, "stage3": 2 * lv, "walk": 0}
-        run_args = f"--only {workload} --steps 1"
     else:
-        ob = op_bytes(WORKLOADS[workload])
-        run_args = (f"--workload {workload} --chain-only --no-cpu --steps 1 --warmup 0" if workload == HEADLINE
-                    else f"--only {workload} --steps 1 --warmup 0")
+        ob = dict(op_bytes(WORKLOADS[workload]), layer_ops=layer_ops_bytes(WORKLOADS[workload]))
     commands = pmc_commands(fetch_dir, write_dir, copy_fetch_dir, copy_write_dir, run_args)
     lines = [f"# HBM traffic per dispatch, workload {workload} (rocprofv3 --pmc, one counter per run)", "#",
              "# commands (from the repo root):"] + [f"#   {c}" for c in commands] + [
@@ -885,7 +1006,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default=HEADLINE, choices=sorted(WORKLOADS) + sorted(ATTN_WORKLOADS) + [SAMPLER, Q3_B1],
+    ap.add_argument("--workload", default=HEADLINE, choices=sorted(WORKLOADS) + sorted(ATTN_WORKLOADS) + [SAMPLER, Q3_B1, Q3_B64],
                     help="op-chain workload to run (attention names only select --pmc-summary kernels)")
     ap.add_argument("--cpu-seconds", type=float, default=8.0, help="CPU time budget of the headline baseline")
     ap.add_argument("--no-cpu", action="store_true")
@@ -899,12 +1020,18 @@ def main():
                     help="print the traffic summary of four rocprofv3 --pmc output directories and exit")
     ap.add_argument("--trace-summary", nargs=2, metavar=("DIR", "COMMAND"),
                     help="print the summary of a rocprofv3 --kernel-trace --stats directory and exit")
+    ap.add_argument("--sq-summary", nargs=len(SQ_PASSES), metavar=tuple(f"SQ_{i}" for i in range(len(SQ_PASSES))),
+                    help="print the SQ-counter summary of the rocprofv3 --pmc output directories of "
+                         "sq_commands() and exit")
     args = ap.parse_args()
     if args.pmc_summary:
         print(pmc_summary(*args.pmc_summary, workload=args.workload))
         return
     if args.trace_summary:
         print(trace_summary(*args.trace_summary))
+        return
+    if args.sq_summary:
+        print(sq_summary(args.sq_summary, workload=args.workload))
         return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); the op chain shards "
@@ -936,6 +1063,8 @@ def main():
             r = measure_sampler(anelm, max(args.steps, 20), rows=1)
         elif args.only == "convert-qwen3-8b-bf16":
             r = measure_convert(anelm)
+        elif args.only == "dropin-per-call":
+            r = dropin_per_call()
         elif args.only in Q3_WORKLOADS:
             import tempfile
 
@@ -1011,6 +1140,9 @@ def main():
             cpu_configs["sampling-1x151936"] = cpu_sampler(0.5, rows=1)
             cpu_configs["attention-qwen3-8b-decode"] = cpu_attention(ATTN_WORKLOADS["attention-qwen3-8b-decode-b1"], 1.5)
             cpu_configs["convert-qwen3-8b-bf16"] = cpu_convert(1.5)
+    dropin = None
+    if not args.no_cpu and not args.headline_only:
+        dropin = dropin_per_call()
     out = {
         "metric": METRIC,
         "value": head["GBps"],
@@ -1039,6 +1171,7 @@ def main():
         "ops": head["ops"],
         "configs": configs,
         "cpu_configs": cpu_configs,
+        "dropin_per_call": dropin,
     }
     print(json.dumps(out))
 

@@ -11,7 +11,8 @@ import os
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "liboracle.so")
+# ANELM_ORACLE_LIB names another build of the same library (the sanitizer build)
+LIB_PATH = os.environ.get("ANELM_ORACLE_LIB") or os.path.join(HERE, "liboracle.so")
 
 _P, _L, _I, _F, _S = ctypes.c_void_p, ctypes.c_long, ctypes.c_int, ctypes.c_float, ctypes.c_size_t
 _U16 = ctypes.c_uint16
