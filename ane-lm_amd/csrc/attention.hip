@@ -16,7 +16,9 @@
 //   phase 3: the same position mapping over V rows, weighted accumulation.
 // With one chunk per sequence the workgroup writes the normalised output;
 // otherwise it writes (max, sum, unnormalised output) partials that a second
-// kernel merges.
+// kernel merges.  The grid is (kv head, sequence, chunk), chunk slowest: a
+// short ring is done by its chunk 0 alone (the other chunks exit at once), and
+// with chunks dispatched last those workgroups all start in the first round.
 #include "anelm_common.hpp"
 
 namespace anelm {
@@ -143,8 +145,8 @@ __global__ __launch_bounds__(kAttnThreads) void gqa_decode_kernel(AttnArgs a) {
     __shared__ float hm[GM], hl[GM];
 
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wid = tid / kWave;
-    const int split = blockIdx.x, kvh = blockIdx.y;
-    const long b = blockIdx.z;
+    const int kvh = blockIdx.x, split = blockIdx.z;
+    const long b = blockIdx.y;
     const int qpos = QK >= 0 ? a.pos[b] : 0;   // read beside the ring state
     int start, len;
     ring_state(a, b, start, len);
@@ -510,7 +512,7 @@ int group_max(int D) { return kMaxGD / D < 8 ? kMaxGD / D : 8; }
 
 template <int D, int GM, int QK>
 void launch_gm(const AttnArgs& a, long batch, hipStream_t st) {
-    const dim3 grid(a.nsplit, a.nkv, batch);
+    const dim3 grid(a.nkv, batch, a.nsplit);
     if (a.nsplit == 1) {
         hipLaunchKernelGGL((gqa_decode_kernel<D, GM, true, QK>), grid, dim3(kAttnThreads), 0, st, a);
     } else {

@@ -339,6 +339,18 @@ def test_decode_big_vocab_past_16_rows(hip, orc, rng, tmp_path, B, ld_pad):
     assert _decode_vs_oracle(hip, orc, rng, path, t, d, B, steps=18, cap=16, ld_pad=ld_pad) < 4e-3
 
 
+@pytest.mark.parametrize("B,steps", [(1, 200), (3, 170), (20, 170)])
+def test_decode_long_rings_match_oracle(hip, orc, rng, tmp_path, B, steps):
+    """Rings longer than one attention chunk: at capacity 160 the rings pass
+    128 rows (from then on the attention splits each over 5 chunks of 32
+    whose partials a second launch merges), fill up and wrap.  Every step
+    against the oracle."""
+    t, d = tiny_qwen3(rng)
+    path = tmp_path / "long.safetensors"
+    save_qwen3(path, t)
+    assert _decode_vs_oracle(hip, orc, rng, path, t, d, B, steps=steps, cap=160) < 4e-3
+
+
 @pytest.mark.parametrize("B", [3, 9, 20])
 def test_decode_dims_not_multiples_of_32(hip, orc, rng, tmp_path, B):
     """Hidden and intermediate sizes that are not multiples of 32 (H 224 is,
