@@ -20,7 +20,7 @@ namespace doc {
 constexpr int kLayers = 64;
 
 // the layer loop of a device-resident forward (qwen3.cpp:497-530)
-extern float *x, *xn, *q, *k, *v, *attn, *y, *h, *g, *u, *probs, *logits, *r, *qkv;
+extern float *x, *xn, *xn2, *q, *k, *v, *attn, *mlp, *y, *h, *g, *u, *probs, *logits, *r, *qkv;
 extern const void* embed_f16;
 extern int32_t *ids, *bad_count, *hist, *hist_len;
 extern const int32_t* pos;
