@@ -73,6 +73,19 @@ __device__ __forceinline__ float group16_sum(float v) {
     return v;
 }
 
+// Sum over the wave, every lane receiving it: the 16-lane DPP sums, then
+// the four row sums (lanes 0, 16, 32, 48) added in a fixed order.  DPP moves
+// and lane reads take a few cycles each, where each step of a shuffle sum
+// (wave_sum) is an LDS permute round trip.  Every lane of the wave active.
+__device__ __forceinline__ float wave_sum_rows(float v) {
+    v = group16_sum(v);
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return (r0 + r1) + (r2 + r3);
+}
+
 __device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
 #pragma unroll
     for (int d = 32; d >= 1; d >>= 1) {
@@ -223,11 +236,22 @@ struct Gamma4 {
     __device__ __forceinline__ void load(const void* w, int c) {
         bits = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(w) + c);
     }
+    // fp16: the conversion instruction widens every non-NaN value exactly
+    // (normal, subnormal, zero, infinity) in one operation; a NaN keeps its
+    // payload unquieted only through the integer widening, which the wave
+    // takes when any of its lanes holds one.
     __device__ __forceinline__ float4 get() const {
-        if constexpr (DT == ANELM_F16)
-            return make_float4(f16_to_f32_exact(bits.x & 0xFFFFu), f16_to_f32_exact(bits.x >> 16),
-                               f16_to_f32_exact(bits.y & 0xFFFFu), f16_to_f32_exact(bits.y >> 16));
-        else
+        if constexpr (DT == ANELM_F16) {
+            const float4 f = make_float4((float)__builtin_bit_cast(_Float16, (uint16_t)(bits.x & 0xFFFFu)),
+                                         (float)__builtin_bit_cast(_Float16, (uint16_t)(bits.x >> 16)),
+                                         (float)__builtin_bit_cast(_Float16, (uint16_t)(bits.y & 0xFFFFu)),
+                                         (float)__builtin_bit_cast(_Float16, (uint16_t)(bits.y >> 16)));
+            const bool nan = f.x != f.x || f.y != f.y || f.z != f.z || f.w != f.w;
+            if (__builtin_expect(__ballot(nan) != 0, 0))
+                return make_float4(f16_to_f32_exact(bits.x & 0xFFFFu), f16_to_f32_exact(bits.x >> 16),
+                                   f16_to_f32_exact(bits.y & 0xFFFFu), f16_to_f32_exact(bits.y >> 16));
+            return f;
+        } else
             return make_float4(bf16_to_f32(bits.x & 0xFFFFu), bf16_to_f32(bits.x >> 16), bf16_to_f32(bits.y & 0xFFFFu),
                                bf16_to_f32(bits.y >> 16));
     }

@@ -114,8 +114,8 @@ __device__ __forceinline__ void x_chain(const LayerArgs& a, long row) {
         ss2 = fmaf(c.z, c.z, ss2);
         ss2 = fmaf(c.w, c.w, ss2);
     }
-    ss1 = wave_sum(ss1);
-    ss2 = wave_sum(ss2);
+    ss1 = wave_sum_rows(ss1);
+    ss2 = wave_sum_rows(ss2);
     if (nw > 1) {
         if ((tid & 63) == 0) {
             part[0][tid >> 6] = ss1;

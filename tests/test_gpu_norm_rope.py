@@ -62,6 +62,30 @@ def test_rmsnorm_f16_output(hip, orc, rng, rows, dim, dt):
     assert np.all(np.abs(got - want) <= ulp + np.abs(want) * REL_TOL)
 
 
+def test_rmsnorm_f16_gamma_every_pattern(hip, orc):
+    """The row RMSNorm's fp16 gamma widened for all 65,536 bit patterns, four
+    calls of 16,384 columns (the row kernel's full-row shape): x is all ones,
+    so every column's x*s is the same float s (the sum of squares is exact),
+    and each output is fl(s * gamma).  Non-NaN gammas (normal, subnormal,
+    zero, infinity: the conversion instruction) must match the oracle's exact
+    widening bit for bit; the waves that hold NaN patterns take the integer
+    widening and give NaN."""
+    import torch
+
+    x = np.ones((2, 16384), np.float32)
+    for k in range(4):
+        bits = np.arange(k * 16384, (k + 1) * 16384, dtype=np.uint32).astype(np.uint16)
+        w16 = bits.view(np.float16)
+        out = torch.empty(2, 16384, device="cuda")
+        hip.rmsnorm(out, dev(x), dev(bits).view(torch.float16), 1e-6)
+        got = host(out)
+        want = orc.rmsnorm(x[0], w16.astype(np.float32), 1e-6)   # numpy's fp16 widening is exact
+        nan = np.isnan(w16)
+        for r in range(2):
+            assert_bitexact(got[r][~nan], want[~nan], f"patterns {k * 16384}..: row {r}")
+            assert np.all(np.isnan(got[r][nan]))
+
+
 def test_rmsnorm_in_place_and_strided(hip, orc, rng):
     import torch
 
