@@ -110,6 +110,9 @@ _SIGS = {
     "anelm_proj_f16_x16": (_I, [_P, _P, _P, _L, _I, _I, _L, _L, _P]),
     "anelm_proj_f16_fused": (_I, [_P, _P, _P, _L, _I, _I, _L, _L, _P, _F, _I, _P]),
     "anelm_proj_f16_x16_fused": (_I, [_P, _P, _P, _L, _I, _I, _L, _L, _I, _P]),
+    "anelm_proj_tiled_size": (_S, [_I, _I]),
+    "anelm_proj_tile_f16": (_I, [_P, _P, _I, _I, _P]),
+    "anelm_proj_f16_x16_tiled": (_I, [_P, _P, _P, _L, _I, _I, _L, _L, _I, _P]),
     "anelm_qwen3_load": (_P, [ctypes.c_char_p, _P, _I, _I, _P]),
     "anelm_qwen3_free": (None, [_P]),
     "anelm_qwen3_reset": (_I, [_P, _P]),
@@ -602,7 +605,7 @@ def proj_f16_x16(y, x16, w16, stream=None):
                                     _stream(stream)))
 
 
-PROJ_STORE, PROJ_ADD, PROJ_SWIGLU, PROJ_SWIGLU_F16 = 0, 1, 2, 3
+PROJ_STORE, PROJ_ADD, PROJ_SWIGLU, PROJ_SWIGLU_F16, PROJ_STORE_F16 = 0, 1, 2, 3, 4
 
 
 def proj_f16_fused(y, x, w16, norm=None, eps=1e-6, epilogue=PROJ_STORE, stream=None):
@@ -622,6 +625,25 @@ def proj_f16_x16_fused(y, x16, w16, epilogue=PROJ_STORE, stream=None):
     out_dim = w16.shape[0] // 2 if epilogue in (PROJ_SWIGLU, PROJ_SWIGLU_F16) else w16.shape[0]
     _check(lib().anelm_proj_f16_x16_fused(_ptr(y), _ptr(x16), _ptr(w16), batch, out_dim, in_dim, _ld(x16), _ld(y),
                                           epilogue, _stream(stream)))
+
+
+def proj_tiled_size(out_dim, in_dim):
+    """Bytes of the tiled copy of an [out_dim, in_dim] fp16 W (0 if in_dim % 32)."""
+    return lib().anelm_proj_tiled_size(out_dim, in_dim)
+
+
+def proj_tile_f16(w_tiled, w16, stream=None):
+    """w_tiled (uint8/int16 tensor of proj_tiled_size bytes) = the tiled layout of w16 [out, in]."""
+    out_dim, in_dim = w16.shape
+    _check(lib().anelm_proj_tile_f16(_ptr(w_tiled), _ptr(w16), out_dim, in_dim, _stream(stream)))
+
+
+def proj_f16_x16_tiled(y, x16, w_tiled, out_dim, epilogue=PROJ_STORE, stream=None):
+    """y [B, out] = the projection of fp16 rows x16 on a tiled W: fp32 (PROJ_STORE)
+    or fp16 bits (PROJ_STORE_F16)."""
+    batch, in_dim = x16.shape
+    _check(lib().anelm_proj_f16_x16_tiled(_ptr(y), _ptr(x16), _ptr(w_tiled), batch, out_dim, in_dim, _ld(x16),
+                                          _ld(y), epilogue, _stream(stream)))
 
 
 class Qwen3Model:

@@ -302,6 +302,11 @@ __global__ __launch_bounds__(64 * NW) void proj_mfma_kernel(ProjArgs a) {
 // row got 64-byte pieces, which cost a third of the kernel's time.  Weight
 // loads are cached (non-temporal measured slower here).  in_dim a multiple
 // of 256.
+// TILED: W in the tiled layout of anelm_proj_tile_f16, where the 16 bytes
+// that lane l loads for a 16-row tile and a 32-input step lie at lane l's
+// place in one contiguous 1 KB block, so every weight load instruction reads
+// 1 KB in a row instead of 64 bytes from each of 16 rows.  The MFMA operands
+// are the same values either way, so are the outputs.
 constexpr int kLdsR = 8;                       // 32-input steps per load chunk
 constexpr int kLdsHalves = 64 * (1024 + 8);    // the LDS x area: 64 rows of 1024 inputs, or fewer longer rows
 constexpr int kYsLd = 128 + 8;                 // staging row stride (fp16), 128 outputs per batch row
@@ -310,7 +315,7 @@ __host__ __device__ constexpr int lds_rows(int in_dim) {   // batch rows staged 
     return 64 * (in_dim + 8) <= kLdsHalves ? 64 : (32 * (in_dim + 8) <= kLdsHalves ? 32 : 16);
 }
 
-template <int NB, int EPI>
+template <int NB, int EPI, bool TILED = false>
 __global__ __launch_bounds__(512) void proj_lds_kernel(ProjArgs a) {
     static_assert(EPI == kStore || EPI == kStore16, "store epilogues only");
     __shared__ __align__(16) uint16_t xs[kLdsHalves];
@@ -319,15 +324,47 @@ __global__ __launch_bounds__(512) void proj_lds_kernel(ProjArgs a) {
     const int K = a.in_dim, ldx = K + 8;
     const int b0 = blockIdx.y * 16 * NB;
     const uint16_t* xh = static_cast<const uint16_t*>(a.x);
+    const int ngroup = (a.out_dim + 127) / 128;   // 128-row groups (8 tiles)
+    const int rounds = (ngroup - 1 - (int)blockIdx.x) / (int)gridDim.x + 1;
+    const int cpt = K / (32 * kLdsR);             // load chunks per tile
+    const int nq = rounds * cpt;                  // every wave runs all of them (barriers)
+    const uint16_t* wbase = a.w + 8 * (lane >> 4);
+    // the R loads of chunk q (clamped rows: tiles past the end load a valid
+    // row, computed and never stored; a chunk past nq reloads the last one)
+    auto issue = [&](uint4* w, int q) {
+        q = q < nq ? q : nq - 1;
+        const int grp = (int)blockIdx.x + (q / cpt) * (int)gridDim.x;
+        if constexpr (TILED) {
+            // tile 8*grp + wv (clamped to the last; rows past out_dim are zeros)
+            const long ntile = (a.out_dim + 15) / 16;
+            long t = 8L * grp + wv;
+            t = t < ntile ? t : ntile - 1;
+            const uint16_t* p = a.w + ((t * (K / 32) + (q % cpt) * kLdsR) * 64 + lane) * 8;
+#pragma unroll
+            for (int j = 0; j < kLdsR; j++) w[j] = *reinterpret_cast<const uint4*>(p + 512 * j);
+        } else {
+            long r = 128L * grp + 16 * wv + (lane & 15);
+            r = r < a.out_dim ? r : a.out_dim - 1;
+            const uint16_t* p = wbase + r * K + (q % cpt) * (32 * kLdsR);
+#pragma unroll
+            for (int j = 0; j < kLdsR; j++) w[j] = *reinterpret_cast<const uint4*>(p + 32 * j);
+        }
+    };
+    if ((int)blockIdx.x >= ngroup) return;        // whole workgroup (before any barrier)
+    // the first weight chunk does not depend on x: its loads go out before
+    // the x staging, so the two latencies overlap
+    uint4 wa[kLdsR], wb[kLdsR];
+    issue(wa, 0);
+    __builtin_amdgcn_sched_barrier(0);
     {   // stage x rows b0 .. b0 + 16*NB - 1 (zeros past the batch): 8 loads per lane before their stores
-        const int qpr = K / 8, nq = 16 * NB * qpr;
-        for (int base = 0; base < nq; base += 8 * (int)blockDim.x) {
+        const int qpr = K / 8, nx = 16 * NB * qpr;
+        for (int base = 0; base < nx; base += 8 * (int)blockDim.x) {
             uint4 t[8];
             int dst[8];
 #pragma unroll
             for (int u = 0; u < 8; u++) {
                 const int idx = base + u * (int)blockDim.x + (int)threadIdx.x;
-                const int ic = idx < nq ? idx : nq - 1;   // past the end: the last quad again
+                const int ic = idx < nx ? idx : nx - 1;   // past the end: the last quad again
                 const int r = ic / qpr, c = ic - r * qpr;
                 const int b = b0 + r < a.batch ? b0 + r : a.batch - 1;
                 t[u] = *reinterpret_cast<const uint4*>(xh + (long)b * a.ld_x + 8 * c);
@@ -339,23 +376,6 @@ __global__ __launch_bounds__(512) void proj_lds_kernel(ProjArgs a) {
         }
     }
     __syncthreads();
-    const int ngroup = (a.out_dim + 127) / 128;   // 128-row groups (8 tiles)
-    if ((int)blockIdx.x >= ngroup) return;        // whole workgroup
-    const int rounds = (ngroup - 1 - (int)blockIdx.x) / (int)gridDim.x + 1;
-    const int cpt = K / (32 * kLdsR);             // load chunks per tile
-    const int nq = rounds * cpt;                  // every wave runs all of them (barriers)
-    const uint16_t* wbase = a.w + 8 * (lane >> 4);
-    // the R loads of chunk q (clamped rows: tiles past the end load a valid
-    // row, computed and never stored; a chunk past nq reloads the last one)
-    auto issue = [&](uint4* w, int q) {
-        q = q < nq ? q : nq - 1;
-        const int grp = (int)blockIdx.x + (q / cpt) * (int)gridDim.x;
-        long r = 128L * grp + 16 * wv + (lane & 15);
-        r = r < a.out_dim ? r : a.out_dim - 1;
-        const uint16_t* p = wbase + r * K + (q % cpt) * (32 * kLdsR);
-#pragma unroll
-        for (int j = 0; j < kLdsR; j++) w[j] = *reinterpret_cast<const uint4*>(p + 32 * j);
-    };
     const uint16_t* xrow = xs + (lane & 15) * ldx + 8 * (lane >> 4);
     float4v acc[NB];
 #pragma unroll
@@ -424,8 +444,6 @@ __global__ __launch_bounds__(512) void proj_lds_kernel(ProjArgs a) {
     // The scheduling barriers keep each chunk's loads ahead of the previous
     // chunk's MFMAs; without them the scheduler sank the loads below the
     // MFMAs, leaving one chunk in flight.
-    uint4 wa[kLdsR], wb[kLdsR];
-    issue(wa, 0);
     for (int q = 0; q < nq; q += 2) {
         issue(wb, q + 1);
         __builtin_amdgcn_sched_barrier(0);
@@ -693,16 +711,35 @@ bool lds_ok(const ProjArgs& a) {
            aligned16(a.x) && aligned16(a.w);
 }
 
-template <int EPI>
+template <int EPI, bool TILED = false>
 void launch_lds(ProjArgs a, hipStream_t st) {
     const int rows = lds_rows(a.in_dim);
     const int ngroup = (a.out_dim + 127) / 128;
     const int gx = std::min(cu_count(), ngroup);
     const dim3 grid((unsigned)gx, (unsigned)((a.batch + rows - 1) / rows));
     a.vec_y = EPI == kStore ? aligned16(a.y) && a.ld_y % 4 == 0 : aligned8(a.y16) && a.ld_y % 4 == 0;
-    if (rows == 64) proj_lds_kernel<4, EPI><<<grid, dim3(512), 0, st>>>(a);
-    else if (rows == 32) proj_lds_kernel<2, EPI><<<grid, dim3(512), 0, st>>>(a);
-    else proj_lds_kernel<1, EPI><<<grid, dim3(512), 0, st>>>(a);
+    if (rows == 64) proj_lds_kernel<4, EPI, TILED><<<grid, dim3(512), 0, st>>>(a);
+    else if (rows == 32) proj_lds_kernel<2, EPI, TILED><<<grid, dim3(512), 0, st>>>(a);
+    else proj_lds_kernel<1, EPI, TILED><<<grid, dim3(512), 0, st>>>(a);
+}
+
+// The tiled layout: for 16-row tile t and 32-input step s, 64 pieces of 16
+// bytes (8 fp16), piece l = W[16t + l%16][32s + 8(l/16) .. +7], the block at
+// ((t * in_dim/32 + s) * 64) pieces; rows past out_dim are zeros.  One
+// thread per piece.
+__global__ __launch_bounds__(256) void tile_w16_kernel(uint16_t* dst, const uint16_t* src, int out_dim, int in_dim,
+                                                       long npieces) {
+    const long i = (long)blockIdx.x * 256 + threadIdx.x;
+    if (i >= npieces) return;
+    const int steps = in_dim / 32;
+    const int l = (int)(i & 63);
+    const long ts = i >> 6;
+    const int st = (int)(ts % steps);
+    const long t = ts / steps;
+    const long r = 16 * t + (l & 15);
+    uint4 v = make_uint4(0u, 0u, 0u, 0u);
+    if (r < out_dim) v = *reinterpret_cast<const uint4*>(src + r * in_dim + 32 * st + 8 * (l >> 4));
+    *reinterpret_cast<uint4*>(dst + 8 * i) = v;
 }
 
 // ---- MFMA launch shapes -----------------------------------------------------
@@ -849,6 +886,50 @@ extern "C" int anelm_proj_f16_x16_fused(void* y, const uint16_t* x16, const uint
         default: x16_fused<kSwiGLU16>(a, st); break;
     }
     return launch_status("proj_f16_x16_fused");
+}
+
+extern "C" size_t anelm_proj_tiled_size(int out_dim, int in_dim) {
+    if (out_dim <= 0 || in_dim <= 0 || in_dim % 32 != 0) return 0;
+    return (size_t)((out_dim + 15) / 16) * 16 * (size_t)in_dim * sizeof(uint16_t);
+}
+
+extern "C" int anelm_proj_tile_f16(uint16_t* w_tiled, const uint16_t* w16, int out_dim, int in_dim, void* stream) {
+    clear_error();
+    if (!w_tiled || !w16) return fail(ANELM_ERR_INVALID, "proj_tile_f16: null pointer");
+    if (out_dim <= 0 || in_dim <= 0 || in_dim % 32 != 0 || (long)out_dim * in_dim > (1L << 40))
+        return fail(ANELM_ERR_INVALID, "proj_tile_f16: out_dim %d, in_dim %d (a multiple of 32)", out_dim, in_dim);
+    if (!aligned16(w_tiled) || !aligned16(w16)) return fail(ANELM_ERR_INVALID, "proj_tile_f16: needs 16-byte alignment");
+    const size_t bytes = anelm_proj_tiled_size(out_dim, in_dim);
+    const uintptr_t d0 = reinterpret_cast<uintptr_t>(w_tiled), s0 = reinterpret_cast<uintptr_t>(w16);
+    if (d0 < s0 + (uintptr_t)out_dim * in_dim * 2 && s0 < d0 + bytes)
+        return fail(ANELM_ERR_INVALID, "proj_tile_f16: the tiled copy overlaps W");
+    const long npieces = (long)(bytes / 16);
+    tile_w16_kernel<<<dim3((unsigned)((npieces + 255) / 256)), dim3(256), 0, as_stream(stream)>>>(w_tiled, w16, out_dim,
+                                                                                                 in_dim, npieces);
+    return launch_status("proj_tile_f16");
+}
+
+extern "C" int anelm_proj_f16_x16_tiled(void* y, const uint16_t* x16, const uint16_t* w_tiled, long batch, int out_dim,
+                                        int in_dim, long ld_x, long ld_y, int epilogue, void* stream) {
+    clear_error();
+    if (!y || !x16 || !w_tiled) return fail(ANELM_ERR_INVALID, "proj_f16_x16_tiled: null pointer");
+    if (!sizes_ok(batch, out_dim, in_dim, ld_x, ld_y))
+        return fail(ANELM_ERR_INVALID, "proj_f16_x16_tiled: bad sizes or strides");
+    if (in_dim % 256 != 0 || in_dim > 4096 || ld_x % 8 != 0 || !aligned16(x16) || !aligned16(w_tiled))
+        return fail(ANELM_ERR_INVALID,
+                    "proj_f16_x16_tiled: needs in_dim a multiple of 256 up to 4096, ld_x a multiple of 8, 16-byte "
+                    "aligned x and W");
+    if (epilogue != ANELM_PROJ_STORE && epilogue != ANELM_PROJ_STORE_F16)
+        return fail(ANELM_ERR_INVALID, "proj_f16_x16_tiled: epilogue %d (ANELM_PROJ_STORE or ANELM_PROJ_STORE_F16)",
+                    epilogue);
+    const bool f16 = epilogue == ANELM_PROJ_STORE_F16;
+    if (overlaps(y, ld_y, out_dim, f16 ? 2 : 4, x16, ld_x, in_dim, 2, batch))
+        return fail(ANELM_ERR_INVALID, "proj_f16_x16_tiled: y overlaps x (y is written while x is still read)");
+    ProjArgs a = args(static_cast<float*>(y), x16, w_tiled, batch, out_dim, in_dim, ld_x, ld_y);
+    a.y16 = static_cast<uint16_t*>(y);
+    if (f16) launch_lds<kStore16, true>(a, as_stream(stream));
+    else launch_lds<kStore, true>(a, as_stream(stream));
+    return launch_status("proj_f16_x16_tiled");
 }
 
 // Decode-step projections with the neighbouring layer ops fused in, for up

@@ -52,6 +52,7 @@ struct anelm_qwen3 {
     uint16_t* embed = nullptr;       // bf16 [V, H] (widened exactly by the gather)
     uint16_t* final_norm = nullptr;  // bf16 [H]
     uint16_t* lm16 = nullptr;        // fp16 [V, H]
+    uint16_t* lm_tiled = nullptr;    // the same in anelm_proj_tile_f16's layout, past 16 sequences (or null)
     struct Layer {
         uint16_t *qkv16, *o16, *gu16, *down16;   // fp16 projections
         uint16_t *qn, *kn, *w_in, *w_post;       // bf16 gammas
@@ -203,6 +204,20 @@ extern "C" anelm_qwen3* anelm_qwen3_load(const char* path, const anelm_qwen3_con
     ALLOC(m->a16, uint16_t, B * amax);
     ALLOC(m->y16, uint16_t, B * std::max({(long)m->qkvdim, 2 * I, H}));
 #undef ALLOC
+    // Past 16 sequences the LM head streams a tiled copy of its W (1 KB per
+    // load instruction) through the LDS kernel; made once here.
+    if (B > 16 && c.hidden % 256 == 0 && c.hidden <= 4096 && c.vocab >= 8192) {
+        const size_t tb = anelm_proj_tiled_size(c.vocab, c.hidden);
+        if (!(m->lm_tiled = static_cast<uint16_t*>(m->alloc(tb)))) {
+            rc = fail(ANELM_ERR_HIP, "qwen3_load: out of device memory");
+            delete m;
+            return nullptr;
+        }
+        if ((rc = anelm_proj_tile_f16(m->lm_tiled, m->lm16, c.vocab, c.hidden, stream))) {
+            delete m;
+            return nullptr;
+        }
+    }
     m->attn_ws_bytes = anelm_gqa_workspace_size(B, c.n_q_heads, c.n_kv_heads, c.head_dim, m->cap);
     if (m->attn_ws_bytes && !(m->attn_ws = m->alloc(m->attn_ws_bytes))) {
         rc = fail(ANELM_ERR_HIP, "qwen3_load: out of device memory");
@@ -295,7 +310,10 @@ extern "C" int anelm_qwen3_forward(anelm_qwen3* m, const int32_t* ids, const int
         }
         CK(anelm_rmsnorm_f16(m->a16, m->x, m->final_norm, ANELM_BF16, B, (int)H, H, H, c.rms_eps, stream));  // :530
         // the LM head (a 151936-row W streams once through the LDS-staged
-        // kernel) writes the widened logits itself
+        // kernel, from its tiled copy) writes the widened logits itself
+        if (m->lm_tiled)
+            return anelm_proj_f16_x16_tiled(logits, m->a16, m->lm_tiled, B, (int)V, (int)H, H, ld_logits,
+                                            ANELM_PROJ_STORE, stream);
         return anelm_proj_f16_x16_fused(logits, m->a16, m->lm16, B, (int)V, (int)H, H, ld_logits, ANELM_PROJ_STORE,
                                         stream);
     }

@@ -177,6 +177,44 @@ def _ulp16(v):
     return np.spacing(np.abs(v).astype(np.float16)).astype(np.float64)
 
 
+@pytest.mark.parametrize("B,out_dim,in_dim,same_kernel", [(64, 151936, 1024, True), (20, 70001, 256, True),
+                                                           (17, 8192, 4096, True), (1, 8200, 512, False),
+                                                           (33, 16, 4096, False), (5, 1000, 256, False)])
+def test_proj_tiled(hip, orc, rng, B, out_dim, in_dim, same_kernel):
+    """W in the tiled layout (rows past out_dim zero): fp32 and fp16 outputs
+    bit-identical to the row-major LDS kernel where anelm_proj_f16_x16_fused
+    and anelm_linear_f16 take it (more than 16 rows, at least 8192 output
+    rows), and against the oracle everywhere, including a ragged last tile."""
+    import torch
+
+    w = (0.03 * rng.standard_normal((out_dim, in_dim))).astype(np.float16).view(np.uint16)
+    x = rng.standard_normal((B, in_dim)).astype(np.float32)
+    x16 = dev(orc.f32_to_f16_rne(x).reshape(B, in_dim).view(np.int16))
+    dw = dev(w)
+    wt = torch.full((hip.proj_tiled_size(out_dim, in_dim) // 2,), -1, dtype=torch.int16, device="cuda")
+    hip.proj_tile_f16(wt, dw)
+    padded = host(wt).reshape(-1)
+    tiles = (out_dim + 15) // 16
+    # piece l of (tile t, step s) = W[16t + l % 16][32s + 8(l // 16) .. +7]
+    want_layout = np.zeros((tiles * 16, in_dim), np.uint16)
+    want_layout[:out_dim] = w
+    want_layout = want_layout.reshape(tiles, 16, in_dim // 32, 4, 8).transpose(0, 2, 3, 1, 4).reshape(-1)
+    assert np.array_equal(padded.view(np.uint16), want_layout)
+    y = torch.full((B, out_dim), float("nan"), device="cuda")
+    hip.proj_f16_x16_tiled(y, x16, wt, out_dim)
+    y16 = torch.empty(B, out_dim, dtype=torch.int16, device="cuda")
+    hip.proj_f16_x16_tiled(y16, x16, wt, out_dim, epilogue=hip.PROJ_STORE_F16)
+    assert_bitexact(host(y16).view(np.float16).astype(np.float32), host(y), "fp16 output = fp32 output narrowed")
+    if same_kernel:
+        yr = torch.empty(B, out_dim, device="cuda")
+        hip.proj_f16_x16_fused(yr, x16, dw)
+        assert_bitexact(host(y), host(yr), "tiled vs row-major")
+        yr16 = torch.empty(B, out_dim, dtype=torch.int16, device="cuda")
+        hip.linear_f16(yr16, x16, dw)
+        assert_bitexact(host(y16), host(yr16), "tiled vs row-major, fp16 out")
+    check_projection(orc, x, w, host(y).astype(np.float64))
+
+
 @pytest.mark.parametrize("B,out_dim,in_dim", [(1, 1024, 1024), (11, 4096, 1024), (16, 300, 256), (3, 151936, 1024),
                                                (1, 4097, 1024), (2, 4101, 992), (1, 32771, 512), (1, 151936, 1024),
                                                (4, 777, 3072)])
