@@ -45,8 +45,8 @@ WORKLOADS = {
 HEADLINE = "qwen3-8b-prefill"
 OPS = ["rmsnorm", "qknorm_rope", "add_rmsnorm", "silu_mul", "residual_add"]
 # the kernel each op launches at the workload shapes: (name fragment, template fragment)
-OP_KERNELS = {"rmsnorm": ("rmsnorm_row_kernel", "false, false>"), "qknorm_rope": ("qknorm_rope128_w8_kernel", ""),
-              "add_rmsnorm": ("rmsnorm_row_kernel", "true, false>"), "silu_mul": ("silu_mul_vec_kernel", ""),
+OP_KERNELS = {"rmsnorm": ("rmsnorm_row_kernel", "false, false, "), "qknorm_rope": ("qknorm_rope128_w8_kernel", ""),
+              "add_rmsnorm": ("rmsnorm_row_kernel", "true, false, "), "silu_mul": ("silu_mul_vec_kernel", ""),
               "residual_add": ("residual_add_vec_kernel", ""), "layer_ops": ("layer_ops_kernel", "")}
 PROFILES = os.path.join(ROOT, "profiles")
 # The counter runs behind profiles/pmc_traffic_<workload>.txt (run from the repo root):
@@ -767,7 +767,7 @@ SAMPLER = "sampling-64x151936"
 # The 64-sequence decode step's LM head (x staged in LDS) and layer kernels
 Q3_B64 = "qwen3-0.6b-decode-step-b64"
 Q3_B64_KERNELS = {"lm_head": ("proj_lds_kernel", ""), "attention": ("gqa_decode_kernel", ""),
-                  "merge": ("gqa_combine_kernel", ""), "norm_f16": ("rmsnorm_row_kernel", "true>"),
+                  "merge": ("gqa_combine_kernel", ""), "norm_f16": ("rmsnorm_row_kernel", "false, true, "),
                   "proj_add": ("proj_mfma_kernel", "false, 1, 4>"), "gate_up_swiglu": ("proj_mfma_kernel", "false, 3, 4>"),
                   "qkv": ("proj_mfma_kernel", "false, 0, 4>")}
 

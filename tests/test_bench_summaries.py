@@ -11,7 +11,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 sys.path.insert(0, ROOT)
 import bench  # noqa: E402
 
-K = "void anelm::rmsnorm_row_kernel<2, 1, false, false>(anelm::RmsArgs)"
+K = "void anelm::rmsnorm_row_kernel<2, 1, false, false, true>(void*, float*, float const*, void const*, long, int, long, long, long, float)"
 OTHER = "void at::native::vectorized_elementwise_kernel<4, at::native::FillFunctor<float> >(int, at::native::FillFunctor<float>)"
 FIELDS = ["Dispatch_Id", "Kernel_Name", "Counter_Name", "Counter_Value"]
 
