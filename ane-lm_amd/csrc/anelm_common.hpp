@@ -86,6 +86,19 @@ __device__ __forceinline__ float wave_sum_rows(float v) {
     return (r0 + r1) + (r2 + r3);
 }
 
+// Maximum over the wave, every lane receiving it, the same way (fmaxf).
+__device__ __forceinline__ float wave_max_rows(float v) {
+    v = fmaxf(v, dpp_f32<0xB1>(v));    // quad_perm [1,0,3,2]
+    v = fmaxf(v, dpp_f32<0x4E>(v));    // quad_perm [2,3,0,1]
+    v = fmaxf(v, dpp_f32<0x141>(v));   // row_half_mirror
+    v = fmaxf(v, dpp_f32<0x140>(v));   // row_mirror
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
 __device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
 #pragma unroll
     for (int d = 32; d >= 1; d >>= 1) {

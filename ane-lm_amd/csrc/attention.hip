@@ -290,14 +290,14 @@ __global__ __launch_bounds__(kAttnThreads) void gqa_decode_kernel(AttnArgs a) {
     for (int g = wid; g < gc; g += kAttnWaves) {
         float m = -INFINITY;
         for (int i = lane; i < n; i += kWave) m = fmaxf(m, sc[g][i]);
-        m = wave_max(m);
+        m = wave_max_rows(m);
         float l = 0.0f;
         for (int i = lane; i < n; i += kWave) {
             const float e = expf(sc[g][i] - m);
             sc[g][i] = e;
             l += e;
         }
-        l = wave_sum(l);
+        l = wave_sum_rows(l);
         if (fin) {  // the reference's p = e * (1/sum) (core/cpu_ops.cpp:97-98)
             const float inv = 1.0f / l;
             for (int i = lane; i < n; i += kWave) sc[g][i] = sc[g][i] * inv;
@@ -421,7 +421,7 @@ __global__ __launch_bounds__(kWave) void gqa_combine_kernel(AttnArgs a) {
     for (int s = lane + kWave; s < ns; s += kWave) {
         if (p[s * (D + 2) + D + 1] > 0.0f) M = fmaxf(M, p[s * (D + 2) + D]);
     }
-    M = wave_max(M);
+    M = wave_max_rows(M);
     float L = 0.0f;
     float o[D / kWave];
 #pragma unroll
@@ -456,7 +456,7 @@ __global__ __launch_bounds__(kWave) void gqa_combine_kernel(AttnArgs a) {
             }
         }
     }
-    L = wave_sum(L);
+    L = wave_sum_rows(L);
     const float inv = L == 0.0f ? 0.0f : 1.0f / L;   // no live position: zeros (cpu_ops.cpp:177-180)
 #pragma unroll
     for (int i = 0; i < D / kWave; i++) put_out(a, b * a.out_ld + (long)h * D + lane + i * kWave, o[i] * inv);

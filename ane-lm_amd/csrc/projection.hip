@@ -528,7 +528,7 @@ __global__ __launch_bounds__(256) void proj_dot_kernel(ProjArgs a) {
                     sp = fmaf(v.z, v.z, sp);
                     sp = fmaf(v.w, v.w, sp);
                 }
-            sp = wave_sum(sp);
+            sp = wave_sum_rows(sp);
             if (lane == 0) s_part[wv][b] = sp;
         }
         __syncthreads();
@@ -584,7 +584,7 @@ __global__ __launch_bounds__(256) void proj_dot_kernel(ProjArgs a) {
 #pragma unroll
     for (int t = 0; t < NR; t++)
 #pragma unroll
-        for (int b = 0; b < BT; b++) acc[t][b] = wave_sum(acc[t][b]);
+        for (int b = 0; b < BT; b++) acc[t][b] = wave_sum_rows(acc[t][b]);
     // lane b*RPW + t stores row r0 + t of x row b
     float s = 0.f, u = 0.f;
 #pragma unroll
