@@ -611,9 +611,10 @@ PROJ_STORE, PROJ_ADD, PROJ_SWIGLU, PROJ_SWIGLU_F16, PROJ_STORE_F16 = 0, 1, 2, 3,
 def proj_f16_fused(y, x, w16, norm=None, eps=1e-6, epilogue=PROJ_STORE, stream=None):
     """Decode projection with an optional RMSNorm prologue (norm:
     bf16 gamma as int16/bfloat16 tensor) and a store / residual-add / SwiGLU
-    epilogue; for SwiGLU w16 holds the gate rows then the up rows."""
+    epilogue; for SwiGLU w16 holds the gate rows then the up rows; y fp32, or
+    fp16 bits (int16/float16 tensor) with PROJ_SWIGLU_F16."""
     batch, in_dim = x.shape
-    out_dim = w16.shape[0] // 2 if epilogue == PROJ_SWIGLU else w16.shape[0]
+    out_dim = w16.shape[0] // 2 if epilogue in (PROJ_SWIGLU, PROJ_SWIGLU_F16) else w16.shape[0]
     _check(lib().anelm_proj_f16_fused(_ptr(y), _ptr(x), _ptr(w16), batch, out_dim, in_dim, _ld(x), _ld(y),
                                       _ptr(norm), eps, epilogue, _stream(stream)))
 

@@ -464,10 +464,22 @@ __global__ __launch_bounds__(512) void proj_lds_kernel(ProjArgs a) {
 // of each weight row, and the loads of NCH chunks are in flight together.
 // Products are v_dot2_f32_f16 of fp16 pairs into fp32 (a fp16 x fp16
 // product is exact in fp32), a wave sum closes each row, and lane t of the
-// wave writes row t's result.  x comes from cache and is rounded to fp16 (after
-// the fused RMSNorm, if any) on the way in, the same x16 the MFMA path uses.
-// Small out_dim gets the most from it: 1024 output rows are 64 MFMA
-// workgroups but 1024 waves here.
+// wave writes row t's result.  Small out_dim gets the most from it: 1024
+// output rows are 64 MFMA workgroups but 1024 waves here.
+//
+// x comes in one of three forms (XM), each giving the same fp16 operand the
+// MFMA path uses:
+//   kXF32   fp32 rows, rounded to fp16 per element on the way in;
+//   kXNorm  fp32 rows through the fused RMSNorm: the workgroup loads each row
+//           once, reduces its sum of squares and writes the normalised row,
+//           rounded to fp16, to LDS, where the waves read it (one 16-byte
+//           read per chunk instead of two 16-byte global loads and a gamma
+//           load);
+//   kXF16   fp16 rows already rounded by their producer (the attention's
+//           fp16 output, the SwiGLU's fp16 store): half the bytes of fp32.
+// At the one-sequence decode shapes the activation loads were as many
+// instructions as the weight loads or more (fp32 x: two 16-byte loads per
+// one of W), and taking them out of the loop saved 0.5-1.1 us of 3.7-5.2 us.
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ half2v as_half2(uint32_t u) {
@@ -476,10 +488,27 @@ __device__ __forceinline__ half2v as_half2(uint32_t u) {
     return r;
 }
 
-template <int BT, int RPW, int NCH, bool NORM, int EPI>
+__device__ __forceinline__ uint32_t pack_f16(float lo, float hi) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, to_f16(lo)) | ((uint32_t)__builtin_bit_cast(uint16_t, to_f16(hi)) << 16);
+}
+
+enum : int {
+    kXF32 = 0,
+    kXNorm = 1,
+    kXF16 = 2,
+};
+constexpr int kDotNormMaxIn = 4096;   // kXNorm: LDS for the staged rows (8 KB per row of x)
+
+// kXNorm: 4-input slices per thread that cover in_dim for a chunk count
+constexpr int dot_norm_slices(int nch) { return nch <= 2 ? 1 : (nch <= 4 ? 2 : 4); }
+
+template <int BT, int RPW, int NCH, int XM, int EPI>
 __global__ __launch_bounds__(256) void proj_dot_kernel(ProjArgs a) {
-    constexpr int NR = EPI == kSwiGLU ? 2 * RPW : RPW;  // weight rows per wave
+    constexpr int NR = is_swiglu(EPI) ? 2 * RPW : RPW;  // weight rows per wave
+    constexpr bool NORM = XM == kXNorm;
+    constexpr int NS = dot_norm_slices(NCH);
     __shared__ float s_part[4][BT];
+    __shared__ uint4 s_x16[NORM ? BT : 1][NORM ? kDotNormMaxIn / 8 : 1];   // 8 fp16 inputs per entry
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const long r0 = ((long)blockIdx.x * 4 + wv) * RPW;
     // operand rows, clamped: rows past the end compute values that are never stored
@@ -490,6 +519,7 @@ __global__ __launch_bounds__(256) void proj_dot_kernel(ProjArgs a) {
         wp[t] = a.w + ((r < a.out_dim ? r : a.out_dim - 1) + (t >= RPW ? a.pair_rows : 0)) * a.in_dim;
     }
     const float* xf = static_cast<const float*>(a.x);
+    const uint16_t* xh = static_cast<const uint16_t*>(a.x);
     uint4 wr[NCH][NR];
     int idx[NCH];  // this lane's first input in each chunk, clamped into the row
     auto issue = [&](int c0) {
@@ -501,9 +531,29 @@ __global__ __launch_bounds__(256) void proj_dot_kernel(ProjArgs a) {
             for (int t = 0; t < NR; t++) wr[k][t] = ld_nt(reinterpret_cast<const uint4*>(wp[t] + idx[k]));
         }
     };
-    // the first chunks' weight loads go out before the RMSNorm prologue, and
-    // the residual add's y value with them (lane b*RPW + t: row r0 + t of x
-    // row b; clamped, unused where the lane stores nothing)
+    // kXNorm: thread j's slices of x, inputs 4j + 1024s .. +3 (in_dim <=
+    // 1024*NS, a multiple of 8), and their gammas.  They are loaded before the
+    // first weight chunks: loads retire in issue order, so the prologue
+    // below waits only for these while the weights are still in flight.
+    // Rows past the batch and inputs past in_dim are zeros, which leave the
+    // sums unchanged and stage as zeros.
+    float4 xs[NORM ? BT : 1][NORM ? NS : 1];
+    uint2 gs[NORM ? NS : 1];
+    if constexpr (NORM) {
+#pragma unroll
+        for (int sl = 0; sl < NS; sl++) {
+            const int k = 4 * (int)threadIdx.x + 1024 * sl;
+            gs[sl] = k < a.in_dim ? *reinterpret_cast<const uint2*>(a.gamma + k) : make_uint2(0u, 0u);
+#pragma unroll
+            for (int b = 0; b < BT; b++)
+                xs[b][sl] = k < a.in_dim && b < a.batch ? *reinterpret_cast<const float4*>(xf + (long)b * a.ld_x + k)
+                                                        : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    // the first chunks' weight loads, and the residual add's y value with
+    // them (lane b*RPW + t: row r0 + t of x row b; clamped, unused where the
+    // lane stores nothing)
     issue(0);
     float yprev = 0.f;
     if constexpr (EPI == kAdd) {
@@ -512,22 +562,18 @@ __global__ __launch_bounds__(256) void proj_dot_kernel(ProjArgs a) {
         yprev = a.y[(long)b * a.ld_y + r];
     }
 
-    float scale[BT];
-#pragma unroll
-    for (int b = 0; b < BT; b++) scale[b] = 1.0f;
     if constexpr (NORM) {
         // the workgroup's 256 lanes share each row's sum of squares
 #pragma unroll
         for (int b = 0; b < BT; b++) {
             float sp = 0.f;
-            if (b < a.batch)
-                for (int k = 4 * (int)threadIdx.x; k < a.in_dim; k += 1024) {
-                    const float4 v = *reinterpret_cast<const float4*>(xf + (long)b * a.ld_x + k);
-                    sp = fmaf(v.x, v.x, sp);
-                    sp = fmaf(v.y, v.y, sp);
-                    sp = fmaf(v.z, v.z, sp);
-                    sp = fmaf(v.w, v.w, sp);
-                }
+#pragma unroll
+            for (int sl = 0; sl < NS; sl++) {
+                sp = fmaf(xs[b][sl].x, xs[b][sl].x, sp);
+                sp = fmaf(xs[b][sl].y, xs[b][sl].y, sp);
+                sp = fmaf(xs[b][sl].z, xs[b][sl].z, sp);
+                sp = fmaf(xs[b][sl].w, xs[b][sl].w, sp);
+            }
             sp = wave_sum_rows(sp);
             if (lane == 0) s_part[wv][b] = sp;
         }
@@ -535,10 +581,20 @@ __global__ __launch_bounds__(256) void proj_dot_kernel(ProjArgs a) {
 #pragma unroll
         for (int b = 0; b < BT; b++) {
             const float ss = (s_part[0][b] + s_part[1][b]) + (s_part[2][b] + s_part[3][b]);
-            scale[b] = 1.0f / sqrtf(ss / (float)a.in_dim + a.eps);
+            const float scale = 1.0f / sqrtf(ss / (float)a.in_dim + a.eps);
+            uint16_t* row = reinterpret_cast<uint16_t*>(&s_x16[b][0]);
+#pragma unroll
+            for (int sl = 0; sl < NS; sl++) {
+                const int k = 4 * (int)threadIdx.x + 1024 * sl;
+                if (k < a.in_dim) {
+                    const float4 v = norm_scale(xs[b][sl], scale, gs[sl].x, gs[sl].y);
+                    *reinterpret_cast<uint2*>(row + k) = make_uint2(pack_f16(v.x, v.y), pack_f16(v.z, v.w));
+                }
+            }
         }
+        __syncthreads();
     }
-    if (r0 >= a.out_dim) return;  // whole wave, after the workgroup's barrier
+    if (r0 >= a.out_dim) return;  // whole wave, after the workgroup's barriers
 
     float acc[NR][BT];
 #pragma unroll
@@ -547,28 +603,32 @@ __global__ __launch_bounds__(256) void proj_dot_kernel(ProjArgs a) {
         for (int b = 0; b < BT; b++) acc[t][b] = 0.f;
     for (int c0 = 0; c0 < a.in_dim; c0 += 512 * NCH) {
         if (c0) issue(c0);
-        uint4 gq[NORM ? NCH : 1];
-        if constexpr (NORM) {
-#pragma unroll
-            for (int k = 0; k < NCH; k++) gq[k] = *reinterpret_cast<const uint4*>(a.gamma + idx[k]);
-        }
 #pragma unroll
         for (int k = 0; k < NCH; k++) {
             const bool live = c0 + 512 * k + 8 * lane < a.in_dim;
 #pragma unroll
             for (int b = 0; b < BT; b++) {
-                const float* xp = xf + (long)(b < a.batch ? b : a.batch - 1) * a.ld_x + idx[k];
-                float4 p = reinterpret_cast<const float4*>(xp)[0];
-                float4 q = reinterpret_cast<const float4*>(xp)[1];
-                if constexpr (NORM) {
-                    p = norm_scale(p, scale[b], gq[k].x, gq[k].y);
-                    q = norm_scale(q, scale[b], gq[k].z, gq[k].w);
+                const int bb = b < a.batch ? b : a.batch - 1;
+                half2v x0, x1, x2, x3;
+                if constexpr (XM == kXF32) {
+                    const float* xp = xf + (long)bb * a.ld_x + idx[k];
+                    const float4 p = reinterpret_cast<const float4*>(xp)[0];
+                    const float4 q = reinterpret_cast<const float4*>(xp)[1];
+                    const _Float16 z = (_Float16)0.0f;
+                    x0 = live ? half2v{to_f16(p.x), to_f16(p.y)} : half2v{z, z};
+                    x1 = live ? half2v{to_f16(p.z), to_f16(p.w)} : half2v{z, z};
+                    x2 = live ? half2v{to_f16(q.x), to_f16(q.y)} : half2v{z, z};
+                    x3 = live ? half2v{to_f16(q.z), to_f16(q.w)} : half2v{z, z};
+                } else {
+                    uint4 xv;
+                    if constexpr (NORM) xv = s_x16[b][idx[k] >> 3];
+                    else xv = *reinterpret_cast<const uint4*>(xh + (long)bb * a.ld_x + idx[k]);
+                    if (!live) xv = make_uint4(0u, 0u, 0u, 0u);
+                    x0 = as_half2(xv.x);
+                    x1 = as_half2(xv.y);
+                    x2 = as_half2(xv.z);
+                    x3 = as_half2(xv.w);
                 }
-                const _Float16 z = (_Float16)0.0f;
-                const half2v x0 = live ? half2v{to_f16(p.x), to_f16(p.y)} : half2v{z, z};
-                const half2v x1 = live ? half2v{to_f16(p.z), to_f16(p.w)} : half2v{z, z};
-                const half2v x2 = live ? half2v{to_f16(q.x), to_f16(q.y)} : half2v{z, z};
-                const half2v x3 = live ? half2v{to_f16(q.z), to_f16(q.w)} : half2v{z, z};
 #pragma unroll
                 for (int t = 0; t < NR; t++) {
                     float s = acc[t][b];
@@ -593,21 +653,23 @@ __global__ __launch_bounds__(256) void proj_dot_kernel(ProjArgs a) {
         for (int b = 0; b < BT; b++)
             if (lane == b * RPW + t) {
                 s = acc[t][b];
-                if constexpr (EPI == kSwiGLU) u = acc[RPW + t][b];
+                if constexpr (is_swiglu(EPI)) u = acc[RPW + t][b];
             }
     const int t = lane % RPW, b = lane / RPW;
     if (lane < RPW * BT && b < a.batch && r0 + t < a.out_dim) {
-        float* yp = a.y + (long)b * a.ld_y + r0 + t;
-        if constexpr (EPI == kAdd) *yp = yprev + r16(s);
-        else if constexpr (EPI == kSwiGLU) *yp = silu_ref(r16(s)) * r16(u);
-        else *yp = r16(s);
+        const long o = (long)b * a.ld_y + r0 + t;
+        if constexpr (EPI == kAdd) a.y[o] = yprev + r16(s);
+        else if constexpr (EPI == kSwiGLU) a.y[o] = silu_ref(r16(s)) * r16(u);
+        else if constexpr (EPI == kSwiGLU16) a.y16[o] = __builtin_bit_cast(uint16_t, to_f16(silu_ref(r16(s)) * r16(u)));
+        else if constexpr (EPI == kStore16) a.y16[o] = __builtin_bit_cast(uint16_t, to_f16(s));
+        else a.y[o] = r16(s);
     }
 }
 
-template <int BT, int RPW, int NCH, bool NORM, int EPI>
+template <int BT, int RPW, int NCH, int XM, int EPI>
 void launch_dot(const ProjArgs& a, hipStream_t st) {
     const long waves = (a.out_dim + RPW - 1) / RPW;
-    proj_dot_kernel<BT, RPW, NCH, NORM, EPI><<<dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, st>>>(a);
+    proj_dot_kernel<BT, RPW, NCH, XM, EPI><<<dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, st>>>(a);
 }
 
 // Launch shape: all of a 1024-input row in one round of loads (NCH = 2),
@@ -615,27 +677,29 @@ void launch_dot(const ProjArgs& a, hipStream_t st) {
 // wave from 4096 rows up and four from 32768 (the LM head), so that each
 // wave has several loads in flight, one row per wave for the SwiGLU's row
 // pairs and for narrow out_dim, so that there are enough waves.
-template <int BT, bool NORM, int EPI>
+template <int BT, int XM, int EPI>
 void dot_shape(const ProjArgs& a, hipStream_t st) {
     const int chunks = (a.in_dim + 511) / 512;
     if (chunks > 2) {
-        if (chunks <= 4) launch_dot<BT, 1, 4, NORM, EPI>(a, st);
-        else launch_dot<BT, 1, 6, NORM, EPI>(a, st);
-    } else if (BT == 1 && EPI != kSwiGLU && a.out_dim >= 32768) {
-        launch_dot<1, 4, 2, NORM, EPI>(a, st);
-    } else if (EPI != kSwiGLU && a.out_dim >= 4096) {
-        launch_dot<BT, 2, 2, NORM, EPI>(a, st);
-    } else {
-        launch_dot<BT, 1, 2, NORM, EPI>(a, st);
+        if (chunks <= 4) launch_dot<BT, 1, 4, XM, EPI>(a, st);
+        else launch_dot<BT, 1, 6, XM, EPI>(a, st);
+        return;
     }
+    if constexpr (!is_swiglu(EPI)) {
+        if constexpr (BT == 1) {
+            if (a.out_dim >= 32768) return launch_dot<1, 4, 2, XM, EPI>(a, st);
+        }
+        if (a.out_dim >= 4096) return launch_dot<BT, 2, 2, XM, EPI>(a, st);
+    }
+    launch_dot<BT, 1, 2, XM, EPI>(a, st);
 }
 
-template <bool NORM, int EPI>
+template <int XM, int EPI>
 void proj_dot(const ProjArgs& a, hipStream_t st) {
-    if (a.batch == 1) dot_shape<1, NORM, EPI>(a, st);
-    else if (a.batch == 2) dot_shape<2, NORM, EPI>(a, st);
-    else if (a.batch <= 4) dot_shape<4, NORM, EPI>(a, st);
-    else dot_shape<8, NORM, EPI>(a, st);
+    if (a.batch == 1) dot_shape<1, XM, EPI>(a, st);
+    else if (a.batch == 2) dot_shape<2, XM, EPI>(a, st);
+    else if (a.batch <= 4) dot_shape<4, XM, EPI>(a, st);
+    else dot_shape<8, XM, EPI>(a, st);
 }
 
 // Where the dot kernel beats the MFMA kernel (measured at the Qwen3-0.6B
@@ -654,6 +718,10 @@ bool overlaps(const void* y, long ld_y, int out_dim, int y_bytes, const void* x,
 
 bool dot_ok(const float* x, const uint16_t* w16, long batch, int in_dim, long ld_x) {
     return batch <= 8 && in_dim % 8 == 0 && ld_x % 4 == 0 && aligned16(x) && aligned16(w16);
+}
+// fp16 rows: one 16-byte load per 8 inputs
+bool dot16_ok(const uint16_t* x16, const uint16_t* w16, long batch, int in_dim, long ld_x) {
+    return batch <= 8 && in_dim % 8 == 0 && ld_x % 8 == 0 && aligned16(x16) && aligned16(w16);
 }
 
 // ---- any shape (the fallback) ------------------------------------------------
@@ -810,7 +878,7 @@ extern "C" int anelm_proj_f16(float* y, const float* x, const uint16_t* w16, lon
     const bool dot = dot_ok(x, w16, batch, in_dim, ld_x);
     if (mfma_ok(x, false, w16, in_dim, ld_x) && !(dot && dot_wins(batch, out_dim))) return proj_mfma<false>(a, st);
     if (dot) {
-        proj_dot<false, kStore>(a, st);
+        proj_dot<kXF32, kStore>(a, st);
     } else {
         if ((long)out_dim * batch > (1L << 33)) return fail(ANELM_ERR_INVALID, "proj_f16: too large for its shape");
         launch_generic<false, kStore>(a, st);
@@ -856,7 +924,9 @@ template <int EPI>
 void x16_fused(const ProjArgs& a, hipStream_t st) {
     const long tiles16 = (long)((a.out_dim + 15) / 16) * ((a.batch + 15) / 16);
     constexpr int RT = is_swiglu(EPI) ? 2 : 1;
-    if (EPI == kStore && lds_ok(a)) launch_lds<kStore>(a, st);
+    if (dot16_ok(static_cast<const uint16_t*>(a.x), a.w, a.batch, a.in_dim, a.ld_x) && dot_wins(a.batch, a.out_dim))
+        proj_dot<kXF16, EPI>(a, st);
+    else if (EPI == kStore && lds_ok(a)) launch_lds<kStore>(a, st);
     else if (a.batch <= 16 || (!is_swiglu(EPI) && tiles16 < 512)) launch_mfma<true, 1, RT, 8, false, EPI>(a, st);
     else if (is_swiglu(EPI) && a.batch > 32) launch_mfma<true, 4, 2, 4, false, EPI>(a, st);
     else launch_mfma<true, 2, 2, 8, false, EPI>(a, st);
@@ -935,7 +1005,7 @@ extern "C" int anelm_proj_f16_x16_tiled(void* y, const uint16_t* x16, const uint
 // Decode-step projections with the neighbouring layer ops fused in, for up
 // to 16 rows (see the header): the RMSNorm before a projection, the residual
 // add after one, the SwiGLU between the gate|up and down projections.
-extern "C" int anelm_proj_f16_fused(float* y, const float* x, const uint16_t* w16, long batch, int out_dim,
+extern "C" int anelm_proj_f16_fused(void* y, const float* x, const uint16_t* w16, long batch, int out_dim,
                                     int in_dim, long ld_x, long ld_y, const uint16_t* norm_bf16, float eps,
                                     int epilogue, void* stream) {
     clear_error();
@@ -945,31 +1015,36 @@ extern "C" int anelm_proj_f16_fused(float* y, const float* x, const uint16_t* w1
     if (!mfma_ok(x, false, w16, in_dim, ld_x) || (norm_bf16 && !aligned16(norm_bf16)))
         return fail(ANELM_ERR_INVALID,
                     "proj_f16_fused: needs in_dim a multiple of 32, ld_x a multiple of 4, 16-byte aligned x, W, gamma");
-    if (epilogue < ANELM_PROJ_STORE || epilogue > ANELM_PROJ_SWIGLU)
+    if (epilogue < ANELM_PROJ_STORE || epilogue > ANELM_PROJ_SWIGLU_F16)
         return fail(ANELM_ERR_INVALID, "proj_f16_fused: unknown epilogue %d", epilogue);
-    if (overlaps(y, ld_y, out_dim, 4, x, ld_x, in_dim, 4, batch))
+    if (overlaps(y, ld_y, out_dim, epilogue == ANELM_PROJ_SWIGLU_F16 ? 2 : 4, x, ld_x, in_dim, 4, batch))
         return fail(ANELM_ERR_INVALID,
                     "proj_f16_fused: y overlaps x (y is written while x is still read; the residual add takes the "
                     "residual stream as y and the projection input as a separate x)");
-    ProjArgs a = args(y, x, w16, batch, out_dim, in_dim, ld_x, ld_y);
+    ProjArgs a = args(static_cast<float*>(y), x, w16, batch, out_dim, in_dim, ld_x, ld_y);
+    a.y16 = static_cast<uint16_t*>(y);
     a.gamma = norm_bf16;
     a.eps = eps;
     a.pair_rows = out_dim;  // SwiGLU: W holds out_dim gate rows, then out_dim up rows
     hipStream_t st = as_stream(stream);
     const bool norm = norm_bf16 != nullptr;
-    if (dot_ok(x, w16, batch, in_dim, ld_x) && dot_wins(batch, out_dim)) {
+    if (dot_ok(x, w16, batch, in_dim, ld_x) && dot_wins(batch, out_dim) && (!norm || in_dim <= kDotNormMaxIn)) {
         switch (epilogue) {
             case ANELM_PROJ_STORE:
-                if (norm) proj_dot<true, kStore>(a, st);
-                else proj_dot<false, kStore>(a, st);
+                if (norm) proj_dot<kXNorm, kStore>(a, st);
+                else proj_dot<kXF32, kStore>(a, st);
                 break;
             case ANELM_PROJ_ADD:
-                if (norm) proj_dot<true, kAdd>(a, st);
-                else proj_dot<false, kAdd>(a, st);
+                if (norm) proj_dot<kXNorm, kAdd>(a, st);
+                else proj_dot<kXF32, kAdd>(a, st);
+                break;
+            case ANELM_PROJ_SWIGLU:
+                if (norm) proj_dot<kXNorm, kSwiGLU>(a, st);
+                else proj_dot<kXF32, kSwiGLU>(a, st);
                 break;
             default:
-                if (norm) proj_dot<true, kSwiGLU>(a, st);
-                else proj_dot<false, kSwiGLU>(a, st);
+                if (norm) proj_dot<kXNorm, kSwiGLU16>(a, st);
+                else proj_dot<kXF32, kSwiGLU16>(a, st);
                 break;
         }
         return launch_status("proj_f16_fused");
@@ -983,9 +1058,13 @@ extern "C" int anelm_proj_f16_fused(float* y, const float* x, const uint16_t* w1
             if (norm) f32_fused<true, kAdd>(a, st);
             else f32_fused<false, kAdd>(a, st);
             break;
-        default:
+        case ANELM_PROJ_SWIGLU:
             if (norm) f32_fused<true, kSwiGLU>(a, st);
             else f32_fused<false, kSwiGLU>(a, st);
+            break;
+        default:
+            if (norm) f32_fused<true, kSwiGLU16>(a, st);
+            else f32_fused<false, kSwiGLU16>(a, st);
             break;
     }
     return launch_status("proj_f16_fused");

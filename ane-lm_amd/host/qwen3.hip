@@ -319,18 +319,20 @@ extern "C" int anelm_qwen3_forward(anelm_qwen3* m, const int32_t* ids, const int
     }
     if (dims32) {
         // 5 calls per layer: the RMSNorms, residual adds and the SwiGLU
-        // ride in the projections (anelm_proj_f16_fused)
+        // ride in the projections; the attention and the SwiGLU hand the o
+        // and down projections their inputs already rounded to fp16 (the
+        // rounding those projections apply to their inputs anyway)
         for (int L = 0; L < c.layers; L++) {
             const anelm_qwen3::Layer& l = m->layers[L];
             CK(anelm_proj_f16_fused(m->qkv, m->x, l.qkv16, B, m->qkvdim, (int)H, H, m->qkvdim, l.w_in, c.rms_eps,
                                     ANELM_PROJ_STORE, stream));                                   // :503 + first_proj
-            CK(attend(l, m->attn, 0));                                                            // :444-490
-            CK(anelm_proj_f16_fused(m->x, m->attn, l.o16, B, (int)H, m->qdim, m->qdim, H, nullptr, 0.0f,
-                                    ANELM_PROJ_ADD, stream));                                     // o_proj + :516
-            CK(anelm_proj_f16_fused(m->h, m->x, l.gu16, B, (int)I, (int)H, H, I, l.w_post, c.rms_eps,
-                                    ANELM_PROJ_SWIGLU, stream));                                  // :518 + fused_ffn
-            CK(anelm_proj_f16_fused(m->x, m->h, l.down16, B, (int)H, (int)I, I, H, nullptr, 0.0f, ANELM_PROJ_ADD,
-                                    stream));                                                     // down + :527
+            CK(attend(l, m->y16, 1));                                                             // :444-490
+            CK(anelm_proj_f16_x16_fused(m->x, m->y16, l.o16, B, (int)H, m->qdim, m->qdim, H, ANELM_PROJ_ADD,
+                                        stream));                                                 // o_proj + :516
+            CK(anelm_proj_f16_fused(m->y16, m->x, l.gu16, B, (int)I, (int)H, H, I, l.w_post, c.rms_eps,
+                                    ANELM_PROJ_SWIGLU_F16, stream));                              // :518 + fused_ffn
+            CK(anelm_proj_f16_x16_fused(m->x, m->y16, l.down16, B, (int)H, (int)I, I, H, ANELM_PROJ_ADD,
+                                        stream));                                                 // down + :527
         }
         CK(anelm_proj_f16_fused(logits, m->x, m->lm16, B, (int)V, (int)H, H, ld_logits, m->final_norm, c.rms_eps,
                                 ANELM_PROJ_STORE, stream));                                       // :530 + LM head

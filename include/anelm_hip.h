@@ -508,24 +508,28 @@ int anelm_proj_f16_x16(float* y, const uint16_t* x16, const uint16_t* w16, long 
  *   ANELM_PROJ_ADD:    y = y + p (the residual add);
  *   ANELM_PROJ_SWIGLU: W16 holds out_dim gate rows then out_dim up rows, and
  *     y = silu(p_gate) * p_up (the SwiGLU of core/ane_runtime.cpp:393-395 in
- *     the fp32 form of core/cpu_ops.cpp:7-14).
+ *     the fp32 form of core/cpu_ops.cpp:7-14);
+ *   ANELM_PROJ_SWIGLU_F16: the same rounded to fp16 (nearest even) and
+ *     stored as fp16 bits: the down projection's input (anelm_proj_f16_x16_fused).
+ * y is fp32, or fp16 with ANELM_PROJ_SWIGLU_F16; ld_y counts its elements.
  * y must not overlap x.  Each result equals the separate kernels' to within
  * the RMSNorm's summation order.  No counterpart in the reference: the ANE runtime fuses
  * these inside its own fp16 programs. */
 #define ANELM_PROJ_STORE 0
 #define ANELM_PROJ_ADD 1
 #define ANELM_PROJ_SWIGLU 2
-int anelm_proj_f16_fused(float* y, const float* x, const uint16_t* w16, long batch, int out_dim, int in_dim,
+#define ANELM_PROJ_SWIGLU_F16 3
+int anelm_proj_f16_fused(void* y, const float* x, const uint16_t* w16, long batch, int out_dim, int in_dim,
                          long ld_x, long ld_y, const uint16_t* norm_bf16, float eps, int epilogue, void* stream);
 /* The epilogues of anelm_proj_f16_fused on inputs already rounded to fp16
  * (x16 [batch, in_dim], row stride ld_x a multiple of 8: anelm_rmsnorm_f16's
- * output, or a previous ANELM_PROJ_SWIGLU_F16), any batch: the decode step
- * past a few sequences, where one conversion of x beats one per workgroup.
- * y is fp32 (STORE, ADD, SWIGLU) or, with ANELM_PROJ_SWIGLU_F16, fp16: the
- * SwiGLU result rounded to nearest even, i.e. the down projection's input;
- * ld_y counts y's elements; y must not overlap x16.  in_dim a multiple of 32.
- * No counterpart in the reference (see anelm_proj_f16_fused). */
-#define ANELM_PROJ_SWIGLU_F16 3
+ * output, the attention's fp16 output, or a previous ANELM_PROJ_SWIGLU_F16),
+ * any batch: half the activation bytes of fp32 rows, and no rounding in
+ * every workgroup.  y is fp32 (STORE, ADD, SWIGLU) or, with
+ * ANELM_PROJ_SWIGLU_F16, fp16: the SwiGLU result rounded to nearest even,
+ * i.e. the down projection's input; ld_y counts y's elements; y must not
+ * overlap x16.  in_dim a multiple of 32.  No counterpart in the reference
+ * (see anelm_proj_f16_fused). */
 int anelm_proj_f16_x16_fused(void* y, const uint16_t* x16, const uint16_t* w16, long batch, int out_dim,
                              int in_dim, long ld_x, long ld_y, int epilogue, void* stream);
 

@@ -127,7 +127,8 @@ def test_proj_f16_fused_past_16_rows(hip, orc, rng, B, out_dim, in_dim, norm):
 
 
 @pytest.mark.parametrize("B,out_dim,in_dim", [(17, 4096, 1024), (64, 1024, 3072), (3, 1024, 2048), (64, 160, 64),
-                                               (40, 512, 256), (100, 2048, 1024)])
+                                               (40, 512, 256), (100, 2048, 1024), (1, 6144, 1024), (2, 1024, 3072),
+                                               (1, 40000, 1024), (1, 4096, 1024), (8, 1024, 4096), (1, 1000, 4128)])
 def test_proj_f16_x16_fused_epilogues(hip, orc, rng, B, out_dim, in_dim):
     """fp16 rows in (the fp16 RMSNorm's output), each epilogue: store and
     residual add against the oracle, the SwiGLU in fp32 and rounded to fp16
@@ -217,7 +218,7 @@ def test_proj_tiled(hip, orc, rng, B, out_dim, in_dim, same_kernel):
 
 @pytest.mark.parametrize("B,out_dim,in_dim", [(1, 1024, 1024), (11, 4096, 1024), (16, 300, 256), (3, 151936, 1024),
                                                (1, 4097, 1024), (2, 4101, 992), (1, 32771, 512), (1, 151936, 1024),
-                                               (4, 777, 3072)])
+                                               (4, 777, 3072), (1, 1024, 4096), (2, 512, 5120), (8, 1024, 2048)])
 def test_proj_fused_rmsnorm_prologue(hip, orc, rng, B, out_dim, in_dim):
     """The fused RMSNorm equals the oracle's RMSNorm followed by the
     projection (the normalised row rounded to fp16 on the way in)."""
@@ -271,6 +272,44 @@ def test_proj_fused_swiglu(hip, orc, rng, B, inter, in_dim, norm):
     eu = _ulp16(u) + mu * 2.0 ** -21 * 4
     tol = 1.1 * eg * np.abs(u) + np.abs(g / (1 + np.exp(-g))) * eu + eg * eu + np.abs(want) * 1e-6 + 1e-30
     assert np.all(np.abs(host(h).astype(np.float64) - want) <= tol)
+
+
+@pytest.mark.parametrize("B,inter,in_dim,norm", [(1, 3072, 1024, True), (2, 3072, 1024, False), (1, 1001, 4096, True),
+                                                   (16, 384, 256, True), (40, 512, 1024, False), (5, 160, 5120, True)])
+def test_proj_fused_swiglu_f16(hip, orc, rng, B, inter, in_dim, norm):
+    """The fp32-input SwiGLU stored as fp16 (the down projection's input)
+    is the fp32 SwiGLU rounded to nearest even, bit for bit, on the dot and
+    MFMA paths, with and without the fused RMSNorm."""
+    import torch
+
+    x = (2 * rng.standard_normal((B, in_dim))).astype(np.float32)
+    gamma = dev(bf16(1 + 0.1 * rng.standard_normal(in_dim)).view(np.int16)) if norm else None
+    w = dev((0.05 * rng.standard_normal((2 * inter, in_dim))).astype(np.float16).view(np.uint16))
+    h = torch.full((B, inter), float("nan"), device="cuda")
+    hip.proj_f16_fused(h, dev(x), w, norm=gamma, eps=1e-6, epilogue=hip.PROJ_SWIGLU)
+    h16 = torch.full((B, inter), -1, dtype=torch.int16, device="cuda")
+    hip.proj_f16_fused(h16, dev(x), w, norm=gamma, eps=1e-6, epilogue=hip.PROJ_SWIGLU_F16)
+    assert_bitexact(host(h16), orc.f32_to_f16_rne(host(h)).reshape(B, inter), "fp16 SwiGLU vs fp32 SwiGLU rounded")
+
+
+@pytest.mark.parametrize("B,out_dim,in_dim", [(1, 1024, 2048), (1, 1024, 3072), (2, 1024, 3072), (1, 4096, 1024),
+                                               (2, 6000, 1024), (1, 151936, 1024), (4, 1024, 1024), (8, 640, 4096)])
+def test_proj_x16_matches_f32_rows(hip, orc, rng, B, out_dim, in_dim):
+    """Rows that are exact fp16 values give the same bits through the fp32
+    entry (rounded per element in the kernel) and the fp16 entry (rounded by
+    their producer): the decode step hands the o and down projections fp16
+    rows on that basis."""
+    import torch
+
+    x16 = orc.f32_to_f16_rne((2 * rng.standard_normal((B, in_dim))).astype(np.float32)).reshape(B, in_dim)
+    x = x16.view(np.float16).astype(np.float32)
+    w = dev((0.03 * rng.standard_normal((out_dim, in_dim))).astype(np.float16).view(np.uint16))
+    r0 = rng.standard_normal((B, out_dim)).astype(np.float32)
+    for epi in (hip.PROJ_STORE, hip.PROJ_ADD):
+        y32, y16 = dev(r0), dev(r0)
+        hip.proj_f16_fused(y32, dev(x), w, epilogue=epi)
+        hip.proj_f16_x16_fused(y16, dev(x16.view(np.int16)), w, epilogue=epi)
+        assert_bitexact(host(y16), host(y32), f"x16 vs fp32 rows, epilogue {epi}")
 
 
 @pytest.mark.parametrize("tied,B", [(True, 3), (False, 3), (True, 11), (True, 1), (True, 20), (False, 33)])
