@@ -15,8 +15,9 @@
 //   phase 2: chunk softmax numerators (max, exp, sum) in LDS;
 //   phase 3: the same position mapping over V rows, weighted accumulation.
 // With one chunk per sequence the workgroup writes the normalised output;
-// otherwise it writes (max, sum, unnormalised output) partials that a second
-// kernel merges.  The grid is (kv head, sequence, chunk), chunk slowest: a
+// otherwise each chunk writes (max, sum, unnormalised output) partials and
+// counts itself done, and the last chunk of a (sequence, kv head) to finish
+// merges them.  The grid is (kv head, sequence, chunk), chunk slowest: a
 // short ring is done by its chunk 0 alone (the other chunks exit at once), and
 // with chunks dispatched last those workgroups all start in the first round.
 #include "anelm_common.hpp"
@@ -27,7 +28,10 @@ namespace {
 constexpr int kAttnThreads = 256;     // 4 waves
 constexpr int kAttnWaves = kAttnThreads / kWave;
 constexpr int kMaxChunk = 512;        // ring positions per workgroup
-constexpr int kMinChunk = 32;
+// 64, not 32: a workgroup keeps two 32-position batches of loads in flight,
+// so a 64-position chunk costs about one memory round trip like a 32-position
+// one, and a long ring at a small batch has half the chunks to merge.
+constexpr int kMinChunk = 64;
 constexpr int kMaxGD = 1024;          // group heads x head_dim per workgroup
 constexpr long kTargetBlocks = 2048;  // 8 workgroups per CU on 256 CUs
 constexpr int kMaxSplit = 4096;       // chunks per sequence (capacity <= 4096*32)
@@ -54,6 +58,7 @@ struct AttnArgs {
     int g0, gcount;             // q heads g0 .. g0+gcount-1 of every group
     float scale;
     float* ws;                  // [batch*nh][nsplit][head_dim + 2] partials
+    unsigned* ctr;              // [batch*nkv] chunks done (split launches; zero between launches)
     // QK launches (head_dim 128): q (at q, q_ld, q_hs = 128) and the new k and
     // v rows are the raw projection outputs.  q is normalised and rotated on
     // the fly; the workgroup whose chunk holds the ring's newest row (the
@@ -128,6 +133,81 @@ __device__ __forceinline__ void load8(float (&x)[8], const float* p) {
     x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
     x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
 }
+__device__ __forceinline__ void st_dev(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_dev(const float* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Merges the partials of chunks 0 .. live-1 of one (sequence, q head): one
+// wave; lane j owns chunks j, j+64, ... for the (max, sum) merge, then every
+// lane sums its head_dim/64 outputs over the chunks in chunk order.  The
+// first kBatch chunks' output partials are loaded together with the (max,
+// sum) pairs, before the max is known, so a ring of up to kBatch chunks costs
+// one memory round trip.  Loads use clamped indices (chunk live-1 re-read,
+// then discarded) so none sits behind a branch.  An empty chunk (sum 0)
+// contributes nothing; NaN sums propagate.
+template <int D>
+__device__ void merge_head(const AttnArgs& a, long b, int h, int lane, int live) {
+    constexpr int kBatch = D <= 128 ? 32 : 16;  // chunks whose partials are in flight at once
+    const int ns = a.nsplit;
+    const float* p = a.ws + (b * a.nh + h) * ns * (long)(D + 2);
+    auto clampc = [&](int s) { return s < live ? s : live - 1; };
+    // lane j holds chunk j's (max, sum); the first 64 stay in registers
+    const float m0r = ld_dev(p + clampc(lane) * (D + 2) + D);
+    const float l0r = ld_dev(p + clampc(lane) * (D + 2) + D + 1);
+    float v[kBatch][D / kWave];
+#pragma unroll
+    for (int j = 0; j < kBatch; j++)
+#pragma unroll
+        for (int i = 0; i < D / kWave; i++) v[j][i] = ld_dev(p + clampc(j) * (D + 2) + lane + i * kWave);
+    const float m0 = lane < live ? m0r : -INFINITY;
+    const float l0 = lane < live ? l0r : 0.0f;
+    float M = l0 > 0.0f ? m0 : -INFINITY;
+    for (int s = lane + kWave; s < live; s += kWave) {
+        if (ld_dev(p + s * (D + 2) + D + 1) > 0.0f) M = fmaxf(M, ld_dev(p + s * (D + 2) + D));
+    }
+    M = wave_max_rows(M);
+    float L = 0.0f;
+    float o[D / kWave];
+#pragma unroll
+    for (int i = 0; i < D / kWave; i++) o[i] = 0.0f;
+    for (int s0 = 0; s0 < live; s0 += kWave) {
+        const int s = s0 + lane;
+        float ms = m0, ls = l0;
+        if (s0 > 0) {
+            ms = s < live ? ld_dev(p + s * (D + 2) + D) : -INFINITY;
+            ls = s < live ? ld_dev(p + s * (D + 2) + D + 1) : 0.0f;
+        }
+        const float c = (!(ls > 0.0f) && ls == ls) ? 0.0f : expf(ms - M);
+        L = fmaf(ls, c, L);
+        const int cnt = min(kWave, live - s0);
+        for (int j0 = 0; j0 < cnt; j0 += kBatch) {
+            if (s0 + j0 > 0) {  // chunks past the first batch
+#pragma unroll
+                for (int j = 0; j < kBatch; j++)
+#pragma unroll
+                    for (int i = 0; i < D / kWave; i++)
+                        v[j][i] = ld_dev(p + clampc(s0 + j0 + j) * (D + 2) + lane + i * kWave);
+            }
+#pragma unroll
+            for (int j = 0; j < kBatch; j++) {
+                // past the last chunk: weight 0 and value 0 (not the re-read
+                // chunk's value, which could be infinite)
+                const bool on = j0 + j < cnt;
+                const float cj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(c), j0 + j));
+#pragma unroll
+                for (int i = 0; i < D / kWave; i++) o[i] = fmaf(on ? v[j][i] : 0.0f, on ? cj : 0.0f, o[i]);
+            }
+        }
+    }
+    L = wave_sum_rows(L);
+    const float inv = L == 0.0f ? 0.0f : 1.0f / L;   // no live position: zeros (cpu_ops.cpp:177-180)
+#pragma unroll
+    for (int i = 0; i < D / kWave; i++) put_out(a, b * a.out_ld + (long)h * D + lane + i * kWave, o[i] * inv);
+}
+
 // head-row element held in slot i of lane slice ds
 template <int D>
 __device__ __forceinline__ int elem_of(int ds, int i) { return (i < 4 ? 0 : D / 2 - 4) + 4 * ds + i; }
@@ -152,13 +232,14 @@ __global__ __launch_bounds__(kAttnThreads) void gqa_decode_kernel(AttnArgs a) {
     ring_state(a, b, start, len);
     // In a split launch a ring that is short (len <= a.whole, at most one
     // chunk's worth of LDS) is done by chunk 0 alone, which then writes the
-    // normalised output itself; the merge kernel skips that sequence.  The
-    // ring lengths live on the device, so this is decided per sequence here.
+    // normalised output itself, with no partials and no count.  The ring
+    // lengths live on the device, so this is decided per sequence here.
     const bool whole = !FINAL && len <= a.whole;
     if (whole && split > 0) return;
     const bool fin = FINAL || whole;
     const int t0 = split * a.chunk;
-    const int n = whole ? len : min(t0 + a.chunk, len) - t0;     // positions of this chunk (may be <= 0)
+    const int n = whole ? len : min(t0 + a.chunk, len) - t0;     // positions of this chunk
+    if (!fin && n <= 0) return;   // past the ring: neither partials nor a count
     const int ps = wid * PPW + lane / LP;          // position slot within a round
     const int ds = lane % LP;                      // this lane's 8-float slice
     const int row = a.nkv * D;                     // cap * row < 2^31 (checked on the host)
@@ -362,12 +443,12 @@ __global__ __launch_bounds__(kAttnThreads) void gqa_decode_kernel(AttnArgs a) {
         const int h = kvh * a.groups + a.g0 + g;
         if (fin) {
             put_out(a, b * a.out_ld + (long)h * D + d, s);
-        } else {
+        } else {   // device-scope stores: written through for the merging chunk, on any XCD
             float* p = a.ws + ((b * a.nh + h) * a.nsplit + split) * (long)(D + 2);
-            p[d] = s;
+            st_dev(p + d, s);
             if (d == 0) {
-                p[D] = hm[g];
-                p[D + 1] = hl[g];
+                st_dev(p + D, hm[g]);
+                st_dev(p + D + 1, hl[g]);
             }
         }
     }
@@ -384,82 +465,29 @@ __global__ __launch_bounds__(kAttnThreads) void gqa_decode_kernel(AttnArgs a) {
             *reinterpret_cast<float4*>(vd + D / 2) = make_float4(vnew[4], vnew[5], vnew[6], vnew[7]);
         }
     }
-}
-
-// Merges the per-chunk partials of one (sequence, q head), for rings longer
-// than a.whole (chunk 0 wrote the shorter ones' output): one wave; lane j
-// owns chunks j, j+64, ... for the (max, sum) merge, then every lane sums its
-// head_dim/64 outputs over all chunks.  The first kBatch chunks' output
-// partials are loaded together with the (max, sum) pairs, before the max is
-// known, so a ring of up to kBatch chunks costs one memory round trip.
-// Loads use clamped indices (chunk nsplit-1 re-read, then discarded) so
-// none sits behind a branch.
-template <int D>
-__global__ __launch_bounds__(kWave) void gqa_combine_kernel(AttnArgs a) {
-    constexpr int kBatch = D <= 128 ? 64 : 32;  // chunks whose partials are in flight at once
-    const int lane = threadIdx.x;
-    const long bh = blockIdx.x;
-    const long b = bh / a.nh;
-    const int h = (int)(bh % a.nh);
-    int start, len;
-    ring_state(a, b, start, len);
-    if (len <= a.whole) return;   // chunk 0 did the whole ring and wrote the output
-    const int ns = a.nsplit;
-    const float* p = a.ws + bh * ns * (long)(D + 2);
-    auto clampc = [&](int s) { return s < ns ? s : ns - 1; };
-    // lane j holds chunk j's (max, sum); the first 64 stay in registers
-    const float m0r = p[clampc(lane) * (D + 2) + D];
-    const float l0r = p[clampc(lane) * (D + 2) + D + 1];
-    float v[kBatch][D / kWave];
-#pragma unroll
-    for (int j = 0; j < kBatch; j++)
-#pragma unroll
-        for (int i = 0; i < D / kWave; i++) v[j][i] = p[clampc(j) * (D + 2) + lane + i * kWave];
-    const float m0 = lane < ns ? m0r : -INFINITY;
-    const float l0 = lane < ns ? l0r : 0.0f;
-    float M = l0 > 0.0f ? m0 : -INFINITY;
-    for (int s = lane + kWave; s < ns; s += kWave) {
-        if (p[s * (D + 2) + D + 1] > 0.0f) M = fmaxf(M, p[s * (D + 2) + D]);
-    }
-    M = wave_max_rows(M);
-    float L = 0.0f;
-    float o[D / kWave];
-#pragma unroll
-    for (int i = 0; i < D / kWave; i++) o[i] = 0.0f;
-    for (int s0 = 0; s0 < ns; s0 += kWave) {
-        const int s = s0 + lane;
-        float ms = m0, ls = l0;
-        if (s0 > 0) {
-            ms = s < ns ? p[s * (D + 2) + D] : -INFINITY;
-            ls = s < ns ? p[s * (D + 2) + D + 1] : 0.0f;
+    if (!fin) {
+        // Once every thread's partial stores are acknowledged (the wait
+        // covers them), one count per chunk on the (sequence, kv head)
+        // counter; the chunk that brings it to the number of live chunks
+        // merges, and resets the counter for the next launch.  No fence: the
+        // partials were written and are read with device-scope accesses,
+        // which bypass the non-coherent per-XCD L2 (a device-scope fence
+        // here would write back the whole L2).
+        __shared__ int s_last;
+        const int live = (len + a.chunk - 1) / a.chunk;
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (tid == 0) {
+            unsigned* c = a.ctr + b * a.nkv + kvh;
+            const unsigned prior = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const bool last = prior == (unsigned)(live - 1);
+            if (last) __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            s_last = last;
         }
-        // an empty chunk (sum 0) contributes nothing; NaN sums propagate
-        const float c = (!(ls > 0.0f) && ls == ls) ? 0.0f : expf(ms - M);
-        L = fmaf(ls, c, L);
-        const int cnt = min(kWave, ns - s0);
-        for (int j0 = 0; j0 < cnt; j0 += kBatch) {
-            if (s0 + j0 > 0) {  // chunks past the first batch
-#pragma unroll
-                for (int j = 0; j < kBatch; j++)
-#pragma unroll
-                    for (int i = 0; i < D / kWave; i++)
-                        v[j][i] = p[clampc(s0 + j0 + j) * (D + 2) + lane + i * kWave];
-            }
-#pragma unroll
-            for (int j = 0; j < kBatch; j++) {
-                // past the last chunk: weight 0 and value 0 (not the re-read
-                // chunk's value, which could be infinite)
-                const bool live = j0 + j < cnt;
-                const float cj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(c), j0 + j));
-#pragma unroll
-                for (int i = 0; i < D / kWave; i++) o[i] = fmaf(live ? v[j][i] : 0.0f, live ? cj : 0.0f, o[i]);
-            }
-        }
+        __syncthreads();
+        if (!s_last) return;
+        for (int g = wid; g < gc; g += kAttnWaves) merge_head<D>(a, b, kvh * a.groups + a.g0 + g, lane, live);
     }
-    L = wave_sum_rows(L);
-    const float inv = L == 0.0f ? 0.0f : 1.0f / L;   // no live position: zeros (cpu_ops.cpp:177-180)
-#pragma unroll
-    for (int i = 0; i < D / kWave; i++) put_out(a, b * a.out_ld + (long)h * D + lane + i * kWave, o[i] * inv);
 }
 
 // Ring append: one workgroup per sequence.
@@ -535,16 +563,19 @@ void launch_d(AttnArgs a, long batch, hipStream_t st) {
         else if (a.gcount <= 4) launch_gm<D, 4, QK>(a, batch, st);
         else launch_gm<D, (kMaxGD / D < 8 ? kMaxGD / D : 8), QK>(a, batch, st);
     }
-    if (a.nsplit > 1) {
-        hipLaunchKernelGGL((gqa_combine_kernel<D>), dim3(batch * a.nh), dim3(kWave), 0, st, a);
-    }
+}
+
+// Split launches: the partials, then (256-byte aligned) one counter per
+// (sequence, kv head).
+size_t partial_bytes(long batch, int nh, int nsplit, int D) {
+    return ((size_t)batch * nh * nsplit * (D + 2) * sizeof(float) + 255) & ~(size_t)255;
 }
 
 size_t ws_bytes_for(long batch, int nh, int nkv, int D, int cap) {
     const int chunk = pick_chunk(batch * nkv, cap);
     const long nsplit = (cap + chunk - 1) / chunk;
     if (nsplit <= 1) return 0;
-    return (size_t)batch * nh * nsplit * (D + 2) * sizeof(float);
+    return partial_bytes(batch, nh, (int)nsplit, D) + (size_t)batch * nkv * sizeof(unsigned);
 }
 
 int check_common(const void* out, const void* q, const void* kc, const void* vc, long batch, int nh, int nkv,
@@ -574,10 +605,12 @@ int run(AttnArgs a, long batch, int D, int bound, void* ws, size_t ws_bytes, hip
     if (a.nsplit < 1) a.nsplit = 1;
     a.whole = a.chunk > kWholeRows ? a.chunk : kWholeRows;   // <= kMaxChunk, the LDS score rows
     if (a.nsplit > 1) {
-        const size_t need = (size_t)batch * a.nh * a.nsplit * (D + 2) * sizeof(float);
+        const size_t pb = partial_bytes(batch, a.nh, a.nsplit, D);
+        const size_t need = pb + (size_t)batch * a.nkv * sizeof(unsigned);
         if (!ws || ws_bytes < need)
             return fail(ANELM_ERR_WORKSPACE, "gqa_attention: workspace of %zu bytes needed, %zu given", need, ws_bytes);
         if (!aligned16(ws)) return fail(ANELM_ERR_INVALID, "gqa_attention: workspace not 16-byte aligned");
+        a.ctr = reinterpret_cast<unsigned*>(static_cast<char*>(ws) + pb);
     }
     a.ws = static_cast<float*>(ws);
     if (batch == 0) return ANELM_OK;

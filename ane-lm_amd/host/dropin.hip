@@ -350,6 +350,9 @@ void gqa_attention(float* out, const float* q, const float* k_cache, const float
     char* d[4];
     char* dws = nullptr;
     S.get(sz, d, ws, &dws);
+    // the attention's workspace starts zero-filled (pooled scratch holds
+    // whatever the last call on this slot left)
+    if (ws && hipMemsetAsync(dws, 0, ws, S.s()) != hipSuccess) die("gqa_attention", "hipMemsetAsync failed");
     S.h2d(d[0], q, sz[0]);
     S.h2d(d[1], k_cache, sz[1]);
     S.h2d(d[2], v_cache, sz[2]);

@@ -219,7 +219,9 @@ extern "C" anelm_qwen3* anelm_qwen3_load(const char* path, const anelm_qwen3_con
         }
     }
     m->attn_ws_bytes = anelm_gqa_workspace_size(B, c.n_q_heads, c.n_kv_heads, c.head_dim, m->cap);
-    if (m->attn_ws_bytes && !(m->attn_ws = m->alloc(m->attn_ws_bytes))) {
+    if (m->attn_ws_bytes && (!(m->attn_ws = m->alloc(m->attn_ws_bytes)) ||
+                             hipMemsetAsync(m->attn_ws, 0, m->attn_ws_bytes, anelm::as_stream(stream)) != hipSuccess)) {
+        // the attention's workspace starts zero-filled; each call leaves it so
         rc = fail(ANELM_ERR_HIP, "qwen3_load: out of device memory");
         delete m;
         return nullptr;

@@ -375,7 +375,7 @@ def measure_attention(hip, w, steps, layers=8):
     start = torch.randint(0, cap, (B,), generator=g, device="cuda", dtype=torch.int32)
     length = torch.full((B,), cap, device="cuda", dtype=torch.int32)
     out = torch.empty(B, nq * D, device="cuda")
-    ws = torch.empty(max(hip.gqa_workspace_size(B, nq, nk, D, cap), 1), dtype=torch.uint8, device="cuda")
+    ws = torch.zeros(max(hip.gqa_workspace_size(B, nq, nk, D, cap), 1), dtype=torch.uint8, device="cuda")
     call = lambda: [hip.gqa_attention(out, L["q"], L["k"], L["v"], start, length, nq, nk, D, ws) for L in lay]
     gr = capture(call)
     gr.replay()

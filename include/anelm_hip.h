@@ -290,7 +290,11 @@ int anelm_kv_ring_append(float* k_cache, float* v_cache, int32_t* ring_start, in
  * n_heads a multiple of n_kv_heads; q and the caches 16-byte aligned with
  * strides that are multiples of 4.  Needs
  * anelm_gqa_workspace_size(batch, n_heads, n_kv_heads, head_dim, capacity)
- * bytes of device workspace (0 is possible: then workspace may be NULL). */
+ * bytes of device workspace (0 is possible: then workspace may be NULL),
+ * zero-filled before its first use (e.g. hipMemset once after allocating):
+ * it holds per-(sequence, kv head) counters of the chunks of a long ring,
+ * which every call leaves at zero.  Calls that share a workspace must not
+ * overlap. */
 size_t anelm_gqa_workspace_size(long batch, int n_heads, int n_kv_heads, int head_dim, int capacity);
 int anelm_gqa_attention(float* out, const float* q, const float* k_cache, const float* v_cache,
                         const int32_t* ring_start, const int32_t* ring_len, long batch, int n_heads,

@@ -151,10 +151,13 @@ def test_attention_argument_checks(lib):
     P = ctypes.c_void_p
     fake = P(0x1000)
     ws = lib.anelm_gqa_workspace_size
-    # one (sequence, kv head) pair per 32 positions at most -> the chunk is 512
-    # once there are >= 2048 workgroups, else it shrinks towards 32
-    assert ws(64, 32, 8, 128, 2048) == 64 * 32 * 4 * 130 * 4
-    assert ws(1, 32, 8, 128, 2048) == 32 * 64 * 130 * 4
+    # the chunk is 512 positions once there are >= 2048 workgroups, else it
+    # shrinks towards 64; the partials (rounded up to 256 bytes), then one
+    # counter per (sequence, kv head)
+    up = lambda n: (n + 255) // 256 * 256
+    assert ws(64, 32, 8, 128, 2048) == up(64 * 32 * 4 * 130 * 4) + 64 * 8 * 4
+    assert ws(1, 32, 8, 128, 2048) == up(32 * 32 * 130 * 4) + 8 * 4
+    assert ws(3, 12, 4, 64, 1000) == up(3 * 12 * 16 * 66 * 4) + 3 * 4 * 4
     assert ws(512, 16, 8, 128, 512) == 0                        # one chunk: no partials
     assert ws(0, 32, 8, 128, 2048) == 0
     g = lib.anelm_gqa_attention

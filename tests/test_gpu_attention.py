@@ -17,7 +17,7 @@ def ring_call(hip, q, kc, vc, nq, nk, D, start, length, qs=None):
 
     out = torch.full((nq, D), float("nan"), device="cuda")
     n = hip.gqa_workspace_size(1, nq, nk, D, kc.shape[0])
-    ws = torch.empty(max(n, 1), dtype=torch.uint8, device="cuda")
+    ws = torch.zeros(max(n, 1), dtype=torch.uint8, device="cuda")
     hip.gqa_attention_ring(out, dev(q), dev(kc), dev(vc), nq, nk, D, start, length, ws, q_head_stride=qs)
     return host(out)
 
@@ -85,7 +85,7 @@ def batched(hip, B, nq, nk, D, cap, starts, lens, rng, qs=None):
     kc = rng.standard_normal((B, cap, nk * D)).astype(np.float32)
     vc = rng.standard_normal((B, cap, nk * D)).astype(np.float32)
     out = torch.full((B, nq * D), float("nan"), device="cuda")
-    ws = torch.empty(max(hip.gqa_workspace_size(B, nq, nk, D, cap), 1), dtype=torch.uint8, device="cuda")
+    ws = torch.zeros(max(hip.gqa_workspace_size(B, nq, nk, D, cap), 1), dtype=torch.uint8, device="cuda")
     hip.gqa_attention(out, dev(q), dev(kc), dev(vc), dev(np.array(starts, np.int32)), dev(np.array(lens, np.int32)),
                       nq, nk, D, ws, q_head_stride=qs)
     return host(out).reshape(B, nq, D), q, kc, vc
@@ -129,7 +129,7 @@ def test_fp16_output_is_fp32_output_rounded(hip, orc, rng, B, cap, lens):
     q = dev(rng.standard_normal((B, nq * D)).astype(np.float32))
     kc = dev(rng.standard_normal((B, cap, nk * D)).astype(np.float32))
     vc = dev(rng.standard_normal((B, cap, nk * D)).astype(np.float32))
-    ws = torch.empty(max(hip.gqa_workspace_size(B, nq, nk, D, cap), 1), dtype=torch.uint8, device="cuda")
+    ws = torch.zeros(max(hip.gqa_workspace_size(B, nq, nk, D, cap), 1), dtype=torch.uint8, device="cuda")
     st, ln = dev(np.array(starts, np.int32)), dev(np.array(lens, np.int32))
     o32 = torch.empty(B, nq * D, device="cuda")
     hip.gqa_attention(o32, q, kc, vc, st, ln, nq, nk, D, ws)
@@ -161,7 +161,7 @@ def test_bounded_launch(hip, orc, rng, B, cap, bound):
     q = rng.standard_normal((B, nq * D)).astype(np.float32)
     kc = rng.standard_normal((B, cap, nk * D)).astype(np.float32)
     vc = rng.standard_normal((B, cap, nk * D)).astype(np.float32)
-    ws = torch.empty(max(hip.gqa_workspace_size(B, nq, nk, D, cap), 16), dtype=torch.uint8, device="cuda")
+    ws = torch.zeros(max(hip.gqa_workspace_size(B, nq, nk, D, cap), 16), dtype=torch.uint8, device="cuda")
     out = torch.empty(B, nq * D, device="cuda")
     hip.gqa_attention_bounded(out, dev(q), dev(kc), dev(vc), dev(starts), dev(lens), nq, nk, D, bound, ws)
     got = host(out).reshape(B, nq, D)
@@ -205,7 +205,7 @@ def test_append_then_attend_decode_loop(hip, orc, rng):
     vc = np.zeros((B, cap, row), np.float32)
     st = np.zeros((B, 2), np.int32)
     out = torch.empty(B, nq * D, device="cuda")
-    ws = torch.empty(max(hip.gqa_workspace_size(B, nq, nk, D, cap), 1), dtype=torch.uint8, device="cuda")
+    ws = torch.zeros(max(hip.gqa_workspace_size(B, nq, nk, D, cap), 1), dtype=torch.uint8, device="cuda")
     for step in range(30):
         k = rng.standard_normal((B, row)).astype(np.float32)
         v = rng.standard_normal((B, row)).astype(np.float32)
