@@ -640,8 +640,9 @@ def proj_tile_f16(w_tiled, w16, stream=None):
 
 
 def proj_f16_x16_tiled(y, x16, w_tiled, out_dim, epilogue=PROJ_STORE, stream=None):
-    """y [B, out] = the projection of fp16 rows x16 on a tiled W: fp32 (PROJ_STORE)
-    or fp16 bits (PROJ_STORE_F16)."""
+    """The fused epilogues of proj_f16_x16_fused on a tiled W (proj_tile_f16),
+    plus PROJ_STORE_F16: y [B, out_dim] fp32, or fp16 bits with PROJ_STORE_F16 /
+    PROJ_SWIGLU_F16; for the SwiGLU the tiled W holds 2*out_dim rows."""
     batch, in_dim = x16.shape
     _check(lib().anelm_proj_f16_x16_tiled(_ptr(y), _ptr(x16), _ptr(w_tiled), batch, out_dim, in_dim, _ld(x16),
                                           _ld(y), epilogue, _stream(stream)))

@@ -100,7 +100,12 @@ constexpr bool is_swiglu(int epi) { return epi == kSwiGLU || epi == kSwiGLU16; }
 // exactly the separate RMSNorm's output.  kSwiGLU needs RT = 2: tile 0 holds
 // gate rows, tile 1 the up rows pair_rows further on, and out_dim counts the
 // gate rows.
-template <bool XH, int NB, int RT, int R, bool NORM = false, int EPI = kStore, int NW = 4>
+// TILED: W in the tiled layout of anelm_proj_tile_f16 (the 16 x 32 block of
+// a row tile and an input step as one contiguous 1 KB piece in lane order),
+// so a weight load instruction reads 1 KB in a row rather than 64 bytes from
+// each of 16 rows a row pitch apart, which lands on few L2 channels.  The
+// operands, and so the outputs, are the same as with the row-major W.
+template <bool XH, int NB, int RT, int R, bool NORM = false, int EPI = kStore, int NW = 4, bool TILED = false>
 __global__ __launch_bounds__(64 * NW) void proj_mfma_kernel(ProjArgs a) {
     static_assert(!NORM || !XH, "the fused norm reads fp32 x");
     static_assert(!is_swiglu(EPI) || RT == 2, "SwiGLU pairs a gate tile with an up tile");
@@ -110,13 +115,23 @@ __global__ __launch_bounds__(64 * NW) void proj_mfma_kernel(ProjArgs a) {
     const int g = lane >> 4, c = lane & 15;
     const long row0 = (long)blockIdx.x * 16 * (is_swiglu(EPI) ? 1 : RT);
     const int b0 = blockIdx.y * 16 * NB;
-    // operand rows, clamped: rows past the end compute values that are never stored
+    // operand rows, clamped: rows past the end compute values that are never
+    // stored (TILED: tiles past the last load the last one; the SwiGLU's up
+    // tiles start pair_rows/16 tiles on, pair_rows a multiple of 16)
     const uint16_t* wp[RT];
 #pragma unroll
     for (int t = 0; t < RT; t++) {
-        const long r0 = is_swiglu(EPI) ? row0 + c : row0 + 16 * t + c;
-        const long r = (r0 < a.out_dim ? r0 : a.out_dim - 1) + (is_swiglu(EPI) && t == 1 ? a.pair_rows : 0);
-        wp[t] = a.w + r * a.in_dim + 8 * g;
+        if constexpr (TILED) {
+            const long ntile = (a.out_dim + 15) / 16;
+            long tile = row0 / 16 + (is_swiglu(EPI) ? 0 : t);
+            tile = tile < ntile ? tile : ntile - 1;
+            if (is_swiglu(EPI) && t == 1) tile += a.pair_rows / 16;
+            wp[t] = a.w + (tile * (a.in_dim / 32) * 64 + lane) * 8;
+        } else {
+            const long r0 = is_swiglu(EPI) ? row0 + c : row0 + 16 * t + c;
+            const long r = (r0 < a.out_dim ? r0 : a.out_dim - 1) + (is_swiglu(EPI) && t == 1 ? a.pair_rows : 0);
+            wp[t] = a.w + r * a.in_dim + 8 * g;
+        }
     }
     long xoff[NB];
 #pragma unroll
@@ -139,7 +154,7 @@ __global__ __launch_bounds__(64 * NW) void proj_mfma_kernel(ProjArgs a) {
             const int s = s0 + NW * j;
             const int k = 32 * (s < s_end ? s : s_end - 1);  // clamped: in bounds, result unused
 #pragma unroll
-            for (int t = 0; t < RT; t++) wr[j][t] = ld_nt(reinterpret_cast<const uint4*>(wp[t] + k));
+            for (int t = 0; t < RT; t++) wr[j][t] = ld_nt(reinterpret_cast<const uint4*>(wp[t] + (TILED ? 16L * k : k)));
             if constexpr (NORM) gq[j] = *reinterpret_cast<const uint4*>(a.gamma + k + 8 * g);
 #pragma unroll
             for (int nb = 0; nb < NB; nb++) {
@@ -811,11 +826,11 @@ __global__ __launch_bounds__(256) void tile_w16_kernel(uint16_t* dst, const uint
 }
 
 // ---- MFMA launch shapes -----------------------------------------------------
-template <bool XH, int NB, int RT, int R, bool NORM = false, int EPI = kStore, int NW = 4>
+template <bool XH, int NB, int RT, int R, bool NORM = false, int EPI = kStore, int NW = 4, bool TILED = false>
 void launch_mfma(const ProjArgs& a, hipStream_t st) {
     const int rows = 16 * (is_swiglu(EPI) ? 1 : RT);
     const dim3 grid((unsigned)((a.out_dim + rows - 1) / rows), (unsigned)((a.batch + 16 * NB - 1) / (16 * NB)));
-    proj_mfma_kernel<XH, NB, RT, R, NORM, EPI, NW><<<grid, dim3(64 * NW), 0, st>>>(a);
+    proj_mfma_kernel<XH, NB, RT, R, NORM, EPI, NW, TILED><<<grid, dim3(64 * NW), 0, st>>>(a);
 }
 
 // Up to 16 rows: one 16-row batch block, one row tile per workgroup (the
@@ -920,16 +935,21 @@ void f32_fused(const ProjArgs& a, hipStream_t st) {
 // The SwiGLU past 32 rows takes all 64 batch rows of a workgroup (each
 // gate|up tile read by one workgroup): 9.8 us against 11.8 us with 32 at the
 // Qwen3-0.6B shape and 64 rows; the other shapes measured no better so.
-template <int EPI>
-void x16_fused(const ProjArgs& a, hipStream_t st) {
+template <int EPI, bool TILED = false>
+void x16_mfma(const ProjArgs& a, hipStream_t st) {
     const long tiles16 = (long)((a.out_dim + 15) / 16) * ((a.batch + 15) / 16);
     constexpr int RT = is_swiglu(EPI) ? 2 : 1;
+    if (a.batch <= 16 || (!is_swiglu(EPI) && tiles16 < 512)) launch_mfma<true, 1, RT, 8, false, EPI, 4, TILED>(a, st);
+    else if (is_swiglu(EPI) && a.batch > 32) launch_mfma<true, 4, 2, 4, false, EPI, 4, TILED>(a, st);
+    else launch_mfma<true, 2, 2, 8, false, EPI, 4, TILED>(a, st);
+}
+
+template <int EPI>
+void x16_fused(const ProjArgs& a, hipStream_t st) {
     if (dot16_ok(static_cast<const uint16_t*>(a.x), a.w, a.batch, a.in_dim, a.ld_x) && dot_wins(a.batch, a.out_dim))
         proj_dot<kXF16, EPI>(a, st);
     else if (EPI == kStore && lds_ok(a)) launch_lds<kStore>(a, st);
-    else if (a.batch <= 16 || (!is_swiglu(EPI) && tiles16 < 512)) launch_mfma<true, 1, RT, 8, false, EPI>(a, st);
-    else if (is_swiglu(EPI) && a.batch > 32) launch_mfma<true, 4, 2, 4, false, EPI>(a, st);
-    else launch_mfma<true, 2, 2, 8, false, EPI>(a, st);
+    else x16_mfma<EPI>(a, st);
 }
 
 extern "C" int anelm_proj_f16_x16_fused(void* y, const uint16_t* x16, const uint16_t* w16, long batch, int out_dim,
@@ -985,20 +1005,38 @@ extern "C" int anelm_proj_f16_x16_tiled(void* y, const uint16_t* x16, const uint
     if (!y || !x16 || !w_tiled) return fail(ANELM_ERR_INVALID, "proj_f16_x16_tiled: null pointer");
     if (!sizes_ok(batch, out_dim, in_dim, ld_x, ld_y))
         return fail(ANELM_ERR_INVALID, "proj_f16_x16_tiled: bad sizes or strides");
-    if (in_dim % 256 != 0 || in_dim > 4096 || ld_x % 8 != 0 || !aligned16(x16) || !aligned16(w_tiled))
+    if (in_dim % 32 != 0 || ld_x % 8 != 0 || !aligned16(x16) || !aligned16(w_tiled))
         return fail(ANELM_ERR_INVALID,
-                    "proj_f16_x16_tiled: needs in_dim a multiple of 256 up to 4096, ld_x a multiple of 8, 16-byte "
-                    "aligned x and W");
-    if (epilogue != ANELM_PROJ_STORE && epilogue != ANELM_PROJ_STORE_F16)
-        return fail(ANELM_ERR_INVALID, "proj_f16_x16_tiled: epilogue %d (ANELM_PROJ_STORE or ANELM_PROJ_STORE_F16)",
-                    epilogue);
-    const bool f16 = epilogue == ANELM_PROJ_STORE_F16;
+                    "proj_f16_x16_tiled: needs in_dim a multiple of 32, ld_x a multiple of 8, 16-byte aligned x and W");
+    if (epilogue < ANELM_PROJ_STORE || epilogue > ANELM_PROJ_STORE_F16)
+        return fail(ANELM_ERR_INVALID, "proj_f16_x16_tiled: unknown epilogue %d", epilogue);
+    const bool swiglu = epilogue == ANELM_PROJ_SWIGLU || epilogue == ANELM_PROJ_SWIGLU_F16;
+    if (swiglu && out_dim % 16 != 0)
+        return fail(ANELM_ERR_INVALID, "proj_f16_x16_tiled: the SwiGLU needs out_dim (gate rows) a multiple of 16");
+    const bool f16 = epilogue == ANELM_PROJ_STORE_F16 || epilogue == ANELM_PROJ_SWIGLU_F16;
     if (overlaps(y, ld_y, out_dim, f16 ? 2 : 4, x16, ld_x, in_dim, 2, batch))
         return fail(ANELM_ERR_INVALID, "proj_f16_x16_tiled: y overlaps x (y is written while x is still read)");
     ProjArgs a = args(static_cast<float*>(y), x16, w_tiled, batch, out_dim, in_dim, ld_x, ld_y);
     a.y16 = static_cast<uint16_t*>(y);
-    if (f16) launch_lds<kStore16, true>(a, as_stream(stream));
-    else launch_lds<kStore, true>(a, as_stream(stream));
+    a.pair_rows = out_dim;
+    hipStream_t st = as_stream(stream);
+    // the stores stream W through the LDS kernel where anelm_proj_f16_x16_fused
+    // does (past 16 rows, at least 8192 output rows) and up to 16 rows; the
+    // rest takes the MFMA kernel's shapes of anelm_proj_f16_x16_fused
+    const bool lds_shape = in_dim % 256 == 0 && in_dim <= 4096;
+    const bool store = epilogue == ANELM_PROJ_STORE || epilogue == ANELM_PROJ_STORE_F16;
+    if (store && lds_shape && (batch <= 16 || lds_ok(a))) {
+        if (f16) launch_lds<kStore16, true>(a, st);
+        else launch_lds<kStore, true>(a, st);
+        return launch_status("proj_f16_x16_tiled");
+    }
+    switch (epilogue) {
+        case ANELM_PROJ_STORE: x16_mfma<kStore, true>(a, st); break;
+        case ANELM_PROJ_ADD: x16_mfma<kAdd, true>(a, st); break;
+        case ANELM_PROJ_SWIGLU: x16_mfma<kSwiGLU, true>(a, st); break;
+        case ANELM_PROJ_SWIGLU_F16: x16_mfma<kSwiGLU16, true>(a, st); break;
+        default: x16_mfma<kStore16, true>(a, st); break;
+    }
     return launch_status("proj_f16_x16_tiled");
 }
 

@@ -55,6 +55,8 @@ struct anelm_qwen3 {
     uint16_t* lm_tiled = nullptr;    // the same in anelm_proj_tile_f16's layout, past 16 sequences (or null)
     struct Layer {
         uint16_t *qkv16, *o16, *gu16, *down16;   // fp16 projections
+        // the same in anelm_proj_tile_f16's layout, past 16 sequences (or null)
+        uint16_t *qkv_t = nullptr, *o_t = nullptr, *gu_t = nullptr, *down_t = nullptr;
         uint16_t *qn, *kn, *w_in, *w_post;       // bf16 gammas
         float *kc, *vc;                          // [max_batch][cap][kvdim]
         int32_t *start, *len;                    // [max_batch], rows of ring_start / ring_len
@@ -218,6 +220,31 @@ extern "C" anelm_qwen3* anelm_qwen3_load(const char* path, const anelm_qwen3_con
             return nullptr;
         }
     }
+    // Past 16 sequences the layer projections read tiled copies too (each
+    // weight load instruction 1 KB in a row; the row-major weights stay for
+    // steps of up to 16 sequences)
+    if (B > 16 && H % 32 == 0 && I % 32 == 0 && m->qdim % 32 == 0) {
+        for (anelm_qwen3::Layer& l : m->layers) {
+            struct Tile {
+                uint16_t** dst;
+                const uint16_t* src;
+                long rows, cols;
+            } tiles[] = {{&l.qkv_t, l.qkv16, m->qkvdim, H}, {&l.o_t, l.o16, H, m->qdim},
+                         {&l.gu_t, l.gu16, 2 * I, H}, {&l.down_t, l.down16, H, I}};
+            for (const Tile& t : tiles) {
+                const size_t tb = anelm_proj_tiled_size((int)t.rows, (int)t.cols);
+                if (!(*t.dst = static_cast<uint16_t*>(m->alloc(tb)))) {
+                    rc = fail(ANELM_ERR_HIP, "qwen3_load: out of device memory");
+                    delete m;
+                    return nullptr;
+                }
+                if ((rc = anelm_proj_tile_f16(*t.dst, t.src, (int)t.rows, (int)t.cols, stream))) {
+                    delete m;
+                    return nullptr;
+                }
+            }
+        }
+    }
     m->attn_ws_bytes = anelm_gqa_workspace_size(B, c.n_q_heads, c.n_kv_heads, c.head_dim, m->cap);
     if (m->attn_ws_bytes && (!(m->attn_ws = m->alloc(m->attn_ws_bytes)) ||
                              hipMemsetAsync(m->attn_ws, 0, m->attn_ws_bytes, anelm::as_stream(stream)) != hipSuccess)) {
@@ -295,20 +322,24 @@ extern "C" int anelm_qwen3_forward(anelm_qwen3* m, const int32_t* ids, const int
         // (anelm_rmsnorm_f16) and the projections read fp16 rows; the SwiGLU
         // writes the down projection's fp16 input and the residual adds ride
         // in the o and down projections: 7 calls per layer
+        // fp16 rows x16 [B, n_in] (row stride n_in) through W, tiled where the
+        // load made the copy
+        auto proj16 = [&](void* y, const uint16_t* x16, const uint16_t* w, const uint16_t* wt, long n_out, long n_in,
+                          long ld_y, int epilogue) -> int {
+            if (wt)
+                return anelm_proj_f16_x16_tiled(y, x16, wt, B, (int)n_out, (int)n_in, n_in, ld_y, epilogue, stream);
+            return anelm_proj_f16_x16_fused(y, x16, w, B, (int)n_out, (int)n_in, n_in, ld_y, epilogue, stream);
+        };
         for (int L = 0; L < c.layers; L++) {
             const anelm_qwen3::Layer& l = m->layers[L];
             CK(anelm_rmsnorm_f16(m->a16, m->x, l.w_in, ANELM_BF16, B, (int)H, H, H, c.rms_eps, stream));  // :503
-            CK(anelm_proj_f16_x16_fused(m->qkv, m->a16, l.qkv16, B, m->qkvdim, (int)H, H, m->qkvdim,
-                                        ANELM_PROJ_STORE, stream));                               // first_proj
+            CK(proj16(m->qkv, m->a16, l.qkv16, l.qkv_t, m->qkvdim, H, m->qkvdim, ANELM_PROJ_STORE));      // first_proj
             // the attention writes the o projection's fp16 input (y16 is free until the SwiGLU)
             CK(attend(l, m->y16, 1));                                                             // :444-490
-            CK(anelm_proj_f16_x16_fused(m->x, m->y16, l.o16, B, (int)H, m->qdim, m->qdim, H, ANELM_PROJ_ADD,
-                                        stream));                                                 // o_proj + :516
+            CK(proj16(m->x, m->y16, l.o16, l.o_t, H, m->qdim, H, ANELM_PROJ_ADD));               // o_proj + :516
             CK(anelm_rmsnorm_f16(m->a16, m->x, l.w_post, ANELM_BF16, B, (int)H, H, H, c.rms_eps, stream));  // :518
-            CK(anelm_proj_f16_x16_fused(m->y16, m->a16, l.gu16, B, (int)I, (int)H, H, I, ANELM_PROJ_SWIGLU_F16,
-                                        stream));                                                 // fused_ffn
-            CK(anelm_proj_f16_x16_fused(m->x, m->y16, l.down16, B, (int)H, (int)I, I, H, ANELM_PROJ_ADD,
-                                        stream));                                                 // down + :527
+            CK(proj16(m->y16, m->a16, l.gu16, l.gu_t, I, H, I, ANELM_PROJ_SWIGLU_F16));          // fused_ffn
+            CK(proj16(m->x, m->y16, l.down16, l.down_t, H, I, H, ANELM_PROJ_ADD));               // down + :527
         }
         CK(anelm_rmsnorm_f16(m->a16, m->x, m->final_norm, ANELM_BF16, B, (int)H, H, H, c.rms_eps, stream));  // :530
         // the LM head (a 151936-row W streams once through the LDS-staged

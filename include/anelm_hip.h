@@ -537,19 +537,23 @@ int anelm_proj_f16_fused(void* y, const float* x, const uint16_t* w16, long batc
 int anelm_proj_f16_x16_fused(void* y, const uint16_t* x16, const uint16_t* w16, long batch, int out_dim,
                              int in_dim, long ld_x, long ld_y, int epilogue, void* stream);
 
-/* A long fp16 W (an LM head: 151936 rows) in a tiled layout for streaming it
- * once against many rows of x: for each 16-row tile and 32-input step, the
- * 16 x 32 block as one contiguous 1 KB piece in the MFMA operand order, rows
- * past out_dim zero.  anelm_proj_tiled_size gives its bytes (0 unless in_dim
- * is a multiple of 32); anelm_proj_tile_f16 writes it from the row-major W16
- * [out_dim, in_dim] (16-byte aligned, not overlapping; asynchronous).
- * anelm_proj_f16_x16_tiled is anelm_proj_f16_x16_fused's store on the tiled
- * copy, bit-identical to it: y fp32 (ANELM_PROJ_STORE) or fp16 bits
- * (ANELM_PROJ_STORE_F16, the ANE's own output), any batch, in_dim a multiple
- * of 256 up to 4096, ld_x a multiple of 8.  No counterpart in the reference:
- * the ANE runtime splits the LM head into chunks of its own format
- * (core/ane_runtime.cpp:265-408); this is the same contraction laid out for
- * coalesced HBM streaming. */
+/* An fp16 W in a tiled layout for streaming it against many rows of x:
+ * for each 16-row tile and 32-input step, the 16 x 32 block as one
+ * contiguous 1 KB piece in the MFMA operand order, rows past out_dim zero,
+ * so that every 16-byte-per-lane weight load reads 1 KB in a row instead of
+ * 64 bytes from each of 16 rows a row pitch apart.  anelm_proj_tiled_size
+ * gives its bytes (0 unless in_dim is a multiple of 32); anelm_proj_tile_f16
+ * writes it from the row-major W16 [out_dim, in_dim] (16-byte aligned, not
+ * overlapping; asynchronous).  anelm_proj_f16_x16_tiled is
+ * anelm_proj_f16_x16_fused on the tiled copy, every epilogue, plus
+ * ANELM_PROJ_STORE_F16 (the projection rounded to fp16, the ANE's own
+ * output); past 16 rows it runs the same kernels on the same operands, so
+ * its outputs are bit-identical to anelm_proj_f16_x16_fused's on the
+ * row-major W.  in_dim a multiple of 32, ld_x a multiple of 8; for the
+ * SwiGLU the tiled W holds the 2*out_dim rows (gate, then up) and out_dim is
+ * a multiple of 16.  No counterpart in the reference: the ANE runtime splits
+ * its weights into blobs of its own format (core/ane_runtime.cpp:265-408);
+ * this is the same contraction laid out for coalesced HBM streaming. */
 #define ANELM_PROJ_STORE_F16 4
 size_t anelm_proj_tiled_size(int out_dim, int in_dim);
 int anelm_proj_tile_f16(uint16_t* w_tiled, const uint16_t* w16, int out_dim, int in_dim, void* stream);

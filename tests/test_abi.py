@@ -98,17 +98,21 @@ def test_invalid_arguments_return_status_and_message(lib):
     assert lib.anelm_sample(fake, fake, 100, fake, 100, 1, 100, None, 0, None, ctypes.byref(p), fake, fake, 16,
                             None) == -4                                                  # workspace too small
     assert b"workspace" in lib.anelm_last_error()
-    # tiled projection: in_dim not a multiple of 32 / 256, unknown epilogue, W overlapping its tiled copy
+    # tiled projection: in_dim not a multiple of 32, unknown epilogue, a SwiGLU whose gate rows are not a
+    # multiple of 16, W overlapping its tiled copy
     lib.anelm_proj_tiled_size.restype = ctypes.c_size_t
     assert lib.anelm_proj_tiled_size(100, 1000) == 0
     assert lib.anelm_proj_tile_f16(fake, P(0x2000), 100, 1000, None) == -1
     assert lib.anelm_proj_tile_f16(fake, P(0x1100), 100, 1024, None) == -1             # overlap
     assert b"overlap" in lib.anelm_last_error()
-    assert lib.anelm_proj_f16_x16_tiled(P(0x100000), P(0x200000), P(0x300000), 64, 1000, 224, 224, 1000, 0,
-                                        None) == -1                                      # in_dim % 256
-    assert lib.anelm_proj_f16_x16_tiled(P(0x100000), P(0x200000), P(0x300000), 64, 1000, 256, 256, 1000, 1,
-                                        None) == -1                                      # ANELM_PROJ_ADD
+    assert lib.anelm_proj_f16_x16_tiled(P(0x100000), P(0x200000), P(0x300000), 64, 1000, 200, 200, 1000, 0,
+                                        None) == -1                                      # in_dim % 32
+    assert lib.anelm_proj_f16_x16_tiled(P(0x100000), P(0x200000), P(0x300000), 64, 1000, 256, 256, 1000, 5,
+                                        None) == -1                                      # no such epilogue
     assert b"epilogue" in lib.anelm_last_error()
+    assert lib.anelm_proj_f16_x16_tiled(P(0x100000), P(0x200000), P(0x300000), 64, 1000, 256, 256, 1000, 2,
+                                        None) == -1                                      # SwiGLU, 1000 % 16
+    assert b"multiple of 16" in lib.anelm_last_error()
 
 
 def test_tiled_size(lib):

@@ -216,6 +216,41 @@ def test_proj_tiled(hip, orc, rng, B, out_dim, in_dim, same_kernel):
     check_projection(orc, x, w, host(y).astype(np.float64))
 
 
+@pytest.mark.parametrize("B,out_dim,in_dim", [(64, 4096, 1024), (64, 1024, 2048), (64, 1024, 3072), (17, 1000, 256),
+                                               (40, 3072, 1024), (33, 784, 96), (20, 6144, 1024), (64, 16, 4096)])
+def test_proj_tiled_epilogues(hip, orc, rng, B, out_dim, in_dim):
+    """Past 16 rows the tiled W gives every epilogue the same bits as the
+    row-major W (the same kernels on the same operands): store, residual add,
+    SwiGLU in fp32 and fp16, and the fp16 store is the fp32 store narrowed."""
+    import torch
+
+    x16 = dev(orc.f32_to_f16_rne((2 * rng.standard_normal((B, in_dim))).astype(np.float32)).reshape(B, in_dim)
+              .view(np.int16))
+    w = (0.03 * rng.standard_normal((out_dim, in_dim))).astype(np.float16).view(np.uint16)
+    dw = dev(w)
+    wt = torch.full((hip.proj_tiled_size(out_dim, in_dim) // 2,), -1, dtype=torch.int16, device="cuda")
+    hip.proj_tile_f16(wt, dw)
+    r0 = rng.standard_normal((B, out_dim)).astype(np.float32)
+    for epi in (hip.PROJ_STORE, hip.PROJ_ADD):
+        yt, yr = dev(r0), dev(r0)
+        hip.proj_f16_x16_tiled(yt, x16, wt, out_dim, epilogue=epi)
+        hip.proj_f16_x16_fused(yr, x16, dw, epilogue=epi)
+        assert_bitexact(host(yt), host(yr), f"tiled vs row-major, epilogue {epi}")
+    y16 = torch.empty(B, out_dim, dtype=torch.int16, device="cuda")
+    hip.proj_f16_x16_tiled(y16, x16, wt, out_dim, epilogue=hip.PROJ_STORE_F16)
+    ys = torch.empty(B, out_dim, device="cuda")
+    hip.proj_f16_x16_tiled(ys, x16, wt, out_dim)
+    assert_bitexact(host(y16), orc.f32_to_f16_rne(host(ys)).reshape(B, out_dim), "fp16 store = fp32 store narrowed")
+    if out_dim % 32 == 0:   # the SwiGLU: out_dim/2 gate rows (a multiple of 16), then the up rows
+        inter = out_dim // 2
+        for epi, dt in ((hip.PROJ_SWIGLU, torch.float32), (hip.PROJ_SWIGLU_F16, torch.int16)):
+            ht = torch.full((B, inter), -1, dtype=dt, device="cuda")
+            hr = torch.full((B, inter), -1, dtype=dt, device="cuda")
+            hip.proj_f16_x16_tiled(ht, x16, wt, inter, epilogue=epi)
+            hip.proj_f16_x16_fused(hr, x16, dw, epilogue=epi)
+            assert_bitexact(host(ht), host(hr), f"tiled vs row-major SwiGLU, epilogue {epi}")
+
+
 @pytest.mark.parametrize("B,out_dim,in_dim", [(1, 1024, 1024), (11, 4096, 1024), (16, 300, 256), (3, 151936, 1024),
                                                (1, 4097, 1024), (2, 4101, 992), (1, 32771, 512), (1, 151936, 1024),
                                                (4, 777, 3072), (1, 1024, 4096), (2, 512, 5120), (8, 1024, 2048)])
