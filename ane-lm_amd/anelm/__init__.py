@@ -52,6 +52,7 @@ _SIGS = {
     "anelm_version": (_I, []),
     "anelm_rmsnorm": (_I, [_P, _P, _P, _I, _L, _I, _L, _L, _F, _P]),
     "anelm_rmsnorm_f16": (_I, [_P, _P, _P, _I, _L, _I, _L, _L, _F, _P]),
+    "anelm_rmsnorm_f16_tiled": (_I, [_P, _P, _P, _I, _L, _I, _L, _F, _P]),
     "anelm_add_rmsnorm": (_I, [_P, _P, _P, _P, _I, _L, _I, _L, _L, _L, _F, _P]),
     "anelm_qknorm_rope": (_I, [_P, _P, _L, _L, _P, _P, _I, _P, _P, _P, _I, _F, _L, _I, _I, _I, _F, _P]),
     "anelm_qknorm_rope_append": (_I, [_P, _P, _P, _L, _L, _L, _P, _P, _I, _P, _P, _P, _I, _F, _L, _I, _I, _F, _P, _P,
@@ -113,6 +114,7 @@ _SIGS = {
     "anelm_proj_tiled_size": (_S, [_I, _I]),
     "anelm_proj_tile_f16": (_I, [_P, _P, _I, _I, _P]),
     "anelm_proj_f16_x16_tiled": (_I, [_P, _P, _P, _L, _I, _I, _L, _L, _I, _P]),
+    "anelm_proj_f16_tt": (_I, [_P, _P, _P, _L, _I, _I, _L, _I, _P]),
     "anelm_qwen3_load": (_P, [ctypes.c_char_p, _P, _I, _I, _P]),
     "anelm_qwen3_free": (None, [_P]),
     "anelm_qwen3_reset": (_I, [_P, _P]),
@@ -199,6 +201,15 @@ def rmsnorm_f16(out16, x, w, eps=1e-6, stream=None):
     _, _, ldo = _rows(out16)
     _check(lib().anelm_rmsnorm_f16(_ptr(out16), _ptr(x), _ptr(w), _dtype_code(w), rows, dim, ldx, ldo, eps,
                                    _stream(stream)))
+
+
+def rmsnorm_f16_tiled(out_t, x, w, eps=1e-6, stream=None):
+    """out_t (int16/float16, proj_tiled_size(rows, dim) bytes) = rmsnorm_f16 of x
+    in the tiled layout of proj_tile_f16."""
+    rows, dim, ldx = _rows(x)
+    _need(_nbytes(out_t) >= lib().anelm_proj_tiled_size(rows, dim), "rmsnorm_f16_tiled: out_t too small")
+    _check(lib().anelm_rmsnorm_f16_tiled(_ptr(out_t), _ptr(x), _ptr(w), _dtype_code(w), rows, dim, ldx, eps,
+                                         _stream(stream)))
 
 
 def add_rmsnorm(x, y, out, w, eps=1e-6, stream=None):
@@ -430,21 +441,23 @@ def kv_ring_advance(ring_start, ring_len, capacity, batch=None, stream=None):
 
 
 def gqa_attention_qk(out, q, k, v, wq, wk, pos, cos_tab, sin_tab, k_cache, v_cache, ring_start, ring_len, n_heads,
-                     n_kv_heads, workspace, theta=1e6, eps=1e-6, stream=None):
+                     n_kv_heads, workspace, theta=1e6, eps=1e-6, stream=None, tiled=False):
     """qknorm_rope_append + gqa_attention in one launch (head_dim 128) for rings
     already advanced by kv_ring_advance.  q: [B, >= n_heads*128], k, v: [B, >=
     n_kv_heads*128] (row slices of the qkv projection allowed, left as they
-    are); out fp32 or fp16; caches [B, capacity, n_kv_heads*128]."""
+    are); out fp32 or fp16 (tiled: fp16 in the tiled layout of proj_tile_f16,
+    n_heads*128 columns); caches [B, capacity, n_kv_heads*128]."""
     B = q.shape[0]
     cap = k_cache.shape[1]
     _need(k_cache.stride() == v_cache.stride() and k_cache.stride(2) == 1 and k_cache.stride(1) == n_kv_heads * 128,
           "gqa_attention_qk: cache layout")
     wdt = _dtype_code(wq if wq is not None else (wk if wk is not None else q))
     tab_len = cos_tab.shape[0] if cos_tab is not None else 0
-    _check(lib().anelm_gqa_attention_qk(_ptr(out), int(out.element_size() == 2), _ptr(q), _ptr(k), _ptr(v), _ld(q),
+    mode = 2 if tiled else int(out.element_size() == 2)
+    _check(lib().anelm_gqa_attention_qk(_ptr(out), mode, _ptr(q), _ptr(k), _ptr(v), _ld(q),
                                         _ld(k), _ld(v), _ptr(wq), _ptr(wk), wdt, _ptr(pos), _ptr(cos_tab),
                                         _ptr(sin_tab), tab_len, theta, eps, _ptr(k_cache), _ptr(v_cache),
-                                        _ptr(ring_start), _ptr(ring_len), B, n_heads, n_kv_heads, _ld(out), cap,
+                                        _ptr(ring_start), _ptr(ring_len), B, n_heads, n_kv_heads, n_heads * 128 if tiled else _ld(out), cap,
                                         k_cache.stride(0), _ptr(workspace), _nbytes(workspace), _stream(stream)))
 
 
@@ -646,6 +659,18 @@ def proj_f16_x16_tiled(y, x16, w_tiled, out_dim, epilogue=PROJ_STORE, stream=Non
     batch, in_dim = x16.shape
     _check(lib().anelm_proj_f16_x16_tiled(_ptr(y), _ptr(x16), _ptr(w_tiled), batch, out_dim, in_dim, _ld(x16),
                                           _ld(y), epilogue, _stream(stream)))
+
+
+PROJ_SWIGLU_F16_TILED = 5
+
+
+def proj_f16_tt(y, x_t, w_t, batch, out_dim, in_dim, epilogue=PROJ_STORE, stream=None):
+    """The tiled-W projection on x_t in the tiled layout too (batch rows, in_dim
+    columns); y [batch, out_dim] fp32 / fp16 bits, or with PROJ_SWIGLU_F16_TILED
+    fp16 in the tiled layout (batch rows, out_dim columns)."""
+    ld_y = out_dim if epilogue == PROJ_SWIGLU_F16_TILED else _ld(y)
+    _check(lib().anelm_proj_f16_tt(_ptr(y), _ptr(x_t), _ptr(w_t), batch, out_dim, in_dim, ld_y, epilogue,
+                                   _stream(stream)))
 
 
 class Qwen3Model:

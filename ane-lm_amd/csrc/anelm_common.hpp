@@ -99,6 +99,14 @@ __device__ __forceinline__ float wave_max_rows(float v) {
     return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
 }
 
+// Element (r, c) of an fp16 matrix with `cols` columns (a multiple of 32)
+// in the tiled layout of anelm_proj_tile_f16: for each 16-row tile and
+// 32-column step, the 16 x 32 block as 64 pieces of 8, piece l holding row
+// 16t + l%16, columns 32s + 8(l/16) .. +7.
+__device__ __forceinline__ long tiled_index(long r, int c, int cols) {
+    return (((r >> 4) * (cols >> 5) + (c >> 5)) * 64 + (r & 15) + 16 * ((c & 31) >> 3)) * 8 + (c & 7);
+}
+
 __device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
 #pragma unroll
     for (int d = 32; d >= 1; d >>= 1) {

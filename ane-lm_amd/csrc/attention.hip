@@ -41,6 +41,7 @@ static_assert(kWholeRows <= kMaxChunk, "a whole ring's scores fit the LDS rows")
 struct AttnArgs {
     float* out;
     uint16_t* out16;            // when set, outputs go here as fp16 (nearest even) instead of to out
+    int out_cols;               // > 0: out16 in the tiled layout of anelm_proj_tile_f16, this many columns
     const float* q;
     const float* kc;
     const float* vc;
@@ -77,11 +78,16 @@ struct AttnArgs {
     float inv[64];              // RoPE inverse frequencies of the 64 pairs
 };
 
-// An attention output: fp32, or fp16 rounded to nearest even (the input
-// rounding of the projection that follows, done once here).
-__device__ __forceinline__ void put_out(const AttnArgs& a, long i, float v) {
-    if (a.out16) a.out16[i] = __builtin_bit_cast(uint16_t, to_f16(v));
-    else a.out[i] = v;
+// An attention output (sequence b, column col = head*head_dim + d): fp32, or
+// fp16 rounded to nearest even (the input rounding of the projection that
+// follows, done once here), in rows or in the tiled layout.
+__device__ __forceinline__ void put_out(const AttnArgs& a, long b, int col, float v) {
+    if (a.out16) {
+        const long i = a.out_cols > 0 ? tiled_index(b, col, a.out_cols) : b * a.out_ld + col;
+        a.out16[i] = __builtin_bit_cast(uint16_t, to_f16(v));
+    } else {
+        a.out[b * a.out_ld + col] = v;
+    }
 }
 
 // The ring state of sequence b, clamped so that every access stays inside
@@ -205,7 +211,7 @@ __device__ void merge_head(const AttnArgs& a, long b, int h, int lane, int live)
     L = wave_sum_rows(L);
     const float inv = L == 0.0f ? 0.0f : 1.0f / L;   // no live position: zeros (cpu_ops.cpp:177-180)
 #pragma unroll
-    for (int i = 0; i < D / kWave; i++) put_out(a, b * a.out_ld + (long)h * D + lane + i * kWave, o[i] * inv);
+    for (int i = 0; i < D / kWave; i++) put_out(a, b, h * D + lane + i * kWave, o[i] * inv);
 }
 
 // head-row element held in slot i of lane slice ds
@@ -442,7 +448,7 @@ __global__ __launch_bounds__(kAttnThreads) void gqa_decode_kernel(AttnArgs a) {
         for (int w = 1; w < kAttnWaves; w++) s += red[w][g][d];
         const int h = kvh * a.groups + a.g0 + g;
         if (fin) {
-            put_out(a, b * a.out_ld + (long)h * D + d, s);
+            put_out(a, b, h * D + d, s);
         } else {   // device-scope stores: written through for the merging chunk, on any XCD
             float* p = a.ws + ((b * a.nh + h) * a.nsplit + split) * (long)(D + 2);
             st_dev(p + d, s);
@@ -769,11 +775,14 @@ extern "C" int anelm_gqa_attention_qk(void* out, int out_f16, const float* q, co
     const bool wal = w_dtype == ANELM_F32 ? aligned16(wq) && aligned16(wk) : aligned8(wq) && aligned8(wk);
     if (!aligned16(k) || !aligned16(v) || ((k_ld | v_ld) & 3) || !wal || !aligned16(cos_tab) || !aligned16(sin_tab))
         return fail(ANELM_ERR_INVALID, "%s: needs 16-byte aligned rows (strides multiples of 4)", fn);
+    if (out_f16 < 0 || out_f16 > 2) return fail(ANELM_ERR_INVALID, "%s: out_f16 %d (0, 1 or 2)", fn, out_f16);
+    if (out_f16 == 2 && !aligned16(out)) return fail(ANELM_ERR_INVALID, "%s: the tiled output needs 16-byte alignment", fn);
     InvFreq inv;
     rope_inv_freq(&inv, 128, theta);
     AttnArgs a{};
     if (out_f16) a.out16 = static_cast<uint16_t*>(out);
     else a.out = static_cast<float*>(out);
+    if (out_f16 == 2) a.out_cols = n_heads * 128;
     a.q = q; a.kc = k_cache; a.vc = v_cache;
     a.ring_start = ring_start; a.ring_len = ring_len;
     a.nh = n_heads; a.nkv = n_kv_heads;

@@ -40,7 +40,10 @@ __device__ __forceinline__ uint32_t f16_bits_rne(float v) {
 // every Qwen3 shape), so no lane is guarded.  (Two rows per workgroup, both
 // in flight with the gammas loaded once, measured 2 points slower for the
 // RMSNorm and 7 for add + RMSNorm at 8192 rows of 4096.)
-template <int NV, int DT, bool ADD, bool O16 = false, bool FULL = false>
+// TILE (with O16, dim a multiple of 32): the fp16 output in the tiled layout
+// of anelm_proj_tile_f16 (rows of 16, steps of 32 columns, each 16 x 32 block
+// one contiguous 1 KB piece), the input layout of the tiled projection.
+template <int NV, int DT, bool ADD, bool O16 = false, bool FULL = false, bool TILE = false>
 __global__ __launch_bounds__(1024) void rmsnorm_row_kernel(void* out, float* x, const float* y,
                                                            const void* w, long rows, int dim,
                                                            long ld_x, long ld_y, long ld_out,
@@ -107,9 +110,14 @@ __global__ __launch_bounds__(1024) void rmsnorm_row_kernel(void* out, float* x, 
             o.z = (v[i].z * s) * wv.z;
             o.w = (v[i].w * s) * wv.w;
             if constexpr (O16) {
-                uint16_t* orow = static_cast<uint16_t*>(out) + row * ld_out;
-                *reinterpret_cast<uint2*>(orow + c) = make_uint2(f16_bits_rne(o.x) | (f16_bits_rne(o.y) << 16),
-                                                                 f16_bits_rne(o.z) | (f16_bits_rne(o.w) << 16));
+                const uint2 h = make_uint2(f16_bits_rne(o.x) | (f16_bits_rne(o.y) << 16),
+                                           f16_bits_rne(o.z) | (f16_bits_rne(o.w) << 16));
+                if constexpr (TILE) {
+                    *reinterpret_cast<uint2*>(static_cast<uint16_t*>(out) + tiled_index(row, c, dim)) = h;
+                } else {
+                    uint16_t* orow = static_cast<uint16_t*>(out) + row * ld_out;
+                    *reinterpret_cast<uint2*>(orow + c) = h;
+                }
             } else {
                 st_nt(reinterpret_cast<float4*>(static_cast<float*>(out) + row * ld_out + c), o);
             }
@@ -149,7 +157,7 @@ __global__ __launch_bounds__(256) void rmsnorm_block_kernel(void* out, float* x,
     }
 }
 
-template <int DT, bool ADD, bool O16 = false>
+template <int DT, bool ADD, bool O16 = false, bool TILE = false>
 static int launch_rmsnorm_dt(void* out, float* x, const float* y, const void* w, long rows,
                              int dim, long ld_x, long ld_y, long ld_out, float eps,
                              hipStream_t st) {
@@ -158,31 +166,35 @@ static int launch_rmsnorm_dt(void* out, float* x, const float* y, const void* w,
                      (DT == ANELM_F32 ? aligned16(w) : aligned8(w)) &&
                      (!ADD || ((ld_y % 4 == 0) && aligned16(y)));
     const int nvec = dim / 4;  // float4 per row
+    if (TILE && !(vec && nvec <= 1024 * 4))
+        return fail(ANELM_ERR_INVALID, "rmsnorm: the tiled output needs 16-byte aligned x, ld_x a multiple of 4, "
+                                       "an 8-byte aligned gamma and dim <= 16384");
     if (vec && nvec <= 1024 * 4) {
         int nv, threads;
         rms_row_geometry(rows, nvec, nv, threads);
         const dim3 grd((unsigned)rows);
         const bool full = nvec == nv * threads;
 #define ANELM_RMS_ROW(NV_, FULL_) \
-    rmsnorm_row_kernel<NV_, DT, ADD, O16, FULL_><<<grd, threads, 0, st>>>(out, x, y, w, rows, dim, ld_x, ld_y, ld_out, eps)
+    rmsnorm_row_kernel<NV_, DT, ADD, O16, FULL_, TILE><<<grd, threads, 0, st>>>(out, x, y, w, rows, dim, ld_x, ld_y, ld_out, eps)
         if (nv == 1) full ? ANELM_RMS_ROW(1, true) : ANELM_RMS_ROW(1, false);
         else if (nv == 2) full ? ANELM_RMS_ROW(2, true) : ANELM_RMS_ROW(2, false);
         else full ? ANELM_RMS_ROW(4, true) : ANELM_RMS_ROW(4, false);
 #undef ANELM_RMS_ROW
         return launch_status("rmsnorm");
     }
-    rmsnorm_block_kernel<DT, ADD, O16><<<dim3((unsigned)rows), dim3(256), 0, st>>>(out, x, y, w, rows, dim, ld_x,
-                                                                                   ld_y, ld_out, eps);
+    if constexpr (!TILE)
+        rmsnorm_block_kernel<DT, ADD, O16><<<dim3((unsigned)rows), dim3(256), 0, st>>>(out, x, y, w, rows, dim, ld_x,
+                                                                                       ld_y, ld_out, eps);
     return launch_status("rmsnorm");
 }
 
-template <bool ADD, bool O16 = false>
+template <bool ADD, bool O16 = false, bool TILE = false>
 static int launch_rmsnorm(void* out, float* x, const float* y, const void* w, int dt, long rows,
                           int dim, long ld_x, long ld_y, long ld_out, float eps, hipStream_t st) {
     switch (dt) {
-        case ANELM_F32: return launch_rmsnorm_dt<ANELM_F32, ADD, O16>(out, x, y, w, rows, dim, ld_x, ld_y, ld_out, eps, st);
-        case ANELM_F16: return launch_rmsnorm_dt<ANELM_F16, ADD, O16>(out, x, y, w, rows, dim, ld_x, ld_y, ld_out, eps, st);
-        case ANELM_BF16: return launch_rmsnorm_dt<ANELM_BF16, ADD, O16>(out, x, y, w, rows, dim, ld_x, ld_y, ld_out, eps, st);
+        case ANELM_F32: return launch_rmsnorm_dt<ANELM_F32, ADD, O16, TILE>(out, x, y, w, rows, dim, ld_x, ld_y, ld_out, eps, st);
+        case ANELM_F16: return launch_rmsnorm_dt<ANELM_F16, ADD, O16, TILE>(out, x, y, w, rows, dim, ld_x, ld_y, ld_out, eps, st);
+        case ANELM_BF16: return launch_rmsnorm_dt<ANELM_BF16, ADD, O16, TILE>(out, x, y, w, rows, dim, ld_x, ld_y, ld_out, eps, st);
         default: return fail(ANELM_ERR_INVALID, "rmsnorm: unknown weight dtype %d", dt);
     }
 }
@@ -475,6 +487,22 @@ extern "C" int anelm_rmsnorm_f16(uint16_t* out16, const float* x, const void* w,
     clear_error();
     return launch_rmsnorm<false, true>(out16, const_cast<float*>(x), nullptr, w, w_dtype, rows, dim, ld_x, 0, ld_out,
                                        eps, as_stream(stream));
+}
+
+extern "C" int anelm_rmsnorm_f16_tiled(uint16_t* out_t, const float* x, const void* w, int w_dtype, long rows, int dim,
+                                       long ld_x, float eps, void* stream) {
+    if (!out_t || !x || !w) return fail(ANELM_ERR_INVALID, "anelm_rmsnorm_f16_tiled: null pointer");
+    if (rows <= 0 || dim <= 0 || dim % 32 != 0)
+        return fail(ANELM_ERR_INVALID, "anelm_rmsnorm_f16_tiled: rows=%ld dim=%d (a multiple of 32)", rows, dim);
+    if (ld_x < dim) return fail(ANELM_ERR_INVALID, "anelm_rmsnorm_f16_tiled: ld_x < dim");
+    if (rows > 0x7FFFFFFFL) return fail(ANELM_ERR_INVALID, "anelm_rmsnorm_f16_tiled: too many rows");
+    const size_t out_bytes = (size_t)((rows + 15) / 16) * 16 * (size_t)dim * 2u;
+    const uintptr_t o0 = reinterpret_cast<uintptr_t>(out_t), x0 = reinterpret_cast<uintptr_t>(x);
+    if (o0 < x0 + (uintptr_t)((rows - 1) * ld_x + dim) * 4u && x0 < o0 + out_bytes)
+        return fail(ANELM_ERR_INVALID, "anelm_rmsnorm_f16_tiled: out_t overlaps x");
+    clear_error();
+    return launch_rmsnorm<false, true, true>(out_t, const_cast<float*>(x), nullptr, w, w_dtype, rows, dim, ld_x, 0, dim,
+                                             eps, as_stream(stream));
 }
 
 extern "C" int anelm_add_rmsnorm(float* x, const float* y, float* out, const void* w, int w_dtype,

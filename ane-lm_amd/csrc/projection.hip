@@ -91,8 +91,9 @@ enum Epilogue {
     kSwiGLU = 2,  // y = silu(p_gate) * p_up  (core/ane_runtime.cpp:393-395)
     kSwiGLU16 = 3,  // the same rounded to fp16 (nearest even) into y16: the next projection's input
     kStore16 = 4,   // y16 = p as fp16 bits (the ANE kernels' own fp16 output)
+    kSwiGLU16T = 5, // kSwiGLU16 with y16 in the tiled layout (out_dim columns): the tiled projection's input
 };
-constexpr bool is_swiglu(int epi) { return epi == kSwiGLU || epi == kSwiGLU16; }
+constexpr bool is_swiglu(int epi) { return epi == kSwiGLU || epi == kSwiGLU16 || epi == kSwiGLU16T; }
 
 // kNorm (fp32 x): the workgroup first computes the RMSNorm scale
 // 1/sqrtf(ss/dim + eps) of each of its batch rows (core/cpu_ops.cpp:25-31),
@@ -103,10 +104,13 @@ constexpr bool is_swiglu(int epi) { return epi == kSwiGLU || epi == kSwiGLU16; }
 // TILED: W in the tiled layout of anelm_proj_tile_f16 (the 16 x 32 block of
 // a row tile and an input step as one contiguous 1 KB piece in lane order),
 // so a weight load instruction reads 1 KB in a row rather than 64 bytes from
-// each of 16 rows a row pitch apart, which lands on few L2 channels.  The
-// operands, and so the outputs, are the same as with the row-major W.
-template <bool XH, int NB, int RT, int R, bool NORM = false, int EPI = kStore, int NW = 4, bool TILED = false>
+// each of 16 rows a row pitch apart, which lands on few L2 channels.  XT:
+// the fp16 x in the same layout (batch rows as its rows).  The operands, and
+// so the outputs, are the same as with row-major W and x.
+template <bool XH, int NB, int RT, int R, bool NORM = false, int EPI = kStore, int NW = 4, bool TILED = false,
+          bool XT = false>
 __global__ __launch_bounds__(64 * NW) void proj_mfma_kernel(ProjArgs a) {
+    static_assert(!XT || XH, "the tiled x is fp16");
     static_assert(!NORM || !XH, "the fused norm reads fp32 x");
     static_assert(!is_swiglu(EPI) || RT == 2, "SwiGLU pairs a gate tile with an up tile");
     __shared__ float4v part[NW][RT * NB][64];
@@ -133,11 +137,17 @@ __global__ __launch_bounds__(64 * NW) void proj_mfma_kernel(ProjArgs a) {
             wp[t] = a.w + r * a.in_dim + 8 * g;
         }
     }
+    // x rows (clamped); XT: the batch tile's pieces (tiles past the last load the last one)
     long xoff[NB];
 #pragma unroll
     for (int nb = 0; nb < NB; nb++) {
-        const int b = b0 + nb * 16 + c;
-        xoff[nb] = (long)(b < a.batch ? b : a.batch - 1) * a.ld_x + 8 * g;
+        if constexpr (XT) {
+            const long bt = b0 / 16 + nb, last = (a.batch - 1) / 16;
+            xoff[nb] = ((bt < last ? bt : last) * (a.in_dim / 32) * 64 + lane) * 8;
+        } else {
+            const int b = b0 + nb * 16 + c;
+            xoff[nb] = (long)(b < a.batch ? b : a.batch - 1) * a.ld_x + 8 * g;
+        }
     }
     const float* xf = static_cast<const float*>(a.x);
     const uint16_t* xh = static_cast<const uint16_t*>(a.x);
@@ -159,7 +169,7 @@ __global__ __launch_bounds__(64 * NW) void proj_mfma_kernel(ProjArgs a) {
 #pragma unroll
             for (int nb = 0; nb < NB; nb++) {
                 if constexpr (XH) {
-                    xq[j][nb] = *reinterpret_cast<const uint4*>(xh + xoff[nb] + k);
+                    xq[j][nb] = *reinterpret_cast<const uint4*>(xh + xoff[nb] + (XT ? 16L * k : k));
                 } else {
                     xr[j][nb][0] = *reinterpret_cast<const float4*>(xf + xoff[nb] + k);
                     xr[j][nb][1] = *reinterpret_cast<const float4*>(xf + xoff[nb] + k + 4);
@@ -268,6 +278,8 @@ __global__ __launch_bounds__(64 * NW) void proj_mfma_kernel(ProjArgs a) {
                         const float h = silu_ref(r16(gs[i])) * r16(us[i]);
                         if constexpr (EPI == kSwiGLU16)
                             a.y16[(long)b * a.ld_y + r + i] = __builtin_bit_cast(uint16_t, to_f16(h));
+                        else if constexpr (EPI == kSwiGLU16T)
+                            a.y16[tiled_index(b, (int)(r + i), a.out_dim)] = __builtin_bit_cast(uint16_t, to_f16(h));
                         else
                             a.y[(long)b * a.ld_y + r + i] = h;
                     }
@@ -826,11 +838,12 @@ __global__ __launch_bounds__(256) void tile_w16_kernel(uint16_t* dst, const uint
 }
 
 // ---- MFMA launch shapes -----------------------------------------------------
-template <bool XH, int NB, int RT, int R, bool NORM = false, int EPI = kStore, int NW = 4, bool TILED = false>
+template <bool XH, int NB, int RT, int R, bool NORM = false, int EPI = kStore, int NW = 4, bool TILED = false,
+          bool XT = false>
 void launch_mfma(const ProjArgs& a, hipStream_t st) {
     const int rows = 16 * (is_swiglu(EPI) ? 1 : RT);
     const dim3 grid((unsigned)((a.out_dim + rows - 1) / rows), (unsigned)((a.batch + 16 * NB - 1) / (16 * NB)));
-    proj_mfma_kernel<XH, NB, RT, R, NORM, EPI, NW, TILED><<<grid, dim3(64 * NW), 0, st>>>(a);
+    proj_mfma_kernel<XH, NB, RT, R, NORM, EPI, NW, TILED, XT><<<grid, dim3(64 * NW), 0, st>>>(a);
 }
 
 // Up to 16 rows: one 16-row batch block, one row tile per workgroup (the
@@ -935,13 +948,29 @@ void f32_fused(const ProjArgs& a, hipStream_t st) {
 // The SwiGLU past 32 rows takes all 64 batch rows of a workgroup (each
 // gate|up tile read by one workgroup): 9.8 us against 11.8 us with 32 at the
 // Qwen3-0.6B shape and 64 rows; the other shapes measured no better so.
-template <int EPI, bool TILED = false>
+// Shapes on fp16 x (every one 4 waves splitting the input steps, so every
+// shape gives the same bits).  Up to 16 rows: one 16-row batch block, one row
+// tile per workgroup, 8 steps of loads in flight per wave.  Past 16 rows
+// (measured at 64 rows on the Qwen3-0.6B layer shapes): the SwiGLU's gate|up
+// tile pairs take all 64 batch rows of a workgroup with 8 steps in flight;
+// shapes with many output tiles take 32 x 32 tiles; the others 16 x 16 tiles
+// with a wave's whole share of the input steps (up to 24) in flight at once.
+template <int EPI, bool TILED = false, bool XT = false>
 void x16_mfma(const ProjArgs& a, hipStream_t st) {
     const long tiles16 = (long)((a.out_dim + 15) / 16) * ((a.batch + 15) / 16);
     constexpr int RT = is_swiglu(EPI) ? 2 : 1;
-    if (a.batch <= 16 || (!is_swiglu(EPI) && tiles16 < 512)) launch_mfma<true, 1, RT, 8, false, EPI, 4, TILED>(a, st);
-    else if (is_swiglu(EPI) && a.batch > 32) launch_mfma<true, 4, 2, 4, false, EPI, 4, TILED>(a, st);
-    else launch_mfma<true, 2, 2, 8, false, EPI, 4, TILED>(a, st);
+    const int steps = a.in_dim / 32 / 4;   // per wave
+    if (a.batch <= 16) {
+        launch_mfma<true, 1, RT, 8, false, EPI, 4, TILED, XT>(a, st);
+    } else if constexpr (is_swiglu(EPI)) {
+        if (a.batch > 32) launch_mfma<true, 4, 2, 8, false, EPI, 4, TILED, XT>(a, st);
+        else launch_mfma<true, 2, 2, 8, false, EPI, 4, TILED, XT>(a, st);
+    } else {
+        if (tiles16 >= 512) launch_mfma<true, 2, 2, 8, false, EPI, 4, TILED, XT>(a, st);
+        else if (steps > 16) launch_mfma<true, 1, 1, 24, false, EPI, 4, TILED, XT>(a, st);
+        else if (steps > 8) launch_mfma<true, 1, 1, 16, false, EPI, 4, TILED, XT>(a, st);
+        else launch_mfma<true, 1, 1, 8, false, EPI, 4, TILED, XT>(a, st);
+    }
 }
 
 template <int EPI>
@@ -1038,6 +1067,44 @@ extern "C" int anelm_proj_f16_x16_tiled(void* y, const uint16_t* x16, const uint
         default: x16_mfma<kStore16, true>(a, st); break;
     }
     return launch_status("proj_f16_x16_tiled");
+}
+
+extern "C" int anelm_proj_f16_tt(void* y, const uint16_t* x_t, const uint16_t* w_t, long batch, int out_dim,
+                                 int in_dim, long ld_y, int epilogue, void* stream) {
+    clear_error();
+    const char* fn = "proj_f16_tt";
+    if (!y || !x_t || !w_t) return fail(ANELM_ERR_INVALID, "%s: null pointer", fn);
+    if (!sizes_ok(batch, out_dim, in_dim, in_dim, ld_y) || in_dim % 32 != 0)
+        return fail(ANELM_ERR_INVALID, "%s: bad sizes or strides (in_dim a multiple of 32)", fn);
+    if (!aligned16(x_t) || !aligned16(w_t)) return fail(ANELM_ERR_INVALID, "%s: needs 16-byte aligned x and W", fn);
+    if (epilogue < ANELM_PROJ_STORE || epilogue > ANELM_PROJ_SWIGLU_F16_TILED)
+        return fail(ANELM_ERR_INVALID, "%s: unknown epilogue %d", fn, epilogue);
+    const bool swiglu = epilogue == ANELM_PROJ_SWIGLU || epilogue == ANELM_PROJ_SWIGLU_F16 ||
+                        epilogue == ANELM_PROJ_SWIGLU_F16_TILED;
+    if (swiglu && out_dim % 16 != 0)
+        return fail(ANELM_ERR_INVALID, "%s: the SwiGLU needs out_dim (gate rows) a multiple of 16", fn);
+    if (epilogue == ANELM_PROJ_SWIGLU_F16_TILED && (out_dim % 32 != 0 || !aligned16(y)))
+        return fail(ANELM_ERR_INVALID, "%s: the tiled output needs out_dim a multiple of 32 and 16-byte alignment", fn);
+    // x_t holds ceil(batch/16)*16 rows; y its rows (or, tiled, as many padded rows)
+    const long xrows = (batch + 15) / 16 * 16;
+    const int ybytes = epilogue == ANELM_PROJ_STORE_F16 || epilogue == ANELM_PROJ_SWIGLU_F16 ? 2 : 4;
+    const bool ytiled = epilogue == ANELM_PROJ_SWIGLU_F16_TILED;
+    if (ytiled ? overlaps(y, out_dim, out_dim, 2, x_t, in_dim, in_dim, 2, xrows)
+               : overlaps(y, ld_y, out_dim, ybytes, x_t, in_dim, in_dim, 2, xrows))
+        return fail(ANELM_ERR_INVALID, "%s: y overlaps x (y is written while x is still read)", fn);
+    ProjArgs a = args(static_cast<float*>(y), x_t, w_t, batch, out_dim, in_dim, in_dim, ytiled ? out_dim : ld_y);
+    a.y16 = static_cast<uint16_t*>(y);
+    a.pair_rows = out_dim;
+    hipStream_t st = as_stream(stream);
+    switch (epilogue) {
+        case ANELM_PROJ_STORE: x16_mfma<kStore, true, true>(a, st); break;
+        case ANELM_PROJ_ADD: x16_mfma<kAdd, true, true>(a, st); break;
+        case ANELM_PROJ_SWIGLU: x16_mfma<kSwiGLU, true, true>(a, st); break;
+        case ANELM_PROJ_SWIGLU_F16: x16_mfma<kSwiGLU16, true, true>(a, st); break;
+        case ANELM_PROJ_STORE_F16: x16_mfma<kStore16, true, true>(a, st); break;
+        default: x16_mfma<kSwiGLU16T, true, true>(a, st); break;
+    }
+    return launch_status(fn);
 }
 
 // Decode-step projections with the neighbouring layer ops fused in, for up

@@ -203,8 +203,9 @@ extern "C" anelm_qwen3* anelm_qwen3_load(const char* path, const anelm_qwen3_con
     ALLOC(m->o, float, B * H);
     ALLOC(m->gu, float, B * 2 * I);
     ALLOC(m->h, float, B * I);
-    ALLOC(m->a16, uint16_t, B * amax);
-    ALLOC(m->y16, uint16_t, B * std::max({(long)m->qkvdim, 2 * I, H}));
+    const long Bp = (B + 15) / 16 * 16;   // whole 16-row tiles for the tiled activations
+    ALLOC(m->a16, uint16_t, Bp * amax);
+    ALLOC(m->y16, uint16_t, Bp * std::max({(long)m->qkvdim, 2 * I, H}));
 #undef ALLOC
     // Past 16 sequences the LM head streams a tiled copy of its W (1 KB per
     // load instruction) through the LDS kernel; made once here.
@@ -222,7 +223,7 @@ extern "C" anelm_qwen3* anelm_qwen3_load(const char* path, const anelm_qwen3_con
     }
     // Past 16 sequences the layer projections read tiled copies too (each
     // weight load instruction 1 KB in a row; the row-major weights stay for
-    // steps of up to 16 sequences)
+    // steps of up to 16 sequences), and their fp16 inputs are tiled as well
     if (B > 16 && H % 32 == 0 && I % 32 == 0 && m->qdim % 32 == 0) {
         for (anelm_qwen3::Layer& l : m->layers) {
             struct Tile {
@@ -318,28 +319,24 @@ extern "C" int anelm_qwen3_forward(anelm_qwen3* m, const int32_t* ids, const int
     CK(anelm_kv_ring_advance(m->ring_start, m->ring_len, B, c.layers, m->max_batch, m->cap, stream));  // :475-484
     const bool dims32 = H % 32 == 0 && I % 32 == 0 && m->qdim % 32 == 0;
     if (dims32 && B > 16) {
-        // Past 16 rows the RMSNorms round their output to fp16 once
-        // (anelm_rmsnorm_f16) and the projections read fp16 rows; the SwiGLU
-        // writes the down projection's fp16 input and the residual adds ride
-        // in the o and down projections: 7 calls per layer
-        // fp16 rows x16 [B, n_in] (row stride n_in) through W, tiled where the
-        // load made the copy
-        auto proj16 = [&](void* y, const uint16_t* x16, const uint16_t* w, const uint16_t* wt, long n_out, long n_in,
-                          long ld_y, int epilogue) -> int {
-            if (wt)
-                return anelm_proj_f16_x16_tiled(y, x16, wt, B, (int)n_out, (int)n_in, n_in, ld_y, epilogue, stream);
-            return anelm_proj_f16_x16_fused(y, x16, w, B, (int)n_out, (int)n_in, n_in, ld_y, epilogue, stream);
-        };
+        // Past 16 rows every projection input is fp16 in the tiled layout
+        // (16 rows x 32 columns per contiguous 1 KB piece), as are the
+        // weights (made at load): the RMSNorms round their output to fp16
+        // once, the attention writes the o projection's input and the SwiGLU
+        // the down projection's; the residual adds ride in the o and down
+        // projections.  7 calls per layer.
+        if (!m->layers.empty() && !m->layers[0].qkv_t) return fail(ANELM_ERR_INVALID, "qwen3_forward: no tiled weights");
         for (int L = 0; L < c.layers; L++) {
             const anelm_qwen3::Layer& l = m->layers[L];
-            CK(anelm_rmsnorm_f16(m->a16, m->x, l.w_in, ANELM_BF16, B, (int)H, H, H, c.rms_eps, stream));  // :503
-            CK(proj16(m->qkv, m->a16, l.qkv16, l.qkv_t, m->qkvdim, H, m->qkvdim, ANELM_PROJ_STORE));      // first_proj
-            // the attention writes the o projection's fp16 input (y16 is free until the SwiGLU)
-            CK(attend(l, m->y16, 1));                                                             // :444-490
-            CK(proj16(m->x, m->y16, l.o16, l.o_t, H, m->qdim, H, ANELM_PROJ_ADD));               // o_proj + :516
-            CK(anelm_rmsnorm_f16(m->a16, m->x, l.w_post, ANELM_BF16, B, (int)H, H, H, c.rms_eps, stream));  // :518
-            CK(proj16(m->y16, m->a16, l.gu16, l.gu_t, I, H, I, ANELM_PROJ_SWIGLU_F16));          // fused_ffn
-            CK(proj16(m->x, m->y16, l.down16, l.down_t, H, I, H, ANELM_PROJ_ADD));               // down + :527
+            CK(anelm_rmsnorm_f16_tiled(m->a16, m->x, l.w_in, ANELM_BF16, B, (int)H, H, c.rms_eps, stream));  // :503
+            CK(anelm_proj_f16_tt(m->qkv, m->a16, l.qkv_t, B, m->qkvdim, (int)H, m->qkvdim, ANELM_PROJ_STORE,
+                                 stream));                                                        // first_proj
+            CK(attend(l, m->y16, 2));                                                             // :444-490
+            CK(anelm_proj_f16_tt(m->x, m->y16, l.o_t, B, (int)H, m->qdim, H, ANELM_PROJ_ADD, stream));  // o_proj + :516
+            CK(anelm_rmsnorm_f16_tiled(m->a16, m->x, l.w_post, ANELM_BF16, B, (int)H, H, c.rms_eps, stream));  // :518
+            CK(anelm_proj_f16_tt(m->y16, m->a16, l.gu_t, B, (int)I, (int)H, I, ANELM_PROJ_SWIGLU_F16_TILED,
+                                 stream));                                                        // fused_ffn
+            CK(anelm_proj_f16_tt(m->x, m->y16, l.down_t, B, (int)H, (int)I, H, ANELM_PROJ_ADD, stream));  // down + :527
         }
         CK(anelm_rmsnorm_f16(m->a16, m->x, m->final_norm, ANELM_BF16, B, (int)H, H, H, c.rms_eps, stream));  // :530
         // the LM head (a 151936-row W streams once through the LDS-staged

@@ -77,6 +77,15 @@ int anelm_rmsnorm(float* out, const float* x, const void* w, int w_dtype, long r
  * No counterpart in the reference. */
 int anelm_rmsnorm_f16(uint16_t* out16, const float* x, const void* w, int w_dtype, long rows, int dim, long ld_x,
                       long ld_out, float eps, void* stream);
+/* anelm_rmsnorm_f16 with out_t in the tiled layout of anelm_proj_tile_f16
+ * (rows of x as its rows, dim a multiple of 32): for each 16-row tile and
+ * 32-column step, the 16 x 32 block as one contiguous 1 KB piece; rows past
+ * `rows` in the last tile are left as they are.  out_t holds
+ * anelm_proj_tiled_size(rows, dim) bytes, 16-byte aligned; x 16-byte
+ * aligned, ld_x a multiple of 4.  The same fp16 values as anelm_rmsnorm_f16:
+ * the input of anelm_proj_f16_tt.  No counterpart in the reference. */
+int anelm_rmsnorm_f16_tiled(uint16_t* out_t, const float* x, const void* w, int w_dtype, long rows, int dim,
+                            long ld_x, float eps, void* stream);
 /* Fused residual add + RMSNorm:  x[r,:] += y[r,:];  out[r,:] = rmsnorm(x[r,:]).
  * Replaces the pair vDSP_vadd(x_, attn_out, x_) + rmsnorm(x_norm_, x_, ...)
  * of models/llm/qwen3.cpp:516-518.  y may equal out (the reference's
@@ -318,7 +327,10 @@ int anelm_gqa_attention_f16(uint16_t* out16, const float* q, const float* k_cach
  * row itself.  No counterpart in the reference. */
 int anelm_kv_ring_advance(int32_t* ring_start, int32_t* ring_len, long batch, int groups, long group_stride,
                           int capacity, void* stream);
-/* anelm_qknorm_rope_append then anelm_gqa_attention (or _f16, out_f16 != 0)
+/* anelm_qknorm_rope_append then anelm_gqa_attention (out_f16 = 0), or
+ * anelm_gqa_attention_f16 (out_f16 = 1; with out_f16 = 2 the fp16 outputs in
+ * the tiled layout of anelm_proj_tile_f16 with n_heads*128 columns, out
+ * 16-byte aligned, out_ld unused: the input of anelm_proj_f16_tt),
  * in one launch, head_dim 128, for rings that anelm_kv_ring_advance has
  * already advanced: the new row's slot is (start + len - 1) mod capacity.
  * q (q + b*q_ld, n_heads heads 128 apart), k and v (k + b*k_ld, v + b*v_ld,
@@ -559,6 +571,19 @@ size_t anelm_proj_tiled_size(int out_dim, int in_dim);
 int anelm_proj_tile_f16(uint16_t* w_tiled, const uint16_t* w16, int out_dim, int in_dim, void* stream);
 int anelm_proj_f16_x16_tiled(void* y, const uint16_t* x16, const uint16_t* w_tiled, long batch, int out_dim,
                              int in_dim, long ld_x, long ld_y, int epilogue, void* stream);
+/* anelm_proj_f16_x16_tiled with x in the tiled layout too (x_t: batch rows,
+ * in_dim columns, from anelm_rmsnorm_f16_tiled, anelm_gqa_attention_qk with
+ * out_f16 = 2 or a previous ANELM_PROJ_SWIGLU_F16_TILED), so that every
+ * activation load also reads 1 KB in a row.  Every epilogue of
+ * anelm_proj_f16_x16_tiled, plus ANELM_PROJ_SWIGLU_F16_TILED: the fp16
+ * SwiGLU result written in the tiled layout (batch rows, out_dim columns, a
+ * multiple of 32; ld_y unused), the input of the next anelm_proj_f16_tt.
+ * The MFMA kernels of anelm_proj_f16_x16_fused on the same operands: outputs
+ * bit-identical to it past 16 rows.  x_t and W 16-byte aligned, in_dim a
+ * multiple of 32.  No counterpart in the reference. */
+#define ANELM_PROJ_SWIGLU_F16_TILED 5
+int anelm_proj_f16_tt(void* y, const uint16_t* x_t, const uint16_t* w_t, long batch, int out_dim, int in_dim,
+                      long ld_y, int epilogue, void* stream);
 
 /* Qwen3 model shape (the config.json fields of models/llm/qwen3.cpp:55-80);
  * head_dim must be 128 (every Qwen3 size). */
