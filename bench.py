@@ -757,7 +757,7 @@ def _csv_rows(d, suffix):
     return rows
 
 
-ATTN_KERNELS = {"gqa_decode": ("gqa_decode_kernel", ""), "gqa_combine": ("gqa_combine_kernel", "")}
+ATTN_KERNELS = {"gqa_decode": ("gqa_decode_kernel", "")}
 
 
 SAMPLE_KERNELS = {"stage1": ("sample_stage1_kernel", ""), "stage2": ("sample_stage2_kernel", ""),
@@ -765,18 +765,23 @@ SAMPLE_KERNELS = {"stage1": ("sample_stage1_kernel", ""), "stage2": ("sample_sta
 SAMPLER = "sampling-64x151936"
 
 # The 64-sequence decode step's LM head (x staged in LDS) and layer kernels
+# (tiled x and W: <fp16 x, batch tiles, row tiles, steps in flight, norm,
+# epilogue, waves, tiled W, tiled x>)
 Q3_B64 = "qwen3-0.6b-decode-step-b64"
 Q3_B64_KERNELS = {"lm_head": ("proj_lds_kernel", ""), "attention": ("gqa_decode_kernel", ""),
-                  "merge": ("gqa_combine_kernel", ""), "norm_f16": ("rmsnorm_row_kernel", "false, true, "),
-                  "proj_add": ("proj_mfma_kernel", "false, 1, 4>"), "gate_up_swiglu": ("proj_mfma_kernel", "false, 3, 4>"),
-                  "qkv": ("proj_mfma_kernel", "false, 0, 4>")}
+                  "norm_f16_tiled": ("rmsnorm_row_kernel", "false, true, true, true>"),
+                  "qkv": ("proj_mfma_kernel", "<true, 2, 2, 8, false, 0, 4, true, true>"),
+                  "o_proj_add": ("proj_mfma_kernel", "<true, 1, 1, 16, false, 1, 4, true, true>"),
+                  "gate_up_swiglu": ("proj_mfma_kernel", "<true, 4, 2, 8, false, 5, 4, true, true>"),
+                  "down_add": ("proj_mfma_kernel", "<true, 1, 1, 24, false, 1, 4, true, true>")}
 
 # The one-sequence decode step's projections, told apart by their launch
-# shapes (rows per wave, chunks in flight, fused norm, epilogue)
+# shapes <rows of x, rows per wave, chunks in flight, x form (0 fp32, 1 fp32
+# through the fused RMSNorm, 2 fp16), epilogue>
 Q3_B1 = "qwen3-0.6b-decode-step-b1"
-Q3_KERNELS = {"qkv": ("proj_dot_kernel", "<1, 2, 2, true, 0>"), "o_proj": ("proj_dot_kernel", "<1, 1, 4, false, 1>"),
-              "gate_up": ("proj_dot_kernel", "<1, 1, 2, true, 2>"), "down": ("proj_dot_kernel", "<1, 1, 6, false, 1>"),
-              "lm_head": ("proj_dot_kernel", "<1, 4, 2, true, 0>")}
+Q3_KERNELS = {"qkv": ("proj_dot_kernel", "<1, 2, 2, 1, 0>"), "o_proj": ("proj_dot_kernel", "<1, 1, 4, 2, 1>"),
+              "gate_up": ("proj_dot_kernel", "<1, 1, 2, 1, 3>"), "down": ("proj_dot_kernel", "<1, 1, 6, 2, 1>"),
+              "lm_head": ("proj_dot_kernel", "<1, 4, 2, 1, 0>")}
 
 
 def q3_b1_bytes():
@@ -918,7 +923,7 @@ def pmc_summary(fetch_dir, write_dir, copy_fetch_dir, copy_write_dir, workload=H
     run_args = _run_args(workload)
     if workload in ATTN_WORKLOADS:
         w = ATTN_WORKLOADS[workload]
-        ob = {"gqa_decode": attn_bytes(w), "gqa_combine": 0}
+        ob = {"gqa_decode": attn_bytes(w)}
     elif workload == Q3_B1:
         ob = q3_b1_bytes()
     elif workload == Q3_B64:
