@@ -38,14 +38,15 @@ extern float eps, theta;
 
 // the fused decode step: one layer's device weights, caches and ring-state rows
 struct DeviceLayer {
-    const uint16_t *Wqkv, *Wo, *Wgu, *Wdown;   // fp16 projections
-    const uint16_t *g_in, *g_post, *g_q, *g_k; // bf16 gammas
+    const uint16_t *Wqkv, *Wo, *Wgu, *Wdown;       // fp16 projections
+    uint16_t *Wqkv_t, *Wo_t, *Wgu_t, *Wdown_t;     // the same, tiled (anelm_proj_tile_f16)
+    const uint16_t *g_in, *g_post, *g_q, *g_k;     // bf16 gammas
     float *kc, *vc;
     int32_t *start, *len;
 };
 extern DeviceLayer lw;
 extern int32_t *ring_start, *ring_len;   // [layers][max_batch]
-extern uint16_t *x16, *attn16, *h16;
+extern uint16_t *x16, *attn16, *h16;     // fp16 rows, or tiled past 16 sequences
 
 // the Qwen3.5 linear-attention layer (qwen3_5.cpp:513-549), shown for the
 // current layer L

@@ -24,8 +24,11 @@ def test_every_documented_call_compiles(tmp_path):
     ("k_cache[L], v_cache[L], kv_start[L], kv_len[L], B, nq, nk, 128,",
      "kv_start[L], kv_len[L], k_cache[L], v_cache[L], B, nq, nk, 128,"),
     # an argument dropped from the fused projection
-    ("anelm_proj_f16_fused(x, h, lw.Wdown, B, H, I, I, H, NULL, 0, ANELM_PROJ_ADD, s);",
-     "anelm_proj_f16_fused(x, h, lw.Wdown, B, H, I, I, H, NULL, ANELM_PROJ_ADD, s);"),
+    ("anelm_proj_f16_x16_fused(x, h16, lw.Wdown, B, H, I, I, H, ANELM_PROJ_ADD, s);",
+     "anelm_proj_f16_x16_fused(x, h16, lw.Wdown, B, H, I, I, ANELM_PROJ_ADD, s);"),
+    # an argument dropped from the tiled projection
+    ("anelm_proj_f16_tt(x, h16, lw.Wdown_t, B, H, I, H, ANELM_PROJ_ADD, s);",
+     "anelm_proj_f16_tt(x, h16, lw.Wdown_t, B, H, I, ANELM_PROJ_ADD, s);"),
 ])
 def test_planted_mistake_fails(tmp_path, good, bad):
     md = open(integration_doc.DOC, encoding="utf-8").read()
