@@ -793,6 +793,23 @@ def q3_b1_bytes():
             "down": 2 * H * I, "lm_head": 2 * c["vocab"] * H}
 
 
+def q3_b64_bytes(B=64):
+    """Algorithmic bytes per dispatch of the 64-sequence step's kernels: fp16
+    weights once, fp16 inputs once, outputs written once (read too for the
+    residual adds); the attention's K/V rows depend on the ring lengths and
+    are not counted here."""
+    c = Q3_06B
+    H, I, qd = c["hidden"], c["intermediate"], c["n_q_heads"] * D
+    qkvd = qd + 2 * c["n_kv_heads"] * D
+    return {"lm_head": 2 * c["vocab"] * H + B * H * 2 + B * c["vocab"] * 4,
+            "attention": 0,
+            "norm_f16_tiled": B * H * 4 + B * H * 2,
+            "qkv": 2 * qkvd * H + B * H * 2 + B * qkvd * 4,
+            "o_proj_add": 2 * H * qd + B * qd * 2 + 2 * B * H * 4,
+            "gate_up_swiglu": 2 * 2 * I * H + B * H * 2 + B * I * 2,
+            "down_add": 2 * H * I + B * I * 2 + 2 * B * H * 4}
+
+
 def _kernels_of(workload):
     if workload == SAMPLER:
         return SAMPLE_KERNELS
@@ -927,9 +944,7 @@ def pmc_summary(fetch_dir, write_dir, copy_fetch_dir, copy_write_dir, workload=H
     elif workload == Q3_B1:
         ob = q3_b1_bytes()
     elif workload == Q3_B64:
-        c = Q3_06B
-        ob = {k: 0 for k in Q3_B64_KERNELS}
-        ob["lm_head"] = 2 * c["vocab"] * c["hidden"] + 64 * c["vocab"] * 4   # fp16 W once + fp32 logits
+        ob = q3_b64_bytes()
     elif workload == SAMPLER:
         # stage 1 reads the logits; stage 2 reads them again and writes exp(x - max)
         # into the probability buffer; stage 3 reads that and writes the probabilities
