@@ -5,8 +5,9 @@
 // rounded as written, because the probabilities must be bit-identical to
 // the sequential reference formula for the sampled ids to match.
 //
-// Pipeline per call (rows x vocab; chunks of kCH = 4096 logits, sub-tiles of
-// kSub = 256):
+// Pipeline per call (rows x vocab; chunks of K slices of 1024 logits, K = 4
+// unless the call has too few rows to fill the GPU with such chunks, then
+// K = 1; sub-tiles of kSub = 256):
 //   stage1  grid (chunks, rows): penalties + 1/T, per-chunk max (or argmax)
 //   stage2  grid (chunks, rows): e = exp(x - rowmax) into the probability
 //           buffer, exact fixed-point chunk sums
@@ -28,8 +29,8 @@
 
 namespace anelm {
 
-constexpr int kCH = 4096;   // logits per chunk (stage workgroup)
-constexpr int kSub = 256;   // logits per walk sub-tile: one wave's part of a k-slice of a chunk
+constexpr int kSlice = 1024;  // logits per k-slice: 4 per thread of a 256-thread workgroup
+constexpr int kSub = 256;     // logits per walk sub-tile: one wave's part of a k-slice of a chunk
 
 struct SampleArgs {
     const float* logits;
@@ -144,14 +145,15 @@ __device__ __forceinline__ float adjust(float l, uint32_t n, const SampleArgs& a
     return l;
 }
 
-// The 16 adjusted logits of this thread in place (the element order of
-// load_chunk16); the counts come in four 16-byte LDS reads before any use.
-__device__ __forceinline__ void adjust16(float v[16], const uint32_t* cnt, const SampleArgs& a) {
-    uint4 n[4];
+// The 4K adjusted logits of this thread in place (the element order of
+// load_chunk); the counts come in K 16-byte LDS reads before any use.
+template <int K>
+__device__ __forceinline__ void adjust_k(float v[4 * K], const uint32_t* cnt, const SampleArgs& a) {
+    uint4 n[K];
 #pragma unroll
-    for (int k = 0; k < 4; k++) n[k] = *reinterpret_cast<const uint4*>(cnt + k * 1024 + 4 * threadIdx.x);
+    for (int k = 0; k < K; k++) n[k] = *reinterpret_cast<const uint4*>(cnt + k * kSlice + 4 * threadIdx.x);
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
+    for (int k = 0; k < K; k++) {
         v[4 * k] = adjust(v[4 * k], n[k].x, a);
         v[4 * k + 1] = adjust(v[4 * k + 1], n[k].y, a);
         v[4 * k + 2] = adjust(v[4 * k + 2], n[k].z, a);
@@ -159,18 +161,19 @@ __device__ __forceinline__ void adjust16(float v[16], const uint32_t* cnt, const
     }
 }
 
-// The 16 logits of thread tid in chunk c0 (4 float4 slots k*1024 + 4*tid).
+// The 4K logits of thread tid in chunk c0 (K float4 slots k*1024 + 4*tid).
 // A whole chunk of an aligned row (every chunk but a row's last) takes one
-// uniform branch with its four 16-byte loads in flight together; per-lane
+// uniform branch with its K 16-byte loads in flight together; per-lane
 // conditions around each load made the compiler wait for each one before
 // issuing the next.
-__device__ __forceinline__ void load_chunk16(float v[16], const float* row_ptr, long c0, long vocab, bool vec) {
-    if (vec && c0 + kCH <= vocab) {
-        float4 f[4];
+template <int K>
+__device__ __forceinline__ void load_chunk(float v[4 * K], const float* row_ptr, long c0, long vocab, bool vec) {
+    if (vec && c0 + K * kSlice <= vocab) {
+        float4 f[K];
 #pragma unroll
-        for (int k = 0; k < 4; k++) f[k] = ld_nt(reinterpret_cast<const float4*>(row_ptr + c0 + k * 1024 + 4 * threadIdx.x));
+        for (int k = 0; k < K; k++) f[k] = ld_nt(reinterpret_cast<const float4*>(row_ptr + c0 + k * kSlice + 4 * threadIdx.x));
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
+        for (int k = 0; k < K; k++) {
             v[4 * k] = f[k].x;
             v[4 * k + 1] = f[k].y;
             v[4 * k + 2] = f[k].z;
@@ -179,8 +182,8 @@ __device__ __forceinline__ void load_chunk16(float v[16], const float* row_ptr, 
         return;
     }
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
-        const long i = c0 + k * 1024 + 4 * threadIdx.x;
+    for (int k = 0; k < K; k++) {
+        const long i = c0 + k * kSlice + 4 * threadIdx.x;
         if (vec && i + 3 < vocab) {
             const float4 f = ld_nt(reinterpret_cast<const float4*>(row_ptr + i));
             v[4 * k] = f.x;
@@ -422,25 +425,26 @@ __device__ __forceinline__ Fn compose4_scan(const Fn f[4]) {
 }
 
 // ---- stage 1: penalties, 1/T, chunk max (T > 0) or chunk argmax (T <= 0) ----
-template <bool ARGMAX>
+template <bool ARGMAX, int K>
 __global__ __launch_bounds__(256) void sample_stage1_kernel(SampleArgs a, int vec) {
+    constexpr int kCH = K * kSlice;
     __shared__ __align__(16) uint32_t cnt[kCH];
     __shared__ float red_v[4];
     __shared__ int red_i[4];
     const long row = blockIdx.y;
     const long c0 = (long)blockIdx.x * kCH;
-    float v[16];
-    load_chunk16(v, a.logits + row * a.ld_logits, c0, a.vocab, vec != 0);
+    float v[4 * K];
+    load_chunk<K>(v, a.logits + row * a.ld_logits, c0, a.vocab, vec != 0);
     build_counts(cnt, kCH, a, row, c0);
-    adjust16(v, cnt, a);
+    adjust_k<K>(v, cnt, a);
     const int nvalid = a.vocab - c0 < kCH ? (int)(a.vocab - c0) : kCH;
     float best = -INFINITY;
     int besti = INT_MAX;
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
+    for (int k = 0; k < K; k++) {
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-            const int li = k * 1024 + 4 * threadIdx.x + e;
+            const int li = k * kSlice + 4 * threadIdx.x + e;
             const float x = v[4 * k + e];
             if (ARGMAX) {
                 // first index of the maximum among non-NaN values
@@ -533,18 +537,20 @@ __global__ __launch_bounds__(64) void sample_argmax_final_kernel(SampleArgs a) {
 // the probability buffer (in place over the logits for softmax: every
 // workgroup reads its own chunk before writing it), where stage 3 scales them
 // into probabilities without recomputing them.
+template <int K>
 __global__ __launch_bounds__(256) void sample_stage2_kernel(SampleArgs a, int vec, int vec_out) {
+    constexpr int kCH = K * kSlice;
     __shared__ __align__(16) uint32_t cnt[kCH];
     __shared__ float red[4];
     __shared__ uint64_t red_s[4];
     __shared__ int red_f[4];
     const long row = blockIdx.y;
     const long c0 = (long)blockIdx.x * kCH;
-    float v[16];
-    load_chunk16(v, a.logits + row * a.ld_logits, c0, a.vocab, vec != 0);
+    float v[4 * K];
+    load_chunk<K>(v, a.logits + row * a.ld_logits, c0, a.vocab, vec != 0);
     const float mshare = max_share(a, row);
     build_counts(cnt, kCH, a, row, c0);
-    adjust16(v, cnt, a);
+    adjust_k<K>(v, cnt, a);
     const int nvalid = a.vocab - c0 < kCH ? (int)(a.vocab - c0) : kCH;
     const float neg = -reduce_max(mshare, red);
     const float scale = ldexpf(1.0f, a.shift);
@@ -555,7 +561,7 @@ __global__ __launch_bounds__(256) void sample_stage2_kernel(SampleArgs a, int ve
         // a whole chunk: no per-element bounds (a guard per element compiled
         // to an exec-mask branch per element)
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
+        for (int k = 0; k < K; k++) {
             float ev[4];
 #pragma unroll
             for (int e = 0; e < 4; e++) {
@@ -566,22 +572,22 @@ __global__ __launch_bounds__(256) void sample_stage2_kernel(SampleArgs a, int ve
                 nan |= ok ? 0 : 1;
             }
             // cached store: stage 3 reads these back
-            *reinterpret_cast<float4*>(out + c0 + k * 1024 + 4 * threadIdx.x) = make_float4(ev[0], ev[1], ev[2], ev[3]);
+            *reinterpret_cast<float4*>(out + c0 + k * kSlice + 4 * threadIdx.x) = make_float4(ev[0], ev[1], ev[2], ev[3]);
         }
     } else {
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
+    for (int k = 0; k < K; k++) {
         float ev[4];
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-            const int li = k * 1024 + 4 * threadIdx.x + e;
+            const int li = k * kSlice + 4 * threadIdx.x + e;
             const float x = li < nvalid ? sampler_expf(v[4 * k + e] + neg) : 0.0f;
             ev[e] = x;
             const bool ok = x >= 0.0f && x <= 1.0f;
             acc += ok ? (uint64_t)(x * scale) : 0u;
             nan |= ok ? 0 : 1;
         }
-        const long i = c0 + k * 1024 + 4 * threadIdx.x;
+        const long i = c0 + k * kSlice + 4 * threadIdx.x;
         if (vec_out && i + 3 < a.vocab) {  // cached store: stage 3 reads these back
             *reinterpret_cast<float4*>(out + i) = make_float4(ev[0], ev[1], ev[2], ev[3]);
         } else {
@@ -696,16 +702,18 @@ __device__ bool walk_first_lds(const float* sp, long V, float r, uint32_t& cb, l
 
 // ---- stage 3: probabilities and sub-tile maps --------------------------------
 // Wave w's part of k-slice k is the 256 consecutive logits c0 + k*1024 + w*256 +
-// [0, 256): sub-tile 16*chunk + 4k + w.  For each, the wave predicts the binade
+// [0, 256): sub-tile 4K*chunk + 4k + w.  For each, the wave predicts the binade
 // of the running sum at the sub-tile's start from the exact prefix of the
 // earlier chunks' sums plus this chunk's earlier sub-tile sums, and stores
 // the in-order composition of its elements' maps under that binade.  The walk
 // uses a map only if the actual running sum turns out to lie in that binade
 // and the map shows no element leaving it; otherwise it walks exactly.
+template <int K>
 __global__ __launch_bounds__(256) void sample_stage3_kernel(SampleArgs a, int vec_out) {
+    constexpr int kCH = K * kSlice;
     __shared__ uint64_t red_s[4], red_p[4];
     __shared__ int red_f[4];
-    __shared__ float ksum[4][4];  // [k][wave] fp32 sums of exp (prediction only)
+    __shared__ float ksum[K][4];  // [k][wave] fp32 sums of exp (prediction only)
     __shared__ __align__(16) float s_first[kSub];  // sub-tile 0's probabilities for its one-lane walk
     // Workgroups in dispatch order take chunk 0 of every row first: those
     // also walk sub-tile 0 (below), the longest job, so it starts early.
@@ -714,17 +722,20 @@ __global__ __launch_bounds__(256) void sample_stage3_kernel(SampleArgs a, int ve
     const int chunk = (int)(lin / a.rows);
     const long c0 = (long)chunk * kCH;
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-    float v[16];  // exp(adjusted - max), as stage 2 stored them
-    load_chunk16(v, a.probs + row * a.ld_probs, c0, a.vocab, vec_out != 0);
+    // the draw is loaded with the exponentials (the first sub-tile's walk
+    // below compares against it), not behind them
+    const float rdraw = a.r ? a.r[row] : 0.0f;
+    float v[4 * K];  // exp(adjusted - max), as stage 2 stored them
+    load_chunk<K>(v, a.probs + row * a.ld_probs, c0, a.vocab, vec_out != 0);
     const SumShare share = sum_share(a, row, chunk);
     // 1/sum, and the exact prefix of the earlier chunks' sums (the prediction
     // of the running sum at this chunk's start)
     float inv, prefix;
     reduce_sums(share, a, red_s, red_p, red_f, inv, prefix);
-    float p[16];
+    float p[4 * K];
     float* out = a.probs + row * a.ld_probs;
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
+    for (int k = 0; k < K; k++) {
         float ks = 0.f;
 #pragma unroll
         for (int j = 0; j < 4; j++) {
@@ -734,7 +745,7 @@ __global__ __launch_bounds__(256) void sample_stage3_kernel(SampleArgs a, int ve
         }
         ks = wave_sum(ks);
         if (lane == 0) ksum[k][wid] = ks;
-        const long i = c0 + k * 1024 + 4 * threadIdx.x;
+        const long i = c0 + k * kSlice + 4 * threadIdx.x;
         if (vec_out && i + 3 < a.vocab) {  // cached store: the walk reads these back
             *reinterpret_cast<float4*>(out + i) = make_float4(p[4 * k], p[4 * k + 1], p[4 * k + 2], p[4 * k + 3]);
         } else {
@@ -760,20 +771,19 @@ __global__ __launch_bounds__(256) void sample_stage3_kernel(SampleArgs a, int ve
         if (lane == 0) {
             uint32_t cb = 0u;
             long result = -1;
-            const bool done = walk_first_lds(s_first, a.vocab, a.r[row], cb, result);
+            const bool done = walk_first_lds(s_first, a.vocab, rdraw, cb, result);
             a.ws_first[2 * row] = done ? (int32_t)result : -1;
             a.ws_first[2 * row + 1] = (int32_t)cb;
         }
         __builtin_amdgcn_s_setprio(0);
     }
-    const float rdraw = a.r ? a.r[row] : 0.0f;
     float run = prefix;  // running prediction, the same order of additions in every wave
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
+    for (int k = 0; k < K; k++) {
         float here = run;
         for (int w = 0; w < wid; w++) here = here + ksum[k][w];
         const float cpred = here * inv;
-        const long st = (long)chunk * 16 + 4 * k + wid;
+        const long st = (long)chunk * (4 * K) + 4 * k + wid;
         // No map where the walk does not arrive: without a draw (softmax), or
         // when the sub-tile is predicted to start more than skip_margin past
         // r (the sequential sum is within V * 2^-25 of the exact prefix, so
@@ -791,8 +801,8 @@ __global__ __launch_bounds__(256) void sample_stage3_kernel(SampleArgs a, int ve
         const bool ok = cpred == cpred && cpred < INFINITY;
         const int cls = ok ? (cb < 0x00800000u ? 0 : (int)(cb >> 23)) : -1;
         const Binade b = binade_of_class(ok ? cls : 0);
-        const int nv = a.vocab - (c0 + k * 1024 + 256 * wid) < kSub ? (int)(a.vocab - (c0 + k * 1024 + 256 * wid))
-                                                                     : kSub;  // valid elements of the sub-tile
+        const int nv = a.vocab - (c0 + k * kSlice + 256 * wid) < kSub ? (int)(a.vocab - (c0 + k * kSlice + 256 * wid))
+                                                                       : kSub;  // valid elements of the sub-tile
         Fn f[4];
 #pragma unroll
         for (int j = 0; j < 4; j++) {
@@ -935,9 +945,59 @@ __device__ __forceinline__ bool pass_crossing(uint32_t& cb, const uint32_t* x, i
 // when the draw is decided (result set), else sets cb to the running sum's
 // bits at the sub-tile's end.  Adding 0.0f for the padding past V leaves the
 // sum unchanged.
+// The 16 running sums after cum, in index order, and whether the draw ends
+// among them (result set).  One fp32 add per element, as the reference.
+__device__ __forceinline__ bool walk16(const float4 (&q)[4], int i, long V, float r, float& cum, long& result) {
+    float c[16];
+    float run = cum;
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        run = run + q[u].x;
+        c[4 * u] = run;
+        run = run + q[u].y;
+        c[4 * u + 1] = run;
+        run = run + q[u].z;
+        c[4 * u + 2] = run;
+        run = run + q[u].w;
+        c[4 * u + 3] = run;
+    }
+    if (!(c[15] < r)) {  // the draw ends in these 16, or the sum became NaN (cum never decreases)
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+            if (c[e] >= r) {
+                result = i + e;
+                return true;
+            }
+            if (c[e] != c[e]) {  // no later sum can reach r
+                result = V - 1;
+                return true;
+            }
+        }
+    }
+    cum = c[15];
+    return false;
+}
+
 __device__ bool walk_first_lds(const float* sp, long V, float r, uint32_t& cb, long& result) {
     const int nvalid = V < kSub ? (int)V : kSub;
     float cum = 0.0f;
+    if (nvalid == kSub) {
+        // a whole sub-tile: no per-element bounds, and the next 16
+        // probabilities are read from LDS while these 16 are added
+        float4 q[4], nq[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) q[u] = *reinterpret_cast<const float4*>(sp + 4 * u);
+        for (int i = 0; i < kSub; i += 16) {
+            const int n = i + 16 < kSub ? i + 16 : i;
+#pragma unroll
+            for (int u = 0; u < 4; u++) nq[u] = *reinterpret_cast<const float4*>(sp + n + 4 * u);
+            if (walk16(q, i, V, r, cum, result)) return true;
+#pragma unroll
+            for (int u = 0; u < 4; u++) q[u] = nq[u];
+        }
+        cb = __float_as_uint(cum);
+        return false;
+    }
     for (int i = 0; i < nvalid; i += 16) {
         float4 q[4];
 #pragma unroll
@@ -1134,8 +1194,18 @@ struct WsLayout {
 
 static size_t al16(size_t x) { return (x + 15) & ~(size_t)15; }
 
+// 1024-logit slices per chunk: 4, unless rows x chunks of 4096 would leave
+// most of the 256 CUs without a workgroup (a few rows), then 1: the stages'
+// per-wave work is a chain of dependent instructions over a thread's 4K
+// logits and a wave's K sub-tiles, so at one row smaller chunks finish
+// sooner.  The outputs do not depend on it.
+static int chunk_slices(long rows, long vocab) {
+    return rows * ((vocab + 4 * kSlice - 1) / (4 * kSlice)) < 256 ? 1 : 4;
+}
+
 static WsLayout ws_layout(long rows, long vocab) {
-    const size_t nch = (size_t)((vocab + kCH - 1) / kCH);
+    const long kch = (long)chunk_slices(rows, vocab) * kSlice;
+    const size_t nch = (size_t)((vocab + kch - 1) / kch);
     const size_t nsub = (size_t)((vocab + kSub - 1) / kSub);
     const size_t n = (size_t)rows * nch, ns = (size_t)rows * ((nsub + 3) & ~(size_t)3);
     WsLayout l;
@@ -1168,7 +1238,8 @@ static int bind_workspace(SampleArgs& a, void* ws, size_t ws_bytes, long rows, l
     a.ws_cls = reinterpret_cast<int32_t*>(b + l.off_cls);
     a.ws_xing = reinterpret_cast<uint32_t*>(b + l.off_x);
     a.ws_first = reinterpret_cast<int32_t*>(b + l.off_first);
-    a.nchunk = (int)((vocab + kCH - 1) / kCH);
+    const long kch = (long)chunk_slices(rows, vocab) * kSlice;
+    a.nchunk = (int)((vocab + kch - 1) / kch);
     a.nsub = (int)((vocab + kSub - 1) / kSub);
     a.nsub_ld = (a.nsub + 3) & ~3;
     a.shift = 63 - ceil_log2(vocab);
@@ -1213,9 +1284,15 @@ extern "C" int anelm_softmax(float* x, long rows, long n, long ld, void* workspa
     hipStream_t st = as_stream(stream);
     const int vec = (ld % 4 == 0) && aligned16(x);
     const dim3 grd((unsigned)a.nchunk, (unsigned)rows);
-    sample_stage1_kernel<false><<<grd, 256, 0, st>>>(a, vec);
-    sample_stage2_kernel<<<grd, 256, 0, st>>>(a, vec, vec);
-    sample_stage3_kernel<<<grd, 256, 0, st>>>(a, vec);
+    if (chunk_slices(rows, n) == 1) {
+        sample_stage1_kernel<false, 1><<<grd, 256, 0, st>>>(a, vec);
+        sample_stage2_kernel<1><<<grd, 256, 0, st>>>(a, vec, vec);
+        sample_stage3_kernel<1><<<grd, 256, 0, st>>>(a, vec);
+    } else {
+        sample_stage1_kernel<false, 4><<<grd, 256, 0, st>>>(a, vec);
+        sample_stage2_kernel<4><<<grd, 256, 0, st>>>(a, vec, vec);
+        sample_stage3_kernel<4><<<grd, 256, 0, st>>>(a, vec);
+    }
     return launch_status("softmax");
 }
 
@@ -1259,16 +1336,24 @@ int sample_impl(int32_t* ids, float* probs, long ld_probs, const float* logits, 
     hipStream_t st = as_stream(stream);
     const int vec = (ld_logits % 4 == 0) && aligned16(logits);
     const dim3 grd((unsigned)a.nchunk, (unsigned)rows);
+    const bool one = chunk_slices(rows, vocab) == 1;
     if (!sampling) {
-        sample_stage1_kernel<true><<<grd, 256, 0, st>>>(a, vec);
+        if (one) sample_stage1_kernel<true, 1><<<grd, 256, 0, st>>>(a, vec);
+        else sample_stage1_kernel<true, 4><<<grd, 256, 0, st>>>(a, vec);
         sample_argmax_final_kernel<<<dim3((unsigned)rows), 64, 0, st>>>(a);
         return launch_status("sample(argmax)");
     }
     const int vec_out = probs && (ld_probs % 4 == 0) && aligned16(probs);
     a.vec_probs = vec_out;
-    sample_stage1_kernel<false><<<grd, 256, 0, st>>>(a, vec);
-    sample_stage2_kernel<<<grd, 256, 0, st>>>(a, vec, vec_out);
-    sample_stage3_kernel<<<grd, 256, 0, st>>>(a, vec_out);
+    if (one) {
+        sample_stage1_kernel<false, 1><<<grd, 256, 0, st>>>(a, vec);
+        sample_stage2_kernel<1><<<grd, 256, 0, st>>>(a, vec, vec_out);
+        sample_stage3_kernel<1><<<grd, 256, 0, st>>>(a, vec_out);
+    } else {
+        sample_stage1_kernel<false, 4><<<grd, 256, 0, st>>>(a, vec);
+        sample_stage2_kernel<4><<<grd, 256, 0, st>>>(a, vec, vec_out);
+        sample_stage3_kernel<4><<<grd, 256, 0, st>>>(a, vec_out);
+    }
     sample_walk_kernel<<<dim3((unsigned)rows), 64, 0, st>>>(a);
     return launch_status("sample");
 }

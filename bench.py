@@ -288,27 +288,36 @@ def measure_chain(w, steps, warmup, per_op, chain_only=False):
     return r
 
 
-def measure_sampler(hip, steps, rows=64, vocab=VOCAB, freq=0.1):
+def measure_sampler(hip, steps, rows=64, vocab=VOCAB, freq=0.1, calls=8):
     """Logits [rows, 151936] ~N(0,3), history [rows, 256], rep 1.2, T 0.6,
-    freq 0.1 (the reference default) or as given."""
+    freq 0.1 (the reference default) or as given.  One graph holds `calls`
+    sampler calls on distinct logits and outputs (at 64 rows more than the
+    Infinity Cache holds), as a decode loop's graph would hold the sampler;
+    us is per call.  one_call_per_graph: the same with a graph launch per call."""
     import torch
 
     g = torch.Generator(device="cuda").manual_seed(21)
-    logits = 3.0 * torch.randn(rows, vocab, generator=g, device="cuda")
+    logits = [3.0 * torch.randn(rows, vocab, generator=g, device="cuda") for _ in range(calls)]
     hist = torch.randint(0, vocab, (rows, 256), generator=g, device="cuda", dtype=torch.int32)
-    r = torch.rand(rows, generator=g, device="cuda")
-    ids = torch.empty(rows, dtype=torch.int32, device="cuda")
-    probs = torch.empty(rows, vocab, device="cuda")
+    r = [torch.rand(rows, generator=g, device="cuda") for _ in range(calls)]
+    ids = torch.empty(calls, rows, dtype=torch.int32, device="cuda")
+    probs = [torch.empty(rows, vocab, device="cuda") for _ in range(calls)]
     ws = torch.empty(hip.sample_workspace_size(rows, vocab), dtype=torch.uint8, device="cuda")
     p = hip.SamplingParams(frequency_penalty=freq)
-    call = lambda: hip.sample(ids, probs, logits, hist, None, p, r, ws)
-    gr = capture(call)
-    gr.replay()
-    ms = time_region(gr.replay, steps)
     byt = 2 * rows * vocab * 4
+    out = {}
+    for n, key in ((calls, "many"), (1, "one")):
+        gr = capture(lambda: [hip.sample(ids[i], probs[i], logits[i], hist, None, p, r[i], ws) for i in range(n)])
+        gr.replay()
+        ms = time_region(gr.replay, steps) / n
+        out[key] = ms
+        del gr
+    ms = out["many"]
     return dict(us=round(ms * 1e3, 2), GBps=round(byt / ms / 1e6, 1), frac=round(byt / ms / 1e6 / HBM_PEAK_GBPS, 4),
-                rows_per_s=round(rows / (ms / 1e3), 1), bytes=byt,
-                note="algorithmic bytes = logits read once + probabilities written once")
+                rows_per_s=round(rows / (ms / 1e3), 1), bytes=byt, calls_per_graph=calls,
+                one_call_per_graph_us=round(out["one"] * 1e3, 2),
+                note="algorithmic bytes = logits read once + probabilities written once; us per call in a graph of "
+                     f"{calls} calls on distinct inputs (one_call_per_graph_us: a graph launch per call)")
 
 
 def measure_convert(hip, reps=3):

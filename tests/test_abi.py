@@ -130,6 +130,13 @@ def test_workspace_sizes(lib):
     n, ns = 64 * 38, 64 * 596
     assert lib.anelm_sample_workspace_size(64, 151936) == (al(n * 8) + 3 * al(n * 4) + 3 * al(ns * 4) + al(ns * 24)
                                                            + al(64 * 8))   # + sub-tile 0 result per row
+    # a few rows (rows x 38 chunks of 4096 < 256 workgroups): chunks of 1024, 149 per row
+    n, ns = 6 * 149, 6 * 596
+    assert lib.anelm_sample_workspace_size(6, 151936) == (al(n * 8) + 3 * al(n * 4) + 3 * al(ns * 4) + al(ns * 24)
+                                                          + al(6 * 8))
+    n, ns = 7 * 38, 7 * 596
+    assert lib.anelm_sample_workspace_size(7, 151936) == (al(n * 8) + 3 * al(n * 4) + 3 * al(ns * 4) + al(ns * 24)
+                                                          + al(7 * 8))
     assert lib.anelm_sample_workspace_size(0, 10) == 0
     assert lib.anelm_softmax_workspace_size(1, 4096) > 0
 
