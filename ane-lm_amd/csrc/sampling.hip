@@ -784,12 +784,13 @@ __global__ __launch_bounds__(256) void sample_stage3_kernel(SampleArgs a, int ve
         for (int w = 0; w < wid; w++) here = here + ksum[k][w];
         const float cpred = here * inv;
         const long st = (long)chunk * (4 * K) + 4 * k + wid;
-        // No map where the walk does not arrive: without a draw (softmax), or
+        // No map where the walk does not arrive: without a draw (softmax), for
+        // sub-tile 0 (walked exactly above; the walk starts after it), or
         // when the sub-tile is predicted to start more than skip_margin past
         // r (the sequential sum is within V * 2^-25 of the exact prefix, so
         // the draw has ended before it).  A wrong prediction costs the walk an
         // exact walk of the sub-tile (class -1, no crossing), never a result.
-        if (!a.r || cpred >= rdraw + a.skip_margin) {   // wave-uniform
+        if (!a.r || st == 0 || cpred >= rdraw + a.skip_margin) {  // wave-uniform
             if (a.r && lane == 63 && st < a.nsub) {
                 a.ws_cls[row * a.nsub_ld + st] = -1;
                 a.ws_xing[(row * a.nsub_ld + st) * kXWords + 5] = 0xFFFFFFFFu;
