@@ -70,15 +70,15 @@ struct SampleArgs {
 // ---- exp with a fixed IEEE operation sequence ----------------------------
 // Cody & Waite two-constant reduction (Software Manual for the Elementary
 // Functions, 1980), degree-7 Taylor polynomial by Horner with fused
-// multiply-adds, exact power-of-two scaling (two multiplies when the result
-// is subnormal so it is rounded once).  Every operation is a correctly
-// rounded IEEE operation, so the value is reproducible bit for bit on any
-// IEEE machine; it is within 1 ulp of exp.
-__device__ __forceinline__ float pow2i(int k) { return __uint_as_float((uint32_t)(k + 127) << 23); }
-
+// multiply-adds, power-of-two scaling rounded once.  Every operation is a
+// correctly rounded IEEE operation, so the value is reproducible bit for bit
+// on any IEEE machine; it is within 1 ulp of exp.
 __device__ __forceinline__ float sampler_expf(float x) {
-    // Straight-line: the special cases are selected at the end.  The clamp
-    // keeps the body finite (maxnum ignores a NaN); x itself decides.
+    // Straight-line.  The clamp keeps the body finite (maxnum ignores a NaN)
+    // and decides the ends: at -104, k = -150 and p = 0x1.f1e6b6p-1, so the
+    // scaling gives exactly +0 (0 for x < -104); at 89, k = 128 and
+    // p = 0x1.51c2ccp+0, so it gives +inf (inf for x > 89).  A NaN x is
+    // selected at the end.
     const float xc = fminf(fmaxf(x, -104.0f), 89.0f);
     const float kf = rintf(xc * 0x1.715476p+0f);
     const int k = (int)kf;
@@ -92,14 +92,10 @@ __device__ __forceinline__ float sampler_expf(float x) {
     p = fmaf(p, r, 0x1p-1f);
     p = fmaf(p, r, 1.0f);
     p = fmaf(p, r, 1.0f);
-    // p * 2^k in two exact-or-once-rounded multiplies, without a branch:
-    // k < -126: (p * 2^(k+64)) * 2^-64, rounded once as a subnormal;
-    // k > 127:  (p * 2^(k-1)) * 2;  otherwise (p * 2^k) * 1
-    const int ka = k < -126 ? k + 64 : (k > 127 ? k - 1 : k);
-    const float sa = k < -126 ? 0x1p-64f : (k > 127 ? 2.0f : 1.0f);
-    float y = (p * pow2i(ka)) * sa;
-    y = x < -104.0f ? 0.0f : y;
-    y = x > 89.0f ? INFINITY : y;
+    // p * 2^k rounded once (v_ldexp_f32 is the IEEE scaleB operation): the
+    // same value as (p * 2^(k+64)) * 2^-64 for subnormal results,
+    // (p * 2^(k-1)) * 2 above 2^127 and p * 2^k otherwise
+    const float y = ldexpf(p, k);
     return x != x ? x : y;
 }
 
@@ -154,6 +150,16 @@ __device__ __forceinline__ void adjust_k(float v[4 * K], const uint32_t* cnt, co
     for (int k = 0; k < K; k++) n[k] = *reinterpret_cast<const uint4*>(cnt + k * kSlice + 4 * threadIdx.x);
 #pragma unroll
     for (int k = 0; k < K; k++) {
+        // Most 256-logit slices of a wave hold no id of the window (256 ids
+        // in 151936): there only 1/T applies, adjust() with n = 0.  The
+        // branch is wave-uniform.
+        if (__ballot((n[k].x | n[k].y | n[k].z | n[k].w) != 0u) == 0) {
+            if (a.apply_temp) {
+#pragma unroll
+                for (int e = 0; e < 4; e++) v[4 * k + e] = v[4 * k + e] * a.inv_t;
+            }
+            continue;
+        }
         v[4 * k] = adjust(v[4 * k], n[k].x, a);
         v[4 * k + 1] = adjust(v[4 * k + 1], n[k].y, a);
         v[4 * k + 2] = adjust(v[4 * k + 2], n[k].z, a);
@@ -567,8 +573,8 @@ __global__ __launch_bounds__(256) void sample_stage2_kernel(SampleArgs a, int ve
             for (int e = 0; e < 4; e++) {
                 const float x = sampler_expf(v[4 * k + e] + neg);
                 ev[e] = x;
-                const bool ok = x >= 0.0f && x <= 1.0f;
-                acc += ok ? (uint64_t)(x * scale) : 0u;
+                const bool ok = x <= 1.0f;  // e >= 0 always; false for NaN and inf
+                acc += (uint64_t)(ok ? x * scale : 0.0f);
                 nan |= ok ? 0 : 1;
             }
             // cached store: stage 3 reads these back
@@ -583,8 +589,8 @@ __global__ __launch_bounds__(256) void sample_stage2_kernel(SampleArgs a, int ve
             const int li = k * kSlice + 4 * threadIdx.x + e;
             const float x = li < nvalid ? sampler_expf(v[4 * k + e] + neg) : 0.0f;
             ev[e] = x;
-            const bool ok = x >= 0.0f && x <= 1.0f;
-            acc += ok ? (uint64_t)(x * scale) : 0u;
+            const bool ok = x <= 1.0f;  // e >= 0 always; false for NaN and inf
+            acc += (uint64_t)(ok ? x * scale : 0.0f);
             nan |= ok ? 0 : 1;
         }
         const long i = c0 + k * kSlice + 4 * threadIdx.x;
@@ -906,33 +912,31 @@ __device__ void fill_walk_cache(WalkShared& sh, const SampleArgs& a, long row, i
 }
 
 // Pass a crossing sub-tile in O(1) from the exact running sum at its start
-// (bits cb, binade class ccls) with its stored crossing x, if every stored
-// prediction holds: the sum stays in its binade up to element j, leaves it
-// at j, the fp32 sum after j lies in the binade the suffix map was made for
-// and stays there, and no running sum reaches r.  Returns false (nothing
-// changed) otherwise; the caller then walks the sub-tile exactly.
-__device__ __forceinline__ bool pass_crossing(uint32_t& cb, const uint32_t* x, int pcls, float r) {
+// (bits cb) with its stored crossing x (the kXWords words) and predicted
+// class pcls, if every stored prediction holds: the sum starts in the binade
+// pre was made for and stays in it up to element j, leaves it at j, the fp32
+// sum after j lies in the binade the suffix map was made for and stays there,
+// and no running sum reaches r.  Returns false (nothing changed) otherwise;
+// the caller then walks the sub-tile exactly.  Straight-line: every check is
+// evaluated (on wave-uniform values) and decided once at the end.
+__device__ __forceinline__ bool pass_crossing(uint32_t& cb, const uint32_t (&x)[kXWords], int pcls, float r) {
     const int info = (int)x[5];
-    if (info < 0) return false;
     const Binade b = binade_of(__uint_as_float(cb));
-    if (b.cls != pcls) return false;  // pre was made under the predicted start binade
     const uint32_t inc = (b.m0 & 1u) ? x[1] : x[0];
-    if (!(inc < b.mhi - b.m0)) return false;  // leaves before element j
-    const uint32_t mb = b.m0 + inc;
-    if (!(ldexpf((float)mb, -b.sh) < r)) return false;  // the draw ends before j
+    const uint32_t mb = b.m0 + inc;  // m0 < 2^24, inc <= 2^30: no wrap
+    const float base = ldexpf((float)mb, -b.sh);
     const float pj = __uint_as_float(x[4]);
     const uint32_t incj = pick(elem_map(pj, b), mb);
-    if (incj < b.mhi - mb) return false;  // does not leave at j
-    const float c = ldexpf((float)mb, -b.sh) + pj;  // the reference's fp32 add of element j
-    if (!(c < r)) return false;                      // the draw ends at j (or NaN)
+    const float c = base + pj;  // the reference's fp32 add of element j
     const Binade b2 = binade_of(c);
-    if (b2.cls != (info >> 8)) return false;
     const uint32_t inc2 = (b2.m0 & 1u) ? x[3] : x[2];
-    if (!(inc2 < b2.mhi - b2.m0)) return false;  // leaves again
     const float end = ldexpf((float)(b2.m0 + inc2), -b2.sh);
-    if (!(end < r)) return false;  // the draw ends after j
-    cb = __float_as_uint(end);
-    return true;
+    const bool ok = (info >= 0) & (b.cls == pcls)                // a single crossing, made for this binade
+                    & (inc < b.mhi - b.m0) & (base < r)           // no leave and no hit before j
+                    & !(incj < b.mhi - mb) & (c < r)              // leaves at j; the draw does not end there (nor NaN)
+                    & (b2.cls == (info >> 8)) & (inc2 < b2.mhi - b2.m0) & (end < r);  // the rest stays, no hit
+    if (ok) cb = __float_as_uint(end);
+    return ok;
 }
 
 // Exact walk of sub-tile st from the running sum with bits cb.  Inside one
@@ -1144,6 +1148,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1))) void
     uint32_t cb = first_end;  // bits of the running sum
     long result = V - 1;
     long st = 1;
+    // every record of the row in LDS (V <= 2048 sub-tiles): each step reads
+    // its 64 sub-tiles' class, map and crossing in one round of LDS loads
+    const bool all_cached = a.nsub <= nxcache;
     while (st < a.nsub) {
         // Pass as many sub-tiles as possible at once: lane j holds sub-tile
         // st + j; the in-order scan of their maps gives each one's end value
@@ -1154,7 +1161,23 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1))) void
         const uint32_t m0 = ccls ? ((cb & 0x7FFFFFu) | 0x800000u) : cb;
         const uint32_t mhi = ccls ? (1u << 24) : (1u << 23);
         Fn f = {kSat, kSat};
-        if (idx < a.nsub) {
+        int lcls = -1;                   // this lane's predicted class
+        uint32_t lx[kXWords] = {0u, 0u, 0u, 0u, 0u, 0xFFFFFFFFu};  // and crossing (all_cached)
+        if (all_cached) {  // row-uniform; unconditional loads at a clamped index
+            const int ic = idx < a.nsub ? (int)idx : a.nsub - 1;
+            lcls = sh.scls[ic];
+            const uint32_t s0 = sh.sm0[ic], s1 = sh.sm1[ic];
+            const uint2* xp = reinterpret_cast<const uint2*>(&sh.xing[ic * kXWords]);
+#pragma unroll
+            for (int w = 0; w < kXWords / 2; w++) {
+                const uint2 q = xp[w];
+                lx[2 * w] = q.x;
+                lx[2 * w + 1] = q.y;
+            }
+            const bool use = idx < a.nsub && lcls == ccls;
+            f.a0 = use ? s0 : kSat;
+            f.a1 = use ? s1 : kSat;
+        } else if (idx < a.nsub) {
             const int pc = idx < kSumCache ? sh.scls[idx] : a.ws_cls[row * a.nsub_ld + idx];
             if (pc == ccls) {
                 f.a0 = idx < kSumCache ? sh.sm0[idx] : a.ws_map0[row * a.nsub_ld + idx];
@@ -1174,8 +1197,19 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1))) void
         }
         if (npass < 64 && st < a.nsub) {
             // a predicted crossing passes in O(1); anything else is walked exactly
-            const int pc = st < kSumCache ? sh.scls[st] : a.ws_cls[row * a.nsub_ld + st];
-            const bool passed = st < nxcache && pass_crossing(cb, &sh.xing[st * kXWords], pc, r);
+            bool passed = false;
+            if (all_cached) {  // the stopping lane's record, already loaded
+                uint32_t x[kXWords];
+#pragma unroll
+                for (int w = 0; w < kXWords; w++) x[w] = (uint32_t)__builtin_amdgcn_readlane((int)lx[w], npass);
+                passed = pass_crossing(cb, x, __builtin_amdgcn_readlane(lcls, npass), r);
+            } else if (st < nxcache) {
+                uint32_t x[kXWords];
+#pragma unroll
+                for (int w = 0; w < kXWords; w++) x[w] = sh.xing[st * kXWords + w];
+                const int pc = st < kSumCache ? sh.scls[st] : a.ws_cls[row * a.nsub_ld + st];
+                passed = pass_crossing(cb, x, pc, r);
+            }
             if (!passed && walk_subtile(a, st, prow, r, cb, result)) break;
             st += 1;
         }

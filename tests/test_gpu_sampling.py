@@ -67,6 +67,30 @@ def test_softmax(hip, orc, rng, rows, n):
     assert_bitexact(got, ref, "softmax")
 
 
+def test_softmax_wide_range(hip, orc, rng):
+    """x - max across [-160, 0]: exps that are subnormal, that round to zero,
+    and the clamp's ends (-104 and its neighbours), bit-identical to the
+    oracle, whose exp takes x < -104 and x > 89 as special cases."""
+    import torch
+
+    n = 8192
+    x = rng.uniform(-160.0, 0.0, (3, n)).astype(np.float32)
+    x[:, 0] = 0.0
+    edges = np.array([-104.0, np.nextafter(np.float32(-104.0), np.float32(0.0)),
+                      np.nextafter(np.float32(-104.0), np.float32(-200.0)), -103.97, -103.28, -87.3365,
+                      -87.3366, -88.0, -100.0, -149.0, -1e30], np.float32)
+    x[0, 1:1 + len(edges)] = edges
+    x[2] += np.float32(30.0)  # max 30: shifted inputs give the same differences
+    t = dev(x)
+    ws = torch.empty(hip.softmax_workspace_size(3, n), dtype=torch.uint8, device="cuda")
+    hip.softmax(t, ws)
+    ref = np.stack([orc.softmax(row) for row in x])
+    got = host(t)
+    assert (got[0, 1:4] >= 0).all() and got[0, 3] == 0.0  # below -104: exactly zero
+    assert ((got > 0) & (got < np.finfo(np.float32).tiny)).any()  # subnormal results occur
+    assert_bitexact(got, ref, "softmax wide range")
+
+
 @pytest.mark.parametrize("freq", [0.1, 0.0])
 def test_sampler_full_config(hip, orc, rng, freq):
     """Logits [64, 151936] ~N(0,3), history [64, 256] ~U[0,V), rep 1.2, T 0.6."""
