@@ -100,28 +100,49 @@ __device__ __forceinline__ float sampler_expf(float x) {
 }
 
 // ---- history counts --------------------------------------------------------
-// cnt[i - c0] = occurrences of id i in the row's window (the last ctx entries,
-// sampling.cpp:17) for i in [c0, c0 + n), ids outside [0, vocab) ignored
-// (sampling.cpp:23).
-__device__ void build_counts(uint32_t* cnt, int n, const SampleArgs& a, long row, long c0) {
-    // this thread's first window entry is loaded before the LDS is cleared,
-    // so its latency overlaps the clearing and the barrier
-    long hl = 0, start = 0;
-    int id0 = -1;
+// The window is the last ctx entries of the row's history (sampling.cpp:17).
+// Without hist_len it is known from the arguments, and this thread's first
+// entry is loaded by hist_first, ahead of the chunk's logits: loads complete
+// in issue order, so the counts can be built while the logits are in flight.
+// With hist_len the window waits for that device value (build_counts).
+struct HistFirst {
+    long hl, start;  // the window is entries [start, hl)
+    int raw;         // entry start + min(threadIdx.x, n - 1), as loaded
+    bool valid;      // threadIdx.x < n: raw is this thread's first entry
+};
+
+// One unconditional load at a clamped index; nothing uses its value before
+// the chunk's loads are issued (a use would wait for it there).
+__device__ __forceinline__ HistFirst hist_first(const SampleArgs& a, long row) {
+    HistFirst f = {0, 0, -1, false};
+    if (a.use_penalty && !a.hist_len && a.hist_ld > 0) {
+        f.hl = a.hist_ld;
+        f.start = f.hl - a.ctx < 0 ? 0 : f.hl - a.ctx;
+        const long n = f.hl - f.start;  // >= 1
+        f.valid = (long)threadIdx.x < n;
+        f.raw = a.hist[row * a.hist_ld + f.start + (f.valid ? (long)threadIdx.x : n - 1)];
+    }
+    return f;
+}
+
+// cnt[i - c0] = occurrences of id i in the window for i in [c0, c0 + n)
+// (n a multiple of 4), ids outside [0, vocab) ignored (sampling.cpp:23).
+__device__ void build_counts(uint32_t* cnt, int n, const SampleArgs& a, long row, long c0, HistFirst f) {
     const int32_t* h = a.hist + row * a.hist_ld;
-    if (a.use_penalty) {
-        hl = a.hist_len ? (long)a.hist_len[row] : a.hist_ld;
+    int id0 = f.valid ? f.raw : -1;
+    if (a.use_penalty && a.hist_len) {
+        long hl = (long)a.hist_len[row];
         if (hl > a.hist_ld) hl = a.hist_ld;
-        start = hl - a.ctx;
-        if (start < 0) start = 0;
-        const long j = start + threadIdx.x;
+        f.hl = hl;
+        f.start = hl - a.ctx < 0 ? 0 : hl - a.ctx;
+        const long j = f.start + threadIdx.x;
         if (j < hl) id0 = h[j];
     }
-    for (int i = threadIdx.x; i < n; i += blockDim.x) cnt[i] = 0u;
+    for (int i = 4 * threadIdx.x; i < n; i += 4 * blockDim.x) *reinterpret_cast<uint4*>(cnt + i) = make_uint4(0u, 0u, 0u, 0u);
     __syncthreads();
     if (a.use_penalty) {
         if (id0 >= 0 && id0 < a.vocab && id0 >= c0 && id0 < c0 + n) atomicAdd(&cnt[id0 - c0], 1u);
-        for (long j = start + threadIdx.x + blockDim.x; j < hl; j += blockDim.x) {
+        for (long j = f.start + threadIdx.x + blockDim.x; j < f.hl; j += blockDim.x) {
             const int id = h[j];
             if (id >= 0 && id < a.vocab && id >= c0 && id < c0 + n) atomicAdd(&cnt[id - c0], 1u);
         }
@@ -167,39 +188,38 @@ __device__ __forceinline__ void adjust_k(float v[4 * K], const uint32_t* cnt, co
     }
 }
 
-// The 4K logits of thread tid in chunk c0 (K float4 slots k*1024 + 4*tid).
-// A whole chunk of an aligned row (every chunk but a row's last) takes one
-// uniform branch with its K 16-byte loads in flight together; per-lane
-// conditions around each load made the compiler wait for each one before
-// issuing the next.
+// The 4K logits of thread tid in chunk c0 (K float4 slots k*1024 + 4*tid),
+// 0 past the end of the row.  An aligned row whose length is a multiple of 4
+// takes K 16-byte loads with no branch: every lane loads a quad at a clamped
+// index and out-of-range values are selected away afterwards (a branch per
+// lane or per chunk made the compiler wait for earlier loads before issuing
+// these).  Other rows take single loads.
 template <int K>
 __device__ __forceinline__ void load_chunk(float v[4 * K], const float* row_ptr, long c0, long vocab, bool vec) {
-    if (vec && c0 + K * kSlice <= vocab) {
+    if (vec && vocab >= 4 && (vocab & 3) == 0) {
+        const long lastq = vocab - 4;  // the last quad
         float4 f[K];
 #pragma unroll
-        for (int k = 0; k < K; k++) f[k] = ld_nt(reinterpret_cast<const float4*>(row_ptr + c0 + k * kSlice + 4 * threadIdx.x));
+        for (int k = 0; k < K; k++) {
+            const long i = c0 + k * kSlice + 4 * threadIdx.x;
+            f[k] = ld_nt(reinterpret_cast<const float4*>(row_ptr + (i < lastq ? i : lastq)));
+        }
 #pragma unroll
         for (int k = 0; k < K; k++) {
-            v[4 * k] = f[k].x;
-            v[4 * k + 1] = f[k].y;
-            v[4 * k + 2] = f[k].z;
-            v[4 * k + 3] = f[k].w;
+            const long i = c0 + k * kSlice + 4 * threadIdx.x;
+            const bool in = i + 3 < vocab;
+            v[4 * k] = in ? f[k].x : 0.0f;
+            v[4 * k + 1] = in ? f[k].y : 0.0f;
+            v[4 * k + 2] = in ? f[k].z : 0.0f;
+            v[4 * k + 3] = in ? f[k].w : 0.0f;
         }
         return;
     }
 #pragma unroll
     for (int k = 0; k < K; k++) {
         const long i = c0 + k * kSlice + 4 * threadIdx.x;
-        if (vec && i + 3 < vocab) {
-            const float4 f = ld_nt(reinterpret_cast<const float4*>(row_ptr + i));
-            v[4 * k] = f.x;
-            v[4 * k + 1] = f.y;
-            v[4 * k + 2] = f.z;
-            v[4 * k + 3] = f.w;
-        } else {
 #pragma unroll
-            for (int e = 0; e < 4; e++) v[4 * k + e] = (i + e < vocab) ? row_ptr[i + e] : 0.0f;
-        }
+        for (int e = 0; e < 4; e++) v[4 * k + e] = (i + e < vocab) ? row_ptr[i + e] : 0.0f;
     }
 }
 
@@ -208,10 +228,16 @@ __device__ __forceinline__ void load_chunk(float v[4 * K], const float* row_ptr,
 // the chunk's own data, so their latency overlaps the chunk loads), and the
 // workgroup reduces the shares later.
 
-// this thread's share of the row max
-__device__ __forceinline__ float max_share(const SampleArgs& a, long row) {
-    float m = -INFINITY;
-    for (int c = threadIdx.x; c < a.nchunk; c += blockDim.x) m = fmaxf(m, a.ws_max[row * a.nchunk + c]);
+// this thread's share of the row max: its first chunk maximum (one
+// unconditional load at a clamped index, selected only after the chunk's
+// loads are issued: a use would wait for it), then any others
+__device__ __forceinline__ float max_first(const SampleArgs& a, long row) {
+    const int c = (int)threadIdx.x < a.nchunk ? (int)threadIdx.x : a.nchunk - 1;
+    return a.ws_max[row * a.nchunk + c];
+}
+__device__ __forceinline__ float max_rest(const SampleArgs& a, long row, float raw) {
+    float m = (int)threadIdx.x < a.nchunk ? raw : -INFINITY;
+    for (int c = threadIdx.x + blockDim.x; c < a.nchunk; c += blockDim.x) m = fmaxf(m, a.ws_max[row * a.nchunk + c]);
     return m;
 }
 
@@ -235,9 +261,21 @@ struct SumShare {
     int flag;
 };
 
-__device__ __forceinline__ SumShare sum_share(const SampleArgs& a, long row, int before) {
-    SumShare sh = {0, 0, 0};
-    for (int c = threadIdx.x; c < a.nchunk; c += blockDim.x) {
+// its first chunk's values (unconditional loads at a clamped index, used
+// only after the chunk's loads are issued), then any others
+struct SumRaw {
+    uint64_t w;
+    int f;
+};
+__device__ __forceinline__ SumRaw sum_first(const SampleArgs& a, long row) {
+    const int c = (int)threadIdx.x < a.nchunk ? (int)threadIdx.x : a.nchunk - 1;
+    return SumRaw{a.ws_sum[row * a.nchunk + c], a.ws_flag[row * a.nchunk + c]};
+}
+__device__ __forceinline__ SumShare sum_rest(const SampleArgs& a, long row, int before, SumRaw raw) {
+    const int c0 = threadIdx.x;
+    const bool in = c0 < a.nchunk;
+    SumShare sh = {in ? raw.w : 0u, in && c0 < before ? raw.w : 0u, in ? raw.f : 0};
+    for (int c = threadIdx.x + blockDim.x; c < a.nchunk; c += blockDim.x) {
         const uint64_t w = a.ws_sum[row * a.nchunk + c];
         sh.all += w;
         sh.pre += c < before ? w : 0;
@@ -439,9 +477,12 @@ __global__ __launch_bounds__(256) void sample_stage1_kernel(SampleArgs a, int ve
     __shared__ int red_i[4];
     const long row = blockIdx.y;
     const long c0 = (long)blockIdx.x * kCH;
+    const HistFirst hf = hist_first(a, row);
+    __builtin_amdgcn_sched_barrier(0);  // its load goes out before the chunk's
     float v[4 * K];
     load_chunk<K>(v, a.logits + row * a.ld_logits, c0, a.vocab, vec != 0);
-    build_counts(cnt, kCH, a, row, c0);
+    __builtin_amdgcn_sched_barrier(0);
+    build_counts(cnt, kCH, a, row, c0, hf);
     adjust_k<K>(v, cnt, a);
     const int nvalid = a.vocab - c0 < kCH ? (int)(a.vocab - c0) : kCH;
     float best = -INFINITY;
@@ -552,10 +593,16 @@ __global__ __launch_bounds__(256) void sample_stage2_kernel(SampleArgs a, int ve
     __shared__ int red_f[4];
     const long row = blockIdx.y;
     const long c0 = (long)blockIdx.x * kCH;
+    // the row's chunk maxima and this thread's window entry first: loads
+    // complete in issue order, so their waits do not wait for the logits
+    const float mraw = max_first(a, row);
+    const HistFirst hf = hist_first(a, row);
+    __builtin_amdgcn_sched_barrier(0);
     float v[4 * K];
     load_chunk<K>(v, a.logits + row * a.ld_logits, c0, a.vocab, vec != 0);
-    const float mshare = max_share(a, row);
-    build_counts(cnt, kCH, a, row, c0);
+    __builtin_amdgcn_sched_barrier(0);
+    const float mshare = max_rest(a, row, mraw);
+    build_counts(cnt, kCH, a, row, c0, hf);
     adjust_k<K>(v, cnt, a);
     const int nvalid = a.vocab - c0 < kCH ? (int)(a.vocab - c0) : kCH;
     const float neg = -reduce_max(mshare, red);
@@ -731,9 +778,13 @@ __global__ __launch_bounds__(256) void sample_stage3_kernel(SampleArgs a, int ve
     // the draw is loaded with the exponentials (the first sub-tile's walk
     // below compares against it), not behind them
     const float rdraw = a.r ? a.r[row] : 0.0f;
+    // and the chunk sums, so that the reduction below does not wait for them
+    const SumRaw sraw = sum_first(a, row);
+    __builtin_amdgcn_sched_barrier(0);
     float v[4 * K];  // exp(adjusted - max), as stage 2 stored them
     load_chunk<K>(v, a.probs + row * a.ld_probs, c0, a.vocab, vec_out != 0);
-    const SumShare share = sum_share(a, row, chunk);
+    __builtin_amdgcn_sched_barrier(0);
+    const SumShare share = sum_rest(a, row, chunk, sraw);
     // 1/sum, and the exact prefix of the earlier chunks' sums (the prediction
     // of the running sum at this chunk's start)
     float inv, prefix;
@@ -922,14 +973,14 @@ __device__ void fill_walk_cache(WalkShared& sh, const SampleArgs& a, long row, i
 __device__ __forceinline__ bool pass_crossing(uint32_t& cb, const uint32_t (&x)[kXWords], int pcls, float r) {
     const int info = (int)x[5];
     const Binade b = binade_of(__uint_as_float(cb));
-    const uint32_t inc = (b.m0 & 1u) ? x[1] : x[0];
+    const uint32_t inc = pick(Fn{x[0], x[1]}, b.m0);  // arithmetic select: an indexed one went to scratch
     const uint32_t mb = b.m0 + inc;  // m0 < 2^24, inc <= 2^30: no wrap
     const float base = ldexpf((float)mb, -b.sh);
     const float pj = __uint_as_float(x[4]);
     const uint32_t incj = pick(elem_map(pj, b), mb);
     const float c = base + pj;  // the reference's fp32 add of element j
     const Binade b2 = binade_of(c);
-    const uint32_t inc2 = (b2.m0 & 1u) ? x[3] : x[2];
+    const uint32_t inc2 = pick(Fn{x[2], x[3]}, b2.m0);
     const float end = ldexpf((float)(b2.m0 + inc2), -b2.sh);
     const bool ok = (info >= 0) & (b.cls == pcls)                // a single crossing, made for this binade
                     & (inc < b.mhi - b.m0) & (base < r)           // no leave and no hit before j
