@@ -578,6 +578,83 @@ __global__ __launch_bounds__(64) void sample_argmax_final_kernel(SampleArgs a) {
     }
 }
 
+// A lane's sum of floor(e * 2^shift) over its exponentials.  When its 4K
+// terms (each at most 2^shift) stay below 2^53 the sum is kept in fp64:
+// widening, scaling by 2^shift, floor and add are then all exact (4
+// instructions a term, against about 10 for a float -> u64 floor and a 64-bit
+// add), and a NaN or inf term leaves it non-finite.  Otherwise in u64.
+template <bool F64>
+struct LaneSum {
+    double d = 0.0;
+    uint64_t u = 0;
+    int nan = 0;
+    __device__ __forceinline__ void add(float x, float scale, double scaled) {
+        if constexpr (F64) {
+            d += floor((double)x * scaled);
+        } else {
+            const bool ok = x <= 1.0f;  // e >= 0 always; false for NaN and inf
+            u += (uint64_t)(ok ? x * scale : 0.0f);
+            nan |= ok ? 0 : 1;
+        }
+    }
+    __device__ __forceinline__ void finish(uint64_t& acc, int& bad) const {
+        if constexpr (F64) {
+            const bool b = !(d <= 0x1p53);
+            bad = b ? 1 : 0;
+            acc = b ? 0u : (uint64_t)d;
+        } else {
+            bad = nan;
+            acc = u;
+        }
+    }
+};
+
+// The chunk's exponentials e = exp(x - max), stored into the probability
+// buffer (cached: stage 3 reads them back), and this lane's sum of them.
+template <int K, bool F64>
+__device__ __forceinline__ void exp_and_sum(const float (&v)[4 * K], float neg, const SampleArgs& a, long row, long c0,
+                                            int nvalid, int vec_out, uint64_t& acc, int& nan) {
+    constexpr int kCH = K * kSlice;
+    const float scale = ldexpf(1.0f, a.shift);
+    const double scaled = ldexp(1.0, a.shift);
+    float* out = a.probs + row * a.ld_probs;
+    LaneSum<F64> sum;
+    if (nvalid == kCH && vec_out) {
+        // a whole chunk: no per-element bounds (a guard per element compiled
+        // to an exec-mask branch per element)
+#pragma unroll
+        for (int k = 0; k < K; k++) {
+            float ev[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                ev[e] = sampler_expf(v[4 * k + e] + neg);
+                sum.add(ev[e], scale, scaled);
+            }
+            *reinterpret_cast<float4*>(out + c0 + k * kSlice + 4 * threadIdx.x) = make_float4(ev[0], ev[1], ev[2], ev[3]);
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < K; k++) {
+            float ev[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int li = k * kSlice + 4 * threadIdx.x + e;
+                ev[e] = li < nvalid ? sampler_expf(v[4 * k + e] + neg) : 0.0f;
+                sum.add(ev[e], scale, scaled);
+            }
+            const long i = c0 + k * kSlice + 4 * threadIdx.x;
+            if (vec_out && i + 3 < a.vocab) {
+                *reinterpret_cast<float4*>(out + i) = make_float4(ev[0], ev[1], ev[2], ev[3]);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    if (i + e < a.vocab) out[i + e] = ev[e];
+            }
+        }
+    }
+    sum.finish(acc, nan);
+}
+
 // ---- stage 2: exact fixed-point sum of exp(x - max) per chunk ---------------
 // floor(e * 2^shift) summed as integers (associative, so independent of the
 // reduction order); any NaN term flags the row.  The values e are stored in
@@ -606,50 +683,13 @@ __global__ __launch_bounds__(256) void sample_stage2_kernel(SampleArgs a, int ve
     adjust_k<K>(v, cnt, a);
     const int nvalid = a.vocab - c0 < kCH ? (int)(a.vocab - c0) : kCH;
     const float neg = -reduce_max(mshare, red);
-    const float scale = ldexpf(1.0f, a.shift);
-    float* out = a.probs + row * a.ld_probs;
-    uint64_t acc = 0;
-    int nan = 0;
-    if (nvalid == kCH && vec_out) {
-        // a whole chunk: no per-element bounds (a guard per element compiled
-        // to an exec-mask branch per element)
-#pragma unroll
-        for (int k = 0; k < K; k++) {
-            float ev[4];
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const float x = sampler_expf(v[4 * k + e] + neg);
-                ev[e] = x;
-                const bool ok = x <= 1.0f;  // e >= 0 always; false for NaN and inf
-                acc += (uint64_t)(ok ? x * scale : 0.0f);
-                nan |= ok ? 0 : 1;
-            }
-            // cached store: stage 3 reads these back
-            *reinterpret_cast<float4*>(out + c0 + k * kSlice + 4 * threadIdx.x) = make_float4(ev[0], ev[1], ev[2], ev[3]);
-        }
-    } else {
-#pragma unroll
-    for (int k = 0; k < K; k++) {
-        float ev[4];
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-            const int li = k * kSlice + 4 * threadIdx.x + e;
-            const float x = li < nvalid ? sampler_expf(v[4 * k + e] + neg) : 0.0f;
-            ev[e] = x;
-            const bool ok = x <= 1.0f;  // e >= 0 always; false for NaN and inf
-            acc += (uint64_t)(ok ? x * scale : 0.0f);
-            nan |= ok ? 0 : 1;
-        }
-        const long i = c0 + k * kSlice + 4 * threadIdx.x;
-        if (vec_out && i + 3 < a.vocab) {  // cached store: stage 3 reads these back
-            *reinterpret_cast<float4*>(out + i) = make_float4(ev[0], ev[1], ev[2], ev[3]);
-        } else {
-#pragma unroll
-            for (int e = 0; e < 4; e++)
-                if (i + e < a.vocab) out[i + e] = ev[e];
-        }
-    }
-    }
+    constexpr int kLogTerms = K == 1 ? 2 : K == 2 ? 3 : K <= 4 ? 4 : K <= 8 ? 5 : 6;  // ceil(log2(4K)), a lane's terms
+    uint64_t acc;
+    int nan;
+    if (a.shift + kLogTerms <= 53)  // uniform: the lane's sum fits fp64's 53 bits
+        exp_and_sum<K, true>(v, neg, a, row, c0, nvalid, vec_out, acc, nan);
+    else
+        exp_and_sum<K, false>(v, neg, a, row, c0, nvalid, vec_out, acc, nan);
     acc = wave_sum_u64(acc);
     nan = __any(nan) ? 1 : 0;
     if ((threadIdx.x & 63) == 0) {
@@ -1280,13 +1320,15 @@ struct WsLayout {
 
 static size_t al16(size_t x) { return (x + 15) & ~(size_t)15; }
 
-// 1024-logit slices per chunk: 4, unless rows x chunks of 4096 would leave
+// 1024-logit slices per chunk: 3, unless rows x chunks of 4096 would leave
 // most of the 256 CUs without a workgroup (a few rows), then 1: the stages'
 // per-wave work is a chain of dependent instructions over a thread's 4K
 // logits and a wave's K sub-tiles, so at one row smaller chunks finish
-// sooner.  The outputs do not depend on it.
+// sooner.  At 64 rows of 151936, 3 measured 68.5 us a call against 70.7 for
+// 4, 73-75 for 2 and 73-81 for 5, 6 and 8.  The outputs do not depend on it.
+constexpr int kSlicesMany = 3;
 static int chunk_slices(long rows, long vocab) {
-    return rows * ((vocab + 4 * kSlice - 1) / (4 * kSlice)) < 256 ? 1 : 4;
+    return rows * ((vocab + 4 * kSlice - 1) / (4 * kSlice)) < 256 ? 1 : kSlicesMany;
 }
 
 static WsLayout ws_layout(long rows, long vocab) {
@@ -1375,9 +1417,9 @@ extern "C" int anelm_softmax(float* x, long rows, long n, long ld, void* workspa
         sample_stage2_kernel<1><<<grd, 256, 0, st>>>(a, vec, vec);
         sample_stage3_kernel<1><<<grd, 256, 0, st>>>(a, vec);
     } else {
-        sample_stage1_kernel<false, 4><<<grd, 256, 0, st>>>(a, vec);
-        sample_stage2_kernel<4><<<grd, 256, 0, st>>>(a, vec, vec);
-        sample_stage3_kernel<4><<<grd, 256, 0, st>>>(a, vec);
+        sample_stage1_kernel<false, kSlicesMany><<<grd, 256, 0, st>>>(a, vec);
+        sample_stage2_kernel<kSlicesMany><<<grd, 256, 0, st>>>(a, vec, vec);
+        sample_stage3_kernel<kSlicesMany><<<grd, 256, 0, st>>>(a, vec);
     }
     return launch_status("softmax");
 }
@@ -1425,7 +1467,7 @@ int sample_impl(int32_t* ids, float* probs, long ld_probs, const float* logits, 
     const bool one = chunk_slices(rows, vocab) == 1;
     if (!sampling) {
         if (one) sample_stage1_kernel<true, 1><<<grd, 256, 0, st>>>(a, vec);
-        else sample_stage1_kernel<true, 4><<<grd, 256, 0, st>>>(a, vec);
+        else sample_stage1_kernel<true, kSlicesMany><<<grd, 256, 0, st>>>(a, vec);
         sample_argmax_final_kernel<<<dim3((unsigned)rows), 64, 0, st>>>(a);
         return launch_status("sample(argmax)");
     }
@@ -1436,9 +1478,9 @@ int sample_impl(int32_t* ids, float* probs, long ld_probs, const float* logits, 
         sample_stage2_kernel<1><<<grd, 256, 0, st>>>(a, vec, vec_out);
         sample_stage3_kernel<1><<<grd, 256, 0, st>>>(a, vec_out);
     } else {
-        sample_stage1_kernel<false, 4><<<grd, 256, 0, st>>>(a, vec);
-        sample_stage2_kernel<4><<<grd, 256, 0, st>>>(a, vec, vec_out);
-        sample_stage3_kernel<4><<<grd, 256, 0, st>>>(a, vec_out);
+        sample_stage1_kernel<false, kSlicesMany><<<grd, 256, 0, st>>>(a, vec);
+        sample_stage2_kernel<kSlicesMany><<<grd, 256, 0, st>>>(a, vec, vec_out);
+        sample_stage3_kernel<kSlicesMany><<<grd, 256, 0, st>>>(a, vec_out);
     }
     sample_walk_kernel<<<dim3((unsigned)rows), 64, 0, st>>>(a);
     return launch_status("sample");
@@ -1452,7 +1494,7 @@ int sample_impl(int32_t* ids, float* probs, long ld_probs, const float* logits, 
 // hipGetSymbolAddress, with that device current, and kept in scratch_ptr.
 // Nothing in it needs clearing: every word a kernel reads is written earlier
 // in the same call.  Calls that overlap on one GPU share it, and race.
-constexpr size_t kScratchBytes = 4u << 20;   // 188 rows at Qwen3's 151936-row vocabulary
+constexpr size_t kScratchBytes = 4u << 20;   // 186 rows at Qwen3's 151936-row vocabulary
 constexpr int kMaxDevices = 64;
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 void* scratch_ptr[kMaxDevices];

@@ -259,7 +259,7 @@ int anelm_sample(int32_t* ids, float* probs, long ld_probs, const float* logits,
  * the same kernels and results, with the workspace taken from a static
  * 4 MiB device array the library holds on every GPU it runs on until the
  * process ends, so it calls no allocator.  Limit:
- * anelm_sample_workspace_size(rows, vocab) <= 4 MiB (188 rows at a 151936-row
+ * anelm_sample_workspace_size(rows, vocab) <= 4 MiB (186 rows at a 151936-row
  * vocabulary); larger calls return ANELM_ERR_WORKSPACE.  Every call on one GPU
  * shares that GPU's array: calls that overlap on one GPU (on different
  * streams, or from different threads) race and must not be issued.  The

@@ -58,11 +58,11 @@ def test_noalloc_rejects_sizes_past_the_scratch(hip, rng):
     import torch
 
     V = 151936
-    assert hip.sample_workspace_size(188, V) <= 4 << 20 < hip.sample_workspace_size(189, V)
-    logits = torch.zeros(189, V, device="cuda")
-    ids = torch.full((189,), -7, dtype=torch.int32, device="cuda")
-    probs = torch.empty(189, V, device="cuda")
-    r = torch.full((189,), 0.5, device="cuda")
+    assert hip.sample_workspace_size(186, V) <= 4 << 20 < hip.sample_workspace_size(187, V)
+    logits = torch.zeros(187, V, device="cuda")
+    ids = torch.full((187,), -7, dtype=torch.int32, device="cuda")
+    probs = torch.empty(187, V, device="cuda")
+    r = torch.full((187,), 0.5, device="cuda")
     with pytest.raises(hip.AnelmError, match="scratch"):
         hip.sample_noalloc(ids, probs, logits, None, None, hip.SamplingParams(), r)
     assert np.all(host(ids) == -7)                     # nothing was launched
