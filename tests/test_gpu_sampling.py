@@ -106,6 +106,32 @@ def test_sampler_full_config(hip, orc, rng, freq):
     assert np.array_equal(ids, rids)
 
 
+@pytest.mark.parametrize("rows", [8, 1])
+def test_sampler_nan_and_inf_logits_full_vocab(hip, orc, rng, rows):
+    """Rows of 151936 logits, where the exact per-lane sums run in fp64 (chunks
+    of 3072 at 8 rows, of 1024 at one row), with a NaN, a +inf and -inf
+    logits: ids equal the oracle's; probabilities are NaN exactly where the
+    oracle's are and bit-identical elsewhere."""
+    logits = rng.normal(0, 3, (rows, V)).astype(np.float32)
+    logits[0, 5] = np.nan
+    if rows > 1:
+        logits[1, V - 1] = np.nan      # in the last, partial chunk
+        logits[2, 1000] = np.inf
+        logits[3, ::7] = -np.inf
+        logits[4, 77777] = np.nan
+    hist = rng.integers(0, V, (rows, 256)).astype(np.int32)
+    r = drand48_stream(99, rows)
+    params = dict(temperature=0.6, repetition_penalty=1.2, repetition_context_size=256, frequency_penalty=0.1)
+    ids, probs = run_sample(hip, logits, hist, r=r, **params)
+    rids, rprobs = oracle_rows(orc, logits, hist, r=r, **params)
+    assert np.array_equal(ids, rids)
+    gn, rn = np.isnan(probs), np.isnan(rprobs)
+    assert np.array_equal(gn, rn)
+    assert rn[0].all() and ids[0] == V - 1
+    assert_bitexact(np.where(gn, 0.0, probs).astype(np.float32), np.where(rn, 0.0, rprobs).astype(np.float32),
+                    "probabilities")
+
+
 def test_sampler_draws_on_cdf_boundaries(hip, orc, rng):
     """r set to exact running-sum values and their neighbours: any
     deviation from the sequential fp32 walk changes the id."""
