@@ -31,6 +31,8 @@ namespace anelm {
 
 constexpr int kSlice = 1024;  // logits per k-slice: 4 per thread of a 256-thread workgroup
 constexpr int kSub = 256;     // logits per walk sub-tile: one wave's part of a k-slice of a chunk
+constexpr int kFirstSubs = 4; // at most sub-tiles 0..3, chunk 0's first k-slice, walked one add at a time by stage 3
+constexpr int kFirstN = kFirstSubs * kSub;
 
 struct SampleArgs {
     const float* logits;
@@ -58,7 +60,8 @@ struct SampleArgs {
     uint32_t* ws_map1;    // [rows, nsub] sub-tile map, odd start
     int32_t* ws_cls;      // [rows, nsub] predicted binade class (-1: none)
     uint32_t* ws_xing;    // [rows, nsub, kXWords] predicted crossing (see predict_crossing)
-    int32_t* ws_first;    // [rows, 2] sub-tile 0 walked by stage 3: hit index or -1, end bits
+    int32_t* ws_first;    // [rows, 2] sub-tiles 0..first_subs-1 walked by stage 3: hit index or -1, end bits
+    int first_subs;       // sub-tiles stage 3 walks one add at a time (1 or kFirstSubs)
     int nchunk;
     int nsub;
     int nsub_ld;          // row stride of the sub-tile arrays: nsub rounded up to 4 (16-byte rows)
@@ -791,7 +794,7 @@ __device__ __forceinline__ Crossing predict_crossing(Fn acc, const Fn f[4], cons
 }
 
 __device__ bool walk_subtile_p(const float p[4], long base, long V, float r, uint32_t& cb, long& result);
-__device__ bool walk_first_lds(const float* sp, long V, float r, uint32_t& cb, long& result);
+__device__ bool walk_first_lds(const float* sp, int nsubs, long V, float r, uint32_t& cb, long& result);
 
 // ---- stage 3: probabilities and sub-tile maps --------------------------------
 // Wave w's part of k-slice k is the 256 consecutive logits c0 + k*1024 + w*256 +
@@ -807,9 +810,9 @@ __global__ __launch_bounds__(256) void sample_stage3_kernel(SampleArgs a, int ve
     __shared__ uint64_t red_s[4], red_p[4];
     __shared__ int red_f[4];
     __shared__ float ksum[K][4];  // [k][wave] fp32 sums of exp (prediction only)
-    __shared__ __align__(16) float s_first[kSub];  // sub-tile 0's probabilities for its one-lane walk
+    __shared__ __align__(16) float s_first[kFirstN];  // the first k-slice's probabilities for the one-lane walk
     // Workgroups in dispatch order take chunk 0 of every row first: those
-    // also walk sub-tile 0 (below), the longest job, so it starts early.
+    // also walk sub-tiles 0..3 (below), the longest job, so it starts early.
     const long lin = (long)blockIdx.y * gridDim.x + blockIdx.x;
     const long row = lin % a.rows;
     const int chunk = (int)(lin / a.rows);
@@ -851,24 +854,26 @@ __global__ __launch_bounds__(256) void sample_stage3_kernel(SampleArgs a, int ve
                 if (i + j < a.vocab) out[i + j] = p[4 * k + j];
         }
     }
-    // Sub-tile 0 starts from an exact running sum, 0, and crosses a binade
-    // at about every doubling of its element count: a dozen restarts of the
-    // map-based walk.  Lane 0 of each row's first workgroup (dispatched
-    // first) walks it here instead, one fp32 add at a time from LDS, at raised
-    // issue priority, while the rest of the grid runs (and the workgroup's
-    // other waves make their maps), off the walk kernel's critical path.
-    __syncthreads();  // ksum complete; the other waves need not wait for the walk below
+    // The row's first sub-tiles start from an exact running sum, 0, that is
+    // small against single elements: it crosses a binade at about every
+    // doubling, often twice in one sub-tile, where the map-based walk needs
+    // exact walks with restarts.  Lane 0 of each row's first workgroup
+    // (dispatched first) walks the first first_subs sub-tiles (of its first
+    // k-slice, which its four waves stage in LDS) here instead, one fp32 add
+    // at a time, at raised issue priority, while the rest of the grid runs
+    // (and the workgroup's other waves make their maps), off the walk
+    // kernel's critical path.  With many rows that is four sub-tiles (their
+    // exact walks were most of the slowest rows' extra walk time); with a few
+    // rows stage 3 is too short to hide more than one.
+    if (chunk == 0 && a.r)
+        *reinterpret_cast<float4*>(&s_first[wid * kSub + 4 * lane]) = make_float4(p[0], p[1], p[2], p[3]);
+    __syncthreads();  // ksum and s_first complete; the other waves need not wait for the walk below
     if (chunk == 0 && wid == 0 && a.r) {
         __builtin_amdgcn_s_setprio(3);
-        *reinterpret_cast<float4*>(&s_first[4 * lane]) = make_float4(p[0], p[1], p[2], p[3]);
-        // the wave's LDS writes complete before its lane 0 reads them back
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         if (lane == 0) {
             uint32_t cb = 0u;
             long result = -1;
-            const bool done = walk_first_lds(s_first, a.vocab, rdraw, cb, result);
+            const bool done = walk_first_lds(s_first, a.first_subs, a.vocab, rdraw, cb, result);
             a.ws_first[2 * row] = done ? (int32_t)result : -1;
             a.ws_first[2 * row + 1] = (int32_t)cb;
         }
@@ -882,12 +887,13 @@ __global__ __launch_bounds__(256) void sample_stage3_kernel(SampleArgs a, int ve
         const float cpred = here * inv;
         const long st = (long)chunk * (4 * K) + 4 * k + wid;
         // No map where the walk does not arrive: without a draw (softmax), for
-        // sub-tile 0 (walked exactly above; the walk starts after it), or
+        // sub-tiles 0..first_subs-1 (walked exactly above; the walk starts
+        // after them), or
         // when the sub-tile is predicted to start more than skip_margin past
         // r (the sequential sum is within V * 2^-25 of the exact prefix, so
         // the draw has ended before it).  A wrong prediction costs the walk an
         // exact walk of the sub-tile (class -1, no crossing), never a result.
-        if (!a.r || st == 0 || cpred >= rdraw + a.skip_margin) {  // wave-uniform
+        if (!a.r || st < a.first_subs || cpred >= rdraw + a.skip_margin) {  // wave-uniform
             if (a.r && lane == 63 && st < a.nsub) {
                 a.ws_cls[row * a.nsub_ld + st] = -1;
                 a.ws_xing[(row * a.nsub_ld + st) * kXWords + 5] = 0xFFFFFFFFu;
@@ -1035,12 +1041,13 @@ __device__ __forceinline__ bool pass_crossing(uint32_t& cb, const uint32_t (&x)[
 // scan of their maps; an element that leaves the binade is added with an
 // ordinary fp32 add and the scan restarts after it.  Returns true when the
 // draw is decided (result set), else updates cb to the sub-tile's end.
-// The first sub-tile (elements 0 .. min(V, 256) - 1) one fp32 add at a time
-// in index order, from cum = 0: the reference's loop itself, run by one lane
-// over the probabilities staged in LDS (sp, 16-byte aligned).  Returns true
-// when the draw is decided (result set), else sets cb to the running sum's
-// bits at the sub-tile's end.  Adding 0.0f for the padding past V leaves the
-// sum unchanged.
+// The first nsubs sub-tiles (elements 0 .. min(V, 256 * nsubs) - 1, nsubs <=
+// kFirstSubs) one fp32 add at a time in index order, from cum = 0: the
+// reference's loop itself, run by one lane over the probabilities staged in
+// LDS (sp, 16-byte aligned).  Returns
+// true when the draw is decided (result set), else sets cb to the running
+// sum's bits at their end.  Adding 0.0f for the padding past V leaves the sum
+// unchanged.
 // The 16 running sums after cum, in index order, and whether the draw ends
 // among them (result set).  One fp32 add per element, as the reference.
 __device__ __forceinline__ bool walk16(const float4 (&q)[4], int i, long V, float r, float& cum, long& result) {
@@ -1074,17 +1081,18 @@ __device__ __forceinline__ bool walk16(const float4 (&q)[4], int i, long V, floa
     return false;
 }
 
-__device__ bool walk_first_lds(const float* sp, long V, float r, uint32_t& cb, long& result) {
-    const int nvalid = V < kSub ? (int)V : kSub;
+__device__ bool walk_first_lds(const float* sp, int nsubs, long V, float r, uint32_t& cb, long& result) {
+    const int nel = nsubs * kSub;
+    const int nvalid = V < nel ? (int)V : nel;
     float cum = 0.0f;
-    if (nvalid == kSub) {
-        // a whole sub-tile: no per-element bounds, and the next 16
+    if (nvalid == nel) {
+        // whole sub-tiles: no per-element bounds, and the next 16
         // probabilities are read from LDS while these 16 are added
         float4 q[4], nq[4];
 #pragma unroll
         for (int u = 0; u < 4; u++) q[u] = *reinterpret_cast<const float4*>(sp + 4 * u);
-        for (int i = 0; i < kSub; i += 16) {
-            const int n = i + 16 < kSub ? i + 16 : i;
+        for (int i = 0; i < nel; i += 16) {
+            const int n = i + 16 < nel ? i + 16 : i;
 #pragma unroll
             for (int u = 0; u < 4; u++) nq[u] = *reinterpret_cast<const float4*>(sp + n + 4 * u);
             if (walk16(q, i, V, r, cum, result)) return true;
@@ -1223,7 +1231,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1))) void
     const float r = a.r[row];
     const long V = a.vocab;
     const float* prow = a.probs + row * a.ld_probs;
-    const int first_hit = a.ws_first[2 * row];  // sub-tile 0, walked by stage 3
+    const int first_hit = a.ws_first[2 * row];  // sub-tiles 0..first_subs-1, walked by stage 3
     const uint32_t first_end = (uint32_t)a.ws_first[2 * row + 1];
     const int ncache = a.nsub < kSumCache ? a.nsub : kSumCache;
     const int nxcache = a.nsub < kXCache ? a.nsub : kXCache;
@@ -1238,7 +1246,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1))) void
     }
     uint32_t cb = first_end;  // bits of the running sum
     long result = V - 1;
-    long st = 1;
+    long st = a.first_subs;
     // every record of the row in LDS (V <= 2048 sub-tiles): each step reads
     // its 64 sub-tiles' class, map and crossing in one round of LDS loads
     const bool all_cached = a.nsub <= nxcache;
@@ -1370,6 +1378,7 @@ static int bind_workspace(SampleArgs& a, void* ws, size_t ws_bytes, long rows, l
     a.nchunk = (int)((vocab + kch - 1) / kch);
     a.nsub = (int)((vocab + kSub - 1) / kSub);
     a.nsub_ld = (a.nsub + 3) & ~3;
+    a.first_subs = chunk_slices(rows, vocab) == 1 ? 1 : kFirstSubs;
     a.shift = 63 - ceil_log2(vocab);
     // the sequential fp32 running sum of vocab probabilities is within
     // vocab * 2^-25 of the exact prefix (each add errs by half an ulp of a
