@@ -743,6 +743,12 @@ bool overlaps(const void* y, long ld_y, int out_dim, int y_bytes, const void* x,
     return x0 < y1 && y0 < x1;
 }
 
+// Whether [p, p + np) and [q, q + nq) (bytes) share a byte.
+bool spans_overlap(const void* p, long np, const void* q, long nq) {
+    const uintptr_t p0 = reinterpret_cast<uintptr_t>(p), q0 = reinterpret_cast<uintptr_t>(q);
+    return p0 < q0 + (uintptr_t)nq && q0 < p0 + (uintptr_t)np;
+}
+
 bool dot_ok(const float* x, const uint16_t* w16, long batch, int in_dim, long ld_x) {
     return batch <= 8 && in_dim % 8 == 0 && ld_x % 4 == 0 && aligned16(x) && aligned16(w16);
 }
@@ -1089,8 +1095,9 @@ extern "C" int anelm_proj_f16_tt(void* y, const uint16_t* x_t, const uint16_t* w
     const long xrows = (batch + 15) / 16 * 16;
     const int ybytes = epilogue == ANELM_PROJ_STORE_F16 || epilogue == ANELM_PROJ_SWIGLU_F16 ? 2 : 4;
     const bool ytiled = epilogue == ANELM_PROJ_SWIGLU_F16_TILED;
-    if (ytiled ? overlaps(y, out_dim, out_dim, 2, x_t, in_dim, in_dim, 2, xrows)
-               : overlaps(y, ld_y, out_dim, ybytes, x_t, in_dim, in_dim, 2, xrows))
+    // y spans its batch rows (tiled: the padded rows), x_t its padded rows
+    if (spans_overlap(y, ytiled ? xrows * out_dim * 2 : ((batch - 1) * ld_y + out_dim) * ybytes, x_t,
+                      xrows * in_dim * 2))
         return fail(ANELM_ERR_INVALID, "%s: y overlaps x (y is written while x is still read)", fn);
     ProjArgs a = args(static_cast<float*>(y), x_t, w_t, batch, out_dim, in_dim, in_dim, ytiled ? out_dim : ld_y);
     a.y16 = static_cast<uint16_t*>(y);

@@ -119,3 +119,27 @@ def test_proj_f16_tt(hip, orc, rng, B, out_dim, in_dim):
             ht = tiled_buf(B, inter)
             hip.proj_f16_tt(ht, xt, wt, B, inter, in_dim, epilogue=hip.PROJ_SWIGLU_F16_TILED)
             assert_bitexact(untile(host(ht), B, inter), host(hr), "tiled fp16 SwiGLU vs rows")
+
+
+def test_proj_f16_tt_adjacent_buffers(hip, rng):
+    """y's 17 rows followed directly by x_t (32 padded rows) in one buffer:
+    accepted (the overlap check takes y's own rows, not x_t's padded count),
+    and the result equals the same call on separate buffers."""
+    import torch
+
+    B, out_dim, in_dim = 17, 64, 256
+    buf = torch.zeros(B * out_dim + 32 * in_dim // 2, dtype=torch.float32, device="cuda")
+    y = buf[:B * out_dim].view(B, out_dim)
+    xt = buf[B * out_dim:].view(torch.int16)
+    x16 = (rng.standard_normal((B, in_dim)) * 0.5).astype(np.float16)
+    xr = dev(x16.view(np.int16))
+    hip.proj_tile_f16(xt, xr)
+    w = dev((0.03 * rng.standard_normal((out_dim, in_dim))).astype(np.float16).view(np.int16))
+    wt = torch.zeros(hip.proj_tiled_size(out_dim, in_dim) // 2, dtype=torch.int16, device="cuda")
+    hip.proj_tile_f16(wt, w)
+    hip.proj_f16_tt(y, xt, wt, B, out_dim, in_dim, epilogue=hip.PROJ_STORE)
+    ref = torch.zeros(B, out_dim, device="cuda")
+    xt2 = tiled_buf(B, in_dim)
+    hip.proj_tile_f16(xt2, xr)
+    hip.proj_f16_tt(ref, xt2, wt, B, out_dim, in_dim, epilogue=hip.PROJ_STORE)
+    assert_bitexact(host(y), host(ref), "adjacent y and x_t")
