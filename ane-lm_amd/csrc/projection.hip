@@ -471,16 +471,23 @@ __global__ __launch_bounds__(512) void proj_lds_kernel(ProjArgs a) {
     // The scheduling barriers keep each chunk's loads ahead of the previous
     // chunk's MFMAs; without them the scheduler sank the loads below the
     // MFMAs, leaving one chunk in flight.
-    for (int q = 0; q < nq; q += 2) {
+    // Both chunks of an iteration are computed; an odd last chunk (already
+    // in wa) is computed after the loop.  With a conditional second compute
+    // inside the loop, the back edge merged a path with wb's loads still in
+    // flight, and the compiler put a vmcnt wait at the loop head (after a
+    // round's stores it waited on half of the chunk just issued).
+    int q = 0;
+    for (; q + 1 < nq; q += 2) {
         issue(wb, q + 1);
         __builtin_amdgcn_sched_barrier(0);
         compute(wa, q);
         __builtin_amdgcn_sched_barrier(0);
         issue(wa, q + 2);
         __builtin_amdgcn_sched_barrier(0);
-        if (q + 1 < nq) compute(wb, q + 1);
+        compute(wb, q + 1);
         __builtin_amdgcn_sched_barrier(0);
     }
+    if (q < nq) compute(wa, q);
 }
 
 // ---- one or two rows of x: one wave per output row ------------------------
