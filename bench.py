@@ -1195,6 +1195,7 @@ def main():
         "chain_bytes_per_step": head["chain_bytes"],
         "buffer_sets": head["buffer_sets"],
         "carried_x": head.get("carried_x"),
+        "one_launch_per_layer": head.get("one_launch_per_layer"),
         "roofline": roof,
         "cpu_baseline": cpu,
         "ops": head["ops"],
