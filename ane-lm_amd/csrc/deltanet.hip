@@ -69,43 +69,58 @@ __global__ __launch_bounds__(1024) void conv1d_update_kernel(float* y, float* st
                                                              long state_stride) {
     const long b = blockIdx.x;
     const int state_len = kernel_size - 1;
-    int pos = state_pos[b];
-    pos = pos < 0 ? 0 : (pos >= state_len ? 0 : pos);   // keeps every access in the ring
     float* st = state + b * state_stride;
     const float* xb = x + b * ld_x;
     float* yb = y + b * ld_y;
+    int pos;
     if (kernel_size == 4) {
         // the common case: every load of a batch of channels is issued
-        // before the first is used (ring indices pos, pos+1, pos+2 mod 3)
-        const int i1 = pos + 1 == 3 ? 0 : pos + 1;
-        const int i2 = i1 + 1 == 3 ? 0 : i1 + 1;
+        // before the first is used, at a clamped channel (unconditional);
+        // the three ring slots are loaded at fixed offsets and picked by the
+        // ring position afterwards (oldest first: pos, pos+1, pos+2 mod 3),
+        // and the position is loaded after the first batch's loads (a vector
+        // load: as a scalar load it was waited for before any other went out)
         constexpr int kB = 8;
-        for (int c0 = threadIdx.x; c0 < channels; c0 += kB * 1024) {
-            float s0[kB], s1[kB], s2[kB], xc[kB];
-            float4 wc[kB];
+        float t0[kB], t1[kB], t2[kB], xc[kB];
+        float4 wc[kB];
+        auto load = [&](int c0) {
 #pragma unroll
             for (int u = 0; u < kB; u++) {
-                const int c = c0 + u * 1024;
-                if (c < channels) {
-                    const float* sc = st + (long)c * 3;
-                    s0[u] = sc[pos];
-                    s1[u] = sc[i1];
-                    s2[u] = sc[i2];
-                    xc[u] = xb[c];
-                    wc[u] = *reinterpret_cast<const float4*>(w + (long)c * 4);
-                }
+                const int c = c0 + u * 1024 < channels ? c0 + u * 1024 : channels - 1;
+                const float* sc = st + (long)c * 3;
+                t0[u] = sc[0];
+                t1[u] = sc[1];
+                t2[u] = sc[2];
+                xc[u] = xb[c];
+                wc[u] = *reinterpret_cast<const float4*>(w + (long)c * 4);
             }
+        };
+        auto compute = [&](int c0, int p) {
 #pragma unroll
             for (int u = 0; u < kB; u++) {
                 const int c = c0 + u * 1024;
                 if (c < channels) {
-                    const float sum = fmaf(s2[u], wc[u].z, fmaf(s1[u], wc[u].y, fmaf(s0[u], wc[u].x, 0.0f)));
+                    const float o0 = p == 0 ? t0[u] : (p == 1 ? t1[u] : t2[u]);
+                    const float o1 = p == 0 ? t1[u] : (p == 1 ? t2[u] : t0[u]);
+                    const float o2 = p == 0 ? t2[u] : (p == 1 ? t0[u] : t1[u]);
+                    const float sum = fmaf(o2, wc[u].z, fmaf(o1, wc[u].y, fmaf(o0, wc[u].x, 0.0f)));
                     yb[c] = fmaf(xc[u], wc[u].w, sum);
-                    st[(long)c * 3 + pos] = xc[u];
+                    st[(long)c * 3 + p] = xc[u];
                 }
             }
+        };
+        load((int)threadIdx.x);
+        pos = __hip_atomic_load(state_pos + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_sched_barrier(0);
+        pos = pos < 0 ? 0 : (pos >= 3 ? 0 : pos);   // keeps every access in the ring
+        compute((int)threadIdx.x, pos);
+        for (int c0 = (int)threadIdx.x + kB * 1024; c0 < channels; c0 += kB * 1024) {
+            load(c0);
+            compute(c0, pos);
         }
     } else {
+        pos = state_pos[b];
+        pos = pos < 0 ? 0 : (pos >= state_len ? 0 : pos);   // keeps every access in the ring
         for (int c = threadIdx.x; c < channels; c += blockDim.x) {
             float* sc = st + (long)c * state_len;
             const float* wc = w + (long)c * kernel_size;
@@ -127,51 +142,98 @@ __global__ __launch_bounds__(1024) void conv1d_update_kernel(float* y, float* st
 // ---------------------------------------- conv1d + SiLU + q/k L2 normalise
 // The decode step's qwen3_5.cpp:513-531 for kernel size 4 and 128-wide key
 // heads, one workgroup per sequence: channels are [q heads | k heads | v],
-// each q/k head 128 channels.  Wave w takes the 128-channel blocks w, w+16,
-// ...; lane l computes channels 128*blk + l and 128*blk + 64 + l, so every
+// each q/k head 128 channels.  Wave w takes the 128-channel blocks w, w+nw,
+// ... (nw waves, at most 16); lane l computes channels 128*blk + l and 128*blk + 64 + l, so every
 // value is produced by the same operations in the same order as
 // anelm_conv1d_update, anelm_silu and anelm_l2_normalize (whose wave per
 // head sums element l, then l + 64, in lane l) produce it one after the other.
-__device__ __forceinline__ float conv4(const float* st, int pos, int i1, int i2, float xc, float4 wc, long c) {
-    const float* sc = st + c * 3;
-    const float sum = fmaf(sc[i2], wc.z, fmaf(sc[i1], wc.y, fmaf(sc[pos], wc.x, 0.0f)));
+// One channel's kernel-4 convolution: the three ring taps oldest first
+// (s0 at the ring position, then s1, s2), then the new input xc.
+__device__ __forceinline__ float conv4(float s0, float s1, float s2, float xc, float4 wc) {
+    const float sum = fmaf(s2, wc.z, fmaf(s1, wc.y, fmaf(s0, wc.x, 0.0f)));
     return fmaf(xc, wc.w, sum);
 }
 
+// Each wave takes the 128-channel blocks wv, wv + nw, ... of its sequence,
+// BPW at a time: the loads of all BPW blocks (clamped to the last block, so
+// they stay unconditional) go out before the first block's arithmetic, and
+// a channel's three ring taps are loaded at fixed offsets and picked by the
+// ring position afterwards.  The ring position is loaded after the first
+// pass's loads (a vector load: a scalar one was waited for, with the kernel
+// arguments, before any state load went out), so a sequence up to 64 blocks
+// costs one memory round trip.
+template <int BPW>
+struct ConvPass {
+    float xs[BPW][2], t0[BPW][2], t1[BPW][2], t2[BPW][2];
+    float4 wc[BPW][2];
+};
+
+template <int BPW>
 __global__ __launch_bounds__(1024) void conv_silu_l2_kernel(float* y, float* state, int32_t* state_pos, const float* x,
                                                             const float* w, int channels, int nq_ch, long ld_x,
                                                             long ld_y, long state_stride, float q_scale) {
     const long b = blockIdx.x;
-    int pos = state_pos[b];
-    pos = pos < 0 ? 0 : (pos >= 3 ? 0 : pos);   // keeps every access in the ring
-    const int i1 = pos + 1 == 3 ? 0 : pos + 1;
-    const int i2 = i1 + 1 == 3 ? 0 : i1 + 1;
     float* st = state + b * state_stride;
     const float* xb = x + b * ld_x;
     float* yb = y + b * ld_y;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nw = blockDim.x >> 6;
-    for (int blk = wv; blk < channels / 128; blk += nw) {   // uniform within the wave
-        const long c0 = (long)blk * 128 + lane, c1 = c0 + 64;
-        const float x0 = xb[c0], x1 = xb[c1];
-        const float4 w0 = *reinterpret_cast<const float4*>(w + c0 * 4);
-        const float4 w1 = *reinterpret_cast<const float4*>(w + c1 * 4);
-        float y0 = conv4(st, pos, i1, i2, x0, w0, c0);
-        float y1 = conv4(st, pos, i1, i2, x1, w1, c1);
-        st[c0 * 3 + pos] = x0;
-        st[c1 * 3 + pos] = x1;
-        y0 = y0 / (expf(-y0) + 1.0f);   // SiLU, qwen3_5.cpp:514
-        y1 = y1 / (expf(-y1) + 1.0f);
-        if (blk * 128 < 2 * nq_ch) {      // a q or k head: L2 normalise (x scale)
-            float ss = fmaf(y0, y0, 0.0f);
-            ss = fmaf(y1, y1, ss);
-            ss = wave_sum(ss);
-            const float norm = 1.0f / sqrtf(ss + 1e-12f);
-            const float scale = blk * 128 < nq_ch ? q_scale : 1.0f;
-            y0 = (y0 * norm) * scale;
-            y1 = (y1 * norm) * scale;
+    const int nblk = channels / 128;
+    auto load = [&](ConvPass<BPW>& P, int base) {
+#pragma unroll
+        for (int j = 0; j < BPW; j++) {
+            const int blk = base + j * nw + wv;
+            const long bc = blk < nblk ? blk : nblk - 1;
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const long c = bc * 128 + lane + 64 * h;
+                P.xs[j][h] = xb[c];
+                P.wc[j][h] = *reinterpret_cast<const float4*>(w + c * 4);
+                P.t0[j][h] = st[c * 3];
+                P.t1[j][h] = st[c * 3 + 1];
+                P.t2[j][h] = st[c * 3 + 2];
+            }
         }
-        yb[c0] = y0;
-        yb[c1] = y1;
+    };
+    auto compute = [&](const ConvPass<BPW>& P, int base, int pos) {
+#pragma unroll
+        for (int j = 0; j < BPW; j++) {
+            const int blk = base + j * nw + wv;
+            if (blk >= nblk) break;   // uniform within the wave
+            float yv[2];
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const long c = (long)blk * 128 + lane + 64 * h;
+                // taps oldest first: ring slots pos, pos + 1, pos + 2 (mod 3)
+                const float a0 = P.t0[j][h], a1 = P.t1[j][h], a2 = P.t2[j][h];
+                const float o0 = pos == 0 ? a0 : (pos == 1 ? a1 : a2);
+                const float o1 = pos == 0 ? a1 : (pos == 1 ? a2 : a0);
+                const float o2 = pos == 0 ? a2 : (pos == 1 ? a0 : a1);
+                const float yc = conv4(o0, o1, o2, P.xs[j][h], P.wc[j][h]);
+                st[c * 3 + pos] = P.xs[j][h];
+                yv[h] = yc / (expf(-yc) + 1.0f);   // SiLU, qwen3_5.cpp:514
+            }
+            if (blk * 128 < 2 * nq_ch) {   // a q or k head: L2 normalise (x scale)
+                float ss = fmaf(yv[0], yv[0], 0.0f);
+                ss = fmaf(yv[1], yv[1], ss);
+                ss = wave_sum(ss);
+                const float norm = 1.0f / sqrtf(ss + 1e-12f);
+                const float scale = blk * 128 < nq_ch ? q_scale : 1.0f;
+                yv[0] = (yv[0] * norm) * scale;
+                yv[1] = (yv[1] * norm) * scale;
+            }
+            yb[(long)blk * 128 + lane] = yv[0];
+            yb[(long)blk * 128 + lane + 64] = yv[1];
+        }
+    };
+    ConvPass<BPW> P;
+    load(P, 0);
+    int pos = __hip_atomic_load(state_pos + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_sched_barrier(0);
+    pos = pos < 0 ? 0 : (pos >= 3 ? 0 : pos);   // keeps every access in the ring
+    compute(P, 0, pos);
+    for (int base = nw * BPW; base < nblk; base += nw * BPW) {   // past 64 blocks: more passes
+        load(P, base);
+        compute(P, base, pos);
     }
     __syncthreads();
     if (threadIdx.x == 0) state_pos[b] = pos + 1 == 3 ? 0 : pos + 1;
@@ -484,9 +546,24 @@ extern "C" int anelm_conv1d_silu_l2norm(float* y, float* conv_state, int32_t* st
         return fail(ANELM_ERR_INVALID, "conv1d_silu_l2norm: strides overlap");
     if (!aligned16(w)) return fail(ANELM_ERR_INVALID, "conv1d_silu_l2norm: w not 16-byte aligned");
     if (batch == 0) return ANELM_OK;
-    const int waves = channels / 128 < 16 ? channels / 128 : 16;
-    hipLaunchKernelGGL(conv_silu_l2_kernel, dim3(batch), dim3(64 * waves), 0, as_stream(stream), y, conv_state,
-                       state_pos, x, w, channels, n_key_heads * 128, ld_x, ld_y, state_stride, q_scale);
+    const int nblk = channels / 128;
+    const int waves = nblk < 16 ? nblk : 16;
+    const int bpw = (nblk + waves - 1) / waves;   // blocks per wave: one pass up to 4, more passes past that
+    const dim3 grid((unsigned)batch), block((unsigned)(64 * waves));
+    hipStream_t st = as_stream(stream);
+    const int nq_ch = n_key_heads * 128;
+    if (bpw <= 1)
+        conv_silu_l2_kernel<1><<<grid, block, 0, st>>>(y, conv_state, state_pos, x, w, channels, nq_ch, ld_x, ld_y,
+                                                       state_stride, q_scale);
+    else if (bpw == 2)
+        conv_silu_l2_kernel<2><<<grid, block, 0, st>>>(y, conv_state, state_pos, x, w, channels, nq_ch, ld_x, ld_y,
+                                                       state_stride, q_scale);
+    else if (bpw == 3)
+        conv_silu_l2_kernel<3><<<grid, block, 0, st>>>(y, conv_state, state_pos, x, w, channels, nq_ch, ld_x, ld_y,
+                                                       state_stride, q_scale);
+    else
+        conv_silu_l2_kernel<4><<<grid, block, 0, st>>>(y, conv_state, state_pos, x, w, channels, nq_ch, ld_x, ld_y,
+                                                       state_stride, q_scale);
     return launch_status("conv1d_silu_l2norm");
 }
 

@@ -146,7 +146,10 @@ def test_head_slices_of_fused_rows(hip, orc, rng):
     assert max_rel_err(host(out), ref) <= REL_TOL
 
 
-@pytest.mark.parametrize("B,nkh,nvh,steps", [(1, 16, 16, 5), (64, 16, 16, 4), (3, 2, 4, 7), (2, 0, 3, 2)])
+# 128-channel blocks per sequence: 48 (3 per wave of 16), 8 and 3 (one each),
+# 24 (2 per wave), 56 (4 per wave) and 104 (two passes of up to 4 per wave)
+@pytest.mark.parametrize("B,nkh,nvh,steps", [(1, 16, 16, 5), (64, 16, 16, 4), (3, 2, 4, 7), (2, 0, 3, 2),
+                                             (2, 8, 8, 3), (3, 16, 24, 3), (2, 32, 40, 4)])
 def test_conv_silu_l2norm_matches_separate_calls(hip, rng, B, nkh, nvh, steps):
     """The fused conv1d update + SiLU + q/k L2 norm equals anelm_conv1d_update,
     anelm_silu and two anelm_l2_normalize calls bit for bit (outputs, ring
