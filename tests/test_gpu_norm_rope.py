@@ -362,3 +362,53 @@ def test_kv_ring_advance_layers(hip, rng):
         hip.kv_ring_append(kc, kc.clone(), r_s, r_l, kv, kv)
         assert np.array_equal(host(rs)[l, :B], host(r_s)) and np.array_equal(host(rl)[l, :B], host(r_l))
     assert np.array_equal(host(rs)[:, B:], rs0[:, B:]) and np.array_equal(host(rl)[:, B:], rl0[:, B:])
+
+
+@pytest.mark.parametrize("dim", [1024, 4096])
+@pytest.mark.parametrize("kind", ["f32", "f16", "tiled", "add", "add_inplace"])
+def test_rmsnorm_many_rows_same_bits(hip, orc, rng, dim, kind):
+    """8192 rows and 512 rows get the same launch geometry (the row count
+    picks the lanes per row, the same from 256 rows up), so the same rows
+    must come out with the same bits, whatever the grid size; and the rows
+    match the oracle."""
+    import torch
+
+    rows = 8192
+    x = rng.standard_normal((rows, dim), dtype=np.float32)
+    y = rng.standard_normal((rows, dim), dtype=np.float32)
+    wt, w32 = _gamma(rng, dim, "f16")
+
+    def run(n):
+        xs = dev(x[:n].copy())
+        if kind == "f32":
+            o = torch.empty(n, dim, device="cuda")
+            hip.rmsnorm(o, xs, wt, EPS)
+            return host(o), None
+        if kind == "f16":
+            o = torch.empty(n, dim, dtype=torch.int16, device="cuda")
+            hip.rmsnorm_f16(o, xs, wt, EPS)
+            return host(o), None
+        if kind == "tiled":
+            o = torch.zeros(hip.proj_tiled_size(n, dim) // 2, dtype=torch.int16, device="cuda")
+            hip.rmsnorm_f16_tiled(o, xs, wt, EPS)
+            return host(o), None
+        ys = dev(y[:n].copy())
+        if kind == "add":
+            o = torch.empty(n, dim, device="cuda")
+            hip.add_rmsnorm(xs, ys, o, wt, EPS)
+            return host(o), host(xs)
+        hip.add_rmsnorm(xs, ys, ys, wt, EPS)   # out aliases y, same pitch
+        return host(ys), host(xs)
+
+    big, big_x = run(rows)
+    small, small_x = run(512)
+    if kind == "tiled":
+        assert_bitexact(big[: small.size], small, "tiled rmsnorm: 8192 rows vs 512")
+    else:
+        assert_bitexact(big[:512], small, f"{kind}: 8192 rows vs 512")
+    if big_x is not None:
+        assert_bitexact(big_x[:512], small_x, f"{kind}: updated x, 8192 rows vs 512")
+        assert_bitexact(big_x, x + y, f"{kind}: updated x")
+    if kind in ("f32", "add", "add_inplace"):
+        src = x + y if kind != "f32" else x
+        assert max_rel_err(big, orc.rmsnorm_rows(src, w32, EPS)) <= REL_TOL
