@@ -51,6 +51,7 @@ _SIGS = {
     "anelm_last_error": (ctypes.c_char_p, []),
     "anelm_version": (_I, []),
     "anelm_rmsnorm": (_I, [_P, _P, _P, _I, _L, _I, _L, _L, _F, _P]),
+    "anelm_rmsnorm_geometry": (_I, [_L, _I, ctypes.POINTER(_I), ctypes.POINTER(_I)]),
     "anelm_rmsnorm_f16": (_I, [_P, _P, _P, _I, _L, _I, _L, _L, _F, _P]),
     "anelm_rmsnorm_f16_tiled": (_I, [_P, _P, _P, _I, _L, _I, _L, _F, _P]),
     "anelm_add_rmsnorm": (_I, [_P, _P, _P, _P, _I, _L, _I, _L, _L, _L, _F, _P]),
@@ -193,6 +194,14 @@ def rmsnorm(out, x, w, eps=1e-6, stream=None):
     _, _, ldo = _rows(out)
     _check(lib().anelm_rmsnorm(_ptr(out), _ptr(x), _ptr(w), _dtype_code(w), rows, dim, ldx, ldo, eps,
                                _stream(stream)))
+
+
+def rmsnorm_geometry(rows, dim):
+    """(float4 per lane, lanes per row) that rmsnorm and layer_ops launch
+    with for rows of dim floats; (0, 256) for the any-shape kernel."""
+    nv, thr = _I(), _I()
+    _check(lib().anelm_rmsnorm_geometry(rows, dim, ctypes.byref(nv), ctypes.byref(thr)))
+    return nv.value, thr.value
 
 
 def rmsnorm_f16(out16, x, w, eps=1e-6, stream=None):

@@ -479,8 +479,10 @@ __global__ __launch_bounds__(kAttnThreads) void gqa_decode_kernel(AttnArgs a) {
         // partials were written and are read with device-scope accesses,
         // which bypass the non-coherent per-XCD L2 (a device-scope fence
         // here would write back the whole L2).
+        // A bounded launch can hold fewer chunks than a ring longer than its
+        // bound needs: then the nsplit launched chunks are the live ones.
         __shared__ int s_last;
-        const int live = (len + a.chunk - 1) / a.chunk;
+        const int live = min((len + a.chunk - 1) / a.chunk, a.nsplit);
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
         if (tid == 0) {
@@ -571,17 +573,42 @@ void launch_d(AttnArgs a, long batch, hipStream_t st) {
     }
 }
 
-// Split launches: the partials, then (256-byte aligned) one counter per
-// (sequence, kv head).
+// Split launches: the partials from the workspace's start, and one counter
+// per (sequence, kv head) in a region whose place depends on the workspace's
+// size alone: its last 64th, from a 256-byte boundary.  Every call given the
+// same workspace and size therefore finds each counter at the same address,
+// left at zero by the calls before, whatever its batch, chunking or ring
+// lengths, and no call's partials reach into the region (checked per call).
 size_t partial_bytes(long batch, int nh, int nsplit, int D) {
     return ((size_t)batch * nh * nsplit * (D + 2) * sizeof(float) + 255) & ~(size_t)255;
 }
+size_t ctr_offset(size_t ws_bytes) { return (ws_bytes - ws_bytes / 64) & ~(size_t)255; }
+size_t ctr_slots(size_t ws_bytes) { return (ws_bytes - ctr_offset(ws_bytes)) / sizeof(unsigned); }
 
+// A size that serves every call with at most `batch` sequences and a ring
+// bound of at most `cap`.  The chunk follows the batch (pick_chunk), so a
+// smaller batch can need more partials than the largest one: the maximum is
+// taken over the batches up to `batch`.  Past the batch at which the chunk
+// reaches its maximum the partials only grow with the batch, so the loop
+// stops there and `batch` itself is counted last.
 size_t ws_bytes_for(long batch, int nh, int nkv, int D, int cap) {
-    const int chunk = pick_chunk(batch * nkv, cap);
-    const long nsplit = (cap + chunk - 1) / chunk;
-    if (nsplit <= 1) return 0;
-    return partial_bytes(batch, nh, (int)nsplit, D) + (size_t)batch * nkv * sizeof(unsigned);
+    size_t P = 0;
+    auto count = [&](long b) {
+        const int chunk = pick_chunk(b * nkv, cap);
+        const long nsplit = (cap + chunk - 1) / chunk;
+        if (nsplit > 1) {
+            const size_t pb = partial_bytes(b, nh, (int)nsplit, D);
+            P = pb > P ? pb : P;
+        }
+    };
+    for (long b = 1; b < batch && pick_chunk(b * nkv, cap) < kMaxChunk; b++) count(b);
+    count(batch);
+    if (P == 0) return 0;
+    const size_t pairs = (size_t)batch * nkv;
+    size_t S = (((P + 256) * 64 / 63 + 256) + 255) & ~(size_t)255;
+    if (S < 256 * pairs) S = 256 * pairs;
+    while (ctr_offset(S) < P || ctr_slots(S) < pairs) S += 256;
+    return S;
 }
 
 int check_common(const void* out, const void* q, const void* kc, const void* vc, long batch, int nh, int nkv,
@@ -612,11 +639,12 @@ int run(AttnArgs a, long batch, int D, int bound, void* ws, size_t ws_bytes, hip
     a.whole = a.chunk > kWholeRows ? a.chunk : kWholeRows;   // <= kMaxChunk, the LDS score rows
     if (a.nsplit > 1) {
         const size_t pb = partial_bytes(batch, a.nh, a.nsplit, D);
-        const size_t need = pb + (size_t)batch * a.nkv * sizeof(unsigned);
-        if (!ws || ws_bytes < need)
-            return fail(ANELM_ERR_WORKSPACE, "gqa_attention: workspace of %zu bytes needed, %zu given", need, ws_bytes);
+        if (!ws || pb > ctr_offset(ws_bytes) || (size_t)batch * a.nkv > ctr_slots(ws_bytes))
+            return fail(ANELM_ERR_WORKSPACE,
+                        "gqa_attention: workspace of %zu bytes too small for %zu bytes of partials and %ld counters",
+                        ws_bytes, pb, batch * a.nkv);
         if (!aligned16(ws)) return fail(ANELM_ERR_INVALID, "gqa_attention: workspace not 16-byte aligned");
-        a.ctr = reinterpret_cast<unsigned*>(static_cast<char*>(ws) + pb);
+        a.ctr = reinterpret_cast<unsigned*>(static_cast<char*>(ws) + ctr_offset(ws_bytes));
     }
     a.ws = static_cast<float*>(ws);
     if (batch == 0) return ANELM_OK;

@@ -475,6 +475,19 @@ extern "C" int anelm_rmsnorm(float* out, const float* x, const void* w, int w_dt
                                  ld_out, eps, as_stream(stream));
 }
 
+extern "C" int anelm_rmsnorm_geometry(long rows, int dim, int* float4_per_lane, int* threads) {
+    if (!float4_per_lane || !threads) return fail(ANELM_ERR_INVALID, "anelm_rmsnorm_geometry: null pointer");
+    if (rows <= 0 || dim <= 0) return fail(ANELM_ERR_INVALID, "anelm_rmsnorm_geometry: rows=%ld dim=%d", rows, dim);
+    clear_error();
+    if (dim % 4 == 0 && dim / 4 <= 1024 * 4) {
+        rms_row_geometry(rows, dim / 4, *float4_per_lane, *threads);
+    } else {
+        *float4_per_lane = 0;   // the any-shape kernel: 256 threads, two passes
+        *threads = 256;
+    }
+    return ANELM_OK;
+}
+
 extern "C" int anelm_rmsnorm_f16(uint16_t* out16, const float* x, const void* w, int w_dtype, long rows, int dim,
                                  long ld_x, long ld_out, float eps, void* stream) {
     if (!out16 || !x || !w) return fail(ANELM_ERR_INVALID, "anelm_rmsnorm_f16: null pointer");

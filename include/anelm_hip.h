@@ -68,6 +68,13 @@ int anelm_version(void);
 int anelm_rmsnorm(float* out, const float* x, const void* w, int w_dtype, long rows, int dim,
                   long ld_x, long ld_out, float eps, void* stream);
 
+/* The launch geometry that anelm_rmsnorm (16-byte aligned rows) and
+ * anelm_layer_ops choose for `rows` rows of `dim` floats: float4 values per
+ * lane and lanes per row; 0 float4 per lane names the any-shape kernel (dim
+ * not a multiple of 4 or above 16384).  The geometry fixes the order of the
+ * sum of squares.  Launches nothing.  No counterpart in the reference. */
+int anelm_rmsnorm_geometry(long rows, int dim, int* float4_per_lane, int* threads);
+
 /* anelm_rmsnorm with the result rounded to fp16 (nearest even), the ANE
  * kernels' input conversion (core/ane_runtime.cpp:604-612) fused into the
  * norm: out16 = fp16(rmsnorm(x) * w), the same fp32 values as anelm_rmsnorm
@@ -300,10 +307,14 @@ int anelm_kv_ring_append(float* k_cache, float* v_cache, int32_t* ring_start, in
  * strides that are multiples of 4.  Needs
  * anelm_gqa_workspace_size(batch, n_heads, n_kv_heads, head_dim, capacity)
  * bytes of device workspace (0 is possible: then workspace may be NULL),
- * zero-filled before its first use (e.g. hipMemset once after allocating):
- * it holds per-(sequence, kv head) counters of the chunks of a long ring,
- * which every call leaves at zero.  Calls that share a workspace must not
- * overlap. */
+ * zero-filled before its first use (e.g. hipMemset once after allocating).
+ * That size serves every call with at most `batch` sequences and rings of at
+ * most `capacity` rows.  The workspace's last 64th holds per-(sequence, kv
+ * head) counters of the chunks of a long ring, at addresses that depend only
+ * on workspace_bytes; no call writes partial results there and every call
+ * leaves them at zero, so one workspace, passed with the same
+ * workspace_bytes, serves calls of any batch, bound or ring length in any
+ * order.  Calls that share a workspace must not overlap. */
 size_t anelm_gqa_workspace_size(long batch, int n_heads, int n_kv_heads, int head_dim, int capacity);
 int anelm_gqa_attention(float* out, const float* q, const float* k_cache, const float* v_cache,
                         const int32_t* ring_start, const int32_t* ring_len, long batch, int n_heads,

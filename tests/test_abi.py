@@ -163,13 +163,32 @@ def test_attention_argument_checks(lib):
     fake = P(0x1000)
     ws = lib.anelm_gqa_workspace_size
     # the chunk is 512 positions once there are >= 2048 workgroups, else it
-    # shrinks towards 64; the partials (rounded up to 256 bytes), then one
-    # counter per (sequence, kv head)
+    # shrinks towards 64; a call's partials (rounded up to 256 bytes) sit
+    # below the counter region, the workspace's last 64th from a 256-byte
+    # boundary, which holds one counter per (sequence, kv head).  The size
+    # for a batch serves every smaller batch.
     up = lambda n: (n + 255) // 256 * 256
-    assert ws(64, 32, 8, 128, 2048) == up(64 * 32 * 4 * 130 * 4) + 64 * 8 * 4
-    assert ws(1, 32, 8, 128, 2048) == up(32 * 32 * 130 * 4) + 8 * 4
-    assert ws(3, 12, 4, 64, 1000) == up(3 * 12 * 16 * 66 * 4) + 3 * 4 * 4
-    assert ws(512, 16, 8, 128, 512) == 0                        # one chunk: no partials
+
+    def chunk(b, nkv, cap):
+        for c in (512, 256, 128):
+            if b * nkv * -(-cap // c) >= 2048:
+                return c
+        return 64
+
+    def partials(b, nh, nkv, d, cap):
+        ns = -(-cap // chunk(b, nkv, cap))
+        return up(b * nh * ns * (d + 2) * 4) if ns > 1 else 0
+
+    for B, nh, nkv, d, cap in ((64, 32, 8, 128, 2048), (1, 32, 8, 128, 2048), (3, 12, 4, 64, 1000),
+                               (4, 32, 8, 128, 32768), (200, 16, 8, 128, 4096)):
+        n = ws(B, nh, nkv, d, cap)
+        region = (n - n // 64) & ~255
+        assert max(partials(b, nh, nkv, d, cap) for b in range(1, B + 1)) <= region
+        assert (n - region) // 4 >= B * nkv
+        assert n <= 1.05 * max(partials(b, nh, nkv, d, cap) for b in range(1, B + 1)) + 1024   # about 1/63 more
+    assert partials(3, 32, 8, 128, 32768) > partials(4, 32, 8, 128, 32768)   # a smaller batch needing more
+    assert ws(512, 16, 8, 128, 512) > 0                         # one chunk at 512 sequences, not at fewer
+    assert ws(4, 16, 8, 128, 64) == 0                           # one chunk at any batch: no partials
     assert ws(0, 32, 8, 128, 2048) == 0
     g = lib.anelm_gqa_attention
     ok = dict(q_ld=32 * 128, qs=128, out_ld=32 * 128, cap=2048, seq=2048 * 8 * 128)
@@ -257,3 +276,18 @@ def test_deltanet_argument_checks(lib):
     assert b"key_dim" in lib.anelm_last_error() or b"multiple" in lib.anelm_last_error()
     assert lib.anelm_matvec(None, fake, fake, 4, 4, None) == -1
     assert lib.anelm_matvec(fake, fake, fake, 4, 0, None) == -1
+
+
+def test_rmsnorm_geometry_at_the_workload_shapes():
+    """The row geometry (float4 per lane, lanes per row) that fixes the
+    RMSNorm's summation order, at the decode and prefill shapes; a pure host
+    query, so it runs here."""
+    import anelm
+
+    assert anelm.rmsnorm_geometry(1, 1024) == (1, 256)        # 0.6B decode: one float4 per lane
+    assert anelm.rmsnorm_geometry(64, 2560) == (1, 640)       # 4B batched decode
+    assert anelm.rmsnorm_geometry(2048, 1024) == (2, 128)     # 0.6B prefill
+    assert anelm.rmsnorm_geometry(8192, 4096) == (2, 512)     # 8B prefill
+    assert anelm.rmsnorm_geometry(4, 1022) == (0, 256)        # not a multiple of 4: the any-shape kernel
+    with pytest.raises(anelm.AnelmError):
+        anelm.rmsnorm_geometry(0, 1024)

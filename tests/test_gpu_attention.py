@@ -216,3 +216,99 @@ def test_append_then_attend_decode_loop(hip, orc, rng):
         for b in range(B):
             orc.kv_ring_append(kc[b], vc[b], k[b], v[b], st[b])
             check(got[b], q[b], kc[b], vc[b], nq, nk, D, int(st[b, 0]), int(st[b, 1]), orc)
+
+
+def _ctr_region(ws_bytes):
+    """The attention workspace's counter region: its last 64th, from a
+    256-byte boundary (fixed by the workspace's size alone)."""
+    return (ws_bytes - ws_bytes // 64) & ~255
+
+
+def test_workspace_reuse_across_shapes(hip, orc, rng):
+    """One workspace, sized for 64 sequences, serves a sequence of calls
+    whose batch, chunking and ring lengths change (64, 1, 3 sequences; the
+    ring form at a long, a short and again a long cache_len; a bounded call;
+    64 again): every call against the oracle, and the counters are all back
+    at zero at the end."""
+    import torch
+
+    nq, nk, D, cap = 32, 8, 128, 2048
+    n = hip.gqa_workspace_size(64, nq, nk, D, cap)
+    ws = torch.zeros(n, dtype=torch.uint8, device="cuda")
+
+    def batched_call(B, lens):
+        starts = rng.integers(0, cap, B).astype(np.int32)
+        lens = np.asarray(lens, np.int32)
+        q = rng.standard_normal((B, nq * D)).astype(np.float32)
+        kc = rng.standard_normal((B, cap, nk * D)).astype(np.float32)
+        vc = rng.standard_normal((B, cap, nk * D)).astype(np.float32)
+        out = torch.full((B, nq * D), float("nan"), device="cuda")
+        hip.gqa_attention(out, dev(q), dev(kc), dev(vc), dev(starts), dev(lens), nq, nk, D, ws)
+        got = host(out).reshape(B, nq, D)
+        for b in list(range(min(B, 4))) + [B - 1]:
+            check(got[b], q[b], kc[b], vc[b], nq, nk, D, int(starts[b]), int(lens[b]), orc)
+
+    def ring_call_ws(length):
+        q = rng.standard_normal(nq * D).astype(np.float32)
+        kc = rng.standard_normal((cap, nk * D)).astype(np.float32)
+        vc = rng.standard_normal((cap, nk * D)).astype(np.float32)
+        out = torch.full((nq, D), float("nan"), device="cuda")
+        hip.gqa_attention_ring(out, dev(q), dev(kc), dev(vc), nq, nk, D, 7, length, ws)
+        check(host(out), q, kc, vc, nq, nk, D, 7, length, orc)
+
+    batched_call(64, rng.integers(129, cap + 1, 64))
+    batched_call(1, [cap])
+    batched_call(3, [1500, 200, cap])
+    ring_call_ws(cap)
+    ring_call_ws(300)
+    ring_call_ws(cap)
+    batched_call(64, rng.integers(129, cap + 1, 64))
+    batched_call(2, [999, 130])
+    torch.cuda.synchronize()
+    ctr = host(ws)[_ctr_region(n):]
+    assert not ctr.any(), "counters left non-zero"
+
+
+def test_bounded_launch_ring_past_bound(hip, orc, rng):
+    """A bounded launch given a ring longer than its bound attends over the
+    launched chunks' positions only: one sequence, 8 kv heads and capacity
+    2048 give 64-position chunks, so a bound of 200 launches 4 chunks and a
+    700-row ring is attended over its first 256 positions.  The counters are
+    left at zero: a full call on the same workspace afterwards is right."""
+    import torch
+
+    nq, nk, D, cap = 16, 8, 128, 2048
+    n = hip.gqa_workspace_size(1, nq, nk, D, cap)
+    ws = torch.zeros(n, dtype=torch.uint8, device="cuda")
+    q = rng.standard_normal(nq * D).astype(np.float32)
+    kc = rng.standard_normal((cap, nk * D)).astype(np.float32)
+    vc = rng.standard_normal((cap, nk * D)).astype(np.float32)
+    out = torch.full((1, nq * D), float("nan"), device="cuda")
+    start = 1900
+    hip.gqa_attention_bounded(out, dev(q[None]), dev(kc[None]), dev(vc[None]), dev(np.array([start], np.int32)),
+                              dev(np.array([700], np.int32)), nq, nk, D, 200, ws)
+    check(host(out).reshape(nq, D), q, kc, vc, nq, nk, D, start, 256, orc)
+    for length in (700, 2048):
+        hip.gqa_attention(out, dev(q[None]), dev(kc[None]), dev(vc[None]), dev(np.array([start], np.int32)),
+                          dev(np.array([length], np.int32)), nq, nk, D, ws)
+        check(host(out).reshape(nq, D), q, kc, vc, nq, nk, D, start, length, orc)
+    torch.cuda.synchronize()
+    assert not host(ws)[_ctr_region(n):].any(), "counters left non-zero"
+
+
+def test_workspace_size_covers_smaller_batches(hip):
+    """The size for a batch serves every smaller batch: the chunk grows with
+    the batch, so a smaller batch can need more partials (three sequences at
+    capacity 32768 need more than four)."""
+    import torch
+
+    nq, nk, D, cap = 32, 8, 128, 32768
+    n4 = hip.gqa_workspace_size(4, nq, nk, D, cap)
+    assert n4 >= hip.gqa_workspace_size(3, nq, nk, D, cap)
+    ws = torch.zeros(n4, dtype=torch.uint8, device="cuda")
+    q = torch.zeros(3, nq * D, device="cuda")
+    out = torch.empty(3, nq * D, device="cuda")
+    z = torch.zeros(3, dtype=torch.int32, device="cuda")    # empty rings: only the workspace check matters
+    caches = torch.zeros(3, cap, nk * D, device="cuda")
+    hip.gqa_attention(out, q, caches, caches, z, z, nq, nk, D, ws)
+    assert not host(out).any()

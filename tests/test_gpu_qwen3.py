@@ -411,16 +411,22 @@ def test_proj_fused_strided_rows(hip, orc, rng, B, out_dim, in_dim):
     assert np.all(got[:, :4] == -7.0) and np.all(got[:, 4 + out_dim:] == -7.0)
 
 
-def _decode_vs_oracle(hip, orc, rng, path, t, d, B, steps, cap=16, ld_pad=0):
+def _decode_vs_oracle(hip, orc, rng, path, t, d, B, steps, cap=16, ld_pad=0, model=None):
     """`steps` decode steps of B sequences through anelm_qwen3_forward
     against the oracle's step; logits land in a [B, V + ld_pad] buffer whose
-    padding columns must stay untouched.  Returns the worst row error
-    relative to the row's logit scale."""
+    padding columns must stay untouched.  With `model` given, that model
+    (loaded with capacity `cap` and at least B sequences) is reset and used
+    and left open.  Returns the worst row error relative to the row's logit
+    scale."""
     import torch
 
     cfg = hip.Qwen3Config(d["H"], d["L"], d["nq"], d["nk"], d["D"], d["I"], d["V"], 1e6, 1e-6)
     ocfg = orc.Qwen3Config(d["H"], d["L"], d["nq"], d["nk"], d["D"], d["I"], d["V"], 1e6, 1e-6)
-    model = hip.Qwen3Model(path, cfg, max_batch=B, kv_capacity=cap)
+    own = model is None
+    if own:
+        model = hip.Qwen3Model(path, cfg, max_batch=B, kv_capacity=cap)
+    else:
+        model.reset()
     ref = orc.Qwen3(ocfg, t, B, cap)
     V = d["V"]
     buf = torch.full((B, V + ld_pad), -3.0, device="cuda")
@@ -436,7 +442,8 @@ def _decode_vs_oracle(hip, orc, rng, path, t, d, B, steps, cap=16, ld_pad=0):
         assert np.all(got[:, V:] == -3.0), "logits padding written"
         err = np.max(np.abs(got[:, :V] - want), axis=1) / np.max(np.abs(want), axis=1)
         worst = max(worst, float(err.max()))
-    model.close()
+    if own:
+        model.close()
     return worst
 
 
@@ -454,9 +461,9 @@ def test_decode_big_vocab_past_16_rows(hip, orc, rng, tmp_path, B, ld_pad):
 @pytest.mark.parametrize("B,steps", [(1, 200), (3, 170), (20, 170)])
 def test_decode_long_rings_match_oracle(hip, orc, rng, tmp_path, B, steps):
     """Rings longer than one attention chunk: at capacity 160 the rings pass
-    128 rows (from then on the attention splits each over 5 chunks of 32
-    whose partials a second launch merges), fill up and wrap.  Every step
-    against the oracle."""
+    128 rows (from then on the attention splits each over 3 chunks of 64,
+    and the last chunk to finish merges the partials in-kernel), fill up and
+    wrap.  Every step against the oracle."""
     t, d = tiny_qwen3(rng)
     path = tmp_path / "long.safetensors"
     save_qwen3(path, t)
@@ -472,3 +479,22 @@ def test_decode_dims_not_multiples_of_32(hip, orc, rng, tmp_path, B):
     path = tmp_path / "odd.safetensors"
     save_qwen3(path, t)
     assert _decode_vs_oracle(hip, orc, rng, path, t, d, B, steps=18, cap=16, ld_pad=8) < 4e-3
+
+
+def test_decode_workspace_reuse_across_batches(hip, orc, rng, tmp_path):
+    """One model, so one attention workspace, sized for 64 sequences: 140
+    steps of 64 sequences (the rings pass 128 rows and split into chunks
+    from then on), then after a reset 140 steps of one sequence and 135 of
+    three, each phase against a fresh oracle.  A batch change moves the
+    chunking and the partials; the chunk counters must stay where every call
+    finds them zeroed."""
+    t, d = tiny_qwen3(rng)
+    path = tmp_path / "reuse.safetensors"
+    save_qwen3(path, t)
+    cfg = hip.Qwen3Config(d["H"], d["L"], d["nq"], d["nk"], d["D"], d["I"], d["V"], 1e6, 1e-6)
+    model = hip.Qwen3Model(path, cfg, max_batch=64, kv_capacity=160)
+    try:
+        for B, steps in ((64, 140), (1, 140), (3, 135)):
+            assert _decode_vs_oracle(hip, orc, rng, path, t, d, B, steps, cap=160, model=model) < 4e-3, B
+    finally:
+        model.close()
