@@ -9,11 +9,13 @@
 //   x       = x + mlp                               (:527)
 // The three parts share no data, so the grid is three block ranges and no
 // block waits for another:
-//   - one block per token row for the x chain, with the lane layout of the
-//     separate row RMSNorm (rms_row_geometry), so both norms sum their
+//   - the x chain, one token row per rms_row_geometry lane group (a block,
+//     or each wave of a block when the geometry gives one wave per row), with
+//     the lane layout of the separate row RMSNorm, so both norms sum their
 //     squares in the same order and every output has the separate kernels'
 //     bits; x is read once and its final value (x + attn + mlp) written at
-//     once; both norms' sums share one LDS exchange and barrier;
+//     once; both norms' sums share one LDS exchange and barrier (none for a
+//     one-wave row);
 //   - the q/k heads, 16 lanes per head (norm_rope128_w, the separate
 //     kernel's arithmetic); with nq and nk multiples of 8 each wave takes 8
 //     heads of one token, so its position is a scalar load and every load of
@@ -47,20 +49,27 @@ struct LayerArgs {
     int nq, nk;
     long T;
     long n4;          // float4 of the SwiGLU (T * I / 4)
+    int row_threads;  // lanes per token row (rms_row_geometry)
+    int rows_per_block;  // blockDim.x / row_threads (> 1 only for one-wave rows)
     int row_blocks;   // [0, row_blocks): x chain
     int qk_blocks;    // then the q/k heads
     float eps;
 };
 
 // One token row's x chain; lane layout and reduction order of
-// rmsnorm_row_kernel<NV, DT, ...> with blockDim.x lanes.  FULL: every lane
-// holds NV float4 of the row (hidden == 4 * NV * blockDim.x, every Qwen3
+// rmsnorm_row_kernel<NV, DT, ...> with a.row_threads lanes.  FULL: every lane
+// holds NV float4 of the row (hidden == 4 * NV * row_threads, every Qwen3
 // shape), so nothing is guarded; a guarded store let the compiler sink the
 // mlp load, its only use, into the guard, behind a wait for the others.
+// With several rows per block each row is one wave (no LDS exchange, no
+// barrier), and a wave past the last row returns at once.
 template <int NV, int DT, bool FULL>
-__device__ __forceinline__ void x_chain(const LayerArgs& a, long row) {
+__device__ __forceinline__ void x_chain(const LayerArgs& a, long blk) {
     __shared__ float part[2][16];
-    const int tid = threadIdx.x, nthr = blockDim.x, nw = nthr >> 6;
+    const int nthr = a.row_threads, nw = nthr >> 6;
+    const int tid = a.rows_per_block > 1 ? (int)(threadIdx.x & 63) : (int)threadIdx.x;
+    const long row = blk * a.rows_per_block + (a.rows_per_block > 1 ? (long)(threadIdx.x >> 6) : 0L);
+    if (row >= a.T) return;   // a whole wave of the last block (one row per block: blk < T always)
     const int dim = a.H;
     float* xr = a.x + row * dim;
     const float* ar = a.attn + row * dim;
@@ -240,7 +249,7 @@ __global__ __launch_bounds__(1024) void layer_ops_kernel(LayerArgs a, const InvF
 template <int NV, int DT>
 void launch_layer(const LayerArgs& a, const InvFreq& inv, bool w8, int threads, int blocks, hipStream_t st) {
     const dim3 grd((unsigned)blocks), blk((unsigned)threads);
-    const bool full = a.H == 4 * NV * threads;
+    const bool full = a.H == 4 * NV * a.row_threads;
     if (w8 && full) layer_ops_kernel<NV, DT, true, true><<<grd, blk, 0, st>>>(a, inv);
     else if (w8) layer_ops_kernel<NV, DT, true, false><<<grd, blk, 0, st>>>(a, inv);
     else if (full) layer_ops_kernel<NV, DT, false, true><<<grd, blk, 0, st>>>(a, inv);
@@ -284,14 +293,19 @@ extern "C" int anelm_layer_ops(float* x, float* xn_in, float* xn_post, const flo
         !aligned16(q) || !aligned16(k) || !aligned16(h) || !aligned16(g) || !aligned16(u) || !wal ||
         !aligned16(cos_tab) || !aligned16(sin_tab))
         return fail(ANELM_ERR_INVALID, "%s: needs 16-byte aligned rows", fn);
-    int nv, threads;
-    rms_row_geometry(T, hidden / 4, nv, threads);
+    int nv, row_threads;
+    rms_row_geometry(T, hidden / 4, nv, row_threads);
+    // one-wave rows go four to a 256-lane block (the q/k and SwiGLU blocks
+    // take the same block size)
+    const int rpb = row_threads == 64 ? 4 : 1;
+    const int threads = row_threads * rpb;
     const bool w8 = nq % 8 == 0 && nk % 8 == 0;
     const long heads = T * (nq + nk);
     const long qk_blocks = w8 ? (heads / 8 + threads / 64 - 1) / (threads / 64) : (heads + threads / 16 - 1) / (threads / 16);
     const long n4 = T * inter / 4;
     const long silu_blocks = (n4 + 2L * threads - 1) / (2L * threads);
-    const long blocks = T + qk_blocks + silu_blocks;
+    const long row_blocks = (T + rpb - 1) / rpb;
+    const long blocks = row_blocks + qk_blocks + silu_blocks;
     if (blocks > 0x7FFFFFFFL) return fail(ANELM_ERR_INVALID, "%s: too large", fn);
     LayerArgs a;
     a.x = x;
@@ -317,7 +331,9 @@ extern "C" int anelm_layer_ops(float* x, float* xn_in, float* xn_post, const flo
     a.nk = nk;
     a.T = T;
     a.n4 = n4;
-    a.row_blocks = (int)T;
+    a.row_threads = row_threads;
+    a.rows_per_block = rpb;
+    a.row_blocks = (int)row_blocks;
     a.qk_blocks = (int)qk_blocks;
     a.eps = eps;
     InvFreq inv;

@@ -286,7 +286,8 @@ def test_rmsnorm_geometry_at_the_workload_shapes():
 
     assert anelm.rmsnorm_geometry(1, 1024) == (1, 256)        # 0.6B decode: one float4 per lane
     assert anelm.rmsnorm_geometry(64, 2560) == (1, 640)       # 4B batched decode
-    assert anelm.rmsnorm_geometry(2048, 1024) == (2, 128)     # 0.6B prefill
+    assert anelm.rmsnorm_geometry(2048, 1024) == (4, 64)      # 0.6B prefill: one wave per row
+    assert anelm.rmsnorm_geometry(2048, 512) == (2, 64)       # also one wave, two float4 per lane
     assert anelm.rmsnorm_geometry(8192, 4096) == (2, 512)     # 8B prefill
     assert anelm.rmsnorm_geometry(4, 1022) == (0, 256)        # not a multiple of 4: the any-shape kernel
     with pytest.raises(anelm.AnelmError):

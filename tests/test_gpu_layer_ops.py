@@ -1,8 +1,8 @@
 """anelm_layer_ops (a layer's five ops in one launch) against the five
 separate launches it replaces, bit for bit, over several layers at the
 decode and prefill-row shapes and at the two full prefill shapes (0.6B at
-2048 tokens, 8B at 8192 tokens, fp16 gammas: the two-float4-per-lane row
-geometry at 128 and 512 lanes), and the residual stream against the
+2048 tokens: one-wave rows, four to a block; 8B at 8192 tokens: two float4
+per lane at 512 lanes; fp16 gammas), and the residual stream against the
 oracle's per-token layer chain (models/llm/qwen3.cpp:502-528) on every row;
 the norm and SwiGLU outputs against the oracle within 1e-5 (every 64th row
 at the full prefill shapes)."""
@@ -21,8 +21,10 @@ THETA, EPS, D = 1e6, 1e-6, 128
     dict(name="0.6B prefill rows", T=64, H=1024, nq=16, nk=8, I=3072, pmax=2048, layers=2, wdt="bf16"),
     dict(name="8B prefill rows", T=16, H=4096, nq=32, nk=8, I=12288, pmax=8192, layers=2, wdt="f32"),
     dict(name="12+4 heads, ragged rows", T=5, H=2600, nq=12, nk=4, I=1000, pmax=40000, layers=2, wdt="f16"),
-    dict(name="0.6B prefill", T=2048, H=1024, nq=16, nk=8, I=3072, pmax=2048, layers=2, wdt="f16", geom=(2, 128),
+    dict(name="0.6B prefill", T=2048, H=1024, nq=16, nk=8, I=3072, pmax=2048, layers=2, wdt="f16", geom=(4, 64),
          stride=64),
+    dict(name="one-wave rows, ragged block", T=258, H=1024, nq=16, nk=8, I=3072, pmax=2048, layers=1, wdt="bf16",
+         geom=(4, 64)),
     dict(name="8B prefill", T=8192, H=4096, nq=32, nk=8, I=12288, pmax=8192, layers=1, wdt="f16", geom=(2, 512),
          stride=64),
 ], ids=lambda c: c["name"])
