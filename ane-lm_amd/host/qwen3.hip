@@ -2,8 +2,9 @@
 // models/llm/qwen3.cpp:497-564 with every activation kept in HBM, the
 // library's layer-op kernels between the contractions, and the ANE
 // contractions (core/ane_runtime.cpp:265-408: fused q|k|v, o_proj,
-// gate|up -> down, the LM head) as fp16 MFMA projections with fp32
-// accumulation (projection.hip; rocBLAS for shapes it does not take).  The
+// gate|up -> down, the LM head) as fp16 projections with fp32 accumulation,
+// all hand-written (projection.hip: dot kernels for a few rows, MFMA tiles
+// beyond, and an any-shape kernel; no vendor BLAS).  The
 // ANE's interface numerics are kept: weights are the truncating fp16 convert
 // of the bf16 checkpoint (the blobs), activations enter a projection as
 // round-to-nearest fp16 and leave it as fp16 (core/ane_runtime.cpp:600-640).

@@ -746,10 +746,13 @@ def cpu_convert(target_s):
 
 def dropin_per_call():
     """Per-call wall time of the unchanged-caller path: ane_lm::rmsnorm at
-    dim 1024 and 128 (and a layer's 40 head norms from 8 threads) and
-    ane_lm::sample_token at 151936, each a synchronous host-pointer call
-    through the drop-in layer, beside the oracle's single-thread CPU time of
-    the same function (tests/cpp/dropin_timing.cpp, built by build())."""
+    dim 1024 and 128 (and a layer's 40 head norms from 8 threads),
+    ane_lm::sample_token at 151936, and the additive entries
+    hip::qknorm_rope_qwen3 (a layer's 40 head norms + RoPE in one call),
+    hip::residual_add and hip::silu_mul at the Qwen3-8B per-token sizes, each
+    a synchronous host-pointer call through the drop-in layer, beside the
+    oracle's single-thread CPU time of the same function
+    (tests/cpp/dropin_timing.cpp, built by build())."""
     import subprocess
 
     exe = os.path.join(ROOT, "tests", "cpp", "dropin_timing")

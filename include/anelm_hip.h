@@ -362,9 +362,12 @@ int anelm_gqa_attention_qk(void* out, int out_f16, const float* q, const float* 
 /* anelm_gqa_attention for callers that know an upper bound on every ring's
  * length (len_bound >= ring_len[b] for all b; e.g. the tokens decoded since
  * the rings were emptied): only ceil(len_bound / chunk) chunks per sequence
- * are launched, and with one chunk no merge kernel runs.  A ring longer than
- * len_bound is only partly attended.  No counterpart in the reference (its
- * loop already runs over the live rows only, core/cpu_ops.cpp:186-188). */
+ * are launched (at least 64 positions each), and with one chunk the
+ * workgroup writes the output itself, with no partials to merge.  A ring
+ * longer than len_bound is attended over its first positions only: those of
+ * the launched chunks, whose last to finish merges them.  No counterpart in
+ * the reference (its loop already runs over the live rows only,
+ * core/cpu_ops.cpp:186-188). */
 int anelm_gqa_attention_bounded(float* out, const float* q, const float* k_cache, const float* v_cache,
                                 const int32_t* ring_start, const int32_t* ring_len, long batch, int n_heads,
                                 int n_kv_heads, int head_dim, long q_ld, int q_head_stride, long out_ld,

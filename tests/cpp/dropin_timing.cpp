@@ -6,6 +6,13 @@
 //   rmsnorm at dim 128 x 40  -- the per-head q/k norms of one layer from 8
 //                               threads at once, models/llm/qwen3.cpp:451-461
 //   sample_token at 151936   -- once per generated token, generate.cpp:80, :129
+// and the additive entries for the ops the reference performs inline, at the
+// Qwen3-8B per-token shapes, each beside the oracle's same function on one
+// thread:
+//   hip::qknorm_rope_qwen3, 32 q + 8 k heads -- a layer's 40 head norms and
+//                               RoPE in one call, models/llm/qwen3.cpp:444-472
+//   hip::residual_add at 4096 -- models/llm/qwen3.cpp:516, :527
+//   hip::silu_mul at 12288    -- the fused_ffn activation, core/ane_runtime.cpp:393-395
 // Prints one JSON line (microseconds per call: mean and median over the
 // timed calls).  Needs a GPU.
 #include <algorithm>
@@ -116,6 +123,39 @@ int main() {
         stop.store(true);
         for (auto& th : pool) th.join();
         put("rmsnorm_128_x40_heads_8_threads_per_layer", g, c, false);
+    }
+
+    // one token's 40 head norms + RoPE in one call (table row of position 1234)
+    {
+        const int nq = 32, nk = 8, hd = 128;
+        auto q = randv((size_t)nq * hd), k = randv((size_t)nk * hd), wq = randv(hd, 0.02f), wk = randv(hd, 0.02f);
+        for (auto& e : wq) e += 1.f;
+        for (auto& e : wk) e += 1.f;
+        std::vector<float> ctab((size_t)2048 * hd / 2), stab(ctab.size());
+        orc_rope_table(ctab.data(), stab.data(), 2048, hd, 1e6f);
+        const float* cr = &ctab[(size_t)1234 * hd / 2];
+        const float* sr = &stab[(size_t)1234 * hd / 2];
+        Stat g = time_calls([&] { ane_lm::hip::qknorm_rope_qwen3(q.data(), k.data(), nq, nk, hd, wq.data(), wk.data(),
+                                                                 1e-6f, 1234, 1e6f, cr, sr); }, 50, 2000);
+        const int32_t pos = 0;   // the row as a one-row table
+        Stat c = time_calls([&] { orc_qknorm_rope(q.data(), k.data(), (long)nq * hd, (long)nk * hd, wq.data(), wk.data(),
+                                                  &pos, cr, sr, 1, 1e6f, 1, nq, nk, hd, 1e-6f, 1); }, 200, 20000);
+        put("hip_qknorm_rope_qwen3_32q_8k", g, c, false);
+    }
+    {
+        const int n = 4096;
+        auto x = randv(n), y = randv(n);
+        Stat g = time_calls([&] { ane_lm::hip::residual_add(x.data(), y.data(), n); }, 50, 2000);
+        Stat c = time_calls([&] { orc_residual_add(x.data(), y.data(), (size_t)n, 1); }, 200, 20000);
+        put("hip_residual_add_4096", g, c, false);
+    }
+    {
+        const int n = 12288;
+        auto gt = randv(n), ut = randv(n);
+        std::vector<float> h(n);
+        Stat g = time_calls([&] { ane_lm::hip::silu_mul(h.data(), gt.data(), ut.data(), n); }, 50, 2000);
+        Stat c = time_calls([&] { orc_silu_mul(h.data(), gt.data(), ut.data(), (size_t)n, 1); }, 200, 20000);
+        put("hip_silu_mul_12288", g, c, false);
     }
 
     {
