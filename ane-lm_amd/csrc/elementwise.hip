@@ -159,6 +159,8 @@ __global__ __launch_bounds__(256) void bf16_to_f16_vec_kernel(uint4* dst, const 
 // cut into tiles of 256 * 8 * kU elements; workgroup w finds its tensor by a
 // binary search over the tile prefix (uniform, scalar) and converts its
 // tile, the last tile of a tensor also taking the n % 8 tail element-wise.
+// (A lookup in two rounds of independent scalar loads, every 8th entry then
+// 8 neighbours, measured slower: 5.84 against 5.35 ms for the 8B set.)
 constexpr int kCvtBatch = 128;
 struct CvtTable {
     const uint16_t* src[kCvtBatch];

@@ -1018,6 +1018,7 @@ __device__ void fill_walk_cache(WalkShared& sh, const SampleArgs& a, long row, i
 // evaluated (on wave-uniform values) and decided once at the end.
 __device__ __forceinline__ bool pass_crossing(uint32_t& cb, const uint32_t (&x)[kXWords], int pcls, float r) {
     const int info = (int)x[5];
+    if (info < 0) return false;   // no single crossing predicted (uniform: a scalar branch)
     const Binade b = binade_of(__uint_as_float(cb));
     const uint32_t inc = pick(Fn{x[0], x[1]}, b.m0);  // arithmetic select: an indexed one went to scratch
     const uint32_t mb = b.m0 + inc;  // m0 < 2^24, inc <= 2^30: no wrap
@@ -1295,9 +1296,13 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1))) void
             st += npass;
         }
         if (npass < 64 && st < a.nsub) {
-            // a predicted crossing passes in O(1); anything else is walked exactly
+            // a predicted crossing passes in O(1); anything else is walked
+            // exactly.  A stop whose map stays in the binade is the draw
+            // ending inside that map, which no crossing record can pass.
             bool passed = false;
-            if (all_cached) {  // the stopping lane's record, already loaded
+            const bool leaves = !((uint32_t)__builtin_amdgcn_readlane((int)inc, npass) < mhi - m0);
+            if (!leaves) {
+            } else if (all_cached) {  // the stopping lane's record, already loaded
                 uint32_t x[kXWords];
 #pragma unroll
                 for (int w = 0; w < kXWords; w++) x[w] = (uint32_t)__builtin_amdgcn_readlane((int)lx[w], npass);
