@@ -94,6 +94,8 @@ _SIGS = {
     "anelm_ssm_step_gated_norm": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _L, _I, _I, _I, _I, _L, _L, _L, _L,
                                        _L, _F, _P]),
     "anelm_conv1d_silu_l2norm": (_I, [_P, _P, _P, _P, _P, _L, _I, _I, _L, _L, _L, _F, _P]),
+    "anelm_conv_ssm_step_gated_norm": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _L, _I, _L, _L, _L, _L, _L,
+                                            _F, _F, _P]),
     "anelm_matvec": (_I, [_P, _P, _P, _L, _I, _P]),
     "anelm_st_open": (_P, [ctypes.c_char_p]),
     "anelm_st_close": (None, [_P]),
@@ -525,6 +527,25 @@ def conv1d_silu_l2norm(y, conv_state, state_pos, x, w, n_key_heads, q_scale, str
           conv_state.stride(1) == sl, "conv1d_silu_l2norm: shapes")
     _check(lib().anelm_conv1d_silu_l2norm(_ptr(y), _ptr(conv_state), _ptr(state_pos), _ptr(x), _ptr(w), B, ch,
                                           n_key_heads, _ld(x), _ld(y), conv_state.stride(0), q_scale, _stream(stream)))
+
+
+def conv_ssm_step_gated_norm(out, state, conv_state, head_pos, x, conv_w, decay, beta, z, norm_w, q_scale, eps=1e-6,
+                             stream=None):
+    """conv1d_silu_l2norm then ssm_step_gated_norm in one launch, key and value
+    heads of 128, as many key heads as value heads; head_pos: the ring
+    position per (sequence, head), int32 [B, n_heads]."""
+    B, nh, kd, vd = state.shape
+    ch = conv_state.shape[1]
+    _need(kd == 128 and vd == 128 and ch == 3 * nh * 128, "conv_ssm_step_gated_norm: heads of 128, channels")
+    _need(state.stride(3) == 1 and state.stride(2) == vd and state.stride(1) == kd * vd, "ssm_step: state layout")
+    _need(conv_state.shape == (B, ch, 3) and conv_state.stride(2) == 1 and conv_state.stride(1) == 3 and
+          conv_w.shape == (ch, 4) and conv_w.is_contiguous(), "conv_ssm_step_gated_norm: conv shapes")
+    _need(head_pos.numel() == B * nh and head_pos.is_contiguous() and decay.is_contiguous() and
+          beta.is_contiguous(), "conv_ssm_step_gated_norm: layouts")
+    _check(lib().anelm_conv_ssm_step_gated_norm(_ptr(out), _ptr(state), _ptr(conv_state), _ptr(head_pos), _ptr(x),
+                                                _ptr(conv_w), _ptr(decay), _ptr(beta), _ptr(z), _ptr(norm_w),
+                                                _dtype_code(norm_w), B, nh, _ld(x), _ld(z), _ld(out), state.stride(0),
+                                                conv_state.stride(0), q_scale, eps, _stream(stream)))
 
 
 def matvec(y, W, x, stream=None):

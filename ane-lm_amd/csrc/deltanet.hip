@@ -365,6 +365,157 @@ __global__ __launch_bounds__(256) void ssm_step_kernel(SsmArgs a) {
     }
 }
 
+// ------------------------------------- conv + SiLU + L2 norm + delta-rule step
+// qwen3_5.cpp:513-549 for one (sequence, head) per workgroup, with 128-wide
+// key and value heads and one key head per value head: waves 0, 1 and 2
+// compute the conv1d, SiLU (and for q and k the L2 norm, q scaled) of the
+// head's own q, k and v channels -- the operations and lane mapping of
+// conv_silu_l2_kernel, lane l on channels l and l + 64 -- and update those
+// channels' ring slots; then the delta-rule step and the gated RMSNorm of
+// ssm_step_kernel<128, 128, GATED> run on them from LDS.  The state loads go
+// out first, the conv's loads with them.  No workgroup touches another's
+// channels, so each (sequence, head) keeps its own ring position
+// (head_pos[b * nh + h]), advanced by its workgroup.
+struct ConvSsmArgs {
+    float* state;
+    float* conv_state;
+    int32_t* head_pos;
+    const float* x;
+    const float* conv_w;
+    const float* decay;
+    const float* beta;
+    const float* z;
+    const void* nw;
+    float* out;
+    int nh;
+    long ld_x, ld_z, ld_out, state_stride, conv_stride;
+    float q_scale, eps;
+};
+
+template <int GATED>
+__global__ __launch_bounds__(256) void conv_ssm_kernel(ConvSsmArgs a) {
+    constexpr int KD = 128, VD = 128;
+    constexpr int CG = VD / 4, RG = 256 / CG, RPT = KD / RG;
+    __shared__ float sk[KD], sq[KD], sv[VD], sdelta[VD];
+    __shared__ float red[RG][VD];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int cg = tid % CG, rg = tid / CG;
+    const long bh = blockIdx.x;
+    const long b = bh / a.nh;
+    const int h = (int)(bh % a.nh);
+    const int nq_ch = a.nh * 128;
+    float* S = a.state + b * a.state_stride + (long)h * KD * VD;
+    float4 s[RPT];
+#pragma unroll
+    for (int r = 0; r < RPT; r++) s[r] = ld_nt(reinterpret_cast<const float4*>(S + (long)(rg * RPT + r) * VD) + cg);
+    // this wave's 128 channels: q (wave 0), k (wave 1) or v (wave 2) of head
+    // h; wave 3 loads wave 2's again (clamped) and discards them
+    const int part = wv < 3 ? wv : 2;
+    const long cb = (long)part * nq_ch + (long)h * 128;
+    float* st = a.conv_state + b * a.conv_stride;
+    const float* xb = a.x + b * a.ld_x;
+    float xs[2], t0[2], t1[2], t2[2];
+    float4 wc[2];
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+        const long c = cb + lane + 64 * u;
+        xs[u] = xb[c];
+        wc[u] = *reinterpret_cast<const float4*>(a.conv_w + c * 4);
+        t0[u] = st[c * 3];
+        t1[u] = st[c * 3 + 1];
+        t2[u] = st[c * 3 + 2];
+    }
+    int pos = __hip_atomic_load(a.head_pos + bh, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const float decay = a.decay[bh], beta = a.beta[bh];
+    __builtin_amdgcn_sched_barrier(0);
+    pos = pos < 0 ? 0 : (pos >= 3 ? 0 : pos);   // keeps every access in the ring
+    if (wv < 3) {
+        float yv[2];
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const long c = cb + lane + 64 * u;
+            const float o0 = pos == 0 ? t0[u] : (pos == 1 ? t1[u] : t2[u]);
+            const float o1 = pos == 0 ? t1[u] : (pos == 1 ? t2[u] : t0[u]);
+            const float o2 = pos == 0 ? t2[u] : (pos == 1 ? t0[u] : t1[u]);
+            const float yc = conv4(o0, o1, o2, xs[u], wc[u]);
+            st[c * 3 + pos] = xs[u];
+            yv[u] = yc / (expf(-yc) + 1.0f);   // SiLU, qwen3_5.cpp:514
+        }
+        if (wv < 2) {   // q or k: L2 normalise (q scaled)
+            float ss = fmaf(yv[0], yv[0], 0.0f);
+            ss = fmaf(yv[1], yv[1], ss);
+            ss = wave_sum(ss);
+            const float norm = 1.0f / sqrtf(ss + 1e-12f);
+            const float scale = wv == 0 ? a.q_scale : 1.0f;
+            yv[0] = (yv[0] * norm) * scale;
+            yv[1] = (yv[1] * norm) * scale;
+        }
+        float* dst = wv == 0 ? sq : (wv == 1 ? sk : sv);
+        dst[lane] = yv[0];
+        dst[lane + 64] = yv[1];
+    }
+    __syncthreads();   // every wave has read the ring position
+    if (tid == 0) a.head_pos[bh] = pos + 1 == 3 ? 0 : pos + 1;
+    // Sk = S^T k (ssm_step_kernel's operations from here on)
+    float4 p = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int r = 0; r < RPT; r++) {
+        const float kr = sk[rg * RPT + r];
+        p.x = fmaf(s[r].x, kr, p.x);
+        p.y = fmaf(s[r].y, kr, p.y);
+        p.z = fmaf(s[r].z, kr, p.z);
+        p.w = fmaf(s[r].w, kr, p.w);
+    }
+    *reinterpret_cast<float4*>(&red[rg][4 * cg]) = p;
+    __syncthreads();
+    for (int j = tid; j < VD; j += 256) {
+        float t = red[0][j];
+#pragma unroll
+        for (int g = 1; g < RG; g++) t += red[g][j];
+        sdelta[j] = sv[j] - t;
+    }
+    __syncthreads();
+    const float4 d = *reinterpret_cast<const float4*>(&sdelta[4 * cg]);
+    p = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int r = 0; r < RPT; r++) {
+        const float bk = beta * sk[rg * RPT + r];
+        s[r].x = fmaf(bk, d.x, s[r].x * decay);
+        s[r].y = fmaf(bk, d.y, s[r].y * decay);
+        s[r].z = fmaf(bk, d.z, s[r].z * decay);
+        s[r].w = fmaf(bk, d.w, s[r].w * decay);
+        const float qr = sq[rg * RPT + r];
+        p.x = fmaf(s[r].x, qr, p.x);
+        p.y = fmaf(s[r].y, qr, p.y);
+        p.z = fmaf(s[r].z, qr, p.z);
+        p.w = fmaf(s[r].w, qr, p.w);
+        st_nt(reinterpret_cast<float4*>(S + (long)(rg * RPT + r) * VD) + cg, s[r]);
+    }
+    *reinterpret_cast<float4*>(&red[rg][4 * cg]) = p;   // red was last read before the previous barrier
+    __syncthreads();
+    for (int j = tid; j < VD; j += 256) {   // y into sdelta (last read before the previous barrier)
+        float t = red[0][j];
+#pragma unroll
+        for (int g = 1; g < RG; g++) t += red[g][j];
+        sdelta[j] = t;
+    }
+    __syncthreads();
+    if (tid < kWave) {
+        float ss = 0.0f;
+        for (int i = tid; i < VD; i += kWave) ss = fmaf(sdelta[i], sdelta[i], ss);
+        ss = wave_sum(ss);
+        const float sc = 1.0f / sqrtf(ss / (float)VD + a.eps);
+        const float* zr = a.z + b * a.ld_z + (long)h * VD;
+        float* orow = a.out + b * a.ld_out + (long)h * VD;
+        for (int i = tid; i < VD; i += kWave) {
+            float o = (sdelta[i] * sc) * load_w<GATED>(a.nw, i);
+            const float zi = zr[i];
+            o = o / (1.0f + expf(-zi));
+            orow[i] = o * zi;
+        }
+    }
+}
+
 // ------------------------------------------------------------ matvec
 // core/cpu_ops.cpp:100-103: y = W x, W [out_dim, in_dim] row-major fp32.
 // One wave per row; W is streamed once (non-temporal), x comes from cache.
@@ -565,6 +716,40 @@ extern "C" int anelm_conv1d_silu_l2norm(float* y, float* conv_state, int32_t* st
         conv_silu_l2_kernel<4><<<grid, block, 0, st>>>(y, conv_state, state_pos, x, w, channels, nq_ch, ld_x, ld_y,
                                                        state_stride, q_scale);
     return launch_status("conv1d_silu_l2norm");
+}
+
+extern "C" int anelm_conv_ssm_step_gated_norm(float* out, float* state, float* conv_state, int32_t* head_pos,
+                                              const float* x, const float* conv_w, const float* decay,
+                                              const float* beta, const float* z, const void* norm_w, int w_dtype,
+                                              long batch, int n_heads, long ld_x, long ld_z, long ld_out,
+                                              long state_stride, long conv_state_stride, float q_scale, float eps,
+                                              void* stream) {
+    const char* fn = "conv_ssm_step_gated_norm";
+    clear_error();
+    if (!out || !state || !conv_state || !head_pos || !x || !conv_w || !decay || !beta || !z || !norm_w)
+        return fail(ANELM_ERR_INVALID, "%s: null pointer", fn);
+    if (w_dtype != ANELM_F32 && w_dtype != ANELM_F16 && w_dtype != ANELM_BF16)
+        return fail(ANELM_ERR_INVALID, "%s: weight dtype %d", fn, w_dtype);
+    if (batch < 0 || n_heads <= 0 || batch > 0x7FFFFFFFL / n_heads)
+        return fail(ANELM_ERR_INVALID, "%s: bad sizes", fn);
+    const long channels = 3L * n_heads * 128;
+    if (batch > 1 && (ld_x < channels || ld_z < (long)n_heads * 128 || ld_out < (long)n_heads * 128 ||
+                      state_stride < (long)n_heads * 128 * 128 || conv_state_stride < channels * 3))
+        return fail(ANELM_ERR_INVALID, "%s: strides overlap", fn);
+    if (!aligned16(state) || (state_stride & 3) || !aligned16(conv_w))
+        return fail(ANELM_ERR_INVALID, "%s: state and conv weights 16-byte aligned", fn);
+    if (batch == 0) return ANELM_OK;
+    ConvSsmArgs a{};
+    a.state = state; a.conv_state = conv_state; a.head_pos = head_pos; a.x = x; a.conv_w = conv_w;
+    a.decay = decay; a.beta = beta; a.z = z; a.nw = norm_w; a.out = out; a.nh = n_heads;
+    a.ld_x = ld_x; a.ld_z = ld_z; a.ld_out = ld_out; a.state_stride = state_stride; a.conv_stride = conv_state_stride;
+    a.q_scale = q_scale; a.eps = eps;
+    const dim3 grid((unsigned)(batch * n_heads)), block(256);
+    hipStream_t st = as_stream(stream);
+    if (w_dtype == ANELM_F32) conv_ssm_kernel<ANELM_F32><<<grid, block, 0, st>>>(a);
+    else if (w_dtype == ANELM_F16) conv_ssm_kernel<ANELM_F16><<<grid, block, 0, st>>>(a);
+    else conv_ssm_kernel<ANELM_BF16><<<grid, block, 0, st>>>(a);
+    return launch_status(fn);
 }
 
 extern "C" int anelm_matvec(float* y, const float* W, const float* x, long out_dim, int in_dim, void* stream) {

@@ -421,13 +421,16 @@ DN_WORKLOADS = {
 def dn_bytes(w):
     """Per layer and token: the delta-rule states read and written once (the
     dominant term), conv rings read and written, q/k/v/z/x/y activations and
-    the conv weights once."""
+    the conv weights once; for the one-launch layer, the same less the conv
+    output's store and re-read."""
     B, nvh, nkh, kd, vd, K = w["B"], w["nvh"], w["nkh"], w["kd"], w["vd"], w["K"]
     ch = 2 * nkh * kd + nvh * vd
     state = B * nvh * kd * vd * 4 * 2
     conv = B * ch * (K - 1) * 4 * 2 + ch * K * 4 + B * ch * 4 * 2
     acts = B * (2 * nkh * kd * 4 * 2 + nvh * vd * 4 * 3 + nvh * vd * 4 * 2)
-    return dict(ssm_step=state + B * (2 * nkh * kd + 2 * nvh * vd) * 4, layer=state + conv + acts)
+    # one launch: the conv's q, k, v stay on chip (not written, not re-read)
+    one = state + conv - B * ch * 4 + B * (nvh * vd * 4 * 2)
+    return dict(ssm_step=state + B * (2 * nkh * kd + 2 * nvh * vd) * 4, layer=state + conv + acts, layer_one_call=one)
 
 
 def measure_deltanet(hip, w, steps, layers=8):
@@ -444,7 +447,8 @@ def measure_deltanet(hip, w, steps, layers=8):
     rn = lambda *s: torch.randn(*s, generator=g, device="cuda")
     lay = [dict(S=0.05 * rn(B, nvh, kd, vd), conv=rn(B, ch, K - 1), cw=rn(ch, K), pos=torch.zeros(B, dtype=torch.int32, device="cuda"),
                 decay=torch.rand(B, nvh, generator=g, device="cuda"), beta=torch.rand(B, nvh, generator=g, device="cuda"),
-                nw=1.0 + 0.02 * rn(vd)) for _ in range(layers)]
+                nw=1.0 + 0.02 * rn(vd), hpos=torch.zeros(B, nvh, dtype=torch.int32, device="cuda"))
+           for _ in range(layers)]
     x = rn(B, ch)
     z = rn(B, nvh * vd)
     mixed = torch.empty(B, ch, device="cuda")
@@ -461,6 +465,10 @@ def measure_deltanet(hip, w, steps, layers=8):
                      L["decay"], L["beta"], nkh)                                # :533-542
         hip.rmsnorm_gated(out, y, z, L["nw"], heads=nvh)                         # :545-549
 
+    def layer_one(L):   # the same in one launch (ring positions per head)
+        hip.conv_ssm_step_gated_norm(out, L["S"], L["conv"], L["hpos"], x, L["cw"], L["decay"], L["beta"], z,
+                                     L["nw"], qs)  # :513-549
+
     def layer(L):   # the same in two launches
         hip.conv1d_silu_l2norm(mixed, L["conv"], L["pos"], x, L["cw"], nkh, qs)  # :513-531
         hip.ssm_step_gated_norm(out, L["S"], mixed[:, :nkh * kd], mixed[:, nkh * kd:2 * nkh * kd],
@@ -472,6 +480,12 @@ def measure_deltanet(hip, w, steps, layers=8):
     g6 = capture(lambda: [layer_separate(L) for L in lay])
     g6.replay()
     ms6 = time_region(g6.replay, steps) / layers
+    ms1 = None
+    if nvh == nkh and kd == 128 and vd == 128 and K == 4:
+        g1 = capture(lambda: [layer_one(L) for L in lay])
+        g1.replay()
+        ms1 = time_region(g1.replay, steps) / layers
+        del g1
     gs = capture(lambda: [hip.ssm_step(y, L["S"], mixed[:, :nkh * kd], mixed[:, nkh * kd:2 * nkh * kd],
                                        mixed[:, 2 * nkh * kd:], L["decay"], L["beta"], nkh) for L in lay])
     gs.replay()
@@ -481,11 +495,14 @@ def measure_deltanet(hip, w, steps, layers=8):
     torch.cuda.empty_cache()
     f = lambda byt, ms: dict(us=round(ms * 1e3, 2), GBps=round(byt / ms / 1e6, 1),
                              frac=round(byt / ms / 1e6 / HBM_PEAK_GBPS, 4), bytes=byt)
-    return dict(layer=dict(f(b["layer"], ms), tokens_per_s=round(B / (ms / 1e3), 1)),
-                layer_six_calls=f(b["layer"], ms6), ssm_step=f(b["ssm_step"], ms_s),
-                note="per layer; algorithmic bytes = delta-rule states read+written once, conv rings, activations; "
-                     "layer = anelm_conv1d_silu_l2norm + anelm_ssm_step_gated_norm, layer_six_calls = the six "
-                     "separate ops")
+    r = dict(layer=dict(f(b["layer"], ms), tokens_per_s=round(B / (ms / 1e3), 1)),
+             layer_six_calls=f(b["layer"], ms6), ssm_step=f(b["ssm_step"], ms_s),
+             note="per layer; algorithmic bytes = delta-rule states read+written once, conv rings, activations; "
+                  "layer = anelm_conv1d_silu_l2norm + anelm_ssm_step_gated_norm, layer_one_call = "
+                  "anelm_conv_ssm_step_gated_norm, layer_six_calls = the six separate ops")
+    if ms1 is not None:
+        r["layer_one_call"] = dict(f(b["layer_one_call"], ms1), tokens_per_s=round(B / (ms1 / 1e3), 1))
+    return r
 
 
 def cpu_attention(w, target_s):

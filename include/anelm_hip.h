@@ -446,6 +446,22 @@ int anelm_ssm_step_gated_norm(float* out, float* state, const float* q, const fl
                               long batch, int n_heads, int n_key_heads, int key_dim, int value_dim, long ld_qk,
                               long ld_v, long ld_z, long ld_out, long state_stride, float eps, void* stream);
 
+/* The decode step's whole linear-attention core (models/llm/qwen3_5.cpp:513-549)
+ * in one launch, for n_heads key heads = n_heads value heads of 128:
+ * anelm_conv1d_silu_l2norm on x ([q heads | k heads | v], 3*128*n_heads
+ * channels; conv_w [channels, 4], 16-byte aligned; conv_state per sequence
+ * [channels, 3] at conv_state + b*conv_state_stride), then
+ * anelm_ssm_step_gated_norm on its q, k, v.  out and the state are
+ * bit-identical to those two calls'; the conv's q, k, v are not stored.  The
+ * ring position is kept per (sequence, head): head_pos [batch*n_heads], each
+ * advanced by one (heads of a sequence stay equal when they start equal; an
+ * out-of-range value is taken as 0).  No counterpart in the reference. */
+int anelm_conv_ssm_step_gated_norm(float* out, float* state, float* conv_state, int32_t* head_pos,
+                                   const float* x, const float* conv_w, const float* decay, const float* beta,
+                                   const float* z, const void* norm_w, int w_dtype, long batch, int n_heads, long ld_x,
+                                   long ld_z, long ld_out, long state_stride, long conv_state_stride, float q_scale,
+                                   float eps, void* stream);
+
 /* y = W x, W [out_dim, in_dim] row-major fp32 (ane_lm::matvec,
  * core/cpu_ops.cpp:100-103, cpu_ops.h:37; the reference's CPU LM head and
  * DeltaNet a/b projections, models/llm/qwen3_5.cpp:509-510, :689). */

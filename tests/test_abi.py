@@ -274,6 +274,14 @@ def test_deltanet_argument_checks(lib):
     assert s(fake, fake, fake, fake, fake, fake, fake, 1, 16, 16, 96, 128, 2048, 2048, 2048, 16 * 128 * 128, None) == -1
     assert s(fake, fake, fake, fake, fake, fake, fake, 1, 16, 5, 128, 128, 2048, 2048, 2048, 16 * 128 * 128, None) == -1
     assert b"key_dim" in lib.anelm_last_error() or b"multiple" in lib.anelm_last_error()
+    c = lib.anelm_conv_ssm_step_gated_norm
+    n = 16 * 128
+    ok = [fake, fake, fake, fake, fake, fake, fake, fake, fake, fake, 0, 2, 16, 3 * n, n, n, 16 * 128 * 128, 3 * n * 3,
+          ctypes.c_float(0.088), ctypes.c_float(1e-6), None]
+    for i, v in ((3, None), (10, 7), (12, 0), (13, 3 * n - 128), (16, 16 * 128 * 128 - 4), (17, 3 * n * 3 - 1)):
+        bad = list(ok)
+        bad[i] = v                     # no ring positions / dtype / heads / overlapping x, state or ring rows
+        assert c(*bad) == -1, i
     assert lib.anelm_matvec(None, fake, fake, 4, 4, None) == -1
     assert lib.anelm_matvec(fake, fake, fake, 4, 0, None) == -1
 

@@ -203,3 +203,40 @@ def test_ssm_step_gated_norm_matches_separate_calls(hip, rng, B, nvh, nkh, kd, v
     hip.ssm_step_gated_norm(outb, Sb, q, k, v, decay, beta, z, nw, nkh)
     assert_bitexact(host(outb), host(outa), "gated outputs")
     assert_bitexact(host(Sb), host(Sa), "states")
+
+
+@pytest.mark.parametrize("B,nh,wdt,steps,pad", [(64, 16, "f32", 4, 0), (1, 16, "bf16", 5, 0), (3, 2, "f16", 4, 128),
+                                                (5, 3, "f32", 3, 0)])
+def test_conv_ssm_step_gated_norm_matches_two_calls(hip, rng, B, nh, wdt, steps, pad):
+    """The one-launch conv + SiLU + L2 norm + state step + gated RMSNorm equals
+    anelm_conv1d_silu_l2norm then anelm_ssm_step_gated_norm bit for bit
+    (outputs, delta-rule states, conv rings, ring positions), over several
+    steps so the ring wraps; x and z as views into wider rows when pad > 0."""
+    import torch
+
+    ch, n = 3 * nh * 128, nh * 128
+    qs = float(1.0 / np.sqrt(128.0))
+    cw = dev((0.5 * rng.standard_normal((ch, 4))).astype(np.float32))
+    ring0 = rng.standard_normal((B, ch, 3)).astype(np.float32)
+    S0 = (0.05 * rng.standard_normal((B, nh, 128, 128))).astype(np.float32)
+    pos0 = rng.integers(-1, 4, B).astype(np.int32)          # out-of-range positions are taken as 0
+    w32 = (1 + 0.1 * rng.standard_normal(128)).astype(np.float32)
+    nw = {"f32": torch.from_numpy(w32), "f16": torch.from_numpy(w32).half(),
+          "bf16": torch.from_numpy(w32).bfloat16()}[wdt].cuda()
+    Sa, ra, pa = dev(S0), dev(ring0), dev(pos0)
+    Sb, rb, pb = dev(S0), dev(ring0), dev(np.repeat(pos0, nh))
+    mixed = torch.empty(B, ch, device="cuda")
+    for step in range(steps):
+        xz = dev((2 * rng.standard_normal((B, ch + n + pad))).astype(np.float32))
+        x, z = xz[:, :ch], xz[:, ch + pad:]
+        decay = dev(rng.uniform(0.5, 1.0, (B, nh)).astype(np.float32))
+        beta = dev(rng.uniform(0.0, 1.0, (B, nh)).astype(np.float32))
+        outa = torch.empty(B, n, device="cuda")
+        hip.conv1d_silu_l2norm(mixed, ra, pa, x, cw, nh, qs)
+        hip.ssm_step_gated_norm(outa, Sa, mixed[:, :n], mixed[:, n:2 * n], mixed[:, 2 * n:], decay, beta, z, nw, nh)
+        outb = torch.full((B, n), float("nan"), device="cuda")
+        hip.conv_ssm_step_gated_norm(outb, Sb, rb, pb, x, cw, decay, beta, z, nw, qs)
+        assert_bitexact(host(outb), host(outa), f"step {step}: gated outputs")
+        assert_bitexact(host(Sb), host(Sa), f"step {step}: states")
+        assert_bitexact(host(rb), host(ra), f"step {step}: conv rings")
+        assert np.array_equal(host(pb).reshape(B, nh), np.repeat(host(pa)[:, None], nh, axis=1)), f"step {step}"
