@@ -403,7 +403,7 @@ __global__ __launch_bounds__(256) void conv_ssm_kernel(ConvSsmArgs a) {
     const long bh = blockIdx.x;
     const long b = bh / a.nh;
     const int h = (int)(bh % a.nh);
-    const int nq_ch = a.nh * 128;
+    const long nq_ch = (long)a.nh * 128;
     float* S = a.state + b * a.state_stride + (long)h * KD * VD;
     float4 s[RPT];
 #pragma unroll

@@ -54,6 +54,7 @@ extern int L;
 extern float *mixed, *pre_oproj;
 extern float* conv_state[kLayers];
 extern int32_t* conv_pos[kLayers];
+extern int32_t* conv_head_pos[kLayers];   // per (sequence, head)
 extern const float* conv_w[kLayers];
 extern float* ssm_state[kLayers];
 extern const float* norm_w[kLayers];
