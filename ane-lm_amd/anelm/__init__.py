@@ -540,8 +540,8 @@ def conv_ssm_step_gated_norm(out, state, conv_state, head_pos, x, conv_w, decay,
     _need(state.stride(3) == 1 and state.stride(2) == vd and state.stride(1) == kd * vd, "ssm_step: state layout")
     _need(conv_state.shape == (B, ch, 3) and conv_state.stride(2) == 1 and conv_state.stride(1) == 3 and
           conv_w.shape == (ch, 4) and conv_w.is_contiguous(), "conv_ssm_step_gated_norm: conv shapes")
-    _need(head_pos.numel() == B * nh and head_pos.is_contiguous() and decay.is_contiguous() and
-          beta.is_contiguous(), "conv_ssm_step_gated_norm: layouts")
+    _need(head_pos.numel() == B * nh and head_pos.is_contiguous() and str(head_pos.dtype) == "torch.int32" and
+          decay.is_contiguous() and beta.is_contiguous(), "conv_ssm_step_gated_norm: layouts")
     _check(lib().anelm_conv_ssm_step_gated_norm(_ptr(out), _ptr(state), _ptr(conv_state), _ptr(head_pos), _ptr(x),
                                                 _ptr(conv_w), _ptr(decay), _ptr(beta), _ptr(z), _ptr(norm_w),
                                                 _dtype_code(norm_w), B, nh, _ld(x), _ld(z), _ld(out), state.stride(0),

@@ -409,10 +409,14 @@ __global__ __launch_bounds__(256) void conv_ssm_kernel(ConvSsmArgs a) {
 #pragma unroll
     for (int r = 0; r < RPT; r++) s[r] = ld_nt(reinterpret_cast<const float4*>(S + (long)(rg * RPT + r) * VD) + cg);
     // this wave's 128 channels: q (wave 0), k (wave 1) or v (wave 2) of head
-    // h; wave 3 loads wave 2's again (clamped) and discards them
+    // h.  Wave 3 issues the same loads unconditionally (a load in a branch is
+    // waited for at the branch's end) at wave 2's channels and discards them;
+    // its ring taps come from the read-only weights (in bounds: c*3 + 2 <
+    // 4*channels), so it reads nothing that wave 2 writes.
     const int part = wv < 3 ? wv : 2;
     const long cb = (long)part * nq_ch + (long)h * 128;
     float* st = a.conv_state + b * a.conv_stride;
+    const float* taps = wv < 3 ? st : a.conv_w;
     const float* xb = a.x + b * a.ld_x;
     float xs[2], t0[2], t1[2], t2[2];
     float4 wc[2];
@@ -421,9 +425,9 @@ __global__ __launch_bounds__(256) void conv_ssm_kernel(ConvSsmArgs a) {
         const long c = cb + lane + 64 * u;
         xs[u] = xb[c];
         wc[u] = *reinterpret_cast<const float4*>(a.conv_w + c * 4);
-        t0[u] = st[c * 3];
-        t1[u] = st[c * 3 + 1];
-        t2[u] = st[c * 3 + 2];
+        t0[u] = taps[c * 3];
+        t1[u] = taps[c * 3 + 1];
+        t2[u] = taps[c * 3 + 2];
     }
     int pos = __hip_atomic_load(a.head_pos + bh, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const float decay = a.decay[bh], beta = a.beta[bh];
