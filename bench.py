@@ -800,6 +800,9 @@ def _csv_rows(d, suffix):
 
 
 ATTN_KERNELS = {"gqa_decode": ("gqa_decode_kernel", "")}
+DN_B64 = "deltanet-qwen3.5-0.8b-decode-b64"
+DN_KERNELS = {"layer_one_call": ("conv_ssm_kernel", ""), "conv_silu_l2": ("conv_silu_l2_kernel", ""),
+              "ssm_step_gated": ("ssm_step_kernel", "128, 0>"), "ssm_step": ("ssm_step_kernel", "128, -1>")}
 
 
 SAMPLE_KERNELS = {"stage1": ("sample_stage1_kernel", ""), "stage2": ("sample_stage2_kernel", ""),
@@ -859,6 +862,8 @@ def _kernels_of(workload):
         return Q3_KERNELS
     if workload == Q3_B64:
         return Q3_B64_KERNELS
+    if workload == DN_B64:
+        return DN_KERNELS
     return ATTN_KERNELS if workload in ATTN_WORKLOADS else OP_KERNELS
 
 
@@ -987,6 +992,15 @@ def pmc_summary(fetch_dir, write_dir, copy_fetch_dir, copy_write_dir, workload=H
         ob = q3_b1_bytes()
     elif workload == Q3_B64:
         ob = q3_b64_bytes()
+    elif workload == DN_B64:
+        w = DN_WORKLOADS[workload]
+        B, nvh, nkh, kd, vd = w["B"], w["nvh"], w["nkh"], w["kd"], w["vd"]
+        ch = 2 * nkh * kd + nvh * vd
+        d = dn_bytes(w)
+        state = B * nvh * kd * vd * 4 * 2
+        ob = {"layer_one_call": d["layer_one_call"], "ssm_step": d["ssm_step"],
+              "ssm_step_gated": state + B * (2 * nkh * kd + 3 * nvh * vd) * 4,   # q, k, v, z in; out
+              "conv_silu_l2": B * ch * 3 * 4 * 2 + ch * 4 * 4 + B * ch * 4 * 2}  # rings, weights, x in, y out
     elif workload == SAMPLER:
         # stage 1 reads the logits; stage 2 reads them again and writes exp(x - max)
         # into the probability buffer; stage 3 reads that and writes the probabilities
@@ -1068,7 +1082,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default=HEADLINE, choices=sorted(WORKLOADS) + sorted(ATTN_WORKLOADS) + [SAMPLER, Q3_B1, Q3_B64],
+    ap.add_argument("--workload", default=HEADLINE, choices=sorted(WORKLOADS) + sorted(ATTN_WORKLOADS) + [SAMPLER, Q3_B1, Q3_B64, DN_B64],
                     help="op-chain workload to run (attention names only select --pmc-summary kernels)")
     ap.add_argument("--cpu-seconds", type=float, default=8.0, help="CPU time budget of the headline baseline")
     ap.add_argument("--no-cpu", action="store_true")
