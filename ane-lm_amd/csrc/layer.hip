@@ -17,9 +17,9 @@
 //     once; both norms' sums share one LDS exchange and barrier (none for a
 //     one-wave row);
 //   - the q/k heads, 16 lanes per head (norm_rope128_w, the separate
-//     kernel's arithmetic); with nq and nk multiples of 8 each wave takes 8
-//     heads of one token, so its position is a scalar load and every load of
-//     the wave goes out before the first wait;
+//     kernel's arithmetic); with nq and nk multiples of 4 each wave takes 4
+//     heads of one token, so its position is a scalar load and every load
+//     of the wave goes out before the first wait;
 //   - the SwiGLU, two float4 of g, u and h per lane.
 #include "anelm_common.hpp"
 
@@ -159,53 +159,48 @@ __device__ __forceinline__ void x_chain(const LayerArgs& a, long blk) {
     }
 }
 
-// q/k heads: flat index over the T*nq q heads then the T*nk k heads.  W8:
-// each wave owns 8 consecutive heads (all of one token, nq and nk multiples
-// of 8), two per 16-lane group; else one head per 16-lane group.
-template <int DT, bool W8>
+// The q/k part takes one head per 16-lane group, four heads to a wave.
+// Against 8 per wave (two per group, as qknorm_rope128_w8_kernel) the heads
+// spread over twice the waves and each wave's dependent chain is half as
+// long: 4B decode at 64 tokens 5.92 -> 5.23 us per layer, the prefill shapes
+// unchanged, 0.6B decode (24 heads) 2.27 -> 2.33.  (The separate kernel keeps
+// 8: at 64 tokens 4 per wave measured 4.29 against 4.07 us there.)  The
+// arithmetic per head is the same either way.
+
+// q/k heads: flat index over the T*nq q heads then the T*nk k heads, one
+// head per 16-lane group.  W4: each wave owns 4 consecutive heads (all of one
+// token, nq and nk multiples of 4), so the token is wave-uniform and its
+// position a scalar load; else each group loads its own token's position.
+template <int DT, bool W4>
 __device__ __forceinline__ void qk_heads(const LayerArgs& a, const InvFreq& inv, int blk) {
     const uint32_t nqh = (uint32_t)a.T * (uint32_t)a.nq;
     const uint32_t heads = nqh + (uint32_t)a.T * (uint32_t)a.nk;
     const int j0 = 4 * (threadIdx.x & 15);
-    constexpr int HPG = W8 ? 2 : 1;
-    uint32_t first;   // this 16-lane group's first head
-    if (W8) {
-        const uint32_t w0 = ((uint32_t)blk * (blockDim.x >> 6) + (threadIdx.x >> 6)) * 8u;
-        if (w0 >= heads) return;   // whole wave
-        first = w0 + ((threadIdx.x >> 4) & 3);
-    } else {
-        first = (uint32_t)blk * (blockDim.x >> 4) + (threadIdx.x >> 4);
-        if (first >= heads) return;   // whole 16-lane group
+    const uint32_t head = (uint32_t)blk * (blockDim.x >> 4) + (threadIdx.x >> 4);
+    if (W4) {
+        if ((head & ~3u) >= heads) return;   // whole wave (heads is a multiple of 4)
+    } else if (head >= heads) {
+        return;   // whole 16-lane group
     }
-    const bool isq = first < nqh;
-    uint32_t t = isq ? first / (uint32_t)a.nq : (first - nqh) / (uint32_t)a.nk;
-    if (W8) t = __builtin_amdgcn_readfirstlane(t);
+    const bool isq = head < nqh;
+    uint32_t t = isq ? head / (uint32_t)a.nq : (head - nqh) / (uint32_t)a.nk;
+    if (W4) t = __builtin_amdgcn_readfirstlane(t);
     const int p = a.pos[t];
     Gamma4<DT> glo, ghi;
     glo.load(isq ? a.wq : a.wk, j0);
     ghi.load(isq ? a.wq : a.wk, j0 + 64);
-    float* v[HPG];
-    float4 lo[HPG], hi[HPG];
-#pragma unroll
-    for (int i = 0; i < HPG; i++) {
-        const uint32_t hh = first + 4u * (uint32_t)i;
-        v[i] = isq ? a.q + (long)t * a.nq * 128 + (long)(hh - t * (uint32_t)a.nq) * 128
-                   : a.k + (long)t * a.nk * 128 + (long)(hh - nqh - t * (uint32_t)a.nk) * 128;
-        lo[i] = ld_nt(reinterpret_cast<const float4*>(v[i] + j0));
-        hi[i] = ld_nt(reinterpret_cast<const float4*>(v[i] + 64 + j0));
-    }
+    float* v = isq ? a.q + (long)t * a.nq * 128 + (long)(head - t * (uint32_t)a.nq) * 128
+                   : a.k + (long)t * a.nk * 128 + (long)(head - nqh - t * (uint32_t)a.nk) * 128;
+    const float4 lo = ld_nt(reinterpret_cast<const float4*>(v + j0));
+    const float4 hi = ld_nt(reinterpret_cast<const float4*>(v + 64 + j0));
     const int pr = p < 0 ? 0 : (p >= a.tab_len ? a.tab_len - 1 : p);
     float4 c = *reinterpret_cast<const float4*>(a.cos_tab + (long)pr * 64 + j0);
     float4 s = *reinterpret_cast<const float4*>(a.sin_tab + (long)pr * 64 + j0);
     if (p != pr) rope_cs4(p, j0, a.cos_tab, a.sin_tab, a.tab_len, inv.v, c, s);   // past the table
-    const float4 wl = glo.get(), wh = ghi.get();
-#pragma unroll
-    for (int i = 0; i < HPG; i++) {
-        float4 ol, oh;
-        norm_rope128_w(lo[i], hi[i], true, wl, wh, c, s, a.eps, ol, oh);
-        st_nt(reinterpret_cast<float4*>(v[i] + j0), ol);
-        st_nt(reinterpret_cast<float4*>(v[i] + 64 + j0), oh);
-    }
+    float4 ol, oh;
+    norm_rope128_w(lo, hi, true, glo.get(), ghi.get(), c, s, a.eps, ol, oh);
+    st_nt(reinterpret_cast<float4*>(v + j0), ol);
+    st_nt(reinterpret_cast<float4*>(v + 64 + j0), oh);
 }
 
 // two float4 of g, u and h per lane, a block's lanes on consecutive float4
@@ -231,7 +226,7 @@ __device__ __forceinline__ void swiglu(const LayerArgs& a, int blk) {
     }
 }
 
-template <int NV, int DT, bool W8, bool FULL>
+template <int NV, int DT, bool W4, bool FULL>
 __global__ __launch_bounds__(1024) void layer_ops_kernel(LayerArgs a, const InvFreq inv) {
     int blk = blockIdx.x;
     if (blk < a.row_blocks) {
@@ -240,29 +235,29 @@ __global__ __launch_bounds__(1024) void layer_ops_kernel(LayerArgs a, const InvF
     }
     blk -= a.row_blocks;
     if (blk < a.qk_blocks) {
-        qk_heads<DT, W8>(a, inv, blk);
+        qk_heads<DT, W4>(a, inv, blk);
         return;
     }
     swiglu(a, blk - a.qk_blocks);
 }
 
 template <int NV, int DT>
-void launch_layer(const LayerArgs& a, const InvFreq& inv, bool w8, int threads, int blocks, hipStream_t st) {
+void launch_layer(const LayerArgs& a, const InvFreq& inv, bool w4, int threads, int blocks, hipStream_t st) {
     const dim3 grd((unsigned)blocks), blk((unsigned)threads);
     const bool full = a.H == 4 * NV * a.row_threads;
-    if (w8 && full) layer_ops_kernel<NV, DT, true, true><<<grd, blk, 0, st>>>(a, inv);
-    else if (w8) layer_ops_kernel<NV, DT, true, false><<<grd, blk, 0, st>>>(a, inv);
+    if (w4 && full) layer_ops_kernel<NV, DT, true, true><<<grd, blk, 0, st>>>(a, inv);
+    else if (w4) layer_ops_kernel<NV, DT, true, false><<<grd, blk, 0, st>>>(a, inv);
     else if (full) layer_ops_kernel<NV, DT, false, true><<<grd, blk, 0, st>>>(a, inv);
     else layer_ops_kernel<NV, DT, false, false><<<grd, blk, 0, st>>>(a, inv);
 }
 
 template <int DT>
-void launch_layer_dt(int nv, const LayerArgs& a, const InvFreq& inv, bool w8, int threads, int blocks,
+void launch_layer_dt(int nv, const LayerArgs& a, const InvFreq& inv, bool w4, int threads, int blocks,
                      hipStream_t st) {
     switch (nv) {
-        case 1: launch_layer<1, DT>(a, inv, w8, threads, blocks, st); break;
-        case 2: launch_layer<2, DT>(a, inv, w8, threads, blocks, st); break;
-        default: launch_layer<4, DT>(a, inv, w8, threads, blocks, st); break;
+        case 1: launch_layer<1, DT>(a, inv, w4, threads, blocks, st); break;
+        case 2: launch_layer<2, DT>(a, inv, w4, threads, blocks, st); break;
+        default: launch_layer<4, DT>(a, inv, w4, threads, blocks, st); break;
     }
 }
 
@@ -299,9 +294,9 @@ extern "C" int anelm_layer_ops(float* x, float* xn_in, float* xn_post, const flo
     // take the same block size)
     const int rpb = row_threads == 64 ? 4 : 1;
     const int threads = row_threads * rpb;
-    const bool w8 = nq % 8 == 0 && nk % 8 == 0;
+    const bool w4 = nq % 4 == 0 && nk % 4 == 0;
     const long heads = T * (nq + nk);
-    const long qk_blocks = w8 ? (heads / 8 + threads / 64 - 1) / (threads / 64) : (heads + threads / 16 - 1) / (threads / 16);
+    const long qk_blocks = (heads + threads / 16 - 1) / (threads / 16);   // one head per 16 lanes
     const long n4 = T * inter / 4;
     const long silu_blocks = (n4 + 2L * threads - 1) / (2L * threads);
     const long row_blocks = (T + rpb - 1) / rpb;
@@ -341,9 +336,9 @@ extern "C" int anelm_layer_ops(float* x, float* xn_in, float* xn_post, const flo
     clear_error();
     hipStream_t st = as_stream(stream);
     switch (w_dtype) {
-        case ANELM_F32: launch_layer_dt<ANELM_F32>(nv, a, inv, w8, threads, (int)blocks, st); break;
-        case ANELM_F16: launch_layer_dt<ANELM_F16>(nv, a, inv, w8, threads, (int)blocks, st); break;
-        default: launch_layer_dt<ANELM_BF16>(nv, a, inv, w8, threads, (int)blocks, st); break;
+        case ANELM_F32: launch_layer_dt<ANELM_F32>(nv, a, inv, w4, threads, (int)blocks, st); break;
+        case ANELM_F16: launch_layer_dt<ANELM_F16>(nv, a, inv, w4, threads, (int)blocks, st); break;
+        default: launch_layer_dt<ANELM_BF16>(nv, a, inv, w4, threads, (int)blocks, st); break;
     }
     return launch_status("layer_ops");
 }
