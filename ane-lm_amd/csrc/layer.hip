@@ -163,7 +163,7 @@ __device__ __forceinline__ void x_chain(const LayerArgs& a, long blk) {
 // Against 8 per wave (two per group, as qknorm_rope128_w8_kernel) the heads
 // spread over twice the waves and each wave's dependent chain is half as
 // long: 4B decode at 64 tokens 5.92 -> 5.23 us per layer, the prefill shapes
-// unchanged, 0.6B decode (24 heads) 2.27 -> 2.33.  (The separate kernel keeps
+// and the 0.6B decode unchanged within run-to-run noise.  (The separate kernel keeps
 // 8: at 64 tokens 4 per wave measured 4.29 against 4.07 us there.)  The
 // arithmetic per head is the same either way.
 
@@ -204,6 +204,8 @@ __device__ __forceinline__ void qk_heads(const LayerArgs& a, const InvFreq& inv,
 }
 
 // two float4 of g, u and h per lane, a block's lanes on consecutive float4
+// (one per lane measured slower at 64 and 2048 tokens: 5.92 against 5.24 us
+// per layer at 4B decode)
 __device__ __forceinline__ void swiglu(const LayerArgs& a, int blk) {
     const long i0 = (long)blk * 2 * blockDim.x + threadIdx.x;
     float4 gv[2], uv[2];
