@@ -87,6 +87,8 @@ _SIGS = {
     "anelm_kv_ring_advance": (_I, [_P, _P, _L, _I, _L, _I, _P]),
     "anelm_gqa_attention_qk": (_I, [_P, _I, _P, _P, _P, _L, _L, _L, _P, _P, _I, _P, _P, _P, _I, _F, _F, _P, _P, _P, _P,
                                     _L, _I, _I, _L, _I, _L, _P, _S, _P]),
+    "anelm_gqa_attention_qk_append": (_I, [_P, _I, _P, _P, _P, _L, _L, _L, _P, _P, _I, _P, _P, _P, _I, _F, _F, _P, _P,
+                                           _P, _P, _L, _I, _I, _L, _I, _L, _P, _S, _P]),
     "anelm_rmsnorm_gated": (_I, [_P, _P, _P, _P, _I, _L, _I, _I, _L, _L, _L, _F, _P]),
     "anelm_l2_normalize": (_I, [_P, _L, _I, _I, _L, _F, _P]),
     "anelm_conv1d_update": (_I, [_P, _P, _P, _P, _P, _L, _I, _I, _L, _L, _L, _P]),
@@ -452,9 +454,10 @@ def kv_ring_advance(ring_start, ring_len, capacity, batch=None, stream=None):
 
 
 def gqa_attention_qk(out, q, k, v, wq, wk, pos, cos_tab, sin_tab, k_cache, v_cache, ring_start, ring_len, n_heads,
-                     n_kv_heads, workspace, theta=1e6, eps=1e-6, stream=None, tiled=False):
+                     n_kv_heads, workspace, theta=1e6, eps=1e-6, stream=None, tiled=False, advance=False):
     """qknorm_rope_append + gqa_attention in one launch (head_dim 128) for rings
-    already advanced by kv_ring_advance.  q: [B, >= n_heads*128], k, v: [B, >=
+    already advanced by kv_ring_advance (advance=True: the call advances them
+    first, anelm_gqa_attention_qk_append).  q: [B, >= n_heads*128], k, v: [B, >=
     n_kv_heads*128] (row slices of the qkv projection allowed, left as they
     are); out fp32 or fp16 (tiled: fp16 in the tiled layout of proj_tile_f16,
     n_heads*128 columns); caches [B, capacity, n_kv_heads*128]."""
@@ -465,11 +468,11 @@ def gqa_attention_qk(out, q, k, v, wq, wk, pos, cos_tab, sin_tab, k_cache, v_cac
     wdt = _dtype_code(wq if wq is not None else (wk if wk is not None else q))
     tab_len = cos_tab.shape[0] if cos_tab is not None else 0
     mode = 2 if tiled else int(out.element_size() == 2)
-    _check(lib().anelm_gqa_attention_qk(_ptr(out), mode, _ptr(q), _ptr(k), _ptr(v), _ld(q),
-                                        _ld(k), _ld(v), _ptr(wq), _ptr(wk), wdt, _ptr(pos), _ptr(cos_tab),
-                                        _ptr(sin_tab), tab_len, theta, eps, _ptr(k_cache), _ptr(v_cache),
-                                        _ptr(ring_start), _ptr(ring_len), B, n_heads, n_kv_heads, n_heads * 128 if tiled else _ld(out), cap,
-                                        k_cache.stride(0), _ptr(workspace), _nbytes(workspace), _stream(stream)))
+    fn = lib().anelm_gqa_attention_qk_append if advance else lib().anelm_gqa_attention_qk
+    _check(fn(_ptr(out), mode, _ptr(q), _ptr(k), _ptr(v), _ld(q), _ld(k), _ld(v), _ptr(wq), _ptr(wk), wdt, _ptr(pos),
+              _ptr(cos_tab), _ptr(sin_tab), tab_len, theta, eps, _ptr(k_cache), _ptr(v_cache), _ptr(ring_start),
+              _ptr(ring_len), B, n_heads, n_kv_heads, n_heads * 128 if tiled else _ld(out), cap, k_cache.stride(0),
+              _ptr(workspace), _nbytes(workspace), _stream(stream)))
 
 
 def rmsnorm_gated(out, x, z, w, eps=1e-6, heads=1, stream=None):

@@ -629,8 +629,9 @@ int check_common(const void* out, const void* q, const void* kc, const void* vc,
     return ANELM_OK;
 }
 
-// qk: -1, or the weight dtype of a QK launch (head_dim 128)
-int run(AttnArgs a, long batch, int D, int bound, void* ws, size_t ws_bytes, hipStream_t st, int qk = -1) {
+// The chunking of a launch and the workspace it needs, checked before
+// anything is launched.
+int plan(AttnArgs& a, long batch, int D, int bound, void* ws, size_t ws_bytes) {
     a.groups = a.nh / a.nkv;
     a.scale = 1.0f / sqrtf((float)D);   // core/cpu_ops.cpp:183
     a.chunk = pick_chunk(batch * a.nkv, a.cap);  // from the capacity, so the workspace size holds for any bound
@@ -647,14 +648,62 @@ int run(AttnArgs a, long batch, int D, int bound, void* ws, size_t ws_bytes, hip
         a.ctr = reinterpret_cast<unsigned*>(static_cast<char*>(ws) + ctr_offset(ws_bytes));
     }
     a.ws = static_cast<float*>(ws);
-    if (batch == 0) return ANELM_OK;
+    return ANELM_OK;
+}
+
+// qk: -1, or the weight dtype of a QK launch (head_dim 128)
+void dispatch(const AttnArgs& a, long batch, int D, hipStream_t st, int qk = -1) {
     if (qk == ANELM_F32) launch_d<128, ANELM_F32>(a, batch, st);
     else if (qk == ANELM_F16) launch_d<128, ANELM_F16>(a, batch, st);
     else if (qk == ANELM_BF16) launch_d<128, ANELM_BF16>(a, batch, st);
     else if (D == 64) launch_d<64>(a, batch, st);
     else if (D == 128) launch_d<128>(a, batch, st);
     else launch_d<256>(a, batch, st);
+}
+
+int run(AttnArgs a, long batch, int D, int bound, void* ws, size_t ws_bytes, hipStream_t st, int qk = -1) {
+    const int rc = plan(a, batch, D, bound, ws, ws_bytes);
+    if (rc) return rc;
+    if (batch == 0) return ANELM_OK;
+    dispatch(a, batch, D, st, qk);
     return launch_status("gqa_attention");
+}
+
+// The arguments of a QK launch (anelm_gqa_attention_qk), checked.
+int qk_args(AttnArgs& a, const char* fn, void* out, int out_f16, const float* q, const float* k, const float* v,
+            long q_ld, long k_ld, long v_ld, const void* wq, const void* wk, int w_dtype, const int32_t* pos,
+            const float* cos_tab, const float* sin_tab, int tab_len, float theta, float eps, float* k_cache,
+            float* v_cache, const int32_t* ring_start, const int32_t* ring_len, long batch, int n_heads,
+            int n_kv_heads, long out_ld, int capacity, long cache_seq_stride) {
+    int rc = check_common(out, q, k_cache, v_cache, batch, n_heads, n_kv_heads, 128, q_ld, 128, out_ld, capacity,
+                          cache_seq_stride);
+    if (rc) return rc;
+    if (!ring_start || !ring_len || !k || !v || !pos) return fail(ANELM_ERR_INVALID, "%s: null pointer", fn);
+    const long row = (long)n_kv_heads * 128;
+    if (batch > 1 && (k_ld < row || v_ld < row)) return fail(ANELM_ERR_INVALID, "%s: k/v strides overlap", fn);
+    if (tab_len < 1 || !cos_tab || !sin_tab) return fail(ANELM_ERR_INVALID, "%s: needs a RoPE table of >= 1 row", fn);
+    if (!wq || !wk) return fail(ANELM_ERR_INVALID, "%s: needs both q and k gammas", fn);
+    if (w_dtype < ANELM_F32 || w_dtype > ANELM_BF16) return fail(ANELM_ERR_INVALID, "%s: dtype", fn);
+    const bool wal = w_dtype == ANELM_F32 ? aligned16(wq) && aligned16(wk) : aligned8(wq) && aligned8(wk);
+    if (!aligned16(k) || !aligned16(v) || ((k_ld | v_ld) & 3) || !wal || !aligned16(cos_tab) || !aligned16(sin_tab))
+        return fail(ANELM_ERR_INVALID, "%s: needs 16-byte aligned rows (strides multiples of 4)", fn);
+    if (out_f16 < 0 || out_f16 > 2) return fail(ANELM_ERR_INVALID, "%s: out_f16 %d (0, 1 or 2)", fn, out_f16);
+    if (out_f16 == 2 && !aligned16(out)) return fail(ANELM_ERR_INVALID, "%s: the tiled output needs 16-byte alignment", fn);
+    InvFreq inv;
+    rope_inv_freq(&inv, 128, theta);
+    if (out_f16) a.out16 = static_cast<uint16_t*>(out);
+    else a.out = static_cast<float*>(out);
+    if (out_f16 == 2) a.out_cols = n_heads * 128;
+    a.q = q; a.kc = k_cache; a.vc = v_cache;
+    a.ring_start = ring_start; a.ring_len = ring_len;
+    a.nh = n_heads; a.nkv = n_kv_heads;
+    a.q_ld = q_ld; a.q_hs = 128; a.out_ld = out_ld;
+    a.cap = capacity; a.seq_stride = cache_seq_stride;
+    a.kraw = k; a.vraw = v; a.k_ld = k_ld; a.v_ld = v_ld;
+    a.wq = wq; a.wk = wk; a.pos = pos;
+    a.cos_tab = cos_tab; a.sin_tab = sin_tab; a.tab_len = tab_len; a.eps = eps;
+    for (int j = 0; j < 64; j++) a.inv[j] = inv.v[j];
+    return ANELM_OK;
 }
 
 }  // namespace
@@ -789,36 +838,39 @@ extern "C" int anelm_gqa_attention_qk(void* out, int out_f16, const float* q, co
                                       const int32_t* ring_start, const int32_t* ring_len, long batch, int n_heads,
                                       int n_kv_heads, long out_ld, int capacity, long cache_seq_stride,
                                       void* workspace, size_t workspace_bytes, void* stream) {
-    const char* fn = "gqa_attention_qk";
     clear_error();
-    int rc = check_common(out, q, k_cache, v_cache, batch, n_heads, n_kv_heads, 128, q_ld, 128, out_ld, capacity,
-                          cache_seq_stride);
-    if (rc) return rc;
-    if (!ring_start || !ring_len || !k || !v || !pos) return fail(ANELM_ERR_INVALID, "%s: null pointer", fn);
-    const long row = (long)n_kv_heads * 128;
-    if (batch > 1 && (k_ld < row || v_ld < row)) return fail(ANELM_ERR_INVALID, "%s: k/v strides overlap", fn);
-    if (tab_len < 1 || !cos_tab || !sin_tab) return fail(ANELM_ERR_INVALID, "%s: needs a RoPE table of >= 1 row", fn);
-    if (!wq || !wk) return fail(ANELM_ERR_INVALID, "%s: needs both q and k gammas", fn);
-    if (w_dtype < ANELM_F32 || w_dtype > ANELM_BF16) return fail(ANELM_ERR_INVALID, "%s: dtype", fn);
-    const bool wal = w_dtype == ANELM_F32 ? aligned16(wq) && aligned16(wk) : aligned8(wq) && aligned8(wk);
-    if (!aligned16(k) || !aligned16(v) || ((k_ld | v_ld) & 3) || !wal || !aligned16(cos_tab) || !aligned16(sin_tab))
-        return fail(ANELM_ERR_INVALID, "%s: needs 16-byte aligned rows (strides multiples of 4)", fn);
-    if (out_f16 < 0 || out_f16 > 2) return fail(ANELM_ERR_INVALID, "%s: out_f16 %d (0, 1 or 2)", fn, out_f16);
-    if (out_f16 == 2 && !aligned16(out)) return fail(ANELM_ERR_INVALID, "%s: the tiled output needs 16-byte alignment", fn);
-    InvFreq inv;
-    rope_inv_freq(&inv, 128, theta);
     AttnArgs a{};
-    if (out_f16) a.out16 = static_cast<uint16_t*>(out);
-    else a.out = static_cast<float*>(out);
-    if (out_f16 == 2) a.out_cols = n_heads * 128;
-    a.q = q; a.kc = k_cache; a.vc = v_cache;
-    a.ring_start = ring_start; a.ring_len = ring_len;
-    a.nh = n_heads; a.nkv = n_kv_heads;
-    a.q_ld = q_ld; a.q_hs = 128; a.out_ld = out_ld;
-    a.cap = capacity; a.seq_stride = cache_seq_stride;
-    a.kraw = k; a.vraw = v; a.k_ld = k_ld; a.v_ld = v_ld;
-    a.wq = wq; a.wk = wk; a.pos = pos;
-    a.cos_tab = cos_tab; a.sin_tab = sin_tab; a.tab_len = tab_len; a.eps = eps;
-    for (int j = 0; j < 64; j++) a.inv[j] = inv.v[j];
+    const int rc = qk_args(a, "gqa_attention_qk", out, out_f16, q, k, v, q_ld, k_ld, v_ld, wq, wk, w_dtype, pos,
+                           cos_tab, sin_tab, tab_len, theta, eps, k_cache, v_cache, ring_start, ring_len, batch,
+                           n_heads, n_kv_heads, out_ld, capacity, cache_seq_stride);
+    if (rc) return rc;
     return run(a, batch, 128, capacity, workspace, workspace_bytes, as_stream(stream), w_dtype);
+}
+
+// The same with the rings' advance in the call (qwen3.cpp:475-484, then the
+// append and attention of :487-492): every argument and the workspace are
+// checked before anything is launched, then one launch advances the batch's
+// rings and the next makes, stores and attends over the new rows.
+extern "C" int anelm_gqa_attention_qk_append(void* out, int out_f16, const float* q, const float* k,
+                                             const float* v, long q_ld, long k_ld, long v_ld, const void* wq,
+                                             const void* wk, int w_dtype, const int32_t* pos, const float* cos_tab,
+                                             const float* sin_tab, int tab_len, float theta, float eps,
+                                             float* k_cache, float* v_cache, int32_t* ring_start, int32_t* ring_len,
+                                             long batch, int n_heads, int n_kv_heads, long out_ld, int capacity,
+                                             long cache_seq_stride, void* workspace, size_t workspace_bytes,
+                                             void* stream) {
+    clear_error();
+    AttnArgs a{};
+    int rc = qk_args(a, "gqa_attention_qk_append", out, out_f16, q, k, v, q_ld, k_ld, v_ld, wq, wk, w_dtype, pos,
+                     cos_tab, sin_tab, tab_len, theta, eps, k_cache, v_cache, ring_start, ring_len, batch, n_heads,
+                     n_kv_heads, out_ld, capacity, cache_seq_stride);
+    if (rc) return rc;
+    rc = plan(a, batch, 128, capacity, workspace, workspace_bytes);
+    if (rc) return rc;
+    if (batch == 0) return ANELM_OK;
+    const hipStream_t st = as_stream(stream);
+    hipLaunchKernelGGL(kv_ring_advance_kernel, dim3((unsigned)((batch + 255) / 256)), dim3(256), 0, st, ring_start,
+                       ring_len, batch, batch, batch, capacity);
+    dispatch(a, batch, 128, st, w_dtype);
+    return launch_status("gqa_attention_qk_append");
 }

@@ -359,6 +359,23 @@ int anelm_gqa_attention_qk(void* out, int out_f16, const float* q, const float* 
                            float* k_cache, float* v_cache, const int32_t* ring_start, const int32_t* ring_len,
                            long batch, int n_heads, int n_kv_heads, long out_ld, int capacity,
                            long cache_seq_stride, void* workspace, size_t workspace_bytes, void* stream);
+/* anelm_kv_ring_advance of the batch's rings (groups 1), then
+ * anelm_gqa_attention_qk, for callers that advance one layer's rings at a
+ * time: the ring append and attention of models/llm/qwen3.cpp:475-492 after
+ * the q/k norm + RoPE of :444-472, with no precondition on the ring state
+ * (anelm_gqa_attention_qk needs rings advanced exactly once since its last
+ * call on them).  Arguments as anelm_gqa_attention_qk, ring state writable;
+ * every argument and the workspace size are checked before anything is
+ * launched, so an error leaves the rings unchanged.  Two launches; outputs,
+ * caches and ring state equal the separate calls' bit for bit.  No
+ * counterpart in the reference. */
+int anelm_gqa_attention_qk_append(void* out, int out_f16, const float* q, const float* k, const float* v,
+                                  long q_ld, long k_ld, long v_ld, const void* wq, const void* wk, int w_dtype,
+                                  const int32_t* pos, const float* cos_tab, const float* sin_tab, int tab_len,
+                                  float theta, float eps, float* k_cache, float* v_cache, int32_t* ring_start,
+                                  int32_t* ring_len, long batch, int n_heads, int n_kv_heads, long out_ld,
+                                  int capacity, long cache_seq_stride, void* workspace, size_t workspace_bytes,
+                                  void* stream);
 /* anelm_gqa_attention for callers that know an upper bound on every ring's
  * length (len_bound >= ring_len[b] for all b; e.g. the tokens decoded since
  * the rings were emptied): only ceil(len_bound / chunk) chunks per sequence

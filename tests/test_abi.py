@@ -219,6 +219,17 @@ def test_attention_argument_checks(lib):
     assert call_qk(tab_len=0) == -1 and b"table" in lib.anelm_last_error()
     assert call_qk(k_ld=1000) == -1                                            # k rows overlap
     assert call_qk(dt=7) == -1
+    qa = lib.anelm_gqa_attention_qk_append
+
+    def call_qa(wq=fake, k_ld=48 * 128, ws_bytes=1 << 30):
+        row = 48 * 128
+        return qa(fake, 1, fake, fake, fake, row, k_ld, row, wq, fake, 2, fake, fake, fake, 4096, 1e6, 1e-6, fake,
+                  fake, fake, fake, 2, 32, 8, 32 * 128, 2048, 2048 * 8 * 128, fake, ws_bytes, None)
+
+    # every check comes before the advance launch: a rejected call changes no ring
+    assert call_qa(wq=None) == -1 and b"gqa_attention_qk_append" in lib.anelm_last_error()
+    assert call_qa(k_ld=1000) == -1
+    assert call_qa(ws_bytes=16) == -4 and b"workspace" in lib.anelm_last_error()
     adv = lib.anelm_kv_ring_advance
     assert adv(None, fake, 4, 2, 8, 2048, None) == -1
     assert adv(fake, fake, 4, 2, 3, 2048, None) == -1                          # groups' rings overlap

@@ -343,6 +343,58 @@ def test_gqa_attention_qk_matches_separate_kernels(hip, orc, rng, B, nq, nk, cap
     assert np.array_equal(host(rs2), host(rs)) and np.array_equal(host(rl2), host(rl))
     assert_bitexact(host(b), qkv, "raw q|k|v rows")
 
+    # the same call with the advance inside it (anelm_gqa_attention_qk_append)
+    kc3, vc3, rs3, rl3 = dev(kc0), dev(vc0), dev(rs0), dev(rl0)
+    got3 = torch.full((B, nq * D), float("nan"), dtype=odt, device="cuda")
+    hip.gqa_attention_qk(got3, b[:, :nq * D], b[:, nq * D:(nq + nk) * D], b[:, (nq + nk) * D:], wq, wk, *tabs, kc3,
+                         vc3, rs3, rl3, nq, nk, ws, THETA, EPS, advance=True)
+    assert_bitexact(host(got3), host(ref), "attention output (advance in the call)")
+    assert_bitexact(host(kc3), host(kc), "k cache (advance in the call)")
+    assert_bitexact(host(vc3), host(vc), "v cache (advance in the call)")
+    assert np.array_equal(host(rs3), host(rs)) and np.array_equal(host(rl3), host(rl))
+
+
+@pytest.mark.parametrize("B,cap", [(3, 64), (2, 1024)])
+def test_gqa_attention_qk_append_steps(hip, orc, rng, B, cap):
+    """Successive decode steps through anelm_gqa_attention_qk_append, from
+    empty rings past a wrap of the smaller ring, equal anelm_qknorm_rope_append
+    then anelm_gqa_attention step for step, bit for bit (outputs, caches and
+    ring state), with one workspace reused by every step."""
+    import torch
+
+    D, nq, nk, dt = 128, 16, 8, "bf16"
+    row = (nq + 2 * nk) * D
+    wq, _ = _gamma(rng, D, dt)
+    wk, _ = _gamma(rng, D, dt)
+    c_tab, s_tab = orc.rope_table(2048, D, THETA)
+    tabs = (dev(c_tab), dev(s_tab))
+    ws = torch.zeros(max(hip.gqa_workspace_size(B, nq, nk, D, cap), 16), dtype=torch.uint8, device="cuda")
+    ws2 = torch.zeros_like(ws)
+    kc = torch.zeros((B, cap, nk * D), device="cuda")
+    vc = torch.zeros_like(kc)
+    kc2, vc2 = kc.clone(), vc.clone()
+    rs = torch.zeros(B, dtype=torch.int32, device="cuda")
+    rl = torch.zeros_like(rs)
+    rs2, rl2 = rs.clone(), rl.clone()
+    steps = cap + 5 if cap <= 64 else 70
+    for t in range(steps):
+        raw = rng.standard_normal((B, row), dtype=np.float32)
+        pos = dev(np.full(B, t, np.int32))
+        a = dev(raw)   # normalised and rotated in place by the separate kernels
+        hip.qknorm_rope_append(a[:, :nq * D], a[:, nq * D:(nq + nk) * D], a[:, (nq + nk) * D:], wq, wk, pos,
+                               tabs[0], tabs[1], kc, vc, rs, rl, THETA, EPS, nq=nq, nk=nk)
+        ref = torch.full((B, nq * D), float("nan"), device="cuda")
+        hip.gqa_attention(ref, a[:, :nq * D], kc, vc, rs, rl, nq, nk, D, ws)
+        b = dev(raw)
+        got = torch.full((B, nq * D), float("nan"), device="cuda")
+        hip.gqa_attention_qk(got, b[:, :nq * D], b[:, nq * D:(nq + nk) * D], b[:, (nq + nk) * D:], wq, wk, pos,
+                             tabs[0], tabs[1], kc2, vc2, rs2, rl2, nq, nk, ws2, THETA, EPS, advance=True)
+        assert_bitexact(host(got), host(ref), f"attention output, step {t}")
+    assert_bitexact(host(kc2), host(kc), "k cache")
+    assert_bitexact(host(vc2), host(vc), "v cache")
+    assert np.array_equal(host(rs2), host(rs)) and np.array_equal(host(rl2), host(rl))
+    assert int(host(rl2).min()) == min(steps, cap)
+
 
 def test_kv_ring_advance_layers(hip, rng):
     """Advancing [layers, max_batch] ring state for the first B sequences of
