@@ -41,13 +41,14 @@ void check_hip(hipError_t e, const char* what) {
 // once.  Slots live until the process ends: the HIP runtime may already be
 // shut down when static destructors run, and the pinned buffers, once read
 // by kernels, are never returned.
-constexpr size_t kPinBytes = (size_t)512 << 10;
+constexpr size_t kPinBytes = (size_t)1 << 20;       // per slot
+constexpr size_t kZeroCopyBytes = (size_t)512 << 10;  // operands the kernels read and write in host memory
 
 struct Slot {
     hipStream_t stream = nullptr;
     char* dev = nullptr;
     size_t dev_cap = 0;
-    char* pin = nullptr;   // kPinBytes of pinned, coherent host memory the kernels read and write directly
+    char* pin = nullptr;   // kPinBytes of pinned, coherent host memory: zero-copy operands, or a staging image
 };
 
 std::mutex g_pool_mu;
@@ -94,17 +95,28 @@ class Lease {
             off[i] = total;
             total += (sizes[i] + 255) & ~(size_t)255;
         }
-        zero_copy_ = total <= kPinBytes;
-        const size_t dev_need = (zero_copy_ ? 0 : total) + scratch;
-        if (dev_need > slot_->dev_cap) {
-            if (slot_->dev) check_hip(hipFree(slot_->dev), "hipFree");
-            const size_t ncap = dev_need < ((size_t)1 << 20) ? ((size_t)1 << 20) : dev_need;
-            check_hip(hipMalloc(reinterpret_cast<void**>(&slot_->dev), ncap), "hipMalloc");
-            slot_->dev_cap = ncap;
-        }
+        zero_copy_ = total <= kZeroCopyBytes;
+        device((zero_copy_ ? 0 : total) + scratch);
         char* base = zero_copy_ ? slot_->pin : slot_->dev;
         for (size_t i = 0; i < N; i++) out[i] = base + off[i];
         if (scratch_out) *scratch_out = slot_->dev + (zero_copy_ ? 0 : total);
+    }
+    // The slot's device buffer, at least n bytes.
+    char* device(size_t n) {
+        if (n > slot_->dev_cap) {
+            if (slot_->dev) check_hip(hipFree(slot_->dev), "hipFree");
+            const size_t ncap = n < ((size_t)1 << 20) ? ((size_t)1 << 20) : n;
+            check_hip(hipMalloc(reinterpret_cast<void**>(&slot_->dev), ncap), "hipMalloc");
+            slot_->dev_cap = ncap;
+        }
+        return slot_->dev;
+    }
+    // The slot's pinned buffer (kPinBytes), for a call that lays out its own
+    // staging image; the call's sync() orders its reuse.
+    char* pinned() const { return slot_->pin; }
+    // One copy of the first n bytes of the pinned buffer to d.
+    void h2d_staged(void* d, size_t n) {
+        check_hip(hipMemcpyAsync(d, slot_->pin, n, hipMemcpyHostToDevice, s()), "hipMemcpy H2D");
     }
     void h2d(void* d, const void* h, size_t n) {
         if (zero_copy_)
@@ -372,22 +384,47 @@ int sample_token(const float* logits, int vocab_size, const SamplingParams& para
     Lease S;
     const long nh = (long)recent_tokens.size();
     const size_t ws = anelm_sample_workspace_size(1, vocab_size);
-    // the probabilities (d[4]) are written and never read back
-    const size_t sz[5] = {(size_t)vocab_size * 4, (size_t)(nh > 0 ? nh : 1) * 4, 16, 16, (size_t)vocab_size * 4};
-    char* d[5];
-    char* dws = nullptr;
-    S.get(sz, d, ws, &dws);
-    S.h2d(d[0], logits, sz[0]);
-    if (nh > 0) S.h2d(d[1], recent_tokens.data(), (size_t)nh * 4);
     const bool draw = params.temperature > 0.0f;
     // the reference's draw (sampling.cpp:58), only on the sampling path
     const float r = draw ? (float)drand48() : 0.0f;
-    S.h2d(d[2], &r, 4);
     anelm_sampling_params p;
     p.temperature = params.temperature;
     p.repetition_penalty = params.repetition_penalty;
     p.repetition_context_size = params.repetition_context_size;
     p.frequency_penalty = params.frequency_penalty;
+    auto up = [](size_t n) { return (n + 255) & ~(size_t)255; };
+    const size_t lb = (size_t)vocab_size * 4, hb = (size_t)(nh > 0 ? nh : 1) * 4;
+    const size_t o_hist = up(lb), o_r = o_hist + up(hb), in_bytes = o_r + 256;
+    if (in_bytes + 256 <= kPinBytes) {
+        // The inputs as one image in the pinned buffer, one copy to the
+        // device (the vocabulary's logits are read by several kernels, so
+        // they go to HBM once rather than over the bus per read); the id
+        // comes back zero-copy behind the image, the probabilities (written,
+        // never read back) and the workspace stay on the device.
+        char* pin = S.pinned();
+        char* dev = S.device(in_bytes + up(lb) + ws);
+        std::memcpy(pin, logits, lb);
+        if (nh > 0) std::memcpy(pin + o_hist, recent_tokens.data(), (size_t)nh * 4);
+        std::memcpy(pin + o_r, &r, 4);
+        volatile int32_t* id = reinterpret_cast<volatile int32_t*>(pin + in_bytes);
+        S.h2d_staged(dev, in_bytes);
+        check_rc(anelm_sample(const_cast<int32_t*>(id), reinterpret_cast<float*>(dev + in_bytes), vocab_size,
+                              reinterpret_cast<const float*>(dev), vocab_size, 1, vocab_size,
+                              nh > 0 ? reinterpret_cast<const int32_t*>(dev + o_hist) : nullptr, nh, nullptr, &p,
+                              reinterpret_cast<const float*>(dev + o_r), ws ? dev + in_bytes + up(lb) : nullptr, ws,
+                              S.s()),
+                 "sample_token");
+        S.sync();
+        return *id;
+    }
+    // the probabilities (d[4]) are written and never read back
+    const size_t sz[5] = {lb, hb, 16, 16, lb};
+    char* d[5];
+    char* dws = nullptr;
+    S.get(sz, d, ws, &dws);
+    S.h2d(d[0], logits, sz[0]);
+    if (nh > 0) S.h2d(d[1], recent_tokens.data(), (size_t)nh * 4);
+    S.h2d(d[2], &r, 4);
     check_rc(anelm_sample(reinterpret_cast<int32_t*>(d[3]), reinterpret_cast<float*>(d[4]), vocab_size,
                           reinterpret_cast<const float*>(d[0]),
                           vocab_size, 1, vocab_size, nh > 0 ? reinterpret_cast<const int32_t*>(d[1]) : nullptr, nh,
