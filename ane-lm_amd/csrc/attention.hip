@@ -20,6 +20,9 @@
 // merges them.  The grid is (kv head, sequence, chunk), chunk slowest: a
 // short ring is done by its chunk 0 alone (the other chunks exit at once), and
 // with chunks dispatched last those workgroups all start in the first round.
+// With many (sequence, kv head) pairs and rings of at most 2048 rows, one
+// workgroup per pair takes the whole ring instead (the same phases over up
+// to 2048 positions), and nothing is merged.
 #include "anelm_common.hpp"
 
 namespace anelm {
@@ -27,7 +30,16 @@ namespace {
 
 constexpr int kAttnThreads = 256;     // 4 waves
 constexpr int kAttnWaves = kAttnThreads / kWave;
-constexpr int kMaxChunk = 512;        // ring positions per workgroup
+constexpr int kMaxChunk = 512;        // ring positions per workgroup of a split launch
+// Whole-ring launches: with at least kWholeRingPairs (sequence, kv head)
+// pairs (two per CU) and rings of at most kWholeRingMax rows, one workgroup
+// per pair attends over the whole ring and writes the output itself: no
+// partials, counts or merges, whose tail latency in every split workgroup
+// (device-scope stores, a count, the last chunk's loads) left its CU idle.
+// 64 sequences at 8B shapes with 2048-row rings: 175 -> 165 us.  Below two
+// pairs per CU some CUs would run two rings and others one.
+constexpr int kWholeRingMax = 2048;
+constexpr long kWholeRingPairs = 512;
 // 64, not 32: a workgroup keeps two 32-position batches of loads in flight,
 // so a 64-position chunk costs about one memory round trip like a 32-position
 // one, and a long ring at a small batch has half the chunks to merge.
@@ -76,6 +88,7 @@ struct AttnArgs {
     int tab_len;
     float eps;
     float inv[64];              // RoPE inverse frequencies of the 64 pairs
+    int whole_ring;             // launch one workgroup per (sequence, kv head) over the whole ring
 };
 
 // An attention output (sequence b, column col = head*head_dim + d): fp32, or
@@ -218,7 +231,7 @@ __device__ void merge_head(const AttnArgs& a, long b, int h, int lane, int live)
 template <int D>
 __device__ __forceinline__ int elem_of(int ds, int i) { return (i < 4 ? 0 : D / 2 - 4) + 4 * ds + i; }
 
-template <int D, int GM, bool FINAL, int QK = -1>
+template <int D, int GM, bool FINAL, int QK = -1, int MC = kMaxChunk>   // MC: chunk positions whose scores fit in LDS
 __global__ __launch_bounds__(kAttnThreads) void gqa_decode_kernel(AttnArgs a) {
     static_assert(QK < 0 || D == 128, "the fused q/k norm + RoPE is for 128-wide heads");
     constexpr int LP = D / 8;                  // lanes per position
@@ -226,7 +239,7 @@ __global__ __launch_bounds__(kAttnThreads) void gqa_decode_kernel(AttnArgs a) {
     constexpr int PPB = PPW * kAttnWaves;      // positions per workgroup per round
     constexpr int U = 2;                       // rounds per batch of loads (two batches in flight)
     constexpr int STEP = U * PPB;              // positions per batch
-    __shared__ float sc[GM][kMaxChunk];        // scores, then weights
+    __shared__ float sc[GM][MC];               // scores, then weights
     __shared__ float red[kAttnWaves][GM][D];   // per-wave partial outputs
     __shared__ float hm[GM], hl[GM];
 
@@ -548,6 +561,16 @@ int group_max(int D) { return kMaxGD / D < 8 ? kMaxGD / D : 8; }
 
 template <int D, int GM, int QK>
 void launch_gm(const AttnArgs& a, long batch, hipStream_t st) {
+    if constexpr (GM <= 4) {   // the whole ring's scores within 32 KB of LDS
+        if (a.whole_ring) {
+            AttnArgs w = a;
+            w.nsplit = 1;
+            w.chunk = w.whole = a.cap;
+            hipLaunchKernelGGL((gqa_decode_kernel<D, GM, true, QK, kWholeRingMax>), dim3(a.nkv, batch, 1),
+                               dim3(kAttnThreads), 0, st, w);
+            return;
+        }
+    }
     const dim3 grid(a.nkv, batch, a.nsplit);
     if (a.nsplit == 1) {
         hipLaunchKernelGGL((gqa_decode_kernel<D, GM, true, QK>), grid, dim3(kAttnThreads), 0, st, a);
@@ -648,6 +671,8 @@ int plan(AttnArgs& a, long batch, int D, int bound, void* ws, size_t ws_bytes) {
         a.ctr = reinterpret_cast<unsigned*>(static_cast<char*>(ws) + ctr_offset(ws_bytes));
     }
     a.ws = static_cast<float*>(ws);
+    // every ring attended whole (not a bounded launch shorter than the rings)
+    a.whole_ring = bound >= a.cap && a.cap <= kWholeRingMax && batch * a.nkv >= kWholeRingPairs;
     return ANELM_OK;
 }
 

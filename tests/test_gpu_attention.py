@@ -116,12 +116,34 @@ def test_whole_ring_threshold(hip, orc, rng):
         check(got[b], q[b], kc[b], vc[b], nq, nk, D, starts[b], lens[b], orc)
 
 
+@pytest.mark.parametrize("B,nq,nk,D,cap", [
+    (64, 8, 8, 128, 1024),     # one q head per kv head, 512 pairs: whole-ring workgroups
+    (63, 16, 8, 128, 1024),    # 504 pairs: split launch, the threshold's other side
+    (128, 8, 4, 64, 300),      # head_dim 64, groups of 2
+    (128, 16, 4, 256, 200),    # head_dim 256, groups of 4
+    (64, 64, 8, 128, 256),     # groups of 8: above the whole-ring LDS budget, split launch
+])
+def test_whole_ring_launches(hip, orc, rng, B, nq, nk, D, cap):
+    """At two or more (sequence, kv head) pairs per CU and rings of at most
+    2048 rows, one workgroup per pair attends over its whole ring: ring
+    states empty, single, full, wrapped and random, against the oracle."""
+    starts = rng.integers(-cap, 2 * cap, B)
+    lens = rng.integers(0, cap + 1, B)
+    lens[:5] = [0, 1, cap, cap, cap - 1]
+    starts[2] = 0
+    got, q, kc, vc = batched(hip, B, nq, nk, D, cap, starts, lens, rng)
+    for b in list(range(8)) + list(range(B - 8, B)):
+        st = int(starts[b]) % cap
+        check(got[b], q[b], kc[b], vc[b], nq, nk, D, st, int(lens[b]), orc)
+
+
 @pytest.mark.parametrize("B,cap,lens", [(6, 2048, [0, 1, 127, 128, 129, 2048]), (3, 100, [1, 50, 100]),
-                                       (3, 32, [1, 20, 32])])
+                                       (3, 32, [1, 20, 32]), (64, 256, [0, 1, 256, 255] + [77] * 60)])
 def test_fp16_output_is_fp32_output_rounded(hip, orc, rng, B, cap, lens):
     """The fp16-output attention writes the fp32 attention's values rounded
     to nearest even, bit for bit: whole rings written by chunk 0, split rings
-    through the merge, and a single-chunk launch."""
+    through the merge, a single-chunk launch, and one workgroup per ring at
+    64 sequences."""
     import torch
 
     nq, nk, D = 16, 8, 128
