@@ -273,7 +273,7 @@ __global__ __launch_bounds__(kAttnThreads) void gqa_decode_kernel(AttnArgs a) {
     // the loops) and are discarded.
     // QK: the newest row (position len-1) is made here, in this lane's slice
     // layout, by the workgroup whose chunk holds it, substituted for what the
-    // caches held at its slot, and written to the caches at the end.  The
+    // caches held at its slot, and written to the caches once made.  The
     // RoPE angles, gammas, raw k and v, the q heads and the first K batch are
     // all loaded before any of them is used, so the loads overlap.
     float knew[8], vnew[8], kr[8];
@@ -353,6 +353,18 @@ __global__ __launch_bounds__(kAttnThreads) void gqa_decode_kernel(AttnArgs a) {
                                gkl, gkh, rc, rs, a.eps, ol, oh);
                 knew[0] = ol.x; knew[1] = ol.y; knew[2] = ol.z; knew[3] = ol.w;
                 knew[4] = oh.x; knew[5] = oh.y; knew[6] = oh.z; knew[7] = oh.w;
+                // The new row goes to the caches now, not behind the
+                // outputs: this workgroup's own loads of its slot (the only
+                // ones) are replaced by these registers whatever they return.
+                if (tid < LP) {   // one 16-lane group stores the row
+                    const long slot = ring_slot(a, start, t0, tnew, n);
+                    float* kd = const_cast<float*>(kbase) + slot * row;
+                    float* vd = const_cast<float*>(vbase) + slot * row;
+                    *reinterpret_cast<float4*>(kd) = ol;
+                    *reinterpret_cast<float4*>(kd + D / 2) = oh;
+                    *reinterpret_cast<float4*>(vd) = make_float4(vnew[0], vnew[1], vnew[2], vnew[3]);
+                    *reinterpret_cast<float4*>(vd + D / 2) = make_float4(vnew[4], vnew[5], vnew[6], vnew[7]);
+                }
             }
         }
         auto scores = [&](const float (&kx)[U][8], int r0) {
@@ -469,19 +481,6 @@ __global__ __launch_bounds__(kAttnThreads) void gqa_decode_kernel(AttnArgs a) {
                 st_dev(p + D, hm[g]);
                 st_dev(p + D + 1, hl[g]);
             }
-        }
-    }
-    // QK: the new row goes to the caches last, once this workgroup's own
-    // reads of the chunk (which may cover its slot) are done
-    if constexpr (QK >= 0) {
-        if (owns && tid < LP) {   // one 16-lane group stores the row
-            const long slot = ring_slot(a, start, t0, tnew, n);
-            float* kd = const_cast<float*>(kbase) + slot * row;
-            float* vd = const_cast<float*>(vbase) + slot * row;
-            *reinterpret_cast<float4*>(kd) = make_float4(knew[0], knew[1], knew[2], knew[3]);
-            *reinterpret_cast<float4*>(kd + D / 2) = make_float4(knew[4], knew[5], knew[6], knew[7]);
-            *reinterpret_cast<float4*>(vd) = make_float4(vnew[0], vnew[1], vnew[2], vnew[3]);
-            *reinterpret_cast<float4*>(vd + D / 2) = make_float4(vnew[4], vnew[5], vnew[6], vnew[7]);
         }
     }
     if (!fin) {
