@@ -5,7 +5,7 @@
 // rounded as written, because the probabilities must be bit-identical to
 // the sequential reference formula for the sampled ids to match.
 //
-// Pipeline per call (rows x vocab; chunks of K slices of 1024 logits, K = 4
+// Pipeline per call (rows x vocab; chunks of K slices of 1024 logits, K = 3
 // unless the call has too few rows to fill the GPU with such chunks, then
 // K = 1; sub-tiles of kSub = 256):
 //   stage1  grid (chunks, rows): penalties + 1/T, per-chunk max (or argmax)
@@ -19,6 +19,10 @@
 //           walking the others exactly, with no barriers
 // Stages 1 and 2 recompute the adjusted logit from the input (a few flops)
 // instead of storing it; stage 3 reads the exponentials stage 2 stored.
+// With many sampling rows stages 1-3 run as one launch instead (chunks of
+// kFusedK slices kept in registers, row barriers between the stages; see
+// "stages 1-3 in one launch"): the logits are read once and the
+// probabilities written once.
 #pragma clang fp contract(off)
 
 #include <climits>
@@ -61,6 +65,10 @@ struct SampleArgs {
     int32_t* ws_cls;      // [rows, nsub] predicted binade class (-1: none)
     uint32_t* ws_xing;    // [rows, nsub, kXWords] predicted crossing (see predict_crossing)
     int32_t* ws_first;    // [rows, 2] sub-tiles 0..first_subs-1 walked by stage 3: hit index or -1, end bits
+    // the one-launch path (stages 1-3 in one kernel) only; null otherwise
+    uint64_t* ws_tok;     // [rows, 2, nchunk] done flags of its two row barriers
+    uint64_t* ws_rowtok;  // [rows, 2] the call's token, and the token again when a row barrier gave up
+    uint64_t* epoch;      // one-launch calls made on this workspace (advanced by the walk)
     int first_subs;       // sub-tiles stage 3 walks one add at a time (1 or kFirstSubs)
     int nchunk;
     int nsub;
@@ -129,8 +137,12 @@ __device__ __forceinline__ HistFirst hist_first(const SampleArgs& a, long row) {
 }
 
 // cnt[i - c0] = occurrences of id i in the window for i in [c0, c0 + n)
-// (n a multiple of 4), ids outside [0, vocab) ignored (sampling.cpp:23).
-__device__ void build_counts(uint32_t* cnt, int n, const SampleArgs& a, long row, long c0, HistFirst f) {
+// (n a multiple of 8), ids outside [0, vocab) ignored (sampling.cpp:23).
+// PK: two 16-bit counts per word (id i - c0 in half (i - c0) & 1 of word
+// (i - c0) / 2), half the LDS; for windows of at most 65535 ids, so that no
+// count carries into its neighbour.
+template <bool PK = false>
+__device__ __forceinline__ void build_counts(uint32_t* cnt, int n, const SampleArgs& a, long row, long c0, HistFirst f) {
     const int32_t* h = a.hist + row * a.hist_ld;
     int id0 = f.valid ? f.raw : -1;
     if (a.use_penalty && a.hist_len) {
@@ -141,14 +153,19 @@ __device__ void build_counts(uint32_t* cnt, int n, const SampleArgs& a, long row
         const long j = f.start + threadIdx.x;
         if (j < hl) id0 = h[j];
     }
-    for (int i = 4 * threadIdx.x; i < n; i += 4 * blockDim.x) *reinterpret_cast<uint4*>(cnt + i) = make_uint4(0u, 0u, 0u, 0u);
+    const int words = PK ? n / 2 : n;
+    for (int i = 4 * threadIdx.x; i < words; i += 4 * blockDim.x) *reinterpret_cast<uint4*>(cnt + i) = make_uint4(0u, 0u, 0u, 0u);
     __syncthreads();
-    if (a.use_penalty) {
-        if (id0 >= 0 && id0 < a.vocab && id0 >= c0 && id0 < c0 + n) atomicAdd(&cnt[id0 - c0], 1u);
-        for (long j = f.start + threadIdx.x + blockDim.x; j < f.hl; j += blockDim.x) {
-            const int id = h[j];
-            if (id >= 0 && id < a.vocab && id >= c0 && id < c0 + n) atomicAdd(&cnt[id - c0], 1u);
+    auto count = [&](int id) {
+        if (id >= 0 && id < a.vocab && id >= c0 && id < c0 + n) {
+            const int o = (int)(id - c0);
+            if (PK) atomicAdd(&cnt[o >> 1], 1u << (16 * (o & 1)));
+            else atomicAdd(&cnt[o], 1u);
         }
+    };
+    if (a.use_penalty) {
+        count(id0);
+        for (long j = f.start + threadIdx.x + blockDim.x; j < f.hl; j += blockDim.x) count(h[j]);
     }
     __syncthreads();
 }
@@ -167,11 +184,19 @@ __device__ __forceinline__ float adjust(float l, uint32_t n, const SampleArgs& a
 
 // The 4K adjusted logits of this thread in place (the element order of
 // load_chunk); the counts come in K 16-byte LDS reads before any use.
-template <int K>
+// PK: the counts two per word (build_counts<true>).
+template <int K, bool PK = false>
 __device__ __forceinline__ void adjust_k(float v[4 * K], const uint32_t* cnt, const SampleArgs& a) {
     uint4 n[K];
 #pragma unroll
-    for (int k = 0; k < K; k++) n[k] = *reinterpret_cast<const uint4*>(cnt + k * kSlice + 4 * threadIdx.x);
+    for (int k = 0; k < K; k++) {
+        if constexpr (PK) {
+            const uint2 w = *reinterpret_cast<const uint2*>(cnt + (k * kSlice + 4 * threadIdx.x) / 2);
+            n[k] = make_uint4(w.x & 0xFFFFu, w.x >> 16, w.y & 0xFFFFu, w.y >> 16);
+        } else {
+            n[k] = *reinterpret_cast<const uint4*>(cnt + k * kSlice + 4 * threadIdx.x);
+        }
+    }
 #pragma unroll
     for (int k = 0; k < K; k++) {
         // Most 256-logit slices of a wave hold no id of the window (256 ids
@@ -291,7 +316,7 @@ __device__ __forceinline__ SumShare sum_rest(const SampleArgs& a, long row, int 
 // exact power-of-two scaling, correctly rounded reciprocal (cpu_ops.cpp:95-97),
 // and the prefix as a float (a prediction only).  Any block size; the values
 // do not depend on it.
-__device__ void reduce_sums(SumShare sh, const SampleArgs& a, uint64_t* red_s, uint64_t* red_p, int* red_f,
+__device__ __forceinline__ void reduce_sums(SumShare sh, const SampleArgs& a, uint64_t* red_s, uint64_t* red_p, int* red_f,
                             float& inv, float& prefix) {
     uint64_t s = wave_sum_u64(sh.all), pre = wave_sum_u64(sh.pre);
     int f = __any(sh.flag) ? 1 : 0;
@@ -658,6 +683,28 @@ __device__ __forceinline__ void exp_and_sum(const float (&v)[4 * K], float neg, 
     sum.finish(acc, nan);
 }
 
+// The same exponentials kept in v (0 past the end of the row) instead of
+// stored, and this lane's sum of them.  The exp is computed for every slot
+// and the padding selected away (no branch per element).
+template <int K, bool F64>
+__device__ __forceinline__ void exp_and_sum_keep(float (&v)[4 * K], float neg, const SampleArgs& a, int nvalid,
+                                                 uint64_t& acc, int& nan) {
+    const float scale = ldexpf(1.0f, a.shift);
+    const double scaled = ldexp(1.0, a.shift);
+    LaneSum<F64> sum;
+#pragma unroll
+    for (int k = 0; k < K; k++) {
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int li = k * kSlice + 4 * threadIdx.x + e;
+            const float ev = sampler_expf(v[4 * k + e] + neg);
+            v[4 * k + e] = li < nvalid ? ev : 0.0f;
+            sum.add(v[4 * k + e], scale, scaled);
+        }
+    }
+    sum.finish(acc, nan);
+}
+
 // ---- stage 2: exact fixed-point sum of exp(x - max) per chunk ---------------
 // floor(e * 2^shift) summed as integers (associative, so independent of the
 // reduction order); any NaN term flags the row.  The values e are stored in
@@ -804,54 +851,40 @@ __device__ bool walk_first_lds(const float* sp, int nsubs, long V, float r, uint
 // the in-order composition of its elements' maps under that binade.  The walk
 // uses a map only if the actual running sum turns out to lie in that binade
 // and the map shows no element leaving it; otherwise it walks exactly.
+// Stage 3's work once the chunk's exponentials v (0 past the end of the row),
+// 1/sum and the exact prefix of the earlier chunks' sums are known: the
+// probabilities, the first sub-tiles' walk (chunk 0) and the sub-tile maps.
+// ksum and s_first are the workgroup's LDS.
 template <int K>
-__global__ __launch_bounds__(256) void sample_stage3_kernel(SampleArgs a, int vec_out) {
+__device__ __forceinline__ void probs_and_maps(const SampleArgs& a, const float (&v)[4 * K], long row, int chunk,
+                                               float inv, float prefix, float rdraw, int vec_out, float (*ksum)[4],
+                                               float* s_first) {
     constexpr int kCH = K * kSlice;
-    __shared__ uint64_t red_s[4], red_p[4];
-    __shared__ int red_f[4];
-    __shared__ float ksum[K][4];  // [k][wave] fp32 sums of exp (prediction only)
-    __shared__ __align__(16) float s_first[kFirstN];  // the first k-slice's probabilities for the one-lane walk
-    // Workgroups in dispatch order take chunk 0 of every row first: those
-    // also walk sub-tiles 0..3 (below), the longest job, so it starts early.
-    const long lin = (long)blockIdx.y * gridDim.x + blockIdx.x;
-    const long row = lin % a.rows;
-    const int chunk = (int)(lin / a.rows);
     const long c0 = (long)chunk * kCH;
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-    // the draw is loaded with the exponentials (the first sub-tile's walk
-    // below compares against it), not behind them
-    const float rdraw = a.r ? a.r[row] : 0.0f;
-    // and the chunk sums, so that the reduction below does not wait for them
-    const SumRaw sraw = sum_first(a, row);
-    __builtin_amdgcn_sched_barrier(0);
-    float v[4 * K];  // exp(adjusted - max), as stage 2 stored them
-    load_chunk<K>(v, a.probs + row * a.ld_probs, c0, a.vocab, vec_out != 0);
-    __builtin_amdgcn_sched_barrier(0);
-    const SumShare share = sum_rest(a, row, chunk, sraw);
-    // 1/sum, and the exact prefix of the earlier chunks' sums (the prediction
-    // of the running sum at this chunk's start)
-    float inv, prefix;
-    reduce_sums(share, a, red_s, red_p, red_f, inv, prefix);
-    float p[4 * K];
+    // p = e * (1/sum), one rounding: made here for the stores and again from
+    // the same e where the maps need it, so only the exponentials stay live
+    // across the walk and the maps (the same bits, fewer registers)
     float* out = a.probs + row * a.ld_probs;
 #pragma unroll
     for (int k = 0; k < K; k++) {
         float ks = 0.f;
+        float p[4];
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const float e = v[4 * k + j];  // 0 past the end of the row
             ks += e;
-            p[4 * k + j] = e * inv;
+            p[j] = e * inv;
         }
         ks = wave_sum(ks);
         if (lane == 0) ksum[k][wid] = ks;
         const long i = c0 + k * kSlice + 4 * threadIdx.x;
         if (vec_out && i + 3 < a.vocab) {  // cached store: the walk reads these back
-            *reinterpret_cast<float4*>(out + i) = make_float4(p[4 * k], p[4 * k + 1], p[4 * k + 2], p[4 * k + 3]);
+            *reinterpret_cast<float4*>(out + i) = make_float4(p[0], p[1], p[2], p[3]);
         } else {
 #pragma unroll
             for (int j = 0; j < 4; j++)
-                if (i + j < a.vocab) out[i + j] = p[4 * k + j];
+                if (i + j < a.vocab) out[i + j] = p[j];
         }
     }
     // The row's first sub-tiles start from an exact running sum, 0, that is
@@ -866,7 +899,8 @@ __global__ __launch_bounds__(256) void sample_stage3_kernel(SampleArgs a, int ve
     // exact walks were most of the slowest rows' extra walk time); with a few
     // rows stage 3 is too short to hide more than one.
     if (chunk == 0 && a.r)
-        *reinterpret_cast<float4*>(&s_first[wid * kSub + 4 * lane]) = make_float4(p[0], p[1], p[2], p[3]);
+        *reinterpret_cast<float4*>(&s_first[wid * kSub + 4 * lane]) =
+            make_float4(v[0] * inv, v[1] * inv, v[2] * inv, v[3] * inv);
     __syncthreads();  // ksum and s_first complete; the other waves need not wait for the walk below
     if (chunk == 0 && wid == 0 && a.r) {
         __builtin_amdgcn_s_setprio(3);
@@ -907,16 +941,17 @@ __global__ __launch_bounds__(256) void sample_stage3_kernel(SampleArgs a, int ve
         const Binade b = binade_of_class(ok ? cls : 0);
         const int nv = a.vocab - (c0 + k * kSlice + 256 * wid) < kSub ? (int)(a.vocab - (c0 + k * kSlice + 256 * wid))
                                                                        : kSub;  // valid elements of the sub-tile
+        const float p[4] = {v[4 * k] * inv, v[4 * k + 1] * inv, v[4 * k + 2] * inv, v[4 * k + 3] * inv};
         Fn f[4];
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            const Fn m = elem_map(p[4 * k + j], b);
+            const Fn m = elem_map(p[j], b);
             const bool in = 4 * lane + j < nv;
             f[j].a0 = in ? m.a0 : 0u;
             f[j].a1 = in ? m.a1 : 0u;
         }
         const Fn acc = compose4_scan(f);
-        const Crossing x = predict_crossing(acc, f, &p[4 * k], nv, ok, cb, cls, b);
+        const Crossing x = predict_crossing(acc, f, p, nv, ok, cb, cls, b);
         if (lane == 63 && st < a.nsub) {
             a.ws_map0[row * a.nsub_ld + st] = acc.a0;
             a.ws_map1[row * a.nsub_ld + st] = acc.a1;
@@ -931,6 +966,193 @@ __global__ __launch_bounds__(256) void sample_stage3_kernel(SampleArgs a, int ve
         }
         run = run + ((ksum[k][0] + ksum[k][1]) + (ksum[k][2] + ksum[k][3]));
     }
+}
+
+template <int K>
+__global__ __launch_bounds__(256) void sample_stage3_kernel(SampleArgs a, int vec_out) {
+    constexpr int kCH = K * kSlice;
+    __shared__ uint64_t red_s[4], red_p[4];
+    __shared__ int red_f[4];
+    __shared__ float ksum[K][4];  // [k][wave] fp32 sums of exp (prediction only)
+    __shared__ __align__(16) float s_first[kFirstN];  // the first k-slice's probabilities for the one-lane walk
+    // Workgroups in dispatch order take chunk 0 of every row first: those
+    // also walk sub-tiles 0..3 (below), the longest job, so it starts early.
+    const long lin = (long)blockIdx.y * gridDim.x + blockIdx.x;
+    const long row = lin % a.rows;
+    const int chunk = (int)(lin / a.rows);
+    const long c0 = (long)chunk * kCH;
+    // the draw is loaded with the exponentials (the first sub-tile's walk
+    // below compares against it), not behind them
+    const float rdraw = a.r ? a.r[row] : 0.0f;
+    // and the chunk sums, so that the reduction below does not wait for them
+    const SumRaw sraw = sum_first(a, row);
+    __builtin_amdgcn_sched_barrier(0);
+    float v[4 * K];  // exp(adjusted - max), as stage 2 stored them
+    load_chunk<K>(v, a.probs + row * a.ld_probs, c0, a.vocab, vec_out != 0);
+    __builtin_amdgcn_sched_barrier(0);
+    const SumShare share = sum_rest(a, row, chunk, sraw);
+    // 1/sum, and the exact prefix of the earlier chunks' sums (the prediction
+    // of the running sum at this chunk's start)
+    float inv, prefix;
+    reduce_sums(share, a, red_s, red_p, red_f, inv, prefix);
+    probs_and_maps<K>(a, v, row, chunk, inv, prefix, rdraw, vec_out, ksum, s_first);
+}
+
+// ---- stages 1-3 in one launch (many rows) -----------------------------------
+// As three launches, stages 1 and 2 each read the logits and stage 3 reads the
+// exponentials that stage 2 wrote: each stage is a short kernel whose
+// workgroups make a few dependent memory round trips, and the ramp and drain
+// of every launch leave the GPU part idle.  Here each workgroup keeps its
+// chunk in registers through all three stages (adjusted logits, then
+// exponentials, then probabilities): the logits are read once and the
+// probabilities written once.  The same operations on the same values give
+// the same bits as the three launches.
+//
+// Between the stages the row's workgroups meet at a barrier.  A workgroup
+// publishes its chunk maximum (then its chunk sum) with device-scope stores,
+// waits for them to complete, and sets its done flag to this call's token;
+// its first wave then polls the row's flags with device-scope loads (they
+// bypass the per-XCD L2, which is not coherent across XCDs).  No counter
+// takes the arrivals: arrivals on one address serialise at the memory side.
+// The token is the workspace's epoch + 1, and the walk, which runs after
+// every workgroup of this launch has finished, advances the epoch: flags
+// never need clearing, and a flag left by an earlier call never matches.
+// The barriers need all of a row's workgroups resident at once; the host
+// takes this path only when the whole grid fits on the GPU at once.  A wait
+// still gives up after kRowWaitTicks of real time, marks its row (the walk
+// then returns id -1 for it) and goes on, so every wave exits.
+constexpr int kFusedK = 12;              // 12288 logits per workgroup
+constexpr uint64_t kRowWaitTicks = 20000000u;  // 0.2 s of s_memrealtime (100 MHz)
+
+__device__ __forceinline__ uint64_t ld_agent(const uint64_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent(uint64_t* p, uint64_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_agent(const float* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int32_t ld_agent(const int32_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent(int32_t* p, int32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Wave 0 polls the n flags until every one holds tok (false after
+// kRowWaitTicks); the workgroup's barrier then hands the answer to all.
+__device__ bool row_wait(const uint64_t* flags, int n, uint64_t tok, int* s_ok) {
+    if (threadIdx.x < kWave) {
+        const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+        bool ok = false;
+        while (true) {
+            bool mine = true;
+            for (int c = threadIdx.x; c < n; c += kWave) mine = mine && ld_agent(flags + c) == tok;
+            if (__all(mine)) {
+                ok = true;
+                break;
+            }
+            if (__builtin_amdgcn_s_memrealtime() - t0 > kRowWaitTicks) break;
+            __builtin_amdgcn_s_sleep(1);
+        }
+        if (threadIdx.x == 0) *s_ok = ok ? 1 : 0;
+    }
+    __syncthreads();
+    return *s_ok != 0;
+}
+
+// Grid (nchunk, rows), chunks of K slices, rows counted fastest as in stage 3.
+template <int K>
+__global__ __launch_bounds__(256) void sample_fused_kernel(SampleArgs a, int vec, int vec_out) {
+    constexpr int kCH = K * kSlice;
+    __shared__ __align__(16) uint32_t cnt[kCH / 2];   // window counts, two per word
+    __shared__ float red[4];
+    __shared__ uint64_t red_s[4], red_p[4];
+    __shared__ int red_f[4];
+    __shared__ float ksum[K][4];
+    __shared__ __align__(16) float s_first[kFirstN];
+    __shared__ uint64_t s_tok;
+    __shared__ int s_ok[2];
+    const long lin = (long)blockIdx.y * gridDim.x + blockIdx.x;
+    const long row = lin % a.rows;
+    const int chunk = (int)(lin / a.rows);
+    const long c0 = (long)chunk * kCH;
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    if (threadIdx.x == 0) s_tok = ld_agent(a.epoch) + 1u;   // read before build_counts' barriers
+    const float rdraw = a.r[row];
+    const HistFirst hf = hist_first(a, row);
+    __builtin_amdgcn_sched_barrier(0);
+    float v[4 * K];
+    load_chunk<K>(v, a.logits + row * a.ld_logits, c0, a.vocab, vec != 0);
+    __builtin_amdgcn_sched_barrier(0);
+    build_counts<true>(cnt, kCH, a, row, c0, hf);
+    adjust_k<K, true>(v, cnt, a);
+    const int nvalid = a.vocab - c0 < kCH ? (int)(a.vocab - c0) : kCH;
+    const uint64_t tok = s_tok;
+    uint64_t* flags1 = a.ws_tok + row * 2 * a.nchunk;
+    uint64_t* flags2 = flags1 + a.nchunk;
+    bool ok = true;
+
+    // stage 1: the chunk maximum of the adjusted logits
+    float best = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < K; k++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) best = k * kSlice + 4 * (int)threadIdx.x + e < nvalid ? fmaxf(best, v[4 * k + e]) : best;
+    best = wave_max(best);
+    if (lane == 0) red[wid] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        if (chunk == 0) st_agent(a.ws_rowtok + 2 * row, tok);
+        st_agent(a.ws_max + row * a.nchunk + chunk, fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])));
+        __builtin_amdgcn_s_waitcnt(0);   // the maximum has landed before the flag says so
+        st_agent(flags1 + chunk, tok);
+    }
+    ok = row_wait(flags1, a.nchunk, tok, &s_ok[0]) && ok;
+    float m = -INFINITY;
+    for (int c = threadIdx.x; c < a.nchunk; c += blockDim.x) m = fmaxf(m, ld_agent(a.ws_max + row * a.nchunk + c));
+    const float neg = -reduce_max(m, red);
+
+    // stage 2: the exponentials, kept, and the chunk's exact sum
+    constexpr int kLogTerms = K <= 4 ? 4 : K <= 8 ? 5 : 6;  // ceil(log2(4K)), a lane's terms
+    static_assert(4 * K <= (1 << kLogTerms), "a lane's terms");
+    uint64_t acc;
+    int nan;
+    if (a.shift + kLogTerms <= 53)
+        exp_and_sum_keep<K, true>(v, neg, a, nvalid, acc, nan);
+    else
+        exp_and_sum_keep<K, false>(v, neg, a, nvalid, acc, nan);
+    acc = wave_sum_u64(acc);
+    nan = __any(nan) ? 1 : 0;
+    if (lane == 0) {
+        red_s[wid] = acc;
+        red_f[wid] = nan;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        st_agent(a.ws_sum + row * a.nchunk + chunk, red_s[0] + red_s[1] + red_s[2] + red_s[3]);
+        st_agent(a.ws_flag + row * a.nchunk + chunk, red_f[0] | red_f[1] | red_f[2] | red_f[3]);
+        __builtin_amdgcn_s_waitcnt(0);
+        st_agent(flags2 + chunk, tok);
+    }
+    ok = row_wait(flags2, a.nchunk, tok, &s_ok[1]) && ok;
+    if (!ok && threadIdx.x == 0) st_agent(a.ws_rowtok + 2 * row + 1, tok);   // the walk returns -1 for this row
+    SumShare sh = {0u, 0u, 0};
+    for (int c = threadIdx.x; c < a.nchunk; c += blockDim.x) {
+        const uint64_t w = ld_agent(a.ws_sum + row * a.nchunk + c);
+        sh.all += w;
+        sh.pre += c < chunk ? w : 0u;
+        sh.flag |= ld_agent(a.ws_flag + row * a.nchunk + c);
+    }
+    float inv, prefix;
+    reduce_sums(sh, a, red_s, red_p, red_f, inv, prefix);
+
+    // stage 3
+    probs_and_maps<K>(a, v, row, chunk, inv, prefix, rdraw, vec_out, ksum, s_first);
 }
 
 // ---- the walk ------------------------------------------------------------------
@@ -1229,6 +1451,15 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1))) void
     __shared__ WalkShared sh;
     const int lane = threadIdx.x;
     const long row = blockIdx.x;
+    if (a.epoch) {
+        // after a one-launch call: the next call's token is one more, and a
+        // row whose barrier gave up in that launch has no valid draw
+        if (row == 0 && lane == 0) st_agent(a.epoch, ld_agent(a.epoch) + 1u);
+        if (ld_agent(a.ws_rowtok + 2 * row + 1) == ld_agent(a.ws_rowtok + 2 * row)) {
+            if (lane == 0) a.ids[row] = -1;
+            return;
+        }
+    }
     const float r = a.r[row];
     const long V = a.vocab;
     const float* prow = a.probs + row * a.ld_probs;
@@ -1328,7 +1559,8 @@ static int ceil_log2(long n) {
 }
 
 struct WsLayout {
-    size_t off_sum, off_max, off_arg, off_flag, off_m0, off_m1, off_cls, off_x, off_first, total;
+    size_t off_epoch, off_rowtok, off_tok, off_sum, off_max, off_arg, off_flag, off_m0, off_m1, off_cls, off_x,
+        off_first, total;
 };
 
 static size_t al16(size_t x) { return (x + 15) & ~(size_t)15; }
@@ -1349,8 +1581,14 @@ static WsLayout ws_layout(long rows, long vocab) {
     const size_t nch = (size_t)((vocab + kch - 1) / kch);
     const size_t nsub = (size_t)((vocab + kSub - 1) / kSub);
     const size_t n = (size_t)rows * nch, ns = (size_t)rows * ((nsub + 3) & ~(size_t)3);
+    const size_t nchf = (size_t)((vocab + kFusedK * kSlice - 1) / (kFusedK * kSlice));
     WsLayout l;
-    l.off_sum = 0;
+    // the one-launch path's epoch first, at the same place for every shape
+    // (it counts the calls made on the workspace, whatever their shapes)
+    l.off_epoch = 0;
+    l.off_rowtok = 256;
+    l.off_tok = l.off_rowtok + al16((size_t)rows * 2 * sizeof(uint64_t));
+    l.off_sum = l.off_tok + al16((size_t)rows * 2 * nchf * sizeof(uint64_t));
     l.off_max = l.off_sum + al16(n * sizeof(uint64_t));
     l.off_arg = l.off_max + al16(n * sizeof(float));
     l.off_flag = l.off_arg + al16(n * sizeof(int32_t));
@@ -1379,6 +1617,9 @@ static int bind_workspace(SampleArgs& a, void* ws, size_t ws_bytes, long rows, l
     a.ws_cls = reinterpret_cast<int32_t*>(b + l.off_cls);
     a.ws_xing = reinterpret_cast<uint32_t*>(b + l.off_x);
     a.ws_first = reinterpret_cast<int32_t*>(b + l.off_first);
+    a.ws_tok = nullptr;   // set by the one-launch path
+    a.ws_rowtok = nullptr;
+    a.epoch = nullptr;
     const long kch = (long)chunk_slices(rows, vocab) * kSlice;
     a.nchunk = (int)((vocab + kch - 1) / kch);
     a.nsub = (int)((vocab + kSub - 1) / kSub);
@@ -1441,6 +1682,49 @@ extern "C" int anelm_softmax(float* x, long rows, long n, long ld, void* workspa
 namespace anelm {
 namespace {
 
+// The one-launch path from this many rows.  Per call at 151936 logits (8
+// calls on distinct inputs in a graph), one launch against three: 64 rows
+// 63.8 / 66.5 us, 48 rows 59.4 / 60.6, 32 rows 55.1 / 55.4, 24 rows 53.9 /
+// 52.1, 16 rows 50.5 / 47.0.  Both are bound by the stages' vector
+// instructions (about 100 per logit: penalties, the exact exp, the exact
+// fixed-point sum, the sub-tile maps), not by their bytes; one launch saves
+// the re-reads and the launches' ramps, and its row barriers cost more than
+// that saves when the grid is small.
+constexpr long kFusedMinRows = 48;
+constexpr int kCapDevices = 64;
+
+// Workgroups of the one-launch kernel the current device holds at once
+// (occupancy per CU x CUs), looked up once per device; 0 if unknown.
+long fused_capacity() {
+    static std::mutex mu;
+    static long cap[kCapDevices];
+    static bool known[kCapDevices];
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kCapDevices) return 0;
+    std::lock_guard<std::mutex> lock(mu);
+    if (!known[dev]) {
+        int nb = 0, cus = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, sample_fused_kernel<kFusedK>, 256, 0) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
+            (void)hipGetLastError();
+            nb = cus = 0;
+        }
+        cap[dev] = (long)nb * cus;
+        known[dev] = true;
+    }
+    return cap[dev];
+}
+
+// Whether a sampling call takes the one-launch path: many rows, aligned rows
+// (16-byte loads and stores throughout), a window short enough for 16-bit
+// counts, and a grid that fits on the GPU at once with a tenth to spare.
+bool use_fused(long rows, long vocab, long hist_ld, int ctx, bool penalty, int vec, int vec_out) {
+    if (rows < kFusedMinRows || !vec || !vec_out) return false;
+    if (penalty && (ctx < hist_ld ? (long)ctx : hist_ld) > 65535) return false;
+    const long nchf = (vocab + kFusedK * kSlice - 1) / (kFusedK * kSlice);
+    return rows * nchf * 10 <= fused_capacity() * 9;
+}
+
 // The sampler behind both entry points; `who` names the caller in errors.
 int sample_impl(int32_t* ids, float* probs, long ld_probs, const float* logits, long ld_logits, long rows, long vocab,
                 const int32_t* hist, long hist_ld, const int32_t* hist_len, const anelm_sampling_params* params,
@@ -1487,7 +1771,15 @@ int sample_impl(int32_t* ids, float* probs, long ld_probs, const float* logits, 
     }
     const int vec_out = probs && (ld_probs % 4 == 0) && aligned16(probs);
     a.vec_probs = vec_out;
-    if (one) {
+    if (use_fused(rows, vocab, hist_ld, a.ctx, a.use_penalty != 0, vec, vec_out)) {
+        char* b = static_cast<char*>(workspace);
+        const WsLayout l = ws_layout(rows, vocab);
+        a.epoch = reinterpret_cast<uint64_t*>(b + l.off_epoch);
+        a.ws_rowtok = reinterpret_cast<uint64_t*>(b + l.off_rowtok);
+        a.ws_tok = reinterpret_cast<uint64_t*>(b + l.off_tok);
+        a.nchunk = (int)((vocab + kFusedK * kSlice - 1) / (kFusedK * kSlice));
+        sample_fused_kernel<kFusedK><<<dim3((unsigned)a.nchunk, (unsigned)rows), 256, 0, st>>>(a, vec, vec_out);
+    } else if (one) {
         sample_stage1_kernel<false, 1><<<grd, 256, 0, st>>>(a, vec);
         sample_stage2_kernel<1><<<grd, 256, 0, st>>>(a, vec, vec_out);
         sample_stage3_kernel<1><<<grd, 256, 0, st>>>(a, vec_out);
@@ -1507,8 +1799,9 @@ int sample_impl(int32_t* ids, float* probs, long ld_probs, const float* logits, 
 // is only a stand-in symbol): each device's address is looked up once with
 // hipGetSymbolAddress, with that device current, and kept in scratch_ptr.
 // Nothing in it needs clearing: every word a kernel reads is written earlier
-// in the same call.  Calls that overlap on one GPU share it, and race.
-constexpr size_t kScratchBytes = 4u << 20;   // 186 rows at Qwen3's 151936-row vocabulary
+// in the same call, except the one-launch path's epoch and flags, which work
+// from any contents.  Calls that overlap on one GPU share it, and race.
+constexpr size_t kScratchBytes = 4u << 20;   // 184 rows at Qwen3's 151936-row vocabulary
 constexpr int kMaxDevices = 64;
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 void* scratch_ptr[kMaxDevices];

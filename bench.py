@@ -805,8 +805,9 @@ DN_KERNELS = {"layer_one_call": ("conv_ssm_kernel", ""), "conv_silu_l2": ("conv_
               "ssm_step_gated": ("ssm_step_kernel", "128, 0>"), "ssm_step": ("ssm_step_kernel", "128, -1>")}
 
 
-SAMPLE_KERNELS = {"stage1": ("sample_stage1_kernel", ""), "stage2": ("sample_stage2_kernel", ""),
-                  "stage3": ("sample_stage3_kernel", ""), "walk": ("sample_walk_kernel", "")}
+SAMPLE_KERNELS = {"stages_one_launch": ("sample_fused_kernel", ""), "stage1": ("sample_stage1_kernel", ""),
+                  "stage2": ("sample_stage2_kernel", ""), "stage3": ("sample_stage3_kernel", ""),
+                  "walk": ("sample_walk_kernel", "")}
 SAMPLER = "sampling-64x151936"
 
 # The 64-sequence decode step's LM head (x staged in LDS) and layer kernels
@@ -1002,10 +1003,12 @@ def pmc_summary(fetch_dir, write_dir, copy_fetch_dir, copy_write_dir, workload=H
               "ssm_step_gated": state + B * (2 * nkh * kd + 3 * nvh * vd) * 4,   # q, k, v, z in; out
               "conv_silu_l2": B * ch * 3 * 4 * 2 + ch * 4 * 4 + B * ch * 4 * 2}  # rings, weights, x in, y out
     elif workload == SAMPLER:
-        # stage 1 reads the logits; stage 2 reads them again and writes exp(x - max)
-        # into the probability buffer; stage 3 reads that and writes the probabilities
+        # the one launch (64 rows) reads the logits and writes the probabilities
+        # once; as three launches stage 1 reads the logits, stage 2 reads them
+        # again and writes exp(x - max) into the probability buffer, stage 3
+        # reads that and writes the probabilities
         lv = 64 * VOCAB * 4
-        ob = {"stage1": lv, "stage2": 2 * lv, "stage3": 2 * lv, "walk": 0}
+        ob = {"stages_one_launch": 2 * lv, "stage1": lv, "stage2": 2 * lv, "stage3": 2 * lv, "walk": 0}
     else:
         ob = dict(op_bytes(WORKLOADS[workload]), layer_ops=layer_ops_bytes(WORKLOADS[workload]))
     commands = pmc_commands(fetch_dir, write_dir, copy_fetch_dir, copy_write_dir, run_args)

@@ -1,0 +1,159 @@
+"""The sampler's one-launch path (stages 1-3 in one kernel with per-row
+barriers), which anelm_sample takes from 48 rows when the rows are 16-byte
+aligned and the grid fits on the GPU at once: token ids bit-exact against the
+oracle (core/sampling.cpp:10-66) and probabilities bit-identical, on the edge
+cases the three-launch path is tested on, on workspaces that start with
+arbitrary contents and are reused across shapes, and bit-identical to the
+three-launch path itself (taken for the same rows when the probability rows
+are not 16-byte aligned)."""
+import numpy as np
+import pytest
+
+from helpers import assert_bitexact, dev, host
+from test_gpu_sampling import V, drand48_stream, oracle_rows
+
+pytestmark = pytest.mark.gpu
+
+PARAMS = dict(temperature=0.6, repetition_penalty=1.2, repetition_context_size=256, frequency_penalty=0.1)
+
+
+def _rows4(a):
+    """[rows, vocab] float32 on the device in rows of a multiple of 4 floats
+    (16-byte aligned rows, whatever the vocabulary)."""
+    import torch
+
+    rows, vocab = a.shape
+    buf = torch.zeros(rows, (vocab + 3) // 4 * 4, device="cuda")
+    buf[:, :vocab] = dev(np.ascontiguousarray(a))
+    return buf[:, :vocab]
+
+
+def _call(hip, logits, ws, hist=None, hist_len=None, r=None, ld_pad=0, **params):
+    """anelm_sample with the given workspace on 16-byte aligned logits rows;
+    probability rows aligned too, or with ld_pad = 1 one float longer
+    (unaligned: the three launches)."""
+    import torch
+
+    rows, vocab = logits.shape
+    p = hip.SamplingParams(**params)
+    ids = torch.full((rows,), -7, dtype=torch.int32, device="cuda")
+    pbuf = torch.full((rows, (vocab + 3) // 4 * 4 + ld_pad), float("nan"), device="cuda")
+    probs = pbuf[:, :vocab]
+    hip.sample(ids, probs, _rows4(logits), dev(hist) if hist is not None else None,
+               dev(hist_len) if hist_len is not None else None, p, dev(r), ws)
+    return host(ids), host(probs)
+
+
+def _epoch(ws):
+    """The workspace's first 8 bytes: one-launch calls made on it."""
+    return int(host(ws[:8]).view(np.uint64)[0])
+
+
+def _check(ids, probs, rids, rprobs, what):
+    assert np.array_equal(ids, rids), what
+    gn, rn = np.isnan(probs), np.isnan(rprobs)
+    assert np.array_equal(gn, rn), what
+    assert_bitexact(np.where(gn, 0.0, probs).astype(np.float32), np.where(rn, 0.0, rprobs).astype(np.float32), what)
+
+
+def test_fused_path_taken_from_48_rows(hip, orc, rng):
+    """The epoch in the workspace's first word counts one-launch calls: it
+    advances once per call at 64 and 48 rows and stays put at 47 rows (three
+    launches), and the ids and probabilities match the oracle each time."""
+    import torch
+
+    ws = torch.zeros(hip.sample_workspace_size(64, V), dtype=torch.uint8, device="cuda")
+    expect = 0
+    for rows, fused in ((64, True), (48, True), (47, False), (64, True)):
+        logits = rng.normal(0, 3, (rows, V)).astype(np.float32)
+        hist = rng.integers(0, V, (rows, 256)).astype(np.int32)
+        r = rng.uniform(0, 1, rows).astype(np.float32)
+        ids, probs = _call(hip, logits, ws, hist, r=r, **PARAMS)
+        expect += 1 if fused else 0
+        assert _epoch(ws) == expect, (rows, _epoch(ws))
+        rids, rprobs = oracle_rows(orc, logits, hist, r=r, **PARAMS)
+        _check(ids, probs, rids, rprobs, f"{rows} rows")
+
+
+def test_fused_equals_three_launches(hip, rng):
+    """The same 48 rows through both paths (unaligned probability rows take
+    the three launches): ids and probabilities bit-identical."""
+    import torch
+
+    rows = 48
+    logits = rng.normal(0, 3, (rows, V)).astype(np.float32)
+    hist = rng.integers(0, V, (rows, 256)).astype(np.int32)
+    r = drand48_stream(7, rows)
+    ws = torch.empty(hip.sample_workspace_size(rows, V), dtype=torch.uint8, device="cuda")
+    ws.fill_(0xFF)
+    a_ids, a_probs = _call(hip, logits, ws, hist, r=r, **PARAMS)
+    assert _epoch(ws) == 0          # 0xFF..FF + 1 wraps: one one-launch call made
+    b_ids, b_probs = _call(hip, logits, ws, hist, r=r, ld_pad=1, **PARAMS)
+    assert _epoch(ws) == 0          # the three launches leave it
+    assert np.array_equal(a_ids, b_ids)
+    assert_bitexact(a_probs, b_probs, "one launch against three")
+
+
+def test_fused_nan_inf_and_history_lengths(hip, orc, rng):
+    """48 rows of 151936: NaN, +inf and -inf logits (one in the last, partial
+    chunk), device history lengths from 0 to the whole history, out-of-range
+    and repeated ids, against the oracle."""
+    rows = 48
+    logits = rng.normal(0, 3, (rows, V)).astype(np.float32)
+    logits[0, 5] = np.nan
+    logits[1, V - 1] = np.nan
+    logits[2, 1000] = np.inf
+    logits[3, ::7] = -np.inf
+    logits[4, 77777] = np.nan
+    logits[5, 12287:12290] = np.inf       # across a chunk boundary
+    hist = rng.integers(-5, V + 5, (rows, 300)).astype(np.int32)
+    hist[6:9, :150] = hist[6:9, :1]       # heavy duplicates
+    hl = rng.integers(0, 301, rows).astype(np.int32)
+    hl[:4] = [0, 1, 256, 300]
+    r = drand48_stream(99, rows)
+    for ctx in (256, 7):
+        params = dict(PARAMS, repetition_context_size=ctx, frequency_penalty=0.25)
+        ids, probs = _call(hip, logits, _ws(hip, rows, V), hist, hl, r, **params)
+        rids, rprobs = oracle_rows(orc, logits, hist, hl, r, **params)
+        _check(ids, probs, rids, rprobs, f"ctx {ctx}")
+        assert ids[0] == V - 1
+
+
+def _ws(hip, rows, vocab):
+    import torch
+
+    return torch.empty(hip.sample_workspace_size(rows, vocab), dtype=torch.uint8, device="cuda")
+
+
+@pytest.mark.parametrize("vocab", [12289, 4099, 24576, 8])
+def test_fused_vocab_shapes(hip, orc, rng, vocab):
+    """Vocabularies of one chunk and a single element (12289), not a multiple
+    of 4 (4099), exactly two chunks (24576) and tiny (8), at 48 rows."""
+    rows = 48
+    logits = (rng.normal(0, 3, (rows, vocab)) / 0.6).astype(np.float32)
+    hist = rng.integers(0, vocab, (rows, 64)).astype(np.int32)
+    r = rng.uniform(0, 1, rows).astype(np.float32)
+    r[0] = 0.0
+    r[1] = np.float32(1.0 - 2.0 ** -24)
+    ids, probs = _call(hip, logits, _ws(hip, rows, vocab), hist, r=r, **PARAMS)
+    rids, rprobs = oracle_rows(orc, logits, hist, r=r, **PARAMS)
+    _check(ids, probs, rids, rprobs, f"vocab {vocab}")
+
+
+def test_fused_workspace_reused_across_shapes(hip, orc, rng):
+    """One workspace that starts as random bytes serves calls of 64, 48 and
+    56 rows over three vocabularies, then 64 rows again: every call matches
+    the oracle (flags left by a call of another shape never pass a barrier)."""
+    import torch
+
+    cap = max(hip.sample_workspace_size(64, V), hip.sample_workspace_size(56, 50000))
+    ws = torch.from_numpy(rng.integers(0, 256, cap, dtype=np.uint8)).cuda()
+    e0 = _epoch(ws)
+    for k, (rows, vocab) in enumerate(((64, V), (48, 50000), (56, 9000), (64, V))):
+        logits = rng.normal(0, 3, (rows, vocab)).astype(np.float32)
+        hist = rng.integers(0, vocab, (rows, 256)).astype(np.int32)
+        r = rng.uniform(0, 1, rows).astype(np.float32)
+        ids, probs = _call(hip, logits, ws, hist, r=r, **PARAMS)
+        rids, rprobs = oracle_rows(orc, logits, hist, r=r, **PARAMS)
+        _check(ids, probs, rids, rprobs, f"call {k}: {rows} x {vocab}")
+        assert _epoch(ws) == (e0 + k + 1) % (1 << 64)
