@@ -19,6 +19,10 @@ constexpr int kU_cvt = 1;   // bf16 -> fp16 (packed 16-bit arithmetic, see cvt_p
 
 // ------------------------------------------------------------ residual add
 // qwen3.cpp:516/:527: x = x + y, one IEEE add per element (bit-exact).
+// x, y and the store all non-temporal: at 8192 rows of 4096 alone, 62.7 us
+// against 65.0 with x read through the caches and 70.6 with everything
+// cached; in the layer chain, where x was just written by the add + RMSNorm
+// through the caches, it measured no slower (418.3 against 420.8 us per layer).
 template <int kU>
 __global__ __launch_bounds__(256) void residual_add_vec_kernel(float4* x, const float4* y, size_t n4) {
     const size_t base = (size_t)blockIdx.x * (256 * kU) + threadIdx.x;
@@ -27,7 +31,7 @@ __global__ __launch_bounds__(256) void residual_add_vec_kernel(float4* x, const 
     for (int i = 0; i < kU; i++) {
         const size_t idx = base + (size_t)i * 256;
         if (idx < n4) {
-            a[i] = x[idx];
+            a[i] = ld_nt(x + idx);
             b[i] = ld_nt(y + idx);
         }
     }
