@@ -71,10 +71,14 @@ def test_graph_replays_match_eager(hip):
                 f"replay {rep}: {name} differs from eager"
 
 
-def test_sampler_graph_replays_match_eager(hip, rng):
+@pytest.mark.parametrize("rows,V", [(8, 20000), (64, 151936)])
+def test_sampler_graph_replays_match_eager(hip, rng, rows, V):
+    """At 64 rows the sampler is one launch for stages 1-3 whose row
+    barriers take their token from the workspace's epoch, which the walk
+    advances on the device: every replay of the captured call (new logits
+    and draws each time) matches the eager call, and advances the epoch."""
     import torch
 
-    rows, V = 8, 20000
     logits = dev(rng.normal(0, 3, (rows, V)).astype(np.float32))
     hist = dev(rng.integers(0, V, (rows, 256)).astype(np.int32))
     r = dev(rng.uniform(0, 1, rows).astype(np.float32))
@@ -87,13 +91,19 @@ def test_sampler_graph_replays_match_eager(hip, rng):
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
         hip.sample(ids_g, pr_g, logits, hist, None, p, r, ws_g)
+    epoch = lambda ws: int(host(ws[:8]).view(np.uint64)[0])
+    e0 = epoch(ws_g)
     for rep in range(3):
         r.copy_(torch.rand(rows, device="cuda"))      # new draws each step, read by both
+        logits.normal_(0.0, 3.0)                      # and new logits
         hip.sample(ids_e, pr_e, logits, hist, None, p, r, ws_e)
         g.replay()
         torch.cuda.synchronize()
         assert np.array_equal(host(ids_e), host(ids_g)), f"replay {rep}: ids"
         assert np.array_equal(host(pr_e).view(np.uint32), host(pr_g).view(np.uint32)), f"replay {rep}: probs"
+        if rows >= 48:
+            assert epoch(ws_g) == (e0 + rep + 1) % (1 << 64), f"replay {rep}: epoch"
+            assert host(ids_g).min() >= 0
 
 
 @pytest.mark.parametrize("B,steps,V", [(1, 140, 300), (3, 30, 300), (20, 24, 300), (20, 8, 70000), (9, 8, 300)])
