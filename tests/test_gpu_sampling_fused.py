@@ -157,3 +157,28 @@ def test_fused_workspace_reused_across_shapes(hip, orc, rng):
         rids, rprobs = oracle_rows(orc, logits, hist, r=r, **PARAMS)
         _check(ids, probs, rids, rprobs, f"call {k}: {rows} x {vocab}")
         assert _epoch(ws) == (e0 + k + 1) % (1 << 64)
+
+
+def test_long_window_takes_three_launches(hip, orc, rng):
+    """A window of more than 65535 ids (its counts would not fit 16 bits)
+    makes anelm_sample take the three launches at 48 rows: the epoch stays
+    put and the results match the oracle."""
+    import torch
+
+    rows, vocab, n = 48, 6000, 70000
+    logits = rng.normal(0, 3, (rows, vocab)).astype(np.float32)
+    hist = rng.integers(0, vocab, (rows, n)).astype(np.int32)
+    hist[:, : n // 2] = hist[:, :1]            # one id counted 35000 times and more
+    r = rng.uniform(0, 1, rows).astype(np.float32)
+    params = dict(PARAMS, repetition_context_size=n)
+    ws = torch.zeros(hip.sample_workspace_size(rows, vocab), dtype=torch.uint8, device="cuda")
+    ids, probs = _call(hip, logits, ws, hist, r=r, **params)
+    assert _epoch(ws) == 0
+    rids, rprobs = oracle_rows(orc, logits, hist, r=r, **params)
+    _check(ids, probs, rids, rprobs, "window of 70000")
+    # the same rows with a window of 65535 take the one launch
+    params = dict(PARAMS, repetition_context_size=65535)
+    ids, probs = _call(hip, logits, ws, hist, r=r, **params)
+    assert _epoch(ws) == 1
+    rids, rprobs = oracle_rows(orc, logits, hist, r=r, **params)
+    _check(ids, probs, rids, rprobs, "window of 65535")
