@@ -182,3 +182,39 @@ def test_long_window_takes_three_launches(hip, orc, rng):
     assert _epoch(ws) == 1
     rids, rprobs = oracle_rows(orc, logits, hist, r=r, **params)
     _check(ids, probs, rids, rprobs, "window of 65535")
+
+
+def test_concurrent_calls_on_four_streams(hip, rng):
+    """Four 64-row one-launch calls issued at once on four streams (together
+    four times the workgroups the GPU holds at once, so their grids cannot be
+    resident together): every call still returns what it returns alone,
+    bit for bit, and no row comes back -1 (a row barrier that gave up)."""
+    import torch
+
+    rows, V, n = 64, 151936, 4
+    p = hip.SamplingParams()
+    logits = [dev(rng.normal(0, 3, (rows, V)).astype(np.float32)) for _ in range(n)]
+    hist = [dev(rng.integers(0, V, (rows, 256)).astype(np.int32)) for _ in range(n)]
+    r = [dev(rng.uniform(0, 1, rows).astype(np.float32)) for _ in range(n)]
+    ws = [torch.empty(hip.sample_workspace_size(rows, V), dtype=torch.uint8, device="cuda") for _ in range(n)]
+    ids = [torch.full((rows,), -7, dtype=torch.int32, device="cuda") for _ in range(n)]
+    probs = [torch.empty(rows, V, device="cuda") for _ in range(n)]
+    ref = []
+    for i in range(n):   # each alone
+        hip.sample(ids[i], probs[i], logits[i], hist[i], None, p, r[i], ws[i])
+        torch.cuda.synchronize()
+        ref.append((host(ids[i]), host(probs[i])))
+    streams = [torch.cuda.Stream() for _ in range(n)]
+    for rep in range(3):
+        for i in range(n):
+            ids[i].fill_(-7)
+        torch.cuda.synchronize()
+        for i in range(n):   # all at once
+            with torch.cuda.stream(streams[i]):
+                hip.sample(ids[i], probs[i], logits[i], hist[i], None, p, r[i], ws[i])
+        torch.cuda.synchronize()
+        for i in range(n):
+            got = host(ids[i])
+            assert got.min() >= 0, f"rep {rep}, call {i}: a row barrier gave up"
+            assert np.array_equal(got, ref[i][0]), f"rep {rep}, call {i}: ids"
+            assert np.array_equal(host(probs[i]).view(np.uint32), ref[i][1].view(np.uint32)), f"rep {rep}, call {i}"
