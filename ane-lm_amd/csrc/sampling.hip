@@ -686,7 +686,8 @@ __device__ __forceinline__ void exp_and_sum(const float (&v)[4 * K], float neg, 
 // The same exponentials kept in v (0 past the end of the row) instead of
 // stored, and this lane's sum of them.  The exp is computed for every slot
 // and the padding selected away (no branch per element).
-template <int K, bool F64>
+// FULL: every slot is in the row (nvalid == K * kSlice), no selects.
+template <int K, bool F64, bool FULL>
 __device__ __forceinline__ void exp_and_sum_keep(float (&v)[4 * K], float neg, const SampleArgs& a, int nvalid,
                                                  uint64_t& acc, int& nan) {
     const float scale = ldexpf(1.0f, a.shift);
@@ -698,7 +699,7 @@ __device__ __forceinline__ void exp_and_sum_keep(float (&v)[4 * K], float neg, c
         for (int e = 0; e < 4; e++) {
             const int li = k * kSlice + 4 * threadIdx.x + e;
             const float ev = sampler_expf(v[4 * k + e] + neg);
-            v[4 * k + e] = li < nvalid ? ev : 0.0f;
+            v[4 * k + e] = FULL || li < nvalid ? ev : 0.0f;
             sum.add(v[4 * k + e], scale, scaled);
         }
     }
@@ -1067,6 +1068,10 @@ __device__ bool row_wait(const uint64_t* flags, int n, uint64_t tok, int* s_ok) 
     return *s_ok != 0;
 }
 
+// At most 128 VGPRs (4 waves per SIMD), so that 4 workgroups fit on a CU and
+// 64 rows of 151936 logits (832 workgroups) on the GPU at once; the cap also
+// measured 1 us faster per call there than the 121 VGPRs left to the
+// compiler (16 bytes of spill per lane).
 // Grid (nchunk, rows), chunks of K slices.  A row's workgroups are
 // consecutive in dispatch order (blockIdx.x its chunk, blockIdx.y the row),
 // so the launch makes progress however few of its workgroups are resident:
@@ -1079,7 +1084,7 @@ __device__ bool row_wait(const uint64_t* flags, int n, uint64_t tok, int* s_ok) 
 // stage 3, measured 64.3 against 65.1 us at 64 rows, but with fewer
 // workgroups resident than the grid no row would have all of its.)
 template <int K>
-__global__ __launch_bounds__(256) void sample_fused_kernel(SampleArgs a, int vec, int vec_out) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void sample_fused_kernel(SampleArgs a, int vec, int vec_out) {
     constexpr int kCH = K * kSlice;
     __shared__ __align__(16) uint32_t cnt[kCH / 2];   // window counts, two per word
     __shared__ float red[4];
@@ -1109,11 +1114,20 @@ __global__ __launch_bounds__(256) void sample_fused_kernel(SampleArgs a, int vec
     bool ok = true;
 
     // stage 1: the chunk maximum of the adjusted logits
+    // A whole chunk, every chunk of a row but its last, takes no selects here
+    // and in the exponentials: 64 rows of 151936, 63.2 -> 60.2 us per call
+    // (the stages are bound by their vector instructions).
     float best = -INFINITY;
+    if (nvalid == kCH) {
 #pragma unroll
-    for (int k = 0; k < K; k++)
+        for (int i = 0; i < 4 * K; i++) best = fmaxf(best, v[i]);
+    } else {
 #pragma unroll
-        for (int e = 0; e < 4; e++) best = k * kSlice + 4 * (int)threadIdx.x + e < nvalid ? fmaxf(best, v[4 * k + e]) : best;
+        for (int k = 0; k < K; k++)
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                best = k * kSlice + 4 * (int)threadIdx.x + e < nvalid ? fmaxf(best, v[4 * k + e]) : best;
+    }
     best = wave_max(best);
     if (lane == 0) red[wid] = best;
     __syncthreads();
@@ -1133,10 +1147,14 @@ __global__ __launch_bounds__(256) void sample_fused_kernel(SampleArgs a, int vec
     static_assert(4 * K <= (1 << kLogTerms), "a lane's terms");
     uint64_t acc;
     int nan;
-    if (a.shift + kLogTerms <= 53)
-        exp_and_sum_keep<K, true>(v, neg, a, nvalid, acc, nan);
-    else
-        exp_and_sum_keep<K, false>(v, neg, a, nvalid, acc, nan);
+    const bool f64 = a.shift + kLogTerms <= 53;   // uniform: the lane's sum fits fp64's 53 bits
+    if (nvalid == kCH) {
+        if (f64) exp_and_sum_keep<K, true, true>(v, neg, a, nvalid, acc, nan);
+        else exp_and_sum_keep<K, false, true>(v, neg, a, nvalid, acc, nan);
+    } else {
+        if (f64) exp_and_sum_keep<K, true, false>(v, neg, a, nvalid, acc, nan);
+        else exp_and_sum_keep<K, false, false>(v, neg, a, nvalid, acc, nan);
+    }
     acc = wave_sum_u64(acc);
     nan = __any(nan) ? 1 : 0;
     if (lane == 0) {
@@ -1694,14 +1712,14 @@ namespace anelm {
 namespace {
 
 // The one-launch path from this many rows.  Per call at 151936 logits (8
-// calls on distinct inputs in a graph), one launch against three: 64 rows
-// 63.8 / 66.5 us, 48 rows 59.4 / 60.6, 32 rows 55.1 / 55.4, 24 rows 53.9 /
-// 52.1, 16 rows 50.5 / 47.0.  Both are bound by the stages' vector
-// instructions (about 100 per logit: penalties, the exact exp, the exact
+// calls on distinct inputs in a graph), one launch against three: 48 rows
+// 56.1 / 60.0 us, 40 rows 55.0 / 58.0, 32 rows 52.2 / 54.9, 24 rows 51.5 /
+// 51.6, 16 rows 50.3 / 47.8.  Both are bound by the stages' vector
+// instructions (about 80 per logit: penalties, the exact exp, the exact
 // fixed-point sum, the sub-tile maps), not by their bytes; one launch saves
 // the re-reads and the launches' ramps, and its row barriers cost more than
 // that saves when the grid is small.
-constexpr long kFusedMinRows = 48;
+constexpr long kFusedMinRows = 32;
 constexpr int kCapDevices = 64;
 
 // Workgroups of the one-launch kernel the current device holds at once
