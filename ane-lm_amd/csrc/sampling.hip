@@ -1712,14 +1712,20 @@ namespace anelm {
 namespace {
 
 // The one-launch path from this many rows.  Per call at 151936 logits (8
-// calls on distinct inputs in a graph), one launch against three: 48 rows
-// 56.1 / 60.0 us, 40 rows 55.0 / 58.0, 32 rows 52.2 / 54.9, 24 rows 51.5 /
-// 51.6, 16 rows 50.3 / 47.8.  Both are bound by the stages' vector
-// instructions (about 80 per logit: penalties, the exact exp, the exact
-// fixed-point sum, the sub-tile maps), not by their bytes; one launch saves
-// the re-reads and the launches' ramps, and its row barriers cost more than
-// that saves when the grid is small.
-constexpr long kFusedMinRows = 32;
+// calls on distinct inputs in a graph), one launch against three: 32 rows
+// 50.1 / 54.7 us, 24 rows 51.0 / 52.4, 16 rows 47.4 / 46.8, 12 rows 45.4 /
+// 43.4, 8 rows 43.9 / 39.9.  Both are bound by their vector instructions and
+// dependent chains, not by their bytes; one launch saves the re-reads and the
+// launches' ramps, and its row barriers cost more than that saves when the
+// grid is small.
+constexpr long kFusedMinRows = 24;
+// Sub-tiles that chunk 0 of each row walks one add at a time in the one
+// launch.  There every workgroup finishes at about the same time, so this
+// walk (about 8 cycles an add) lengthens the launch, where stage 3 of the
+// three launches hid it; what it leaves to the walk costs there instead.
+// Per call at 64 rows (one launch + walk, under the profiler): 0 sub-tiles
+// 43.0 + 20.5 us, 1: 42.9 + 15.5, 2: 43.1 + 14.4, 4: 45.7 + 14.0.
+constexpr int kFusedFirstSubs = 2;
 constexpr int kCapDevices = 64;
 
 // Workgroups of the one-launch kernel the current device holds at once
@@ -1808,6 +1814,7 @@ int sample_impl(int32_t* ids, float* probs, long ld_probs, const float* logits, 
         a.ws_rowtok = reinterpret_cast<uint64_t*>(b + l.off_rowtok);
         a.ws_tok = reinterpret_cast<uint64_t*>(b + l.off_tok);
         a.nchunk = (int)((vocab + kFusedK * kSlice - 1) / (kFusedK * kSlice));
+        a.first_subs = kFusedFirstSubs;
         sample_fused_kernel<kFusedK><<<dim3((unsigned)a.nchunk, (unsigned)rows), 256, 0, st>>>(a, vec, vec_out);
     } else if (one) {
         sample_stage1_kernel<false, 1><<<grd, 256, 0, st>>>(a, vec);

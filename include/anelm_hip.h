@@ -256,7 +256,7 @@ typedef struct anelm_sampling_params {
  *    (sampling.cpp:59-65).
  * r[b] is the uniform draw (the reference's (float)drand48()).
  * Needs anelm_sample_workspace_size(rows, vocab) bytes of device workspace,
- * with any contents (nothing needs clearing).  From 32 sampling rows, with
+ * with any contents (nothing needs clearing).  From 24 sampling rows, with
  * 16-byte aligned logits and probability rows, stages 1-3 run as one launch
  * whose row barriers need the whole grid resident on the GPU at once (the
  * library checks that it fits); a barrier that still waits 0.2 s gives up

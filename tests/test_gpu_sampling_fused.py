@@ -1,5 +1,5 @@
 """The sampler's one-launch path (stages 1-3 in one kernel with per-row
-barriers), which anelm_sample takes from 32 rows when the rows are 16-byte
+barriers), which anelm_sample takes from 24 rows when the rows are 16-byte
 aligned and the grid fits on the GPU at once: token ids bit-exact against the
 oracle (core/sampling.cpp:10-66) and probabilities bit-identical, on the edge
 cases the three-launch path is tested on, on workspaces that start with
@@ -56,15 +56,15 @@ def _check(ids, probs, rids, rprobs, what):
     assert_bitexact(np.where(gn, 0.0, probs).astype(np.float32), np.where(rn, 0.0, rprobs).astype(np.float32), what)
 
 
-def test_fused_path_taken_from_32_rows(hip, orc, rng):
+def test_fused_path_taken_from_24_rows(hip, orc, rng):
     """The epoch in the workspace's first word counts one-launch calls: it
-    advances once per call at 64 and 32 rows and stays put at 31 rows (three
+    advances once per call at 64 and 24 rows and stays put at 23 rows (three
     launches), and the ids and probabilities match the oracle each time."""
     import torch
 
     ws = torch.zeros(hip.sample_workspace_size(64, V), dtype=torch.uint8, device="cuda")
     expect = 0
-    for rows, fused in ((64, True), (32, True), (31, False), (64, True)):
+    for rows, fused in ((64, True), (24, True), (23, False), (64, True)):
         logits = rng.normal(0, 3, (rows, V)).astype(np.float32)
         hist = rng.integers(0, V, (rows, 256)).astype(np.int32)
         r = rng.uniform(0, 1, rows).astype(np.float32)
