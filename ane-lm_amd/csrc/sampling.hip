@@ -122,37 +122,36 @@ struct HistFirst {
     bool valid;      // threadIdx.x < n: raw is this thread's first entry
 };
 
-// One unconditional load at a clamped index; nothing uses its value before
-// the chunk's loads are issued (a use would wait for it there).
+// One unconditional load at a clamped index, with no branch (a load inside a
+// branch made the compiler wait for it where the branch ends, before the
+// chunk's loads went out); nothing uses its value before the chunk's loads
+// are issued.  Without such a window the load reads the first logit and the
+// value is never used.
 __device__ __forceinline__ HistFirst hist_first(const SampleArgs& a, long row) {
-    HistFirst f = {0, 0, -1, false};
-    if (a.use_penalty && !a.hist_len && a.hist_ld > 0) {
-        f.hl = a.hist_ld;
-        f.start = f.hl - a.ctx < 0 ? 0 : f.hl - a.ctx;
-        const long n = f.hl - f.start;  // >= 1
-        f.valid = (long)threadIdx.x < n;
-        f.raw = a.hist[row * a.hist_ld + f.start + (f.valid ? (long)threadIdx.x : n - 1)];
-    }
+    const bool on = a.use_penalty && !a.hist_len && a.hist_ld > 0;   // uniform
+    HistFirst f;
+    f.hl = on ? a.hist_ld : 0;
+    f.start = on && f.hl - a.ctx > 0 ? f.hl - a.ctx : 0;
+    const long n = f.hl - f.start;  // >= 1 when on
+    f.valid = on && (long)threadIdx.x < n;
+    const int32_t* p = on ? a.hist + row * a.hist_ld + f.start + (f.valid ? (long)threadIdx.x : n - 1)
+                          : reinterpret_cast<const int32_t*>(a.logits);
+    f.raw = *p;
     return f;
 }
+
+__device__ __forceinline__ int first_id(const HistFirst& f) { return f.valid ? f.raw : -1; }
 
 // cnt[i - c0] = occurrences of id i in the window for i in [c0, c0 + n)
 // (n a multiple of 8), ids outside [0, vocab) ignored (sampling.cpp:23).
 // PK: two 16-bit counts per word (id i - c0 in half (i - c0) & 1 of word
 // (i - c0) / 2), half the LDS; for windows of at most 65535 ids, so that no
 // count carries into its neighbour.
+// id0: the window's first entry for this thread (first_id, -1 for none).
 template <bool PK = false>
-__device__ __forceinline__ void build_counts(uint32_t* cnt, int n, const SampleArgs& a, long row, long c0, HistFirst f) {
+__device__ __forceinline__ void build_counts(uint32_t* cnt, int n, const SampleArgs& a, long row, long c0, HistFirst f,
+                                             int id0) {
     const int32_t* h = a.hist + row * a.hist_ld;
-    int id0 = f.valid ? f.raw : -1;
-    if (a.use_penalty && a.hist_len) {
-        long hl = (long)a.hist_len[row];
-        if (hl > a.hist_ld) hl = a.hist_ld;
-        f.hl = hl;
-        f.start = hl - a.ctx < 0 ? 0 : hl - a.ctx;
-        const long j = f.start + threadIdx.x;
-        if (j < hl) id0 = h[j];
-    }
     const int words = PK ? n / 2 : n;
     for (int i = 4 * threadIdx.x; i < words; i += 4 * blockDim.x) *reinterpret_cast<uint4*>(cnt + i) = make_uint4(0u, 0u, 0u, 0u);
     __syncthreads();
@@ -163,7 +162,15 @@ __device__ __forceinline__ void build_counts(uint32_t* cnt, int n, const SampleA
             else atomicAdd(&cnt[o], 1u);
         }
     };
-    if (a.use_penalty) {
+    // The two windows in separate branches: a value that one of them loads
+    // late (the device length, then the entries) is never the other's, so the
+    // first entry's count waits only for its own early load.
+    if (a.use_penalty && a.hist_len) {
+        long hl = (long)a.hist_len[row];
+        if (hl > a.hist_ld) hl = a.hist_ld;
+        const long start = hl - a.ctx < 0 ? 0 : hl - a.ctx;
+        for (long j = start + threadIdx.x; j < hl; j += blockDim.x) count(h[j]);
+    } else if (a.use_penalty) {
         count(id0);
         for (long j = f.start + threadIdx.x + blockDim.x; j < f.hl; j += blockDim.x) count(h[j]);
     }
@@ -222,16 +229,40 @@ __device__ __forceinline__ void adjust_k(float v[4 * K], const uint32_t* cnt, co
 // index and out-of-range values are selected away afterwards (a branch per
 // lane or per chunk made the compiler wait for earlier loads before issuing
 // these).  Other rows take single loads.
-template <int K>
-__device__ __forceinline__ void load_chunk(float v[4 * K], const float* row_ptr, long c0, long vocab, bool vec) {
-    if (vec && vocab >= 4 && (vocab & 3) == 0) {
+// In two parts: load_chunk_issue sends the quad loads, load_chunk_finish
+// makes the values (the selects wait for the loads).  Work placed between the
+// two (the window counts, the row's chunk maxima or sums) runs while the
+// chunk is in flight; the element path is complete after the first part.
+// Q (the quad path) is a template parameter, not a run-time branch: with both
+// paths in one kernel the compiler joined them before the quad loads and
+// waited there for every load issued earlier.
+__host__ __device__ inline bool chunk_quads(long vocab, bool vec) { return vec && vocab >= 4 && (vocab & 3) == 0; }
+
+template <int K, bool Q>
+__device__ __forceinline__ void load_chunk_issue(float4 (&f)[K], float (&v)[4 * K], const float* row_ptr, long c0, long vocab) {
+    if constexpr (Q) {
         const long lastq = vocab - 4;  // the last quad
-        float4 f[K];
 #pragma unroll
         for (int k = 0; k < K; k++) {
             const long i = c0 + k * kSlice + 4 * threadIdx.x;
             f[k] = ld_nt(reinterpret_cast<const float4*>(row_ptr + (i < lastq ? i : lastq)));
         }
+    } else {
+#pragma unroll
+        for (int k = 0; k < K; k++) {
+            const long i = c0 + k * kSlice + 4 * threadIdx.x;
+#pragma unroll
+            for (int e = 0; e < 4; e++) v[4 * k + e] = (i + e < vocab) ? row_ptr[i + e] : 0.0f;
+        }
+        // complete here: where a run-time branch picks this path or the
+        // quad loads, nothing of it is left pending where the paths join
+        __builtin_amdgcn_s_waitcnt(0);
+    }
+}
+
+template <int K, bool Q>
+__device__ __forceinline__ void load_chunk_finish(float (&v)[4 * K], const float4 (&f)[K], long c0, long vocab) {
+    if constexpr (Q) {
 #pragma unroll
         for (int k = 0; k < K; k++) {
             const long i = c0 + k * kSlice + 4 * threadIdx.x;
@@ -241,13 +272,6 @@ __device__ __forceinline__ void load_chunk(float v[4 * K], const float* row_ptr,
             v[4 * k + 2] = in ? f[k].z : 0.0f;
             v[4 * k + 3] = in ? f[k].w : 0.0f;
         }
-        return;
-    }
-#pragma unroll
-    for (int k = 0; k < K; k++) {
-        const long i = c0 + k * kSlice + 4 * threadIdx.x;
-#pragma unroll
-        for (int e = 0; e < 4; e++) v[4 * k + e] = (i + e < vocab) ? row_ptr[i + e] : 0.0f;
     }
 }
 
@@ -497,8 +521,8 @@ __device__ __forceinline__ Fn compose4_scan(const Fn f[4]) {
 }
 
 // ---- stage 1: penalties, 1/T, chunk max (T > 0) or chunk argmax (T <= 0) ----
-template <bool ARGMAX, int K>
-__global__ __launch_bounds__(256) void sample_stage1_kernel(SampleArgs a, int vec) {
+template <bool ARGMAX, int K, bool Q>
+__global__ __launch_bounds__(256) void sample_stage1_kernel(SampleArgs a) {
     constexpr int kCH = K * kSlice;
     __shared__ __align__(16) uint32_t cnt[kCH];
     __shared__ float red_v[4];
@@ -508,9 +532,11 @@ __global__ __launch_bounds__(256) void sample_stage1_kernel(SampleArgs a, int ve
     const HistFirst hf = hist_first(a, row);
     __builtin_amdgcn_sched_barrier(0);  // its load goes out before the chunk's
     float v[4 * K];
-    load_chunk<K>(v, a.logits + row * a.ld_logits, c0, a.vocab, vec != 0);
+    float4 q[K];
+    load_chunk_issue<K, Q>(q, v, a.logits + row * a.ld_logits, c0, a.vocab);
     __builtin_amdgcn_sched_barrier(0);
-    build_counts(cnt, kCH, a, row, c0, hf);
+    build_counts(cnt, kCH, a, row, c0, hf, first_id(hf));   // while the chunk is in flight
+    load_chunk_finish<K, Q>(v, q, c0, a.vocab);
     adjust_k<K>(v, cnt, a);
     const int nvalid = a.vocab - c0 < kCH ? (int)(a.vocab - c0) : kCH;
     float best = -INFINITY;
@@ -712,8 +738,8 @@ __device__ __forceinline__ void exp_and_sum_keep(float (&v)[4 * K], float neg, c
 // the probability buffer (in place over the logits for softmax: every
 // workgroup reads its own chunk before writing it), where stage 3 scales them
 // into probabilities without recomputing them.
-template <int K>
-__global__ __launch_bounds__(256) void sample_stage2_kernel(SampleArgs a, int vec, int vec_out) {
+template <int K, bool Q>
+__global__ __launch_bounds__(256) void sample_stage2_kernel(SampleArgs a, int vec_out) {
     constexpr int kCH = K * kSlice;
     __shared__ __align__(16) uint32_t cnt[kCH];
     __shared__ float red[4];
@@ -727,10 +753,12 @@ __global__ __launch_bounds__(256) void sample_stage2_kernel(SampleArgs a, int ve
     const HistFirst hf = hist_first(a, row);
     __builtin_amdgcn_sched_barrier(0);
     float v[4 * K];
-    load_chunk<K>(v, a.logits + row * a.ld_logits, c0, a.vocab, vec != 0);
+    float4 q[K];
+    load_chunk_issue<K, Q>(q, v, a.logits + row * a.ld_logits, c0, a.vocab);
     __builtin_amdgcn_sched_barrier(0);
     const float mshare = max_rest(a, row, mraw);
-    build_counts(cnt, kCH, a, row, c0, hf);
+    build_counts(cnt, kCH, a, row, c0, hf, first_id(hf));   // while the chunk is in flight
+    load_chunk_finish<K, Q>(v, q, c0, a.vocab);
     adjust_k<K>(v, cnt, a);
     const int nvalid = a.vocab - c0 < kCH ? (int)(a.vocab - c0) : kCH;
     const float neg = -reduce_max(mshare, red);
@@ -969,7 +997,7 @@ __device__ __forceinline__ void probs_and_maps(const SampleArgs& a, const float 
     }
 }
 
-template <int K>
+template <int K, bool Q>
 __global__ __launch_bounds__(256) void sample_stage3_kernel(SampleArgs a, int vec_out) {
     constexpr int kCH = K * kSlice;
     __shared__ uint64_t red_s[4], red_p[4];
@@ -989,13 +1017,15 @@ __global__ __launch_bounds__(256) void sample_stage3_kernel(SampleArgs a, int ve
     const SumRaw sraw = sum_first(a, row);
     __builtin_amdgcn_sched_barrier(0);
     float v[4 * K];  // exp(adjusted - max), as stage 2 stored them
-    load_chunk<K>(v, a.probs + row * a.ld_probs, c0, a.vocab, vec_out != 0);
+    float4 q[K];
+    load_chunk_issue<K, Q>(q, v, a.probs + row * a.ld_probs, c0, a.vocab);
     __builtin_amdgcn_sched_barrier(0);
     const SumShare share = sum_rest(a, row, chunk, sraw);
     // 1/sum, and the exact prefix of the earlier chunks' sums (the prediction
-    // of the running sum at this chunk's start)
+    // of the running sum at this chunk's start), while the chunk is in flight
     float inv, prefix;
     reduce_sums(share, a, red_s, red_p, red_f, inv, prefix);
+    load_chunk_finish<K, Q>(v, q, c0, a.vocab);
     probs_and_maps<K>(a, v, row, chunk, inv, prefix, rdraw, vec_out, ksum, s_first);
 }
 
@@ -1092,23 +1122,46 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void s
     __shared__ int red_f[4];
     __shared__ float ksum[K][4];
     __shared__ __align__(16) float s_first[kFirstN];
-    __shared__ uint64_t s_tok;
     __shared__ int s_ok[2];
     const long row = blockIdx.y;
     const int chunk = (int)blockIdx.x;
     const long c0 = (long)chunk * kCH;
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-    if (threadIdx.x == 0) s_tok = ld_agent(a.epoch) + 1u;   // read before build_counts' barriers
+    // The call's token: the epoch, which only the walk kernel (a later
+    // launch) changes, so a plain load sees the last call's value; the load
+    // goes out first, and the token is taken into scalar registers once the
+    // chunk has arrived.
+    const uint64_t epoch = *a.epoch;
     const float rdraw = a.r[row];
-    const HistFirst hf = hist_first(a, row);
-    __builtin_amdgcn_sched_barrier(0);
     float v[4 * K];
-    load_chunk<K>(v, a.logits + row * a.ld_logits, c0, a.vocab, vec != 0);
+    float4 q[K];
+    // A run-time choice of the load path, not a template parameter: with only
+    // the quad path compiled in, the register allocation spilled inside the
+    // exponentials (96 bytes per lane against 16).  Each path loads its own
+    // window entry first (the empty asm statements keep the compiler from
+    // hoisting that load out of both): the compiler's view of the branch
+    // includes a path through neither, and an entry loaded before the branch
+    // was the newest load on it, which made the count wait for every quad.
+    const bool quads = chunk_quads(a.vocab, vec != 0);
+    HistFirst hf;
+    if (quads) {
+        asm volatile("; quad path");
+        hf = hist_first(a, row);
+        __builtin_amdgcn_sched_barrier(0);
+        load_chunk_issue<K, true>(q, v, a.logits + row * a.ld_logits, c0, a.vocab);
+    } else {
+        asm volatile("; element path");
+        hf = hist_first(a, row);
+        load_chunk_issue<K, false>(q, v, a.logits + row * a.ld_logits, c0, a.vocab);
+    }
     __builtin_amdgcn_sched_barrier(0);
-    build_counts<true>(cnt, kCH, a, row, c0, hf);
+    const int id0 = first_id(hf);
+    build_counts<true>(cnt, kCH, a, row, c0, hf, id0);   // while the chunk is in flight
+    if (quads) load_chunk_finish<K, true>(v, q, c0, a.vocab);
+    const uint64_t tok = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(epoch >> 32)) << 32 |
+                          (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)epoch)) + 1u;
     adjust_k<K, true>(v, cnt, a);
     const int nvalid = a.vocab - c0 < kCH ? (int)(a.vocab - c0) : kCH;
-    const uint64_t tok = s_tok;
     uint64_t* flags1 = a.ws_tok + row * 2 * a.nchunk;
     uint64_t* flags2 = flags1 + a.nchunk;
     bool ok = true;
@@ -1480,15 +1533,15 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1))) void
     __shared__ WalkShared sh;
     const int lane = threadIdx.x;
     const long row = blockIdx.x;
-    if (a.epoch) {
-        // after a one-launch call: the next call's token is one more, and a
-        // row whose barrier gave up in that launch has no valid draw
-        if (row == 0 && lane == 0) st_agent(a.epoch, ld_agent(a.epoch) + 1u);
-        if (ld_agent(a.ws_rowtok + 2 * row + 1) == ld_agent(a.ws_rowtok + 2 * row)) {
-            if (lane == 0) a.ids[row] = -1;
-            return;
-        }
-    }
+    // After a one-launch call: the next call's token is one more, and a row
+    // whose barrier gave up in that launch has no valid draw.  The tokens were
+    // written by that launch, so plain loads see them; they go out with the
+    // cache fill's loads, unconditionally (after three launches they read a
+    // chunk sum instead), and are compared after it.
+    if (a.epoch && row == 0 && lane == 0)
+        __hip_atomic_fetch_add(a.epoch, (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint64_t* tp = a.epoch ? a.ws_rowtok + 2 * row : a.ws_sum + row * a.nchunk;
+    const uint64_t tok0 = tp[0], tok1 = tp[a.epoch ? 1 : 0];
     const float r = a.r[row];
     const long V = a.vocab;
     const float* prow = a.probs + row * a.ld_probs;
@@ -1498,6 +1551,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1))) void
     const int nxcache = a.nsub < kXCache ? a.nsub : kXCache;
     fill_walk_cache(sh, a, row, ncache, nxcache);
     __syncthreads();
+    if (a.epoch && tok0 == tok1) {
+        if (lane == 0) a.ids[row] = -1;
+        return;
+    }
     // "cum < r" on bit patterns: cum >= 0, so cum < r <=> bits(cum) < bits(r)
     // for r > 0; for r <= 0 or NaN no sub-tile is passed without a walk
     const uint32_t rb = r > 0.0f ? __float_as_uint(r) : 0u;
@@ -1676,6 +1733,25 @@ extern "C" size_t anelm_sample_workspace_size(long rows, long vocab) {
     return ws_layout(rows, vocab).total;
 }
 
+namespace anelm {
+namespace {
+// Stages 1-3 (the quad paths chosen per input: logits for stages 1 and 2,
+// the stored exponentials for stage 3).
+template <int K>
+void launch_stages(const SampleArgs& a, dim3 grd, bool q_in, bool q_out, int vec_out, hipStream_t st) {
+    if (q_in) {
+        sample_stage1_kernel<false, K, true><<<grd, 256, 0, st>>>(a);
+        sample_stage2_kernel<K, true><<<grd, 256, 0, st>>>(a, vec_out);
+    } else {
+        sample_stage1_kernel<false, K, false><<<grd, 256, 0, st>>>(a);
+        sample_stage2_kernel<K, false><<<grd, 256, 0, st>>>(a, vec_out);
+    }
+    if (q_out) sample_stage3_kernel<K, true><<<grd, 256, 0, st>>>(a, vec_out);
+    else sample_stage3_kernel<K, false><<<grd, 256, 0, st>>>(a, vec_out);
+}
+}  // namespace
+}  // namespace anelm
+
 extern "C" int anelm_softmax(float* x, long rows, long n, long ld, void* workspace, size_t workspace_bytes,
                              void* stream) {
     if (!x) return fail(ANELM_ERR_INVALID, "anelm_softmax: null pointer");
@@ -1695,16 +1771,10 @@ extern "C" int anelm_softmax(float* x, long rows, long n, long ld, void* workspa
     clear_error();
     hipStream_t st = as_stream(stream);
     const int vec = (ld % 4 == 0) && aligned16(x);
+    const bool q = chunk_quads(n, vec != 0);
     const dim3 grd((unsigned)a.nchunk, (unsigned)rows);
-    if (chunk_slices(rows, n) == 1) {
-        sample_stage1_kernel<false, 1><<<grd, 256, 0, st>>>(a, vec);
-        sample_stage2_kernel<1><<<grd, 256, 0, st>>>(a, vec, vec);
-        sample_stage3_kernel<1><<<grd, 256, 0, st>>>(a, vec);
-    } else {
-        sample_stage1_kernel<false, kSlicesMany><<<grd, 256, 0, st>>>(a, vec);
-        sample_stage2_kernel<kSlicesMany><<<grd, 256, 0, st>>>(a, vec, vec);
-        sample_stage3_kernel<kSlicesMany><<<grd, 256, 0, st>>>(a, vec);
-    }
+    if (chunk_slices(rows, n) == 1) launch_stages<1>(a, grd, q, q, vec, st);
+    else launch_stages<kSlicesMany>(a, grd, q, q, vec, st);
     return launch_status("softmax");
 }
 
@@ -1751,11 +1821,12 @@ long fused_capacity() {
 }
 
 // Whether a sampling call takes the one-launch path: many rows, aligned rows
-// (16-byte loads and stores throughout), a window short enough for 16-bit
+// of a length that is a multiple of 4 (16-byte loads and stores throughout),
+// a window short enough for 16-bit
 // counts, and a grid that fits on the GPU at once with a tenth to spare (for
 // speed: the launch completes without that too, row after row).
 bool use_fused(long rows, long vocab, long hist_ld, int ctx, bool penalty, int vec, int vec_out) {
-    if (rows < kFusedMinRows || !vec || !vec_out) return false;
+    if (rows < kFusedMinRows || !chunk_quads(vocab, vec) || !chunk_quads(vocab, vec_out)) return false;
     if (penalty && (ctx < hist_ld ? (long)ctx : hist_ld) > 65535) return false;
     const long nchf = (vocab + kFusedK * kSlice - 1) / (kFusedK * kSlice);
     return rows * nchf * 10 <= fused_capacity() * 9;
@@ -1799,9 +1870,15 @@ int sample_impl(int32_t* ids, float* probs, long ld_probs, const float* logits, 
     const int vec = (ld_logits % 4 == 0) && aligned16(logits);
     const dim3 grd((unsigned)a.nchunk, (unsigned)rows);
     const bool one = chunk_slices(rows, vocab) == 1;
+    const bool q_in = chunk_quads(vocab, vec != 0);
     if (!sampling) {
-        if (one) sample_stage1_kernel<true, 1><<<grd, 256, 0, st>>>(a, vec);
-        else sample_stage1_kernel<true, kSlicesMany><<<grd, 256, 0, st>>>(a, vec);
+        if (one) {
+            if (q_in) sample_stage1_kernel<true, 1, true><<<grd, 256, 0, st>>>(a);
+            else sample_stage1_kernel<true, 1, false><<<grd, 256, 0, st>>>(a);
+        } else {
+            if (q_in) sample_stage1_kernel<true, kSlicesMany, true><<<grd, 256, 0, st>>>(a);
+            else sample_stage1_kernel<true, kSlicesMany, false><<<grd, 256, 0, st>>>(a);
+        }
         sample_argmax_final_kernel<<<dim3((unsigned)rows), 64, 0, st>>>(a);
         return launch_status("sample(argmax)");
     }
@@ -1816,14 +1893,10 @@ int sample_impl(int32_t* ids, float* probs, long ld_probs, const float* logits, 
         a.nchunk = (int)((vocab + kFusedK * kSlice - 1) / (kFusedK * kSlice));
         a.first_subs = kFusedFirstSubs;
         sample_fused_kernel<kFusedK><<<dim3((unsigned)a.nchunk, (unsigned)rows), 256, 0, st>>>(a, vec, vec_out);
-    } else if (one) {
-        sample_stage1_kernel<false, 1><<<grd, 256, 0, st>>>(a, vec);
-        sample_stage2_kernel<1><<<grd, 256, 0, st>>>(a, vec, vec_out);
-        sample_stage3_kernel<1><<<grd, 256, 0, st>>>(a, vec_out);
     } else {
-        sample_stage1_kernel<false, kSlicesMany><<<grd, 256, 0, st>>>(a, vec);
-        sample_stage2_kernel<kSlicesMany><<<grd, 256, 0, st>>>(a, vec, vec_out);
-        sample_stage3_kernel<kSlicesMany><<<grd, 256, 0, st>>>(a, vec_out);
+        const bool q_out = chunk_quads(vocab, vec_out != 0);
+        if (one) launch_stages<1>(a, grd, q_in, q_out, vec_out, st);
+        else launch_stages<kSlicesMany>(a, grd, q_in, q_out, vec_out, st);
     }
     sample_walk_kernel<<<dim3((unsigned)rows), 64, 0, st>>>(a);
     return launch_status("sample");

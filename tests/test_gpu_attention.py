@@ -172,8 +172,8 @@ def test_batched_other_shapes(hip, orc, rng, B, nq, nk, D, cap):
 @pytest.mark.parametrize("B,cap,bound", [(1, 2048, 30), (1, 2048, 700), (64, 2048, 33), (3, 4096, 4096)])
 def test_bounded_launch(hip, orc, rng, B, cap, bound):
     """Every ring no longer than the bound: the bounded launch (fewer chunks;
-    no merge kernel when one chunk suffices) matches the oracle like the full
-    one does."""
+    no partials to merge when one chunk suffices) matches the oracle like the
+    full one does."""
     import torch
 
     nq, nk, D = 16, 8, 128
