@@ -1821,12 +1821,11 @@ long fused_capacity() {
 }
 
 // Whether a sampling call takes the one-launch path: many rows, aligned rows
-// of a length that is a multiple of 4 (16-byte loads and stores throughout),
-// a window short enough for 16-bit
+// (16-byte loads and stores throughout), a window short enough for 16-bit
 // counts, and a grid that fits on the GPU at once with a tenth to spare (for
 // speed: the launch completes without that too, row after row).
 bool use_fused(long rows, long vocab, long hist_ld, int ctx, bool penalty, int vec, int vec_out) {
-    if (rows < kFusedMinRows || !chunk_quads(vocab, vec) || !chunk_quads(vocab, vec_out)) return false;
+    if (rows < kFusedMinRows || !vec || !vec_out) return false;
     if (penalty && (ctx < hist_ld ? (long)ctx : hist_ld) > 65535) return false;
     const long nchf = (vocab + kFusedK * kSlice - 1) / (kFusedK * kSlice);
     return rows * nchf * 10 <= fused_capacity() * 9;

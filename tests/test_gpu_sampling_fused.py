@@ -128,14 +128,19 @@ def _ws(hip, rows, vocab):
 @pytest.mark.parametrize("vocab", [12289, 4099, 24576, 8])
 def test_fused_vocab_shapes(hip, orc, rng, vocab):
     """Vocabularies of one chunk and a single element (12289), not a multiple
-    of 4 (4099), exactly two chunks (24576) and tiny (8), at 48 rows."""
+    of 4 (4099; the kernel's element-wise loads), exactly two chunks (24576)
+    and tiny (8), at 48 rows, each through the one launch (the epoch
+    advances)."""
     rows = 48
     logits = (rng.normal(0, 3, (rows, vocab)) / 0.6).astype(np.float32)
     hist = rng.integers(0, vocab, (rows, 64)).astype(np.int32)
     r = rng.uniform(0, 1, rows).astype(np.float32)
     r[0] = 0.0
     r[1] = np.float32(1.0 - 2.0 ** -24)
-    ids, probs = _call(hip, logits, _ws(hip, rows, vocab), hist, r=r, **PARAMS)
+    ws = _ws(hip, rows, vocab)
+    e0 = _epoch(ws)
+    ids, probs = _call(hip, logits, ws, hist, r=r, **PARAMS)
+    assert _epoch(ws) == (e0 + 1) % (1 << 64), f"vocab {vocab}: the one-launch path was not taken"
     rids, rprobs = oracle_rows(orc, logits, hist, r=r, **PARAMS)
     _check(ids, probs, rids, rprobs, f"vocab {vocab}")
 
