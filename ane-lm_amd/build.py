@@ -117,7 +117,7 @@ def build_dropin_check(name: str = "dropin_check") -> str:
 
 
 def check_integration_doc() -> None:
-    """Compile every call INTEGRATION.md documents against the headers."""
+    """Compile every call the integration guide documents against the headers."""
     cpp = os.path.join(ROOT, "tests", "cpp")
     if not os.path.exists(os.path.join(cpp, "integration_doc.py")):
         return

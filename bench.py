@@ -1113,7 +1113,7 @@ def main():
         print(sq_summary(args.sq_summary, workload=args.workload))
         return
     if args.gpus != 1:
-        print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); the op chain shards "
+        print(f"bench.py measures one GPU only (--gpus {args.gpus} requested); the op chain shards "
               f"per token with no communication, so N GPUs would run N independent copies.", file=sys.stderr)
         sys.exit(2)
 

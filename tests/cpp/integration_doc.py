@@ -1,4 +1,4 @@
-"""Compile every call that INTEGRATION.md documents against the library's
+"""Compile every call that the integration guide documents against the library's
 headers, so the integration guide cannot drift from the ABI.
 
 Each ```c block of the guide becomes the body of a function of its own;

@@ -1,4 +1,4 @@
-// Declarations of the names that INTEGRATION.md's code uses, so that every
+// Declarations of the names that the integration guide's code uses, so that every
 // call it documents can be compiled against the library's real headers
 // (include/anelm_hip.h and the ane_lm:: drop-in headers).  Nothing here is
 // defined or run: tests/cpp/integration_doc.py wraps each documented block in

@@ -1,4 +1,4 @@
-"""INTEGRATION.md's documented calls compile against the library's headers
+"""The integration guide's documented calls compile against the library's headers
 (include/anelm_hip.h and the ane_lm:: drop-in headers), and the check
 catches a wrong argument order.  CPU only: g++ -fsyntax-only."""
 import os
