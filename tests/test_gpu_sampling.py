@@ -234,3 +234,38 @@ def test_sampler_leaves_logits_unchanged(hip, rng):
     hip.sample(ids, probs, lt, dev(rng.integers(0, 5000, (4, 256)).astype(np.int32)), None, p,
                dev(np.full(4, 0.5, np.float32)), ws)
     assert np.array_equal(host(lt), logits)
+
+
+@pytest.mark.parametrize("rows", [8, 32])
+def test_sampler_row_alignments_agree(hip, orc, rng, rows):
+    """Logits rows and probability rows each 16-byte aligned or starting one
+    float off (the element-wise loads, stores, or both; at 32 rows aligned
+    inputs take the one launch, the others the three launches): ids and
+    probabilities bit-identical across all four, and the ids equal to the
+    oracle's."""
+    import torch
+
+    logits = rng.normal(0, 3, (rows, V)).astype(np.float32)
+    hist = rng.integers(0, V, (rows, 256)).astype(np.int32)
+    r = drand48_stream(31, rows)
+    p = hip.SamplingParams(temperature=0.6, repetition_penalty=1.2, repetition_context_size=256,
+                           frequency_penalty=0.1)
+    ws = torch.empty(hip.sample_workspace_size(rows, V), dtype=torch.uint8, device="cuda")
+    out = {}
+    for off_in in (0, 1):
+        lbuf = torch.zeros(rows * V + 4, device="cuda")
+        lg = lbuf[off_in:off_in + rows * V].view(rows, V)
+        lg.copy_(dev(logits))
+        for off_out in (0, 1):
+            pbuf = torch.full((rows * V + 4,), float("nan"), device="cuda")
+            pr = pbuf[off_out:off_out + rows * V].view(rows, V)
+            ids = torch.full((rows,), -7, dtype=torch.int32, device="cuda")
+            hip.sample(ids, pr, lg, dev(hist), None, p, dev(r), ws)
+            out[(off_in, off_out)] = (host(ids), host(pr))
+    base_ids, base_probs = out[(0, 0)]
+    for key, (ids, probs) in out.items():
+        assert np.array_equal(ids, base_ids), key
+        assert_bitexact(probs, base_probs, f"offsets {key}")
+    rids, _ = oracle_rows(orc, logits, hist, r=r, temperature=0.6, repetition_penalty=1.2,
+                          repetition_context_size=256, frequency_penalty=0.1)
+    assert np.array_equal(base_ids, rids)
