@@ -20,7 +20,7 @@
 // Stages 1 and 2 recompute the adjusted logit from the input (a few flops)
 // instead of storing it; stage 3 reads the exponentials stage 2 stored.
 // With many sampling rows stages 1-3 run as one launch instead (chunks of
-// kFusedK slices kept in registers, row barriers between the stages; see
+// 4, 8 or 12 slices kept in registers, row barriers between the stages; see
 // "stages 1-3 in one launch"): the logits are read once and the
 // probabilities written once.
 #pragma clang fp contract(off)
@@ -1054,7 +1054,9 @@ __global__ __launch_bounds__(256) void sample_stage3_kernel(SampleArgs a, int ve
 // fits on the GPU at once, where it measured faster.  A wait still gives up
 // after kRowWaitTicks of real time, marks its row (the walk then returns id
 // -1 for it) and goes on, so every wave exits.
-constexpr int kFusedK = 12;              // 12288 logits per workgroup
+// Chunk sizes of the one launch, in k-slices (4096, 8192, 12288 logits per
+// workgroup); the host takes the smallest whose grid fits on the GPU at once.
+constexpr int kFusedKMin = 4;
 constexpr uint64_t kRowWaitTicks = 20000000u;  // 0.2 s of s_memrealtime (100 MHz)
 
 __device__ __forceinline__ uint64_t ld_agent(const uint64_t* p) {
@@ -1651,15 +1653,19 @@ struct WsLayout {
 
 static size_t al16(size_t x) { return (x + 15) & ~(size_t)15; }
 
-// 1024-logit slices per chunk: 3, unless rows x chunks of 4096 would leave
-// most of the 256 CUs without a workgroup (a few rows), then 1: the stages'
-// per-wave work is a chain of dependent instructions over a thread's 4K
-// logits and a wave's K sub-tiles, so at one row smaller chunks finish
-// sooner.  At 64 rows of 151936, 3 measured 68.5 us a call against 70.7 for
-// 4, 73-75 for 2 and 73-81 for 5, 6 and 8.  The outputs do not depend on it.
+// 1024-logit slices per chunk of the three launches: 1 up to about 14
+// workgroups of 1024 logits per CU (24 rows of 151936), else 3.  The
+// stages' per-wave work is a chain of dependent instructions over a
+// thread's 4K logits and a wave's K sub-tiles, so smaller chunks finish
+// sooner until the grid is many rounds deep.  Per call at 151936 (8 calls on
+// distinct inputs per graph), chunks of 1 against 3: 7 rows 31.9 / 41.2 us,
+// 12 rows 37.2 / 42.8, 16 rows 43.2 / 47.2, 24 rows 52.9 / 53.6 (unaligned
+// probabilities), 32 rows 59.4 / 56.6; at 64 rows 3 measured 68.5 us against
+// 70.7 for 4, 73-75 for 2 and 73-81 for 5, 6 and 8.  The outputs do not
+// depend on it.
 constexpr int kSlicesMany = 3;
 static int chunk_slices(long rows, long vocab) {
-    return rows * ((vocab + 4 * kSlice - 1) / (4 * kSlice)) < 256 ? 1 : kSlicesMany;
+    return rows * ((vocab + kSlice - 1) / kSlice) < 3600 ? 1 : kSlicesMany;
 }
 
 static WsLayout ws_layout(long rows, long vocab) {
@@ -1667,7 +1673,10 @@ static WsLayout ws_layout(long rows, long vocab) {
     const size_t nch = (size_t)((vocab + kch - 1) / kch);
     const size_t nsub = (size_t)((vocab + kSub - 1) / kSub);
     const size_t n = (size_t)rows * nch, ns = (size_t)rows * ((nsub + 3) & ~(size_t)3);
-    const size_t nchf = (size_t)((vocab + kFusedK * kSlice - 1) / (kFusedK * kSlice));
+    // the one launch's flags, for its smallest chunks (the most per row); its
+    // chunk maxima and sums use the regions below, which hold a chunk of 3
+    // k-slices or fewer per entry
+    const size_t nchf = (size_t)((vocab + kFusedKMin * kSlice - 1) / (kFusedKMin * kSlice));
     WsLayout l;
     // the one-launch path's epoch first, at the same place for every shape
     // (it counts the calls made on the workspace, whatever their shapes)
@@ -1782,13 +1791,10 @@ namespace anelm {
 namespace {
 
 // The one-launch path from this many rows.  Per call at 151936 logits (8
-// calls on distinct inputs in a graph), one launch against three: 32 rows
-// 50.1 / 54.7 us, 24 rows 51.0 / 52.4, 16 rows 47.4 / 46.8, 12 rows 45.4 /
-// 43.4, 8 rows 43.9 / 39.9.  Both are bound by their vector instructions and
-// dependent chains, not by their bytes; one launch saves the re-reads and the
-// launches' ramps, and its row barriers cost more than that saves when the
-// grid is small.
-constexpr long kFusedMinRows = 24;
+// calls on distinct inputs in a graph), one launch (chunks of 4 k-slices)
+// against three (chunks of 1): 6 rows 33.3 / 30.7 us, 8 rows 36.1 / 33.2, 10
+// rows 35.7 / 35.3, 12 rows 36.2 / 37.2, 16 rows 38.8 / 43.2.
+constexpr long kFusedMinRows = 12;
 // Sub-tiles that chunk 0 of each row walks one add at a time in the one
 // launch.  There every workgroup finishes at about the same time, so this
 // walk (about 8 cycles an add) lengthens the launch, where stage 3 of the
@@ -1798,8 +1804,10 @@ constexpr long kFusedMinRows = 24;
 constexpr int kFusedFirstSubs = 2;
 constexpr int kCapDevices = 64;
 
-// Workgroups of the one-launch kernel the current device holds at once
-// (occupancy per CU x CUs), looked up once per device; 0 if unknown.
+// Workgroups of the one-launch kernel with chunks of K k-slices that the
+// current device holds at once (occupancy per CU x CUs), looked up once per
+// device; 0 if unknown.
+template <int K>
 long fused_capacity() {
     static std::mutex mu;
     static long cap[kCapDevices];
@@ -1809,7 +1817,7 @@ long fused_capacity() {
     std::lock_guard<std::mutex> lock(mu);
     if (!known[dev]) {
         int nb = 0, cus = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, sample_fused_kernel<kFusedK>, 256, 0) != hipSuccess ||
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, sample_fused_kernel<K>, 256, 0) != hipSuccess ||
             hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
             (void)hipGetLastError();
             nb = cus = 0;
@@ -1820,15 +1828,28 @@ long fused_capacity() {
     return cap[dev];
 }
 
-// Whether a sampling call takes the one-launch path: many rows, aligned rows
-// (16-byte loads and stores throughout), a window short enough for 16-bit
-// counts, and a grid that fits on the GPU at once with a tenth to spare (for
-// speed: the launch completes without that too, row after row).
-bool use_fused(long rows, long vocab, long hist_ld, int ctx, bool penalty, int vec, int vec_out) {
-    if (rows < kFusedMinRows || !vec || !vec_out) return false;
-    if (penalty && (ctx < hist_ld ? (long)ctx : hist_ld) > 65535) return false;
-    const long nchf = (vocab + kFusedK * kSlice - 1) / (kFusedK * kSlice);
-    return rows * nchf * 10 <= fused_capacity() * 9;
+template <int K>
+bool fused_fits(long rows, long vocab) {
+    const long nchf = (vocab + K * kSlice - 1) / (K * kSlice);
+    return rows * nchf * 10 <= fused_capacity<K>() * 9;
+}
+
+// The one launch's chunk size in k-slices for a sampling call, or 0 for the
+// three launches: many rows, aligned rows (16-byte loads and stores
+// throughout), a window short enough for 16-bit counts, and the smallest
+// chunks whose grid fits on the GPU at once with a tenth to spare (for
+// speed: the launch completes without that too, row after row).  Smaller
+// chunks put more of the GPU on the rows and shorten each workgroup's
+// chain; per call at 151936 logits (8 calls on distinct inputs per graph),
+// chunks of 4 / 8 / 12 k-slices: 32 rows 42.7 / 46.1 / 50.5 us, 48 rows
+// (4 does not fit) 50.0 / 55.5; 64 rows only 12 fits.
+int fused_k(long rows, long vocab, long hist_ld, int ctx, bool penalty, int vec, int vec_out) {
+    if (rows < kFusedMinRows || !vec || !vec_out) return 0;
+    if (penalty && (ctx < hist_ld ? (long)ctx : hist_ld) > 65535) return 0;
+    if (fused_fits<4>(rows, vocab)) return 4;
+    if (fused_fits<8>(rows, vocab)) return 8;
+    if (fused_fits<12>(rows, vocab)) return 12;
+    return 0;
 }
 
 // The sampler behind both entry points; `who` names the caller in errors.
@@ -1883,15 +1904,18 @@ int sample_impl(int32_t* ids, float* probs, long ld_probs, const float* logits, 
     }
     const int vec_out = probs && (ld_probs % 4 == 0) && aligned16(probs);
     a.vec_probs = vec_out;
-    if (use_fused(rows, vocab, hist_ld, a.ctx, a.use_penalty != 0, vec, vec_out)) {
+    if (const int fk = fused_k(rows, vocab, hist_ld, a.ctx, a.use_penalty != 0, vec, vec_out)) {
         char* b = static_cast<char*>(workspace);
         const WsLayout l = ws_layout(rows, vocab);
         a.epoch = reinterpret_cast<uint64_t*>(b + l.off_epoch);
         a.ws_rowtok = reinterpret_cast<uint64_t*>(b + l.off_rowtok);
         a.ws_tok = reinterpret_cast<uint64_t*>(b + l.off_tok);
-        a.nchunk = (int)((vocab + kFusedK * kSlice - 1) / (kFusedK * kSlice));
+        a.nchunk = (int)((vocab + fk * kSlice - 1) / (fk * kSlice));
         a.first_subs = kFusedFirstSubs;
-        sample_fused_kernel<kFusedK><<<dim3((unsigned)a.nchunk, (unsigned)rows), 256, 0, st>>>(a, vec, vec_out);
+        const dim3 g((unsigned)a.nchunk, (unsigned)rows);
+        if (fk == 4) sample_fused_kernel<4><<<g, 256, 0, st>>>(a, vec, vec_out);
+        else if (fk == 8) sample_fused_kernel<8><<<g, 256, 0, st>>>(a, vec, vec_out);
+        else sample_fused_kernel<12><<<g, 256, 0, st>>>(a, vec, vec_out);
     } else {
         const bool q_out = chunk_quads(vocab, vec_out != 0);
         if (one) launch_stages<1>(a, grd, q_in, q_out, vec_out, st);
@@ -1910,7 +1934,7 @@ int sample_impl(int32_t* ids, float* probs, long ld_probs, const float* logits, 
 // Nothing in it needs clearing: every word a kernel reads is written earlier
 // in the same call, except the one-launch path's epoch and flags, which work
 // from any contents.  Calls that overlap on one GPU share it, and race.
-constexpr size_t kScratchBytes = 4u << 20;   // 184 rows at Qwen3's 151936-row vocabulary
+constexpr size_t kScratchBytes = 4u << 20;   // 181 rows at Qwen3's 151936-row vocabulary
 constexpr int kMaxDevices = 64;
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 void* scratch_ptr[kMaxDevices];

@@ -256,7 +256,7 @@ typedef struct anelm_sampling_params {
  *    (sampling.cpp:59-65).
  * r[b] is the uniform draw (the reference's (float)drand48()).
  * Needs anelm_sample_workspace_size(rows, vocab) bytes of device workspace,
- * with any contents (nothing needs clearing).  From 24 sampling rows, with
+ * with any contents (nothing needs clearing).  From 12 sampling rows, with
  * 16-byte aligned logits and probability rows, stages 1-3 run as one launch
  * whose row barriers need the whole grid resident on the GPU at once (the
  * library checks that it fits); a barrier that still waits 0.2 s gives up
@@ -272,7 +272,7 @@ int anelm_sample(int32_t* ids, float* probs, long ld_probs, const float* logits,
  * the same kernels and results, with the workspace taken from a static
  * 4 MiB device array the library holds on every GPU it runs on until the
  * process ends, so it calls no allocator.  Limit:
- * anelm_sample_workspace_size(rows, vocab) <= 4 MiB (184 rows at a 151936-row
+ * anelm_sample_workspace_size(rows, vocab) <= 4 MiB (181 rows at a 151936-row
  * vocabulary); larger calls return ANELM_ERR_WORKSPACE.  Every call on one GPU
  * shares that GPU's array: calls that overlap on one GPU (on different
  * streams, or from different threads) race and must not be issued.  The

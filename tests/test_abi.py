@@ -124,23 +124,23 @@ def test_tiled_size(lib):
 
 def test_workspace_sizes(lib):
     # the one-launch path's epoch (256 bytes), its per-row tokens (two u64) and
-    # its two barriers' flags (u64 per row and chunk of 12288 logits: 13 at
-    # 151936), then 64 rows x 50 chunks of 3072 logits (u64 sums, f32 maxima,
+    # its two barriers' flags (u64 per row and chunk of its smallest chunks,
+    # 4096 logits: 38 at 151936), then 64 rows x 50 chunks of 3072 logits (u64 sums, f32 maxima,
     # i32 argmax, i32 flags) + 64 rows x 594 sub-tiles of 256, rows padded to
     # 596 (two u32 map words, i32 binade class, six u32 words of the predicted
     # crossing), 16-byte aligned
     al = lambda b: (b + 15) // 16 * 16
-    tok = lambda rows: 256 + al(rows * 16) + al(rows * 2 * 13 * 8)
+    tok = lambda rows: 256 + al(rows * 16) + al(rows * 2 * 38 * 8)
     n, ns = 64 * 50, 64 * 596
     assert lib.anelm_sample_workspace_size(64, 151936) == (tok(64) + al(n * 8) + 3 * al(n * 4) + 3 * al(ns * 4)
                                                            + al(ns * 24) + al(64 * 8))   # + sub-tile 0 result per row
-    # a few rows (rows x 38 chunks of 4096 < 256 workgroups): chunks of 1024, 149 per row
-    n, ns = 6 * 149, 6 * 596
-    assert lib.anelm_sample_workspace_size(6, 151936) == (tok(6) + al(n * 8) + 3 * al(n * 4) + 3 * al(ns * 4)
-                                                          + al(ns * 24) + al(6 * 8))
-    n, ns = 7 * 50, 7 * 596
-    assert lib.anelm_sample_workspace_size(7, 151936) == (tok(7) + al(n * 8) + 3 * al(n * 4) + 3 * al(ns * 4)
-                                                          + al(ns * 24) + al(7 * 8))
+    # fewer rows (rows x 149 chunks of 1024 < 3600 workgroups): chunks of 1024, 149 per row
+    n, ns = 24 * 149, 24 * 596
+    assert lib.anelm_sample_workspace_size(24, 151936) == (tok(24) + al(n * 8) + 3 * al(n * 4) + 3 * al(ns * 4)
+                                                           + al(ns * 24) + al(24 * 8))
+    n, ns = 25 * 50, 25 * 596
+    assert lib.anelm_sample_workspace_size(25, 151936) == (tok(25) + al(n * 8) + 3 * al(n * 4) + 3 * al(ns * 4)
+                                                           + al(ns * 24) + al(25 * 8))
     assert lib.anelm_sample_workspace_size(0, 10) == 0
     assert lib.anelm_softmax_workspace_size(1, 4096) > 0
 

@@ -1,6 +1,8 @@
 """The sampler's one-launch path (stages 1-3 in one kernel with per-row
-barriers), which anelm_sample takes from 24 rows when the rows are 16-byte
-aligned and the grid fits on the GPU at once: token ids bit-exact against the
+barriers), which anelm_sample takes from 12 rows when the rows are 16-byte
+aligned and the grid fits on the GPU at once (chunks of 4, 8 or 12 k-slices,
+the smallest that fits: 4 up to about 40 rows of 151936, 8 at 48, 12 at 64):
+token ids bit-exact against the
 oracle (core/sampling.cpp:10-66) and probabilities bit-identical, on the edge
 cases the three-launch path is tested on, on workspaces that start with
 arbitrary contents and are reused across shapes, and bit-identical to the
@@ -56,15 +58,16 @@ def _check(ids, probs, rids, rprobs, what):
     assert_bitexact(np.where(gn, 0.0, probs).astype(np.float32), np.where(rn, 0.0, rprobs).astype(np.float32), what)
 
 
-def test_fused_path_taken_from_24_rows(hip, orc, rng):
+def test_fused_path_taken_from_12_rows(hip, orc, rng):
     """The epoch in the workspace's first word counts one-launch calls: it
-    advances once per call at 64 and 24 rows and stays put at 23 rows (three
-    launches), and the ids and probabilities match the oracle each time."""
+    advances once per call at 64, 48, 16 and 12 rows (chunks of 12, 8, 4 and
+    4 k-slices) and stays put at 11 rows (three launches), and the ids and
+    probabilities match the oracle each time."""
     import torch
 
     ws = torch.zeros(hip.sample_workspace_size(64, V), dtype=torch.uint8, device="cuda")
     expect = 0
-    for rows, fused in ((64, True), (24, True), (23, False), (64, True)):
+    for rows, fused in ((64, True), (48, True), (16, True), (12, True), (11, False), (64, True)):
         logits = rng.normal(0, 3, (rows, V)).astype(np.float32)
         hist = rng.integers(0, V, (rows, 256)).astype(np.int32)
         r = rng.uniform(0, 1, rows).astype(np.float32)
@@ -75,12 +78,13 @@ def test_fused_path_taken_from_24_rows(hip, orc, rng):
         _check(ids, probs, rids, rprobs, f"{rows} rows")
 
 
-def test_fused_equals_three_launches(hip, rng):
-    """The same 48 rows through both paths (unaligned probability rows take
-    the three launches): ids and probabilities bit-identical."""
+@pytest.mark.parametrize("rows", [16, 48, 64])
+def test_fused_equals_three_launches(hip, rng, rows):
+    """The same rows through both paths (unaligned probability rows take the
+    three launches), at each one-launch chunk size (4, 8 and 12 k-slices at
+    16, 48 and 64 rows): ids and probabilities bit-identical."""
     import torch
 
-    rows = 48
     logits = rng.normal(0, 3, (rows, V)).astype(np.float32)
     hist = rng.integers(0, V, (rows, 256)).astype(np.int32)
     r = drand48_stream(7, rows)
