@@ -1100,10 +1100,13 @@ __device__ bool row_wait(const uint64_t* flags, int n, uint64_t tok, int* s_ok) 
     return *s_ok != 0;
 }
 
-// At most 128 VGPRs (4 waves per SIMD), so that 4 workgroups fit on a CU and
-// 64 rows of 151936 logits (832 workgroups) on the GPU at once; the cap also
-// measured 1 us faster per call there than the 121 VGPRs left to the
-// compiler (16 bytes of spill per lane).
+// Registers: chunks of 12 k-slices at most 128 VGPRs (4 waves per SIMD), so
+// that 4 workgroups fit on a CU (the cap also measured 1 us faster per call
+// than the 121 VGPRs left to the compiler, 16 bytes of spill per lane);
+// chunks of 8 at most 96 (5 per CU, no spill), so that 64 rows of 151936
+// (1216 workgroups) fit on the GPU at once with them: 58.7 -> 53.4 us per
+// call against chunks of 12 (at 80 VGPRs, 6 per CU, it spilled 56 bytes per
+// lane and took 55.5-55.9); chunks of 4 take 68 (7 per CU) uncapped.
 // Grid (nchunk, rows), chunks of K slices.  A row's workgroups are
 // consecutive in dispatch order (blockIdx.x its chunk, blockIdx.y the row),
 // so the launch makes progress however few of its workgroups are resident:
@@ -1116,7 +1119,7 @@ __device__ bool row_wait(const uint64_t* flags, int n, uint64_t tok, int* s_ok) 
 // stage 3, measured 64.3 against 65.1 us at 64 rows, but with fewer
 // workgroups resident than the grid no row would have all of its.)
 template <int K>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void sample_fused_kernel(SampleArgs a, int vec, int vec_out) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(K == 8 ? 5 : 4))) void sample_fused_kernel(SampleArgs a, int vec, int vec_out) {
     constexpr int kCH = K * kSlice;
     __shared__ __align__(16) uint32_t cnt[kCH / 2];   // window counts, two per word
     __shared__ float red[4];
@@ -1828,21 +1831,24 @@ long fused_capacity() {
     return cap[dev];
 }
 
+// Fits in 95% of what the GPU holds at once (85% with chunks of 4 k-slices:
+// 44 rows of 151936 at 93% of their capacity took 56.8 us per call against
+// 49.1 with chunks of 8, 40 rows at 85% 46.9 us).
 template <int K>
 bool fused_fits(long rows, long vocab) {
     const long nchf = (vocab + K * kSlice - 1) / (K * kSlice);
-    return rows * nchf * 10 <= fused_capacity<K>() * 9;
+    return rows * nchf * 20 <= fused_capacity<K>() * (K == 4 ? 17 : 19);
 }
 
 // The one launch's chunk size in k-slices for a sampling call, or 0 for the
 // three launches: many rows, aligned rows (16-byte loads and stores
 // throughout), a window short enough for 16-bit counts, and the smallest
-// chunks whose grid fits on the GPU at once with a tenth to spare (for
-// speed: the launch completes without that too, row after row).  Smaller
-// chunks put more of the GPU on the rows and shorten each workgroup's
-// chain; per call at 151936 logits (8 calls on distinct inputs per graph),
-// chunks of 4 / 8 / 12 k-slices: 32 rows 42.7 / 46.1 / 50.5 us, 48 rows
-// (4 does not fit) 50.0 / 55.5; 64 rows only 12 fits.
+// chunks whose grid fits on the GPU at once with room to spare (fused_fits;
+// for speed: the launch completes without that too, row after row).  Smaller chunks put
+// more of the GPU on the rows and shorten each workgroup's chain; per call at
+// 151936 logits (8 calls on distinct inputs per graph), chunks of 4 / 8 / 12
+// k-slices: 32 rows 42.7 / 46.1 / 50.5 us, 48 rows (4 does not fit) 50.0 /
+// 55.5, 64 rows (8 at 5 workgroups per CU) 53.4 / 58.7.
 int fused_k(long rows, long vocab, long hist_ld, int ctx, bool penalty, int vec, int vec_out) {
     if (rows < kFusedMinRows || !vec || !vec_out) return 0;
     if (penalty && (ctx < hist_ld ? (long)ctx : hist_ld) > 65535) return 0;

@@ -74,7 +74,7 @@ def test_graph_replays_match_eager(hip):
 @pytest.mark.parametrize("rows,V", [(3, 20000), (16, 20000), (64, 151936)])
 def test_sampler_graph_replays_match_eager(hip, rng, rows, V):
     """From 12 rows the sampler is one launch for stages 1-3 (chunks of 4
-    k-slices at 16 rows here, 12 at 64) whose row barriers take their token
+    k-slices at 16 rows here, 8 at 64) whose row barriers take their token
     from the workspace's epoch, which the walk advances on the device; at 3
     rows it is three launches and the epoch stays.  Every replay of the
     captured call (new logits and draws each time) matches the eager call."""
